@@ -1,0 +1,275 @@
+"""ana_amd: hhefesto/ana's decoder token loop on MI355X.
+
+The product is libana.so (ana_amd/csrc, C ABI in include/ana.h). This module
+is a thin ctypes mirror of the engine seam the reference's host code drives
+(bend/Decode.bend's dc.* over bend/Dense/Decode.bend's dd.*): load, reset,
+feed, feeds, logits, top, pick, and the token loop. It never computes
+anything itself and raises if libana.so is missing.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+from .config import Config
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libana.so")
+
+ANA_OK, ANA_EINVAL, ANA_ECKPT, ANA_EDEVICE, ANA_ENOMEM, ANA_EUNSUP = range(6)
+EXACT_FP32 = 0
+EOS = 1  # bend/Tokenizer.bend: BOS 0, EOS 1
+
+
+class AnaError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(msg)
+        self.code = code
+
+
+class _Cfg(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in
+                ("vocab", "ctx", "d", "f", "layers", "heads", "rglru", "qk", "sinks", "tied")]
+
+
+class _Opts(C.Structure):
+    _fields_ = [("device", C.c_int), ("numerics", C.c_int), ("max_seqs", C.c_uint32),
+                ("prefill_chunk", C.c_uint32)]
+
+
+class _Sampling(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float)]
+
+
+# every symbol include/ana.h declares, with its signature
+_u32p = C.POINTER(C.c_uint32)
+_u64p = C.POINTER(C.c_uint64)
+_f32p = C.POINTER(C.c_float)
+SIGNATURES = {
+    "ana_open": (C.c_int, [C.c_char_p, C.POINTER(_Opts), C.POINTER(C.c_void_p)]),
+    "ana_config_of": (C.c_int, [C.c_void_p, C.POINTER(_Cfg), _u64p]),
+    "ana_reset": (C.c_int, [C.c_void_p, C.c_uint32]),
+    "ana_feed": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p, _u32p]),
+    "ana_feeds": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, _u32p, C.c_uint32]),
+    "ana_logits": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _f32p]),
+    "ana_top": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p]),
+    "ana_pick": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, C.POINTER(_Sampling), _u64p, _u32p]),
+    "ana_rng_seeded": (None, [C.c_uint64, _u64p]),
+    "ana_generate": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p, _u32p, C.c_uint32,
+                               C.POINTER(_Sampling), _u64p, _u32p]),
+    "ana_state": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, _f32p, C.c_size_t]),
+    "ana_prof": (C.c_int, [C.c_void_p, C.c_int]),
+    "ana_prof_read": (C.c_int, [C.c_void_p, C.c_uint32, _u64p, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "ana_error": (C.c_char_p, [C.c_void_p]),
+    "ana_close": (None, [C.c_void_p]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """libana.so, loaded once; raises when it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() (or python ana_amd/build.py)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _u32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint32).reshape(-1))
+
+
+def _p(a: np.ndarray, t):
+    return a.ctypes.data_as(C.POINTER(t))
+
+
+@dataclass
+class Settings:
+    """bend/Decode.bend:147-148: temperature, top-k (off = 2^32-1), top-p."""
+
+    temperature: float = float(np.float32(0.8))
+    top_k: int = 0xFFFFFFFF
+    top_p: float = float(np.float32(0.95))
+
+    @property
+    def greedy(self) -> bool:
+        return self.temperature <= 0.0
+
+    def _c(self) -> _Sampling:
+        return _Sampling(self.temperature, self.top_k, self.top_p)
+
+
+def _f32_or(s: str, d: float) -> float:
+    try:
+        return float(np.float32(float(s)))
+    except ValueError:
+        return float(np.float32(d))
+
+
+def settings(temp: str = "0.8", topk: str = "", topp: str = "0.95") -> Settings:
+    """dc.settings (bend/Decode.bend:546-548): non-numeric values fall back
+    to the defaults TEMPERATURE 0.8, TOP_K off, TOP_P 0.95."""
+    k = int(topk) if topk.isdigit() and int(topk) < 2 ** 32 else 0xFFFFFFFF
+    return Settings(_f32_or(temp, 0.8), k, _f32_or(topp, 0.95))
+
+
+def u64_read(s: str):
+    """U64.read (bend/Num.bend:147-170): digits only, wrapping; None otherwise."""
+    if not s or not s.isdigit() or not s.isascii():
+        return None
+    v = 0
+    for ch in s:
+        v = (v * 10 + ord(ch) - 48) & 0xFFFFFFFFFFFFFFFF
+    return v
+
+
+def rng_seeded(seed: int) -> np.ndarray:
+    """Rng.seeded (bend/Sample.bend:68-93): 4 xoshiro words for a seed."""
+    r = np.zeros(4, dtype=np.uint64)
+    lib().ana_rng_seeded(seed & 0xFFFFFFFFFFFFFFFF, _p(r, C.c_uint64))
+    return r
+
+
+def rng_of(sample_seed: str) -> np.ndarray:
+    """dc.rng.of: SAMPLE_SEED parsed as U64, else seed 0."""
+    v = u64_read(sample_seed)
+    return rng_seeded(0 if v is None else v)
+
+
+class Decoder:
+    """A checkpoint on a device with state for max_seqs sequences."""
+
+    def __init__(self, path: str, device: int = 0, max_seqs: int = 1, prefill_chunk: int = 64,
+                 numerics: int = EXACT_FP32):
+        L = lib()
+        h = C.c_void_p()
+        o = _Opts(device, numerics, max_seqs, prefill_chunk)
+        r = L.ana_open(path.encode(), C.byref(o), C.byref(h))
+        if r != ANA_OK:
+            raise AnaError(r, L.ana_error(None).decode())
+        self.h = h
+        cfg = _Cfg()
+        step = C.c_uint64()
+        self._check(L.ana_config_of(h, C.byref(cfg), C.byref(step)))
+        self.config = Config(cfg.vocab, cfg.ctx, cfg.d, cfg.f, cfg.layers, cfg.heads,
+                             bool(cfg.rglru), bool(cfg.qk), bool(cfg.sinks), bool(cfg.tied))
+        self.step_saved = step.value
+        self.max_seqs = max_seqs
+
+    def _check(self, r: int) -> None:
+        if r != ANA_OK:
+            raise AnaError(r, lib().ana_error(self.h).decode())
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().ana_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    @property
+    def vocab(self) -> int:
+        return self.config.vocab
+
+    def reset(self, seq: int = 0) -> None:
+        """dd.reset / dc.en.reset."""
+        self._check(lib().ana_reset(self.h, seq))
+
+    def feed(self, seqs, pos, toks) -> None:
+        """dd.feed for each listed sequence (one token each)."""
+        s, p, t = _u32(seqs), _u32(pos), _u32(toks)
+        self._check(lib().ana_feed(self.h, s.size, _p(s, C.c_uint32), _p(p, C.c_uint32), _p(t, C.c_uint32)))
+
+    def feeds(self, seq: int, pos: int, toks) -> None:
+        """dd.feeds: a prompt a chunk at a time."""
+        t = _u32(toks)
+        self._check(lib().ana_feeds(self.h, seq, pos, _p(t, C.c_uint32), t.size))
+
+    def logits(self, seqs) -> np.ndarray:
+        s = _u32(seqs)
+        out = np.empty((s.size, self.vocab), dtype=np.float32)
+        self._check(lib().ana_logits(self.h, s.size, _p(s, C.c_uint32), _p(out, C.c_float)))
+        return out
+
+    def top(self, seqs) -> np.ndarray:
+        """dd.top: greedy pick on the device (vocab on a NaN max)."""
+        s = _u32(seqs)
+        out = np.empty(s.size, dtype=np.uint32)
+        self._check(lib().ana_top(self.h, s.size, _p(s, C.c_uint32), _p(out, C.c_uint32)))
+        return out
+
+    def pick(self, seqs, st: Settings, rng: np.ndarray | None = None) -> np.ndarray:
+        """S.pick on the device; rng (n x 4 uint64) advances in place."""
+        s = _u32(seqs)
+        out = np.empty(s.size, dtype=np.uint32)
+        rp = None
+        if rng is not None:
+            assert rng.dtype == np.uint64 and rng.flags.c_contiguous and rng.size == 4 * s.size
+            rp = _p(rng, C.c_uint64)
+        sc = st._c()
+        self._check(lib().ana_pick(self.h, s.size, _p(s, C.c_uint32), C.byref(sc), rp, _p(out, C.c_uint32)))
+        return out
+
+    def generate(self, seqs, pos, toks, steps: int, st: Settings | None = None,
+                 rng: np.ndarray | None = None) -> np.ndarray:
+        """The token loop for each sequence: feed, head, pick, feed the pick."""
+        s, p, t = _u32(seqs), _u32(pos), _u32(toks)
+        out = np.empty((s.size, steps), dtype=np.uint32)
+        sp = C.byref(st._c()) if st is not None else None
+        rp = _p(rng, C.c_uint64) if rng is not None else None
+        self._check(lib().ana_generate(self.h, s.size, _p(s, C.c_uint32), _p(p, C.c_uint32),
+                                       _p(t, C.c_uint32), steps, sp, rp, _p(out, C.c_uint32)))
+        return out
+
+    KINDS = ("gemv", "head", "attn", "gla", "pick")
+
+    def prof(self, on: bool) -> None:
+        """Start (and clear) or stop per-launch event timing."""
+        self._check(lib().ana_prof(self.h, int(on)))
+
+    def prof_read(self) -> dict:
+        """{kind: (launches, ms, algorithmic bytes)} since prof(True)."""
+        out = {}
+        for k, name in enumerate(self.KINDS):
+            n, ms, b = C.c_uint64(), C.c_double(), C.c_double()
+            self._check(lib().ana_prof_read(self.h, k, C.byref(n), C.byref(ms), C.byref(b)))
+            out[name] = (n.value, ms.value, b.value)
+        return out
+
+    def state(self, seq: int, layer: int) -> np.ndarray:
+        c = self.config
+        if layer == c.layers:
+            n = c.d
+        elif c.is_softmax(layer):
+            n = 2 * c.ctx * c.d
+        else:
+            n = c.heads * c.hd * c.hd
+        out = np.empty(n, dtype=np.float32)
+        self._check(lib().ana_state(self.h, seq, layer, _p(out, C.c_float), n))
+        return out
+
+
+def truncate_at_eos(row: np.ndarray) -> np.ndarray:
+    """Generate's stop (bend/Generate.bend:31-51): the picks through the first EOS."""
+    hit = np.nonzero(row == EOS)[0]
+    return row if hit.size == 0 else row[: hit[0] + 1]

@@ -1,0 +1,546 @@
+// libana: the C ABI of include/ana.h over the kernels.
+//
+// One context = one checkpoint on one device, one HIP stream, and state for
+// max_seqs sequences. A sequence's states are one contiguous region (per
+// layer: the GLA S of heads x hd x hd floats, or the softmax K ring then V
+// ring of ctx x d floats each), followed in a separate array by the residual
+// row of its last fed token, which the head reads (the store's x cell in
+// bend/Dense/Decode.bend).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "ana_internal.h"
+
+using namespace ana;
+
+struct ana_ctx {
+  int device = 0;
+  hipStream_t st = nullptr;
+  ana_config cfg{};
+  uint64_t P = 0, step = 0, fin = 0;
+  std::vector<Blk> blk;
+  std::vector<uint64_t> layer_off;   // floats from a sequence's state start
+  uint64_t seq_stride = 0;           // floats per sequence
+  uint32_t max_seqs = 1, chunk = 64, wb = 1;
+  float* W = nullptr;                // parameters [P]
+  float* state = nullptr;            // [max_seqs][seq_stride]
+  float* xs = nullptr;               // [max_seqs][d]
+  // workspace, wb rows
+  float *X = nullptr, *XA = nullptr, *QKV = nullptr, *Z = nullptr, *O = nullptr, *HH = nullptr;
+  float* LG = nullptr;               // [max_seqs][vocab]
+  uint32_t *d_seq = nullptr, *d_pos = nullptr, *d_tok = nullptr, *d_pick = nullptr, *d_out = nullptr;
+  uint64_t* d_rng = nullptr;
+  size_t out_cap = 0;
+  std::string err;
+  // kernel timing (ana_prof)
+  bool prof = false;
+  double attn_bytes = 0.0;           // per softmax-layer launch of the current step
+  std::vector<hipEvent_t> ev;        // pool, two per recorded launch
+  struct Rec { uint32_t kind; double bytes; };
+  std::vector<Rec> recs;
+};
+
+static const size_t kProfMax = 16384;
+
+// bracket one launch with events on the context's stream
+struct ProfScope {
+  ana_ctx* c;
+  uint32_t kind;
+  double bytes;
+  bool on;
+  ProfScope(ana_ctx* c_, uint32_t k, double b) : c(c_), kind(k), bytes(b), on(false) {
+    if (!c->prof || c->recs.size() >= kProfMax) return;
+    const size_t i = c->recs.size();
+    if (c->ev.size() < 2 * (i + 1)) {
+      hipEvent_t a, e;
+      if (hipEventCreate(&a) != hipSuccess) return;
+      if (hipEventCreate(&e) != hipSuccess) { (void)hipEventDestroy(a); return; }
+      c->ev.push_back(a);
+      c->ev.push_back(e);
+    }
+    if (hipEventRecord(c->ev[2 * i], c->st) != hipSuccess) return;
+    on = true;
+  }
+  ~ProfScope() {
+    if (!on) return;
+    const size_t i = c->recs.size();
+    if (hipEventRecord(c->ev[2 * i + 1], c->st) == hipSuccess) c->recs.push_back({kind, bytes});
+  }
+};
+
+static thread_local std::string g_open_err;
+
+static int fail(ana_ctx* c, int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (c) c->err = buf;
+  else g_open_err = buf;
+  return code;
+}
+
+#define HIPCHK(ctx, x)                                                                  \
+  do {                                                                                  \
+    hipError_t e_ = (x);                                                                \
+    if (e_ != hipSuccess)                                                               \
+      return fail(ctx, ANA_EDEVICE, "device fault: %s (%s:%d)", hipGetErrorString(e_), \
+                  __FILE__, __LINE__);                                                  \
+  } while (0)
+
+template <class T>
+static hipError_t dalloc(T** p, size_t n) {
+  return hipMalloc((void**)p, std::max<size_t>(n, 1) * sizeof(T));
+}
+
+static void release(ana_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  void* ps[] = {c->W, c->state, c->xs, c->X, c->XA, c->QKV, c->Z, c->O, c->HH, c->LG,
+                c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_rng};
+  for (void* p : ps)
+    if (p) (void)hipFree(p);
+  for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
+  if (c->st) (void)hipStreamDestroy(c->st);
+}
+
+static StateRef sref(const ana_ctx* c, uint32_t l) {
+  return StateRef{c->state, c->seq_stride, c->layer_off[l]};
+}
+
+// what the kernels require of a configuration
+static const char* unsupported(const ana_config& c) {
+  if (c.heads == 0 || c.d % c.heads) return "model dim is not a multiple of the head count";
+  const uint32_t hd = c.d / c.heads;
+  if (hd > 64) return "head dimension above 64";
+  if (c.d % 4 || c.f % 4 || hd % 4) return "model, MLP and head dimensions must be multiples of 4";
+  if (c.sinks && c.heads % 4) return "with head sinks the head count must be a multiple of 4";
+  if (c.ctx == 0 || c.ctx > 4096) return "context above 4096 slots";
+  if (c.vocab < 2 || c.vocab > 65536) return "vocabulary outside 2..65536";
+  return nullptr;
+}
+
+extern "C" void ana_rng_seeded(uint64_t seed, uint64_t r[4]) {
+  // Rng.seeded: four SplitMix64 draws (bend/Sample.bend:68-93)
+  uint64_t s = seed;
+  for (int i = 0; i < 4; i++) {
+    s += 0x9E3779B97F4A7C15ull;
+    uint64_t z = (s ^ (s >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    r[i] = z ^ (z >> 31);
+  }
+}
+
+extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
+  if (!path || !out) return fail(nullptr, ANA_EINVAL, "ana_open: null argument");
+  *out = nullptr;
+  ana_opts o{};
+  o.max_seqs = 1;
+  if (opts) o = *opts;
+  if (o.numerics != ANA_EXACT_FP32) return fail(nullptr, ANA_EUNSUP, "ana_open: unknown numerics mode %d", o.numerics);
+  if (o.max_seqs == 0) o.max_seqs = 1;
+  if (o.prefill_chunk == 0) o.prefill_chunk = 64;
+  Ftc2 ck;
+  std::string why = read_ftc2(path, &ck);
+  if (!why.empty()) return fail(nullptr, ANA_ECKPT, "%s", why.c_str());
+  if (const char* u = unsupported(ck.cfg)) return fail(nullptr, ANA_EUNSUP, "ana_open: %s", u);
+  ana_ctx* c = new ana_ctx();
+  c->device = o.device;
+  c->cfg = ck.cfg;
+  c->step = ck.step;
+  c->P = params_of(ck.cfg);
+  c->blk = layout_of(ck.cfg, &c->fin);
+  c->max_seqs = o.max_seqs;
+  c->chunk = o.prefill_chunk;
+  c->wb = std::max(c->max_seqs, c->chunk);
+  const ana_config& cf = c->cfg;
+  const uint32_t d = cf.d, hd = d / cf.heads;
+  uint64_t off = 0;
+  for (uint32_t l = 0; l < cf.layers; l++) {
+    c->layer_off.push_back(off);
+    off += c->blk[l].gla ? (uint64_t)cf.heads * hd * hd : 2ull * cf.ctx * d;
+  }
+  c->seq_stride = off;
+  auto bad = [&](hipError_t e) {
+    int r = fail(nullptr, e == hipErrorOutOfMemory ? ANA_ENOMEM : ANA_EDEVICE, "device fault: %s",
+                 hipGetErrorString(e));
+    release(c);
+    delete c;
+    return r;
+  };
+  hipError_t e;
+  if ((e = hipSetDevice(c->device)) != hipSuccess) return bad(e);
+  if ((e = hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking)) != hipSuccess) return bad(e);
+  const uint64_t wb = c->wb;
+  if ((e = dalloc(&c->W, c->P)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->state, c->seq_stride * c->max_seqs)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->xs, (uint64_t)d * c->max_seqs)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->X, wb * d)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->XA, wb * d)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->QKV, wb * 3 * d)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->Z, wb * d)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->O, wb * d)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->HH, wb * cf.f)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->LG, (uint64_t)c->max_seqs * cf.vocab)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->d_seq, wb)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->d_pos, wb)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->d_tok, wb)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->d_pick, wb)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->d_rng, 4 * wb)) != hipSuccess) return bad(e);
+  if ((e = hipMemcpyAsync(c->W, ck.raw.data(), 4 * c->P, hipMemcpyHostToDevice, c->st)) != hipSuccess) return bad(e);
+  if ((e = launch_bswap(reinterpret_cast<uint32_t*>(c->W), c->P, c->st)) != hipSuccess) return bad(e);
+  if ((e = launch_zero(c->state, c->seq_stride * c->max_seqs, c->st)) != hipSuccess) return bad(e);
+  if ((e = launch_zero(c->xs, (uint64_t)d * c->max_seqs, c->st)) != hipSuccess) return bad(e);
+  if ((e = hipStreamSynchronize(c->st)) != hipSuccess) return bad(e);
+  *out = c;
+  return ANA_OK;
+}
+
+extern "C" int ana_config_of(const ana_ctx* c, ana_config* out, uint64_t* step) {
+  if (!c || !out) return ANA_EINVAL;
+  *out = c->cfg;
+  if (step) *step = c->step;
+  return ANA_OK;
+}
+
+extern "C" const char* ana_error(const ana_ctx* c) { return c ? c->err.c_str() : g_open_err.c_str(); }
+
+extern "C" void ana_close(ana_ctx* c) {
+  if (!c) return;
+  (void)hipStreamSynchronize(c->st);
+  release(c);
+  delete c;
+}
+
+extern "C" int ana_reset(ana_ctx* c, uint32_t seq) {
+  if (!c) return ANA_EINVAL;
+  if (seq >= c->max_seqs) return fail(c, ANA_EINVAL, "ana_reset: sequence %u outside 0..%u", seq, c->max_seqs - 1);
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, launch_zero(c->state + (uint64_t)seq * c->seq_stride, c->seq_stride, c->st));
+  HIPCHK(c, launch_zero(c->xs + (uint64_t)seq * c->cfg.d, c->cfg.d, c->st));
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  return ANA_OK;
+}
+
+// ------------------------------------------------------------------ the step
+
+// algorithmic bytes of a product: weights once, activations in and out
+static double gemv_bytes(const GemvArgs& g) {
+  double rows = g.seg[0].rows + (g.nseg > 1 ? g.seg[1].rows : 0);
+  double out_rows = g.mode == GM_SILU ? g.seg[0].rows : rows;
+  double b = 4.0 * rows * g.K + 4.0 * g.B * g.K + 4.0 * g.B * out_rows;
+  if (g.mode == GM_RESID) b += 4.0 * g.B * out_rows;
+  return b;
+}
+
+static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g, uint32_t kind) {
+  ProfScope ps(c, kind, gemv_bytes(g));
+  return launch_gemv(g, c->st);
+}
+
+static GemvArgs gemv1(const float* X, uint32_t ldx, const float* ng, uint32_t K, const float* W,
+                      uint32_t rows, float* Y, uint32_t ldy, uint32_t B) {
+  GemvArgs a{};
+  a.X = X; a.ldx = ldx; a.ng = ng; a.K = K;
+  a.seg[0] = GemvSeg{W, rows, Y, ldy};
+  a.nseg = 1;
+  a.mode = GM_PLAIN;
+  a.B = B;
+  return a;
+}
+
+// every layer for B rows of X (embedded already). Row b is sequence seq[b]
+// at position pos[b] (device arrays), or, for a chunk (seq == nullptr), one
+// sequence seq0 at positions pos0 + b.
+static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_t* pos,
+                      uint32_t seq0, uint32_t pos0) {
+  const ana_config& cf = c->cfg;
+  const uint32_t d = cf.d, f = cf.f;
+  const float* W = c->W;
+  const bool chunk = seq == nullptr;
+  const bool fresh = chunk && (uint64_t)pos0 + B <= cf.ctx;
+  for (uint32_t l = 0; l < cf.layers; l++) {
+    const Blk& b = c->blk[l];
+    // norm + q|k|v (+ the gate's z): dd.gla / dd.sm `pre`
+    GemvArgs g = gemv1(c->X, d, W + b.ra, d, W + b.wq, 3 * d, c->QKV, 3 * d, B);
+    if (b.gla) {
+      g.seg[1] = GemvSeg{W + b.wa, d, c->Z, d};
+      g.nseg = 2;
+    }
+    HIPCHK(c, gemv_timed(c, g, ANA_K_GEMV));
+    if (b.gla) {
+      if (chunk) {
+        HIPCHK(c, launch_gla_chunk(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr,
+                                   c->state + (uint64_t)seq0 * c->seq_stride + c->layer_off[l], c->O,
+                                   d, cf.heads, cf.rglru, B, c->st));
+      } else {
+        // S read and written once per sequence, q|k|v|z in, o out
+        ProfScope ps(c, ANA_K_GLA, (double)B * (8.0 * cf.heads * (d / cf.heads) * (d / cf.heads) + 4.0 * 5 * d));
+        HIPCHK(c, launch_gla_step(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), seq,
+                                  c->O, d, cf.heads, cf.rglru, B, c->st));
+      }
+    } else {
+      AttnArgs a{};
+      a.gq = cf.qk ? W + b.gq : nullptr;
+      a.gk = cf.qk ? W + b.gk : nullptr;
+      a.sink = cf.sinks ? W + b.sink : nullptr;
+      a.KV = sref(c, l);
+      a.d = d; a.heads = cf.heads; a.ctx = cf.ctx;
+      if (!chunk) {
+        a.QKV = c->QKV; a.O = c->O; a.seq = seq; a.pos = pos; a.B = B; a.write_kv = 1;
+        ProfScope ps(c, ANA_K_ATTN, c->attn_bytes);
+        HIPCHK(c, launch_attn(a, c->st));
+      } else if (fresh) {
+        // before the ring wraps: every row's write, then every row's
+        // attention (dd.sm.writes then dd.sm.rows)
+        HIPCHK(c, launch_kv_write(c->QKV, a.gk, a.KV, seq0, pos0, d, cf.heads, cf.ctx, B, c->st));
+        a.QKV = c->QKV; a.O = c->O; a.seq = nullptr; a.seq0 = seq0; a.pos = nullptr; a.pos0 = pos0;
+        a.B = B; a.write_kv = 0;
+        HIPCHK(c, launch_attn(a, c->st));
+      } else {
+        // past the wrap: each token's write and attention in turn (dd.sm.toks)
+        for (uint32_t t = 0; t < B; t++) {
+          a.QKV = c->QKV + (size_t)t * 3 * d; a.O = c->O + (size_t)t * d;
+          a.seq = nullptr; a.seq0 = seq0; a.pos = nullptr; a.pos0 = pos0 + t; a.B = 1; a.write_kv = 1;
+          HIPCHK(c, launch_attn(a, c->st));
+        }
+      }
+    }
+    // M.tail: xa = x + Wo o; hh = silu(g) * u on norm(xa); x = xa + Wd hh
+    GemvArgs wo = gemv1(c->O, d, nullptr, d, W + b.wo, d, c->XA, d, B);
+    wo.mode = GM_RESID; wo.R = c->X; wo.ldr = d;
+    HIPCHK(c, gemv_timed(c, wo, ANA_K_GEMV));
+    GemvArgs gu = gemv1(c->XA, d, W + b.rf, d, W + b.wg, f, c->HH, f, B);
+    gu.seg[1] = GemvSeg{W + b.wu, f, c->HH, f};
+    gu.nseg = 2;
+    gu.mode = GM_SILU;
+    HIPCHK(c, gemv_timed(c, gu, ANA_K_GEMV));
+    GemvArgs wd = gemv1(c->HH, f, nullptr, f, W + b.wd, d, c->X, d, B);
+    wd.mode = GM_RESID; wd.R = c->XA; wd.ldr = d;
+    HIPCHK(c, gemv_timed(c, wd, ANA_K_GEMV));
+  }
+  return ANA_OK;
+}
+
+// head on B rows of src: final RMSNorm, then the tied embedding
+static int run_head(ana_ctx* c, const float* src, uint32_t B) {
+  const ana_config& cf = c->cfg;
+  GemvArgs h = gemv1(src, cf.d, c->W + c->fin, cf.d, c->W, cf.vocab, c->LG, cf.vocab, B);
+  HIPCHK(c, gemv_timed(c, h, ANA_K_HEAD));
+  return ANA_OK;
+}
+
+// algorithmic bytes of one softmax layer's attention for rows at these
+// positions: the live K and V rows read, the new k and v written, q in, o out
+static double attn_bytes_of(const ana_ctx* c, const uint32_t* pos, uint32_t n, uint32_t plus) {
+  const ana_config& cf = c->cfg;
+  double b = 0.0;
+  for (uint32_t i = 0; i < n; i++) {
+    const uint64_t p = (uint64_t)pos[i] + plus;
+    const uint64_t live = std::min<uint64_t>(p, cf.ctx - 1) + 1;
+    b += 4.0 * cf.d * (2.0 * live + 2.0 + 3.0 + 1.0);
+  }
+  return b;
+}
+
+static int check_seqs(ana_ctx* c, const char* fn, uint32_t n, const uint32_t* seq) {
+  if (n == 0 || n > c->max_seqs || !seq) return fail(c, ANA_EINVAL, "%s: %u sequences (1..%u)", fn, n, c->max_seqs);
+  std::vector<uint8_t> seen(c->max_seqs, 0);
+  for (uint32_t i = 0; i < n; i++) {
+    if (seq[i] >= c->max_seqs) return fail(c, ANA_EINVAL, "%s: sequence %u outside 0..%u", fn, seq[i], c->max_seqs - 1);
+    if (seen[seq[i]]++) return fail(c, ANA_EINVAL, "%s: sequence %u listed twice", fn, seq[i]);
+  }
+  return ANA_OK;
+}
+
+extern "C" int ana_feed(ana_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+                        const uint32_t* tok) {
+  if (!c) return ANA_EINVAL;
+  if (int r = check_seqs(c, "ana_feed", n, seq)) return r;
+  if (!pos || !tok) return fail(c, ANA_EINVAL, "ana_feed: null argument");
+  for (uint32_t i = 0; i < n; i++)
+    if (tok[i] >= c->cfg.vocab) return fail(c, ANA_EINVAL, "ana_feed: token %u outside the vocabulary", tok[i]);
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipMemcpyAsync(c->d_seq, seq, 4 * n, hipMemcpyHostToDevice, c->st));
+  HIPCHK(c, hipMemcpyAsync(c->d_pos, pos, 4 * n, hipMemcpyHostToDevice, c->st));
+  HIPCHK(c, hipMemcpyAsync(c->d_tok, tok, 4 * n, hipMemcpyHostToDevice, c->st));
+  HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, n, c->X, c->st));
+  if (c->prof) c->attn_bytes = attn_bytes_of(c, pos, n, 0);
+  if (int r = run_layers(c, n, c->d_seq, c->d_pos, 0, 0)) return r;
+  HIPCHK(c, launch_scatter_rows(c->X, c->d_seq, n, c->cfg.d, c->xs, c->st));
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  return ANA_OK;
+}
+
+extern "C" int ana_feeds(ana_ctx* c, uint32_t seq, uint32_t pos, const uint32_t* toks, uint32_t len) {
+  if (!c) return ANA_EINVAL;
+  if (seq >= c->max_seqs) return fail(c, ANA_EINVAL, "ana_feeds: sequence %u outside 0..%u", seq, c->max_seqs - 1);
+  if (len == 0) return ANA_OK;
+  if (!toks) return fail(c, ANA_EINVAL, "ana_feeds: null tokens");
+  for (uint32_t i = 0; i < len; i++)
+    if (toks[i] >= c->cfg.vocab) return fail(c, ANA_EINVAL, "ana_feeds: token %u outside the vocabulary", toks[i]);
+  HIPCHK(c, hipSetDevice(c->device));
+  for (uint32_t t0 = 0; t0 < len; t0 += c->chunk) {
+    const uint32_t T = std::min(c->chunk, len - t0);
+    HIPCHK(c, hipMemcpyAsync(c->d_tok, toks + t0, 4 * T, hipMemcpyHostToDevice, c->st));
+    HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, T, c->X, c->st));
+    if (int r = run_layers(c, T, nullptr, nullptr, seq, pos + t0)) return r;
+    HIPCHK(c, hipMemcpyAsync(c->xs + (uint64_t)seq * c->cfg.d, c->X + (uint64_t)(T - 1) * c->cfg.d,
+                             4 * c->cfg.d, hipMemcpyDeviceToDevice, c->st));
+  }
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  return ANA_OK;
+}
+
+static int head_of(ana_ctx* c, const char* fn, uint32_t n, const uint32_t* seq) {
+  if (int r = check_seqs(c, fn, n, seq)) return r;
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipMemcpyAsync(c->d_seq, seq, 4 * n, hipMemcpyHostToDevice, c->st));
+  HIPCHK(c, launch_gather_rows(c->xs, c->d_seq, n, c->cfg.d, c->X, c->st));
+  return run_head(c, c->X, n);
+}
+
+extern "C" int ana_logits(ana_ctx* c, uint32_t n, const uint32_t* seq, float* out) {
+  if (!c) return ANA_EINVAL;
+  if (!out) return fail(c, ANA_EINVAL, "ana_logits: null output");
+  if (int r = head_of(c, "ana_logits", n, seq)) return r;
+  HIPCHK(c, hipMemcpyAsync(out, c->LG, (size_t)4 * n * c->cfg.vocab, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  return ANA_OK;
+}
+
+extern "C" int ana_top(ana_ctx* c, uint32_t n, const uint32_t* seq, uint32_t* tok) {
+  if (!c) return ANA_EINVAL;
+  if (!tok) return fail(c, ANA_EINVAL, "ana_top: null output");
+  if (int r = head_of(c, "ana_top", n, seq)) return r;
+  HIPCHK(c, launch_top(c->LG, c->cfg.vocab, n, c->d_pick, c->st));
+  HIPCHK(c, hipMemcpyAsync(tok, c->d_pick, 4 * n, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  return ANA_OK;
+}
+
+static PickArgs pick_args(ana_ctx* c, uint32_t n, const ana_sampling* s, uint32_t store_first) {
+  PickArgs p{};
+  p.logits = c->LG;
+  p.vocab = c->cfg.vocab;
+  p.B = n;
+  p.temp = s ? s->temperature : 0.0f;
+  p.topk = s ? s->top_k : 0xFFFFFFFFu;
+  p.topp = s ? s->top_p : 1.0f;
+  p.rng = c->d_rng;
+  p.tok = c->d_pick;
+  p.store_first = store_first;
+  return p;
+}
+
+extern "C" int ana_pick(ana_ctx* c, uint32_t n, const uint32_t* seq, const ana_sampling* s,
+                        uint64_t* rng, uint32_t* tok) {
+  if (!c) return ANA_EINVAL;
+  if (!s || !tok) return fail(c, ANA_EINVAL, "ana_pick: null argument");
+  const bool greedy = s->temperature <= 0.0f;
+  if (!greedy && !rng) return fail(c, ANA_EINVAL, "ana_pick: sampling needs rng state");
+  if (int r = head_of(c, "ana_pick", n, seq)) return r;
+  if (!greedy) HIPCHK(c, hipMemcpyAsync(c->d_rng, rng, 32 * n, hipMemcpyHostToDevice, c->st));
+  HIPCHK(c, launch_pick(pick_args(c, n, s, 0), c->st));
+  HIPCHK(c, hipMemcpyAsync(tok, c->d_pick, 4 * n, hipMemcpyDeviceToHost, c->st));
+  if (!greedy) HIPCHK(c, hipMemcpyAsync(rng, c->d_rng, 32 * n, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  return ANA_OK;
+}
+
+extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+                            const uint32_t* tok, uint32_t steps, const ana_sampling* s,
+                            uint64_t* rng, uint32_t* out) {
+  if (!c) return ANA_EINVAL;
+  if (int r = check_seqs(c, "ana_generate", n, seq)) return r;
+  if (!pos || !tok || (steps && !out)) return fail(c, ANA_EINVAL, "ana_generate: null argument");
+  const bool greedy = !s || s->temperature <= 0.0f;
+  if (!greedy && !rng) return fail(c, ANA_EINVAL, "ana_generate: sampling needs rng state");
+  for (uint32_t i = 0; i < n; i++)
+    if (tok[i] >= c->cfg.vocab) return fail(c, ANA_EINVAL, "ana_generate: token %u outside the vocabulary", tok[i]);
+  if (steps == 0) return ANA_OK;
+  HIPCHK(c, hipSetDevice(c->device));
+  const size_t need = (size_t)n * steps;
+  if (need > c->out_cap) {
+    if (c->d_out) HIPCHK(c, hipFree(c->d_out));
+    c->d_out = nullptr;
+    c->out_cap = 0;
+    HIPCHK(c, dalloc(&c->d_out, need));
+    c->out_cap = need;
+  }
+  HIPCHK(c, hipMemcpyAsync(c->d_seq, seq, 4 * n, hipMemcpyHostToDevice, c->st));
+  HIPCHK(c, hipMemcpyAsync(c->d_pos, pos, 4 * n, hipMemcpyHostToDevice, c->st));
+  HIPCHK(c, hipMemcpyAsync(c->d_tok, tok, 4 * n, hipMemcpyHostToDevice, c->st));
+  if (!greedy) HIPCHK(c, hipMemcpyAsync(c->d_rng, rng, 32 * n, hipMemcpyHostToDevice, c->st));
+  const PickArgs pa = pick_args(c, n, greedy ? nullptr : s, 1);
+  for (uint32_t k = 0; k < steps; k++) {
+    HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, n, c->X, c->st));
+    if (c->prof) c->attn_bytes = attn_bytes_of(c, pos, n, k);
+    if (int r = run_layers(c, n, c->d_seq, c->d_pos, 0, 0)) return r;
+    if (int r = run_head(c, c->X, n)) return r;
+    {
+      ProfScope ps(c, ANA_K_PICK, 4.0 * n * c->cfg.vocab);
+      HIPCHK(c, launch_pick(pa, c->st));
+    }
+    HIPCHK(c, launch_advance(c->d_pos, c->d_tok, c->d_pick, c->d_out, steps, k, n, c->st));
+  }
+  HIPCHK(c, launch_scatter_rows(c->X, c->d_seq, n, c->cfg.d, c->xs, c->st));
+  HIPCHK(c, hipMemcpyAsync(out, c->d_out, 4 * need, hipMemcpyDeviceToHost, c->st));
+  if (!greedy) HIPCHK(c, hipMemcpyAsync(rng, c->d_rng, 32 * n, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  return ANA_OK;
+}
+
+extern "C" int ana_prof(ana_ctx* c, int on) {
+  if (!c) return ANA_EINVAL;
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  c->prof = on != 0;
+  c->recs.clear();
+  return ANA_OK;
+}
+
+extern "C" int ana_prof_read(ana_ctx* c, uint32_t kind, uint64_t* launches, double* ms,
+                             double* bytes) {
+  if (!c || kind >= ANA_K_KINDS) return ANA_EINVAL;
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  uint64_t n = 0;
+  double t = 0.0, by = 0.0;
+  for (size_t i = 0; i < c->recs.size(); i++) {
+    if (c->recs[i].kind != kind) continue;
+    float e = 0.0f;
+    HIPCHK(c, hipEventElapsedTime(&e, c->ev[2 * i], c->ev[2 * i + 1]));
+    n++;
+    t += e;
+    by += c->recs[i].bytes;
+  }
+  if (launches) *launches = n;
+  if (ms) *ms = t;
+  if (bytes) *bytes = by;
+  return ANA_OK;
+}
+
+extern "C" int ana_state(ana_ctx* c, uint32_t seq, uint32_t layer, float* out, size_t n) {
+  if (!c || !out) return ANA_EINVAL;
+  if (seq >= c->max_seqs || layer > c->cfg.layers) return fail(c, ANA_EINVAL, "ana_state: no such sequence or layer");
+  const float* src;
+  size_t cnt;
+  if (layer == c->cfg.layers) {
+    src = c->xs + (uint64_t)seq * c->cfg.d;
+    cnt = c->cfg.d;
+  } else {
+    src = c->state + (uint64_t)seq * c->seq_stride + c->layer_off[layer];
+    const uint64_t end = layer + 1 < c->cfg.layers ? c->layer_off[layer + 1] : c->seq_stride;
+    cnt = end - c->layer_off[layer];
+  }
+  if (n != cnt) return fail(c, ANA_EINVAL, "ana_state: layer %u holds %zu floats, not %zu", layer, cnt, n);
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipMemcpyAsync(out, src, 4 * cnt, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  return ANA_OK;
+}

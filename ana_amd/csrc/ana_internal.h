@@ -1,0 +1,142 @@
+// Internal declarations shared by libana's translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/ana.h"
+
+namespace ana {
+
+// One layer's parameter offsets in the FTC2 vector (BP of
+// bend/Dense/Layout.bend:99-100, placed by BP.gla.at / BP.sm.at, 627-655).
+struct Blk {
+  bool gla;
+  uint64_t ra, wq, wk, wv, wo, wa, lam, gq, gk, sink, rf, wg, wu, wd, end;
+};
+
+uint64_t params_of(const ana_config& c);                       // Config.params
+std::string model_id_of(const ana_config& c);                  // Config.model_id
+std::vector<Blk> layout_of(const ana_config& c, uint64_t* fin); // BP.list, blocks.end
+
+// A checkpoint read from disk: config, step, and the parameter bytes exactly
+// as stored (big-endian f32), so the device does the byte swap.
+struct Ftc2 {
+  ana_config cfg;
+  uint64_t step = 0;
+  std::vector<uint8_t> raw;   // P * 4 bytes, big-endian
+};
+// Returns "" on success, else the reference's message.
+std::string read_ftc2(const char* path, Ftc2* out);
+
+// ---------------------------------------------------------------- kernels
+// Every kernel computes in IEEE f32 with products and sums rounded
+// separately (compiled with -ffp-contract=off) and exp/log through double,
+// so each output takes the reference's F32 steps in the reference's order.
+
+// A matrix-vector product over a batch of rows, y[b][o] = sum_q x[b][q] W[o][q]
+// (q ascending from 0.0f), over up to two row segments.
+struct GemvSeg {
+  const float* W;     // [rows][K] row-major
+  uint32_t rows;
+  float* Y;           // output rows: Y[b * ldy + o]
+  uint32_t ldy;
+};
+enum GemvMode : uint32_t {
+  GM_PLAIN = 0,       // y = s
+  GM_RESID = 1,       // y = r + s (add2 of bend/Dense/Model.bend:44-45)
+  GM_SILU = 2,        // seg0 gate rows, seg1 up rows: y = silu(g) * u
+};
+struct GemvArgs {
+  const float* X;     // [B][ldx]
+  uint32_t ldx;
+  const float* ng;    // RMSNorm gains over K (nullptr: x used as is)
+  uint32_t K;
+  GemvSeg seg[2];
+  uint32_t nseg;
+  uint32_t mode;
+  const float* R;     // GM_RESID: residual rows R[b * ldr + o]
+  uint32_t ldr;
+  uint32_t B;         // batch rows
+  uint32_t rows_wg;   // output rows per workgroup
+  uint32_t bt;        // batch rows per workgroup
+  uint32_t qc;        // K chunk staged in LDS
+};
+hipError_t launch_gemv(const GemvArgs& a, hipStream_t st);
+// the tile shape launch_gemv uses for a product (exposed for tests/bench)
+void gemv_shape(uint32_t rows, uint32_t K, uint32_t B, uint32_t mode, GemvArgs* a);
+
+// Per-sequence state addressing: a sequence's states start at
+// base + seq * seq_stride; a layer's at + layer_off.
+struct StateRef {
+  float* base;
+  uint64_t seq_stride;
+  uint64_t layer_off;
+};
+
+hipError_t launch_embed(const float* E, const uint32_t* tok, uint32_t d, uint32_t B, float* X,
+                        hipStream_t st);
+hipError_t launch_bswap(uint32_t* w, uint64_t n, hipStream_t st);
+
+// GLA decode step for B sequences (one token each): per-head L2 norms, the
+// gate, S' = al S + kh v^T in place, o = qh^T S'.
+hipError_t launch_gla_step(const float* QKV, const float* Z, const float* lam, StateRef S,
+                           const uint32_t* seq, float* O, uint32_t d, uint32_t heads,
+                           uint32_t rglru, uint32_t B, hipStream_t st);
+// GLA over T tokens of one sequence, token after token (S kept on chip).
+hipError_t launch_gla_chunk(const float* QKV, const float* Z, const float* lam, float* S,
+                            float* O, uint32_t d, uint32_t heads, uint32_t rglru, uint32_t T,
+                            hipStream_t st);
+
+// Softmax attention over the ring for B (seq, pos) rows. write_kv: qk-norm
+// and write this row's k and v into its slot first (the decode step); else
+// the slots were written before (a chunk before the ring wraps).
+struct AttnArgs {
+  const float* QKV;     // [B][3d]
+  const float* gq;      // qk-norm gains (nullptr when off)
+  const float* gk;
+  const float* sink;    // per-head sink logits (nullptr when off)
+  StateRef KV;          // K ring [ctx][d] then V ring [ctx][d]
+  const uint32_t* seq;  // per row: state slot (nullptr: all rows seq0)
+  uint32_t seq0;
+  const uint32_t* pos;  // per row position (device)
+  uint32_t pos0;        // when pos is nullptr: row b is at pos0 + b
+  float* O;             // [B][d]
+  uint32_t d, heads, ctx, B, write_kv;
+};
+hipError_t launch_attn(const AttnArgs& a, hipStream_t st);
+// write k (qk-normed) and v of T rows at positions pos0.. into the rings
+hipError_t launch_kv_write(const float* QKV, const float* gk, StateRef KV, uint32_t seq,
+                           uint32_t pos0, uint32_t d, uint32_t heads, uint32_t ctx, uint32_t T,
+                           hipStream_t st);
+
+// dd.pick over B logit rows: least index reaching the max, vocab on NaN
+hipError_t launch_top(const float* logits, uint32_t vocab, uint32_t B, uint32_t* tok,
+                      hipStream_t st);
+// S.pick over B logit rows
+struct PickArgs {
+  const float* logits;  // [B][vocab]
+  uint32_t vocab, B;
+  float temp;
+  uint32_t topk;
+  float topp;
+  uint64_t* rng;        // [B][4]
+  uint32_t* tok;
+  uint32_t store_first; // greedy as the dense engine picks: dd.top, and
+                        // Sample.argmax only when dd.top answers vocab
+};
+hipError_t launch_pick(const PickArgs& a, hipStream_t st);
+
+// small helpers for the token loop
+hipError_t launch_gather_rows(const float* src, const uint32_t* idx, uint32_t n, uint32_t d,
+                              float* dst, hipStream_t st);
+hipError_t launch_scatter_rows(const float* src, const uint32_t* idx, uint32_t n, uint32_t d,
+                               float* dst, hipStream_t st);
+hipError_t launch_advance(uint32_t* pos, uint32_t* tok, const uint32_t* pick, uint32_t* out,
+                          uint32_t steps, uint32_t step, uint32_t B, hipStream_t st);
+hipError_t launch_zero(float* p, uint64_t n, hipStream_t st);
+
+}  // namespace ana

@@ -1,0 +1,303 @@
+// S.pick (bend/Sample.bend:95-254) on the device, one workgroup per sequence.
+//
+// The reference keeps the logits in a left-packed binary tree of depth
+// dv = depth(vocab) (bend/Tensor.bend) and every sum and max is that tree's
+// pairwise reduction. Here a thread owns LPT consecutive leaves; it reduces
+// them pairwise in registers, then lanes combine with xor partners (level m
+// joins the groups that differ in lane bit m, left group first) and waves
+// combine the same way through LDS: each partial is a node of the
+// reference's tree, so the results are its bits. Absent leaves (index >=
+// vocab, the tree's VZ) count 0.0 in sums and -3e38 in the max, as V.sum and
+// V.max give VZ; Sample.argmax gives VZ the pair (-3e38, 0).
+#include "ana_internal.h"
+#include "numerics.h"
+
+#pragma clang fp contract(off)
+
+namespace ana {
+
+namespace {
+
+struct Add { __device__ float operator()(float a, float b) const { return a + b; } };
+// F32.max a b = (a < b ? b : a): a is the left subtree
+struct Max { __device__ float operator()(float a, float b) const { return a < b ? b : a; } };
+
+template <int LPT, class Op>
+__device__ __forceinline__ float local_reduce(const float (&x)[LPT], Op op) {
+  float t[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; i++) t[i] = x[i];
+#pragma unroll
+  for (int s = 1; s < LPT; s *= 2)
+#pragma unroll
+    for (int i = 0; i < LPT; i += 2 * s) t[i] = op(t[i], t[i + s]);
+  return t[0];
+}
+
+// The tree above the threads: NT = leaves/LPT threads, a power of two.
+template <class Op>
+__device__ float tree_up(float v, Op op, float* red, uint32_t tid, uint32_t NT) {
+  const uint32_t lane = tid & 63;
+  for (uint32_t m = 1; m < 64 && m < NT; m <<= 1) {
+    const float o = __shfl_xor(v, m, 64);
+    v = (lane & m) ? op(o, v) : op(v, o);
+  }
+  if (NT <= 64) {
+    // every lane of the first group holds the root; share lane 0's
+    if (tid == 0) red[0] = v;
+    __syncthreads();
+    const float r = red[0];
+    __syncthreads();
+    return r;
+  }
+  const uint32_t nw = NT >> 6;
+  if (lane == 0 && (tid >> 6) < nw) red[tid >> 6] = v;
+  __syncthreads();
+  float w[16];
+  for (uint32_t i = 0; i < nw; i++) w[i] = red[i];
+  for (uint32_t s = 1; s < nw; s *= 2)
+    for (uint32_t i = 0; i < nw; i += 2 * s) w[i] = op(w[i], w[i + s]);
+  __syncthreads();
+  return w[0];
+}
+
+// Sample.argmax's pairs: the right one wins only when strictly greater
+__device__ __forceinline__ void best_join(float& av, uint32_t& ai, float bv, uint32_t bi) {
+  if (bv > av) { av = bv; ai = bi; }
+}
+
+template <int LPT>
+__device__ uint32_t tree_argmax(const float (&x)[LPT], uint32_t base, uint32_t vocab, float* redf,
+                                uint32_t* redi, uint32_t tid, uint32_t NT) {
+  float v[LPT];
+  uint32_t ix[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; i++) {
+    const bool here = base + i < vocab;
+    v[i] = here ? x[i] : -3.0e38f;
+    ix[i] = here ? base + i : 0u;
+  }
+#pragma unroll
+  for (int s = 1; s < LPT; s *= 2)
+#pragma unroll
+    for (int i = 0; i < LPT; i += 2 * s) best_join(v[i], ix[i], v[i + s], ix[i + s]);
+  float bv = v[0];
+  uint32_t bi = ix[0];
+  const uint32_t lane = tid & 63;
+  for (uint32_t m = 1; m < 64 && m < NT; m <<= 1) {
+    const float ov = __shfl_xor(bv, m, 64);
+    const uint32_t oi = __shfl_xor(bi, m, 64);
+    if (lane & m) {  // partner is the left subtree
+      float lv = ov;
+      uint32_t li = oi;
+      best_join(lv, li, bv, bi);
+      bv = lv;
+      bi = li;
+    } else {
+      best_join(bv, bi, ov, oi);
+    }
+  }
+  if (NT <= 64) {
+    if (tid == 0) redi[0] = bi;
+    __syncthreads();
+    const uint32_t r = redi[0];
+    __syncthreads();
+    return r;
+  }
+  const uint32_t nw = NT >> 6;
+  if (lane == 0 && (tid >> 6) < nw) {
+    redf[tid >> 6] = bv;
+    redi[tid >> 6] = bi;
+  }
+  __syncthreads();
+  float wv[16];
+  uint32_t wi[16];
+  for (uint32_t i = 0; i < nw; i++) { wv[i] = redf[i]; wi[i] = redi[i]; }
+  for (uint32_t s = 1; s < nw; s *= 2)
+    for (uint32_t i = 0; i < nw; i += 2 * s) best_join(wv[i], wi[i], wv[i + s], wi[i + s]);
+  __syncthreads();
+  return wi[0];
+}
+
+__device__ __forceinline__ uint64_t rotl64(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+
+// Rng.next (bend/Sample.bend:57-66): the file's transition, which is not
+// textbook xoshiro256** (s0' and s1' differ)
+__device__ uint64_t rng_next(uint64_t* r) {
+  const uint64_t s0 = r[0], s1 = r[1], s2 = r[2], s3 = r[3];
+  const uint64_t t = s1 << 17;
+  const uint64_t w = rotl64(s1 * 5, 7) * 9;
+  r[0] = (s0 ^ s3) ^ (s1 ^ s2);
+  r[1] = s1 ^ s2;
+  r[2] = (s2 ^ s0) ^ t;
+  r[3] = rotl64(s3 ^ s1, 45);
+  return w;
+}
+
+}  // namespace
+
+template <int LPT>
+__global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t dv) {
+  __shared__ float red[16];
+  __shared__ uint32_t redi[16];
+  __shared__ float heap[2048];
+  __shared__ float leaf[LPT];
+  __shared__ uint32_t who;
+  const uint32_t b = blockIdx.x, tid = threadIdx.x;
+  const uint32_t v = a.vocab;
+  const uint32_t base = tid * LPT;
+  const bool active = tid < NT;
+  const float* lg = a.logits + (size_t)b * v;
+  float x[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; i++) x[i] = (active && base + i < v) ? lg[base + i] : 0.0f;
+
+  // greedy on the store (dc.px.top, bend/Decode.bend:407-418): dd.pick's
+  // least index reaching the max; only a NaN max falls back to argmax
+  if (a.temp <= 0.0f && a.store_first) {
+    float r = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < LPT; i++)
+      if (active && base + i < v) r = x[i] > r ? x[i] : r;
+    for (uint32_t m = 1; m < 64; m <<= 1) {
+      const float o = __shfl_xor(r, m, 64);
+      r = o > r ? o : r;
+    }
+    if ((tid & 63) == 0) red[tid >> 6] = r;
+    __syncthreads();
+    float top = red[0];
+    for (int w = 1; w < 16; w++) top = red[w] > top ? red[w] : top;
+    uint32_t best = v;
+#pragma unroll
+    for (int i = LPT - 1; i >= 0; i--)
+      if (active && base + i < v && top <= x[i]) best = base + i;
+    for (uint32_t m = 1; m < 64; m <<= 1) {
+      const uint32_t o = __shfl_xor(best, m, 64);
+      best = o < best ? o : best;
+    }
+    __syncthreads();
+    if ((tid & 63) == 0) redi[tid >> 6] = best;
+    __syncthreads();
+    uint32_t bb = redi[0];
+    for (int w = 1; w < 16; w++) bb = redi[w] < bb ? redi[w] : bb;
+    __syncthreads();
+    if (bb < v) {
+      if (tid == 0) a.tok[b] = bb;
+      return;
+    }
+  }
+  // greedy: Sample.argmax over the tree, the rng untouched
+  if (a.temp <= 0.0f) {
+    const uint32_t t = tree_argmax<LPT>(x, base, v, red, redi, tid, NT);
+    if (tid == 0) a.tok[b] = t;
+    return;
+  }
+  // peak = V.max(logits)
+  float pm[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; i++) pm[i] = (active && base + i < v) ? x[i] : -3.0e38f;
+  const float peak = tree_up(local_reduce<LPT>(pm, Max()), Max(), red, tid, NT);
+
+  // top-k: the largest t in [peak-100, peak] (40 bisection steps) keeping
+  // at least k logits >= t; the rest go to -3e38 (sample.topk)
+  if (a.topk < v) {
+    const float need = (float)a.topk;
+    float lo = peak - 100.0f, hi = peak;
+    for (int it = 0; it < 40; it++) {
+      const float mid = 0.5f * (lo + hi);
+      float c[LPT];
+#pragma unroll
+      for (int i = 0; i < LPT; i++) c[i] = (active && base + i < v && x[i] >= mid) ? 1.0f : 0.0f;
+      const float cnt = tree_up(local_reduce<LPT>(c, Add()), Add(), red, tid, NT);
+      if (cnt >= need) lo = mid; else hi = mid;
+    }
+#pragma unroll
+    for (int i = 0; i < LPT; i++) x[i] = x[i] >= lo ? x[i] : -3.0e38f;
+  }
+  // w = exp((x - peak) / temp) (exp.at); absent leaves stay 0
+  float w[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; i++) w[i] = (active && base + i < v) ? dexp((x[i] - peak) / a.temp) : 0.0f;
+
+  // top-p: the largest t in [0, 1] whose kept mass reaches p of the total
+  if (a.topp < 1.0f) {
+    const float need = a.topp * tree_up(local_reduce<LPT>(w, Add()), Add(), red, tid, NT);
+    float lo = 0.0f, hi = 1.0f;
+    for (int it = 0; it < 40; it++) {
+      const float mid = 0.5f * (lo + hi);
+      float c[LPT];
+#pragma unroll
+      for (int i = 0; i < LPT; i++) c[i] = w[i] >= mid ? w[i] : 0.0f;
+      const float mass = tree_up(local_reduce<LPT>(c, Add()), Add(), red, tid, NT);
+      if (mass >= need) lo = mid; else hi = mid;
+    }
+#pragma unroll
+    for (int i = 0; i < LPT; i++) w[i] = w[i] >= lo ? w[i] : 0.0f;
+  }
+
+  // the draw: thread sums into a heap of the tree above the threads, then
+  // draw.go walks from the root (left iff u < sum(left) or the right is VZ)
+  if (active) heap[NT + tid] = local_reduce<LPT>(w, Add());
+  __syncthreads();
+  for (uint32_t n = NT >> 1; n >= 1; n >>= 1) {
+    for (uint32_t i = tid; i < n; i += 1024) heap[n + i] = heap[2 * (n + i)] + heap[2 * (n + i) + 1];
+    __syncthreads();
+  }
+  uint32_t pbase = 0;
+  float u = 0.0f;
+  int p = (int)dv;
+  if (tid == 0) {
+    uint64_t* r = a.rng + (size_t)b * 4;
+    const uint64_t word = rng_next(r);
+    const float unit = (float)(uint32_t)((word >> 32) >> 8) / 16777216.0f;
+    u = unit * heap[1];
+    const uint32_t lptlog = __builtin_ctz(LPT);
+    while (p > (int)lptlog) {
+      const uint32_t half = 1u << (p - 1);
+      const float ml = heap[(NT * LPT) / half + pbase / half];
+      const bool left = (u < ml) || (pbase + half >= v);
+      if (!left) { u = u - ml; pbase += half; }
+      p--;
+    }
+    who = pbase / LPT;
+  }
+  __syncthreads();
+  if (tid == who) {
+#pragma unroll
+    for (int i = 0; i < LPT; i++) leaf[i] = w[i];
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float tmp[LPT];
+    while (p > 0) {
+      const uint32_t half = 1u << (p - 1);
+      const uint32_t off = pbase % LPT;
+      for (uint32_t i = 0; i < half; i++) tmp[i] = leaf[off + i];
+      for (uint32_t s = 1; s < half; s *= 2)
+        for (uint32_t i = 0; i < half; i += 2 * s) tmp[i] = tmp[i] + tmp[i + s];
+      const float ml = tmp[0];
+      const bool left = (u < ml) || (pbase + half >= v);
+      if (!left) { u = u - ml; pbase += half; }
+      p--;
+    }
+    a.tok[b] = pbase;
+  }
+}
+
+hipError_t launch_pick(const PickArgs& a, hipStream_t st) {
+  uint32_t dv = 0;
+  while ((1ull << dv) < a.vocab) dv++;
+  const uint64_t vpad = 1ull << dv;
+  uint32_t lpt = vpad > 1024 ? (uint32_t)(vpad / 1024) : 1u;
+  const uint32_t NT = (uint32_t)(vpad / lpt);
+  switch (lpt) {
+#define ANA_PICK(L) \
+  case L: hipLaunchKernelGGL(k_pick<L>, dim3(a.B), dim3(1024), 0, st, a, NT, dv); break;
+    ANA_PICK(1) ANA_PICK(2) ANA_PICK(4) ANA_PICK(8) ANA_PICK(16) ANA_PICK(32) ANA_PICK(64)
+#undef ANA_PICK
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace ana

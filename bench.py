@@ -1,0 +1,217 @@
+"""Decode throughput of libana on one MI355X (BASELINE.json's metric).
+
+Workload: the reference's 115M model at ctx 2048 (fp100m: d 768, f 2048,
+12 layers 9 GLA + 3 softmax, 12 heads, vocab 32768, RG-LRU, qk-norm, sinks),
+random-init weights in an FTC2 file this script writes, synthetic prompts.
+A step is one token for every sequence of the batch: the whole decode step
+(embedding, 12 layers, LM head, greedy pick on the device), run by
+ana_generate's on-device token loop with inputs already in HBM.
+
+B = 1 (the headline `value`): a 1920-token prompt through chunked prefill,
+then W warm-up and K timed decode steps at positions 1920+ (the full
+2048-slot window). B = 64 is reported beside it (128-token prompts).
+
+The roofline entry is the dominant kernel, the exact matrix-vector product:
+its algorithmic bytes (weights once, activations in and out) over its
+launches' HIP-event time on the library's stream, against 8 TB/s.
+cpu_baseline: the CPU oracle (a restatement of the reference's dense
+decoder; the reference's Bend toolchain is absent) on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import ana_amd  # noqa: E402
+from ana_amd import ckpt  # noqa: E402
+from ana_amd import config as cf  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def ensure_ckpt(c: cf.Config, path: str) -> str:
+    want = len(ckpt.manifest_bytes(c)) + 8 + 4 * c.params + 16
+    if not (os.path.exists(path) and os.path.getsize(path) == want):
+        t = time.perf_counter()
+        ckpt.write(path, c, ckpt.init_params(c, "normal", 0))
+        log(f"wrote {path} ({want / 1e6:.0f} MB) in {time.perf_counter() - t:.1f}s")
+    return path
+
+
+def step_bytes(c: cf.Config, positions) -> float:
+    """Algorithmic HBM bytes of one decode step: every weight once (the tied
+    head reads all of E; the gather reads one row per sequence), per
+    sequence the GLA states read and written and the live K/V rows read."""
+    w = 4.0 * (c.params - c.vocab * c.d + c.vocab * c.d)
+    per = 0.0
+    for p in positions:
+        live = min(p, c.ctx - 1) + 1
+        per += c.gla_layers * 2 * c.heads * c.hd * c.hd * 4.0
+        per += c.softmax_layers * (2 * live * c.d * 4.0 + 2 * c.d * 4.0)
+    return w + per
+
+
+def run_batch(path: str, c: cf.Config, B: int, prompt: int, warmup: int, steps: int, prof_steps: int):
+    seqs = list(range(B))
+    with ana_amd.Decoder(path, max_seqs=B, prefill_chunk=64) as dec:
+        t = time.perf_counter()
+        first, pos = [], []
+        for b in seqs:
+            pr = ckpt.prompt(b, prompt, c.vocab)
+            dec.feeds(b, 0, pr[:-1])
+            first.append(int(pr[-1]))
+            pos.append(prompt - 1)
+        log(f"B={B}: prefill {B}x{prompt - 1} tokens in {time.perf_counter() - t:.2f}s")
+        tok = np.array(first, dtype=np.uint32)
+        pos = np.array(pos, dtype=np.uint32)
+        if warmup:
+            out = dec.generate(seqs, pos, tok, warmup)
+            tok, pos = out[:, -1].copy(), pos + warmup
+        t0 = time.perf_counter()
+        out = dec.generate(seqs, pos, tok, steps)
+        t1 = time.perf_counter()
+        positions = [int(p) + k for k in range(steps) for p in pos]
+        tok, pos = out[:, -1].copy(), pos + steps
+        dec.prof(True)
+        dec.generate(seqs, pos, tok, prof_steps)
+        stats = dec.prof_read()
+        dec.prof(False)
+    dt = t1 - t0
+    sb = step_bytes(c, positions) / steps
+    return {
+        "tok_s": B * steps / dt,
+        "ms_per_step": 1000.0 * dt / steps,
+        "step_bytes": sb,
+        "step_gbs": sb * steps / dt / 1e9,
+        "stats": stats,
+    }
+
+
+def cpu_baseline(path: str, c: cf.Config, seconds: float) -> dict:
+    """The oracle's dense decode on the host cores, bounded to ~`seconds`."""
+    from oracle import oracle as O
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    O.set_threads(threads)
+    m = O.Model(path)
+    st = O.State(m)
+    pr = ckpt.prompt(0, 8, c.vocab)
+    for p, t in enumerate(pr):
+        st.feed(p, int(t))
+    pos, n = len(pr), 0
+    tok = O.top(st.logits())
+    t0 = time.perf_counter()
+    while True:
+        st.feed(pos, tok)
+        tok = O.top(st.logits())
+        pos += 1
+        n += 1
+        if time.perf_counter() - t0 > seconds or n >= 512:
+            break
+    dt = time.perf_counter() - t0
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": n / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+        "sample": (f"CPU oracle (C restatement of the reference's dense decoder, AVX2 no-FMA, "
+                   f"pthreads) greedy decode of {n} tokens at positions 8..{pos - 1}, B=1, same "
+                   f"115M ctx-2048 checkpoint; it scores every ring slot as the reference does, so "
+                   f"a token costs the same at any position; {cpu}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--prompt", type=int, default=1920)
+    ap.add_argument("--b64", type=int, default=1, help="also measure B=64 (1/0)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--ckpt", default=os.environ.get("ANA_BENCH_CKPT", "/tmp/ana_bench_fp100m.ftc2"))
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print("bench.py: this build measures one GPU only; the decode path shards by sequence "
+              "with no collective (see DESIGN.md), so run --gpus 1.", file=sys.stderr)
+        return 2
+    c = cf.FP100M
+    path = ensure_ckpt(c, a.ckpt)
+    r1 = run_batch(path, c, 1, a.prompt, a.warmup, a.steps, min(a.steps, 32))
+    g = r1["stats"]["gemv"]
+    h = r1["stats"]["head"]
+    launches, ms, by = g[0] + h[0], g[1] + h[1], g[2] + h[2]
+    achieved = by / (ms / 1e3) / 1e9 if ms > 0 else 0.0
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        try:
+            traffic = json.load(open(tpath)).get("gemv_exact_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    extra = {}
+    if a.b64:
+        r64 = run_batch(path, c, 64, 128, 2, 32, 8)
+        extra["b64"] = {k: r64[k] for k in ("tok_s", "ms_per_step", "step_gbs")}
+        extra["b64"]["workload"] = "B=64, 128-token prompts, 32 greedy steps at positions 129+"
+    cpu = cpu_baseline(path, c, a.cpu_seconds) if a.cpu_seconds > 0 else None
+    kern = {k: {"launches": v[0], "ms": round(v[1], 4), "gb": round(v[2] / 1e9, 4)}
+            for k, v in r1["stats"].items()}
+    line = {
+        "metric": "decode tok/s for 115M ctx2048 at B=1 and B=64; % of HBM roofline",
+        "value": round(r1["tok_s"], 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(r1["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: random-init N(0,0.02) FTC2 checkpoint (seed 0), uniform-random prompts",
+        "config": {
+            "workload": "115M fp100m (d768 f2048 L12 h12 v32768, RG-LRU, qk-norm, sinks) ctx 2048 "
+                        "greedy decode, B=1, 1920-token prompt, exact fp32 (bit-exact with the "
+                        "reference's CPU kernels)",
+            "batch": 1, "prompt": a.prompt, "ctx": c.ctx, "numerics": "exact_fp32",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k_gemv_exact (layer products + LM head)",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 5),
+            "traffic": traffic,
+            "launches": launches,
+            "avg_launch_us": round(1e3 * ms / max(launches, 1), 3),
+        },
+        "step_gbs": round(r1["step_gbs"], 2),
+        "step_frac": round(r1["step_gbs"] / HBM_PEAK_GBS, 5),
+        "kernels": kern,
+        "cpu_baseline": cpu,
+        **extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,155 @@
+/*
+ * libana -- MI355X (gfx950) decoder token loop for hhefesto/ana checkpoints.
+ *
+ * A plain C ABI over hand-written HIP kernels. It replaces the dense engine
+ * seam of bend/Decode.bend (EDense, driven through Dd.dd.{load, feed, feeds,
+ * logits, top, reset} of bend/Dense/Decode.bend:531-699) at engine
+ * granularity: one call runs a whole decode step (every layer), not one
+ * bulk op.
+ *
+ * Conventions
+ *   - Every int-returning function answers 0 on success, or a nonzero
+ *     ANA_E* code; ana_error(ctx) (or ana_error(NULL) after a failed
+ *     ana_open) then holds the message, using the reference's wording where
+ *     the reference has one (e.g. "checkpoint: short read").
+ *   - Host buffers are the caller's, read or written only during the call.
+ *     Device memory is the library's.
+ *   - A context is single-threaded: the caller serialises calls on it, as
+ *     the reference serialises the GPU with FT.mu (bend/effs/bulk.c:79-92).
+ *     Every call returns after its device work has completed.
+ *   - Sequences are slots 0 .. max_seqs-1 of a context; each keeps its own
+ *     recurrent state (GLA S per layer and head, softmax K/V rings) and the
+ *     residual row of the last token fed, as one dense store does for one
+ *     sequence in the reference.
+ *   - Positions count tokens from 0 per sequence; the softmax ring slot is
+ *     pos mod ctx and the last live slot min(pos, ctx-1)
+ *     (bend/Dense/Decode.bend:540-545).
+ */
+#ifndef ANA_H
+#define ANA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ANA_ABI_VERSION 1
+
+/* error codes */
+#define ANA_OK 0
+#define ANA_EINVAL 1     /* bad argument (sequence, position, token, size) */
+#define ANA_ECKPT 2      /* checkpoint rejected (Manifest.problem, short read, ...) */
+#define ANA_EDEVICE 3    /* HIP error: "device fault" */
+#define ANA_ENOMEM 4     /* device allocation failed */
+#define ANA_EUNSUP 5     /* configuration outside what the kernels handle */
+
+/* numerics modes */
+#define ANA_EXACT_FP32 0 /* bit-exact with the reference's CPU kernels */
+
+/* bend/Config.bend:7-10 */
+typedef struct {
+  uint32_t vocab, ctx, d, f, layers, heads;
+  uint32_t rglru, qk, sinks, tied;
+} ana_config;
+
+typedef struct {
+  int device;              /* HIP device ordinal */
+  int numerics;            /* ANA_EXACT_FP32 */
+  uint32_t max_seqs;       /* sequences the context keeps state for (>= 1) */
+  uint32_t prefill_chunk;  /* tokens per prefill chunk; 0 = 64, as ANA_PREFILL_CHUNK */
+} ana_opts;
+
+/* the decoding settings of bend/Decode.bend:147-148,546-548 */
+typedef struct {
+  float temperature;       /* <= 0: greedy (argmax, least index on ties) */
+  uint32_t top_k;          /* on when < vocab (0xFFFFFFFF = off) */
+  float top_p;             /* on when < 1 */
+} ana_sampling;
+
+/* Open an FTC2 checkpoint on a device.
+ * Replaces dc.loaded.dense + Dd.dd.of.n + Dd.dd.load
+ * (bend/Decode.bend:501-520, bend/Dense/Decode.bend:492-518,689-699): the
+ * manifest is validated as Manifest.problem (bend/Checkpoint.bend:162-170),
+ * the parameter count and a tied head are required, and the P big-endian
+ * floats are read into device memory. All sequences start reset. */
+int ana_open(const char* ftc2_path, const ana_opts* opts, struct ana_ctx** out);
+
+/* The checkpoint's config and the Adam step it was saved at. */
+int ana_config_of(const struct ana_ctx* ctx, ana_config* out, uint64_t* step);
+
+/* Zero one sequence's states: dd.reset (bend/Dense/Decode.bend:534-538). */
+int ana_reset(struct ana_ctx* ctx, uint32_t seq);
+
+/* One token into each of n sequences (distinct seq[i]), no head:
+ * dd.feed (bend/Dense/Decode.bend:548-551) for n sequences at once. */
+int ana_feed(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+             const uint32_t* tok);
+
+/* len tokens into one sequence from pos, a chunk at a time: dd.feeds
+ * (bend/Dense/Decode.bend:637-639). In ANA_EXACT_FP32 the states and the
+ * residual row are bit-identical to len ana_feed calls. */
+int ana_feeds(struct ana_ctx* ctx, uint32_t seq, uint32_t pos, const uint32_t* toks, uint32_t len);
+
+/* The head on each listed sequence's last fed token: n x vocab floats,
+ * dd.logits (bend/Dense/Decode.bend:641-646). */
+int ana_logits(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, float* out);
+
+/* Greedy's pick on the device: dd.top (bend/Dense/Decode.bend:475-484,
+ * 648-660), the least index reaching the maximum logit; vocab when no logit
+ * does (a NaN maximum), where the caller falls back to ana_pick. */
+int ana_top(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, uint32_t* tok);
+
+/* S.pick (bend/Sample.bend:246-254) on the device: greedy (tree argmax)
+ * when temperature <= 0, else temperature, top-k and top-p by 40-step
+ * bisections and one inverse-CDF draw in tree order. rng holds n x 4 u64
+ * xoshiro words (bend/Sample.bend:49-93), advanced in place by one draw for
+ * each sampled sequence (untouched when greedy). */
+int ana_pick(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, const ana_sampling* s,
+             uint64_t* rng, uint32_t* tok);
+
+/* Rng.seeded (bend/Sample.bend:68-93): the 4 words for a seed. */
+void ana_rng_seeded(uint64_t seed, uint64_t rng[4]);
+
+/* The token loop of bend/Generate.bend:39-51 on the device, for n sequences
+ * at once: steps times, feed each sequence's current token at its position,
+ * run the head and pick (greedy when s is NULL or temperature <= 0), and
+ * feed the pick back. tok[i] is sequence i's first token at pos[i]; out
+ * receives n x steps picks (row i = sequence i). EOS does not stop the loop;
+ * a caller wanting Generate's stop truncates each row after its first 1.
+ * rng as ana_pick (NULL when greedy). */
+int ana_generate(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+                 const uint32_t* tok, uint32_t steps, const ana_sampling* s, uint64_t* rng,
+                 uint32_t* out);
+
+/* Copy one sequence's state out (for parity checks): layer l's GLA S
+ * (heads x hd x hd floats) or K ring then V ring (2 x ctx x d floats); l ==
+ * layers gives the residual row (d floats). n is the float count of out. */
+int ana_state(struct ana_ctx* ctx, uint32_t seq, uint32_t layer, float* out, size_t n);
+
+/* Kernel timing (no counterpart in the reference; for benchmarks and
+ * profiling). While on, every launch of the listed kinds is bracketed by HIP
+ * events on the context's stream and its algorithmic bytes are counted;
+ * ana_prof_read sums them since the last ana_prof(ctx, 1). */
+#define ANA_K_GEMV 0     /* the layers' matrix-vector products */
+#define ANA_K_HEAD 1     /* the LM head's product */
+#define ANA_K_ATTN 2     /* softmax attention over the ring */
+#define ANA_K_GLA 3      /* the GLA state update and readout */
+#define ANA_K_PICK 4     /* greedy pick / sampler */
+#define ANA_K_KINDS 5
+int ana_prof(struct ana_ctx* ctx, int on);
+int ana_prof_read(struct ana_ctx* ctx, uint32_t kind, uint64_t* launches, double* ms,
+                  double* bytes);
+
+/* The last error on ctx, or of the last failed ana_open when ctx is NULL. */
+const char* ana_error(const struct ana_ctx* ctx);
+
+void ana_close(struct ana_ctx* ctx);
+
+typedef struct ana_ctx ana_ctx;
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,233 @@
+"""libana on the GPU against the CPU oracle, bit for bit (ANA_EXACT_FP32).
+
+The cases are the reference's own (bend/tests/decode-dense.bend,
+bend/tests/prefill-dense.bend): small4_v3 and its no-arms twin, 96 tokens of
+the LCG window on ctx 64 (the ring wraps), the six chunked-prefill runs;
+plus batches of sequences at staggered positions, the on-device token loop,
+the sampler on the model's own logits, and the 115M shape.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import ana_amd
+from ana_amd import ckpt
+from ana_amd import config as cf
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+VEC = json.load(open(os.path.join(HERE, "golden", "reference_vectors.json")))
+CFGS = {"v3-arms": cf.SMALL4_V3, "no-arms": cf.SMALL4_NOARMS}
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def ckpts(tmp_path_factory):
+    d = tmp_path_factory.mktemp("ck")
+    out = {}
+    for name, c in CFGS.items():
+        p = str(d / f"{name}.ftc2")
+        ckpt.write(p, c, ckpt.init_params(c, "hash"))
+        out[name] = p
+    return out
+
+
+@pytest.mark.parametrize("name", list(CFGS))
+def test_feed_bit_exact(oracle, ckpts, name):
+    path = ckpts[name]
+    print(f"case feed {name}", flush=True)
+    m = oracle.Model(path)
+    st = oracle.State(m)
+    with ana_amd.Decoder(path) as dec:
+        for pos, t in enumerate(VEC["window"]):
+            dec.feed([0], [pos], [t])
+            st.feed(pos, t)
+            want = st.logits()
+            got = dec.logits([0])[0]
+            assert np.array_equal(bits(got), bits(want)), (pos, np.abs(got - want).max())
+            assert dec.top([0])[0] == oracle.top(want)
+        for l in range(m.layers):
+            assert np.array_equal(bits(dec.state(0, l)), bits(st.layer(l))), l
+        assert np.array_equal(bits(dec.state(0, m.layers)), bits(st.x()))
+        # a reset then the same tokens: the same bits (decode-dense's law)
+        dec.reset(0)
+        for pos, t in enumerate(VEC["window"][:70]):
+            dec.feed([0], [pos], [t])
+        st.reset()
+        for pos, t in enumerate(VEC["window"][:70]):
+            st.feed(pos, t)
+        assert np.array_equal(bits(dec.logits([0])[0]), bits(st.logits()))
+
+
+@pytest.mark.parametrize("name", list(CFGS))
+def test_chunked_prefill_is_feed(oracle, ckpts, name):
+    """bend/tests/prefill-dense.bend's six runs at chunk 16: states, logits
+    and the greedy pick bit for bit equal to feeding one token at a time."""
+    path = ckpts[name]
+    m = oracle.Model(path)
+    ts = VEC["window"]
+    with ana_amd.Decoder(path, prefill_chunk=VEC["prefill_chunk"]) as dec:
+        for run in VEC["prefill_runs"]:
+            print(f"case prefill {name} {run['name']}", flush=True)
+            xs, pre = ts[: run["n"]], run["pre"]
+            st = oracle.State(m)
+            for pos, t in enumerate(xs):
+                st.feed(pos, t)
+            dec.reset(0)
+            for pos in range(pre):
+                dec.feed([0], [pos], [xs[pos]])
+            dec.feeds(0, pre, xs[pre:])
+            for l in range(m.layers + 1):
+                want = st.layer(l) if l < m.layers else st.x()
+                assert np.array_equal(bits(dec.state(0, l)), bits(want)), (run["name"], l)
+            lg = st.logits()
+            assert np.array_equal(bits(dec.logits([0])[0]), bits(lg))
+            assert dec.top([0])[0] == oracle.top(lg)
+
+
+@pytest.mark.parametrize("name", list(CFGS))
+def test_batched_sequences(oracle, ckpts, name):
+    """Four sequences at staggered positions fed together: each one's bits
+    are its own single-sequence run's."""
+    path = ckpts[name]
+    print(f"case batch {name}", flush=True)
+    m = oracle.Model(path)
+    rng = np.random.default_rng(11)
+    n, steps = 4, 80
+    streams = rng.integers(0, m.vocab, size=(n, steps + 40)).astype(np.uint32)
+    starts = [0, 3, 17, 40]
+    sts = [oracle.State(m) for _ in range(n)]
+    with ana_amd.Decoder(path, max_seqs=6) as dec:
+        seqs = [5, 0, 2, 3]
+        for i, s in enumerate(seqs):
+            dec.feeds(s, 0, streams[i, : starts[i]])
+            for p in range(starts[i]):
+                sts[i].feed(p, int(streams[i, p]))
+        for k in range(steps):
+            pos = [starts[i] + k for i in range(n)]
+            tok = [int(streams[i, pos[i]]) for i in range(n)]
+            dec.feed(seqs, pos, tok)
+            for i in range(n):
+                sts[i].feed(pos[i], tok[i])
+        got = dec.logits(seqs)
+        for i in range(n):
+            assert np.array_equal(bits(got[i]), bits(sts[i].logits())), i
+        tops = dec.top(seqs)
+        for i in range(n):
+            assert tops[i] == oracle.top(got[i])
+
+
+@pytest.mark.parametrize("name", list(CFGS))
+def test_token_loop_greedy(oracle, ckpts, name):
+    """ana_generate's on-device loop = the host loop of Generate.bend on the
+    oracle (feed, head, greedy pick on the store, feed the pick)."""
+    path = ckpts[name]
+    print(f"case generate {name}", flush=True)
+    m = oracle.Model(path)
+    prompts = [VEC["window"][:9], VEC["window"][20:33], VEC["window"][40:45]]
+    steps = 70
+    with ana_amd.Decoder(path, max_seqs=3, prefill_chunk=16) as dec:
+        first, pos0 = [], []
+        for i, pr in enumerate(prompts):
+            dec.feeds(i, 0, pr[:-1])
+            first.append(pr[-1])
+            pos0.append(len(pr) - 1)
+        out = dec.generate([0, 1, 2], pos0, first, steps)
+    for i, pr in enumerate(prompts):
+        st = oracle.State(m)
+        for p, t in enumerate(pr):
+            st.feed(p, t)
+        want = []
+        pos = len(pr)
+        for _ in range(steps):
+            lg = st.logits()
+            t = oracle.top(lg)
+            if t == m.vocab:
+                t = oracle.tree_argmax(lg)
+            want.append(t)
+            st.feed(pos, t)
+            pos += 1
+        assert list(out[i]) == want, i
+
+
+SETTINGS = [(0.8, 40, 0.9), (1.0, 0xFFFFFFFF, 0.95), (0.5, 5, 1.0), (0.8, 0xFFFFFFFF, 1.0),
+            (1.5, 3, 0.5), (0.0, 40, 0.9)]
+
+
+def _check_pick(oracle, dec, seqs, lgs):
+    for temp, k, p in SETTINGS:
+        st = ana_amd.Settings(float(np.float32(temp)), k, float(np.float32(p)))
+        rng = np.stack([oracle.rng_seeded(100 + s) for s in seqs])
+        want_rng = rng.copy()
+        want = [oracle.pick(lgs[i], st.temperature, k, st.top_p, want_rng[i]) for i in range(len(seqs))]
+        got = dec.pick(seqs, st, rng)
+        assert list(got) == want, (temp, k, p)
+        assert np.array_equal(rng, want_rng), (temp, k, p)
+
+
+def test_sampler_small_vocab(oracle, ckpts):
+    path = ckpts["v3-arms"]
+    print("case pick v258", flush=True)
+    with ana_amd.Decoder(path, max_seqs=4) as dec:
+        for s in range(4):
+            dec.feeds(s, 0, VEC["window"][s * 7: s * 7 + 12])
+        seqs = [0, 1, 2, 3]
+        _check_pick(oracle, dec, seqs, dec.logits(seqs))
+
+
+def test_sampler_32k_vocab(oracle, tmp_path):
+    """The v1 config (vocab 32768: a perfect depth-15 tree)."""
+    c = cf.V1
+    path = str(tmp_path / "v1.ftc2")
+    ckpt.write(path, c, ckpt.init_params(c, "normal", 0))
+    print("case pick v32768", flush=True)
+    oracle.set_threads(8)
+    with ana_amd.Decoder(path, max_seqs=3) as dec:
+        pr = ckpt.prompt(0, 16, c.vocab)
+        for s in range(3):
+            dec.feeds(s, 0, pr[s:])
+        lgs = dec.logits([0, 1, 2])
+        _check_pick(oracle, dec, [0, 1, 2], lgs)
+        # the model's logits are the oracle's too
+        m = oracle.Model(path)
+        st = oracle.State(m)
+        st.feeds(0, [int(t) for t in pr[1:]])
+        assert np.array_equal(bits(lgs[1]), bits(st.logits()))
+
+
+def test_115m_shape(oracle, tmp_path):
+    """fp100m's dimensions (d 768, f 2048, 12 layers, 12 heads, vocab 32768,
+    all arms) at ctx 2048: a prompt through feeds, then steps, bit for bit."""
+    c = cf.FP100M
+    path = str(tmp_path / "fp100m.ftc2")
+    ckpt.write(path, c, ckpt.init_params(c, "normal", 0))
+    print("case 115m", flush=True)
+    oracle.set_threads(8)
+    m = oracle.Model(path)
+    st = oracle.State(m)
+    pr = [int(t) for t in ckpt.prompt(1, 12, c.vocab)]
+    with ana_amd.Decoder(path, max_seqs=2) as dec:
+        dec.feeds(1, 0, pr[:10])
+        for p in range(10):
+            st.feed(p, pr[p])
+        for p in (10, 11):
+            dec.feed([1], [p], [pr[p]])
+            st.feed(p, pr[p])
+            lg = st.logits()
+            got = dec.logits([1])[0]
+            assert np.array_equal(bits(got), bits(lg)), (p, np.abs(got - lg).max())
+        out = dec.generate([1], [12], [int(oracle.top(lg))], 3)
+    want = []
+    pos, t = 12, int(oracle.top(lg))
+    for _ in range(3):
+        st.feed(pos, t)
+        t = oracle.top(st.logits())
+        want.append(t)
+        pos += 1
+    assert list(out[0]) == want

@@ -1,0 +1,336 @@
+"""The CPU oracle pinned against the reference's own known answers and laws.
+
+These run without a GPU. They hold the oracle (oracle/ana_oracle.c) to:
+- the U64 known answers of bend/tests/num.bend and the file's RNG transition;
+- greedy's tie vectors (bend/tests/decode-dense.bend:199-220);
+- the dense step within 1e-5 relative of the tree meaning before and after
+  the ring wraps, reset => same bits, store pick = tree argmax
+  (bend/tests/decode-dense.bend:13-22);
+- closed forms on hand-built weights (uniform attention, zero blocks,
+  the sink in the denominator, the GLA state recurrence), so a mistake
+  shared by both restatements still fails;
+- the sampler's thresholds against brute force and its draw against the
+  cumulative mass.
+"""
+import json
+import math
+import os
+import struct
+
+import numpy as np
+import pytest
+
+from ana_amd import ckpt
+from ana_amd import config as cf
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+VEC = json.load(open(os.path.join(HERE, "golden", "reference_vectors.json")))
+M64 = (1 << 64) - 1
+
+
+def u64(hl):
+    return (hl[0] << 32) | hl[1]
+
+
+def rotl(x, k):
+    return ((x << k) | (x >> (64 - k))) & M64
+
+
+def test_num_kats(oracle):
+    k = VEC["num_kats"]
+    assert f"{(u64(k['mul']['a']) * u64(k['mul']['b'])) & M64:016x}" == k["mul"]["hex"]
+    assert f"{rotl(u64(k['rotl45']['a']), 45):016x}" == k["rotl45"]["hex"]
+    assert f"{u64(k['shr30']['a']) >> 30:016x}" == k["shr30"]["hex"]
+    assert f"{(u64(k['add']['a']) + u64(k['add']['b'])) & M64:016x}" == k["add"]["hex"]
+    assert f"{oracle.u64_read(k['read']['s']):016x}" == k["read"]["hex"]
+    assert struct.unpack(">f", bytes(k["f32_from_bits"]["bytes"]))[0] == k["f32_from_bits"]["value"]
+    # U64.read: a non-digit poisons, the empty string is None, overflow wraps
+    assert oracle.u64_read("12a") is None
+    assert oracle.u64_read("") is None
+    assert oracle.u64_read("18446744073709551616") == 0
+
+
+def _splitmix(s):
+    s2 = (s + 0x9E3779B97F4A7C15) & M64
+    z = ((s2 ^ (s2 >> 30)) * 0xBF58476D1CE4E5B9) & M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M64
+    return z ^ (z >> 31), s2
+
+
+def test_rng_is_the_files_transition(oracle):
+    """Rng.seeded and Rng.next expanded by hand from bend/Sample.bend:57-93,
+    with the two constants of the transition that differ from textbook
+    xoshiro256** (s0' includes s2, s1' excludes s0)."""
+    for seed in (0, 1, 42, 2 ** 63 + 5):
+        st, s = [], seed
+        for _ in range(4):
+            z, s = _splitmix(s)
+            st.append(z)
+        r = oracle.rng_seeded(seed)
+        assert [int(x) for x in r] == st
+        for _ in range(5):
+            s0, s1, s2, s3 = st
+            w = (rotl((s1 * 5) & M64, 7) * 9) & M64
+            st = [s0 ^ s3 ^ s1 ^ s2, s1 ^ s2, s2 ^ s0 ^ ((s1 << 17) & M64), rotl(s3 ^ s1, 45)]
+            assert oracle.rng_next(r) == w
+            assert [int(x) for x in r] == st
+    # and it is not textbook xoshiro: the second draw differs
+    r = oracle.rng_seeded(7)
+    s0, s1, s2, s3 = [int(x) for x in r]
+    oracle.rng_next(r)
+    tb1 = s1 ^ s2 ^ s0
+    assert int(r[1]) != tb1 or s0 == 0
+
+
+def test_tie_vectors(oracle):
+    for xs, want in zip(VEC["ties"], VEC["tie_picks"]):
+        lg = np.array([float(x) for x in xs], dtype=np.float32)
+        assert oracle.top(lg) == want
+        assert oracle.tree_argmax(lg) == want
+
+
+def test_store_pick_nan_and_inf(oracle):
+    lg = np.array([np.nan, 5.0, 5.0, 1.0], dtype=np.float32)
+    assert oracle.top(lg) == 1           # NaN never reaches the max
+    assert oracle.top(np.full(4, np.nan, dtype=np.float32)) == 4  # vocab: the fallback signal
+    lg = np.array([-np.inf, -np.inf, -np.inf], dtype=np.float32)
+    assert oracle.top(lg) == 0
+
+
+def _ckpt(tmp_path, c, kind="hash", seed=0, name="m.ftc2"):
+    p = ckpt.init_params(c, kind, seed)
+    path = str(tmp_path / name)
+    ckpt.write(path, c, p)
+    return path, p
+
+
+@pytest.mark.parametrize("c", [cf.SMALL4_V3, cf.SMALL4_NOARMS], ids=["v3-arms", "no-arms"])
+def test_dense_matches_meaning(oracle, tmp_path, c):
+    """bend/tests/decode-dense.bend: 96 positions on ctx 64 (the ring wraps);
+    dense vs tree within 1e-5 relative on each side of the wrap; a reset
+    reproduces the bits; the store pick is the tree argmax at every position."""
+    path, _ = _ckpt(tmp_path, c)
+    m = oracle.Model(path)
+    st, tr = oracle.State(m), oracle.Tree(m)
+    ts = VEC["window"]
+    dense, tree = [], []
+    for pos, t in enumerate(ts):
+        st.feed(pos, t)
+        dense.append(st.logits())
+        tree.append(tr.step(pos, t))
+    dense, tree = np.array(dense), np.array(tree)
+    for seg in (slice(0, c.ctx), slice(c.ctx, None)):
+        d = np.abs(dense[seg] - tree[seg]).max()
+        s = np.abs(tree[seg]).max()
+        assert d / s <= 1e-5, (seg, d, s)
+    st.reset()
+    again = []
+    for pos, t in enumerate(ts):
+        st.feed(pos, t)
+        again.append(st.logits())
+    assert np.array_equal(np.array(again).view(np.uint32), dense.view(np.uint32))
+    for lg in dense:
+        assert oracle.top(lg) == oracle.tree_argmax(lg)
+
+
+def _blank(c):
+    """Parameters with every matrix zero, gains 1, nothing else set."""
+    blocks, fin = cf.layout(c)
+    p = np.zeros(c.params, dtype=np.float32)
+    for b in blocks:
+        p[b.ra:b.ra + c.d] = 1.0
+        p[b.rf:b.rf + c.d] = 1.0
+    p[fin:fin + c.d] = 1.0
+    return p, blocks, fin
+
+
+def test_zero_blocks_leave_the_residual(oracle):
+    """With zero matrices every block adds exactly 0, so the logits are
+    E . rmsnorm(E[tok]) (a closed form independent of summation order up to
+    rounding)."""
+    c = cf.Config(64, 16, 32, 48, 4, 2, True, True, True)
+    p, _, _ = _blank(c)
+    rng = np.random.default_rng(1)
+    E = rng.standard_normal((c.vocab, c.d)).astype(np.float32)
+    p[: c.vocab * c.d] = E.reshape(-1)
+    m = oracle.Model(cfg=c, params=p)
+    st = oracle.State(m)
+    for pos, tok in enumerate([3, 9, 9, 1]):
+        st.feed(pos, tok)
+        x = E[tok].astype(np.float64)
+        assert np.array_equal(st.x(), E[tok])
+        want = E.astype(np.float64) @ (x / np.sqrt((x * x).mean() + 1e-5))
+        np.testing.assert_allclose(st.logits(), want, rtol=2e-6, atol=2e-6)
+
+
+def test_attention_closed_form(oracle):
+    """Wq = Wk = 0 makes every score 0: the softmax is uniform over the live
+    slots, and with sinks each head's denominator gains exp(sink - max(0,
+    sink)). Wv = I and Wo = I then put the mean of the live values (scaled
+    by the sink) into the residual; the MLP is off (Wd = 0)."""
+    c = cf.Config(16, 8, 8, 8, 4, 2, False, False, True)
+    p, blocks, fin = _blank(c)
+    rng = np.random.default_rng(2)
+    E = rng.standard_normal((c.vocab, c.d)).astype(np.float32)
+    p[: c.vocab * c.d] = E.reshape(-1)
+    sm = blocks[3]
+    d = c.d
+    p[sm.wv:sm.wv + d * d] = np.eye(d, dtype=np.float32).reshape(-1)
+    p[sm.wo:sm.wo + d * d] = np.eye(d, dtype=np.float32).reshape(-1)
+    sinks = np.array([0.5, -1.0], dtype=np.float32)
+    p[sm.sink:sm.sink + c.heads] = sinks
+    m = oracle.Model(cfg=c, params=p)
+    st = oracle.State(m)
+    toks = [1, 4, 7, 2, 9, 11, 3, 5, 6, 8, 10]    # 11 tokens on ctx 8: wraps
+    for pos, t in enumerate(toks):
+        st.feed(pos, t)
+        x = E[t].astype(np.float64)
+        nrm = x / np.sqrt((x * x).mean() + 1e-5)
+        live = [E[u].astype(np.float64) / np.sqrt((E[u].astype(np.float64) ** 2).mean() + 1e-5)
+                for u in toks[max(0, pos - c.ctx + 1): pos + 1]]
+        V = np.array(live)
+        want = x.copy()
+        hd = c.hd
+        for h in range(c.heads):
+            mx = max(0.0, float(sinks[h]))
+            w = np.exp(0.0 - mx)
+            den = w * len(live) + math.exp(float(sinks[h]) - mx)
+            want[h * hd:(h + 1) * hd] += (w * V[:, h * hd:(h + 1) * hd]).sum(0) / den
+        np.testing.assert_allclose(st.x(), want, rtol=2e-5, atol=2e-6)
+        del nrm
+
+
+def test_gla_state_closed_form(oracle):
+    """One GLA layer with sigmoid gates: Wa = 0 gives alpha = 1/2 exactly;
+    Wq = Wk = Wv = I. Then S_t = S_{t-1}/2 + k^ v^T with k^ the per-head L2
+    normalised key, and the state is checked against that recurrence in
+    float64 (the residual stream is irrelevant: Wo = Wd = 0)."""
+    c = cf.Config(16, 8, 8, 8, 1, 2, False, False, False)
+    p, blocks, fin = _blank(c)
+    rng = np.random.default_rng(3)
+    E = rng.standard_normal((c.vocab, c.d)).astype(np.float32)
+    p[: c.vocab * c.d] = E.reshape(-1)
+    b = blocks[0]
+    d, hd = c.d, c.hd
+    for w in (b.wq, b.wk, b.wv):
+        p[w:w + d * d] = np.eye(d, dtype=np.float32).reshape(-1)
+    m = oracle.Model(cfg=c, params=p)
+    st = oracle.State(m)
+    S = np.zeros((c.heads, hd, hd))
+    for pos, t in enumerate([2, 5, 5, 13, 0, 7]):
+        st.feed(pos, t)
+        x = E[t].astype(np.float64)
+        n = x / np.sqrt((x * x).mean() + 1e-5)
+        for h in range(c.heads):
+            k = n[h * hd:(h + 1) * hd]
+            kh = k / np.sqrt(1e-6 + (k * k).sum())
+            S[h] = 0.5 * S[h] + np.outer(kh, k)
+        np.testing.assert_allclose(st.layer(0).reshape(S.shape), S, rtol=1e-5, atol=1e-6)
+
+
+def test_rglru_state_closed_form(oracle):
+    """One GLA layer with the RG-LRU gate: Wa = 0 gives z = 0, sigmoid(z) =
+    1/2, so la = min(-1e-4, 4 log sigmoid(lam)) (Griffin's gate at c = 8),
+    alpha = exp(la) and the key is scaled by sqrt(1 - alpha^2). With
+    Wq = Wk = Wv = I the state follows S_t = alpha S_{t-1} + (s k^) v^T,
+    checked in float64."""
+    c = cf.Config(16, 8, 8, 8, 1, 2, True, False, False)
+    p, blocks, fin = _blank(c)
+    rng = np.random.default_rng(6)
+    E = rng.standard_normal((c.vocab, c.d)).astype(np.float32)
+    p[: c.vocab * c.d] = E.reshape(-1)
+    b = blocks[0]
+    d, hd = c.d, c.hd
+    for w in (b.wq, b.wk, b.wv):
+        p[w:w + d * d] = np.eye(d, dtype=np.float32).reshape(-1)
+    lam = np.array([4.0, 2.0, 0.5, -1.0, 9.0, 12.0, 0.0, 3.0], dtype=np.float32)
+    p[b.lam:b.lam + d] = lam
+    m = oracle.Model(cfg=c, params=p)
+    st = oracle.State(m)
+    lam64 = lam.astype(np.float64)
+    la = np.minimum(-1e-4, 4.0 * -np.log1p(np.exp(-lam64)))
+    alpha, scale = np.exp(la), np.sqrt(1 - np.exp(2 * la))
+    S = np.zeros((c.heads, hd, hd))
+    for pos, t in enumerate([2, 5, 5, 13, 0, 7]):
+        st.feed(pos, t)
+        x = E[t].astype(np.float64)
+        n = x / np.sqrt((x * x).mean() + 1e-5)
+        for h in range(c.heads):
+            k = n[h * hd:(h + 1) * hd]
+            kh = k / np.sqrt(1e-6 + (k * k).sum()) * scale[h * hd:(h + 1) * hd]
+            S[h] = alpha[h * hd:(h + 1) * hd, None] * S[h] + np.outer(kh, k)
+        np.testing.assert_allclose(st.layer(0).reshape(S.shape), S, rtol=1e-5, atol=1e-6)
+
+
+def test_sampler_thresholds_and_draw(oracle):
+    rng = np.random.default_rng(4)
+    for v in (258, 1000, 4096, 32768):
+        lg = (rng.standard_normal(v) * 3).astype(np.float32)
+        for k in (1, 5, 40):
+            t = oracle.topk_threshold(lg, k)
+            kth = np.sort(lg)[::-1][k - 1]
+            assert (lg >= t).sum() >= k
+            # the bisection stops within float spacing below the k-th largest
+            assert kth - 100 * 2.0 ** -39 - 8 * np.spacing(np.abs(kth)) <= t <= kth
+        w = np.exp((lg - lg.max()) / 0.8).astype(np.float32)
+        for p_ in (0.5, 0.9):
+            t = oracle.topp_threshold(w, p_)
+            assert w[w >= t].astype(np.float64).sum() >= p_ * w.astype(np.float64).sum() * (1 - 1e-5)
+        # top-k 1 is the argmax, whatever the temperature and top-p
+        r = oracle.rng_seeded(9)
+        assert oracle.pick(lg, 1.3, 1, 0.9, r) == int(np.argmax(lg))
+        # greedy leaves the rng untouched
+        r0 = r.copy()
+        assert oracle.pick(lg, 0.0, 40, 0.9, r) == oracle.tree_argmax(lg)
+        assert np.array_equal(r, r0)
+
+
+def test_draw_follows_cumulative_mass(oracle):
+    """With top-k and top-p off the draw is inverse CDF over index order:
+    the pick i satisfies cum[i-1] <= u*total < cum[i] up to rounding."""
+    rng = np.random.default_rng(5)
+    v = 512
+    lg = rng.standard_normal(v).astype(np.float32)
+    seeds = range(200)
+    counts = np.zeros(v)
+    for s in seeds:
+        r = oracle.rng_seeded(s)
+        r2 = r.copy()
+        word = oracle.rng_next(r2)
+        unit = ((word >> 32) >> 8) / 16777216.0
+        w = np.exp((lg.astype(np.float64) - lg.max()) / 1.0)
+        cum = np.cumsum(w)
+        u = unit * cum[-1]
+        i = oracle.pick(lg, 1.0, 0xFFFFFFFF, 1.0, r)
+        assert np.array_equal(r, r2)
+        lo = cum[i - 1] if i else 0.0
+        assert lo - 1e-4 * cum[-1] <= u <= cum[i] + 1e-4 * cum[-1]
+        counts[i] += 1
+    assert counts.sum() == len(seeds)
+
+
+def test_ftc2_round_trip_and_errors(oracle, tmp_path):
+    c = cf.SMALL4_V3
+    path, p = _ckpt(tmp_path, c, "normal", 3)
+    assert ckpt.read_config(path) == c
+    m = oracle.Model(path)
+    assert m.vocab == c.vocab and m.step == 0
+    assert oracle.params(c) == c.params
+    assert oracle.model_id(c) == c.model_id
+    raw = open(path, "rb").read()
+    bad = tmp_path / "bad.ftc2"
+    bad.write_bytes(b"FTC3" + raw[4:])
+    with pytest.raises(ValueError, match="magic is not FTC2"):
+        oracle.Model(str(bad))
+    bad.write_bytes(raw[: len(raw) - 20])
+    with pytest.raises(ValueError, match="short read"):
+        oracle.Model(str(bad))
+
+
+def test_params_formula():
+    # bend/Config.bend:243-253 at the reference's 115M (arms off / on) and
+    # BASELINE's f = 3072 variant
+    assert cf.Config(32768, 2048, 768, 2048, 12, 12, False, False, False).params == 115_428_096
+    assert cf.FP100M.params == 115_435_428
+    assert cf.Config(32768, 2048, 768, 3072, 12, 12, False, False, False).params == 143_739_648
+    assert cf.V1.params == 12_781_824
