@@ -31,12 +31,26 @@ struct ana_ctx {
   float* state = nullptr;            // [max_seqs][seq_stride]
   float* xs = nullptr;               // [max_seqs][d]
   // workspace, wb rows
-  float *X = nullptr, *XA = nullptr, *QKV = nullptr, *Z = nullptr, *O = nullptr, *HH = nullptr;
+  float *X = nullptr, *XA = nullptr, *XN = nullptr, *QKV = nullptr, *Z = nullptr, *O = nullptr,
+        *HH = nullptr;
   float* LG = nullptr;               // [max_seqs][vocab]
-  uint32_t *d_seq = nullptr, *d_pos = nullptr, *d_tok = nullptr, *d_pick = nullptr, *d_out = nullptr;
+  uint32_t *d_seq = nullptr, *d_pos = nullptr, *d_tok = nullptr, *d_pick = nullptr, *d_out = nullptr,
+           *d_step = nullptr;
   uint64_t* d_rng = nullptr;
+  unsigned long long* d_amax = nullptr;  // [wb] greedy argmax keys
   size_t out_cap = 0;
   std::string err;
+  // one decode step of ana_generate captured as a HIP graph, replayed per step
+  hipGraphExec_t gexec = nullptr;
+  struct GKey {
+    uint32_t n, steps;
+    float temp, topp;
+    uint32_t topk;
+    const uint32_t* out;
+    bool operator==(const GKey& o) const {
+      return n == o.n && steps == o.steps && temp == o.temp && topp == o.topp && topk == o.topk && out == o.out;
+    }
+  } gkey{};
   // kernel timing (ana_prof)
   bool prof = false;
   double attn_bytes = 0.0;           // per softmax-layer launch of the current step
@@ -102,8 +116,9 @@ static hipError_t dalloc(T** p, size_t n) {
 static void release(ana_ctx* c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
-  void* ps[] = {c->W, c->state, c->xs, c->X, c->XA, c->QKV, c->Z, c->O, c->HH, c->LG,
-                c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_rng};
+  if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
+  void* ps[] = {c->W, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
+                c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax};
   for (void* p : ps)
     if (p) (void)hipFree(p);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
@@ -183,6 +198,9 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = dalloc(&c->xs, (uint64_t)d * c->max_seqs)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->X, wb * d)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->XA, wb * d)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->XN, wb * d)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->d_step, 2)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->d_amax, wb)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->QKV, wb * 3 * d)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->Z, wb * d)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->O, wb * d)) != hipSuccess) return bad(e);
@@ -244,15 +262,31 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g, uint32_t kind) {
   return launch_gemv(g, c->st);
 }
 
-static GemvArgs gemv1(const float* X, uint32_t ldx, const float* ng, uint32_t K, const float* W,
-                      uint32_t rows, float* Y, uint32_t ldy, uint32_t B) {
+static GemvArgs gemv1(const float* X, uint32_t ldx, uint32_t K, const float* W, uint32_t rows,
+                      float* Y, uint32_t ldy, uint32_t B) {
   GemvArgs a{};
-  a.X = X; a.ldx = ldx; a.ng = ng; a.K = K;
+  a.X = X; a.ldx = ldx; a.K = K;
   a.seg[0] = GemvSeg{W, rows, Y, ldy};
   a.nseg = 1;
   a.mode = GM_PLAIN;
   a.B = B;
   return a;
+}
+
+// RMSNorm(X; g) then the product: inside the product for small batches,
+// else a norm kernel into XN first
+static int norm_gemv(ana_ctx* c, const float* X, const float* g, GemvArgs a, uint32_t kind) {
+  if (a.B <= kSmallB) {
+    a.X = X;
+    a.ldx = c->cfg.d;
+    a.ng = g;
+  } else {
+    HIPCHK(c, launch_rmsnorm(X, g, c->cfg.d, a.B, c->XN, c->st));
+    a.X = c->XN;
+    a.ldx = c->cfg.d;
+  }
+  HIPCHK(c, gemv_timed(c, a, kind));
+  return ANA_OK;
 }
 
 // every layer for B rows of X (embedded already). Row b is sequence seq[b]
@@ -267,13 +301,13 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
   const bool fresh = chunk && (uint64_t)pos0 + B <= cf.ctx;
   for (uint32_t l = 0; l < cf.layers; l++) {
     const Blk& b = c->blk[l];
-    // norm + q|k|v (+ the gate's z): dd.gla / dd.sm `pre`
-    GemvArgs g = gemv1(c->X, d, W + b.ra, d, W + b.wq, 3 * d, c->QKV, 3 * d, B);
+    // norm, then q|k|v (+ the gate's z): dd.gla / dd.sm `pre`
+    GemvArgs g = gemv1(c->X, d, d, W + b.wq, 3 * d, c->QKV, 3 * d, B);
     if (b.gla) {
       g.seg[1] = GemvSeg{W + b.wa, d, c->Z, d};
       g.nseg = 2;
     }
-    HIPCHK(c, gemv_timed(c, g, ANA_K_GEMV));
+    if (int r = norm_gemv(c, c->X, W + b.ra, g, ANA_K_GEMV)) return r;
     if (b.gla) {
       if (chunk) {
         HIPCHK(c, launch_gla_chunk(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr,
@@ -293,15 +327,16 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
       a.KV = sref(c, l);
       a.d = d; a.heads = cf.heads; a.ctx = cf.ctx;
       if (!chunk) {
-        a.QKV = c->QKV; a.O = c->O; a.seq = seq; a.pos = pos; a.B = B; a.write_kv = 1;
+        // each sequence's write, then its attention (dd.sm.write, dd.sm.attend)
+        a.QKV = c->QKV; a.O = c->O; a.B = B; a.seq = seq; a.pos = pos; a.write_kv = 1;
         ProfScope ps(c, ANA_K_ATTN, c->attn_bytes);
         HIPCHK(c, launch_attn(a, c->st));
       } else if (fresh) {
         // before the ring wraps: every row's write, then every row's
-        // attention (dd.sm.writes then dd.sm.rows)
-        HIPCHK(c, launch_kv_write(c->QKV, a.gk, a.KV, seq0, pos0, d, cf.heads, cf.ctx, B, c->st));
-        a.QKV = c->QKV; a.O = c->O; a.seq = nullptr; a.seq0 = seq0; a.pos = nullptr; a.pos0 = pos0;
-        a.B = B; a.write_kv = 0;
+        // attention (dd.sm.writes, then dd.sm.rows)
+        a.QKV = c->QKV; a.O = c->O; a.B = B;
+        a.seq = nullptr; a.seq0 = seq0; a.pos = nullptr; a.pos0 = pos0; a.write_kv = 0;
+        HIPCHK(c, launch_kv_write(a, c->st));
         HIPCHK(c, launch_attn(a, c->st));
       } else {
         // past the wrap: each token's write and attention in turn (dd.sm.toks)
@@ -313,26 +348,30 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
       }
     }
     // M.tail: xa = x + Wo o; hh = silu(g) * u on norm(xa); x = xa + Wd hh
-    GemvArgs wo = gemv1(c->O, d, nullptr, d, W + b.wo, d, c->XA, d, B);
+    GemvArgs wo = gemv1(c->O, d, d, W + b.wo, d, c->XA, d, B);
     wo.mode = GM_RESID; wo.R = c->X; wo.ldr = d;
     HIPCHK(c, gemv_timed(c, wo, ANA_K_GEMV));
-    GemvArgs gu = gemv1(c->XA, d, W + b.rf, d, W + b.wg, f, c->HH, f, B);
+    GemvArgs gu = gemv1(c->XA, d, d, W + b.wg, f, c->HH, f, B);
     gu.seg[1] = GemvSeg{W + b.wu, f, c->HH, f};
     gu.nseg = 2;
     gu.mode = GM_SILU;
-    HIPCHK(c, gemv_timed(c, gu, ANA_K_GEMV));
-    GemvArgs wd = gemv1(c->HH, f, nullptr, f, W + b.wd, d, c->X, d, B);
+    if (int r = norm_gemv(c, c->XA, W + b.rf, gu, ANA_K_GEMV)) return r;
+    GemvArgs wd = gemv1(c->HH, f, f, W + b.wd, d, c->X, d, B);
     wd.mode = GM_RESID; wd.R = c->XA; wd.ldr = d;
     HIPCHK(c, gemv_timed(c, wd, ANA_K_GEMV));
   }
   return ANA_OK;
 }
 
-// head on B rows of src: final RMSNorm, then the tied embedding
-static int run_head(ana_ctx* c, const float* src, uint32_t B) {
+// head on B rows of src: final RMSNorm, then the tied embedding. With
+// `greedy`, small batches also leave dd.pick's argmax keys in d_amax (the
+// caller cleared them), larger ones dd.top's picks in d_pick.
+static int run_head(ana_ctx* c, const float* src, uint32_t B, bool greedy) {
   const ana_config& cf = c->cfg;
-  GemvArgs h = gemv1(src, cf.d, c->W + c->fin, cf.d, c->W, cf.vocab, c->LG, cf.vocab, B);
-  HIPCHK(c, gemv_timed(c, h, ANA_K_HEAD));
+  GemvArgs h = gemv1(src, cf.d, cf.d, c->W, cf.vocab, c->LG, cf.vocab, B);
+  if (greedy && B <= kSmallB) h.amax = c->d_amax;
+  if (int r = norm_gemv(c, src, c->W + c->fin, h, ANA_K_HEAD)) return r;
+  if (greedy && B > kSmallB) HIPCHK(c, launch_top(c->LG, cf.vocab, B, c->d_pick, c->st));
   return ANA_OK;
 }
 
@@ -370,7 +409,7 @@ extern "C" int ana_feed(ana_ctx* c, uint32_t n, const uint32_t* seq, const uint3
   HIPCHK(c, hipMemcpyAsync(c->d_seq, seq, 4 * n, hipMemcpyHostToDevice, c->st));
   HIPCHK(c, hipMemcpyAsync(c->d_pos, pos, 4 * n, hipMemcpyHostToDevice, c->st));
   HIPCHK(c, hipMemcpyAsync(c->d_tok, tok, 4 * n, hipMemcpyHostToDevice, c->st));
-  HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, n, c->X, c->st));
+  HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, n, c->X, nullptr, c->st));
   if (c->prof) c->attn_bytes = attn_bytes_of(c, pos, n, 0);
   if (int r = run_layers(c, n, c->d_seq, c->d_pos, 0, 0)) return r;
   HIPCHK(c, launch_scatter_rows(c->X, c->d_seq, n, c->cfg.d, c->xs, c->st));
@@ -389,7 +428,7 @@ extern "C" int ana_feeds(ana_ctx* c, uint32_t seq, uint32_t pos, const uint32_t*
   for (uint32_t t0 = 0; t0 < len; t0 += c->chunk) {
     const uint32_t T = std::min(c->chunk, len - t0);
     HIPCHK(c, hipMemcpyAsync(c->d_tok, toks + t0, 4 * T, hipMemcpyHostToDevice, c->st));
-    HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, T, c->X, c->st));
+    HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, T, c->X, nullptr, c->st));
     if (int r = run_layers(c, T, nullptr, nullptr, seq, pos + t0)) return r;
     HIPCHK(c, hipMemcpyAsync(c->xs + (uint64_t)seq * c->cfg.d, c->X + (uint64_t)(T - 1) * c->cfg.d,
                              4 * c->cfg.d, hipMemcpyDeviceToDevice, c->st));
@@ -403,13 +442,14 @@ static int head_of(ana_ctx* c, const char* fn, uint32_t n, const uint32_t* seq) 
   HIPCHK(c, hipSetDevice(c->device));
   HIPCHK(c, hipMemcpyAsync(c->d_seq, seq, 4 * n, hipMemcpyHostToDevice, c->st));
   HIPCHK(c, launch_gather_rows(c->xs, c->d_seq, n, c->cfg.d, c->X, c->st));
-  return run_head(c, c->X, n);
+  return ANA_OK;
 }
 
 extern "C" int ana_logits(ana_ctx* c, uint32_t n, const uint32_t* seq, float* out) {
   if (!c) return ANA_EINVAL;
   if (!out) return fail(c, ANA_EINVAL, "ana_logits: null output");
   if (int r = head_of(c, "ana_logits", n, seq)) return r;
+  if (int r = run_head(c, c->X, n, false)) return r;
   HIPCHK(c, hipMemcpyAsync(out, c->LG, (size_t)4 * n * c->cfg.vocab, hipMemcpyDeviceToHost, c->st));
   HIPCHK(c, hipStreamSynchronize(c->st));
   return ANA_OK;
@@ -419,7 +459,9 @@ extern "C" int ana_top(ana_ctx* c, uint32_t n, const uint32_t* seq, uint32_t* to
   if (!c) return ANA_EINVAL;
   if (!tok) return fail(c, ANA_EINVAL, "ana_top: null output");
   if (int r = head_of(c, "ana_top", n, seq)) return r;
-  HIPCHK(c, launch_top(c->LG, c->cfg.vocab, n, c->d_pick, c->st));
+  HIPCHK(c, launch_zero_u64(c->d_amax, n, c->st));
+  if (int r = run_head(c, c->X, n, true)) return r;
+  if (n <= kSmallB) HIPCHK(c, launch_keys_to_tok(c->d_amax, c->cfg.vocab, n, c->d_pick, c->st));
   HIPCHK(c, hipMemcpyAsync(tok, c->d_pick, 4 * n, hipMemcpyDeviceToHost, c->st));
   HIPCHK(c, hipStreamSynchronize(c->st));
   return ANA_OK;
@@ -446,11 +488,39 @@ extern "C" int ana_pick(ana_ctx* c, uint32_t n, const uint32_t* seq, const ana_s
   const bool greedy = s->temperature <= 0.0f;
   if (!greedy && !rng) return fail(c, ANA_EINVAL, "ana_pick: sampling needs rng state");
   if (int r = head_of(c, "ana_pick", n, seq)) return r;
+  if (int r = run_head(c, c->X, n, false)) return r;
   if (!greedy) HIPCHK(c, hipMemcpyAsync(c->d_rng, rng, 32 * n, hipMemcpyHostToDevice, c->st));
   HIPCHK(c, launch_pick(pick_args(c, n, s, 0), c->st));
   HIPCHK(c, hipMemcpyAsync(tok, c->d_pick, 4 * n, hipMemcpyDeviceToHost, c->st));
   if (!greedy) HIPCHK(c, hipMemcpyAsync(rng, c->d_rng, 32 * n, hipMemcpyDeviceToHost, c->st));
   HIPCHK(c, hipStreamSynchronize(c->st));
+  return ANA_OK;
+}
+
+// one decode step of the token loop: embed the current tokens, every
+// layer, the head, the pick, then advance (pos + 1, tok = pick, record)
+static int gen_step(ana_ctx* c, uint32_t n, uint32_t steps, const PickArgs& pa, bool greedy) {
+  HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, n, c->X, c->d_amax, c->st));
+  if (int r = run_layers(c, n, c->d_seq, c->d_pos, 0, 0)) return r;
+  if (int r = run_head(c, c->X, n, greedy)) return r;
+  if (!greedy) {
+    ProfScope ps(c, ANA_K_PICK, 4.0 * n * c->cfg.vocab);
+    HIPCHK(c, launch_pick(pa, c->st));
+  }
+  AdvanceArgs ad{};
+  ad.logits = c->LG;
+  ad.vocab = c->cfg.vocab;
+  ad.B = n;
+  ad.steps = steps;
+  ad.amax = greedy && n <= kSmallB ? c->d_amax : nullptr;
+  ad.pick = c->d_pick;
+  ad.greedy = greedy;
+  ad.pos = c->d_pos;
+  ad.tok = c->d_tok;
+  ad.out = c->d_out;
+  ad.step = c->d_step;
+  ProfScope ps(c, ANA_K_PICK, 16.0 * n);
+  HIPCHK(c, launch_advance(ad, c->st));
   return ANA_OK;
 }
 
@@ -468,6 +538,7 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
   HIPCHK(c, hipSetDevice(c->device));
   const size_t need = (size_t)n * steps;
   if (need > c->out_cap) {
+    if (c->gexec) { HIPCHK(c, hipGraphExecDestroy(c->gexec)); c->gexec = nullptr; }
     if (c->d_out) HIPCHK(c, hipFree(c->d_out));
     c->d_out = nullptr;
     c->out_cap = 0;
@@ -478,17 +549,30 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
   HIPCHK(c, hipMemcpyAsync(c->d_pos, pos, 4 * n, hipMemcpyHostToDevice, c->st));
   HIPCHK(c, hipMemcpyAsync(c->d_tok, tok, 4 * n, hipMemcpyHostToDevice, c->st));
   if (!greedy) HIPCHK(c, hipMemcpyAsync(c->d_rng, rng, 32 * n, hipMemcpyHostToDevice, c->st));
+  HIPCHK(c, launch_zero_u32(c->d_step, 2, c->st));
   const PickArgs pa = pick_args(c, n, greedy ? nullptr : s, 1);
-  for (uint32_t k = 0; k < steps; k++) {
-    HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, n, c->X, c->st));
-    if (c->prof) c->attn_bytes = attn_bytes_of(c, pos, n, k);
-    if (int r = run_layers(c, n, c->d_seq, c->d_pos, 0, 0)) return r;
-    if (int r = run_head(c, c->X, n)) return r;
-    {
-      ProfScope ps(c, ANA_K_PICK, 4.0 * n * c->cfg.vocab);
-      HIPCHK(c, launch_pick(pa, c->st));
+  if (c->prof) {
+    // timed launch by launch: no graph
+    for (uint32_t k = 0; k < steps; k++) {
+      c->attn_bytes = attn_bytes_of(c, pos, n, k);
+      if (int r = gen_step(c, n, steps, pa, greedy)) return r;
     }
-    HIPCHK(c, launch_advance(c->d_pos, c->d_tok, c->d_pick, c->d_out, steps, k, n, c->st));
+  } else {
+    ana_ctx::GKey key{n, steps, pa.temp, pa.topp, pa.topk, c->d_out};
+    if (!c->gexec || !(c->gkey == key)) {
+      if (c->gexec) { HIPCHK(c, hipGraphExecDestroy(c->gexec)); c->gexec = nullptr; }
+      hipGraph_t g = nullptr;
+      HIPCHK(c, hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
+      const int r = gen_step(c, n, steps, pa, greedy);
+      const hipError_t ec = hipStreamEndCapture(c->st, &g);
+      if (r) { if (g) (void)hipGraphDestroy(g); return r; }
+      HIPCHK(c, ec);
+      const hipError_t ei = hipGraphInstantiate(&c->gexec, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      HIPCHK(c, ei);
+      c->gkey = key;
+    }
+    for (uint32_t k = 0; k < steps; k++) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
   }
   HIPCHK(c, launch_scatter_rows(c->X, c->d_seq, n, c->cfg.d, c->xs, c->st));
   HIPCHK(c, hipMemcpyAsync(out, c->d_out, 4 * need, hipMemcpyDeviceToHost, c->st));

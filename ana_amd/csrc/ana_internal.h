@@ -53,7 +53,6 @@ enum GemvMode : uint32_t {
 struct GemvArgs {
   const float* X;     // [B][ldx]
   uint32_t ldx;
-  const float* ng;    // RMSNorm gains over K (nullptr: x used as is)
   uint32_t K;
   GemvSeg seg[2];
   uint32_t nseg;
@@ -61,13 +60,28 @@ struct GemvArgs {
   const float* R;     // GM_RESID: residual rows R[b * ldr + o]
   uint32_t ldr;
   uint32_t B;         // batch rows
-  uint32_t rows_wg;   // output rows per workgroup
-  uint32_t bt;        // batch rows per workgroup
-  uint32_t qc;        // K chunk staged in LDS
+  const float* ng;    // RMSNorm gains over K, applied to X first (B <= 4 only)
+  unsigned long long* amax;  // per batch row: max of argmax keys of seg 0's outputs
 };
+// small-batch products take the norm and the argmax inside (B <= 4)
+constexpr uint32_t kSmallB = 4;
 hipError_t launch_gemv(const GemvArgs& a, hipStream_t st);
-// the tile shape launch_gemv uses for a product (exposed for tests/bench)
-void gemv_shape(uint32_t rows, uint32_t K, uint32_t B, uint32_t mode, GemvArgs* a);
+
+// dd.pick as a key: larger value wins, then the lower index; -0 counts as
+// +0 and NaN never enters (key 0 = no candidate)
+__host__ __device__ inline unsigned long long argmax_key(float v, uint32_t i) {
+  if (v != v) return 0ull;
+  if (v == 0.0f) v = 0.0f;
+  uint32_t u;
+  __builtin_memcpy(&u, &v, 4);
+  const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)o << 32) | (0xFFFFFFFFu - i);
+}
+
+// M.norm (bend/Dense/Model.bend:27-30) on B rows of d: y = (x * s) * g with
+// s = 1 / sqrt((sum x*x) / d + 1e-5), the sum in index order
+hipError_t launch_rmsnorm(const float* X, const float* g, uint32_t d, uint32_t B, float* Y,
+                          hipStream_t st);
 
 // Per-sequence state addressing: a sequence's states start at
 // base + seq * seq_stride; a layer's at + layer_off.
@@ -77,8 +91,9 @@ struct StateRef {
   uint64_t layer_off;
 };
 
+// X[b] = E[tok[b]]; also clears amax[b] (nullptr: nothing to clear)
 hipError_t launch_embed(const float* E, const uint32_t* tok, uint32_t d, uint32_t B, float* X,
-                        hipStream_t st);
+                        unsigned long long* amax, hipStream_t st);
 hipError_t launch_bswap(uint32_t* w, uint64_t n, hipStream_t st);
 
 // GLA decode step for B sequences (one token each): per-head L2 norms, the
@@ -91,9 +106,10 @@ hipError_t launch_gla_chunk(const float* QKV, const float* Z, const float* lam, 
                             float* O, uint32_t d, uint32_t heads, uint32_t rglru, uint32_t T,
                             hipStream_t st);
 
-// Softmax attention over the ring for B (seq, pos) rows. write_kv: qk-norm
-// and write this row's k and v into its slot first (the decode step); else
-// the slots were written before (a chunk before the ring wraps).
+// Softmax attention over the ring for B (seq, pos) rows. write_kv: each
+// row writes its own k (qk-normed) and v into its slot first (the decode
+// step); else the slots were written before (launch_kv_write, a chunk before
+// the ring wraps).
 struct AttnArgs {
   const float* QKV;     // [B][3d]
   const float* gq;      // qk-norm gains (nullptr when off)
@@ -108,10 +124,8 @@ struct AttnArgs {
   uint32_t d, heads, ctx, B, write_kv;
 };
 hipError_t launch_attn(const AttnArgs& a, hipStream_t st);
-// write k (qk-normed) and v of T rows at positions pos0.. into the rings
-hipError_t launch_kv_write(const float* QKV, const float* gk, StateRef KV, uint32_t seq,
-                           uint32_t pos0, uint32_t d, uint32_t heads, uint32_t ctx, uint32_t T,
-                           hipStream_t st);
+// each row's k (qk-normed when gk) and v into slot pos mod ctx (dd.sm.write)
+hipError_t launch_kv_write(const AttnArgs& a, hipStream_t st);
 
 // dd.pick over B logit rows: least index reaching the max, vocab on NaN
 hipError_t launch_top(const float* logits, uint32_t vocab, uint32_t B, uint32_t* tok,
@@ -135,8 +149,30 @@ hipError_t launch_gather_rows(const float* src, const uint32_t* idx, uint32_t n,
                               float* dst, hipStream_t st);
 hipError_t launch_scatter_rows(const float* src, const uint32_t* idx, uint32_t n, uint32_t d,
                                float* dst, hipStream_t st);
-hipError_t launch_advance(uint32_t* pos, uint32_t* tok, const uint32_t* pick, uint32_t* out,
-                          uint32_t steps, uint32_t step, uint32_t B, hipStream_t st);
+// The token loop's step end for B sequences: the pick (from the sampler's
+// pick[b], or greedy: the amax key or top[b] of dd.pick, falling back to
+// Sample.argmax over the logits when there is none), recorded at
+// out[b * steps + *step], fed next (tok = pick, pos + 1); then *step + 1.
+// The step index lives in device memory, so one captured step serves every
+// iteration.
+struct AdvanceArgs {
+  const float* logits;              // [B][vocab]
+  uint32_t vocab, B, steps;
+  const unsigned long long* amax;   // greedy, keys (or nullptr)
+  const uint32_t* pick;             // sampled picks, or greedy dd.pick results
+  uint32_t greedy;
+  uint32_t* pos;
+  uint32_t* tok;
+  uint32_t* out;
+  uint32_t* step;
+  uint32_t* last;                   // [B]: the pick, for ana_top-like readers
+};
+hipError_t launch_advance(const AdvanceArgs& a, hipStream_t st);
+// greedy picks from amax keys (dd.top), vocab where there is none
+hipError_t launch_keys_to_tok(const unsigned long long* amax, uint32_t vocab, uint32_t B,
+                              uint32_t* tok, hipStream_t st);
 hipError_t launch_zero(float* p, uint64_t n, hipStream_t st);
+hipError_t launch_zero_u32(uint32_t* p, uint32_t n, hipStream_t st);
+hipError_t launch_zero_u64(unsigned long long* p, uint32_t n, hipStream_t st);
 
 }  // namespace ana

@@ -6,7 +6,10 @@
 // (this file is compiled with -ffp-contract=off and the pragma below),
 // exp/log go through double and are rounded to float, sqrt and division are
 // the correctly rounded IEEE operations. Parallelism is only ever across
-// outputs (rows, heads, sequences); each reduction chain stays in one lane.
+// outputs (rows, heads, sequences); each reduction chain stays in one lane,
+// and the wide, parallel part of the work (loading weights, forming
+// products) is spread over the whole workgroup and staged in LDS so that
+// the in-order chains only add.
 #include "ana_internal.h"
 #include "numerics.h"
 
@@ -14,13 +17,18 @@
 
 namespace ana {
 
+namespace {
+constexpr float4 kZero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+}
+
 // ------------------------------------------------------------------ products
 
-// Row pointer and output slot for tile row r of workgroup tile t.
-__device__ __forceinline__ bool gemv_row(const GemvArgs& a, uint32_t t, uint32_t r,
+// Weight row and output slot of tile row r of workgroup tile t (R rows per
+// tile; in GM_SILU the first R/2 rows are gate rows j, the rest up rows j).
+__device__ __forceinline__ bool gemv_row(const GemvArgs& a, uint32_t R, uint32_t t, uint32_t r,
                                          const float** w, uint32_t* seg, uint32_t* lr) {
   if (a.mode == GM_SILU) {
-    const uint32_t half = a.rows_wg >> 1;
+    const uint32_t half = R >> 1;
     const uint32_t s = r < half ? 0u : 1u;
     const uint32_t j = t * half + (s ? r - half : r);
     if (j >= a.seg[s].rows) return false;
@@ -29,7 +37,7 @@ __device__ __forceinline__ bool gemv_row(const GemvArgs& a, uint32_t t, uint32_t
     *lr = j;
     return true;
   }
-  const uint32_t vr = t * a.rows_wg + r;
+  const uint32_t vr = t * R + r;
   uint32_t s = 0, j = vr;
   if (j >= a.seg[0].rows) {
     j -= a.seg[0].rows;
@@ -42,171 +50,324 @@ __device__ __forceinline__ bool gemv_row(const GemvArgs& a, uint32_t t, uint32_t
   return true;
 }
 
-// One workgroup: rows_wg output rows x bt batch rows. Per K chunk the
-// weights and the (normalised) activations are staged in LDS, every thread
-// forms products x*w, and lane c = b*rows_wg + r adds its row's products in
-// q order: the chain of bulk.c's ft_gemm_loop, one lane per output.
-__global__ __launch_bounds__(256) void k_gemv_exact(GemvArgs a) {
+// the result of chain (b, r): plain, plus the residual, or (GM_SILU, via
+// LDS `outs` [BT][R]) silu(gate) * up
+__device__ __forceinline__ void gemv_store(const GemvArgs& a, uint32_t R, uint32_t t, uint32_t r,
+                                           uint32_t b, float s) {
+  const float* wp;
+  uint32_t sg, lr;
+  if (!gemv_row(a, R, t, r, &wp, &sg, &lr)) return;
+  float y = s;
+  if (a.mode == GM_RESID) y = a.R[(size_t)b * a.ldr + lr] + s;
+  a.seg[sg].Y[(size_t)b * a.seg[sg].ldy + lr] = y;
+}
+
+// Small batches (B <= 4 rows per workgroup): R x BT chain lanes (<= 32, one
+// wave). The weights of a K chunk are loaded into registers, up to 16 float4
+// a thread, all in flight at once (the next chunk's while the current one
+// is being summed); the activations sit in LDS. With `ng` the workgroup
+// first normalises its activation rows (M.norm, bend/Dense/Model.bend:27-30:
+// ss = sum x*x in order, x * (1/sqrt(ss/K + 1e-5)) * g) while the first
+// weights are still arriving. Every thread multiplies its weights by the
+// activations and writes the products; lane c = b*R + r then adds its row's
+// products in q order: bulk.c's ft_gemm_loop, one lane per output. With
+// `amax` the outputs of segment 0 also compete for dd.pick's argmax.
+template <int BT>
+__global__ __launch_bounds__(256) void k_gemv_small(GemvArgs a, uint32_t R, uint32_t QC) {
   extern __shared__ float4 lds4[];
-  const uint32_t R = a.rows_wg, BT = a.bt, QC = a.qc, K = a.K;
-  const uint32_t Q4 = QC >> 2;
+  const uint32_t Q4 = QC >> 2, PS4 = Q4 + 1;
   const uint32_t tid = threadIdx.x;
   const uint32_t b0 = blockIdx.y * BT;
-  const uint32_t nb = min(BT, a.B - b0);
+  const uint32_t nb = min((uint32_t)BT, a.B - b0);
   const uint32_t Lc = R * BT;
-  float4* Ws = lds4;                          // [R][Q4]
-  float4* Xs = Ws + R * Q4;                   // [BT][Q4]
-  float4* P = Xs + BT * Q4;                   // [Lc][Q4 + 1]
-  float* rs = reinterpret_cast<float*>(P + Lc * (Q4 + 1));  // [BT]
-  float* outs = rs + BT;                      // [Lc]
+  const uint32_t K = a.K;
+  float4* Xs = lds4;                                      // [BT][Q4]
+  float4* P = Xs + BT * Q4;                               // [Lc][PS4]
+  float* outs = reinterpret_cast<float*>(P + Lc * PS4);  // [Lc, rounded up to 4]
+  float* rs = outs + ((Lc + 3) & ~3u);                    // [4]
+  float4* Xf = reinterpret_cast<float4*>(rs + 4);         // [BT][K/4] when ng
 
-  // RMSNorm prologue (M.norm, bend/Dense/Model.bend:27-30): ss = sum x*x in
-  // j order, scale = 1 / sqrt(ss / K + 1e-5)
-  if (a.ng) {
-    if (tid < nb) {
-      const float4* x = reinterpret_cast<const float4*>(a.X + (size_t)(b0 + tid) * a.ldx);
-      float ss = 0.0f;
-      for (uint32_t j = 0; j < (K >> 2); j++) {
-        const float4 v = x[j];
-        ss = ss + v.x * v.x;
-        ss = ss + v.y * v.y;
-        ss = ss + v.z * v.z;
-        ss = ss + v.w * v.w;
-      }
-      rs[tid] = ex_rms_scale(ss, (float)K);
-    }
-    __syncthreads();
-  }
-
-  float s = 0.0f;
-  for (uint32_t q0 = 0; q0 < K; q0 += QC) {
-    const uint32_t qc4 = (min(QC, K - q0)) >> 2;
-    for (uint32_t i = tid; i < R * qc4; i += 256) {
-      const uint32_t r = i / qc4, q4 = i - r * qc4;
+  float4 w[16];
+  // weights of the chunk at q0 into w[]; item i = tid + 256 j is (row r, float4 q4)
+  auto load_w = [&](uint32_t q0) {
+    const uint32_t qc4 = min(QC, K - q0) >> 2;
+    const uint32_t dr = 256 / qc4, dq = 256 - dr * qc4;
+    uint32_t r = tid / qc4, q4 = tid - r * qc4;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      w[j] = kZero4;
       const float* wp;
       uint32_t sg, lr;
-      float4 w = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (gemv_row(a, blockIdx.x, r, &wp, &sg, &lr))
-        w = *reinterpret_cast<const float4*>(wp + q0 + 4 * q4);
-      Ws[r * Q4 + q4] = w;
+      if (r < R && gemv_row(a, R, blockIdx.x, r, &wp, &sg, &lr))
+        w[j] = *reinterpret_cast<const float4*>(wp + q0 + 4 * q4);
+      r += dr;
+      q4 += dq;
+      if (q4 >= qc4) { q4 -= qc4; r++; }
     }
+  };
+  load_w(0);
+  if (a.ng) {
+    const uint32_t K4 = K >> 2;
+    for (uint32_t i = tid; i < BT * K4; i += 256) {
+      const uint32_t b = i / K4, k4 = i - b * K4;
+      Xf[i] = b < nb ? *reinterpret_cast<const float4*>(a.X + (size_t)(b0 + b) * a.ldx + 4 * k4) : kZero4;
+    }
+    __syncthreads();
+    if (tid < nb) rs[tid] = ex_rms_scale(chain_sumsq_lds(0.0f, reinterpret_cast<const float*>(Xf + tid * K4), K), (float)K);
+    __syncthreads();
+  }
+  float s = 0.0f;
+  for (uint32_t q0 = 0; q0 < K; q0 += QC) {
+    const uint32_t qc4 = min(QC, K - q0) >> 2;
     for (uint32_t i = tid; i < BT * qc4; i += 256) {
       const uint32_t b = i / qc4, q4 = i - b * qc4;
-      float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      float4 x = kZero4;
       if (b < nb) {
-        x = *reinterpret_cast<const float4*>(a.X + (size_t)(b0 + b) * a.ldx + q0 + 4 * q4);
         if (a.ng) {
-          const float sc = rs[b];
+          const float4 v = Xf[b * (K >> 2) + (q0 >> 2) + q4];
           const float4 g = *reinterpret_cast<const float4*>(a.ng + q0 + 4 * q4);
-          x.x = (x.x * sc) * g.x;
-          x.y = (x.y * sc) * g.y;
-          x.z = (x.z * sc) * g.z;
-          x.w = (x.w * sc) * g.w;
+          const float sc = rs[b];
+          x = make_float4((v.x * sc) * g.x, (v.y * sc) * g.y, (v.z * sc) * g.z, (v.w * sc) * g.w);
+        } else {
+          x = *reinterpret_cast<const float4*>(a.X + (size_t)(b0 + b) * a.ldx + q0 + 4 * q4);
         }
       }
       Xs[b * Q4 + q4] = x;
     }
     __syncthreads();
-    for (uint32_t i = tid; i < Lc * qc4; i += 256) {
-      const uint32_t c = i / qc4, q4 = i - c * qc4;
-      const uint32_t b = c / R, r = c - b * R;
-      const float4 x = Xs[b * Q4 + q4], w = Ws[r * Q4 + q4];
-      P[c * (Q4 + 1) + q4] = make_float4(x.x * w.x, x.y * w.y, x.z * w.z, x.w * w.w);
-    }
-    __syncthreads();
-    if (tid < Lc) {
-      const float4* p = P + tid * (Q4 + 1);
-      for (uint32_t q4 = 0; q4 < qc4; q4++) {
-        const float4 v = p[q4];
-        s = s + v.x;
-        s = s + v.y;
-        s = s + v.z;
-        s = s + v.w;
+    {
+      const uint32_t dr = 256 / qc4, dq = 256 - dr * qc4;
+      uint32_t r = tid / qc4, q4 = tid - r * qc4;
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        if (r < R) {
+#pragma unroll
+          for (int b = 0; b < BT; b++) {
+            const float4 x = Xs[b * Q4 + q4];
+            P[(b * R + r) * PS4 + q4] = make_float4(x.x * w[j].x, x.y * w[j].y, x.z * w[j].z, x.w * w[j].w);
+          }
+        }
+        r += dr;
+        q4 += dq;
+        if (q4 >= qc4) { q4 -= qc4; r++; }
       }
     }
+    if (q0 + QC < K) load_w(q0 + QC);
+    __syncthreads();
+    if (tid < Lc) s = chain_sum_lds(s, reinterpret_cast<const float*>(P + tid * PS4), qc4 * 4);
     __syncthreads();
   }
-
+  const uint32_t b = tid / R, r = tid - b * R;
   if (a.mode == GM_SILU) {
     if (tid < Lc) outs[tid] = s;
     __syncthreads();
     const uint32_t half = R >> 1;
-    if (tid < Lc) {
-      const uint32_t b = tid / R, r = tid - b * R;
-      if (r < half && b < nb) {
-        const uint32_t j = blockIdx.x * half + r;
-        if (j < a.seg[0].rows) {
-          // hh = silu(g) * u (bend/Dense/Model.bend:58-59)
-          const float u = outs[b * R + r + half];
-          a.seg[0].Y[(size_t)(b0 + b) * a.seg[0].ldy + j] = ex_silu(s) * u;
+    if (tid < Lc && r < half && b < nb) {
+      const uint32_t j = blockIdx.x * half + r;
+      // hh = silu(g) * u (bend/Dense/Model.bend:58-59)
+      if (j < a.seg[0].rows)
+        a.seg[0].Y[(size_t)(b0 + b) * a.seg[0].ldy + j] = ex_silu(s) * outs[b * R + r + half];
+    }
+    return;
+  }
+  if (tid < Lc && b < nb) gemv_store(a, R, blockIdx.x, r, b0 + b, s);
+  if (a.amax && tid < 64) {
+    // the workgroup's best key per batch row, then one atomic each
+    unsigned long long key = 0;
+    if (tid < Lc && b < nb) {
+      const uint32_t vr = blockIdx.x * R + r;
+      if (vr < a.seg[0].rows) key = argmax_key(s, vr);
+    }
+#pragma unroll
+    for (int bb = 0; bb < BT; bb++) {
+      unsigned long long k = (tid < Lc && b == (uint32_t)bb) ? key : 0ull;
+      for (int m = 32; m >= 1; m >>= 1) {
+        const unsigned long long o = __shfl_xor(k, m, 64);
+        k = o > k ? o : k;
+      }
+      if (tid == 0 && (uint32_t)bb < nb && k) atomicMax(&a.amax[b0 + bb], k);
+    }
+  }
+}
+
+// Larger batches: a tile of RT rows x 64 batch rows, every thread owning RT/4
+// chains (one row, RT/4 consecutive batch rows). Per K chunk of 64 the
+// weights [r][q] and the activations, transposed to [q][b], sit in LDS; each
+// chain multiplies and adds in q order.
+template <int RT>
+__global__ __launch_bounds__(256) void k_gemm_exact(GemvArgs a) {
+  constexpr int CPT = RT / 4;
+  constexpr int QC = 64;
+  constexpr int XS = 64 + 4;
+  __shared__ float Ws[RT][QC + 4];
+  __shared__ float Xs[QC][XS];
+  __shared__ float outs[64][RT];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t r = tid % RT, bg = tid / RT;
+  const uint32_t b0 = blockIdx.y * 64;
+  const uint32_t nb = min(64u, a.B - b0);
+  const float* wrow;
+  uint32_t sg, lr;
+  const bool rok = gemv_row(a, RT, blockIdx.x, r, &wrow, &sg, &lr);
+  float s[CPT];
+#pragma unroll
+  for (int j = 0; j < CPT; j++) s[j] = 0.0f;
+  for (uint32_t q0 = 0; q0 < a.K; q0 += QC) {
+    const uint32_t qc = min((uint32_t)QC, a.K - q0), qc4 = qc >> 2;
+    // activations: 64 x qc, transposed into Xs[q][b]; all loads first
+    float4 xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t i = tid + 256 * j, b = i & 63, q4 = i >> 6;
+      xv[j] = (q4 < qc4 && b < nb) ? *reinterpret_cast<const float4*>(a.X + (size_t)(b0 + b) * a.ldx + q0 + 4 * q4)
+                                   : kZero4;
+    }
+    float4 wv = kZero4;
+    const uint32_t wi = tid, wr = wi / 16, wq4 = wi % 16;
+    if (wr < RT && wq4 < qc4) {
+      const float* wp;
+      uint32_t s2, l2;
+      if (gemv_row(a, RT, blockIdx.x, wr, &wp, &s2, &l2)) wv = *reinterpret_cast<const float4*>(wp + q0 + 4 * wq4);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t i = tid + 256 * j, b = i & 63, q4 = i >> 6;
+      Xs[4 * q4 + 0][b] = xv[j].x;
+      Xs[4 * q4 + 1][b] = xv[j].y;
+      Xs[4 * q4 + 2][b] = xv[j].z;
+      Xs[4 * q4 + 3][b] = xv[j].w;
+    }
+    if (wr < RT) *reinterpret_cast<float4*>(&Ws[wr][4 * wq4]) = wv;
+    __syncthreads();
+    for (uint32_t q = 0; q < qc; q += 4) {
+      const float4 w = *reinterpret_cast<const float4*>(&Ws[r][q]);
+      const float wq[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        if constexpr (CPT == 4) {
+          const float4 x = *reinterpret_cast<const float4*>(&Xs[q + u][bg * 4]);
+          s[0] = s[0] + x.x * wq[u];
+          s[1] = s[1] + x.y * wq[u];
+          s[2] = s[2] + x.z * wq[u];
+          s[3] = s[3] + x.w * wq[u];
+        } else {
+#pragma unroll
+          for (int j = 0; j < CPT; j++) s[j] = s[j] + Xs[q + u][bg * CPT + j] * wq[u];
         }
+      }
+    }
+    __syncthreads();
+  }
+  if (a.mode == GM_SILU) {
+#pragma unroll
+    for (int j = 0; j < CPT; j++) outs[bg * CPT + j][r] = s[j];
+    __syncthreads();
+    const uint32_t half = RT / 2;
+    if (r < half && rok) {
+#pragma unroll
+      for (int j = 0; j < CPT; j++) {
+        const uint32_t b = bg * CPT + j;
+        if (b < nb)
+          a.seg[0].Y[(size_t)(b0 + b) * a.seg[0].ldy + lr] = ex_silu(s[j]) * outs[b][r + half];
       }
     }
     return;
   }
-  if (tid < Lc) {
-    const uint32_t b = tid / R, r = tid - b * R;
-    const float* wp;
-    uint32_t sg, lr;
-    if (b < nb && gemv_row(a, blockIdx.x, r, &wp, &sg, &lr)) {
-      float y = s;
-      if (a.mode == GM_RESID) y = a.R[(size_t)(b0 + b) * a.ldr + lr] + s;
-      a.seg[sg].Y[(size_t)(b0 + b) * a.seg[sg].ldy + lr] = y;
+#pragma unroll
+  for (int j = 0; j < CPT; j++) {
+    const uint32_t b = bg * CPT + j;
+    if (b < nb) gemv_store(a, RT, blockIdx.x, r, b0 + b, s[j]);
+  }
+}
+
+static size_t small_lds(uint32_t R, uint32_t BT, uint32_t QC, uint32_t K, bool norm) {
+  const uint32_t Lc = R * BT, Lc4 = (Lc + 3) & ~3u;
+  return (size_t)BT * (QC / 4) * 16 + (size_t)Lc * (QC / 4 + 1) * 16 + (size_t)Lc4 * 4 + 16 +
+         (norm ? (size_t)BT * K * 4 : 0);
+}
+
+hipError_t launch_gemv(const GemvArgs& a, hipStream_t st) {
+  const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
+                                          : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
+  if (a.B <= kSmallB) {
+    const uint32_t BT = a.B <= 1 ? 1 : a.B <= 2 ? 2 : 4;
+    // rows per workgroup: about one workgroup per CU, chain lanes <= 64
+    uint32_t R = rows / 256;
+    R = R < 1 ? 1 : R;
+    const uint32_t rmax = 32 / BT;
+    R = R > rmax ? rmax : R;
+    if (a.mode == GM_SILU) R = R < 2 ? 2 : (R & ~1u);
+    const uint32_t Lc = R * BT;
+    uint32_t QC = a.K;
+    const uint32_t fixed = 16 * Lc + 4 * ((Lc + 3) & ~3u) + 16 + (a.ng ? BT * a.K * 4 : 0);
+    const uint32_t by_lds = (65536 - fixed) / (4 * (BT + Lc));
+    const uint32_t by_regs = 16384 / R;
+    QC = QC < by_lds ? QC : by_lds;
+    QC = QC < by_regs ? QC : by_regs;
+    QC &= ~3u;
+    const uint32_t per = a.mode == GM_SILU ? R / 2 : R;
+    const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
+    dim3 grid(tiles, (a.B + BT - 1) / BT);
+    const size_t lds = small_lds(R, BT, QC, a.K, a.ng != nullptr);
+    if (QC < 4 || lds > 65536 || R * (QC / 4) > 16 * 256) return hipErrorInvalidValue;
+    switch (BT) {
+      case 1: hipLaunchKernelGGL(k_gemv_small<1>, grid, dim3(256), lds, st, a, R, QC); break;
+      case 2: hipLaunchKernelGGL(k_gemv_small<2>, grid, dim3(256), lds, st, a, R, QC); break;
+      default: hipLaunchKernelGGL(k_gemv_small<4>, grid, dim3(256), lds, st, a, R, QC); break;
     }
+    return hipGetLastError();
   }
-}
-
-static size_t gemv_lds(uint32_t R, uint32_t BT, uint32_t QC) {
-  const uint32_t Q4 = QC / 4, Lc = R * BT;
-  return ((size_t)R * Q4 + (size_t)BT * Q4 + (size_t)Lc * (Q4 + 1)) * 16 + (BT + Lc) * 4;
-}
-
-void gemv_shape(uint32_t rows, uint32_t K, uint32_t B, uint32_t mode, GemvArgs* a) {
-  // batch rows per workgroup, then rows per workgroup so that a launch has
-  // about 256+ workgroups (one per CU) while R*BT chain lanes stay <= 256
-  const uint32_t BT = B <= 64 ? B : 64;
-  uint32_t tiles_b = (B + BT - 1) / BT;
-  uint32_t R = 256 / BT;
-  uint32_t want = rows / (256 / tiles_b > 0 ? 256 / tiles_b : 1);
-  if (want < 1) want = 1;
-  if (R > want) R = want;
-  if (R > 64) R = 64;
-  if (mode == GM_SILU) {
-    R = R < 2 ? 2 : (R & ~1u);
-    if (R * BT > 256) R = (256 / BT) & ~1u;
-    if (R < 2) R = 2;
-  }
-  // K chunk: as large as fits 64 KB of LDS
-  uint32_t QC = K;
-  while (QC > 4 && gemv_lds(R, BT, QC) > 65536) QC = ((QC / 2) + 3) & ~3u;
-  a->rows_wg = R;
-  a->bt = BT;
-  a->qc = QC;
-}
-
-hipError_t launch_gemv(const GemvArgs& a0, hipStream_t st) {
-  GemvArgs a = a0;
-  uint32_t rows = a.mode == GM_SILU ? a.seg[0].rows * 2 : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
-  if (a.rows_wg == 0) gemv_shape(rows, a.K, a.B, a.mode, &a);
-  const uint32_t per = a.mode == GM_SILU ? a.rows_wg / 2 : a.rows_wg;
+  if (a.ng || a.amax) return hipErrorInvalidValue;  // batched products take neither
+  const uint32_t RT = rows >= 4096 ? 16 : 4;
+  const uint32_t per = a.mode == GM_SILU ? RT / 2 : RT;
   const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
-  dim3 grid(tiles, (a.B + a.bt - 1) / a.bt);
-  hipLaunchKernelGGL(k_gemv_exact, grid, dim3(256), gemv_lds(a.rows_wg, a.bt, a.qc), st, a);
+  dim3 grid(tiles, (a.B + 63) / 64);
+  if (RT == 16) hipLaunchKernelGGL(k_gemm_exact<16>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(k_gemm_exact<4>, grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ norm
+
+__global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ X,
+                                                 const float* __restrict__ g, uint32_t d,
+                                                 float* __restrict__ Y) {
+  extern __shared__ float4 xs4[];
+  __shared__ float scale;
+  const uint32_t tid = threadIdx.x, d4 = d >> 2;
+  const float4* x = reinterpret_cast<const float4*>(X + (size_t)blockIdx.x * d);
+  for (uint32_t i = tid; i < d4; i += 256) xs4[i] = x[i];
+  __syncthreads();
+  if (tid == 0) scale = ex_rms_scale(chain_sumsq_lds(0.0f, reinterpret_cast<const float*>(xs4), d), (float)d);
+  __syncthreads();
+  const float sc = scale;
+  const float4* g4 = reinterpret_cast<const float4*>(g);
+  float4* y = reinterpret_cast<float4*>(Y + (size_t)blockIdx.x * d);
+  for (uint32_t i = tid; i < d4; i += 256) {
+    const float4 v = xs4[i], gg = g4[i];
+    y[i] = make_float4((v.x * sc) * gg.x, (v.y * sc) * gg.y, (v.z * sc) * gg.z, (v.w * sc) * gg.w);
+  }
+}
+
+hipError_t launch_rmsnorm(const float* X, const float* g, uint32_t d, uint32_t B, float* Y,
+                          hipStream_t st) {
+  hipLaunchKernelGGL(k_rmsnorm, dim3(B), dim3(256), (size_t)d * 4, st, X, g, d, Y);
   return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ embed
 
 __global__ void k_embed(const float* __restrict__ E, const uint32_t* __restrict__ tok, uint32_t d,
-                        float* __restrict__ X) {
+                        float* __restrict__ X, unsigned long long* amax) {
   const uint32_t b = blockIdx.x;
+  if (amax && threadIdx.x == 0) amax[b] = 0ull;
   const float* src = E + (size_t)tok[b] * d;
   for (uint32_t j = threadIdx.x; j < d; j += blockDim.x) X[(size_t)b * d + j] = src[j];
 }
 
 hipError_t launch_embed(const float* E, const uint32_t* tok, uint32_t d, uint32_t B, float* X,
-                        hipStream_t st) {
-  hipLaunchKernelGGL(k_embed, dim3(B), dim3(256), 0, st, E, tok, d, X);
+                        unsigned long long* amax, hipStream_t st) {
+  hipLaunchKernelGGL(k_embed, dim3(B), dim3(256), 0, st, E, tok, d, X, amax);
   return hipGetLastError();
 }
 
@@ -227,45 +388,44 @@ hipError_t launch_bswap(uint32_t* w, uint64_t n, hipStream_t st) {
 // head: L2 norms (M.l2), the gate (dd.gate: RG-LRU or sigmoid), the state
 // update S' = al*S + kh*v and the readout o = qh^T S' (no 1/sqrt(hd)).
 // nT tokens run in order, S staying in LDS between them.
+template <int HD>
 __global__ __launch_bounds__(256) void k_gla(const float* __restrict__ QKV,
                                               const float* __restrict__ Z,
                                               const float* __restrict__ lam, StateRef S,
                                               const uint32_t* __restrict__ seq, uint32_t seq0,
-                                              float* __restrict__ O, uint32_t d, uint32_t hd,
-                                              uint32_t rglru, uint32_t nT) {
-  __shared__ float q[64], k[64], v[64], z[64], al[64], kh[64], qh[64], sq[2];
-  __shared__ float Sl[64 * 65];
+                                              float* __restrict__ O, uint32_t d, uint32_t rglru,
+                                              uint32_t nT) {
+  constexpr int SP = HD + 1;
+  constexpr int NE = (HD * HD + 255) / 256;
+  __shared__ float q[HD], k[HD], v[HD], z[HD], al[HD], kh[HD], qh[HD], sq[2];
+  __shared__ float Sl[HD * SP];
   const uint32_t h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const uint32_t sl = seq ? seq[b] : seq0;
-  float* Sg = S.base + (size_t)sl * S.seq_stride + S.layer_off + (size_t)h * hd * hd;
-  const uint32_t hh2 = hd * hd;
-  for (uint32_t e = tid; e < hh2; e += 256) Sl[(e / hd) * 65 + (e % hd)] = Sg[e];
+  float* Sg = S.base + (size_t)sl * S.seq_stride + S.layer_off + (size_t)h * HD * HD;
+#pragma unroll
+  for (int j = 0; j < NE; j++) {
+    const uint32_t e = tid + 256 * j;
+    if (e < HD * HD) Sl[(e / HD) * SP + (e % HD)] = Sg[e];
+  }
   for (uint32_t t = 0; t < nT; t++) {
     const uint32_t row = seq ? b : t;   // batch row (step) or token row (chunk)
     const float* x = QKV + (size_t)row * 3 * d;
     __syncthreads();
-    if (tid < hd) {
-      q[tid] = x[h * hd + tid];
-      k[tid] = x[d + h * hd + tid];
-      v[tid] = x[2 * d + h * hd + tid];
-      z[tid] = Z[(size_t)row * d + h * hd + tid];
+    if (tid < HD) {
+      q[tid] = x[h * HD + tid];
+      k[tid] = x[d + h * HD + tid];
+      v[tid] = x[2 * d + h * HD + tid];
+      z[tid] = Z[(size_t)row * d + h * HD + tid];
     }
     __syncthreads();
-    if (tid == 0) {
-      float s = 0.0f;
-      for (uint32_t i = 0; i < hd; i++) s = s + q[i] * q[i];
-      sq[0] = s;
-    } else if (tid == 64) {
-      float s = 0.0f;
-      for (uint32_t i = 0; i < hd; i++) s = s + k[i] * k[i];
-      sq[1] = s;
-    }
+    if (tid == 0) sq[0] = chain_sumsq_lds(0.0f, q, HD);
+    else if (tid == 64) sq[1] = chain_sumsq_lds(0.0f, k, HD);
     __syncthreads();
-    if (tid < hd) {
+    if (tid < HD) {
       qh[tid] = q[tid] / csqrt(1.0e-6f + sq[0]);
       const float kn = k[tid] / csqrt(1.0e-6f + sq[1]);
       if (rglru) {
-        const float la = ex_rglru_log_gate(z[tid], lam[h * hd + tid]);
+        const float la = ex_rglru_log_gate(z[tid], lam[h * HD + tid]);
         kh[tid] = kn * ex_rglru_write_scale(la);
         al[tid] = dexp(la);
       } else {
@@ -274,27 +434,45 @@ __global__ __launch_bounds__(256) void k_gla(const float* __restrict__ QKV,
       }
     }
     __syncthreads();
-    for (uint32_t e = tid; e < hh2; e += 256) {
-      const uint32_t ia = e / hd, ib = e - ia * hd;
-      float* p = &Sl[ia * 65 + ib];
-      *p = (al[ia] * *p) + (kh[ia] * v[ib]);
+#pragma unroll
+    for (int j = 0; j < NE; j++) {
+      const uint32_t e = tid + 256 * j;
+      if (e < HD * HD) {
+        const uint32_t ia = e / HD, ib = e % HD;
+        float* p = &Sl[ia * SP + ib];
+        *p = (al[ia] * *p) + (kh[ia] * v[ib]);
+      }
     }
     __syncthreads();
-    if (tid < hd) {
+    if (tid < HD) {
       float acc = 0.0f;
-      for (uint32_t i = 0; i < hd; i++) acc = acc + qh[i] * Sl[i * 65 + tid];
-      O[(size_t)row * d + h * hd + tid] = acc;
+#pragma unroll
+      for (int i = 0; i < HD; i++) acc = acc + qh[i] * Sl[i * SP + tid];
+      O[(size_t)row * d + h * HD + tid] = acc;
     }
   }
   __syncthreads();
-  for (uint32_t e = tid; e < hh2; e += 256) Sg[e] = Sl[(e / hd) * 65 + (e % hd)];
+#pragma unroll
+  for (int j = 0; j < NE; j++) {
+    const uint32_t e = tid + 256 * j;
+    if (e < HD * HD) Sg[e] = Sl[(e / HD) * SP + (e % HD)];
+  }
 }
+
+#define ANA_HD_DISPATCH(HDV, LAUNCH) \
+  switch (HDV) {                     \
+    case 64: LAUNCH(64); break;      \
+    case 32: LAUNCH(32); break;      \
+    case 16: LAUNCH(16); break;      \
+    default: return hipErrorInvalidValue; \
+  }
 
 hipError_t launch_gla_step(const float* QKV, const float* Z, const float* lam, StateRef S,
                            const uint32_t* seq, float* O, uint32_t d, uint32_t heads,
                            uint32_t rglru, uint32_t B, hipStream_t st) {
-  hipLaunchKernelGGL(k_gla, dim3(heads, B), dim3(256), 0, st, QKV, Z, lam, S, seq, 0u, O, d,
-                     d / heads, rglru, 1u);
+#define L_(H) hipLaunchKernelGGL(k_gla<H>, dim3(heads, B), dim3(256), 0, st, QKV, Z, lam, S, seq, 0u, O, d, rglru, 1u)
+  ANA_HD_DISPATCH(d / heads, L_)
+#undef L_
   return hipGetLastError();
 }
 
@@ -302,8 +480,9 @@ hipError_t launch_gla_chunk(const float* QKV, const float* Z, const float* lam, 
                             float* O, uint32_t d, uint32_t heads, uint32_t rglru, uint32_t T,
                             hipStream_t st) {
   StateRef S{Sbase, 0, 0};
-  hipLaunchKernelGGL(k_gla, dim3(heads, 1), dim3(256), 0, st, QKV, Z, lam, S,
-                     (const uint32_t*)nullptr, 0u, O, d, d / heads, rglru, T);
+#define L_(H) hipLaunchKernelGGL(k_gla<H>, dim3(heads, 1), dim3(256), 0, st, QKV, Z, lam, S, (const uint32_t*)nullptr, 0u, O, d, rglru, T)
+  ANA_HD_DISPATCH(d / heads, L_)
+#undef L_
   return hipGetLastError();
 }
 
@@ -318,61 +497,80 @@ __device__ __forceinline__ float wave_max_gt(float r) {
   return r;
 }
 
-// qk-norm for one head (M.qkn, bend/Dense/Model.bend:39-42), in place;
-// lanes < hd hold x, the chain runs in lane `chain`.
-__device__ __forceinline__ void qk_norm(float* x, const float* g, uint32_t hd, float* ssum,
-                                        uint32_t tid, uint32_t chain) {
-  if (tid == chain) {
-    float s = 0.0f;
-    for (uint32_t i = 0; i < hd; i++) s = s + x[i] * x[i];
-    *ssum = ex_rms_scale(s, (float)hd);
-  }
-  __syncthreads();
-  if (tid < hd) x[tid] = (x[tid] * *ssum) * (1.0f + g[tid]);
-  __syncthreads();
-}
-
 #define ATTN_TC 128
 
-// dd.sm.attend (bend/Dense/Decode.bend:321-353) for one (row, head): scores
-// over the live slots t' <= npos, the masked max (with the sink), exp,
-// se = sum e in slot order, den (+ exp(sink - m)), oi = sum_t' e*V in slot
-// order, o = (1/den) * oi. Masked slots are skipped: the reference adds
-// exactly +0 to each sum there (e = 0 and, with finite V, 0*V = +-0 to a
-// sum that is never -0) and -inf to the max.
+// dd.sm.attend (bend/Dense/Decode.bend:321-353) for one (row, head). With
+// write_kv the row's k (qk-normed) and v go into slot pos mod ctx first
+// (dd.sm.write) and the row reads its own slot from LDS; else every slot was
+// written before. Scores over the live slots t' <= npos (each a chain over
+// c), the masked max (with the sink), e = exp(sc*s - m), se = sum e in slot
+// order, den (+ exp(sink - m)), oi = sum_t' e*V in slot order,
+// o = (1/den) * oi. Masked slots are skipped: the reference adds exactly +0
+// to each sum there (e = 0 and, with finite V, 0*V = +-0 to a sum that is
+// never -0) and -inf to the max.
+template <int HD>
 __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   extern __shared__ float dyn[];
-  __shared__ float q[64], k[64], v[64], red[4], nrm[2];
+  __shared__ float q[HD], kk[HD], vs[HD], red[4], nrm[2];
+  constexpr int PS = ATTN_TC + 4;
+  constexpr int NV = (ATTN_TC * HD / 4 + 255) / 256;
   const uint32_t h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const uint32_t d = a.d, hd = d / a.heads, ctx = a.ctx;
+  const uint32_t d = a.d, ctx = a.ctx;
   const uint32_t pos = a.pos ? a.pos[b] : a.pos0 + b;
   const uint32_t slot = pos % ctx, npos = pos < ctx - 1 ? pos : ctx - 1;
   const uint32_t sl = a.seq ? a.seq[b] : a.seq0;
   float* Kr = a.KV.base + (size_t)sl * a.KV.seq_stride + a.KV.layer_off;
   float* Vr = Kr + (size_t)ctx * d;
   float* ss = dyn;                          // [ctx]: sc*s, then e
-  float* P = dyn + ctx;                     // [hd][ATTN_TC + 4]
+  float* P = dyn + ctx;                     // [HD][PS]
   const float* x = a.QKV + (size_t)b * 3 * d;
-  if (tid < hd) {
-    q[tid] = x[h * hd + tid];
-    k[tid] = x[d + h * hd + tid];
-    v[tid] = x[2 * d + h * hd + tid];
+  const bool wkv = a.write_kv != 0;
+  if (tid < HD) {
+    q[tid] = x[h * HD + tid];
+    if (wkv) {
+      kk[tid] = x[d + h * HD + tid];
+      vs[tid] = x[2 * d + h * HD + tid];
+    }
   }
   __syncthreads();
   if (a.gq) {
-    qk_norm(q, a.gq, hd, &nrm[0], tid, 0);
-    if (a.write_kv) qk_norm(k, a.gk, hd, &nrm[1], tid, 64);
+    // M.qkn on q and k (bend/Dense/Model.bend:39-42), two chains at once
+    if (tid == 0) nrm[0] = ex_rms_scale(chain_sumsq_lds(0.0f, q, HD), (float)HD);
+    else if (tid == 64 && wkv) nrm[1] = ex_rms_scale(chain_sumsq_lds(0.0f, kk, HD), (float)HD);
+    __syncthreads();
+    if (tid < HD) {
+      q[tid] = (q[tid] * nrm[0]) * (1.0f + a.gq[tid]);
+      if (wkv) kk[tid] = (kk[tid] * nrm[1]) * (1.0f + a.gk[tid]);
+    }
+    __syncthreads();
   }
-  if (a.write_kv && tid < hd) {
-    Kr[(size_t)slot * d + h * hd + tid] = k[tid];
-    Vr[(size_t)slot * d + h * hd + tid] = v[tid];
+  if (wkv && tid < HD) {
+    Kr[(size_t)slot * d + h * HD + tid] = kk[tid];
+    Vr[(size_t)slot * d + h * HD + tid] = vs[tid];
   }
-  const float sc = 1.0f / csqrt((float)hd);
+  float qr[HD];
+#pragma unroll
+  for (int c = 0; c < HD; c++) qr[c] = q[c];
+  const float sc = 1.0f / csqrt((float)HD);
   // scores: s = sum_c q_c K[t'][c] (a gemm chain over c), kept as sc*s
   for (uint32_t t = tid; t <= npos; t += 256) {
-    const float* kr = (a.write_kv && t == slot) ? k : Kr + (size_t)t * d + h * hd;
     float acc = 0.0f;
-    for (uint32_t c = 0; c < hd; c++) acc = acc + q[c] * kr[c];
+    if (wkv && t == slot) {
+#pragma unroll
+      for (int c = 0; c < HD; c++) acc = acc + qr[c] * kk[c];
+    } else {
+      const float4* k4 = reinterpret_cast<const float4*>(Kr + (size_t)t * d + h * HD);
+      float4 kv[HD / 4];
+#pragma unroll
+      for (int u = 0; u < HD / 4; u++) kv[u] = k4[u];
+#pragma unroll
+      for (int u = 0; u < HD / 4; u++) {
+        acc = acc + qr[4 * u + 0] * kv[u].x;
+        acc = acc + qr[4 * u + 1] * kv[u].y;
+        acc = acc + qr[4 * u + 2] * kv[u].z;
+        acc = acc + qr[4 * u + 3] * kv[u].w;
+      }
+    }
     ss[t] = sc * acc;
   }
   __syncthreads();
@@ -394,74 +592,82 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   for (uint32_t t = tid; t <= npos; t += 256) ss[t] = dexp(ss[t] - m);
   __syncthreads();
   float oi = 0.0f, se = 0.0f;
-  const uint32_t PS = ATTN_TC + 4;
+  float4 vv[NV];
+  auto load_v = [&](uint32_t t0) {
+    const uint32_t tc = min((uint32_t)ATTN_TC, npos + 1 - t0);
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      const uint32_t i = tid + 256 * j, t = i / (HD / 4), c4 = i % (HD / 4);
+      vv[j] = kZero4;
+      if (t < tc) {
+        if (wkv && t0 + t == slot) vv[j] = *reinterpret_cast<const float4*>(&vs[4 * c4]);
+        else vv[j] = *reinterpret_cast<const float4*>(Vr + (size_t)(t0 + t) * d + h * HD + 4 * c4);
+      }
+    }
+  };
+  load_v(0);
   for (uint32_t t0 = 0; t0 <= npos; t0 += ATTN_TC) {
     const uint32_t tc = min((uint32_t)ATTN_TC, npos + 1 - t0);
-    for (uint32_t i = tid; i < tc * hd; i += 256) {
-      const uint32_t t = i / hd, c = i - t * hd, tt = t0 + t;
-      const float vv = (a.write_kv && tt == slot) ? v[c] : Vr[(size_t)tt * d + h * hd + c];
-      P[c * PS + t] = ss[tt] * vv;
-    }
-    __syncthreads();
-    if (tid < hd) {
-      const float* p = P + tid * PS;
-      uint32_t t = 0;
-      for (; t + 4 <= tc; t += 4) {
-        const float4 w4 = *reinterpret_cast<const float4*>(p + t);
-        oi = oi + w4.x;
-        oi = oi + w4.y;
-        oi = oi + w4.z;
-        oi = oi + w4.w;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      const uint32_t i = tid + 256 * j, t = i / (HD / 4), c4 = i % (HD / 4);
+      if (t < tc) {
+        const float e = ss[t0 + t];
+        P[(4 * c4 + 0) * PS + t] = e * vv[j].x;
+        P[(4 * c4 + 1) * PS + t] = e * vv[j].y;
+        P[(4 * c4 + 2) * PS + t] = e * vv[j].z;
+        P[(4 * c4 + 3) * PS + t] = e * vv[j].w;
       }
-      for (; t < tc; t++) oi = oi + p[t];
-    } else if (tid == 64) {
-      for (uint32_t t = 0; t < tc; t++) se = se + ss[t0 + t];
     }
+    if (t0 + ATTN_TC <= npos) load_v(t0 + ATTN_TC);
+    __syncthreads();
+    if (tid < HD) oi = chain_sum_lds(oi, P + tid * PS, tc);
+    else if (tid == 64) se = chain_sum_lds(se, ss + t0, tc);
     __syncthreads();
   }
   if (tid == 64) red[0] = a.sink ? se + dexp(sink - m) : se;
   __syncthreads();
-  if (tid < hd) a.O[(size_t)b * d + h * hd + tid] = (1.0f / red[0]) * oi;
+  if (tid < HD) a.O[(size_t)b * d + h * HD + tid] = (1.0f / red[0]) * oi;
 }
 
 hipError_t launch_attn(const AttnArgs& a, hipStream_t st) {
-  const size_t lds = ((size_t)a.ctx + (size_t)(a.d / a.heads) * (ATTN_TC + 4)) * 4;
-  hipLaunchKernelGGL(k_attn, dim3(a.heads, a.B), dim3(256), lds, st, a);
+  const uint32_t hd = a.d / a.heads;
+  const size_t lds = ((size_t)a.ctx + (size_t)hd * (ATTN_TC + 4)) * 4;
+#define L_(H) hipLaunchKernelGGL(k_attn<H>, dim3(a.heads, a.B), dim3(256), lds, st, a)
+  ANA_HD_DISPATCH(hd, L_)
+#undef L_
   return hipGetLastError();
 }
 
-// a chunk's k (qk-normed) and v into their slots (dd.sm.writes)
-__global__ __launch_bounds__(64) void k_kv_write(const float* __restrict__ QKV,
-                                                 const float* __restrict__ gk, StateRef KV,
-                                                 uint32_t seq, uint32_t pos0, uint32_t d,
-                                                 uint32_t hd, uint32_t ctx) {
-  __shared__ float k[64], nrm;
-  const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-  const float* x = QKV + (size_t)t * 3 * d;
-  if (tid < hd) k[tid] = x[d + h * hd + tid];
+// dd.sm.write (bend/Dense/Decode.bend:295-304): row b's k (after qk-norm
+// when on) and v into slot pos mod ctx of its sequence's rings
+template <int HD>
+__global__ __launch_bounds__(64) void k_kv_write(AttnArgs a) {
+  __shared__ float k[HD], nrm;
+  const uint32_t h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const uint32_t d = a.d;
+  const float* x = a.QKV + (size_t)b * 3 * d;
+  if (tid < HD) k[tid] = x[d + h * HD + tid];
   __syncthreads();
-  if (gk) {
-    if (tid == 0) {
-      float s = 0.0f;
-      for (uint32_t i = 0; i < hd; i++) s = s + k[i] * k[i];
-      nrm = ex_rms_scale(s, (float)hd);
-    }
+  if (a.gk) {
+    if (tid == 0) nrm = ex_rms_scale(chain_sumsq_lds(0.0f, k, HD), (float)HD);
     __syncthreads();
-    if (tid < hd) k[tid] = (k[tid] * nrm) * (1.0f + gk[tid]);
+    if (tid < HD) k[tid] = (k[tid] * nrm) * (1.0f + a.gk[tid]);
   }
-  const uint32_t slot = (pos0 + t) % ctx;
-  float* Kr = KV.base + (size_t)seq * KV.seq_stride + KV.layer_off;
-  if (tid < hd) {
-    Kr[(size_t)slot * d + h * hd + tid] = k[tid];
-    Kr[(size_t)ctx * d + (size_t)slot * d + h * hd + tid] = x[2 * d + h * hd + tid];
+  const uint32_t pos = a.pos ? a.pos[b] : a.pos0 + b;
+  const uint32_t slot = pos % a.ctx;
+  const uint32_t sl = a.seq ? a.seq[b] : a.seq0;
+  float* Kr = a.KV.base + (size_t)sl * a.KV.seq_stride + a.KV.layer_off;
+  if (tid < HD) {
+    Kr[(size_t)slot * d + h * HD + tid] = k[tid];
+    Kr[(size_t)a.ctx * d + (size_t)slot * d + h * HD + tid] = x[2 * d + h * HD + tid];
   }
 }
 
-hipError_t launch_kv_write(const float* QKV, const float* gk, StateRef KV, uint32_t seq,
-                           uint32_t pos0, uint32_t d, uint32_t heads, uint32_t ctx, uint32_t T,
-                           hipStream_t st) {
-  hipLaunchKernelGGL(k_kv_write, dim3(heads, T), dim3(64), 0, st, QKV, gk, KV, seq, pos0, d,
-                     d / heads, ctx);
+hipError_t launch_kv_write(const AttnArgs& a, hipStream_t st) {
+#define L_(H) hipLaunchKernelGGL(k_kv_write<H>, dim3(a.heads, a.B), dim3(64), 0, st, a)
+  ANA_HD_DISPATCH(a.d / a.heads, L_)
+#undef L_
   return hipGetLastError();
 }
 
@@ -526,23 +732,6 @@ hipError_t launch_scatter_rows(const float* src, const uint32_t* idx, uint32_t n
   return hipGetLastError();
 }
 
-// the token loop's step end: record the pick, feed it next at pos + 1
-__global__ void k_advance(uint32_t* pos, uint32_t* tok, const uint32_t* pick, uint32_t* out,
-                          uint32_t steps, uint32_t step, uint32_t B) {
-  const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= B) return;
-  out[(size_t)b * steps + step] = pick[b];
-  tok[b] = pick[b];
-  pos[b] = pos[b] + 1;
-}
-
-hipError_t launch_advance(uint32_t* pos, uint32_t* tok, const uint32_t* pick, uint32_t* out,
-                          uint32_t steps, uint32_t step, uint32_t B, hipStream_t st) {
-  hipLaunchKernelGGL(k_advance, dim3((B + 255) / 256), dim3(256), 0, st, pos, tok, pick, out,
-                     steps, step, B);
-  return hipGetLastError();
-}
-
 __global__ void k_zero(float* p, uint64_t n) {
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (uint64_t)gridDim.x * blockDim.x)
@@ -551,6 +740,37 @@ __global__ void k_zero(float* p, uint64_t n) {
 
 hipError_t launch_zero(float* p, uint64_t n, hipStream_t st) {
   hipLaunchKernelGGL(k_zero, dim3(2048), dim3(256), 0, st, p, n);
+  return hipGetLastError();
+}
+
+__global__ void k_zero_u32(uint32_t* p, uint32_t n) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+hipError_t launch_zero_u32(uint32_t* p, uint32_t n, hipStream_t st) {
+  hipLaunchKernelGGL(k_zero_u32, dim3((n + 255) / 256), dim3(256), 0, st, p, n);
+  return hipGetLastError();
+}
+
+__global__ void k_zero_u64(unsigned long long* p, uint32_t n) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0ull;
+}
+
+hipError_t launch_zero_u64(unsigned long long* p, uint32_t n, hipStream_t st) {
+  hipLaunchKernelGGL(k_zero_u64, dim3((n + 255) / 256), dim3(256), 0, st, p, n);
+  return hipGetLastError();
+}
+
+__global__ void k_keys_to_tok(const unsigned long long* amax, uint32_t vocab, uint32_t B, uint32_t* tok) {
+  const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < B) tok[b] = amax[b] ? 0xFFFFFFFFu - (uint32_t)(amax[b] & 0xFFFFFFFFull) : vocab;
+}
+
+hipError_t launch_keys_to_tok(const unsigned long long* amax, uint32_t vocab, uint32_t B,
+                              uint32_t* tok, hipStream_t st) {
+  hipLaunchKernelGGL(k_keys_to_tok, dim3((B + 255) / 256), dim3(256), 0, st, amax, vocab, B, tok);
   return hipGetLastError();
 }
 

@@ -63,3 +63,78 @@ __device__ __forceinline__ float ex_rms_scale(float ss, float n) {
 }
 
 }  // namespace ana
+
+namespace ana {
+
+// s = (((s + p[0]) + p[1]) + ...) + p[n-1]: one in-order chain over LDS
+// (p 16-byte aligned), with the next 8 float4 loads in flight
+// while the current 32 adds run.
+__device__ __forceinline__ float chain_sum_lds(float s, const float* __restrict__ p, uint32_t n) {
+  const float4* q = reinterpret_cast<const float4*>(p);
+  const uint32_t n4 = n >> 2;
+  uint32_t i = 0;
+  if (n4 >= 8) {
+    float4 a[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) a[u] = q[u];
+    for (i = 8; i + 8 <= n4; i += 8) {
+      float4 b[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) b[u] = q[i + u];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        s = s + a[u].x;
+        s = s + a[u].y;
+        s = s + a[u].z;
+        s = s + a[u].w;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) a[u] = b[u];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      s = s + a[u].x;
+      s = s + a[u].y;
+      s = s + a[u].z;
+      s = s + a[u].w;
+    }
+  }
+  for (; i < n4; i++) {
+    const float4 v = q[i];
+    s = s + v.x;
+    s = s + v.y;
+    s = s + v.z;
+    s = s + v.w;
+  }
+  for (uint32_t j = n4 << 2; j < n; j++) s = s + p[j];
+  return s;
+}
+
+// s = s + x0*x0 + x1*x1 ... in order (M.norm's sum of squares)
+__device__ __forceinline__ float chain_sumsq_lds(float s, const float* __restrict__ p, uint32_t n) {
+  const float4* q = reinterpret_cast<const float4*>(p);
+  const uint32_t n4 = n >> 2;
+  uint32_t i = 0;
+  for (; i + 8 <= n4; i += 8) {
+    float4 a[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) a[u] = q[i + u];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      s = s + a[u].x * a[u].x;
+      s = s + a[u].y * a[u].y;
+      s = s + a[u].z * a[u].z;
+      s = s + a[u].w * a[u].w;
+    }
+  }
+  for (; i < n4; i++) {
+    const float4 v = q[i];
+    s = s + v.x * v.x;
+    s = s + v.y * v.y;
+    s = s + v.z * v.z;
+    s = s + v.w * v.w;
+  }
+  return s;
+}
+
+}  // namespace ana

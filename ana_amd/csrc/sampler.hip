@@ -284,6 +284,67 @@ __global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t
   }
 }
 
+// the token loop's step end (see AdvanceArgs); step[1] counts the
+// workgroups done, so the last one moves the step index on
+template <int LPT>
+__global__ __launch_bounds__(1024) void k_advance(AdvanceArgs a, uint32_t NT) {
+  __shared__ float red[16];
+  __shared__ uint32_t redi[16];
+  const uint32_t b = blockIdx.x, tid = threadIdx.x, v = a.vocab;
+  const uint32_t k = a.step[0];
+  uint32_t t;
+  if (a.greedy) {
+    uint32_t cand;
+    if (a.amax) {
+      const unsigned long long key = a.amax[b];
+      cand = key ? 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull) : v;
+    } else {
+      cand = a.pick[b];
+    }
+    if (cand < v) {
+      t = cand;
+    } else {
+      // no logit reaches the max (NaN): Sample.argmax over the tree
+      const uint32_t base = tid * LPT;
+      const bool active = tid < NT;
+      const float* lg = a.logits + (size_t)b * v;
+      float x[LPT];
+#pragma unroll
+      for (int i = 0; i < LPT; i++) x[i] = (active && base + i < v) ? lg[base + i] : 0.0f;
+      t = tree_argmax<LPT>(x, base, v, red, redi, tid, NT);
+    }
+  } else {
+    t = a.pick[b];
+  }
+  if (tid == 0) {
+    a.out[(size_t)b * a.steps + k] = t;
+    a.tok[b] = t;
+    a.pos[b] = a.pos[b] + 1;
+    if (a.last) a.last[b] = t;
+    __threadfence();
+    if (atomicAdd(&a.step[1], 1u) == a.B - 1) {
+      a.step[1] = 0;
+      a.step[0] = k + 1;
+    }
+  }
+}
+
+hipError_t launch_advance(const AdvanceArgs& a, hipStream_t st) {
+  uint32_t dv = 0;
+  while ((1ull << dv) < a.vocab) dv++;
+  const uint64_t vpad = 1ull << dv;
+  const uint32_t lpt = vpad > 1024 ? (uint32_t)(vpad / 1024) : 1u;
+  const uint32_t NT = (uint32_t)(vpad / lpt);
+  switch (lpt) {
+#define ANA_ADV(L) \
+  case L: hipLaunchKernelGGL(k_advance<L>, dim3(a.B), dim3(1024), 0, st, a, NT); break;
+    ANA_ADV(1) ANA_ADV(2) ANA_ADV(4) ANA_ADV(8) ANA_ADV(16) ANA_ADV(32) ANA_ADV(64)
+#undef ANA_ADV
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_pick(const PickArgs& a, hipStream_t st) {
   uint32_t dv = 0;
   while ((1ull << dv) < a.vocab) dv++;
