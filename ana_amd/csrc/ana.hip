@@ -38,10 +38,13 @@ struct ana_ctx {
            *d_step = nullptr;
   uint64_t* d_rng = nullptr;
   unsigned long long* d_amax = nullptr;  // [wb] greedy argmax keys
+  float *d_ss = nullptr, *d_pm = nullptr; // split attention scratch
   size_t out_cap = 0;
   std::string err;
-  // one decode step of ana_generate captured as a HIP graph, replayed per step
-  hipGraphExec_t gexec = nullptr;
+  // ana_generate's decode step captured as HIP graphs, replayed per step:
+  // one step, and kGraphSteps steps back to back (a graph launch costs tens
+  // of microseconds on the host side, so several steps share one)
+  hipGraphExec_t gexec = nullptr, gexec_n = nullptr;
   struct GKey {
     uint32_t n, steps;
     float temp, topp;
@@ -55,19 +58,26 @@ struct ana_ctx {
   bool prof = false;
   double attn_bytes = 0.0;           // per softmax-layer launch of the current step
   std::vector<hipEvent_t> ev;        // pool, two per recorded launch
-  struct Rec { uint32_t kind; double bytes; };
+  struct Rec { uint32_t kind; double bytes; bool attn; };
   std::vector<Rec> recs;
+  uint64_t acc_n[ANA_K_KINDS] = {};
+  double acc_ms[ANA_K_KINDS] = {}, acc_bytes[ANA_K_KINDS] = {};
 };
+
+static const uint32_t kGraphSteps = 8;
 
 static const size_t kProfMax = 16384;
 
 // bracket one launch with events on the context's stream
+// (ext: the launch itself records the pair, hipExtLaunchKernelGGL's start
+// and stop events, which bracket exactly the kernel's execution)
 struct ProfScope {
   ana_ctx* c;
   uint32_t kind;
   double bytes;
-  bool on;
-  ProfScope(ana_ctx* c_, uint32_t k, double b) : c(c_), kind(k), bytes(b), on(false) {
+  bool on, ext;
+  ProfScope(ana_ctx* c_, uint32_t k, double b, bool ext_ = false)
+      : c(c_), kind(k), bytes(b), on(false), ext(ext_) {
     if (!c->prof || c->recs.size() >= kProfMax) return;
     const size_t i = c->recs.size();
     if (c->ev.size() < 2 * (i + 1)) {
@@ -77,13 +87,16 @@ struct ProfScope {
       c->ev.push_back(a);
       c->ev.push_back(e);
     }
-    if (hipEventRecord(c->ev[2 * i], c->st) != hipSuccess) return;
+    if (!ext && hipEventRecord(c->ev[2 * i], c->st) != hipSuccess) return;
     on = true;
   }
+  hipEvent_t start() const { return on && ext ? c->ev[2 * c->recs.size()] : nullptr; }
+  hipEvent_t stop() const { return on && ext ? c->ev[2 * c->recs.size() + 1] : nullptr; }
   ~ProfScope() {
     if (!on) return;
     const size_t i = c->recs.size();
-    if (hipEventRecord(c->ev[2 * i + 1], c->st) == hipSuccess) c->recs.push_back({kind, bytes});
+    if (ext || hipEventRecord(c->ev[2 * i + 1], c->st) == hipSuccess)
+      c->recs.push_back({kind, bytes, kind == ANA_K_ATTN});
   }
 };
 
@@ -117,8 +130,10 @@ static void release(ana_ctx* c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
+  if (c->gexec_n) (void)hipGraphExecDestroy(c->gexec_n);
   void* ps[] = {c->W, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
-                c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax};
+                c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
+                c->d_ss, c->d_pm};
   for (void* p : ps)
     if (p) (void)hipFree(p);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
@@ -201,6 +216,8 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = dalloc(&c->XN, wb * d)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_step, 2)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_amax, wb)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->d_ss, wb * cf.heads * cf.ctx)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->d_pm, wb * cf.heads * ((cf.ctx + kAttnTS - 1) / kAttnTS))) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->QKV, wb * 3 * d)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->Z, wb * d)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->O, wb * d)) != hipSuccess) return bad(e);
@@ -258,8 +275,8 @@ static double gemv_bytes(const GemvArgs& g) {
 }
 
 static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g, uint32_t kind) {
-  ProfScope ps(c, kind, gemv_bytes(g));
-  return launch_gemv(g, c->st);
+  ProfScope ps(c, kind, gemv_bytes(g), true);
+  return launch_gemv(g, c->st, ps.start(), ps.stop());
 }
 
 static GemvArgs gemv1(const float* X, uint32_t ldx, uint32_t K, const float* W, uint32_t rows,
@@ -326,6 +343,7 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
       a.sink = cf.sinks ? W + b.sink : nullptr;
       a.KV = sref(c, l);
       a.d = d; a.heads = cf.heads; a.ctx = cf.ctx;
+      a.ss = c->d_ss; a.pm = c->d_pm;
       if (!chunk) {
         // each sequence's write, then its attention (dd.sm.write, dd.sm.attend)
         a.QKV = c->QKV; a.O = c->O; a.B = B; a.seq = seq; a.pos = pos; a.write_kv = 1;
@@ -539,6 +557,7 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
   const size_t need = (size_t)n * steps;
   if (need > c->out_cap) {
     if (c->gexec) { HIPCHK(c, hipGraphExecDestroy(c->gexec)); c->gexec = nullptr; }
+    if (c->gexec_n) { HIPCHK(c, hipGraphExecDestroy(c->gexec_n)); c->gexec_n = nullptr; }
     if (c->d_out) HIPCHK(c, hipFree(c->d_out));
     c->d_out = nullptr;
     c->out_cap = 0;
@@ -551,8 +570,22 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
   if (!greedy) HIPCHK(c, hipMemcpyAsync(c->d_rng, rng, 32 * n, hipMemcpyHostToDevice, c->st));
   HIPCHK(c, launch_zero_u32(c->d_step, 2, c->st));
   const PickArgs pa = pick_args(c, n, greedy ? nullptr : s, 1);
+  // capture `count` steps into a graph
+  auto capture = [&](uint32_t count, hipGraphExec_t* ex) -> int {
+    hipGraph_t g = nullptr;
+    HIPCHK(c, hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
+    int r = 0;
+    for (uint32_t i = 0; i < count && !r; i++) r = gen_step(c, n, steps, pa, greedy);
+    const hipError_t ec = hipStreamEndCapture(c->st, &g);
+    if (r) { if (g) (void)hipGraphDestroy(g); return r; }
+    HIPCHK(c, ec);
+    const hipError_t ei = hipGraphInstantiate(ex, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    HIPCHK(c, ei);
+    return ANA_OK;
+  };
   if (c->prof) {
-    // timed launch by launch: no graph
+    // launch by launch, each product timed by its own start/stop events
     for (uint32_t k = 0; k < steps; k++) {
       c->attn_bytes = attn_bytes_of(c, pos, n, k);
       if (int r = gen_step(c, n, steps, pa, greedy)) return r;
@@ -561,18 +594,14 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
     ana_ctx::GKey key{n, steps, pa.temp, pa.topp, pa.topk, c->d_out};
     if (!c->gexec || !(c->gkey == key)) {
       if (c->gexec) { HIPCHK(c, hipGraphExecDestroy(c->gexec)); c->gexec = nullptr; }
-      hipGraph_t g = nullptr;
-      HIPCHK(c, hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
-      const int r = gen_step(c, n, steps, pa, greedy);
-      const hipError_t ec = hipStreamEndCapture(c->st, &g);
-      if (r) { if (g) (void)hipGraphDestroy(g); return r; }
-      HIPCHK(c, ec);
-      const hipError_t ei = hipGraphInstantiate(&c->gexec, g, nullptr, nullptr, 0);
-      (void)hipGraphDestroy(g);
-      HIPCHK(c, ei);
+      if (c->gexec_n) { HIPCHK(c, hipGraphExecDestroy(c->gexec_n)); c->gexec_n = nullptr; }
+      if (int r = capture(1, &c->gexec)) return r;
+      if (int r = capture(kGraphSteps, &c->gexec_n)) return r;
       c->gkey = key;
     }
-    for (uint32_t k = 0; k < steps; k++) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
+    uint32_t k = 0;
+    for (; k + kGraphSteps <= steps; k += kGraphSteps) HIPCHK(c, hipGraphLaunch(c->gexec_n, c->st));
+    for (; k < steps; k++) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
   }
   HIPCHK(c, launch_scatter_rows(c->X, c->d_seq, n, c->cfg.d, c->xs, c->st));
   HIPCHK(c, hipMemcpyAsync(out, c->d_out, 4 * need, hipMemcpyDeviceToHost, c->st));
@@ -586,6 +615,11 @@ extern "C" int ana_prof(ana_ctx* c, int on) {
   HIPCHK(c, hipStreamSynchronize(c->st));
   c->prof = on != 0;
   c->recs.clear();
+  for (uint32_t k = 0; k < ANA_K_KINDS; k++) {
+    c->acc_n[k] = 0;
+    c->acc_ms[k] = 0.0;
+    c->acc_bytes[k] = 0.0;
+  }
   return ANA_OK;
 }
 
@@ -593,8 +627,8 @@ extern "C" int ana_prof_read(ana_ctx* c, uint32_t kind, uint64_t* launches, doub
                              double* bytes) {
   if (!c || kind >= ANA_K_KINDS) return ANA_EINVAL;
   HIPCHK(c, hipStreamSynchronize(c->st));
-  uint64_t n = 0;
-  double t = 0.0, by = 0.0;
+  uint64_t n = c->acc_n[kind];
+  double t = c->acc_ms[kind], by = c->acc_bytes[kind];
   for (size_t i = 0; i < c->recs.size(); i++) {
     if (c->recs[i].kind != kind) continue;
     float e = 0.0f;

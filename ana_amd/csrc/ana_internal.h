@@ -65,7 +65,9 @@ struct GemvArgs {
 };
 // small-batch products take the norm and the argmax inside (B <= 4)
 constexpr uint32_t kSmallB = 4;
-hipError_t launch_gemv(const GemvArgs& a, hipStream_t st);
+// e0/e1: optional start/stop events recorded by the launch itself
+hipError_t launch_gemv(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nullptr,
+                       hipEvent_t e1 = nullptr);
 
 // dd.pick as a key: larger value wins, then the lower index; -0 counts as
 // +0 and NaN never enters (key 0 = no candidate)
@@ -122,7 +124,11 @@ struct AttnArgs {
   uint32_t pos0;        // when pos is nullptr: row b is at pos0 + b
   float* O;             // [B][d]
   uint32_t d, heads, ctx, B, write_kv;
+  float* ss;            // scratch [B][heads][ctx]: sc * score
+  float* pm;            // scratch [B][heads][ctx / kAttnTS]: partial maxima
 };
+// slots per workgroup in the split attention's score pass
+constexpr uint32_t kAttnTS = 128;
 hipError_t launch_attn(const AttnArgs& a, hipStream_t st);
 // each row's k (qk-normed when gk) and v into slot pos mod ctx (dd.sm.write)
 hipError_t launch_kv_write(const AttnArgs& a, hipStream_t st);

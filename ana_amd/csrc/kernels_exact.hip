@@ -10,6 +10,9 @@
 // and the wide, parallel part of the work (loading weights, forming
 // products) is spread over the whole workgroup and staged in LDS so that
 // the in-order chains only add.
+#include <hip/hip_ext.h>
+#include <stdlib.h>
+
 #include "ana_internal.h"
 #include "numerics.h"
 
@@ -17,52 +20,52 @@
 
 namespace ana {
 
-namespace {
-constexpr float4 kZero4 = {0.0f, 0.0f, 0.0f, 0.0f};
-}
+// a zero float4 in registers (a namespace-scope constant would be loaded
+// from memory through a flat pointer select)
+#define kZero4 make_float4(0.0f, 0.0f, 0.0f, 0.0f)
 
 // ------------------------------------------------------------------ products
 
-// Weight row and output slot of tile row r of workgroup tile t (R rows per
-// tile; in GM_SILU the first R/2 rows are gate rows j, the rest up rows j).
-__device__ __forceinline__ bool gemv_row(const GemvArgs& a, uint32_t R, uint32_t t, uint32_t r,
-                                         const float** w, uint32_t* seg, uint32_t* lr) {
-  if (a.mode == GM_SILU) {
+// The two row segments as plain values (a runtime index into GemvArgs.seg
+// would send every lookup through memory).
+struct Segs {
+  const float* W0;
+  const float* W1;
+  uint32_t rows0, rows1, nseg, silu, K;
+  __device__ __forceinline__ explicit Segs(const GemvArgs& a)
+      : W0(a.seg[0].W), W1(a.seg[1].W), rows0(a.seg[0].rows), rows1(a.seg[1].rows), nseg(a.nseg),
+        silu(a.mode == GM_SILU), K(a.K) {}
+  // weight row of tile row r of workgroup tile t (R rows per tile; with
+  // silu the first R/2 rows are gate rows j, the rest up rows j); written
+  // with selects only, so loads that depend on it stay in straight-line code
+  __device__ __forceinline__ bool row(uint32_t R, uint32_t t, uint32_t r, const float** w,
+                                      uint32_t* seg, uint32_t* lr) const {
     const uint32_t half = R >> 1;
-    const uint32_t s = r < half ? 0u : 1u;
-    const uint32_t j = t * half + (s ? r - half : r);
-    if (j >= a.seg[s].rows) return false;
-    *w = a.seg[s].W + (size_t)j * a.K;
-    *seg = s;
+    const uint32_t vs = t * R + r;
+    const uint32_t sg_s = r >= half ? 1u : 0u;
+    const uint32_t j_s = t * half + r - sg_s * half;
+    const uint32_t sg_p = vs >= rows0 ? 1u : 0u;
+    const uint32_t j_p = vs - sg_p * rows0;
+    const uint32_t sg = silu ? sg_s : sg_p;
+    const uint32_t j = silu ? j_s : j_p;
+    const bool ok = j < (sg ? rows1 : rows0) && (sg == 0 || nseg > 1);
+    *w = (sg ? W1 : W0) + (size_t)j * K;
+    *seg = sg;
     *lr = j;
-    return true;
+    return ok;
   }
-  const uint32_t vr = t * R + r;
-  uint32_t s = 0, j = vr;
-  if (j >= a.seg[0].rows) {
-    j -= a.seg[0].rows;
-    s = 1;
-    if (a.nseg < 2 || j >= a.seg[1].rows) return false;
-  }
-  *w = a.seg[s].W + (size_t)j * a.K;
-  *seg = s;
-  *lr = j;
-  return true;
-}
+};
 
-// the result of chain (b, r): plain, plus the residual, or (GM_SILU, via
-// LDS `outs` [BT][R]) silu(gate) * up
-__device__ __forceinline__ void gemv_store(const GemvArgs& a, uint32_t R, uint32_t t, uint32_t r,
-                                           uint32_t b, float s) {
-  const float* wp;
-  uint32_t sg, lr;
-  if (!gemv_row(a, R, t, r, &wp, &sg, &lr)) return;
+// the result of chain (b, row lr of segment sg): plain or plus the residual
+__device__ __forceinline__ void gemv_store(const GemvArgs& a, uint32_t sg, uint32_t lr, uint32_t b,
+                                           float s) {
   float y = s;
   if (a.mode == GM_RESID) y = a.R[(size_t)b * a.ldr + lr] + s;
-  a.seg[sg].Y[(size_t)b * a.seg[sg].ldy + lr] = y;
+  if (sg) a.seg[1].Y[(size_t)b * a.seg[1].ldy + lr] = y;
+  else a.seg[0].Y[(size_t)b * a.seg[0].ldy + lr] = y;
 }
 
-// Small batches (B <= 4 rows per workgroup): R x BT chain lanes (<= 32, one
+// Small batches (B <= 4 rows per workgroup): R x BT chain lanes (<= 64, one
 // wave). The weights of a K chunk are loaded into registers, up to 16 float4
 // a thread, all in flight at once (the next chunk's while the current one
 // is being summed); the activations sit in LDS. With `ng` the workgroup
@@ -87,34 +90,48 @@ __global__ __launch_bounds__(256) void k_gemv_small(GemvArgs a, uint32_t R, uint
   float* rs = outs + ((Lc + 3) & ~3u);                    // [4]
   float4* Xf = reinterpret_cast<float4*>(rs + 4);         // [BT][K/4] when ng
 
+  const Segs sgs(a);
   float4 w[16];
   // weights of the chunk at q0 into w[]; item i = tid + 256 j is (row r, float4 q4)
   auto load_w = [&](uint32_t q0) {
+    // branch-free, so the compiler keeps all 16 loads in flight (a load
+    // inside a branch gets a full wait at the branch's end)
     const uint32_t qc4 = min(QC, K - q0) >> 2;
     const uint32_t dr = 256 / qc4, dq = 256 - dr * qc4;
     uint32_t r = tid / qc4, q4 = tid - r * qc4;
 #pragma unroll
     for (int j = 0; j < 16; j++) {
-      w[j] = kZero4;
       const float* wp;
       uint32_t sg, lr;
-      if (r < R && gemv_row(a, R, blockIdx.x, r, &wp, &sg, &lr))
-        w[j] = *reinterpret_cast<const float4*>(wp + q0 + 4 * q4);
+      const bool okr = sgs.row(R, blockIdx.x, r, &wp, &sg, &lr);
+      const bool ok = (r < R) & okr;
+      // an item outside the tile loads W0's first float4 instead: its
+      // products belong to no stored output, so its value never matters
+      const size_t off = ok ? (size_t)(wp - sgs.W0) + q0 + 4 * q4 : 0;
+      w[j] = *reinterpret_cast<const float4*>(sgs.W0 + off);
       r += dr;
       q4 += dq;
-      if (q4 >= qc4) { q4 -= qc4; r++; }
+      const uint32_t wrap = q4 >= qc4 ? 1u : 0u;
+      q4 -= wrap * qc4;
+      r += wrap;
     }
   };
-  load_w(0);
   if (a.ng) {
-    const uint32_t K4 = K >> 2;
-    for (uint32_t i = tid; i < BT * K4; i += 256) {
+    // the activation rows into LDS first, then the weights are issued and
+    // the norm's chain runs while they arrive
+    const uint32_t K4 = K >> 2, n4 = BT * K4;
+    for (uint32_t i = tid; i < n4; i += 256) {
       const uint32_t b = i / K4, k4 = i - b * K4;
-      Xf[i] = b < nb ? *reinterpret_cast<const float4*>(a.X + (size_t)(b0 + b) * a.ldx + 4 * k4) : kZero4;
+      float4 x = kZero4;
+      if (b < nb) x = *reinterpret_cast<const float4*>(a.X + (size_t)(b0 + b) * a.ldx + 4 * k4);
+      Xf[i] = x;
     }
     __syncthreads();
+    load_w(0);
     if (tid < nb) rs[tid] = ex_rms_scale(chain_sumsq_lds(0.0f, reinterpret_cast<const float*>(Xf + tid * K4), K), (float)K);
     __syncthreads();
+  } else {
+    load_w(0);
   }
   float s = 0.0f;
   for (uint32_t q0 = 0; q0 < K; q0 += QC) {
@@ -170,7 +187,11 @@ __global__ __launch_bounds__(256) void k_gemv_small(GemvArgs a, uint32_t R, uint
     }
     return;
   }
-  if (tid < Lc && b < nb) gemv_store(a, R, blockIdx.x, r, b0 + b, s);
+  if (tid < Lc && b < nb) {
+    const float* wp;
+    uint32_t sg, lr;
+    if (sgs.row(R, blockIdx.x, r, &wp, &sg, &lr)) gemv_store(a, sg, lr, b0 + b, s);
+  }
   if (a.amax && tid < 64) {
     // the workgroup's best key per batch row, then one atomic each
     unsigned long long key = 0;
@@ -206,9 +227,10 @@ __global__ __launch_bounds__(256) void k_gemm_exact(GemvArgs a) {
   const uint32_t r = tid % RT, bg = tid / RT;
   const uint32_t b0 = blockIdx.y * 64;
   const uint32_t nb = min(64u, a.B - b0);
+  const Segs sgs(a);
   const float* wrow;
   uint32_t sg, lr;
-  const bool rok = gemv_row(a, RT, blockIdx.x, r, &wrow, &sg, &lr);
+  const bool rok = sgs.row(RT, blockIdx.x, r, &wrow, &sg, &lr);
   float s[CPT];
 #pragma unroll
   for (int j = 0; j < CPT; j++) s[j] = 0.0f;
@@ -219,15 +241,15 @@ __global__ __launch_bounds__(256) void k_gemm_exact(GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const uint32_t i = tid + 256 * j, b = i & 63, q4 = i >> 6;
-      xv[j] = (q4 < qc4 && b < nb) ? *reinterpret_cast<const float4*>(a.X + (size_t)(b0 + b) * a.ldx + q0 + 4 * q4)
-                                   : kZero4;
+      xv[j] = kZero4;
+      if (q4 < qc4 && b < nb) xv[j] = *reinterpret_cast<const float4*>(a.X + (size_t)(b0 + b) * a.ldx + q0 + 4 * q4);
     }
     float4 wv = kZero4;
     const uint32_t wi = tid, wr = wi / 16, wq4 = wi % 16;
     if (wr < RT && wq4 < qc4) {
       const float* wp;
       uint32_t s2, l2;
-      if (gemv_row(a, RT, blockIdx.x, wr, &wp, &s2, &l2)) wv = *reinterpret_cast<const float4*>(wp + q0 + 4 * wq4);
+      if (sgs.row(RT, blockIdx.x, wr, &wp, &s2, &l2)) wv = *reinterpret_cast<const float4*>(wp + q0 + 4 * wq4);
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -273,33 +295,56 @@ __global__ __launch_bounds__(256) void k_gemm_exact(GemvArgs a) {
     }
     return;
   }
+  if (rok) {
 #pragma unroll
-  for (int j = 0; j < CPT; j++) {
-    const uint32_t b = bg * CPT + j;
-    if (b < nb) gemv_store(a, RT, blockIdx.x, r, b0 + b, s[j]);
+    for (int j = 0; j < CPT; j++) {
+      const uint32_t b = bg * CPT + j;
+      if (b < nb) gemv_store(a, sg, lr, b0 + b, s[j]);
+    }
   }
 }
 
 static size_t small_lds(uint32_t R, uint32_t BT, uint32_t QC, uint32_t K, bool norm) {
   const uint32_t Lc = R * BT, Lc4 = (Lc + 3) & ~3u;
   return (size_t)BT * (QC / 4) * 16 + (size_t)Lc * (QC / 4 + 1) * 16 + (size_t)Lc4 * 4 + 16 +
-         (norm ? (size_t)BT * K * 4 : 0);
+         (norm ? (size_t)BT * K * 4 + 16 : 0);
 }
 
-hipError_t launch_gemv(const GemvArgs& a, hipStream_t st) {
+// tile sizing knobs (environment, read once): workgroups a small-batch
+// product aims for, and its most rows per workgroup
+static uint32_t env_u32(const char* name, uint32_t dflt) {
+  const char* v = getenv(name);
+  if (!v || !*v) return dflt;
+  const unsigned long x = strtoul(v, nullptr, 10);
+  return x ? (uint32_t)x : dflt;
+}
+static const uint32_t kTargetWgs = env_u32("ANA_GEMV_WGS", 256);
+static const uint32_t kRmax = env_u32("ANA_GEMV_RMAX", 64);
+
+// a launch, through hipExtLaunchKernelGGL when timing events are given
+#define ANA_LAUNCH(K, GRID, BLOCK, LDS, ST, E0, E1, ...)                                 \
+  do {                                                                                  \
+    if (E0) hipExtLaunchKernelGGL(K, GRID, BLOCK, LDS, ST, E0, E1, 0, __VA_ARGS__);      \
+    else hipLaunchKernelGGL(K, GRID, BLOCK, LDS, ST, __VA_ARGS__);                      \
+  } while (0)
+
+hipError_t launch_gemv(const GemvArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
                                           : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
   if (a.B <= kSmallB) {
     const uint32_t BT = a.B <= 1 ? 1 : a.B <= 2 ? 2 : 4;
-    // rows per workgroup: about one workgroup per CU, chain lanes <= 64
-    uint32_t R = rows / 256;
+    // rows per workgroup: chain lanes fill (at most) one wave, and a wave
+    // of chains costs the SIMD the same issue slots however few lanes it
+    // has, so fewer, fuller workgroups win
+    uint32_t R = rows / kTargetWgs;
     R = R < 1 ? 1 : R;
-    const uint32_t rmax = 32 / BT;
+    uint32_t rmax = 64 / BT;
+    rmax = rmax > kRmax ? kRmax : rmax;
     R = R > rmax ? rmax : R;
     if (a.mode == GM_SILU) R = R < 2 ? 2 : (R & ~1u);
     const uint32_t Lc = R * BT;
     uint32_t QC = a.K;
-    const uint32_t fixed = 16 * Lc + 4 * ((Lc + 3) & ~3u) + 16 + (a.ng ? BT * a.K * 4 : 0);
+    const uint32_t fixed = 16 * Lc + 4 * ((Lc + 3) & ~3u) + 16 + (a.ng ? BT * a.K * 4 + 16 : 0);
     const uint32_t by_lds = (65536 - fixed) / (4 * (BT + Lc));
     const uint32_t by_regs = 16384 / R;
     QC = QC < by_lds ? QC : by_lds;
@@ -309,11 +354,12 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t st) {
     const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
     dim3 grid(tiles, (a.B + BT - 1) / BT);
     const size_t lds = small_lds(R, BT, QC, a.K, a.ng != nullptr);
-    if (QC < 4 || lds > 65536 || R * (QC / 4) > 16 * 256) return hipErrorInvalidValue;
+    if (QC < 4 || lds > 65536 || R * (QC / 4) > 16 * 256 || (a.ng && BT * a.K > 8192))
+      return hipErrorInvalidValue;
     switch (BT) {
-      case 1: hipLaunchKernelGGL(k_gemv_small<1>, grid, dim3(256), lds, st, a, R, QC); break;
-      case 2: hipLaunchKernelGGL(k_gemv_small<2>, grid, dim3(256), lds, st, a, R, QC); break;
-      default: hipLaunchKernelGGL(k_gemv_small<4>, grid, dim3(256), lds, st, a, R, QC); break;
+      case 1: ANA_LAUNCH(k_gemv_small<1>, grid, dim3(256), lds, st, e0, e1, a, R, QC); break;
+      case 2: ANA_LAUNCH(k_gemv_small<2>, grid, dim3(256), lds, st, e0, e1, a, R, QC); break;
+      default: ANA_LAUNCH(k_gemv_small<4>, grid, dim3(256), lds, st, e0, e1, a, R, QC); break;
     }
     return hipGetLastError();
   }
@@ -322,8 +368,8 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t st) {
   const uint32_t per = a.mode == GM_SILU ? RT / 2 : RT;
   const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
   dim3 grid(tiles, (a.B + 63) / 64);
-  if (RT == 16) hipLaunchKernelGGL(k_gemm_exact<16>, grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(k_gemm_exact<4>, grid, dim3(256), 0, st, a);
+  if (RT == 16) ANA_LAUNCH(k_gemm_exact<16>, grid, dim3(256), 0, st, e0, e1, a);
+  else ANA_LAUNCH(k_gemm_exact<4>, grid, dim3(256), 0, st, e0, e1, a);
   return hipGetLastError();
 }
 
@@ -630,8 +676,160 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   if (tid < HD) a.O[(size_t)b * d + h * HD + tid] = (1.0f / red[0]) * oi;
 }
 
+// The same attention split over workgroups, for few rows at long context.
+// Pass 1, per (head, block of kAttnTS slots, row): the row's write (by the
+// block holding its slot), its scores sc*s into `ss` and the block's max
+// into `pm`. Pass 2, per (head, 16 columns, row): m from the blocks' maxima
+// (a max is exact in any order), then e = exp(sc*s - m), the products e*V
+// and the in-order chains se and oi, slot block after slot block.
+template <int HD>
+__global__ __launch_bounds__(kAttnTS) void k_attn_scores(AttnArgs a) {
+  __shared__ float q[HD], kk[HD], vs[HD], red[2], nrm[2];
+  const uint32_t h = blockIdx.x, sb = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const uint32_t d = a.d, ctx = a.ctx, ns = (ctx + kAttnTS - 1) / kAttnTS;
+  const uint32_t pos = a.pos ? a.pos[b] : a.pos0 + b;
+  const uint32_t slot = pos % ctx, npos = pos < ctx - 1 ? pos : ctx - 1;
+  const uint32_t sl = a.seq ? a.seq[b] : a.seq0;
+  float* Kr = a.KV.base + (size_t)sl * a.KV.seq_stride + a.KV.layer_off;
+  float* Vr = Kr + (size_t)ctx * d;
+  const uint32_t t0 = sb * kAttnTS;
+  float* pm = a.pm + ((size_t)b * a.heads + h) * ns;
+  if (t0 > npos) {
+    if (tid == 0) pm[sb] = -INFINITY;
+    return;
+  }
+  const bool mine = a.write_kv && slot >= t0 && slot < t0 + kAttnTS;
+  const float* x = a.QKV + (size_t)b * 3 * d;
+  if (tid < HD) {
+    q[tid] = x[h * HD + tid];
+    if (mine) {
+      kk[tid] = x[d + h * HD + tid];
+      vs[tid] = x[2 * d + h * HD + tid];
+    }
+  }
+  __syncthreads();
+  if (a.gq) {
+    if (tid == 0) nrm[0] = ex_rms_scale(chain_sumsq_lds(0.0f, q, HD), (float)HD);
+    else if (tid == 64 && mine) nrm[1] = ex_rms_scale(chain_sumsq_lds(0.0f, kk, HD), (float)HD);
+    __syncthreads();
+    if (tid < HD) {
+      q[tid] = (q[tid] * nrm[0]) * (1.0f + a.gq[tid]);
+      if (mine) kk[tid] = (kk[tid] * nrm[1]) * (1.0f + a.gk[tid]);
+    }
+    __syncthreads();
+  }
+  if (mine && tid < HD) {
+    Kr[(size_t)slot * d + h * HD + tid] = kk[tid];
+    Vr[(size_t)slot * d + h * HD + tid] = vs[tid];
+  }
+  const float sc = 1.0f / csqrt((float)HD);
+  const uint32_t t = t0 + tid;
+  float y = -INFINITY;
+  if (t <= npos) {
+    float acc = 0.0f;
+    if (mine && t == slot) {
+#pragma unroll
+      for (int c = 0; c < HD; c++) acc = acc + q[c] * kk[c];
+    } else {
+      const float4* k4 = reinterpret_cast<const float4*>(Kr + (size_t)t * d + h * HD);
+      float4 kv[HD / 4];
+#pragma unroll
+      for (int u = 0; u < HD / 4; u++) kv[u] = k4[u];
+#pragma unroll
+      for (int u = 0; u < HD / 4; u++) {
+        acc = acc + q[4 * u + 0] * kv[u].x;
+        acc = acc + q[4 * u + 1] * kv[u].y;
+        acc = acc + q[4 * u + 2] * kv[u].z;
+        acc = acc + q[4 * u + 3] * kv[u].w;
+      }
+    }
+    y = sc * acc;
+    a.ss[((size_t)b * a.heads + h) * ctx + t] = y;
+  }
+  const float r = wave_max_gt(y);
+  if ((tid & 63) == 0) red[tid >> 6] = r;
+  __syncthreads();
+  if (tid == 0) pm[sb] = red[1] > red[0] ? red[1] : red[0];
+}
+
+#define ATTN_CG 16
+#define ATTN_TC2 256
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_out(AttnArgs a) {
+  constexpr int PS = ATTN_TC2 + 4;
+  __shared__ __align__(16) float es[ATTN_TC2];
+  __shared__ __align__(16) float P[ATTN_CG * PS];
+  __shared__ float red[1];
+  const uint32_t h = blockIdx.x, cg = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const uint32_t d = a.d, ctx = a.ctx, ns = (ctx + kAttnTS - 1) / kAttnTS;
+  const uint32_t pos = a.pos ? a.pos[b] : a.pos0 + b;
+  const uint32_t npos = pos < ctx - 1 ? pos : ctx - 1;
+  const uint32_t sl = a.seq ? a.seq[b] : a.seq0;
+  const float* Vr = a.KV.base + (size_t)sl * a.KV.seq_stride + a.KV.layer_off + (size_t)ctx * d;
+  const float* ssr = a.ss + ((size_t)b * a.heads + h) * ctx;
+  const float* pm = a.pm + ((size_t)b * a.heads + h) * ns;
+  float m = -INFINITY;
+  for (uint32_t i = 0; i <= npos / kAttnTS; i++) m = pm[i] > m ? pm[i] : m;
+  float sink = 0.0f;
+  if (a.sink) {
+    sink = a.sink[h];
+    m = ex_max(m, sink);    // dd.sm.max: m1 < sink ? sink : m1
+  }
+  const uint32_t c0 = cg * ATTN_CG;
+  float oi = 0.0f, se = 0.0f;
+  // V for a chunk: items (t, float4 c4) of this column group, 4 a thread
+  constexpr int NV = ATTN_TC2 * (ATTN_CG / 4) / 256;
+  float4 vv[NV];
+  float sv = 0.0f;
+  auto load = [&](uint32_t t0) {
+    const uint32_t tc = min((uint32_t)ATTN_TC2, npos + 1 - t0);
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      const uint32_t i = tid + 256 * j, t = i / (ATTN_CG / 4), c4 = i % (ATTN_CG / 4);
+      const uint32_t tt = t < tc ? t0 + t : t0;
+      vv[j] = *reinterpret_cast<const float4*>(Vr + (size_t)tt * d + h * HD + c0 + 4 * c4);
+    }
+    sv = tid < tc ? ssr[t0 + tid] : 0.0f;
+  };
+  load(0);
+  for (uint32_t t0 = 0; t0 <= npos; t0 += ATTN_TC2) {
+    const uint32_t tc = min((uint32_t)ATTN_TC2, npos + 1 - t0);
+    if (tid < tc) es[tid] = dexp(sv - m);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      const uint32_t i = tid + 256 * j, t = i / (ATTN_CG / 4), c4 = i % (ATTN_CG / 4);
+      if (t < tc) {
+        const float e = es[t];
+        P[(4 * c4 + 0) * PS + t] = e * vv[j].x;
+        P[(4 * c4 + 1) * PS + t] = e * vv[j].y;
+        P[(4 * c4 + 2) * PS + t] = e * vv[j].z;
+        P[(4 * c4 + 3) * PS + t] = e * vv[j].w;
+      }
+    }
+    if (t0 + ATTN_TC2 <= npos) load(t0 + ATTN_TC2);
+    __syncthreads();
+    if (tid < ATTN_CG) oi = chain_sum_lds(oi, P + tid * PS, tc);
+    else if (tid == 64) se = chain_sum_lds(se, es, tc);
+    __syncthreads();
+  }
+  if (tid == 64) red[0] = a.sink ? se + dexp(sink - m) : se;
+  __syncthreads();
+  if (tid < ATTN_CG) a.O[(size_t)b * d + h * HD + c0 + tid] = (1.0f / red[0]) * oi;
+}
+
 hipError_t launch_attn(const AttnArgs& a, hipStream_t st) {
   const uint32_t hd = a.d / a.heads;
+  if (a.ss && a.pm && hd % ATTN_CG == 0) {
+    const uint32_t ns = (a.ctx + kAttnTS - 1) / kAttnTS;
+#define L_(H)                                                                                   \
+  hipLaunchKernelGGL(k_attn_scores<H>, dim3(a.heads, ns, a.B), dim3(kAttnTS), 0, st, a);      \
+  hipLaunchKernelGGL(k_attn_out<H>, dim3(a.heads, H / ATTN_CG, a.B), dim3(256), 0, st, a)
+    ANA_HD_DISPATCH(hd, L_)
+#undef L_
+    return hipGetLastError();
+  }
   const size_t lds = ((size_t)a.ctx + (size_t)hd * (ATTN_TC + 4)) * 4;
 #define L_(H) hipLaunchKernelGGL(k_attn<H>, dim3(a.heads, a.B), dim3(256), lds, st, a)
   ANA_HD_DISPATCH(hd, L_)
