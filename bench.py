@@ -50,11 +50,12 @@ def ensure_ckpt(c: cf.Config, path: str) -> str:
     return path
 
 
-def step_bytes(c: cf.Config, positions) -> float:
-    """Algorithmic HBM bytes of one decode step: every weight once (the tied
-    head reads all of E; the gather reads one row per sequence), per
-    sequence the GLA states read and written and the live K/V rows read."""
-    w = 4.0 * (c.params - c.vocab * c.d + c.vocab * c.d)
+def run_bytes(c: cf.Config, positions, steps: int) -> float:
+    """Algorithmic HBM bytes of `steps` decode steps: every weight once per
+    step (the tied head reads all of E; the gather reads one row per
+    sequence), and per (sequence, position) the GLA states read and written
+    and the live K/V rows read."""
+    w = 4.0 * (c.params - c.vocab * c.d + c.vocab * c.d) * steps
     per = 0.0
     for p in positions:
         live = min(p, c.ctx - 1) + 1
@@ -89,7 +90,7 @@ def run_batch(path: str, c: cf.Config, B: int, prompt: int, warmup: int, steps: 
         stats = dec.prof_read()
         dec.prof(False)
     dt = t1 - t0
-    sb = step_bytes(c, positions) / steps
+    sb = run_bytes(c, positions, steps) / steps
     return {
         "tok_s": B * steps / dt,
         "ms_per_step": 1000.0 * dt / steps,
