@@ -293,15 +293,9 @@ static GemvArgs gemv1(const float* X, uint32_t ldx, uint32_t K, const float* W, 
 // RMSNorm(X; g) then the product: inside the product for small batches,
 // else a norm kernel into XN first
 static int norm_gemv(ana_ctx* c, const float* X, const float* g, GemvArgs a, uint32_t kind) {
-  if (a.B <= kSmallB) {
-    a.X = X;
-    a.ldx = c->cfg.d;
-    a.ng = g;
-  } else {
-    HIPCHK(c, launch_rmsnorm(X, g, c->cfg.d, a.B, c->XN, c->st));
-    a.X = c->XN;
-    a.ldx = c->cfg.d;
-  }
+  a.X = X;
+  a.ldx = c->cfg.d;
+  a.ng = g;
   HIPCHK(c, gemv_timed(c, a, kind));
   return ANA_OK;
 }

@@ -211,95 +211,251 @@ __global__ __launch_bounds__(256) void k_gemv_small(GemvArgs a, uint32_t R, uint
   }
 }
 
-// Larger batches: a tile of RT rows x 64 batch rows, every thread owning RT/4
-// chains (one row, RT/4 consecutive batch rows). Per K chunk of 64 the
-// weights [r][q] and the activations, transposed to [q][b], sit in LDS; each
-// chain multiplies and adds in q order.
-template <int RT>
+// Larger batches (prefill chunks, batched decode): a tile of TR weight rows
+// x TB batch rows per workgroup; thread (ti, tj) owns RI x BJ chains (rows
+// ti*RI.., batch rows tj*BJ..). The K axis goes in chunks of KC. Every
+// thread moves NL float4 of each chunk (weights and activations, coalesced
+// along k) through a ring of D register sets, so D-1 chunks are in flight
+// from HBM while one is added; a chunk is stored k-major into one of two
+// LDS buffers, and each chain multiplies and adds in q order out of LDS:
+// bulk.c's ft_gemm_loop, one lane per output. With `ng` the workgroup first
+// runs M.norm's sum of squares for its TB rows (one in-order chain per row,
+// while the first chunks are in flight) and stages (x * rs) * g.
+template <int TR, int TB, int RI, int BJ, int KC, int D, int G>
 __global__ __launch_bounds__(256) void k_gemm_exact(GemvArgs a) {
-  constexpr int CPT = RT / 4;
-  constexpr int QC = 64;
-  constexpr int XS = 64 + 4;
-  __shared__ float Ws[RT][QC + 4];
-  __shared__ float Xs[QC][XS];
-  __shared__ float outs[64][RT];
+  constexpr int NJ = TB / BJ, NI = TR / RI;
+  static_assert(NI * NJ == 256, "one chain block per thread");
+  constexpr int K4 = KC / 4;
+  constexpr int LW = TR * K4, LX = TB * K4, NL = (LW + LX + 255) / 256;
+  static_assert(K4 % (2 * G) == 0, "whole read groups per chunk");
+  __shared__ float4 Ws[2][K4][TR + 1];
+  __shared__ float4 Xs[2][K4][TB + 1];
+  __shared__ float rs[TB];
+  __shared__ float outs[TB][TR + 1];
   const uint32_t tid = threadIdx.x;
-  const uint32_t r = tid % RT, bg = tid / RT;
-  const uint32_t b0 = blockIdx.y * 64;
-  const uint32_t nb = min(64u, a.B - b0);
+  const uint32_t tj = tid % NJ, ti = tid / NJ;
+  const uint32_t b0 = blockIdx.y * TB;
+  const uint32_t nb = min((uint32_t)TB, a.B - b0);
   const Segs sgs(a);
-  const float* wrow;
-  uint32_t sg, lr;
-  const bool rok = sgs.row(RT, blockIdx.x, r, &wrow, &sg, &lr);
-  float s[CPT];
+  const bool norm = a.ng != nullptr;
+  const uint32_t nch = (a.K + KC - 1) / KC;
+
+  // the NL float4 this thread moves per chunk: item i = tid + 256 j;
+  // i < LW: weight row i / K4, k4 = i % K4; else batch row (i-LW) / K4
+  const float* src[NL];
+  uint32_t dk4[NL], drow[NL];
+  bool ok[NL];
 #pragma unroll
-  for (int j = 0; j < CPT; j++) s[j] = 0.0f;
-  for (uint32_t q0 = 0; q0 < a.K; q0 += QC) {
-    const uint32_t qc = min((uint32_t)QC, a.K - q0), qc4 = qc >> 2;
-    // activations: 64 x qc, transposed into Xs[q][b]; all loads first
-    float4 xv[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const uint32_t i = tid + 256 * j, b = i & 63, q4 = i >> 6;
-      xv[j] = kZero4;
-      if (q4 < qc4 && b < nb) xv[j] = *reinterpret_cast<const float4*>(a.X + (size_t)(b0 + b) * a.ldx + q0 + 4 * q4);
+  for (int j = 0; j < NL; j++) {
+    const uint32_t i = tid + 256 * j;
+    if (i < (uint32_t)LW) {
+      const uint32_t r = i / K4;
+      const float* w;
+      uint32_t sg, lr;
+      ok[j] = sgs.row(TR, blockIdx.x, r, &w, &sg, &lr);
+      src[j] = ok[j] ? w : sgs.W0;
+      dk4[j] = i % K4;
+      drow[j] = r;
+    } else {
+      const uint32_t b = (i - LW) / K4;
+      ok[j] = b < nb && i < (uint32_t)(LW + LX);
+      src[j] = a.X + (size_t)(b0 + (ok[j] ? b : 0)) * a.ldx;
+      dk4[j] = (i - LW) % K4;
+      drow[j] = b;
     }
-    float4 wv = kZero4;
-    const uint32_t wi = tid, wr = wi / 16, wq4 = wi % 16;
-    if (wr < RT && wq4 < qc4) {
-      const float* wp;
-      uint32_t s2, l2;
-      if (sgs.row(RT, blockIdx.x, wr, &wp, &s2, &l2)) wv = *reinterpret_cast<const float4*>(wp + q0 + 4 * wq4);
+  }
+  float4 v[D][NL];
+  auto load = [&](float4 (&r)[NL], uint32_t c) {
+#pragma unroll
+    for (int j = 0; j < NL; j++) {
+      const uint32_t q = c * KC + 4 * dk4[j];
+      const bool in = ok[j] && q < a.K;
+      // an unconditional load from a clamped address, so that it stays in
+      // flight; items out of range are never added or stored, so they are
+      // not zeroed (writing the destination would wait for the load)
+      r[j] = *reinterpret_cast<const float4*>(src[j] + (in ? q : 0));
     }
+  };
+  auto store = [&](const float4 (&r)[NL], int buf, uint32_t c) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const uint32_t i = tid + 256 * j, b = i & 63, q4 = i >> 6;
-      Xs[4 * q4 + 0][b] = xv[j].x;
-      Xs[4 * q4 + 1][b] = xv[j].y;
-      Xs[4 * q4 + 2][b] = xv[j].z;
-      Xs[4 * q4 + 3][b] = xv[j].w;
-    }
-    if (wr < RT) *reinterpret_cast<float4*>(&Ws[wr][4 * wq4]) = wv;
-    __syncthreads();
-    for (uint32_t q = 0; q < qc; q += 4) {
-      const float4 w = *reinterpret_cast<const float4*>(&Ws[r][q]);
-      const float wq[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        if constexpr (CPT == 4) {
-          const float4 x = *reinterpret_cast<const float4*>(&Xs[q + u][bg * 4]);
-          s[0] = s[0] + x.x * wq[u];
-          s[1] = s[1] + x.y * wq[u];
-          s[2] = s[2] + x.z * wq[u];
-          s[3] = s[3] + x.w * wq[u];
-        } else {
-#pragma unroll
-          for (int j = 0; j < CPT; j++) s[j] = s[j] + Xs[q + u][bg * CPT + j] * wq[u];
+    for (int j = 0; j < NL; j++) {
+      const uint32_t i = tid + 256 * j;
+      if (i < (uint32_t)LW) {
+        Ws[buf][dk4[j]][drow[j]] = r[j];
+      } else if (i < (uint32_t)(LW + LX)) {
+        float4 x = r[j];
+        if (norm) {
+          const uint32_t q = c * KC + 4 * dk4[j];
+          const float sc = rs[drow[j]];
+          const float4 g = *reinterpret_cast<const float4*>(a.ng + (q < a.K ? q : 0));
+          x.x = (x.x * sc) * g.x;
+          x.y = (x.y * sc) * g.y;
+          x.z = (x.z * sc) * g.z;
+          x.w = (x.w * sc) * g.w;
         }
+        Xs[buf][dk4[j]][drow[j]] = x;
       }
     }
+  };
+
+#pragma unroll
+  for (int u = 0; u < D; u++)
+    if ((uint32_t)u < nch) load(v[u], u);
+  if (norm) {
+    // M.norm (bend/Dense/Model.bend:27-30): ss = sum_q x_q * x_q in order,
+    // one chain per batch row over the activations staged chunk by chunk
+    // through the X buffers (the weights of the first chunks keep arriving)
+    constexpr int PX = (LX + 255) / 256;
+    float4 xr[2][PX];
+    auto xload = [&](float4 (&r)[PX], uint32_t c) {
+#pragma unroll
+      for (int j = 0; j < PX; j++) {
+        const uint32_t i = tid + 256 * j, b = i / K4, q = c * KC + 4 * (i % K4);
+        const bool in = i < (uint32_t)LX && b < nb && q < a.K;
+        r[j] = *reinterpret_cast<const float4*>(a.X + (size_t)(b0 + (in ? b : 0)) * a.ldx + (in ? q : 0));
+      }
+    };
+    auto xstore = [&](const float4 (&r)[PX], int buf) {
+#pragma unroll
+      for (int j = 0; j < PX; j++) {
+        const uint32_t i = tid + 256 * j;
+        if (i < (uint32_t)LX) Xs[buf][i % K4][i / K4] = r[j];
+      }
+    };
+    float ss = 0.0f;
+    xload(xr[0], 0);
+    xstore(xr[0], 0);
+    __syncthreads();
+    for (uint32_t c = 0; c < nch; c++) {
+      const int bf = c & 1;
+      if (c + 1 < nch) xload(xr[1], c + 1);
+      if (tid < (uint32_t)TB) {
+        const uint32_t n4 = min((uint32_t)K4, (a.K - c * KC) >> 2);
+#pragma unroll 8
+        for (uint32_t k4 = 0; k4 < n4; k4++) {
+          const float4 x = Xs[bf][k4][tid];
+          ss = ss + x.x * x.x;
+          ss = ss + x.y * x.y;
+          ss = ss + x.z * x.z;
+          ss = ss + x.w * x.w;
+        }
+      }
+      if (c + 1 < nch) xstore(xr[1], bf ^ 1);
+      __syncthreads();
+    }
+    if (tid < (uint32_t)TB) rs[tid] = ex_rms_scale(ss, (float)a.K);
     __syncthreads();
   }
+  store(v[0], 0, 0);
+  __syncthreads();
+
+  float s[RI][BJ];
+#pragma unroll
+  for (int i = 0; i < RI; i++)
+#pragma unroll
+    for (int j = 0; j < BJ; j++) s[i][j] = 0.0f;
+
+  auto step = [&](const float4 (&w)[RI], const float4 (&x)[BJ]) {
+#pragma unroll
+    for (int i = 0; i < RI; i++)
+#pragma unroll
+      for (int j = 0; j < BJ; j++) s[i][j] = s[i][j] + x[j].x * w[i].x;
+#pragma unroll
+    for (int i = 0; i < RI; i++)
+#pragma unroll
+      for (int j = 0; j < BJ; j++) s[i][j] = s[i][j] + x[j].y * w[i].y;
+#pragma unroll
+    for (int i = 0; i < RI; i++)
+#pragma unroll
+      for (int j = 0; j < BJ; j++) s[i][j] = s[i][j] + x[j].z * w[i].z;
+#pragma unroll
+    for (int i = 0; i < RI; i++)
+#pragma unroll
+      for (int j = 0; j < BJ; j++) s[i][j] = s[i][j] + x[j].w * w[i].w;
+  };
+  // one chunk out of LDS buffer buf: groups of G k4 steps in two register
+  // sets, the next group's reads issued before the current group adds
+  auto chunk = [&](int buf, uint32_t n4) {
+    float4 wa[G][RI], xa[G][BJ], wb[G][RI], xb[G][BJ];
+    auto rd = [&](float4 (&w)[G][RI], float4 (&x)[G][BJ], uint32_t kb) {
+#pragma unroll
+      for (int u = 0; u < G; u++) {
+#pragma unroll
+        for (int i = 0; i < RI; i++) w[u][i] = Ws[buf][kb + u][ti * RI + i];
+#pragma unroll
+        for (int j = 0; j < BJ; j++) x[u][j] = Xs[buf][kb + u][tj * BJ + j];
+      }
+    };
+    uint32_t k4 = 0;
+    if (n4 >= 2 * G) {
+      rd(wa, xa, 0);
+      for (; k4 + 2 * G <= n4; k4 += 2 * G) {
+        rd(wb, xb, k4 + G);
+#pragma unroll
+        for (int u = 0; u < G; u++) step(wa[u], xa[u]);
+        const uint32_t kn = k4 + 2 * G <= (uint32_t)K4 - G ? k4 + 2 * G : 0;
+        rd(wa, xa, kn);
+#pragma unroll
+        for (int u = 0; u < G; u++) step(wb[u], xb[u]);
+      }
+    }
+    for (; k4 < n4; k4++) {
+      float4 w[RI], x[BJ];
+#pragma unroll
+      for (int i = 0; i < RI; i++) w[i] = Ws[buf][k4][ti * RI + i];
+#pragma unroll
+      for (int j = 0; j < BJ; j++) x[j] = Xs[buf][k4][tj * BJ + j];
+      step(w, x);
+    }
+  };
+
+  // chunk c sits in LDS buffer c & 1 and (before that) in register set c % D
+  for (uint32_t c0 = 0; c0 < nch; c0 += D) {
+#pragma unroll
+    for (int u = 0; u < D; u++) {
+      const uint32_t c = c0 + u;
+      if (c < nch) {
+        chunk(c & 1, min((uint32_t)K4, (a.K - c * KC) >> 2));
+        if (c + 1 < nch) store(v[(u + 1) % D], (c + 1) & 1, c + 1);
+        if (c + D < nch) load(v[u], c + D);
+        __syncthreads();
+      }
+    }
+  }
+
   if (a.mode == GM_SILU) {
+    // gate rows are tile rows [0, TR/2), their up rows TR/2 further
 #pragma unroll
-    for (int j = 0; j < CPT; j++) outs[bg * CPT + j][r] = s[j];
+    for (int i = 0; i < RI; i++)
+#pragma unroll
+      for (int j = 0; j < BJ; j++) outs[tj * BJ + j][ti * RI + i] = s[i][j];
     __syncthreads();
-    const uint32_t half = RT / 2;
-    if (r < half && rok) {
 #pragma unroll
-      for (int j = 0; j < CPT; j++) {
-        const uint32_t b = bg * CPT + j;
-        if (b < nb)
-          a.seg[0].Y[(size_t)(b0 + b) * a.seg[0].ldy + lr] = ex_silu(s[j]) * outs[b][r + half];
+    for (int i = 0; i < RI; i++) {
+      const uint32_t r = ti * RI + i;
+      const float* w;
+      uint32_t sg, lr;
+      if (r < (uint32_t)TR / 2 && sgs.row(TR, blockIdx.x, r, &w, &sg, &lr)) {
+#pragma unroll
+        for (int j = 0; j < BJ; j++) {
+          const uint32_t b = tj * BJ + j;
+          if (b < nb)
+            a.seg[0].Y[(size_t)(b0 + b) * a.seg[0].ldy + lr] = ex_silu(s[i][j]) * outs[b][r + TR / 2];
+        }
       }
     }
     return;
   }
-  if (rok) {
 #pragma unroll
-    for (int j = 0; j < CPT; j++) {
-      const uint32_t b = bg * CPT + j;
-      if (b < nb) gemv_store(a, sg, lr, b0 + b, s[j]);
+  for (int i = 0; i < RI; i++) {
+    const float* w;
+    uint32_t sg, lr;
+    if (sgs.row(TR, blockIdx.x, ti * RI + i, &w, &sg, &lr)) {
+#pragma unroll
+      for (int j = 0; j < BJ; j++) {
+        const uint32_t b = tj * BJ + j;
+        if (b < nb) gemv_store(a, sg, lr, b0 + b, s[i][j]);
+      }
     }
   }
 }
@@ -363,13 +519,17 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t st, hipEvent_t e0, hipEven
     }
     return hipGetLastError();
   }
-  if (a.ng || a.amax) return hipErrorInvalidValue;  // batched products take neither
-  const uint32_t RT = rows >= 4096 ? 16 : 4;
-  const uint32_t per = a.mode == GM_SILU ? RT / 2 : RT;
+  if (a.amax) return hipErrorInvalidValue;  // batched products store logits instead
+  if (a.ng && (a.K & 3)) return hipErrorInvalidValue;
+  // one chain per thread over 16 x 16 tiles while that still leaves a few
+  // workgroups per CU; 2 x 2 chains per thread over 32 x 32 tiles beyond
+  const bool big = (uint64_t)rows * a.B >= 256ull * 1024;
+  const uint32_t TR = big ? 32 : 16, TB = TR;
+  const uint32_t per = a.mode == GM_SILU ? TR / 2 : TR;
   const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
-  dim3 grid(tiles, (a.B + 63) / 64);
-  if (RT == 16) ANA_LAUNCH(k_gemm_exact<16>, grid, dim3(256), 0, st, e0, e1, a);
-  else ANA_LAUNCH(k_gemm_exact<4>, grid, dim3(256), 0, st, e0, e1, a);
+  dim3 grid(tiles, (a.B + TB - 1) / TB);
+  if (big) ANA_LAUNCH((k_gemm_exact<32, 32, 2, 2, 64, 3, 1>), grid, dim3(256), 0, st, e0, e1, a);
+  else ANA_LAUNCH((k_gemm_exact<16, 16, 1, 1, 128, 4, 4>), grid, dim3(256), 0, st, e0, e1, a);
   return hipGetLastError();
 }
 
