@@ -21,6 +21,8 @@ LIB_PATH = os.path.join(HERE, "libana.so")
 
 ANA_OK, ANA_EINVAL, ANA_ECKPT, ANA_EDEVICE, ANA_ENOMEM, ANA_EUNSUP = range(6)
 EXACT_FP32 = 0
+FAST_FP32 = 1
+BF16 = 2
 EOS = 1  # bend/Tokenizer.bend: BOS 0, EOS 1
 
 

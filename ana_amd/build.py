@@ -15,7 +15,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libana.so")
-SOURCES = ["ana.hip", "kernels_exact.hip", "sampler.hip", "ftc2.cpp"]
+SOURCES = ["ana.hip", "kernels_exact.hip", "kernels_fast.hip", "sampler.hip", "ftc2.cpp"]
+OBJDIR = os.path.join(HERE, "_build")
 
 
 def hipcc() -> str:
@@ -35,17 +36,29 @@ def flags() -> list[str]:
 
 
 def build(verbose: bool = False) -> str:
-    """Compile every source into ana_amd/libana.so (always recompiles)."""
+    """Compile every source (in parallel) and link ana_amd/libana.so; always
+    recompiles."""
+    from concurrent.futures import ThreadPoolExecutor
+    os.makedirs(OBJDIR, exist_ok=True)
+    compile_flags = [f for f in flags() if f != "-shared"]
+
+    def one(src: str) -> str:
+        obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
+        cmd = [hipcc(), *compile_flags, "-c", "-o", obj, os.path.join(CSRC, src)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {src}:\n" + r.stdout + r.stderr)
+        return obj
+
+    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
+        objs = list(ex.map(one, SOURCES))
     tmp = LIB + ".tmp"
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    cmd = [hipcc(), *flags(), "-o", tmp, *srcs]
-    if verbose:
-        print(" ".join(cmd), flush=True)
+    cmd = [hipcc(), *flags(), "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + r.stdout + r.stderr)
-    if verbose and r.stderr.strip():
-        print(r.stderr, file=sys.stderr)
+        raise RuntimeError("hipcc link failed:\n" + r.stdout + r.stderr)
     os.replace(tmp, LIB)
     return LIB
 

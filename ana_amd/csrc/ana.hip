@@ -27,7 +27,9 @@ struct ana_ctx {
   std::vector<uint64_t> layer_off;   // floats from a sequence's state start
   uint64_t seq_stride = 0;           // floats per sequence
   uint32_t max_seqs = 1, chunk = 64, wb = 1;
+  int mode = ANA_EXACT_FP32;         // numerics
   float* W = nullptr;                // parameters [P]
+  uint16_t* Wh = nullptr;            // ANA_BF16: the parameters as bfloat16 [P]
   float* state = nullptr;            // [max_seqs][seq_stride]
   float* xs = nullptr;               // [max_seqs][d]
   // workspace, wb rows
@@ -39,6 +41,7 @@ struct ana_ctx {
   uint64_t* d_rng = nullptr;
   unsigned long long* d_amax = nullptr;  // [wb] greedy argmax keys
   float *d_ss = nullptr, *d_pm = nullptr; // split attention scratch
+  float* d_part = nullptr;           // fast attention's per-split partials
   size_t out_cap = 0;
   std::string err;
   // ana_generate's decode step captured as HIP graphs, replayed per step:
@@ -131,7 +134,7 @@ static void release(ana_ctx* c) {
   (void)hipSetDevice(c->device);
   if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
   if (c->gexec_n) (void)hipGraphExecDestroy(c->gexec_n);
-  void* ps[] = {c->W, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
+  void* ps[] = {c->W, c->Wh, c->d_part, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
                 c->d_ss, c->d_pm};
   for (void* p : ps)
@@ -173,7 +176,8 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   ana_opts o{};
   o.max_seqs = 1;
   if (opts) o = *opts;
-  if (o.numerics != ANA_EXACT_FP32) return fail(nullptr, ANA_EUNSUP, "ana_open: unknown numerics mode %d", o.numerics);
+  if (o.numerics != ANA_EXACT_FP32 && o.numerics != ANA_FAST_FP32 && o.numerics != ANA_BF16)
+    return fail(nullptr, ANA_EUNSUP, "ana_open: unknown numerics mode %d", o.numerics);
   if (o.max_seqs == 0) o.max_seqs = 1;
   if (o.prefill_chunk == 0) o.prefill_chunk = 64;
   Ftc2 ck;
@@ -182,6 +186,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if (const char* u = unsupported(ck.cfg)) return fail(nullptr, ANA_EUNSUP, "ana_open: %s", u);
   ana_ctx* c = new ana_ctx();
   c->device = o.device;
+  c->mode = o.numerics;
   c->cfg = ck.cfg;
   c->step = ck.step;
   c->P = params_of(ck.cfg);
@@ -215,7 +220,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = dalloc(&c->XA, wb * d)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->XN, wb * d)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_step, 2)) != hipSuccess) return bad(e);
-  if ((e = dalloc(&c->d_amax, wb)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->d_amax, wb * kAmaxPerRow)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_ss, wb * cf.heads * cf.ctx)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_pm, wb * cf.heads * ((cf.ctx + kAttnTS - 1) / kAttnTS))) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->QKV, wb * 3 * d)) != hipSuccess) return bad(e);
@@ -228,8 +233,13 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = dalloc(&c->d_tok, wb)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_pick, wb)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_rng, 4 * wb)) != hipSuccess) return bad(e);
+  if (c->mode != ANA_EXACT_FP32 &&
+      (e = dalloc(&c->d_part, attn_fast_part_floats(kSmallB, cf.heads, cf.ctx, hd))) != hipSuccess)
+    return bad(e);
+  if (c->mode == ANA_BF16 && (e = dalloc(&c->Wh, c->P)) != hipSuccess) return bad(e);
   if ((e = hipMemcpyAsync(c->W, ck.raw.data(), 4 * c->P, hipMemcpyHostToDevice, c->st)) != hipSuccess) return bad(e);
   if ((e = launch_bswap(reinterpret_cast<uint32_t*>(c->W), c->P, c->st)) != hipSuccess) return bad(e);
+  if (c->Wh && (e = launch_to_bf16(c->W, c->Wh, c->P, c->st)) != hipSuccess) return bad(e);
   if ((e = launch_zero(c->state, c->seq_stride * c->max_seqs, c->st)) != hipSuccess) return bad(e);
   if ((e = launch_zero(c->xs, (uint64_t)d * c->max_seqs, c->st)) != hipSuccess) return bad(e);
   if ((e = hipStreamSynchronize(c->st)) != hipSuccess) return bad(e);
@@ -274,9 +284,25 @@ static double gemv_bytes(const GemvArgs& g) {
   return b;
 }
 
-static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g, uint32_t kind) {
-  ProfScope ps(c, kind, gemv_bytes(g), true);
-  return launch_gemv(g, c->st, ps.start(), ps.stop());
+// the fast modes' small-batch decode products stream bf16 (ANA_BF16) or
+// fp32 rows with split-K sums; prefill chunks and larger batches keep the
+// exact kernels in every mode
+static bool fast_path(const ana_ctx* c, uint32_t B) { return c->mode != ANA_EXACT_FP32 && B <= kSmallB; }
+
+static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind) {
+  if (fast_path(c, g0.B)) {
+    GemvArgs g = g0;
+    if (c->Wh) {
+      g.Wh0 = c->Wh + (g.seg[0].W - c->W);
+      g.Wh1 = g.nseg > 1 ? c->Wh + (g.seg[1].W - c->W) : nullptr;
+    }
+    double by = gemv_bytes(g);
+    if (c->Wh) by -= 2.0 * (g.seg[0].rows + (g.nseg > 1 ? g.seg[1].rows : 0)) * g.K;
+    ProfScope ps(c, kind, by, true);
+    return launch_gemv_fast(g, c->st, ps.start(), ps.stop());
+  }
+  ProfScope ps(c, kind, gemv_bytes(g0), true);
+  return launch_gemv(g0, c->st, ps.start(), ps.stop());
 }
 
 static GemvArgs gemv1(const float* X, uint32_t ldx, uint32_t K, const float* W, uint32_t rows,
@@ -327,8 +353,12 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
       } else {
         // S read and written once per sequence, q|k|v|z in, o out
         ProfScope ps(c, ANA_K_GLA, (double)B * (8.0 * cf.heads * (d / cf.heads) * (d / cf.heads) + 4.0 * 5 * d));
-        HIPCHK(c, launch_gla_step(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), seq,
-                                  c->O, d, cf.heads, cf.rglru, B, c->st));
+        if (fast_path(c, B))
+          HIPCHK(c, launch_gla_fast(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), seq,
+                                    c->O, d, cf.heads, cf.rglru, B, c->st));
+        else
+          HIPCHK(c, launch_gla_step(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), seq,
+                                    c->O, d, cf.heads, cf.rglru, B, c->st));
       }
     } else {
       AttnArgs a{};
@@ -342,7 +372,12 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
         // each sequence's write, then its attention (dd.sm.write, dd.sm.attend)
         a.QKV = c->QKV; a.O = c->O; a.B = B; a.seq = seq; a.pos = pos; a.write_kv = 1;
         ProfScope ps(c, ANA_K_ATTN, c->attn_bytes);
-        HIPCHK(c, launch_attn(a, c->st));
+        if (fast_path(c, B)) {
+          a.part = c->d_part;
+          HIPCHK(c, launch_attn_fast(a, c->st));
+        } else {
+          HIPCHK(c, launch_attn(a, c->st));
+        }
       } else if (fresh) {
         // before the ring wraps: every row's write, then every row's
         // attention (dd.sm.writes, then dd.sm.rows)
@@ -471,7 +506,7 @@ extern "C" int ana_top(ana_ctx* c, uint32_t n, const uint32_t* seq, uint32_t* to
   if (!c) return ANA_EINVAL;
   if (!tok) return fail(c, ANA_EINVAL, "ana_top: null output");
   if (int r = head_of(c, "ana_top", n, seq)) return r;
-  HIPCHK(c, launch_zero_u64(c->d_amax, n, c->st));
+  HIPCHK(c, launch_zero_u64(c->d_amax, (uint32_t)(n * kAmaxPerRow), c->st));
   if (int r = run_head(c, c->X, n, true)) return r;
   if (n <= kSmallB) HIPCHK(c, launch_keys_to_tok(c->d_amax, c->cfg.vocab, n, c->d_pick, c->st));
   HIPCHK(c, hipMemcpyAsync(tok, c->d_pick, 4 * n, hipMemcpyDeviceToHost, c->st));

@@ -60,14 +60,57 @@ struct GemvArgs {
   const float* R;     // GM_RESID: residual rows R[b * ldr + o]
   uint32_t ldr;
   uint32_t B;         // batch rows
-  const float* ng;    // RMSNorm gains over K, applied to X first (B <= 4 only)
-  unsigned long long* amax;  // per batch row: max of argmax keys of seg 0's outputs
+  const float* ng;    // RMSNorm gains over K, applied to X first
+  unsigned long long* amax;  // per batch row (amax_at): argmax keys of seg 0's outputs
+                             // (small batches only)
+  const uint16_t* Wh0;       // fast products: the segments' rows as bfloat16
+  const uint16_t* Wh1;       // (nullptr: read the fp32 rows)
 };
+// The two row segments as plain values (a runtime index into GemvArgs.seg
+// would send every lookup through memory).
+struct Segs {
+  const float* W0;
+  const float* W1;
+  uint32_t rows0, rows1, nseg, silu, K;
+  __device__ __forceinline__ explicit Segs(const GemvArgs& a)
+      : W0(a.seg[0].W), W1(a.seg[1].W), rows0(a.seg[0].rows), rows1(a.seg[1].rows), nseg(a.nseg),
+        silu(a.mode == GM_SILU), K(a.K) {}
+  // weight row of tile row r of workgroup tile t (R rows per tile; with
+  // silu the first R/2 rows are gate rows j, the rest up rows j); written
+  // with selects only, so loads that depend on it stay in straight-line code
+  __device__ __forceinline__ bool row(uint32_t R, uint32_t t, uint32_t r, const float** w,
+                                      uint32_t* seg, uint32_t* lr) const {
+    const uint32_t half = R >> 1;
+    const uint32_t vs = t * R + r;
+    const uint32_t sg_s = r >= half ? 1u : 0u;
+    const uint32_t j_s = t * half + r - sg_s * half;
+    const uint32_t sg_p = vs >= rows0 ? 1u : 0u;
+    const uint32_t j_p = vs - sg_p * rows0;
+    const uint32_t sg = silu ? sg_s : sg_p;
+    const uint32_t j = silu ? j_s : j_p;
+    const bool ok = j < (sg ? rows1 : rows0) && (sg == 0 || nseg > 1);
+    *w = (sg ? W1 : W0) + (size_t)j * K;
+    *seg = sg;
+    *lr = j;
+    return ok;
+  }
+};
+
 // small-batch products take the norm and the argmax inside (B <= 4)
 constexpr uint32_t kSmallB = 4;
 // e0/e1: optional start/stop events recorded by the launch itself
 hipError_t launch_gemv(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nullptr,
                        hipEvent_t e1 = nullptr);
+
+// Greedy argmax keys: each batch row has kAmaxSlots keys, kAmaxStride
+// apart (separate cache lines), and a workgroup raises slot
+// blockIdx.x % kAmaxSlots, so thousands of workgroups do not queue on one
+// address; the pick is the max over a row's slots.
+constexpr uint32_t kAmaxSlots = 32, kAmaxStride = 16;
+__host__ __device__ inline size_t amax_at(uint32_t b, uint32_t slot) {
+  return ((size_t)b * kAmaxSlots + slot) * kAmaxStride;
+}
+constexpr size_t kAmaxPerRow = (size_t)kAmaxSlots * kAmaxStride;
 
 // dd.pick as a key: larger value wins, then the lower index; -0 counts as
 // +0 and NaN never enters (key 0 = no candidate)
@@ -126,6 +169,7 @@ struct AttnArgs {
   uint32_t d, heads, ctx, B, write_kv;
   float* ss;            // scratch [B][heads][ctx]: sc * score
   float* pm;            // scratch [B][heads][ctx / kAttnTS]: partial maxima
+  float* part;          // fast attention: per split (m, l, o[hd])
 };
 // slots per workgroup in the split attention's score pass
 constexpr uint32_t kAttnTS = 128;
@@ -178,6 +222,18 @@ hipError_t launch_advance(const AdvanceArgs& a, hipStream_t st);
 hipError_t launch_keys_to_tok(const unsigned long long* amax, uint32_t vocab, uint32_t B,
                               uint32_t* tok, hipStream_t st);
 hipError_t launch_zero(float* p, uint64_t n, hipStream_t st);
+
+// ---------------------------------------------------------------- fast modes
+// Reassociated (tree / fused multiply-add) versions of the decode step's
+// kernels for ANA_FAST_FP32 and ANA_BF16, B <= kSmallB rows.
+hipError_t launch_to_bf16(const float* w, uint16_t* h, uint64_t n, hipStream_t st);
+hipError_t launch_gemv_fast(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nullptr,
+                            hipEvent_t e1 = nullptr);
+hipError_t launch_gla_fast(const float* QKV, const float* Z, const float* lam, StateRef S,
+                           const uint32_t* seq, float* O, uint32_t d, uint32_t heads,
+                           uint32_t rglru, uint32_t B, hipStream_t st);
+hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st);
+size_t attn_fast_part_floats(uint32_t B, uint32_t heads, uint32_t ctx, uint32_t hd);
 hipError_t launch_zero_u32(uint32_t* p, uint32_t n, hipStream_t st);
 hipError_t launch_zero_u64(unsigned long long* p, uint32_t n, hipStream_t st);
 

@@ -26,36 +26,6 @@ namespace ana {
 
 // ------------------------------------------------------------------ products
 
-// The two row segments as plain values (a runtime index into GemvArgs.seg
-// would send every lookup through memory).
-struct Segs {
-  const float* W0;
-  const float* W1;
-  uint32_t rows0, rows1, nseg, silu, K;
-  __device__ __forceinline__ explicit Segs(const GemvArgs& a)
-      : W0(a.seg[0].W), W1(a.seg[1].W), rows0(a.seg[0].rows), rows1(a.seg[1].rows), nseg(a.nseg),
-        silu(a.mode == GM_SILU), K(a.K) {}
-  // weight row of tile row r of workgroup tile t (R rows per tile; with
-  // silu the first R/2 rows are gate rows j, the rest up rows j); written
-  // with selects only, so loads that depend on it stay in straight-line code
-  __device__ __forceinline__ bool row(uint32_t R, uint32_t t, uint32_t r, const float** w,
-                                      uint32_t* seg, uint32_t* lr) const {
-    const uint32_t half = R >> 1;
-    const uint32_t vs = t * R + r;
-    const uint32_t sg_s = r >= half ? 1u : 0u;
-    const uint32_t j_s = t * half + r - sg_s * half;
-    const uint32_t sg_p = vs >= rows0 ? 1u : 0u;
-    const uint32_t j_p = vs - sg_p * rows0;
-    const uint32_t sg = silu ? sg_s : sg_p;
-    const uint32_t j = silu ? j_s : j_p;
-    const bool ok = j < (sg ? rows1 : rows0) && (sg == 0 || nseg > 1);
-    *w = (sg ? W1 : W0) + (size_t)j * K;
-    *seg = sg;
-    *lr = j;
-    return ok;
-  }
-};
-
 // the result of chain (b, row lr of segment sg): plain or plus the residual
 __device__ __forceinline__ void gemv_store(const GemvArgs& a, uint32_t sg, uint32_t lr, uint32_t b,
                                            float s) {
@@ -206,7 +176,7 @@ __global__ __launch_bounds__(256) void k_gemv_small(GemvArgs a, uint32_t R, uint
         const unsigned long long o = __shfl_xor(k, m, 64);
         k = o > k ? o : k;
       }
-      if (tid == 0 && (uint32_t)bb < nb && k) atomicMax(&a.amax[b0 + bb], k);
+      if (tid == 0 && (uint32_t)bb < nb && k) atomicMax(&a.amax[amax_at(b0 + bb, blockIdx.x % kAmaxSlots)], k);
     }
   }
 }
@@ -566,7 +536,7 @@ hipError_t launch_rmsnorm(const float* X, const float* g, uint32_t d, uint32_t B
 __global__ void k_embed(const float* __restrict__ E, const uint32_t* __restrict__ tok, uint32_t d,
                         float* __restrict__ X, unsigned long long* amax) {
   const uint32_t b = blockIdx.x;
-  if (amax && threadIdx.x == 0) amax[b] = 0ull;
+  if (amax && threadIdx.x < kAmaxSlots) amax[amax_at(b, threadIdx.x)] = 0ull;
   const float* src = E + (size_t)tok[b] * d;
   for (uint32_t j = threadIdx.x; j < d; j += blockDim.x) X[(size_t)b * d + j] = src[j];
 }
@@ -1123,7 +1093,10 @@ hipError_t launch_zero_u64(unsigned long long* p, uint32_t n, hipStream_t st) {
 
 __global__ void k_keys_to_tok(const unsigned long long* amax, uint32_t vocab, uint32_t B, uint32_t* tok) {
   const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b < B) tok[b] = amax[b] ? 0xFFFFFFFFu - (uint32_t)(amax[b] & 0xFFFFFFFFull) : vocab;
+  if (b >= B) return;
+  unsigned long long k = 0;
+  for (uint32_t s = 0; s < kAmaxSlots; s++) k = amax[amax_at(b, s)] > k ? amax[amax_at(b, s)] : k;
+  tok[b] = k ? 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull) : vocab;
 }
 
 hipError_t launch_keys_to_tok(const unsigned long long* amax, uint32_t vocab, uint32_t B,

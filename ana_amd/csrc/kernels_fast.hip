@@ -1,0 +1,604 @@
+// Fast decode kernels (ANA_FAST_FP32, ANA_BF16) for gfx950.
+//
+// The same decode step as the exact kernels, with the reductions split
+// across lanes and reassociated (tree sums, fused multiply-adds), so that the
+// weights stream at HBM rate instead of waiting on one lane's in-order chain.
+// Results are within a stated tolerance of the reference rather than equal
+// to it. ANA_BF16 reads the matrices as bfloat16 (rounded to nearest even
+// once, at load); activations, accumulation and recurrent state stay fp32.
+#include <hip/hip_ext.h>
+
+#include "ana_internal.h"
+#include "numerics.h"
+
+namespace ana {
+
+// ------------------------------------------------------------------ weights
+
+// fp32 bits -> bfloat16, round to nearest even; NaN stays a quiet NaN
+__global__ void k_to_bf16(const uint32_t* __restrict__ w, uint16_t* __restrict__ h, uint64_t n) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t u = w[i];
+    uint16_t r;
+    if ((u & 0x7fffffffu) > 0x7f800000u) r = (uint16_t)((u >> 16) | 0x40u);
+    else r = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    h[i] = r;
+  }
+}
+
+hipError_t launch_to_bf16(const float* w, uint16_t* h, uint64_t n, hipStream_t st) {
+  hipLaunchKernelGGL(k_to_bf16, dim3(4096), dim3(256), 0, st, reinterpret_cast<const uint32_t*>(w), h, n);
+  return hipGetLastError();
+}
+
+// four consecutive weights of a row as floats
+template <int WT> struct WLoad;
+template <> struct WLoad<0> {
+  using V = float4;
+  __device__ static __forceinline__ V load(const float* f, const uint16_t*, uint32_t k) {
+    return *reinterpret_cast<const float4*>(f + k);
+  }
+  __device__ static __forceinline__ float4 f4(const V& v) { return v; }
+};
+template <> struct WLoad<1> {
+  using V = uint2;
+  __device__ static __forceinline__ V load(const float*, const uint16_t* h, uint32_t k) {
+    return *reinterpret_cast<const uint2*>(h + k);
+  }
+  __device__ static __forceinline__ float4 f4(const V& v) {
+    return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                       __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
+  }
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+__device__ __forceinline__ float fast_silu(float z) { return z / (1.0f + __expf(-z)); }
+
+// ------------------------------------------------------------------ products
+
+// Small batches (B <= 4): one wave per workgroup, RW rows of the product.
+// Lane l covers k = 4 (l + 64 j), j < NF, of every row (split K): it loads
+// its slices of the BT activation rows first, then all RW x NF weight
+// slices at once (so they stream while the activations are normalised),
+// multiplies with fused multiply-adds and the wave sums each row's 64
+// partial dot products. Epilogues as the exact product's: plain, residual,
+// SiLU gate (tile rows [0, RW/2) gate, RW/2 further their up rows) and the
+// greedy argmax key.
+template <int WT, int BT, int RW, int NF>
+__global__ __launch_bounds__(64) void k_gemv_fast(GemvArgs a) {
+  using WL = WLoad<WT>;
+  __shared__ float4 xs[BT][NF * 64];
+  const uint32_t lane = threadIdx.x, K = a.K;
+  const uint32_t nb = a.B < (uint32_t)BT ? a.B : (uint32_t)BT;
+  const Segs sgs(a);
+  // activations (and the norm's gains) first: their wait leaves the weight
+  // loads issued after them in flight
+  float4 xv[BT][NF], gv[NF];
+#pragma unroll
+  for (int b = 0; b < BT; b++)
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+      const uint32_t k = 4 * (lane + 64 * j);
+      const bool in = k < K && (uint32_t)b < nb;
+      xv[b][j] = *reinterpret_cast<const float4*>(a.X + (size_t)(in ? b : 0) * a.ldx + (in ? k : 0));
+    }
+  if (a.ng) {
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+      const uint32_t k = 4 * (lane + 64 * j);
+      gv[j] = *reinterpret_cast<const float4*>(a.ng + (k < K ? k : 0));
+    }
+  }
+  typename WL::V wv[RW][NF];
+  uint32_t lr[RW], sg[RW];
+  bool rok[RW];
+#pragma unroll
+  for (int r = 0; r < RW; r++) {
+    const float* w;
+    rok[r] = sgs.row(RW, blockIdx.x, r, &w, &sg[r], &lr[r]);
+    const uint16_t* wh = (sg[r] ? a.Wh1 : a.Wh0) + (size_t)lr[r] * K;
+    if (!rok[r]) {
+      w = sgs.W0;
+      wh = a.Wh0;
+    }
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+      const uint32_t k = 4 * (lane + 64 * j);
+      wv[r][j] = WL::load(w, wh, k < K ? k : 0);
+    }
+  }
+  // M.norm on the lane's slices: ss over the row by a wave sum
+#pragma unroll
+  for (int b = 0; b < BT; b++) {
+    float4 x4[NF];
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+      const uint32_t k = 4 * (lane + 64 * j);
+      x4[j] = (k < K && (uint32_t)b < nb) ? xv[b][j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    if (a.ng) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NF; j++) ss += x4[j].x * x4[j].x + x4[j].y * x4[j].y + x4[j].z * x4[j].z + x4[j].w * x4[j].w;
+      ss = wave_sum(ss);
+      const float rs = 1.0f / sqrtf(ss / (float)K + 1.0e-5f);
+#pragma unroll
+      for (int j = 0; j < NF; j++) {
+        x4[j].x = (x4[j].x * rs) * gv[j].x;
+        x4[j].y = (x4[j].y * rs) * gv[j].y;
+        x4[j].z = (x4[j].z * rs) * gv[j].z;
+        x4[j].w = (x4[j].w * rs) * gv[j].w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NF; j++) xs[b][j * 64 + lane] = x4[j];
+  }
+  float acc[RW][BT];
+#pragma unroll
+  for (int r = 0; r < RW; r++) {
+#pragma unroll
+    for (int b = 0; b < BT; b++) acc[r][b] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+      const float4 w4 = WL::f4(wv[r][j]);
+#pragma unroll
+      for (int b = 0; b < BT; b++) {
+        const float4 x4 = xs[b][j * 64 + lane];
+        acc[r][b] = fmaf(w4.x, x4.x, acc[r][b]);
+        acc[r][b] = fmaf(w4.y, x4.y, acc[r][b]);
+        acc[r][b] = fmaf(w4.z, x4.z, acc[r][b]);
+        acc[r][b] = fmaf(w4.w, x4.w, acc[r][b]);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < BT; b++) acc[r][b] = wave_sum(acc[r][b]);
+  }
+  if (a.mode == GM_SILU) {
+#pragma unroll
+    for (int r = 0; r < RW / 2; r++)
+#pragma unroll
+      for (int b = 0; b < BT; b++)
+        if (lane == (uint32_t)(r * BT + b) && rok[r] && (uint32_t)b < nb)
+          a.seg[0].Y[(size_t)b * a.seg[0].ldy + lr[r]] = fast_silu(acc[r][b]) * acc[r + RW / 2][b];
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < RW; r++)
+#pragma unroll
+    for (int b = 0; b < BT; b++)
+      if (lane == (uint32_t)(r * BT + b) && rok[r] && (uint32_t)b < nb) {
+        float y = acc[r][b];
+        if (a.mode == GM_RESID) y = a.R[(size_t)b * a.ldr + lr[r]] + y;
+        if (sg[r]) a.seg[1].Y[(size_t)b * a.seg[1].ldy + lr[r]] = y;
+        else a.seg[0].Y[(size_t)b * a.seg[0].ldy + lr[r]] = y;
+      }
+  if (a.amax && lane < (uint32_t)BT && lane < nb) {
+    unsigned long long k = 0;
+#pragma unroll
+    for (int r = 0; r < RW; r++)
+#pragma unroll
+      for (int b = 0; b < BT; b++)
+        if ((uint32_t)b == lane && rok[r] && sg[r] == 0) {
+          const unsigned long long kk = argmax_key(acc[r][b], lr[r]);
+          k = kk > k ? kk : k;
+        }
+    if (k) atomicMax(&a.amax[amax_at(lane, blockIdx.x % kAmaxSlots)], k);
+  }
+}
+
+#define ANA_LAUNCH_F(K, GRID, BLOCK, LDS, ST, E0, E1, ...)                               \
+  do {                                                                                  \
+    if (E0) hipExtLaunchKernelGGL(K, GRID, BLOCK, LDS, ST, E0, E1, 0, __VA_ARGS__);      \
+    else hipLaunchKernelGGL(K, GRID, BLOCK, LDS, ST, __VA_ARGS__);                      \
+  } while (0)
+
+template <int WT, int BT, int RW, int NF>
+static hipError_t gemv_fast_go(const GemvArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
+                                          : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
+  const uint32_t per = a.mode == GM_SILU ? RW / 2 : RW;
+  const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
+  ANA_LAUNCH_F((k_gemv_fast<WT, BT, RW, NF>), dim3(tiles), dim3(64), 0, st, e0, e1, a);
+  return hipGetLastError();
+}
+
+template <int WT, int BT>
+static hipError_t gemv_fast_nf(const GemvArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  const uint32_t nf = (a.K + 255) / 256;
+  if (nf <= 1) return gemv_fast_go<WT, BT, 8, 1>(a, st, e0, e1);
+  if (nf <= 2) return gemv_fast_go<WT, BT, 8, 2>(a, st, e0, e1);
+  if (nf <= 3) return gemv_fast_go<WT, BT, 4, 3>(a, st, e0, e1);
+  if (nf <= 4) return gemv_fast_go<WT, BT, 4, 4>(a, st, e0, e1);
+  if constexpr (BT <= 4) {
+    if (nf <= 6) return gemv_fast_go<WT, BT, 2, 6>(a, st, e0, e1);
+  }
+  if constexpr (BT <= 2) {
+    if (nf <= 8) return gemv_fast_go<WT, BT, 2, 8>(a, st, e0, e1);
+    if (nf <= 12) return gemv_fast_go<WT, BT, 2, 12>(a, st, e0, e1);
+  }
+  return hipErrorInvalidValue;
+}
+
+// the widest batch tile whose activation slices fit the registers
+static uint32_t fast_bt(uint32_t K, uint32_t B) {
+  const uint32_t nf = (K + 255) / 256;
+  const uint32_t cap = nf <= 6 ? 4 : nf <= 12 ? 2 : 0;
+  const uint32_t bt = B <= 1 ? 1 : B <= 2 ? 2 : 4;
+  return bt < cap ? bt : cap;
+}
+
+hipError_t launch_gemv_fast(const GemvArgs& a0, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  if (a0.B == 0 || a0.B > kSmallB || (a0.K & 3) || fast_bt(a0.K, 1) == 0) return hipErrorInvalidValue;
+  const bool bf = a0.Wh0 != nullptr;
+  if (bf && a0.nseg > 1 && !a0.Wh1) return hipErrorInvalidValue;
+  const uint32_t BT = fast_bt(a0.K, a0.B);
+  // batch rows in tiles of BT; one launch per tile (the events bracket the
+  // first and the last)
+  for (uint32_t b0 = 0; b0 < a0.B; b0 += BT) {
+    GemvArgs a = a0;
+    a.B = a0.B - b0 < BT ? a0.B - b0 : BT;
+    a.X += (size_t)b0 * a.ldx;
+    a.seg[0].Y += (size_t)b0 * a.seg[0].ldy;
+    a.seg[1].Y += (size_t)b0 * a.seg[1].ldy;
+    if (a.R) a.R += (size_t)b0 * a.ldr;
+    if (a.amax) a.amax += b0 * kAmaxPerRow;
+    hipEvent_t s0 = b0 == 0 ? e0 : nullptr, s1 = b0 + BT >= a0.B ? e1 : nullptr;
+    hipError_t e;
+    if (s0 && !s1) {
+      (void)hipEventRecord(s0, st);
+      s0 = nullptr;
+    }
+    if (!s0 && s1) {
+      // start recorded already (or by the first tile): stop after this launch
+      if (bf) e = BT == 1 ? gemv_fast_nf<1, 1>(a, st, nullptr, nullptr) : BT == 2 ? gemv_fast_nf<1, 2>(a, st, nullptr, nullptr) : gemv_fast_nf<1, 4>(a, st, nullptr, nullptr);
+      else e = BT == 1 ? gemv_fast_nf<0, 1>(a, st, nullptr, nullptr) : BT == 2 ? gemv_fast_nf<0, 2>(a, st, nullptr, nullptr) : gemv_fast_nf<0, 4>(a, st, nullptr, nullptr);
+      if (e != hipSuccess) return e;
+      (void)hipEventRecord(s1, st);
+      continue;
+    }
+    if (bf) e = BT == 1 ? gemv_fast_nf<1, 1>(a, st, s0, s1) : BT == 2 ? gemv_fast_nf<1, 2>(a, st, s0, s1) : gemv_fast_nf<1, 4>(a, st, s0, s1);
+    else e = BT == 1 ? gemv_fast_nf<0, 1>(a, st, s0, s1) : BT == 2 ? gemv_fast_nf<0, 2>(a, st, s0, s1) : gemv_fast_nf<0, 4>(a, st, s0, s1);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+// ------------------------------------------------------------------ GLA
+
+// One decode token of dd.gla for one head, one block of CB state columns:
+// L2 norms of q and k (wave sums), the gate (Ex.bend's expressions in float
+// arithmetic), S' = al*S + kh v^T on the block, and o over the block's
+// columns = qh^T S' (per-thread partials, then lane shuffles and LDS).
+__device__ __forceinline__ float f_sigmoid(float z) {
+  if (0.0f <= z) return 1.0f / (1.0f + expf(-z));
+  const float e = expf(z);
+  return e / (1.0f + e);
+}
+__device__ __forceinline__ float f_log_sigmoid(float z) {
+  return -(fmaxf(-z, 0.0f) + log1pf(expf(-fabsf(z))));
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_gla_fast(const float* __restrict__ QKV,
+                                                   const float* __restrict__ Z,
+                                                   const float* __restrict__ lam, StateRef S,
+                                                   const uint32_t* __restrict__ seq,
+                                                   float* __restrict__ O, uint32_t d,
+                                                   uint32_t rglru) {
+  constexpr int CB = 16, C4 = CB / 4;
+  constexpr int RPP = 256 / C4;           // state rows per pass (64)
+  constexpr int NP = (HD + RPP - 1) / RPP;
+  __shared__ float al[HD], kh[HD], qh[HD], v[CB], sq[2];
+  __shared__ float4 part[4][C4];
+  const uint32_t h = blockIdx.x, cb = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const uint32_t sl = seq[b];
+  float* Sg = S.base + (size_t)sl * S.seq_stride + S.layer_off + (size_t)h * HD * HD + cb * CB;
+  const float* x = QKV + (size_t)b * 3 * d;
+  // the block of S first: it does not depend on this token
+  const uint32_t c4 = tid % C4, r0 = tid / C4;
+  float4 sv[NP];
+#pragma unroll
+  for (int p = 0; p < NP; p++) {
+    const uint32_t r = r0 + RPP * p;
+    sv[p] = *reinterpret_cast<const float4*>(Sg + (size_t)(r < HD ? r : 0) * HD + 4 * c4);
+  }
+  float qv = 0.0f, kv = 0.0f, zv = 0.0f, lv = 0.0f;
+  if ((int)tid < HD) {
+    qv = x[h * HD + tid];
+    kv = x[d + h * HD + tid];
+    zv = Z[(size_t)b * d + h * HD + tid];
+    if (rglru) lv = lam[h * HD + tid];
+  }
+  if (tid < 64) {
+    const float s0 = wave_sum(qv * qv), s1 = wave_sum(kv * kv);
+    if (tid == 0) {
+      sq[0] = s0;
+      sq[1] = s1;
+    }
+  }
+  if (tid < CB) v[tid] = x[2 * d + h * HD + cb * CB + tid];
+  __syncthreads();
+  if ((int)tid < HD) {
+    qh[tid] = qv / sqrtf(1.0e-6f + sq[0]);
+    const float kn = kv / sqrtf(1.0e-6f + sq[1]);
+    if (rglru) {
+      // dd.gate's RG-LRU arm (bend/Dense/Ex.bend:158-162)
+      const float la = fminf(ANA_CAP, (8.0f * f_sigmoid(zv)) * f_log_sigmoid(lv));
+      kh[tid] = kn * sqrtf(1.0f - expf(2.0f * la));
+      al[tid] = expf(la);
+    } else {
+      al[tid] = f_sigmoid(zv);
+      kh[tid] = kn;
+    }
+  }
+  __syncthreads();
+  float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int p = 0; p < NP; p++) {
+    const uint32_t r = r0 + RPP * p;
+    if (r < HD) {
+      const float a_ = al[r], k_ = kh[r], q_ = qh[r];
+      float4 s = sv[p];
+      s.x = fmaf(a_, s.x, k_ * v[4 * c4 + 0]);
+      s.y = fmaf(a_, s.y, k_ * v[4 * c4 + 1]);
+      s.z = fmaf(a_, s.z, k_ * v[4 * c4 + 2]);
+      s.w = fmaf(a_, s.w, k_ * v[4 * c4 + 3]);
+      *reinterpret_cast<float4*>(Sg + (size_t)r * HD + 4 * c4) = s;
+      o.x = fmaf(q_, s.x, o.x);
+      o.y = fmaf(q_, s.y, o.y);
+      o.z = fmaf(q_, s.z, o.z);
+      o.w = fmaf(q_, s.w, o.w);
+    }
+  }
+  // sum over the rows: lanes differing in bits 2..5 share a column quad
+#pragma unroll
+  for (int m = 4; m < 64; m <<= 1) {
+    o.x += __shfl_xor(o.x, m, 64);
+    o.y += __shfl_xor(o.y, m, 64);
+    o.z += __shfl_xor(o.z, m, 64);
+    o.w += __shfl_xor(o.w, m, 64);
+  }
+  if ((tid & 63) < (uint32_t)C4) part[tid >> 6][tid & 63] = o;
+  __syncthreads();
+  if (tid < CB) {
+    const uint32_t c = tid / 4, e = tid % 4;
+    float acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      const float4 p4 = part[w][c];
+      acc += e == 0 ? p4.x : e == 1 ? p4.y : e == 2 ? p4.z : p4.w;
+    }
+    O[(size_t)b * d + h * HD + cb * CB + tid] = acc;
+  }
+}
+
+hipError_t launch_gla_fast(const float* QKV, const float* Z, const float* lam, StateRef S,
+                           const uint32_t* seq, float* O, uint32_t d, uint32_t heads,
+                           uint32_t rglru, uint32_t B, hipStream_t st) {
+  const uint32_t hd = d / heads;
+  if (hd % 16) return hipErrorInvalidValue;
+#define L_(H) hipLaunchKernelGGL(k_gla_fast<H>, dim3(heads, H / 16, B), dim3(256), 0, st, QKV, Z, lam, S, seq, O, d, rglru)
+  switch (hd) {
+    case 64: L_(64); break;
+    case 32: L_(32); break;
+    case 16: L_(16); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef L_
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ attention
+
+// Split softmax attention (flash decoding). Pass 1, per (head, split of
+// kFastTS ring slots, row): qk-norm of q (and of k for the row's own slot,
+// which the split holding it writes to the ring first), the scores, the
+// split's max m, l = sum exp(s - m) and o = sum exp(s - m) v. Pass 2 folds
+// the splits and the sink: m* = max(m_i, sink), den = sum l_i e^(m_i - m*)
+// + e^(sink - m*), o = sum o_i e^(m_i - m*) / den.
+constexpr uint32_t kFastTS = 64;
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_fast_part(AttnArgs a) {
+  constexpr int C4 = HD / 4;       // column quads
+  constexpr int QD = HD / 4;       // dims per score lane (4 lanes a slot)
+  __shared__ float q[HD], kk[HD], vs[HD], es[kFastTS], red[4], nrm[2];
+  __shared__ float4 op[4][C4];
+  const uint32_t h = blockIdx.x, sp = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const uint32_t d = a.d, ctx = a.ctx, ns = (ctx + kFastTS - 1) / kFastTS;
+  const uint32_t pos = a.pos[b];
+  const uint32_t slot = pos % ctx, npos = pos < ctx - 1 ? pos : ctx - 1;
+  const uint32_t sl = a.seq[b];
+  float* Kr = a.KV.base + (size_t)sl * a.KV.seq_stride + a.KV.layer_off;
+  float* Vr = Kr + (size_t)ctx * d;
+  const uint32_t t0 = sp * kFastTS;
+  float* out = a.part + (((size_t)b * a.heads + h) * ns + sp) * (HD + 2);
+  if (t0 > npos) {
+    if (tid == 0) {
+      out[0] = -INFINITY;
+      out[1] = 0.0f;
+    }
+    if ((int)tid < HD) out[2 + tid] = 0.0f;
+    return;
+  }
+  const bool mine = a.write_kv && slot >= t0 && slot < t0 + kFastTS;
+  const uint32_t nt = min(kFastTS, npos + 1 - t0);
+  // score lanes: slot i = tid / 4, dims [qq * QD, (qq + 1) * QD)
+  const uint32_t i = tid >> 2, qq = tid & 3, t = t0 + i;
+  const bool live = i < nt;
+  // V lanes: column quad c4, slots g, g + 256 / C4, ...
+  constexpr int GS = 256 / C4;
+  const uint32_t c4 = tid % C4, g = tid / C4;
+  float4 kv[QD / 4], vv[(kFastTS + GS - 1) / GS];
+  {
+    const float4* k4 = reinterpret_cast<const float4*>(Kr + (size_t)(live ? t : t0) * d + h * HD + qq * QD);
+#pragma unroll
+    for (int u = 0; u < QD / 4; u++) kv[u] = k4[u];
+#pragma unroll
+    for (int j = 0; j < (int)((kFastTS + GS - 1) / GS); j++) {
+      const uint32_t ii = g + GS * j;
+      vv[j] = *reinterpret_cast<const float4*>(Vr + (size_t)(t0 + (ii < nt ? ii : 0)) * d + h * HD + 4 * c4);
+    }
+  }
+  const float* x = a.QKV + (size_t)b * 3 * d;
+  if (tid < 64) {
+    const float qv = (int)tid < HD ? x[h * HD + tid] : 0.0f;
+    if ((int)tid < HD) q[tid] = qv;
+    if (a.gq) {
+      const float s2 = wave_sum(qv * qv);
+      if (tid == 0) nrm[0] = 1.0f / sqrtf(s2 / (float)HD + 1.0e-5f);
+    }
+  } else if (tid < 128 && mine) {
+    const uint32_t e = tid - 64;
+    const float kx = (int)e < HD ? x[d + h * HD + e] : 0.0f;
+    if ((int)e < HD) {
+      kk[e] = kx;
+      vs[e] = x[2 * d + h * HD + e];
+    }
+    if (a.gk) {
+      const float s2 = wave_sum(kx * kx);
+      if (e == 0) nrm[1] = 1.0f / sqrtf(s2 / (float)HD + 1.0e-5f);
+    }
+  }
+  __syncthreads();
+  if (a.gq && (int)tid < HD) q[tid] = (q[tid] * nrm[0]) * (1.0f + a.gq[tid]);
+  if (mine && tid >= 64 && (int)(tid - 64) < HD) {
+    const uint32_t e = tid - 64;
+    if (a.gk) kk[e] = (kk[e] * nrm[1]) * (1.0f + a.gk[e]);
+    Kr[(size_t)slot * d + h * HD + e] = kk[e];
+    Vr[(size_t)slot * d + h * HD + e] = vs[e];
+  }
+  __syncthreads();
+  const float sc = 1.0f / sqrtf((float)HD);
+  float acc = 0.0f;
+  if (mine && t == slot) {
+#pragma unroll
+    for (int c = 0; c < QD; c++) acc = fmaf(q[qq * QD + c], kk[qq * QD + c], acc);
+  } else {
+#pragma unroll
+    for (int u = 0; u < QD / 4; u++) {
+      const uint32_t c = qq * QD + 4 * u;
+      acc = fmaf(q[c + 0], kv[u].x, acc);
+      acc = fmaf(q[c + 1], kv[u].y, acc);
+      acc = fmaf(q[c + 2], kv[u].z, acc);
+      acc = fmaf(q[c + 3], kv[u].w, acc);
+    }
+  }
+  acc += __shfl_xor(acc, 1, 64);
+  acc += __shfl_xor(acc, 2, 64);
+  const float y = live ? sc * acc : -INFINITY;
+  // split max, then exp and its sum
+  float m = y;
+#pragma unroll
+  for (int s2 = 32; s2 >= 4; s2 >>= 1) {
+    const float o = __shfl_xor(m, s2, 64);
+    m = o > m ? o : m;
+  }
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float e = live ? __expf(y - m) : 0.0f;
+  if (qq == 0) es[i] = e;
+  const float ls = wave_sum(qq == 0 ? e : 0.0f);
+  __syncthreads();
+  if ((tid & 63) == 0) red[tid >> 6] = ls;
+  float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int j = 0; j < (int)((kFastTS + GS - 1) / GS); j++) {
+    const uint32_t ii = g + GS * j;
+    if (ii < nt) {
+      float4 v4 = vv[j];
+      if (mine && t0 + ii == slot) v4 = make_float4(vs[4 * c4], vs[4 * c4 + 1], vs[4 * c4 + 2], vs[4 * c4 + 3]);
+      const float ev = es[ii];
+      o.x = fmaf(ev, v4.x, o.x);
+      o.y = fmaf(ev, v4.y, o.y);
+      o.z = fmaf(ev, v4.z, o.z);
+      o.w = fmaf(ev, v4.w, o.w);
+    }
+  }
+  // sum over the slot groups: lanes differing above the column-quad bits
+#pragma unroll
+  for (int s2 = C4; s2 < 64; s2 <<= 1) {
+    o.x += __shfl_xor(o.x, s2, 64);
+    o.y += __shfl_xor(o.y, s2, 64);
+    o.z += __shfl_xor(o.z, s2, 64);
+    o.w += __shfl_xor(o.w, s2, 64);
+  }
+  if ((tid & 63) < (uint32_t)C4) op[tid >> 6][tid & 63] = o;
+  __syncthreads();
+  if ((int)tid < HD) {
+    const uint32_t c = tid / 4, e4 = tid % 4;
+    float s2 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      const float4 p4 = op[w][c];
+      s2 += e4 == 0 ? p4.x : e4 == 1 ? p4.y : e4 == 2 ? p4.z : p4.w;
+    }
+    out[2 + tid] = s2;
+  }
+  if (tid == 0) {
+    out[0] = m;
+    out[1] = red[0] + red[1] + red[2] + red[3];
+  }
+}
+
+// ns <= 64 splits (one lane each)
+template <int HD>
+__global__ __launch_bounds__(64) void k_attn_fast_comb(AttnArgs a) {
+  __shared__ float wgt[64];
+  __shared__ float den_s;
+  const uint32_t h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const uint32_t ns = (a.ctx + kFastTS - 1) / kFastTS;
+  const float* p = a.part + ((size_t)b * a.heads + h) * ns * (HD + 2);
+  // every split's (m, l) at once, one lane each
+  const float mi = tid < ns ? p[tid * (HD + 2)] : -INFINITY;
+  const float li = tid < ns ? p[tid * (HD + 2) + 1] : 0.0f;
+  float m = mi;
+#pragma unroll
+  for (int s2 = 32; s2 >= 1; s2 >>= 1) m = fmaxf(m, __shfl_xor(m, s2, 64));
+  float sink = 0.0f;
+  if (a.sink) {
+    sink = a.sink[h];
+    m = fmaxf(m, sink);
+  }
+  const float w = mi == -INFINITY ? 0.0f : __expf(mi - m);
+  wgt[tid] = w;
+  const float den = wave_sum(li * w);
+  if (tid == 0) den_s = a.sink ? den + __expf(sink - m) : den;
+  __syncthreads();
+  if ((int)tid < HD) {
+    float o = 0.0f;
+#pragma unroll 8
+    for (uint32_t i = 0; i < ns; i++) o = fmaf(p[i * (HD + 2) + 2 + tid], wgt[i], o);
+    a.O[(size_t)b * a.d + h * HD + tid] = o / den_s;
+  }
+}
+
+hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st) {
+  const uint32_t hd = a.d / a.heads;
+  const uint32_t ns = (a.ctx + kFastTS - 1) / kFastTS;
+  if (!a.part || !a.seq || !a.pos || hd % 4 || hd > 64 || ns > 64) return hipErrorInvalidValue;
+#define L_(H)                                                                                   \
+  hipLaunchKernelGGL(k_attn_fast_part<H>, dim3(a.heads, ns, a.B), dim3(256), 0, st, a);        \
+  hipLaunchKernelGGL(k_attn_fast_comb<H>, dim3(a.heads, a.B), dim3(64), 0, st, a)
+  switch (hd) {
+    case 64: L_(64); break;
+    case 32: L_(32); break;
+    case 16: L_(16); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef L_
+  return hipGetLastError();
+}
+
+size_t attn_fast_part_floats(uint32_t B, uint32_t heads, uint32_t ctx, uint32_t hd) {
+  return (size_t)B * heads * ((ctx + kFastTS - 1) / kFastTS) * (hd + 2);
+}
+
+}  // namespace ana

@@ -296,7 +296,8 @@ __global__ __launch_bounds__(1024) void k_advance(AdvanceArgs a, uint32_t NT) {
   if (a.greedy) {
     uint32_t cand;
     if (a.amax) {
-      const unsigned long long key = a.amax[b];
+      unsigned long long key = 0;
+      for (uint32_t s = 0; s < kAmaxSlots; s++) key = a.amax[amax_at(b, s)] > key ? a.amax[amax_at(b, s)] : key;
       cand = key ? 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull) : v;
     } else {
       cand = a.pick[b];

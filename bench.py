@@ -50,12 +50,12 @@ def ensure_ckpt(c: cf.Config, path: str) -> str:
     return path
 
 
-def run_bytes(c: cf.Config, positions, steps: int) -> float:
+def run_bytes(c: cf.Config, positions, steps: int, wbytes: float = 4.0) -> float:
     """Algorithmic HBM bytes of `steps` decode steps: every weight once per
     step (the tied head reads all of E; the gather reads one row per
     sequence), and per (sequence, position) the GLA states read and written
     and the live K/V rows read."""
-    w = 4.0 * (c.params - c.vocab * c.d + c.vocab * c.d) * steps
+    w = wbytes * (c.params - c.vocab * c.d + c.vocab * c.d) * steps
     per = 0.0
     for p in positions:
         live = min(p, c.ctx - 1) + 1
@@ -64,9 +64,13 @@ def run_bytes(c: cf.Config, positions, steps: int) -> float:
     return w + per
 
 
-def run_batch(path: str, c: cf.Config, B: int, prompt: int, warmup: int, steps: int, prof_steps: int):
+MODES = {"exact": ana_amd.EXACT_FP32, "fast_fp32": ana_amd.FAST_FP32, "bf16": ana_amd.BF16}
+
+
+def run_batch(path: str, c: cf.Config, B: int, prompt: int, warmup: int, steps: int, prof_steps: int,
+              mode: str = "exact"):
     seqs = list(range(B))
-    with ana_amd.Decoder(path, max_seqs=B, prefill_chunk=64) as dec:
+    with ana_amd.Decoder(path, max_seqs=B, prefill_chunk=64, numerics=MODES[mode]) as dec:
         t = time.perf_counter()
         first, pos = [], []
         for b in seqs:
@@ -85,12 +89,14 @@ def run_batch(path: str, c: cf.Config, B: int, prompt: int, warmup: int, steps: 
         t1 = time.perf_counter()
         positions = [int(p) + k for k in range(steps) for p in pos]
         tok, pos = out[:, -1].copy(), pos + steps
-        dec.prof(True)
-        dec.generate(seqs, pos, tok, prof_steps)
-        stats = dec.prof_read()
-        dec.prof(False)
+        stats = {}
+        if prof_steps:
+            dec.prof(True)
+            dec.generate(seqs, pos, tok, prof_steps)
+            stats = dec.prof_read()
+            dec.prof(False)
     dt = t1 - t0
-    sb = run_bytes(c, positions, steps) / steps
+    sb = run_bytes(c, positions, steps, 2.0 if mode == "bf16" and B <= 4 else 4.0) / steps
     return {
         "tok_s": B * steps / dt,
         "ms_per_step": 1000.0 * dt / steps,
@@ -138,12 +144,23 @@ def cpu_baseline(path: str, c: cf.Config, seconds: float) -> dict:
     }
 
 
+KERNEL = {"exact": "k_gemv_small<1> (exact products, norm/residual/SiLU/argmax fused) + LM head",
+          "fast_fp32": "k_gemv_fast<fp32> (split-K products, norm/residual/SiLU/argmax fused) + LM head",
+          "bf16": "k_gemv_fast<bf16> (split-K products over bf16 weights) + LM head"}
+NUMERICS = {"exact": "exact_fp32: bit-exact with the reference's CPU kernels",
+            "fast_fp32": "fast_fp32: fp32 with reassociated sums; logits within 1e-4 of the reference",
+            "bf16": "bf16 weights, fp32 activations/accumulation/state; logits within 2e-2"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--prompt", type=int, default=1920)
+    ap.add_argument("--numerics", choices=list(MODES), default="fast_fp32",
+                    help="the mode `value` is measured in")
+    ap.add_argument("--others", type=int, default=1, help="also measure B=1 in the other modes (1/0)")
     ap.add_argument("--b64", type=int, default=1, help="also measure B=64 (1/0)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--ckpt", default=os.environ.get("ANA_BENCH_CKPT", "/tmp/ana_bench_fp100m.ftc2"))
@@ -154,7 +171,8 @@ def main() -> int:
         return 2
     c = cf.FP100M
     path = ensure_ckpt(c, a.ckpt)
-    r1 = run_batch(path, c, 1, a.prompt, a.warmup, a.steps, min(a.steps, 32))
+    mode = a.numerics
+    r1 = run_batch(path, c, 1, a.prompt, a.warmup, a.steps, min(a.steps, 32), mode)
     g = r1["stats"]["gemv"]
     h = r1["stats"]["head"]
     launches, ms, by = g[0] + h[0], g[1] + h[1], g[2] + h[2]
@@ -163,14 +181,22 @@ def main() -> int:
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
         try:
-            traffic = json.load(open(tpath)).get("gemv_exact_bytes_per_launch")
+            traffic = json.load(open(tpath)).get(f"gemv_{mode}_bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
     extra = {}
+    if a.others:
+        for m in MODES:
+            if m == mode:
+                continue
+            r = run_batch(path, c, 1, a.prompt, a.warmup, a.steps, 0, m)
+            extra[f"b1_{m}"] = {"tok_s": round(r["tok_s"], 2), "ms_per_step": round(r["ms_per_step"], 4),
+                                "step_gbs": round(r["step_gbs"], 2), "numerics": NUMERICS[m]}
     if a.b64:
         r64 = run_batch(path, c, 64, 128, 2, 32, 8)
         extra["b64"] = {k: r64[k] for k in ("tok_s", "ms_per_step", "step_gbs")}
-        extra["b64"]["workload"] = "B=64, 128-token prompts, 32 greedy steps at positions 129+"
+        extra["b64"]["workload"] = ("B=64, 128-token prompts, 32 greedy steps at positions 129+, "
+                                    "exact fp32 (batched products run the exact kernels in every mode)")
     cpu = cpu_baseline(path, c, a.cpu_seconds) if a.cpu_seconds > 0 else None
     kern = {k: {"launches": v[0], "ms": round(v[1], 4), "gb": round(v[2] / 1e9, 4)}
             for k, v in r1["stats"].items()}
@@ -185,17 +211,17 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16" if mode == "bf16" else "f32",
         "data": "synthetic: random-init N(0,0.02) FTC2 checkpoint (seed 0), uniform-random prompts",
         "config": {
             "workload": "115M fp100m (d768 f2048 L12 h12 v32768, RG-LRU, qk-norm, sinks) ctx 2048 "
-                        "greedy decode, B=1, 1920-token prompt, exact fp32 (bit-exact with the "
-                        "reference's CPU kernels)",
-            "batch": 1, "prompt": a.prompt, "ctx": c.ctx, "numerics": "exact_fp32",
+                        "greedy decode, B=1, 1920-token prompt (chunked prefill), then decode at "
+                        "positions 1920+; " + NUMERICS[mode],
+            "batch": 1, "prompt": a.prompt, "ctx": c.ctx, "numerics": mode,
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_gemv_exact (layer products + LM head)",
+            "kernel": KERNEL[mode],
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -47,6 +47,11 @@ extern "C" {
 
 /* numerics modes */
 #define ANA_EXACT_FP32 0 /* bit-exact with the reference's CPU kernels */
+#define ANA_FAST_FP32 1  /* fp32, sums reassociated (split-K, fused multiply-add):
+                            logits within 1e-4 of the reference, relative to their
+                            largest magnitude */
+#define ANA_BF16 2       /* matrices read as bfloat16 (rounded once at load); fp32
+                            activations, accumulation and state: logits within 2e-2 */
 
 /* bend/Config.bend:7-10 */
 typedef struct {
@@ -56,7 +61,7 @@ typedef struct {
 
 typedef struct {
   int device;              /* HIP device ordinal */
-  int numerics;            /* ANA_EXACT_FP32 */
+  int numerics;            /* ANA_EXACT_FP32, ANA_FAST_FP32 or ANA_BF16 */
   uint32_t max_seqs;       /* sequences the context keeps state for (>= 1) */
   uint32_t prefill_chunk;  /* tokens per prefill chunk; 0 = 64, as ANA_PREFILL_CHUNK */
 } ana_opts;
