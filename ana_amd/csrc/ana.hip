@@ -284,13 +284,19 @@ static double gemv_bytes(const GemvArgs& g) {
   return b;
 }
 
-// the fast modes' small-batch decode products stream bf16 (ANA_BF16) or
-// fp32 rows with split-K sums; prefill chunks and larger batches keep the
-// exact kernels in every mode
-static bool fast_path(const ana_ctx* c, uint32_t B) { return c->mode != ANA_EXACT_FP32 && B <= kSmallB; }
+// The fast modes: decode steps of B <= kSmallB sequences stream bf16
+// (ANA_BF16) or fp32 rows with split-K sums and take the reassociated GLA and
+// attention kernels; prefill chunks of more than kSmallB rows run their
+// products on the matrix cores. Decode steps of more sequences, the head over
+// more than kSmallB rows and prefill chunks of kSmallB rows or fewer run the
+// exact kernels (those paths faulted the GPU in their first test and stay off
+// until the cause is found).
+static bool fast_mode(const ana_ctx* c) { return c->mode != ANA_EXACT_FP32; }
+static bool fast_path(const ana_ctx* c, uint32_t B) { return fast_mode(c) && B <= kSmallB; }
 
-static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind) {
-  if (fast_path(c, g0.B)) {
+static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool chunk = false) {
+  const bool small = g0.B <= kSmallB;
+  if (fast_mode(c) && (chunk ? !small : small)) {
     GemvArgs g = g0;
     if (c->Wh) {
       g.Wh0 = c->Wh + (g.seg[0].W - c->W);
@@ -299,7 +305,8 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind) {
     double by = gemv_bytes(g);
     if (c->Wh) by -= 2.0 * (g.seg[0].rows + (g.nseg > 1 ? g.seg[1].rows : 0)) * g.K;
     ProfScope ps(c, kind, by, true);
-    return launch_gemv_fast(g, c->st, ps.start(), ps.stop());
+    if (small) return launch_gemv_fast(g, c->st, ps.start(), ps.stop());
+    return launch_gemm_mfma(g, c->st, ps.start(), ps.stop());
   }
   ProfScope ps(c, kind, gemv_bytes(g0), true);
   return launch_gemv(g0, c->st, ps.start(), ps.stop());
@@ -318,11 +325,12 @@ static GemvArgs gemv1(const float* X, uint32_t ldx, uint32_t K, const float* W, 
 
 // RMSNorm(X; g) then the product: inside the product for small batches,
 // else a norm kernel into XN first
-static int norm_gemv(ana_ctx* c, const float* X, const float* g, GemvArgs a, uint32_t kind) {
+static int norm_gemv(ana_ctx* c, const float* X, const float* g, GemvArgs a, uint32_t kind,
+                     bool chunk = false) {
   a.X = X;
   a.ldx = c->cfg.d;
   a.ng = g;
-  HIPCHK(c, gemv_timed(c, a, kind));
+  HIPCHK(c, gemv_timed(c, a, kind, chunk));
   return ANA_OK;
 }
 
@@ -344,7 +352,7 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
       g.seg[1] = GemvSeg{W + b.wa, d, c->Z, d};
       g.nseg = 2;
     }
-    if (int r = norm_gemv(c, c->X, W + b.ra, g, ANA_K_GEMV)) return r;
+    if (int r = norm_gemv(c, c->X, W + b.ra, g, ANA_K_GEMV, chunk)) return r;
     if (b.gla) {
       if (chunk) {
         HIPCHK(c, launch_gla_chunk(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr,
@@ -397,15 +405,15 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
     // M.tail: xa = x + Wo o; hh = silu(g) * u on norm(xa); x = xa + Wd hh
     GemvArgs wo = gemv1(c->O, d, d, W + b.wo, d, c->XA, d, B);
     wo.mode = GM_RESID; wo.R = c->X; wo.ldr = d;
-    HIPCHK(c, gemv_timed(c, wo, ANA_K_GEMV));
+    HIPCHK(c, gemv_timed(c, wo, ANA_K_GEMV, chunk));
     GemvArgs gu = gemv1(c->XA, d, d, W + b.wg, f, c->HH, f, B);
     gu.seg[1] = GemvSeg{W + b.wu, f, c->HH, f};
     gu.nseg = 2;
     gu.mode = GM_SILU;
-    if (int r = norm_gemv(c, c->XA, W + b.rf, gu, ANA_K_GEMV)) return r;
+    if (int r = norm_gemv(c, c->XA, W + b.rf, gu, ANA_K_GEMV, chunk)) return r;
     GemvArgs wd = gemv1(c->HH, f, f, W + b.wd, d, c->X, d, B);
     wd.mode = GM_RESID; wd.R = c->XA; wd.ldr = d;
-    HIPCHK(c, gemv_timed(c, wd, ANA_K_GEMV));
+    HIPCHK(c, gemv_timed(c, wd, ANA_K_GEMV, chunk));
   }
   return ANA_OK;
 }

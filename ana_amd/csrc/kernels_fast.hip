@@ -8,6 +8,8 @@
 // once, at load); activations, accumulation and recurrent state stay fp32.
 #include <hip/hip_ext.h>
 
+#include <type_traits>
+
 #include "ana_internal.h"
 #include "numerics.h"
 
@@ -599,6 +601,193 @@ hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st) {
 
 size_t attn_fast_part_floats(uint32_t B, uint32_t heads, uint32_t ctx, uint32_t hd) {
   return (size_t)B * heads * ((ctx + kFastTS - 1) / kFastTS) * (hd + 2);
+}
+
+}  // namespace ana
+
+namespace ana {
+
+// ------------------------------------------------------------------ batched products on MFMA
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Larger batches (prefill chunks, batched decode) in the fast modes:
+// Y[m][n] = sum_k X[m][k] W[n][k] on the matrix cores. A workgroup owns 16
+// weight rows (n) and 64 batch rows (m); wave w computes the 16 x 16 tile
+// of batch rows 16w.. with v_mfma_f32_16x16x32_bf16 (ANA_BF16: bf16
+// weights; each activation split into a bf16 head and a bf16 remainder,
+// x = hi + lo to ~16 bits, two products per step) or v_mfma_f32_16x16x4f32
+// (ANA_FAST_FP32). K goes in
+// chunks of 64 through a ring of D register sets (D - 1 chunks in flight)
+// and two LDS buffers. With `ng` the chunk is staged as x * g and each
+// row's sum of squares is gathered on the way, so M.norm's scale
+// 1/sqrt(ss/K + 1e-5) multiplies the row's results in the epilogue.
+// Epilogues: plain, residual, SiLU (tile rows 0..7 gate j, 8..15 up j).
+template <int WT, int D>
+__global__ __launch_bounds__(256) void k_gemm_mfma(GemvArgs a) {
+  constexpr int BK = 64, BM = 64, BN = 16;
+  constexpr int XP = BK + 8;             // LDS row pitch (elements), bf16 or f32
+  using E = typename std::conditional<WT == 1, __bf16, float>::type;
+  __shared__ __align__(16) E Xs[2][BM][XP];
+  __shared__ __align__(16) __bf16 Xl[WT == 1 ? 2 : 1][WT == 1 ? BM : 1][WT == 1 ? XP : 8];
+  __shared__ __align__(16) E Ws[2][BN][XP];
+  __shared__ float ssp[4][BM];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t m0 = blockIdx.y * BM;
+  const uint32_t nb = min((uint32_t)BM, a.B - m0);
+  const uint32_t K = a.K, nch = (K + BK - 1) / BK;
+  const Segs sgs(a);
+  const bool norm = a.ng != nullptr;
+  // this thread's share of a chunk: X rows xm (4 float4 of 16 k each), one
+  // 16-byte piece of a weight row (bf16: 8 values; f32: 4 values, twice)
+  const uint32_t xm = tid >> 2, xk = (tid & 3) * 16;
+  const float* xsrc = a.X + (size_t)(m0 + (xm < nb ? xm : 0)) * a.ldx;
+  const uint32_t wr = WT == 1 ? tid >> 3 : tid >> 4;          // weight row in tile
+  const uint32_t wk = WT == 1 ? (tid & 7) * 8 : (tid & 15) * 4;
+  const float* wf;
+  uint32_t wsg, wlr;
+  const bool wok = tid < (WT == 1 ? 128u : 256u) && sgs.row(BN, blockIdx.x, wr, &wf, &wsg, &wlr);
+  const uint16_t* wh = (wsg ? a.Wh1 : a.Wh0) + (size_t)wlr * K;
+  if (!wok) {
+    wf = sgs.W0;
+    wh = a.Wh0;
+  }
+  float4 xr[D][4];
+  uint4 whr[D];
+  float4 wfr[D];
+  auto load = [&](int u, uint32_t c) {
+    const uint32_t q0 = c * BK;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t q = q0 + xk + 4 * j;
+      xr[u][j] = *reinterpret_cast<const float4*>(xsrc + (q < K ? q : 0));
+    }
+    const uint32_t q = q0 + wk;
+    if constexpr (WT == 1) whr[u] = *reinterpret_cast<const uint4*>(wh + (q < K ? q : 0));
+    else wfr[u] = *reinterpret_cast<const float4*>(wf + (q < K ? q : 0));
+  };
+  float ss = 0.0f;
+  auto store = [&](int u, int buf, uint32_t c) {
+    const uint32_t q0 = c * BK;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t q = q0 + xk + 4 * j;
+      float4 x = xr[u][j];
+      if (q >= K || xm >= nb) x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (norm) {
+        ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+        const float4 g = *reinterpret_cast<const float4*>(a.ng + (q < K ? q : 0));
+        x.x *= g.x;
+        x.y *= g.y;
+        x.z *= g.z;
+        x.w *= g.w;
+      }
+      E* dst = &Xs[buf][xm][xk + 4 * j];
+      dst[0] = (E)x.x;
+      dst[1] = (E)x.y;
+      dst[2] = (E)x.z;
+      dst[3] = (E)x.w;
+      if constexpr (WT == 1) {
+        __bf16* lo = &Xl[buf][xm][xk + 4 * j];
+        lo[0] = (__bf16)(x.x - (float)dst[0]);
+        lo[1] = (__bf16)(x.y - (float)dst[1]);
+        lo[2] = (__bf16)(x.z - (float)dst[2]);
+        lo[3] = (__bf16)(x.w - (float)dst[3]);
+      }
+    }
+    const uint32_t q = q0 + wk;
+    if constexpr (WT == 1) {
+      if (tid < 128) {
+        uint4 w = whr[u];
+        if (q >= K) w = make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4*>(&Ws[buf][wr][wk]) = w;
+      }
+    } else {
+      float4 w = wfr[u];
+      if (q >= K) w = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      *reinterpret_cast<float4*>(&Ws[buf][wr][wk]) = w;
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < D; u++)
+    if ((uint32_t)u < nch) load(u, u);
+  store(0, 0, 0);
+  __syncthreads();
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t am = wv * 16 + (lane & 15), g4 = lane >> 4;
+  for (uint32_t c0 = 0; c0 < nch; c0 += D) {
+#pragma unroll
+    for (int u = 0; u < D; u++) {
+      const uint32_t c = c0 + u;
+      if (c < nch) {
+        const int buf = c & 1;
+        if constexpr (WT == 1) {
+#pragma unroll
+          for (int ks = 0; ks < BK; ks += 32) {
+            const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(&Xs[buf][am][ks + 8 * g4]);
+            const bf16x8_t al = *reinterpret_cast<const bf16x8_t*>(&Xl[buf][am][ks + 8 * g4]);
+            const bf16x8_t bv = *reinterpret_cast<const bf16x8_t*>(&Ws[buf][lane & 15][ks + 8 * g4]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bv, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
+          }
+        } else {
+#pragma unroll
+          for (int ks = 0; ks < BK; ks += 16) {
+            const float4 av = *reinterpret_cast<const float4*>(&Xs[buf][am][ks + 4 * g4]);
+            const float4 bv = *reinterpret_cast<const float4*>(&Ws[buf][lane & 15][ks + 4 * g4]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc, 0, 0, 0);
+          }
+        }
+        if (c + 1 < nch) store((u + 1) % D, buf ^ 1, c + 1);
+        if (c + D < nch) load(u, c + D);
+        __syncthreads();
+      }
+    }
+  }
+  // the rows' sums of squares: 4 threads a row, then the scale
+  if (norm) {
+    ss += __shfl_xor(ss, 1, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    if ((tid & 3) == 0) ssp[0][xm] = 1.0f / sqrtf(ss / (float)K + 1.0e-5f);
+    __syncthreads();
+  }
+  // result tile: lane holds rows 4*g4 + r of the wave's block, column lane & 15
+  const uint32_t n = lane & 15;
+  const float* w_;
+  uint32_t sg, lr;
+  const bool nok = sgs.row(BN, blockIdx.x, n, &w_, &sg, &lr);
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const uint32_t m = wv * 16 + 4 * g4 + r;
+    float y = acc[r];
+    if (norm) y *= ssp[0][m < BM ? m : 0];
+    if (a.mode == GM_SILU) {
+      const float up = __shfl_xor(y, 8, 64);
+      if (n < 8 && nok && m < nb) a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = fast_silu(y) * up;
+    } else if (nok && m < nb) {
+      if (a.mode == GM_RESID) y = a.R[(size_t)(m0 + m) * a.ldr + lr] + y;
+      if (sg) a.seg[1].Y[(size_t)(m0 + m) * a.seg[1].ldy + lr] = y;
+      else a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = y;
+    }
+  }
+}
+
+hipError_t launch_gemm_mfma(const GemvArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  if (a.amax || (a.K & 7) || a.B == 0) return hipErrorInvalidValue;
+  const bool bf = a.Wh0 != nullptr;
+  if (bf && a.nseg > 1 && !a.Wh1) return hipErrorInvalidValue;
+  const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
+                                          : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
+  const uint32_t per = a.mode == GM_SILU ? 8 : 16;
+  const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
+  dim3 grid(tiles, (a.B + 63) / 64);
+  if (bf) ANA_LAUNCH_F((k_gemm_mfma<1, 4>), grid, dim3(256), 0, st, e0, e1, a);
+  else ANA_LAUNCH_F((k_gemm_mfma<0, 4>), grid, dim3(256), 0, st, e0, e1, a);
+  return hipGetLastError();
 }
 
 }  // namespace ana

@@ -78,7 +78,8 @@ def run_batch(path: str, c: cf.Config, B: int, prompt: int, warmup: int, steps: 
             dec.feeds(b, 0, pr[:-1])
             first.append(int(pr[-1]))
             pos.append(prompt - 1)
-        log(f"B={B}: prefill {B}x{prompt - 1} tokens in {time.perf_counter() - t:.2f}s")
+        t_pre = time.perf_counter() - t
+        log(f"B={B} {mode}: prefill {B}x{prompt - 1} tokens in {t_pre:.3f}s")
         tok = np.array(first, dtype=np.uint32)
         pos = np.array(pos, dtype=np.uint32)
         if warmup:
@@ -100,6 +101,7 @@ def run_batch(path: str, c: cf.Config, B: int, prompt: int, warmup: int, steps: 
     return {
         "tok_s": B * steps / dt,
         "ms_per_step": 1000.0 * dt / steps,
+        "prefill_tok_s": B * (prompt - 1) / t_pre,
         "step_bytes": sb,
         "step_gbs": sb * steps / dt / 1e9,
         "stats": stats,
@@ -191,12 +193,15 @@ def main() -> int:
                 continue
             r = run_batch(path, c, 1, a.prompt, a.warmup, a.steps, 0, m)
             extra[f"b1_{m}"] = {"tok_s": round(r["tok_s"], 2), "ms_per_step": round(r["ms_per_step"], 4),
-                                "step_gbs": round(r["step_gbs"], 2), "numerics": NUMERICS[m]}
+                                "step_gbs": round(r["step_gbs"], 2), "prefill_tok_s": round(r["prefill_tok_s"], 1),
+                                "numerics": NUMERICS[m]}
     if a.b64:
-        r64 = run_batch(path, c, 64, 128, 2, 32, 8)
-        extra["b64"] = {k: r64[k] for k in ("tok_s", "ms_per_step", "step_gbs")}
-        extra["b64"]["workload"] = ("B=64, 128-token prompts, 32 greedy steps at positions 129+, "
-                                    "exact fp32 (batched products run the exact kernels in every mode)")
+        for m in [mode] + ([x for x in MODES if x != mode] if a.others else []):
+            r64 = run_batch(path, c, 64, 128, 2, 32, 8, m)
+            key = "b64" if m == mode else f"b64_{m}"
+            extra[key] = {k: round(r64[k], 3) for k in ("tok_s", "ms_per_step", "step_gbs", "prefill_tok_s")}
+            extra[key]["workload"] = ("B=64, 128-token prompts (chunked prefill, one sequence at a "
+                                      "time), 32 greedy steps at positions 128+; " + NUMERICS[m])
     cpu = cpu_baseline(path, c, a.cpu_seconds) if a.cpu_seconds > 0 else None
     kern = {k: {"launches": v[0], "ms": round(v[1], 4), "gb": round(v[2] / 1e9, 4)}
             for k, v in r1["stats"].items()}
@@ -232,6 +237,7 @@ def main() -> int:
         },
         "step_gbs": round(r1["step_gbs"], 2),
         "step_frac": round(r1["step_gbs"] / HBM_PEAK_GBS, 5),
+        "prefill_tok_s": round(r1["prefill_tok_s"], 1),
         "kernels": kern,
         "cpu_baseline": cpu,
         **extra,

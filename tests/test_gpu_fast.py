@@ -121,3 +121,40 @@ def test_fast_token_loop(oracle, small_ckpt, mode):
         assert lg[t] >= lg.max() - 2 * TOL[mode] * scale, (pos, t, int(lg.argmax()))
         st.feed(pos, int(t))
         pos += 1
+
+
+@pytest.mark.skip(reason="its first run faulted the GPU (an illegal memory access reported at the "
+                         "first ana_logits of 8 sequences); no cause found yet, so the paths it "
+                         "covered (fast decode of more than 4 sequences, the matrix-core head, "
+                         "fast products in prefill chunks of 4 rows or fewer) are switched off")
+@pytest.mark.parametrize("mode", MODES)
+def test_fast_batch8_matrix_cores(oracle, small_ckpt, mode):
+    """Eight sequences decoded together: the products run on the matrix cores
+    (B > 4), GLA and attention on the fast kernels; each sequence's logits
+    against its own oracle run, across the ring wrap."""
+    print(f"case fast batch8 mode {mode}", flush=True)
+    m = oracle.Model(small_ckpt)
+    n, steps = 8, 72
+    rng = np.random.default_rng(5)
+    streams = rng.integers(0, m.vocab, size=(n, steps + 8)).astype(np.uint32)
+    starts = [0, 1, 2, 3, 5, 8, 4, 6]
+    sts = [oracle.State(m) for _ in range(n)]
+    worst = 0.0
+    with ana_amd.Decoder(small_ckpt, max_seqs=n, numerics=mode, prefill_chunk=8) as dec:
+        for i in range(n):
+            if starts[i]:
+                dec.feeds(i, 0, streams[i, : starts[i]])
+            for p in range(starts[i]):
+                sts[i].feed(p, int(streams[i, p]))
+        for k in range(steps):
+            pos = [starts[i] + k for i in range(n)]
+            tok = [int(streams[i, pos[i]]) for i in range(n)]
+            dec.feed(list(range(n)), pos, tok)
+            for i in range(n):
+                sts[i].feed(pos[i], tok[i])
+            if k % 12 == 11:
+                got = dec.logits(list(range(n)))
+                for i in range(n):
+                    worst = max(worst, rel_err(got[i], sts[i].logits()))
+    print(f"worst relative error {worst:.3e}", flush=True)
+    assert worst <= TOL[mode], worst
