@@ -234,7 +234,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = dalloc(&c->d_pick, wb)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_rng, 4 * wb)) != hipSuccess) return bad(e);
   if (c->mode != ANA_EXACT_FP32 &&
-      (e = dalloc(&c->d_part, attn_fast_part_floats(kSmallB, cf.heads, cf.ctx, hd))) != hipSuccess)
+      (e = dalloc(&c->d_part, attn_fast_part_floats(std::max(kSmallB, c->chunk), cf.heads, cf.ctx, hd))) != hipSuccess)
     return bad(e);
   if (c->mode == ANA_BF16 && (e = dalloc(&c->Wh, c->P)) != hipSuccess) return bad(e);
   if ((e = hipMemcpyAsync(c->W, ck.raw.data(), 4 * c->P, hipMemcpyHostToDevice, c->st)) != hipSuccess) return bad(e);
@@ -290,7 +290,8 @@ static double gemv_bytes(const GemvArgs& g) {
 // products on the matrix cores. Decode steps of more sequences, the head over
 // more than kSmallB rows and prefill chunks of kSmallB rows or fewer run the
 // exact kernels (those paths faulted the GPU in their first test and stay off
-// until the cause is found).
+// until the cause is found). Prefill chunks of more than kSmallB rows also
+// take the closed-form GLA chunk and the split attention.
 static bool fast_mode(const ana_ctx* c) { return c->mode != ANA_EXACT_FP32; }
 static bool fast_path(const ana_ctx* c, uint32_t B) { return fast_mode(c) && B <= kSmallB; }
 
@@ -344,6 +345,9 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
   const float* W = c->W;
   const bool chunk = seq == nullptr;
   const bool fresh = chunk && (uint64_t)pos0 + B <= cf.ctx;
+  // a fast mode's prefill chunk of more than kSmallB rows: matrix-core
+  // products, the closed-form GLA chunk and the split attention
+  const bool fast_chunk = chunk && fast_mode(c) && B > kSmallB;
   for (uint32_t l = 0; l < cf.layers; l++) {
     const Blk& b = c->blk[l];
     // norm, then q|k|v (+ the gate's z): dd.gla / dd.sm `pre`
@@ -354,7 +358,11 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
     }
     if (int r = norm_gemv(c, c->X, W + b.ra, g, ANA_K_GEMV, chunk)) return r;
     if (b.gla) {
-      if (chunk) {
+      if (chunk && fast_chunk) {
+        HIPCHK(c, launch_gla_chunk_fast(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr,
+                                        c->state + (uint64_t)seq0 * c->seq_stride + c->layer_off[l],
+                                        c->O, d, cf.heads, cf.rglru, B, c->st));
+      } else if (chunk) {
         HIPCHK(c, launch_gla_chunk(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr,
                                    c->state + (uint64_t)seq0 * c->seq_stride + c->layer_off[l], c->O,
                                    d, cf.heads, cf.rglru, B, c->st));
@@ -392,7 +400,12 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
         a.QKV = c->QKV; a.O = c->O; a.B = B;
         a.seq = nullptr; a.seq0 = seq0; a.pos = nullptr; a.pos0 = pos0; a.write_kv = 0;
         HIPCHK(c, launch_kv_write(a, c->st));
-        HIPCHK(c, launch_attn(a, c->st));
+        if (fast_chunk) {
+          a.part = c->d_part;
+          HIPCHK(c, launch_attn_fast(a, c->st));
+        } else {
+          HIPCHK(c, launch_attn(a, c->st));
+        }
       } else {
         // past the wrap: each token's write and attention in turn (dd.sm.toks)
         for (uint32_t t = 0; t < B; t++) {

@@ -233,6 +233,11 @@ hipError_t launch_gla_fast(const float* QKV, const float* Z, const float* lam, S
                            const uint32_t* seq, float* O, uint32_t d, uint32_t heads,
                            uint32_t rglru, uint32_t B, hipStream_t st);
 hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st);
+// GLA over T tokens of one sequence (a prefill chunk) in closed form per
+// 16-token sub-chunk, S read and written once
+hipError_t launch_gla_chunk_fast(const float* QKV, const float* Z, const float* lam, float* S,
+                                 float* O, uint32_t d, uint32_t heads, uint32_t rglru, uint32_t T,
+                                 hipStream_t st);
 // batched products (prefill chunks, B > kSmallB) on the matrix cores: bf16
 // when Wh0 is set, else fp32; no argmax epilogue
 hipError_t launch_gemm_mfma(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nullptr,

@@ -414,9 +414,11 @@ __global__ __launch_bounds__(256) void k_attn_fast_part(AttnArgs a) {
   __shared__ float4 op[4][C4];
   const uint32_t h = blockIdx.x, sp = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const uint32_t d = a.d, ctx = a.ctx, ns = (ctx + kFastTS - 1) / kFastTS;
-  const uint32_t pos = a.pos[b];
+  // a decode row (its sequence and position), or row b of a chunk of one
+  // sequence at positions pos0 + b
+  const uint32_t pos = a.pos ? a.pos[b] : a.pos0 + b;
   const uint32_t slot = pos % ctx, npos = pos < ctx - 1 ? pos : ctx - 1;
-  const uint32_t sl = a.seq[b];
+  const uint32_t sl = a.seq ? a.seq[b] : a.seq0;
   float* Kr = a.KV.base + (size_t)sl * a.KV.seq_stride + a.KV.layer_off;
   float* Vr = Kr + (size_t)ctx * d;
   const uint32_t t0 = sp * kFastTS;
@@ -585,7 +587,7 @@ __global__ __launch_bounds__(64) void k_attn_fast_comb(AttnArgs a) {
 hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st) {
   const uint32_t hd = a.d / a.heads;
   const uint32_t ns = (a.ctx + kFastTS - 1) / kFastTS;
-  if (!a.part || !a.seq || !a.pos || hd % 4 || hd > 64 || ns > 64) return hipErrorInvalidValue;
+  if (!a.part || hd % 4 || hd > 64 || ns > 64) return hipErrorInvalidValue;
 #define L_(H)                                                                                   \
   hipLaunchKernelGGL(k_attn_fast_part<H>, dim3(a.heads, ns, a.B), dim3(256), 0, st, a);        \
   hipLaunchKernelGGL(k_attn_fast_comb<H>, dim3(a.heads, a.B), dim3(64), 0, st, a)
@@ -787,6 +789,143 @@ hipError_t launch_gemm_mfma(const GemvArgs& a, hipStream_t st, hipEvent_t e0, hi
   dim3 grid(tiles, (a.B + 63) / 64);
   if (bf) ANA_LAUNCH_F((k_gemm_mfma<1, 4>), grid, dim3(256), 0, st, e0, e1, a);
   else ANA_LAUNCH_F((k_gemm_mfma<0, 4>), grid, dim3(256), 0, st, e0, e1, a);
+  return hipGetLastError();
+}
+
+}  // namespace ana
+
+namespace ana {
+
+// ------------------------------------------------------------------ GLA over a chunk
+
+// T tokens of one sequence through one head's GLA (bend/Dense/Decode.bend
+// dd.gla over a chunk), for a block of CB state columns: the recurrence
+// S_t = diag(a_t) S_(t-1) + kh_t v_t^T, o_t = qh_t^T S_t taken L tokens at a
+// time in closed form. With c_t the running sum of log a within a
+// sub-chunk, S_t = e^(c_t) S_prev + sum_(s<=t) e^(c_t - c_s) kh_s v_s^T, so
+//   o_t = (qh_t e^(c_t))^T S_prev + sum_(s<=t) P_ts v_s,
+//   P_ts = sum_a qh_t[a] kh_s[a] e^(c_t[a] - c_s[a]),
+// and every exponent is <= 0 (nothing overflows however small the gates).
+template <int HD>
+__global__ __launch_bounds__(256) void k_gla_chunk_fast(const float* __restrict__ QKV,
+                                                         const float* __restrict__ Z,
+                                                         const float* __restrict__ lam,
+                                                         float* __restrict__ Sbase,
+                                                         float* __restrict__ O, uint32_t d,
+                                                         uint32_t rglru, uint32_t T) {
+  constexpr int CB = 16, L = 16;
+  __shared__ float qh[L][HD + 1], kh[L][HD + 1], cl[L][HD + 1];
+  __shared__ float vv[L][CB], P[L][L + 1], Sb[HD][CB + 1], nr[L][2];
+  const uint32_t h = blockIdx.x, cb = blockIdx.y, tid = threadIdx.x;
+  float* Sg = Sbase + (size_t)h * HD * HD + cb * CB;
+  for (uint32_t e = tid; e < HD * CB; e += 256) Sb[e / CB][e % CB] = Sg[(size_t)(e / CB) * HD + e % CB];
+  for (uint32_t s0 = 0; s0 < T; s0 += L) {
+    const uint32_t n = min((uint32_t)L, T - s0);
+    __syncthreads();
+    // q, k norms of the sub-chunk's tokens: 16 lanes a token
+    {
+      const uint32_t t = tid / 16, l = tid % 16;
+      float sq = 0.0f, sk = 0.0f;
+      if (t < n) {
+        const float* x = QKV + (size_t)(s0 + t) * 3 * d + h * HD;
+        for (uint32_t a = l; a < (uint32_t)HD; a += 16) {
+          const float q = x[a], k = x[d + a];
+          sq = fmaf(q, q, sq);
+          sk = fmaf(k, k, sk);
+        }
+      }
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) {
+        sq += __shfl_xor(sq, m, 64);
+        sk += __shfl_xor(sk, m, 64);
+      }
+      if (l == 0 && t < L) {
+        nr[t][0] = 1.0f / sqrtf(1.0e-6f + sq);
+        nr[t][1] = 1.0f / sqrtf(1.0e-6f + sk);
+      }
+    }
+    __syncthreads();
+    // gates: log a (dd.gate in log form) and kh, per token and key dim
+    for (uint32_t e = tid; e < (uint32_t)L * HD; e += 256) {
+      const uint32_t t = e / HD, a = e % HD;
+      float lq = 0.0f, lk = 0.0f, la = 0.0f;
+      if (t < n) {
+        const float* x = QKV + (size_t)(s0 + t) * 3 * d + h * HD;
+        const float z = Z[(size_t)(s0 + t) * d + h * HD + a];
+        lq = x[a] * nr[t][0];
+        const float kn = x[d + a] * nr[t][1];
+        if (rglru) {
+          la = fminf(ANA_CAP, (8.0f * f_sigmoid(z)) * f_log_sigmoid(lam[h * HD + a]));
+          lk = kn * sqrtf(1.0f - expf(2.0f * la));
+        } else {
+          la = f_log_sigmoid(z);
+          lk = kn;
+        }
+      }
+      qh[t][a] = lq;
+      kh[t][a] = lk;
+      cl[t][a] = la;
+    }
+    if (tid < (uint32_t)L * CB) {
+      const uint32_t t = tid / CB, b = tid % CB;
+      vv[t][b] = t < n ? QKV[(size_t)(s0 + t) * 3 * d + 2 * d + h * HD + cb * CB + b] : 0.0f;
+    }
+    __syncthreads();
+    // running sums of log a over the sub-chunk (one lane per key dim)
+    if (tid < (uint32_t)HD) {
+      float c = 0.0f;
+      for (int t = 0; t < L; t++) {
+        c += cl[t][tid];
+        cl[t][tid] = c;
+      }
+    }
+    __syncthreads();
+    // P_ts for s <= t (one lane per pair)
+    {
+      const uint32_t t = tid / L, s = tid % L;
+      float p = 0.0f;
+      if (s <= t && t < n) {
+        for (int a = 0; a < HD; a++) p = fmaf(qh[t][a] * kh[s][a], __expf(cl[t][a] - cl[s][a]), p);
+      }
+      P[t][s] = p;
+    }
+    __syncthreads();
+    // o_t for the block's columns: lane (t, b)
+    {
+      const uint32_t t = tid / CB, b = tid % CB;
+      if (t < n) {
+        float o = 0.0f;
+        for (int a = 0; a < HD; a++) o = fmaf(qh[t][a] * __expf(cl[t][a]), Sb[a][b], o);
+        for (uint32_t s = 0; s <= t; s++) o = fmaf(P[t][s], vv[s][b], o);
+        O[(size_t)(s0 + t) * d + h * HD + cb * CB + b] = o;
+      }
+    }
+    __syncthreads();
+    // S <- e^(c_last) S + sum_s e^(c_last - c_s) kh_s v_s^T
+    for (uint32_t e = tid; e < (uint32_t)HD * CB; e += 256) {
+      const uint32_t a = e / CB, b = e % CB;
+      const float cL = cl[n - 1][a];
+      float s2 = __expf(cL) * Sb[a][b];
+      for (uint32_t s = 0; s < n; s++) s2 = fmaf(__expf(cL - cl[s][a]) * kh[s][a], vv[s][b], s2);
+      Sb[a][b] = s2;
+    }
+  }
+  __syncthreads();
+  for (uint32_t e = tid; e < HD * CB; e += 256) Sg[(size_t)(e / CB) * HD + e % CB] = Sb[e / CB][e % CB];
+}
+
+hipError_t launch_gla_chunk_fast(const float* QKV, const float* Z, const float* lam, float* S,
+                                 float* O, uint32_t d, uint32_t heads, uint32_t rglru, uint32_t T,
+                                 hipStream_t st) {
+  const uint32_t hd = d / heads;
+#define L_(H) hipLaunchKernelGGL(k_gla_chunk_fast<H>, dim3(heads, H / 16), dim3(256), 0, st, QKV, Z, lam, S, O, d, rglru, T)
+  switch (hd) {
+    case 64: L_(64); break;
+    case 32: L_(32); break;
+    case 16: L_(16); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef L_
   return hipGetLastError();
 }
 

@@ -158,3 +158,37 @@ def test_fast_batch8_matrix_cores(oracle, small_ckpt, mode):
                     worst = max(worst, rel_err(got[i], sts[i].logits()))
     print(f"worst relative error {worst:.3e}", flush=True)
     assert worst <= TOL[mode], worst
+
+
+@pytest.fixture(scope="module")
+def noarms_ckpt(tmp_path_factory):
+    d = tmp_path_factory.mktemp("ckn")
+    p = str(d / "noarms.ftc2")
+    ckpt.write(p, cf.SMALL4_NOARMS, ckpt.init_params(cf.SMALL4_NOARMS, "normal", 4))
+    return p
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("arms", ["v3", "noarms"])
+def test_fast_prefill(oracle, small_ckpt, noarms_ckpt, mode, arms):
+    """A 96-token prompt through chunked prefill at chunk 16 (matrix-core
+    products, closed-form GLA chunks, split attention; the last chunks past
+    the ring wrap at ctx 64), then 8 fast decode steps; logits against the
+    oracle fed the same tokens."""
+    path = small_ckpt if arms == "v3" else noarms_ckpt
+    print(f"case fast prefill {arms} mode {mode}", flush=True)
+    m = oracle.Model(path)
+    st = oracle.State(m)
+    ts = VEC["window"]
+    worst = 0.0
+    with ana_amd.Decoder(path, prefill_chunk=16, numerics=mode) as dec:
+        dec.feeds(0, 0, ts[:88])
+        for p in range(88):
+            st.feed(p, ts[p])
+        worst = max(worst, rel_err(dec.logits([0])[0], st.logits()))
+        for p in range(88, 96):
+            dec.feed([0], [p], [ts[p]])
+            st.feed(p, ts[p])
+            worst = max(worst, rel_err(dec.logits([0])[0], st.logits()))
+    print(f"worst relative error {worst:.3e}", flush=True)
+    assert worst <= TOL[mode], worst
