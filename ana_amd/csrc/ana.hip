@@ -42,6 +42,7 @@ struct ana_ctx {
   unsigned long long* d_amax = nullptr;  // [wb] greedy argmax keys
   float *d_ss = nullptr, *d_pm = nullptr; // split attention scratch
   float* d_part = nullptr;           // fast attention's per-split partials
+  float* d_gla = nullptr;            // fast prefill's GLA scan scratch
   size_t out_cap = 0;
   std::string err;
   // ana_generate's decode step captured as HIP graphs, replayed per step:
@@ -134,7 +135,7 @@ static void release(ana_ctx* c) {
   (void)hipSetDevice(c->device);
   if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
   if (c->gexec_n) (void)hipGraphExecDestroy(c->gexec_n);
-  void* ps[] = {c->W, c->Wh, c->d_part, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
+  void* ps[] = {c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
                 c->d_ss, c->d_pm};
   for (void* p : ps)
@@ -237,6 +238,9 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
       (e = dalloc(&c->d_part, attn_fast_part_floats(std::max(kSmallB, c->chunk), cf.heads, cf.ctx, hd))) != hipSuccess)
     return bad(e);
   if (c->mode == ANA_BF16 && (e = dalloc(&c->Wh, c->P)) != hipSuccess) return bad(e);
+  if (c->mode != ANA_EXACT_FP32 &&
+      (e = dalloc(&c->d_gla, gla_scan_floats(c->chunk, d, cf.heads))) != hipSuccess)
+    return bad(e);
   if ((e = hipMemcpyAsync(c->W, ck.raw.data(), 4 * c->P, hipMemcpyHostToDevice, c->st)) != hipSuccess) return bad(e);
   if ((e = launch_bswap(reinterpret_cast<uint32_t*>(c->W), c->P, c->st)) != hipSuccess) return bad(e);
   if (c->Wh && (e = launch_to_bf16(c->W, c->Wh, c->P, c->st)) != hipSuccess) return bad(e);
@@ -359,9 +363,9 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
     if (int r = norm_gemv(c, c->X, W + b.ra, g, ANA_K_GEMV, chunk)) return r;
     if (b.gla) {
       if (chunk && fast_chunk) {
-        HIPCHK(c, launch_gla_chunk_fast(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr,
-                                        c->state + (uint64_t)seq0 * c->seq_stride + c->layer_off[l],
-                                        c->O, d, cf.heads, cf.rglru, B, c->st));
+        HIPCHK(c, launch_gla_scan(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr,
+                                  c->state + (uint64_t)seq0 * c->seq_stride + c->layer_off[l], c->O,
+                                  c->d_gla, d, cf.heads, cf.rglru, B, c->st));
       } else if (chunk) {
         HIPCHK(c, launch_gla_chunk(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr,
                                    c->state + (uint64_t)seq0 * c->seq_stride + c->layer_off[l], c->O,

@@ -238,6 +238,12 @@ hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st);
 hipError_t launch_gla_chunk_fast(const float* QKV, const float* Z, const float* lam, float* S,
                                  float* O, uint32_t d, uint32_t heads, uint32_t rglru, uint32_t T,
                                  hipStream_t st);
+// the same as a chunked scan: 32-token sub-chunks in parallel, then their
+// states carried across (scratch: gla_scan_floats(T, d, heads) floats)
+size_t gla_scan_floats(uint32_t T, uint32_t d, uint32_t heads);
+hipError_t launch_gla_scan(const float* QKV, const float* Z, const float* lam, float* S, float* O,
+                           float* scratch, uint32_t d, uint32_t heads, uint32_t rglru, uint32_t T,
+                           hipStream_t st);
 // batched products (prefill chunks, B > kSmallB) on the matrix cores: bf16
 // when Wh0 is set, else fp32; no argmax epilogue
 hipError_t launch_gemm_mfma(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nullptr,

@@ -930,3 +930,220 @@ hipError_t launch_gla_chunk_fast(const float* QKV, const float* Z, const float* 
 }
 
 }  // namespace ana
+
+namespace ana {
+
+// ------------------------------------------------------------------ GLA over a chunk, two passes
+
+// The same closed form as k_gla_chunk_fast, with the 32-token sub-chunks of
+// a chunk run in parallel (a chunked scan). Pass 1, per (head, column block,
+// sub-chunk j): gates, the intra terms o_t = sum_(s<=t) P_ts v_s, the
+// sub-chunk's decay D_j = e^(c_last) and state contribution
+// U_j = sum_s e^(c_last - c_s) kh_s v_s^T, and qt_t = qh_t e^(c_t).
+// Pass 2, per (head, column block, j): the state entering j,
+// S_(j-1) = D_(j-1) (... (D_0 S_0 + U_0) ...) + U_(j-1), then o_t += qt_t^T S_(j-1);
+// the last sub-chunk's workgroup writes the chunk's final state.
+constexpr int kGlaSub = 32;
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_gla_sub(const float* __restrict__ QKV,
+                                                  const float* __restrict__ Z,
+                                                  const float* __restrict__ lam, float* __restrict__ O,
+                                                  float* __restrict__ Qt, float* __restrict__ Dj,
+                                                  float* __restrict__ Uj, const float* __restrict__ Sbase,
+                                                  float* __restrict__ S0, uint32_t d, uint32_t rglru,
+                                                  uint32_t T) {
+  constexpr int CB = 16, L = kGlaSub;
+  __shared__ float qh[L][HD + 1], kh[L][HD + 1], cl[L][HD + 1];
+  __shared__ float vv[L][CB], P[L][L + 1], nr[L][2];
+  const uint32_t h = blockIdx.x, cb = blockIdx.y, j = blockIdx.z, tid = threadIdx.x;
+  const uint32_t nsub = gridDim.z, s0 = j * L, n = min((uint32_t)L, T - s0);
+  // the state entering the chunk, copied for pass 2 (which rewrites S)
+  if (j == 0) {
+    for (uint32_t e = tid; e < (uint32_t)HD * CB; e += 256) {
+      const size_t off = (size_t)h * HD * HD + (size_t)(e / CB) * HD + cb * CB + e % CB;
+      S0[off] = Sbase[off];
+    }
+  }
+  // q, k, z of the sub-chunk's tokens, and v of the block's columns
+  for (uint32_t e = tid; e < (uint32_t)L * HD; e += 256) {
+    const uint32_t t = e / HD, a = e % HD;
+    float q = 0.0f, k = 0.0f, z = 0.0f;
+    if (t < n) {
+      const float* x = QKV + (size_t)(s0 + t) * 3 * d + h * HD;
+      q = x[a];
+      k = x[d + a];
+      z = Z[(size_t)(s0 + t) * d + h * HD + a];
+    }
+    qh[t][a] = q;
+    kh[t][a] = k;
+    cl[t][a] = z;
+  }
+  for (uint32_t e = tid; e < (uint32_t)L * CB; e += 256) {
+    const uint32_t t = e / CB, b = e % CB;
+    vv[t][b] = t < n ? QKV[(size_t)(s0 + t) * 3 * d + 2 * d + h * HD + cb * CB + b] : 0.0f;
+  }
+  __syncthreads();
+  // L2 norms: 8 lanes a token
+  {
+    const uint32_t t = tid / 8, l = tid % 8;
+    float sq = 0.0f, sk = 0.0f;
+    for (uint32_t a = l; a < (uint32_t)HD; a += 8) {
+      sq = fmaf(qh[t][a], qh[t][a], sq);
+      sk = fmaf(kh[t][a], kh[t][a], sk);
+    }
+#pragma unroll
+    for (int m = 4; m >= 1; m >>= 1) {
+      sq += __shfl_xor(sq, m, 64);
+      sk += __shfl_xor(sk, m, 64);
+    }
+    if (l == 0) {
+      nr[t][0] = 1.0f / sqrtf(1.0e-6f + sq);
+      nr[t][1] = 1.0f / sqrtf(1.0e-6f + sk);
+    }
+  }
+  __syncthreads();
+  // gates: log a and kh (dd.gate), qh
+  for (uint32_t e = tid; e < (uint32_t)L * HD; e += 256) {
+    const uint32_t t = e / HD, a = e % HD;
+    float lq = 0.0f, lk = 0.0f, la = 0.0f;
+    if (t < n) {
+      const float z = cl[t][a];
+      lq = qh[t][a] * nr[t][0];
+      const float kn = kh[t][a] * nr[t][1];
+      if (rglru) {
+        la = fminf(ANA_CAP, (8.0f * f_sigmoid(z)) * f_log_sigmoid(lam[h * HD + a]));
+        lk = kn * sqrtf(1.0f - expf(2.0f * la));
+      } else {
+        la = f_log_sigmoid(z);
+        lk = kn;
+      }
+    }
+    qh[t][a] = lq;
+    kh[t][a] = lk;
+    cl[t][a] = la;
+  }
+  __syncthreads();
+  if (tid < (uint32_t)HD) {
+    float c = 0.0f;
+    for (int t = 0; t < L; t++) {
+      c += cl[t][tid];
+      cl[t][tid] = c;
+    }
+  }
+  __syncthreads();
+  if (cb == 0) {
+    for (uint32_t e = tid; e < n * HD; e += 256) {
+      const uint32_t t = e / HD, a = e % HD;
+      Qt[(size_t)(s0 + t) * d + h * HD + a] = qh[t][a] * __expf(cl[t][a]);
+    }
+    if (tid < (uint32_t)HD) Dj[((size_t)h * nsub + j) * HD + tid] = __expf(cl[n - 1][tid]);
+  }
+  for (uint32_t e = tid; e < (uint32_t)L * L; e += 256) {
+    const uint32_t t = e / L, s = e % L;
+    float p = 0.0f;
+    if (s <= t && t < n)
+      for (int a = 0; a < HD; a++) p = fmaf(qh[t][a] * kh[s][a], __expf(cl[t][a] - cl[s][a]), p);
+    P[t][s] = p;
+  }
+  __syncthreads();
+  for (uint32_t e = tid; e < (uint32_t)L * CB; e += 256) {
+    const uint32_t t = e / CB, b = e % CB;
+    if (t < n) {
+      float o = 0.0f;
+      for (uint32_t s = 0; s <= t; s++) o = fmaf(P[t][s], vv[s][b], o);
+      O[(size_t)(s0 + t) * d + h * HD + cb * CB + b] = o;
+    }
+  }
+  for (uint32_t e = tid; e < (uint32_t)HD * CB; e += 256) {
+    const uint32_t a = e / CB, b = e % CB;
+    const float cL = cl[n - 1][a];
+    float u = 0.0f;
+    for (uint32_t s = 0; s < n; s++) u = fmaf(__expf(cL - cl[s][a]) * kh[s][a], vv[s][b], u);
+    Uj[(((size_t)h * nsub + j) * HD + a) * HD + cb * CB + b] = u;
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_gla_carry(const float* __restrict__ Qt,
+                                                    const float* __restrict__ Dj,
+                                                    const float* __restrict__ Uj,
+                                                    const float* __restrict__ S0,
+                                                    float* __restrict__ Sbase, float* __restrict__ O,
+                                                    uint32_t d, uint32_t T) {
+  constexpr int CB = 16, L = kGlaSub;
+  __shared__ float Sb[HD][CB + 1];
+  const uint32_t h = blockIdx.x, cb = blockIdx.y, j = blockIdx.z, tid = threadIdx.x;
+  const uint32_t nsub = gridDim.z, s0 = j * L, n = min((uint32_t)L, T - s0);
+  float* Sg = Sbase + (size_t)h * HD * HD + cb * CB;
+  const float* S0g = S0 + (size_t)h * HD * HD + cb * CB;
+  // S_(j-1): S_0 through the earlier sub-chunks (HD * CB / 256 elements a thread)
+  constexpr int NE = HD * CB / 256;
+  float sv[NE > 0 ? NE : 1];
+#pragma unroll
+  for (int i = 0; i < NE; i++) {
+    const uint32_t e = tid + 256 * i, a = e / CB, b = e % CB;
+    sv[i] = S0g[(size_t)a * HD + b];
+  }
+  for (uint32_t i = 0; i < j; i++) {
+#pragma unroll
+    for (int q = 0; q < NE; q++) {
+      const uint32_t e = tid + 256 * q, a = e / CB, b = e % CB;
+      sv[q] = fmaf(Dj[((size_t)h * nsub + i) * HD + a], sv[q],
+                   Uj[(((size_t)h * nsub + i) * HD + a) * HD + cb * CB + b]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NE; i++) {
+    const uint32_t e = tid + 256 * i;
+    Sb[e / CB][e % CB] = sv[i];
+  }
+  if (j == nsub - 1) {
+#pragma unroll
+    for (int q = 0; q < NE; q++) {
+      const uint32_t e = tid + 256 * q, a = e / CB, b = e % CB;
+      Sg[(size_t)a * HD + b] = fmaf(Dj[((size_t)h * nsub + j) * HD + a], sv[q],
+                                    Uj[(((size_t)h * nsub + j) * HD + a) * HD + cb * CB + b]);
+    }
+  }
+  __syncthreads();
+  for (uint32_t e = tid; e < n * CB; e += 256) {
+    const uint32_t t = e / CB, b = e % CB;
+    const float* q = Qt + (size_t)(s0 + t) * d + h * HD;
+    float o = 0.0f;
+    for (int a = 0; a < HD; a++) o = fmaf(q[a], Sb[a][b], o);
+    O[(size_t)(s0 + t) * d + h * HD + cb * CB + b] += o;
+  }
+}
+
+size_t gla_scan_floats(uint32_t T, uint32_t d, uint32_t heads) {
+  const uint32_t hd = d / heads, nsub = (T + kGlaSub - 1) / kGlaSub;
+  return (size_t)T * d + (size_t)heads * nsub * hd + (size_t)heads * nsub * hd * hd +
+         (size_t)heads * hd * hd;
+}
+
+hipError_t launch_gla_scan(const float* QKV, const float* Z, const float* lam, float* S, float* O,
+                           float* scratch, uint32_t d, uint32_t heads, uint32_t rglru, uint32_t T,
+                           hipStream_t st) {
+  const uint32_t hd = d / heads, nsub = (T + kGlaSub - 1) / kGlaSub;
+  if (hd % 16 || hd * 16 < 256 || T == 0) return hipErrorInvalidValue;
+  float* Qt = scratch;
+  float* Dj = Qt + (size_t)T * d;
+  float* Uj = Dj + (size_t)heads * nsub * hd;
+  float* S0 = Uj + (size_t)heads * nsub * hd * hd;
+#define L_(H)                                                                                       \
+  hipLaunchKernelGGL(k_gla_sub<H>, dim3(heads, H / 16, nsub), dim3(256), 0, st, QKV, Z, lam, O, Qt, \
+                     Dj, Uj, S, S0, d, rglru, T);                                                   \
+  hipLaunchKernelGGL(k_gla_carry<H>, dim3(heads, H / 16, nsub), dim3(256), 0, st, Qt, Dj, Uj, S0,   \
+                     S, O, d, T)
+  switch (hd) {
+    case 64: L_(64); break;
+    case 32: L_(32); break;
+    case 16: L_(16); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef L_
+  return hipGetLastError();
+}
+
+}  // namespace ana

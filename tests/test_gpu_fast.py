@@ -170,18 +170,19 @@ def noarms_ckpt(tmp_path_factory):
 
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("arms", ["v3", "noarms"])
-def test_fast_prefill(oracle, small_ckpt, noarms_ckpt, mode, arms):
-    """A 96-token prompt through chunked prefill at chunk 16 (matrix-core
-    products, closed-form GLA chunks, split attention; the last chunks past
-    the ring wrap at ctx 64), then 8 fast decode steps; logits against the
-    oracle fed the same tokens."""
+@pytest.mark.parametrize("chunk", [16, 48])
+def test_fast_prefill(oracle, small_ckpt, noarms_ckpt, mode, arms, chunk):
+    """An 88-token prompt through chunked prefill (matrix-core products, the
+    GLA chunk as a scan over 32-token sub-chunks, split attention; chunks past
+    the ring wrap at ctx 64 take the per-token attention), then 8 fast decode
+    steps; logits against the oracle fed the same tokens."""
     path = small_ckpt if arms == "v3" else noarms_ckpt
-    print(f"case fast prefill {arms} mode {mode}", flush=True)
+    print(f"case fast prefill {arms} chunk {chunk} mode {mode}", flush=True)
     m = oracle.Model(path)
     st = oracle.State(m)
     ts = VEC["window"]
     worst = 0.0
-    with ana_amd.Decoder(path, prefill_chunk=16, numerics=mode) as dec:
+    with ana_amd.Decoder(path, prefill_chunk=chunk, numerics=mode) as dec:
         dec.feeds(0, 0, ts[:88])
         for p in range(88):
             st.feed(p, ts[p])
