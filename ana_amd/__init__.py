@@ -56,6 +56,7 @@ SIGNATURES = {
     "ana_reset": (C.c_int, [C.c_void_p, C.c_uint32]),
     "ana_feed": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p, _u32p]),
     "ana_feeds": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, _u32p, C.c_uint32]),
+    "ana_feeds_n": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p, _u32p, _u32p]),
     "ana_logits": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _f32p]),
     "ana_top": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p]),
     "ana_pick": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, C.POINTER(_Sampling), _u64p, _u32p]),
@@ -206,6 +207,18 @@ class Decoder:
         """dd.feeds: a prompt a chunk at a time."""
         t = _u32(toks)
         self._check(lib().ana_feeds(self.h, seq, pos, _p(t, C.c_uint32), t.size))
+
+    def feeds_n(self, seqs, pos, toks) -> None:
+        """dd.feeds for several sequences at once: toks[i] into seqs[i] from
+        pos[i]; each chunk step's rows share the products."""
+        s, p = _u32(seqs), _u32(pos)
+        ts = [_u32(t) for t in toks]
+        ln = np.array([t.size for t in ts], dtype=np.uint32)
+        flat = np.ascontiguousarray(np.concatenate(ts) if ts else np.zeros(0, np.uint32), dtype=np.uint32)
+        if flat.size == 0:
+            flat = np.zeros(1, np.uint32)
+        self._check(lib().ana_feeds_n(self.h, s.size, _p(s, C.c_uint32), _p(p, C.c_uint32),
+                                      _p(ln, C.c_uint32), _p(flat, C.c_uint32)))
 
     def logits(self, seqs) -> np.ndarray:
         s = _u32(seqs)

@@ -27,6 +27,7 @@ struct ana_ctx {
   std::vector<uint64_t> layer_off;   // floats from a sequence's state start
   uint64_t seq_stride = 0;           // floats per sequence
   uint32_t max_seqs = 1, chunk = 64, wb = 1;
+  uint32_t rows = 1;                 // capacity of the row workspaces (a prefill batch)
   int mode = ANA_EXACT_FP32;         // numerics
   float* W = nullptr;                // parameters [P]
   uint16_t* Wh = nullptr;            // ANA_BF16: the parameters as bfloat16 [P]
@@ -195,6 +196,8 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   c->max_seqs = o.max_seqs;
   c->chunk = o.prefill_chunk;
   c->wb = std::max(c->max_seqs, c->chunk);
+  // a batched prefill's step holds every sequence's chunk, up to 8192 rows
+  c->rows = std::max<uint32_t>(c->wb, (uint32_t)std::min<uint64_t>((uint64_t)c->max_seqs * c->chunk, 8192));
   const ana_config& cf = c->cfg;
   const uint32_t d = cf.d, hd = d / cf.heads;
   uint64_t off = 0;
@@ -217,21 +220,21 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = dalloc(&c->W, c->P)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->state, c->seq_stride * c->max_seqs)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->xs, (uint64_t)d * c->max_seqs)) != hipSuccess) return bad(e);
-  if ((e = dalloc(&c->X, wb * d)) != hipSuccess) return bad(e);
-  if ((e = dalloc(&c->XA, wb * d)) != hipSuccess) return bad(e);
-  if ((e = dalloc(&c->XN, wb * d)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->X, (uint64_t)c->rows * d)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->XA, (uint64_t)c->rows * d)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->XN, (uint64_t)c->rows * d)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_step, 2)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_amax, wb * kAmaxPerRow)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_ss, wb * cf.heads * cf.ctx)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_pm, wb * cf.heads * ((cf.ctx + kAttnTS - 1) / kAttnTS))) != hipSuccess) return bad(e);
-  if ((e = dalloc(&c->QKV, wb * 3 * d)) != hipSuccess) return bad(e);
-  if ((e = dalloc(&c->Z, wb * d)) != hipSuccess) return bad(e);
-  if ((e = dalloc(&c->O, wb * d)) != hipSuccess) return bad(e);
-  if ((e = dalloc(&c->HH, wb * cf.f)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->QKV, (uint64_t)c->rows * 3 * d)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->Z, (uint64_t)c->rows * d)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->O, (uint64_t)c->rows * d)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->HH, (uint64_t)c->rows * cf.f)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->LG, (uint64_t)c->max_seqs * cf.vocab)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_seq, wb)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_pos, wb)) != hipSuccess) return bad(e);
-  if ((e = dalloc(&c->d_tok, wb)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->d_tok, c->rows)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_pick, wb)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_rng, 4 * wb)) != hipSuccess) return bad(e);
   if (c->mode != ANA_EXACT_FP32 &&
@@ -339,19 +342,23 @@ static int norm_gemv(ana_ctx* c, const float* X, const float* g, GemvArgs a, uin
   return ANA_OK;
 }
 
-// every layer for B rows of X (embedded already). Row b is sequence seq[b]
-// at position pos[b] (device arrays), or, for a chunk (seq == nullptr), one
-// sequence seq0 at positions pos0 + b.
+// A prefill chunk of one sequence inside a batch of rows: sequence seq at
+// positions pos0.., rows row0 .. row0 + T of the workspaces.
+struct Seg {
+  uint32_t seq, pos0, row0, T;
+};
+
+// every layer for B rows of X (embedded already). Decode (segs == nullptr):
+// row b is sequence seq[b] at position pos[b] (device arrays). Prefill:
+// the rows are chunks of several sequences (segs); the products run over all
+// B rows at once (row-wise the same as one chunk at a time), the GLA and
+// attention per chunk.
 static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_t* pos,
-                      uint32_t seq0, uint32_t pos0) {
+                      const std::vector<Seg>* segs) {
   const ana_config& cf = c->cfg;
   const uint32_t d = cf.d, f = cf.f;
   const float* W = c->W;
-  const bool chunk = seq == nullptr;
-  const bool fresh = chunk && (uint64_t)pos0 + B <= cf.ctx;
-  // a fast mode's prefill chunk of more than kSmallB rows: matrix-core
-  // products, the closed-form GLA chunk and the split attention
-  const bool fast_chunk = chunk && fast_mode(c) && B > kSmallB;
+  const bool chunk = segs != nullptr;
   for (uint32_t l = 0; l < cf.layers; l++) {
     const Blk& b = c->blk[l];
     // norm, then q|k|v (+ the gate's z): dd.gla / dd.sm `pre`
@@ -361,24 +368,29 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
       g.nseg = 2;
     }
     if (int r = norm_gemv(c, c->X, W + b.ra, g, ANA_K_GEMV, chunk)) return r;
-    if (b.gla) {
-      if (chunk && fast_chunk) {
-        HIPCHK(c, launch_gla_scan(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr,
-                                  c->state + (uint64_t)seq0 * c->seq_stride + c->layer_off[l], c->O,
-                                  c->d_gla, d, cf.heads, cf.rglru, B, c->st));
-      } else if (chunk) {
-        HIPCHK(c, launch_gla_chunk(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr,
-                                   c->state + (uint64_t)seq0 * c->seq_stride + c->layer_off[l], c->O,
-                                   d, cf.heads, cf.rglru, B, c->st));
-      } else {
-        // S read and written once per sequence, q|k|v|z in, o out
-        ProfScope ps(c, ANA_K_GLA, (double)B * (8.0 * cf.heads * (d / cf.heads) * (d / cf.heads) + 4.0 * 5 * d));
-        if (fast_path(c, B))
-          HIPCHK(c, launch_gla_fast(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), seq,
-                                    c->O, d, cf.heads, cf.rglru, B, c->st));
+    if (b.gla && !chunk) {
+      // S read and written once per sequence, q|k|v|z in, o out
+      ProfScope ps(c, ANA_K_GLA, (double)B * (8.0 * cf.heads * (d / cf.heads) * (d / cf.heads) + 4.0 * 5 * d));
+      if (fast_path(c, B))
+        HIPCHK(c, launch_gla_fast(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), seq,
+                                  c->O, d, cf.heads, cf.rglru, B, c->st));
+      else
+        HIPCHK(c, launch_gla_step(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), seq,
+                                  c->O, d, cf.heads, cf.rglru, B, c->st));
+    } else if (b.gla) {
+      for (const Seg& sg : *segs) {
+        // a fast mode's chunk of more than kSmallB rows: the closed-form scan
+        const bool fast_chunk = fast_mode(c) && sg.T > kSmallB;
+        float* S = c->state + (uint64_t)sg.seq * c->seq_stride + c->layer_off[l];
+        const float* qkv = c->QKV + (size_t)sg.row0 * 3 * d;
+        const float* z = c->Z + (size_t)sg.row0 * d;
+        float* o = c->O + (size_t)sg.row0 * d;
+        if (fast_chunk)
+          HIPCHK(c, launch_gla_scan(qkv, z, cf.rglru ? W + b.lam : nullptr, S, o, c->d_gla, d, cf.heads,
+                                    cf.rglru, sg.T, c->st));
         else
-          HIPCHK(c, launch_gla_step(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), seq,
-                                    c->O, d, cf.heads, cf.rglru, B, c->st));
+          HIPCHK(c, launch_gla_chunk(qkv, z, cf.rglru ? W + b.lam : nullptr, S, o, d, cf.heads, cf.rglru,
+                                     sg.T, c->st));
       }
     } else {
       AttnArgs a{};
@@ -398,24 +410,31 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
         } else {
           HIPCHK(c, launch_attn(a, c->st));
         }
-      } else if (fresh) {
-        // before the ring wraps: every row's write, then every row's
-        // attention (dd.sm.writes, then dd.sm.rows)
-        a.QKV = c->QKV; a.O = c->O; a.B = B;
-        a.seq = nullptr; a.seq0 = seq0; a.pos = nullptr; a.pos0 = pos0; a.write_kv = 0;
-        HIPCHK(c, launch_kv_write(a, c->st));
-        if (fast_chunk) {
-          a.part = c->d_part;
-          HIPCHK(c, launch_attn_fast(a, c->st));
-        } else {
-          HIPCHK(c, launch_attn(a, c->st));
-        }
       } else {
-        // past the wrap: each token's write and attention in turn (dd.sm.toks)
-        for (uint32_t t = 0; t < B; t++) {
-          a.QKV = c->QKV + (size_t)t * 3 * d; a.O = c->O + (size_t)t * d;
-          a.seq = nullptr; a.seq0 = seq0; a.pos = nullptr; a.pos0 = pos0 + t; a.B = 1; a.write_kv = 1;
-          HIPCHK(c, launch_attn(a, c->st));
+        for (const Seg& sg : *segs) {
+          const bool fresh = (uint64_t)sg.pos0 + sg.T <= cf.ctx;
+          const bool fast_chunk = fast_mode(c) && sg.T > kSmallB;
+          if (fresh) {
+            // before the ring wraps: every row's write, then every row's
+            // attention (dd.sm.writes, then dd.sm.rows)
+            a.QKV = c->QKV + (size_t)sg.row0 * 3 * d; a.O = c->O + (size_t)sg.row0 * d; a.B = sg.T;
+            a.seq = nullptr; a.seq0 = sg.seq; a.pos = nullptr; a.pos0 = sg.pos0; a.write_kv = 0;
+            HIPCHK(c, launch_kv_write(a, c->st));
+            if (fast_chunk) {
+              a.part = c->d_part;
+              HIPCHK(c, launch_attn_fast(a, c->st));
+            } else {
+              HIPCHK(c, launch_attn(a, c->st));
+            }
+          } else {
+            // past the wrap: each token's write and attention in turn (dd.sm.toks)
+            for (uint32_t t = 0; t < sg.T; t++) {
+              a.QKV = c->QKV + (size_t)(sg.row0 + t) * 3 * d; a.O = c->O + (size_t)(sg.row0 + t) * d;
+              a.seq = nullptr; a.seq0 = sg.seq; a.pos = nullptr; a.pos0 = sg.pos0 + t; a.B = 1;
+              a.write_kv = 1;
+              HIPCHK(c, launch_attn(a, c->st));
+            }
+          }
         }
       }
     }
@@ -483,9 +502,66 @@ extern "C" int ana_feed(ana_ctx* c, uint32_t n, const uint32_t* seq, const uint3
   HIPCHK(c, hipMemcpyAsync(c->d_tok, tok, 4 * n, hipMemcpyHostToDevice, c->st));
   HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, n, c->X, nullptr, c->st));
   if (c->prof) c->attn_bytes = attn_bytes_of(c, pos, n, 0);
-  if (int r = run_layers(c, n, c->d_seq, c->d_pos, 0, 0)) return r;
+  if (int r = run_layers(c, n, c->d_seq, c->d_pos, nullptr)) return r;
   HIPCHK(c, launch_scatter_rows(c->X, c->d_seq, n, c->cfg.d, c->xs, c->st));
   HIPCHK(c, hipStreamSynchronize(c->st));
+  return ANA_OK;
+}
+
+// dd.feeds (bend/Dense/Decode.bend:561-639) for n sequences at once. Step j
+// feeds tokens [jC, (j+1)C) of every sequence that has them (C the prefill
+// chunk): their rows go through each product together, the GLA and the
+// attention chunk by chunk, so each sequence ends as n separate dd.feeds
+// would leave it (bit for bit in ANA_EXACT_FP32: products are row-wise the
+// same for any number of rows).
+static int feeds_n(ana_ctx* c, const char* fn, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+                   const uint32_t* len, const uint32_t* toks) {
+  if (n == 0) return ANA_OK;
+  if (!seq || !pos || !len || !toks) return fail(c, ANA_EINVAL, "%s: null argument", fn);
+  std::vector<uint8_t> seen(c->max_seqs, 0);
+  std::vector<uint64_t> off(n);
+  uint64_t total = 0;
+  uint32_t maxlen = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    if (seq[i] >= c->max_seqs) return fail(c, ANA_EINVAL, "%s: sequence %u outside 0..%u", fn, seq[i], c->max_seqs - 1);
+    if (seen[seq[i]]++) return fail(c, ANA_EINVAL, "%s: sequence %u listed twice", fn, seq[i]);
+    off[i] = total;
+    total += len[i];
+    maxlen = std::max(maxlen, len[i]);
+  }
+  for (uint64_t i = 0; i < total; i++)
+    if (toks[i] >= c->cfg.vocab) return fail(c, ANA_EINVAL, "%s: token %u outside the vocabulary", fn, toks[i]);
+  HIPCHK(c, hipSetDevice(c->device));
+  const uint32_t d = c->cfg.d;
+  std::vector<Seg> segs;
+  std::vector<uint32_t> rows;
+  auto flush = [&]() -> int {
+    if (segs.empty()) return ANA_OK;
+    const uint32_t M = (uint32_t)rows.size();
+    HIPCHK(c, hipMemcpyAsync(c->d_tok, rows.data(), 4 * (size_t)M, hipMemcpyHostToDevice, c->st));
+    HIPCHK(c, launch_embed(c->W, c->d_tok, d, M, c->X, nullptr, c->st));
+    if (int r = run_layers(c, M, nullptr, nullptr, &segs)) return r;
+    for (const Seg& sg : segs)
+      HIPCHK(c, hipMemcpyAsync(c->xs + (uint64_t)sg.seq * d, c->X + (uint64_t)(sg.row0 + sg.T - 1) * d,
+                               4 * (size_t)d, hipMemcpyDeviceToDevice, c->st));
+    // the host rows are read by the copy above before they change
+    HIPCHK(c, hipStreamSynchronize(c->st));
+    segs.clear();
+    rows.clear();
+    return ANA_OK;
+  };
+  for (uint32_t t0 = 0; t0 < maxlen; t0 += c->chunk) {
+    for (uint32_t i = 0; i < n; i++) {
+      if (len[i] <= t0) continue;
+      const uint32_t T = std::min(c->chunk, len[i] - t0);
+      if (rows.size() + T > c->rows)
+        if (int r = flush()) return r;
+      segs.push_back(Seg{seq[i], pos[i] + t0, (uint32_t)rows.size(), T});
+      rows.insert(rows.end(), toks + off[i] + t0, toks + off[i] + t0 + T);
+    }
+    // the next step's chunks start from the states this step leaves
+    if (int r = flush()) return r;
+  }
   return ANA_OK;
 }
 
@@ -494,19 +570,13 @@ extern "C" int ana_feeds(ana_ctx* c, uint32_t seq, uint32_t pos, const uint32_t*
   if (seq >= c->max_seqs) return fail(c, ANA_EINVAL, "ana_feeds: sequence %u outside 0..%u", seq, c->max_seqs - 1);
   if (len == 0) return ANA_OK;
   if (!toks) return fail(c, ANA_EINVAL, "ana_feeds: null tokens");
-  for (uint32_t i = 0; i < len; i++)
-    if (toks[i] >= c->cfg.vocab) return fail(c, ANA_EINVAL, "ana_feeds: token %u outside the vocabulary", toks[i]);
-  HIPCHK(c, hipSetDevice(c->device));
-  for (uint32_t t0 = 0; t0 < len; t0 += c->chunk) {
-    const uint32_t T = std::min(c->chunk, len - t0);
-    HIPCHK(c, hipMemcpyAsync(c->d_tok, toks + t0, 4 * T, hipMemcpyHostToDevice, c->st));
-    HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, T, c->X, nullptr, c->st));
-    if (int r = run_layers(c, T, nullptr, nullptr, seq, pos + t0)) return r;
-    HIPCHK(c, hipMemcpyAsync(c->xs + (uint64_t)seq * c->cfg.d, c->X + (uint64_t)(T - 1) * c->cfg.d,
-                             4 * c->cfg.d, hipMemcpyDeviceToDevice, c->st));
-  }
-  HIPCHK(c, hipStreamSynchronize(c->st));
-  return ANA_OK;
+  return feeds_n(c, "ana_feeds", 1, &seq, &pos, &len, toks);
+}
+
+extern "C" int ana_feeds_n(ana_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+                           const uint32_t* len, const uint32_t* toks) {
+  if (!c) return ANA_EINVAL;
+  return feeds_n(c, "ana_feeds_n", n, seq, pos, len, toks);
 }
 
 static int head_of(ana_ctx* c, const char* fn, uint32_t n, const uint32_t* seq) {
@@ -573,7 +643,7 @@ extern "C" int ana_pick(ana_ctx* c, uint32_t n, const uint32_t* seq, const ana_s
 // layer, the head, the pick, then advance (pos + 1, tok = pick, record)
 static int gen_step(ana_ctx* c, uint32_t n, uint32_t steps, const PickArgs& pa, bool greedy) {
   HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, n, c->X, c->d_amax, c->st));
-  if (int r = run_layers(c, n, c->d_seq, c->d_pos, 0, 0)) return r;
+  if (int r = run_layers(c, n, c->d_seq, c->d_pos, nullptr)) return r;
   if (int r = run_head(c, c->X, n, greedy)) return r;
   if (!greedy) {
     ProfScope ps(c, ANA_K_PICK, 4.0 * n * c->cfg.vocab);

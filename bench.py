@@ -68,16 +68,17 @@ MODES = {"exact": ana_amd.EXACT_FP32, "fast_fp32": ana_amd.FAST_FP32, "bf16": an
 
 
 def run_batch(path: str, c: cf.Config, B: int, prompt: int, warmup: int, steps: int, prof_steps: int,
-              mode: str = "exact"):
+              mode: str = "exact", chunk: int = 64):
     seqs = list(range(B))
-    with ana_amd.Decoder(path, max_seqs=B, prefill_chunk=64, numerics=MODES[mode]) as dec:
+    with ana_amd.Decoder(path, max_seqs=B, prefill_chunk=chunk, numerics=MODES[mode]) as dec:
+        prs = [ckpt.prompt(b, prompt, c.vocab) for b in seqs]
+        first = [int(pr[-1]) for pr in prs]
+        pos = [prompt - 1] * B
         t = time.perf_counter()
-        first, pos = [], []
-        for b in seqs:
-            pr = ckpt.prompt(b, prompt, c.vocab)
-            dec.feeds(b, 0, pr[:-1])
-            first.append(int(pr[-1]))
-            pos.append(prompt - 1)
+        if B == 1:
+            dec.feeds(0, 0, prs[0][:-1])
+        else:
+            dec.feeds_n(seqs, [0] * B, [pr[:-1] for pr in prs])
         t_pre = time.perf_counter() - t
         log(f"B={B} {mode}: prefill {B}x{prompt - 1} tokens in {t_pre:.3f}s")
         tok = np.array(first, dtype=np.uint32)
@@ -164,6 +165,7 @@ def main() -> int:
                     help="the mode `value` is measured in")
     ap.add_argument("--others", type=int, default=1, help="also measure B=1 in the other modes (1/0)")
     ap.add_argument("--b64", type=int, default=1, help="also measure B=64 (1/0)")
+    ap.add_argument("--prefill", type=int, default=1, help="also measure B=64 x 512 prefill (1/0)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--ckpt", default=os.environ.get("ANA_BENCH_CKPT", "/tmp/ana_bench_fp100m.ftc2"))
     a = ap.parse_args()
@@ -202,6 +204,29 @@ def main() -> int:
             extra[key] = {k: round(r64[k], 3) for k in ("tok_s", "ms_per_step", "step_gbs", "prefill_tok_s")}
             extra[key]["workload"] = ("B=64, 128-token prompts (chunked prefill, one sequence at a "
                                       "time), 32 greedy steps at positions 128+; " + NUMERICS[m])
+    if a.prefill:
+        # B=64 prefill on the matrix cores: 64 prompts of 512 tokens through
+        # ana_feeds_n at chunk 128 (8192 rows a product), bf16 weights
+        for m in ("bf16", "fast_fp32"):
+            with ana_amd.Decoder(path, max_seqs=64, prefill_chunk=128, numerics=MODES[m]) as dec:
+                prs = [ckpt.prompt(1000 + b, 512, c.vocab) for b in range(64)]
+                dec.feeds_n(list(range(64)), [0] * 64, [pr[:64] for pr in prs])   # warm-up
+                for b in range(64):
+                    dec.reset(b)
+                t = time.perf_counter()
+                dec.feeds_n(list(range(64)), [0] * 64, prs)
+                dt = time.perf_counter() - t
+            ntok = 64 * 512
+            flops = 2.0 * (c.params - c.vocab * c.d) * ntok
+            peak = 2500.0 if m == "bf16" else 157.3
+            extra[f"prefill_b64_{m}"] = {
+                "tok_s": round(ntok / dt, 1), "seconds": round(dt, 4),
+                "tflops": round(flops / dt / 1e12, 2), "peak_tflops": peak,
+                "frac": round(flops / dt / 1e12 / peak, 4),
+                "workload": "64 prompts x 512 tokens through ana_feeds_n, chunk 128; flops = 2 x "
+                            "(P - v d) per token (the products; GLA and attention not counted)",
+            }
+            log(f"prefill B=64 x 512 {m}: {ntok / dt:.0f} tok/s")
     cpu = cpu_baseline(path, c, a.cpu_seconds) if a.cpu_seconds > 0 else None
     kern = {k: {"launches": v[0], "ms": round(v[1], 4), "gb": round(v[2] / 1e9, 4)}
             for k, v in r1["stats"].items()}

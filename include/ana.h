@@ -97,6 +97,15 @@ int ana_feed(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, const uint32_
  * residual row are bit-identical to len ana_feed calls. */
 int ana_feeds(struct ana_ctx* ctx, uint32_t seq, uint32_t pos, const uint32_t* toks, uint32_t len);
 
+/* dd.feeds for n sequences at once (distinct seq[i]): sequence seq[i] takes
+ * len[i] tokens from pos[i]; toks holds the sequences' tokens one after
+ * another. A chunk step feeds every sequence's next chunk together, so the
+ * products run over all their rows at once (the reference prefills one
+ * sequence per process and has no counterpart; its meaning is n ana_feeds
+ * calls, and in ANA_EXACT_FP32 the states are bit-identical to them). */
+int ana_feeds_n(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+                const uint32_t* len, const uint32_t* toks);
+
 /* The head on each listed sequence's last fed token: n x vocab floats,
  * dd.logits (bend/Dense/Decode.bend:641-646). */
 int ana_logits(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, float* out);

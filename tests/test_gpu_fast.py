@@ -193,3 +193,28 @@ def test_fast_prefill(oracle, small_ckpt, noarms_ckpt, mode, arms, chunk):
             worst = max(worst, rel_err(dec.logits([0])[0], st.logits()))
     print(f"worst relative error {worst:.3e}", flush=True)
     assert worst <= TOL[mode], worst
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_fast_feeds_n(oracle, small_ckpt, mode):
+    """ana_feeds_n in a fast mode: five ragged prompts prefilled together
+    (matrix-core products over all their rows), then a decode step each;
+    logits against the oracle."""
+    print(f"case fast feeds_n mode {mode}", flush=True)
+    m = oracle.Model(small_ckpt)
+    seqs, lens = [3, 0, 2, 4, 1], [40, 3, 17, 70, 9]
+    rng = np.random.default_rng(22)
+    toks = [rng.integers(0, m.vocab, size=n + 1).astype(np.uint32) for n in lens]
+    worst = 0.0
+    with ana_amd.Decoder(small_ckpt, max_seqs=5, prefill_chunk=32, numerics=mode) as dec:
+        dec.feeds_n(seqs, [0] * 5, [t[:-1] for t in toks])
+        for i, s in enumerate(seqs):
+            dec.feed([s], [lens[i]], [int(toks[i][-1])])
+        got = dec.logits(seqs)
+    for i in range(5):
+        st = oracle.State(m)
+        for p, t in enumerate(toks[i]):
+            st.feed(p, int(t))
+        worst = max(worst, rel_err(got[i], st.logits()))
+    print(f"worst relative error {worst:.3e}", flush=True)
+    assert worst <= TOL[mode], worst

@@ -231,3 +231,33 @@ def test_115m_shape(oracle, tmp_path):
         want.append(t)
         pos += 1
     assert list(out[0]) == want
+
+
+@pytest.mark.parametrize("name", list(CFGS))
+def test_feeds_n_is_feeds(oracle, ckpts, name):
+    """ana_feeds_n: five sequences of ragged lengths (one across the ring
+    wrap, one starting mid-sequence) prefilled together at chunk 16 leave
+    each sequence's states and logits bit for bit as the oracle fed one
+    token at a time."""
+    path = ckpts[name]
+    print(f"case feeds_n {name}", flush=True)
+    m = oracle.Model(path)
+    seqs, pos, lens = [4, 0, 2, 5, 1], [0, 0, 3, 0, 60], [40, 3, 17, 70, 9]
+    rng = np.random.default_rng(21)
+    toks = [rng.integers(0, m.vocab, size=n).astype(np.uint32) for n in lens]
+    pre = [rng.integers(0, m.vocab, size=p).astype(np.uint32) for p in pos]
+    with ana_amd.Decoder(path, max_seqs=6, prefill_chunk=16) as dec:
+        for s, p, pr in zip(seqs, pos, pre):
+            if p:
+                dec.feeds(s, 0, pr)
+        dec.feeds_n(seqs, pos, toks)
+        got = dec.logits(seqs)
+        for i, s in enumerate(seqs):
+            st = oracle.State(m)
+            for p, t in enumerate(pre[i]):
+                st.feed(p, int(t))
+            for k, t in enumerate(toks[i]):
+                st.feed(pos[i] + k, int(t))
+            assert np.array_equal(bits(got[i]), bits(st.logits())), (i, s)
+            for l in range(m.layers):
+                assert np.array_equal(bits(dec.state(s, l)), bits(st.layer(l))), (i, l)
