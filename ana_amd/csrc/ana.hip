@@ -314,6 +314,7 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
     if (c->Wh) by -= 2.0 * (g.seg[0].rows + (g.nseg > 1 ? g.seg[1].rows : 0)) * g.K;
     ProfScope ps(c, kind, by, true);
     if (small) return launch_gemv_fast(g, c->st, ps.start(), ps.stop());
+    if (g.B >= 128) return launch_gemm_big(g, c->st, ps.start(), ps.stop());
     return launch_gemm_mfma(g, c->st, ps.start(), ps.stop());
   }
   ProfScope ps(c, kind, gemv_bytes(g0), true);

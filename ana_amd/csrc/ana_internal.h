@@ -248,6 +248,9 @@ hipError_t launch_gla_scan(const float* QKV, const float* Z, const float* lam, f
 // when Wh0 is set, else fp32; no argmax epilogue
 hipError_t launch_gemm_mfma(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nullptr,
                             hipEvent_t e1 = nullptr);
+// the same for 128 rows or more, 128 x 128 tiles
+hipError_t launch_gemm_big(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nullptr,
+                           hipEvent_t e1 = nullptr);
 size_t attn_fast_part_floats(uint32_t B, uint32_t heads, uint32_t ctx, uint32_t hd);
 hipError_t launch_zero_u32(uint32_t* p, uint32_t n, hipStream_t st);
 hipError_t launch_zero_u64(unsigned long long* p, uint32_t n, hipStream_t st);

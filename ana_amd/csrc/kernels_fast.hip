@@ -1147,3 +1147,261 @@ hipError_t launch_gla_scan(const float* QKV, const float* Z, const float* lam, f
 }
 
 }  // namespace ana
+
+namespace ana {
+
+// ------------------------------------------------------------------ large-M products on MFMA
+
+// Y[m][n] = sum_k X[m][k] W[n][k] for M >= 128 (prefill batches): a 128 x
+// 128 tile per workgroup, four waves in 2 x 2 each computing 64 x 64 as
+// 4 x 4 MFMA 16 x 16 tiles. K goes in stages of BK through two LDS buffers,
+// the next stage's global loads in registers while the current one is
+// multiplied. ANA_BF16: v_mfma_f32_16x16x32_bf16 on the bf16 weights with
+// each activation as a bf16 head and remainder (two products a step);
+// ANA_FAST_FP32: v_mfma_f32_16x16x4f32. Norm, residual and SiLU as in
+// k_gemm_mfma (SiLU: tile rows 0..63 gate j, 64..127 up j).
+template <int WT>
+__global__ __launch_bounds__(256) void k_gemm_big(GemvArgs a) {
+  constexpr int BM = 128, BN = 128, BK = WT == 1 ? 32 : 16;
+  constexpr int AP = BK + 8;                      // LDS row pitch (elements)
+  using E = typename std::conditional<WT == 1, __bf16, float>::type;
+  __shared__ __align__(16) E As[2][BM][AP];
+  __shared__ __align__(16) __bf16 Al[WT == 1 ? 2 : 1][WT == 1 ? BM : 1][WT == 1 ? AP : 8];
+  __shared__ __align__(16) E Bs[2][BN][AP];
+  __shared__ float rsc[BM];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t wm = wv >> 1, wn = wv & 1;       // the wave's 64 x 64 block
+  const uint32_t m0 = blockIdx.y * BM;
+  const uint32_t nb = min((uint32_t)BM, a.B - m0);
+  const uint32_t K = a.K, nst = (K + BK - 1) / BK;
+  const Segs sgs(a);
+  const bool norm = a.ng != nullptr;
+  // staging: A (fp32 activations) BM x BK, B (weights) BN x BK
+  constexpr int AF4 = BM * BK / 4 / 256;          // float4 of A a thread (bf16: 4, f32: 2)
+  constexpr int BV = WT == 1 ? BN * BK / 8 / 256 : BN * BK / 4 / 256;  // 16-byte pieces of B
+  const float* asrc[AF4];
+  uint32_t am_[AF4], ak_[AF4];
+#pragma unroll
+  for (int j = 0; j < AF4; j++) {
+    const uint32_t i = tid + 256 * j, m = i / (BK / 4), k4 = i % (BK / 4);
+    am_[j] = m;
+    ak_[j] = 4 * k4;
+    asrc[j] = a.X + (size_t)(m0 + (m < nb ? m : 0)) * a.ldx;
+  }
+  const float* bsrcf[BV];
+  const uint16_t* bsrch[BV];
+  uint32_t bn_[BV], bk_[BV];
+#pragma unroll
+  for (int j = 0; j < BV; j++) {
+    const uint32_t i = tid + 256 * j;
+    const uint32_t n = WT == 1 ? i / (BK / 8) : i / (BK / 4);
+    const uint32_t k = WT == 1 ? 8 * (i % (BK / 8)) : 4 * (i % (BK / 4));
+    bn_[j] = n;
+    bk_[j] = k;
+    const float* w;
+    uint32_t sg, lr;
+    const bool ok = sgs.row(BN, blockIdx.x, n, &w, &sg, &lr);
+    bsrcf[j] = ok ? w : sgs.W0;
+    bsrch[j] = ok ? (sg ? a.Wh1 : a.Wh0) + (size_t)lr * K : a.Wh0;
+  }
+  float4 ar[AF4];
+  uint4 brh[BV];
+  float4 brf[BV];
+  auto load = [&](uint32_t s) {
+    const uint32_t q0 = s * BK;
+#pragma unroll
+    for (int j = 0; j < AF4; j++) {
+      const uint32_t q = q0 + ak_[j];
+      ar[j] = *reinterpret_cast<const float4*>(asrc[j] + (q < K ? q : 0));
+    }
+#pragma unroll
+    for (int j = 0; j < BV; j++) {
+      const uint32_t q = q0 + bk_[j];
+      if constexpr (WT == 1) brh[j] = *reinterpret_cast<const uint4*>(bsrch[j] + (q < K ? q : 0));
+      else brf[j] = *reinterpret_cast<const float4*>(bsrcf[j] + (q < K ? q : 0));
+    }
+  };
+  float ss[AF4];
+#pragma unroll
+  for (int j = 0; j < AF4; j++) ss[j] = 0.0f;
+  auto store = [&](int buf, uint32_t s) {
+    const uint32_t q0 = s * BK;
+#pragma unroll
+    for (int j = 0; j < AF4; j++) {
+      const uint32_t q = q0 + ak_[j];
+      float4 x = ar[j];
+      if (q >= K || am_[j] >= nb) x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (norm) {
+        ss[j] += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+        const float4 g = *reinterpret_cast<const float4*>(a.ng + (q < K ? q : 0));
+        x.x *= g.x;
+        x.y *= g.y;
+        x.z *= g.z;
+        x.w *= g.w;
+      }
+      E* dst = &As[buf][am_[j]][ak_[j]];
+      dst[0] = (E)x.x;
+      dst[1] = (E)x.y;
+      dst[2] = (E)x.z;
+      dst[3] = (E)x.w;
+      if constexpr (WT == 1) {
+        __bf16* lo = &Al[buf][am_[j]][ak_[j]];
+        lo[0] = (__bf16)(x.x - (float)dst[0]);
+        lo[1] = (__bf16)(x.y - (float)dst[1]);
+        lo[2] = (__bf16)(x.z - (float)dst[2]);
+        lo[3] = (__bf16)(x.w - (float)dst[3]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < BV; j++) {
+      const uint32_t q = q0 + bk_[j];
+      if constexpr (WT == 1) {
+        uint4 w = brh[j];
+        if (q >= K) w = make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4*>(&Bs[buf][bn_[j]][bk_[j]]) = w;
+      } else {
+        float4 w = brf[j];
+        if (q >= K) w = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        *reinterpret_cast<float4*>(&Bs[buf][bn_[j]][bk_[j]]) = w;
+      }
+    }
+  };
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t r16 = lane & 15, g4 = lane >> 4;
+  load(0);
+  store(0, 0);
+  __syncthreads();
+  for (uint32_t s = 0; s < nst; s++) {
+    const int buf = s & 1;
+    if (s + 1 < nst) load(s + 1);
+    if constexpr (WT == 1) {
+      bf16x8_t bfr[4], ah[4], al[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[buf][wn * 64 + 16 * j + r16][8 * g4]);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        ah[i] = *reinterpret_cast<const bf16x8_t*>(&As[buf][wm * 64 + 16 * i + r16][8 * g4]);
+        al[i] = *reinterpret_cast<const bf16x8_t*>(&Al[buf][wm * 64 + 16 * i + r16][8 * g4]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bfr[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bfr[j], acc[i][j], 0, 0, 0);
+        }
+    } else {
+      float4 bfr[4], afr[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const float4*>(&Bs[buf][wn * 64 + 16 * j + r16][4 * g4]);
+#pragma unroll
+      for (int i = 0; i < 4; i++) afr[i] = *reinterpret_cast<const float4*>(&As[buf][wm * 64 + 16 * i + r16][4 * g4]);
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(afr[i].x, bfr[j].x, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(afr[i].y, bfr[j].y, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(afr[i].z, bfr[j].z, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(afr[i].w, bfr[j].w, acc[i][j], 0, 0, 0);
+        }
+    }
+    if (s + 1 < nst) store(buf ^ 1, s + 1);
+    __syncthreads();
+  }
+  // rows' norm scales: the threads of a row (BK / 4 / AF4... all threads
+  // staging row m) add their sums of squares in LDS
+  if (norm) {
+    if (tid < BM) rsc[tid] = 0.0f;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < AF4; j++) atomicAdd(&rsc[am_[j]], ss[j]);
+    __syncthreads();
+    if (tid < BM) rsc[tid] = 1.0f / sqrtf(rsc[tid] / (float)K + 1.0e-5f);
+    __syncthreads();
+  }
+  // results: tile (i, j) of the wave holds rows wm*64 + 16i + 4*g4 + r,
+  // column wn*64 + 16j + r16
+  if (a.mode == GM_SILU) {
+    // up columns (wn = 1) through LDS to the gate columns (wn = 0), one
+    // 64-row half at a time (64 x 64 floats fit in Bs in both modes)
+    float* up = reinterpret_cast<float*>(&Bs[0][0][0]);
+    static_assert(sizeof(Bs) >= 64 * 64 * sizeof(float), "exchange buffer");
+    for (uint32_t half = 0; half < 2; half++) {
+      if (wn == 1 && wm == half) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              const uint32_t ml = 16 * i + 4 * g4 + r, n = 16 * j + r16;
+              float y = acc[i][j][r];
+              if (norm) y *= rsc[wm * 64 + ml];
+              up[ml * 64 + n] = y;
+            }
+      }
+      __syncthreads();
+      if (wn == 0 && wm == half) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const uint32_t n = 16 * j + r16;
+          const float* w_;
+          uint32_t sg, lr;
+          if (!sgs.row(BN, blockIdx.x, n, &w_, &sg, &lr)) continue;
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              const uint32_t ml = 16 * i + 4 * g4 + r, m = wm * 64 + ml;
+              if (m >= nb) continue;
+              float y = acc[i][j][r];
+              if (norm) y *= rsc[m];
+              a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = fast_silu(y) * up[ml * 64 + n];
+            }
+        }
+      }
+      __syncthreads();
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t n = wn * 64 + 16 * j + r16;
+    const float* w_;
+    uint32_t sg, lr;
+    if (!sgs.row(BN, blockIdx.x, n, &w_, &sg, &lr)) continue;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r;
+        if (m >= nb) continue;
+        float y = acc[i][j][r];
+        if (norm) y *= rsc[m];
+        if (a.mode == GM_RESID) y = a.R[(size_t)(m0 + m) * a.ldr + lr] + y;
+        if (sg) a.seg[1].Y[(size_t)(m0 + m) * a.seg[1].ldy + lr] = y;
+        else a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = y;
+      }
+  }
+}
+
+hipError_t launch_gemm_big(const GemvArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  if (a.amax || (a.K & 7) || a.B == 0) return hipErrorInvalidValue;
+  const bool bf = a.Wh0 != nullptr;
+  if (bf && a.nseg > 1 && !a.Wh1) return hipErrorInvalidValue;
+  const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
+                                          : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
+  const uint32_t per = a.mode == GM_SILU ? 64 : 128;
+  const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
+  dim3 grid(tiles, (a.B + 127) / 128);
+  if (bf) ANA_LAUNCH_F((k_gemm_big<1>), grid, dim3(256), 0, st, e0, e1, a);
+  else ANA_LAUNCH_F((k_gemm_big<0>), grid, dim3(256), 0, st, e0, e1, a);
+  return hipGetLastError();
+}
+
+}  // namespace ana

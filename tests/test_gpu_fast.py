@@ -196,22 +196,28 @@ def test_fast_prefill(oracle, small_ckpt, noarms_ckpt, mode, arms, chunk):
 
 
 @pytest.mark.parametrize("mode", MODES)
-def test_fast_feeds_n(oracle, small_ckpt, mode):
-    """ana_feeds_n in a fast mode: five ragged prompts prefilled together
-    (matrix-core products over all their rows), then a decode step each;
-    logits against the oracle."""
-    print(f"case fast feeds_n mode {mode}", flush=True)
+@pytest.mark.parametrize("shape", ["ragged5", "wide6"])
+def test_fast_feeds_n(oracle, small_ckpt, mode, shape):
+    """ana_feeds_n in a fast mode: ragged prompts prefilled together
+    (matrix-core products over all their rows: 93 rows a step, or 288 for
+    the 128 x 128 tiles), then a decode step each; logits against the
+    oracle."""
+    print(f"case fast feeds_n {shape} mode {mode}", flush=True)
     m = oracle.Model(small_ckpt)
-    seqs, lens = [3, 0, 2, 4, 1], [40, 3, 17, 70, 9]
+    if shape == "ragged5":
+        seqs, lens, chunk = [3, 0, 2, 4, 1], [40, 3, 17, 70, 9], 32
+    else:
+        seqs, lens, chunk = [5, 0, 2, 4, 1, 3], [60, 100, 49, 77, 90, 63], 48
+    n = len(seqs)
     rng = np.random.default_rng(22)
-    toks = [rng.integers(0, m.vocab, size=n + 1).astype(np.uint32) for n in lens]
+    toks = [rng.integers(0, m.vocab, size=k + 1).astype(np.uint32) for k in lens]
     worst = 0.0
-    with ana_amd.Decoder(small_ckpt, max_seqs=5, prefill_chunk=32, numerics=mode) as dec:
-        dec.feeds_n(seqs, [0] * 5, [t[:-1] for t in toks])
+    with ana_amd.Decoder(small_ckpt, max_seqs=n, prefill_chunk=chunk, numerics=mode) as dec:
+        dec.feeds_n(seqs, [0] * n, [t[:-1] for t in toks])
         for i, s in enumerate(seqs):
             dec.feed([s], [lens[i]], [int(toks[i][-1])])
         got = dec.logits(seqs)
-    for i in range(5):
+    for i in range(n):
         st = oracle.State(m)
         for p, t in enumerate(toks[i]):
             st.feed(p, int(t))
