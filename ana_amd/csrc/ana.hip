@@ -44,6 +44,13 @@ struct ana_ctx {
   float *d_ss = nullptr, *d_pm = nullptr; // split attention scratch
   float* d_part = nullptr;           // fast attention's per-split partials
   float* d_gla = nullptr;            // fast prefill's GLA scan scratch
+  GlaScratch gla{};                  // its regions
+  GlaSub* d_gtab = nullptr;          // a prefill step's sub-chunk table
+  uint32_t *d_rseq = nullptr, *d_rpos = nullptr;  // a prefill step's per-row sequence, position
+  uint32_t seg_cap = 1, gsub_cap = 1; // chunks a prefill step holds; table entries
+  // host copies of the step tables, kept until the step's synchronize
+  std::vector<GlaSub> h_gtab;
+  std::vector<uint32_t> h_rseq, h_rpos;
   size_t out_cap = 0;
   std::string err;
   // ana_generate's decode step captured as HIP graphs, replayed per step:
@@ -138,7 +145,7 @@ static void release(ana_ctx* c) {
   if (c->gexec_n) (void)hipGraphExecDestroy(c->gexec_n);
   void* ps[] = {c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
-                c->d_ss, c->d_pm};
+                c->d_ss, c->d_pm, c->d_gtab, c->d_rseq, c->d_rpos};
   for (void* p : ps)
     if (p) (void)hipFree(p);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
@@ -198,6 +205,10 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   c->wb = std::max(c->max_seqs, c->chunk);
   // a batched prefill's step holds every sequence's chunk, up to 8192 rows
   c->rows = std::max<uint32_t>(c->wb, (uint32_t)std::min<uint64_t>((uint64_t)c->max_seqs * c->chunk, 8192));
+  // a step holds at most kMaxSegs chunks (each at least one row), and so
+  // at most rows / kGlaSub + seg_cap sub-chunks
+  c->seg_cap = std::min({c->max_seqs, c->rows, kMaxSegs});
+  c->gsub_cap = c->rows / kGlaSub + c->seg_cap;
   const ana_config& cf = c->cfg;
   const uint32_t d = cf.d, hd = d / cf.heads;
   uint64_t off = 0;
@@ -237,13 +248,17 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = dalloc(&c->d_tok, c->rows)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_pick, wb)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_rng, 4 * wb)) != hipSuccess) return bad(e);
-  if (c->mode != ANA_EXACT_FP32 &&
-      (e = dalloc(&c->d_part, attn_fast_part_floats(std::max(kSmallB, c->chunk), cf.heads, cf.ctx, hd))) != hipSuccess)
-    return bad(e);
+  if (c->mode != ANA_EXACT_FP32) {
+    // the fast kernels' scratch: attention partials for every row of a step,
+    // the GLA scan's regions and tables
+    if ((e = dalloc(&c->d_part, attn_fast_part_floats(c->rows, cf.heads, cf.ctx, hd))) != hipSuccess ||
+        (e = dalloc(&c->d_gla, gla_scan_floats(c->rows, c->gsub_cap, c->seg_cap, d, cf.heads))) != hipSuccess ||
+        (e = dalloc(&c->d_gtab, c->gsub_cap)) != hipSuccess ||
+        (e = dalloc(&c->d_rseq, c->rows)) != hipSuccess || (e = dalloc(&c->d_rpos, c->rows)) != hipSuccess)
+      return bad(e);
+    c->gla = gla_scan_carve(c->d_gla, c->rows, c->gsub_cap, c->seg_cap, d, cf.heads);
+  }
   if (c->mode == ANA_BF16 && (e = dalloc(&c->Wh, c->P)) != hipSuccess) return bad(e);
-  if (c->mode != ANA_EXACT_FP32 &&
-      (e = dalloc(&c->d_gla, gla_scan_floats(c->chunk, d, cf.heads))) != hipSuccess)
-    return bad(e);
   if ((e = hipMemcpyAsync(c->W, ck.raw.data(), 4 * c->P, hipMemcpyHostToDevice, c->st)) != hipSuccess) return bad(e);
   if ((e = launch_bswap(reinterpret_cast<uint32_t*>(c->W), c->P, c->st)) != hipSuccess) return bad(e);
   if (c->Wh && (e = launch_to_bf16(c->W, c->Wh, c->P, c->st)) != hipSuccess) return bad(e);
@@ -360,6 +375,36 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
   const uint32_t d = cf.d, f = cf.f;
   const float* W = c->W;
   const bool chunk = segs != nullptr;
+  // a fast mode's prefill step: the GLA scan's sub-chunk table and each row's
+  // sequence and position, uploaded once for every layer
+  uint32_t nsub = 0, nsp = 0;
+  bool fresh_all = true;
+  if (chunk && fast_mode(c)) {
+    if (segs->size() > c->seg_cap) return fail(c, ANA_EINVAL, "prefill step of %zu chunks (at most %u)", segs->size(), c->seg_cap);
+    c->h_gtab.clear();
+    c->h_rseq.resize(B);
+    c->h_rpos.resize(B);
+    uint64_t maxp = 0;
+    for (uint32_t si = 0; si < segs->size(); si++) {
+      const Seg& sg = (*segs)[si];
+      const uint32_t ns = (sg.T + kGlaSub - 1) / kGlaSub;
+      for (uint32_t j = 0; j < ns; j++)
+        c->h_gtab.push_back(GlaSub{sg.row0 + j * kGlaSub, std::min(kGlaSub, sg.T - j * kGlaSub), j, ns, sg.seq, si, 0, 0});
+      for (uint32_t t = 0; t < sg.T; t++) {
+        c->h_rseq[sg.row0 + t] = sg.seq;
+        c->h_rpos[sg.row0 + t] = sg.pos0 + t;
+      }
+      const uint64_t last = (uint64_t)sg.pos0 + sg.T - 1;
+      if (last >= cf.ctx) fresh_all = false;
+      maxp = std::max(maxp, last);
+    }
+    nsub = (uint32_t)c->h_gtab.size();
+    if (nsub > c->gsub_cap) return fail(c, ANA_EINVAL, "prefill step of %u sub-chunks (at most %u)", nsub, c->gsub_cap);
+    nsp = (uint32_t)(std::min<uint64_t>(maxp, cf.ctx - 1) / kFastTS + 1);
+    HIPCHK(c, hipMemcpyAsync(c->d_gtab, c->h_gtab.data(), sizeof(GlaSub) * nsub, hipMemcpyHostToDevice, c->st));
+    HIPCHK(c, hipMemcpyAsync(c->d_rseq, c->h_rseq.data(), 4 * (size_t)B, hipMemcpyHostToDevice, c->st));
+    HIPCHK(c, hipMemcpyAsync(c->d_rpos, c->h_rpos.data(), 4 * (size_t)B, hipMemcpyHostToDevice, c->st));
+  }
   for (uint32_t l = 0; l < cf.layers; l++) {
     const Blk& b = c->blk[l];
     // norm, then q|k|v (+ the gate's z): dd.gla / dd.sm `pre`
@@ -378,20 +423,16 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
       else
         HIPCHK(c, launch_gla_step(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), seq,
                                   c->O, d, cf.heads, cf.rglru, B, c->st));
+    } else if (b.gla && fast_mode(c)) {
+      // every chunk of the step at once: the closed-form chunked scan
+      HIPCHK(c, launch_gla_scan(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), c->O, c->gla,
+                                c->d_gtab, nsub, d, cf.heads, cf.rglru, c->st));
     } else if (b.gla) {
       for (const Seg& sg : *segs) {
-        // a fast mode's chunk of more than kSmallB rows: the closed-form scan
-        const bool fast_chunk = fast_mode(c) && sg.T > kSmallB;
         float* S = c->state + (uint64_t)sg.seq * c->seq_stride + c->layer_off[l];
-        const float* qkv = c->QKV + (size_t)sg.row0 * 3 * d;
-        const float* z = c->Z + (size_t)sg.row0 * d;
-        float* o = c->O + (size_t)sg.row0 * d;
-        if (fast_chunk)
-          HIPCHK(c, launch_gla_scan(qkv, z, cf.rglru ? W + b.lam : nullptr, S, o, c->d_gla, d, cf.heads,
-                                    cf.rglru, sg.T, c->st));
-        else
-          HIPCHK(c, launch_gla_chunk(qkv, z, cf.rglru ? W + b.lam : nullptr, S, o, d, cf.heads, cf.rglru,
-                                     sg.T, c->st));
+        HIPCHK(c, launch_gla_chunk(c->QKV + (size_t)sg.row0 * 3 * d, c->Z + (size_t)sg.row0 * d,
+                                   cf.rglru ? W + b.lam : nullptr, S, c->O + (size_t)sg.row0 * d, d,
+                                   cf.heads, cf.rglru, sg.T, c->st));
       }
     } else {
       AttnArgs a{};
@@ -411,6 +452,14 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
         } else {
           HIPCHK(c, launch_attn(a, c->st));
         }
+      } else if (fast_mode(c) && fresh_all) {
+        // no chunk reaches the ring's wrap: every row's write, then every
+        // row's attention over the splits up to the step's last position
+        a.QKV = c->QKV; a.O = c->O; a.B = B; a.seq = c->d_rseq; a.pos = c->d_rpos; a.write_kv = 0;
+        HIPCHK(c, launch_kv_write(a, c->st));
+        a.part = c->d_part;
+        a.nsp = nsp;
+        HIPCHK(c, launch_attn_fast(a, c->st));
       } else {
         for (const Seg& sg : *segs) {
           const bool fresh = (uint64_t)sg.pos0 + sg.T <= cf.ctx;
@@ -555,7 +604,7 @@ static int feeds_n(ana_ctx* c, const char* fn, uint32_t n, const uint32_t* seq, 
     for (uint32_t i = 0; i < n; i++) {
       if (len[i] <= t0) continue;
       const uint32_t T = std::min(c->chunk, len[i] - t0);
-      if (rows.size() + T > c->rows)
+      if (rows.size() + T > c->rows || segs.size() == c->seg_cap)
         if (int r = flush()) return r;
       segs.push_back(Seg{seq[i], pos[i] + t0, (uint32_t)rows.size(), T});
       rows.insert(rows.end(), toks + off[i] + t0, toks + off[i] + t0 + T);

@@ -170,7 +170,11 @@ struct AttnArgs {
   float* ss;            // scratch [B][heads][ctx]: sc * score
   float* pm;            // scratch [B][heads][ctx / kAttnTS]: partial maxima
   float* part;          // fast attention: per split (m, l, o[hd])
+  uint32_t nsp;         // fast attention: splits in the grid, those holding
+                        // slots 0 .. nsp * kFastTS - 1 (0: the whole ring)
 };
+// ring slots per split of the fast attention
+constexpr uint32_t kFastTS = 64;
 // slots per workgroup in the split attention's score pass
 constexpr uint32_t kAttnTS = 128;
 hipError_t launch_attn(const AttnArgs& a, hipStream_t st);
@@ -233,17 +237,32 @@ hipError_t launch_gla_fast(const float* QKV, const float* Z, const float* lam, S
                            const uint32_t* seq, float* O, uint32_t d, uint32_t heads,
                            uint32_t rglru, uint32_t B, hipStream_t st);
 hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st);
-// GLA over T tokens of one sequence (a prefill chunk) in closed form per
-// 16-token sub-chunk, S read and written once
-hipError_t launch_gla_chunk_fast(const float* QKV, const float* Z, const float* lam, float* S,
-                                 float* O, uint32_t d, uint32_t heads, uint32_t rglru, uint32_t T,
-                                 hipStream_t st);
-// the same as a chunked scan: 32-token sub-chunks in parallel, then their
-// states carried across (scratch: gla_scan_floats(T, d, heads) floats)
-size_t gla_scan_floats(uint32_t T, uint32_t d, uint32_t heads);
-hipError_t launch_gla_scan(const float* QKV, const float* Z, const float* lam, float* S, float* O,
-                           float* scratch, uint32_t d, uint32_t heads, uint32_t rglru, uint32_t T,
-                           hipStream_t st);
+// GLA over the prefill chunks of one step as a chunked scan: kGlaSub-token
+// sub-chunks in parallel, then their states carried across. The table holds
+// one entry per sub-chunk, those of one chunk consecutive.
+constexpr uint32_t kGlaSub = 32;
+// chunks a batched prefill step holds at most
+constexpr uint32_t kMaxSegs = 256;
+struct GlaSub {
+  uint32_t row;   // first workspace row
+  uint32_t n;     // tokens (1 .. kGlaSub)
+  uint32_t j;     // index inside its chunk
+  uint32_t nsub;  // sub-chunks of its chunk
+  uint32_t seq;   // state slot of the chunk's sequence
+  uint32_t seg;   // the chunk's index in the step (its entering-state copy)
+  uint32_t pad0, pad1;
+};
+// scratch: qt per row, D and U per (sub-chunk, head), the entering states
+// per (chunk, head)
+struct GlaScratch {
+  float *Qt, *Dj, *Uj, *S0;
+};
+size_t gla_scan_floats(uint32_t rows, uint32_t nsub, uint32_t nseg, uint32_t d, uint32_t heads);
+GlaScratch gla_scan_carve(float* p, uint32_t rows, uint32_t nsub, uint32_t nseg, uint32_t d,
+                          uint32_t heads);
+hipError_t launch_gla_scan(const float* QKV, const float* Z, const float* lam, StateRef S, float* O,
+                           const GlaScratch& g, const GlaSub* tab, uint32_t nsub, uint32_t d,
+                           uint32_t heads, uint32_t rglru, hipStream_t st);
 // batched products (prefill chunks, B > kSmallB) on the matrix cores: bf16
 // when Wh0 is set, else fp32; no argmax epilogue
 hipError_t launch_gemm_mfma(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nullptr,

@@ -404,7 +404,6 @@ hipError_t launch_gla_fast(const float* QKV, const float* Z, const float* lam, S
 // split's max m, l = sum exp(s - m) and o = sum exp(s - m) v. Pass 2 folds
 // the splits and the sink: m* = max(m_i, sink), den = sum l_i e^(m_i - m*)
 // + e^(sink - m*), o = sum o_i e^(m_i - m*) / den.
-constexpr uint32_t kFastTS = 64;
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_fast_part(AttnArgs a) {
@@ -413,7 +412,7 @@ __global__ __launch_bounds__(256) void k_attn_fast_part(AttnArgs a) {
   __shared__ float q[HD], kk[HD], vs[HD], es[kFastTS], red[4], nrm[2];
   __shared__ float4 op[4][C4];
   const uint32_t h = blockIdx.x, sp = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
-  const uint32_t d = a.d, ctx = a.ctx, ns = (ctx + kFastTS - 1) / kFastTS;
+  const uint32_t d = a.d, ctx = a.ctx, ns = gridDim.y;
   // a decode row (its sequence and position), or row b of a chunk of one
   // sequence at positions pos0 + b
   const uint32_t pos = a.pos ? a.pos[b] : a.pos0 + b;
@@ -423,14 +422,9 @@ __global__ __launch_bounds__(256) void k_attn_fast_part(AttnArgs a) {
   float* Vr = Kr + (size_t)ctx * d;
   const uint32_t t0 = sp * kFastTS;
   float* out = a.part + (((size_t)b * a.heads + h) * ns + sp) * (HD + 2);
-  if (t0 > npos) {
-    if (tid == 0) {
-      out[0] = -INFINITY;
-      out[1] = 0.0f;
-    }
-    if ((int)tid < HD) out[2 + tid] = 0.0f;
-    return;
-  }
+  // a split past the row's last live slot holds nothing (nor the row's own
+  // slot, which is live); the combine reads only live splits
+  if (t0 > npos) return;
   const bool mine = a.write_kv && slot >= t0 && slot < t0 + kFastTS;
   const uint32_t nt = min(kFastTS, npos + 1 - t0);
   // score lanes: slot i = tid / 4, dims [qq * QD, (qq + 1) * QD)
@@ -552,17 +546,19 @@ __global__ __launch_bounds__(256) void k_attn_fast_part(AttnArgs a) {
   }
 }
 
-// ns <= 64 splits (one lane each)
+// the row's live splits, at most 64 (one lane each), of ns in the grid
 template <int HD>
-__global__ __launch_bounds__(64) void k_attn_fast_comb(AttnArgs a) {
+__global__ __launch_bounds__(64) void k_attn_fast_comb(AttnArgs a, uint32_t ns) {
   __shared__ float wgt[64];
   __shared__ float den_s;
   const uint32_t h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const uint32_t ns = (a.ctx + kFastTS - 1) / kFastTS;
+  const uint32_t pos = a.pos ? a.pos[b] : a.pos0 + b;
+  const uint32_t npos = pos < a.ctx - 1 ? pos : a.ctx - 1;
+  const uint32_t nl = min(ns, npos / kFastTS + 1);
   const float* p = a.part + ((size_t)b * a.heads + h) * ns * (HD + 2);
   // every split's (m, l) at once, one lane each
-  const float mi = tid < ns ? p[tid * (HD + 2)] : -INFINITY;
-  const float li = tid < ns ? p[tid * (HD + 2) + 1] : 0.0f;
+  const float mi = tid < nl ? p[tid * (HD + 2)] : -INFINITY;
+  const float li = tid < nl ? p[tid * (HD + 2) + 1] : 0.0f;
   float m = mi;
 #pragma unroll
   for (int s2 = 32; s2 >= 1; s2 >>= 1) m = fmaxf(m, __shfl_xor(m, s2, 64));
@@ -579,18 +575,19 @@ __global__ __launch_bounds__(64) void k_attn_fast_comb(AttnArgs a) {
   if ((int)tid < HD) {
     float o = 0.0f;
 #pragma unroll 8
-    for (uint32_t i = 0; i < ns; i++) o = fmaf(p[i * (HD + 2) + 2 + tid], wgt[i], o);
+    for (uint32_t i = 0; i < nl; i++) o = fmaf(p[i * (HD + 2) + 2 + tid], wgt[i], o);
     a.O[(size_t)b * a.d + h * HD + tid] = o / den_s;
   }
 }
 
 hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st) {
   const uint32_t hd = a.d / a.heads;
-  const uint32_t ns = (a.ctx + kFastTS - 1) / kFastTS;
-  if (!a.part || hd % 4 || hd > 64 || ns > 64) return hipErrorInvalidValue;
+  const uint32_t full = (a.ctx + kFastTS - 1) / kFastTS;
+  const uint32_t ns = a.nsp ? min(a.nsp, full) : full;
+  if (!a.part || hd % 4 || hd > 64 || full > 64) return hipErrorInvalidValue;
 #define L_(H)                                                                                   \
   hipLaunchKernelGGL(k_attn_fast_part<H>, dim3(a.heads, ns, a.B), dim3(256), 0, st, a);        \
-  hipLaunchKernelGGL(k_attn_fast_comb<H>, dim3(a.heads, a.B), dim3(64), 0, st, a)
+  hipLaunchKernelGGL(k_attn_fast_comb<H>, dim3(a.heads, a.B), dim3(64), 0, st, a, ns)
   switch (hd) {
     case 64: L_(64); break;
     case 32: L_(32); break;
@@ -796,192 +793,60 @@ hipError_t launch_gemm_mfma(const GemvArgs& a, hipStream_t st, hipEvent_t e0, hi
 
 namespace ana {
 
-// ------------------------------------------------------------------ GLA over a chunk
+// ------------------------------------------------------------------ GLA over prefill chunks
 
 // T tokens of one sequence through one head's GLA (bend/Dense/Decode.bend
-// dd.gla over a chunk), for a block of CB state columns: the recurrence
-// S_t = diag(a_t) S_(t-1) + kh_t v_t^T, o_t = qh_t^T S_t taken L tokens at a
-// time in closed form. With c_t the running sum of log a within a
-// sub-chunk, S_t = e^(c_t) S_prev + sum_(s<=t) e^(c_t - c_s) kh_s v_s^T, so
+// dd.gla over a chunk): the recurrence S_t = diag(a_t) S_(t-1) + kh_t v_t^T,
+// o_t = qh_t^T S_t, taken kGlaSub tokens at a time in closed form. With c_t
+// the running sum of log a inside a sub-chunk,
+//   S_t = e^(c_t) S_prev + sum_(s<=t) e^(c_t - c_s) kh_s v_s^T, so
 //   o_t = (qh_t e^(c_t))^T S_prev + sum_(s<=t) P_ts v_s,
 //   P_ts = sum_a qh_t[a] kh_s[a] e^(c_t[a] - c_s[a]),
 // and every exponent is <= 0 (nothing overflows however small the gates).
-template <int HD>
-__global__ __launch_bounds__(256) void k_gla_chunk_fast(const float* __restrict__ QKV,
-                                                         const float* __restrict__ Z,
-                                                         const float* __restrict__ lam,
-                                                         float* __restrict__ Sbase,
-                                                         float* __restrict__ O, uint32_t d,
-                                                         uint32_t rglru, uint32_t T) {
-  constexpr int CB = 16, L = 16;
-  __shared__ float qh[L][HD + 1], kh[L][HD + 1], cl[L][HD + 1];
-  __shared__ float vv[L][CB], P[L][L + 1], Sb[HD][CB + 1], nr[L][2];
-  const uint32_t h = blockIdx.x, cb = blockIdx.y, tid = threadIdx.x;
-  float* Sg = Sbase + (size_t)h * HD * HD + cb * CB;
-  for (uint32_t e = tid; e < HD * CB; e += 256) Sb[e / CB][e % CB] = Sg[(size_t)(e / CB) * HD + e % CB];
-  for (uint32_t s0 = 0; s0 < T; s0 += L) {
-    const uint32_t n = min((uint32_t)L, T - s0);
-    __syncthreads();
-    // q, k norms of the sub-chunk's tokens: 16 lanes a token
-    {
-      const uint32_t t = tid / 16, l = tid % 16;
-      float sq = 0.0f, sk = 0.0f;
-      if (t < n) {
-        const float* x = QKV + (size_t)(s0 + t) * 3 * d + h * HD;
-        for (uint32_t a = l; a < (uint32_t)HD; a += 16) {
-          const float q = x[a], k = x[d + a];
-          sq = fmaf(q, q, sq);
-          sk = fmaf(k, k, sk);
-        }
-      }
-#pragma unroll
-      for (int m = 8; m >= 1; m >>= 1) {
-        sq += __shfl_xor(sq, m, 64);
-        sk += __shfl_xor(sk, m, 64);
-      }
-      if (l == 0 && t < L) {
-        nr[t][0] = 1.0f / sqrtf(1.0e-6f + sq);
-        nr[t][1] = 1.0f / sqrtf(1.0e-6f + sk);
-      }
-    }
-    __syncthreads();
-    // gates: log a (dd.gate in log form) and kh, per token and key dim
-    for (uint32_t e = tid; e < (uint32_t)L * HD; e += 256) {
-      const uint32_t t = e / HD, a = e % HD;
-      float lq = 0.0f, lk = 0.0f, la = 0.0f;
-      if (t < n) {
-        const float* x = QKV + (size_t)(s0 + t) * 3 * d + h * HD;
-        const float z = Z[(size_t)(s0 + t) * d + h * HD + a];
-        lq = x[a] * nr[t][0];
-        const float kn = x[d + a] * nr[t][1];
-        if (rglru) {
-          la = fminf(ANA_CAP, (8.0f * f_sigmoid(z)) * f_log_sigmoid(lam[h * HD + a]));
-          lk = kn * sqrtf(1.0f - expf(2.0f * la));
-        } else {
-          la = f_log_sigmoid(z);
-          lk = kn;
-        }
-      }
-      qh[t][a] = lq;
-      kh[t][a] = lk;
-      cl[t][a] = la;
-    }
-    if (tid < (uint32_t)L * CB) {
-      const uint32_t t = tid / CB, b = tid % CB;
-      vv[t][b] = t < n ? QKV[(size_t)(s0 + t) * 3 * d + 2 * d + h * HD + cb * CB + b] : 0.0f;
-    }
-    __syncthreads();
-    // running sums of log a over the sub-chunk (one lane per key dim)
-    if (tid < (uint32_t)HD) {
-      float c = 0.0f;
-      for (int t = 0; t < L; t++) {
-        c += cl[t][tid];
-        cl[t][tid] = c;
-      }
-    }
-    __syncthreads();
-    // P_ts for s <= t (one lane per pair)
-    {
-      const uint32_t t = tid / L, s = tid % L;
-      float p = 0.0f;
-      if (s <= t && t < n) {
-        for (int a = 0; a < HD; a++) p = fmaf(qh[t][a] * kh[s][a], __expf(cl[t][a] - cl[s][a]), p);
-      }
-      P[t][s] = p;
-    }
-    __syncthreads();
-    // o_t for the block's columns: lane (t, b)
-    {
-      const uint32_t t = tid / CB, b = tid % CB;
-      if (t < n) {
-        float o = 0.0f;
-        for (int a = 0; a < HD; a++) o = fmaf(qh[t][a] * __expf(cl[t][a]), Sb[a][b], o);
-        for (uint32_t s = 0; s <= t; s++) o = fmaf(P[t][s], vv[s][b], o);
-        O[(size_t)(s0 + t) * d + h * HD + cb * CB + b] = o;
-      }
-    }
-    __syncthreads();
-    // S <- e^(c_last) S + sum_s e^(c_last - c_s) kh_s v_s^T
-    for (uint32_t e = tid; e < (uint32_t)HD * CB; e += 256) {
-      const uint32_t a = e / CB, b = e % CB;
-      const float cL = cl[n - 1][a];
-      float s2 = __expf(cL) * Sb[a][b];
-      for (uint32_t s = 0; s < n; s++) s2 = fmaf(__expf(cL - cl[s][a]) * kh[s][a], vv[s][b], s2);
-      Sb[a][b] = s2;
-    }
-  }
-  __syncthreads();
-  for (uint32_t e = tid; e < HD * CB; e += 256) Sg[(size_t)(e / CB) * HD + e % CB] = Sb[e / CB][e % CB];
-}
-
-hipError_t launch_gla_chunk_fast(const float* QKV, const float* Z, const float* lam, float* S,
-                                 float* O, uint32_t d, uint32_t heads, uint32_t rglru, uint32_t T,
-                                 hipStream_t st) {
-  const uint32_t hd = d / heads;
-#define L_(H) hipLaunchKernelGGL(k_gla_chunk_fast<H>, dim3(heads, H / 16), dim3(256), 0, st, QKV, Z, lam, S, O, d, rglru, T)
-  switch (hd) {
-    case 64: L_(64); break;
-    case 32: L_(32); break;
-    case 16: L_(16); break;
-    default: return hipErrorInvalidValue;
-  }
-#undef L_
-  return hipGetLastError();
-}
-
-}  // namespace ana
-
-namespace ana {
-
-// ------------------------------------------------------------------ GLA over a chunk, two passes
-
-// The same closed form as k_gla_chunk_fast, with the 32-token sub-chunks of
-// a chunk run in parallel (a chunked scan). Pass 1, per (head, column block,
-// sub-chunk j): gates, the intra terms o_t = sum_(s<=t) P_ts v_s, the
-// sub-chunk's decay D_j = e^(c_last) and state contribution
-// U_j = sum_s e^(c_last - c_s) kh_s v_s^T, and qt_t = qh_t e^(c_t).
-// Pass 2, per (head, column block, j): the state entering j,
-// S_(j-1) = D_(j-1) (... (D_0 S_0 + U_0) ...) + U_(j-1), then o_t += qt_t^T S_(j-1);
-// the last sub-chunk's workgroup writes the chunk's final state.
-constexpr int kGlaSub = 32;
-
+// Every sub-chunk of every chunk in a prefill step runs in parallel (a
+// chunked scan over a table of sub-chunks; those of one chunk consecutive).
+// Pass 1, per (head, sub-chunk): the gates, the intra terms
+// o_t = sum_(s<=t) P_ts v_s, the sub-chunk's decay D = e^(c_last), its state
+// contribution U = sum_s e^(c_last - c_s) kh_s v_s^T and qt_t = qh_t e^(c_t);
+// a chunk's first sub-chunk also copies the state entering the chunk (pass 2
+// rewrites the state). Pass 2, per (head, column block, sub-chunk j): the
+// state entering j, S_(j-1) = D_(j-1) (... (D_0 S_0 + U_0) ...) + U_(j-1),
+// then o_t += qt_t^T S_(j-1); the chunk's last sub-chunk writes its final
+// state.
 template <int HD>
 __global__ __launch_bounds__(256) void k_gla_sub(const float* __restrict__ QKV,
                                                   const float* __restrict__ Z,
                                                   const float* __restrict__ lam, float* __restrict__ O,
-                                                  float* __restrict__ Qt, float* __restrict__ Dj,
-                                                  float* __restrict__ Uj, const float* __restrict__ Sbase,
-                                                  float* __restrict__ S0, uint32_t d, uint32_t rglru,
-                                                  uint32_t T) {
-  constexpr int CB = 16, L = kGlaSub;
-  __shared__ float qh[L][HD + 1], kh[L][HD + 1], cl[L][HD + 1];
-  __shared__ float vv[L][CB], P[L][L + 1], nr[L][2];
-  const uint32_t h = blockIdx.x, cb = blockIdx.y, j = blockIdx.z, tid = threadIdx.x;
-  const uint32_t nsub = gridDim.z, s0 = j * L, n = min((uint32_t)L, T - s0);
-  // the state entering the chunk, copied for pass 2 (which rewrites S)
-  if (j == 0) {
-    for (uint32_t e = tid; e < (uint32_t)HD * CB; e += 256) {
-      const size_t off = (size_t)h * HD * HD + (size_t)(e / CB) * HD + cb * CB + e % CB;
-      S0[off] = Sbase[off];
-    }
+                                                  GlaScratch g, StateRef S,
+                                                  const GlaSub* __restrict__ tab, uint32_t d,
+                                                  uint32_t rglru) {
+  constexpr int L = kGlaSub;
+  __shared__ float qh[L][HD + 1], kh[L][HD + 1], cl[L][HD + 1], vv[L][HD + 1];
+  __shared__ float P[L][L + 1], nr[L][2];
+  const uint32_t h = blockIdx.x, J = blockIdx.y, tid = threadIdx.x, heads = gridDim.x;
+  const GlaSub u = tab[J];
+  const uint32_t s0 = u.row, n = u.n;
+  if (u.j == 0) {
+    const float4* src = reinterpret_cast<const float4*>(S.base + (size_t)u.seq * S.seq_stride + S.layer_off +
+                                                        (size_t)h * HD * HD);
+    float4* dst = reinterpret_cast<float4*>(g.S0 + ((size_t)u.seg * heads + h) * HD * HD);
+    for (uint32_t e = tid; e < (uint32_t)HD * HD / 4; e += 256) dst[e] = src[e];
   }
-  // q, k, z of the sub-chunk's tokens, and v of the block's columns
+  // q, k, v, z of the sub-chunk's tokens (zeros past its end)
   for (uint32_t e = tid; e < (uint32_t)L * HD; e += 256) {
     const uint32_t t = e / HD, a = e % HD;
-    float q = 0.0f, k = 0.0f, z = 0.0f;
+    float q = 0.0f, k = 0.0f, v = 0.0f, z = 0.0f;
     if (t < n) {
       const float* x = QKV + (size_t)(s0 + t) * 3 * d + h * HD;
       q = x[a];
       k = x[d + a];
+      v = x[2 * d + a];
       z = Z[(size_t)(s0 + t) * d + h * HD + a];
     }
     qh[t][a] = q;
     kh[t][a] = k;
+    vv[t][a] = v;
     cl[t][a] = z;
-  }
-  for (uint32_t e = tid; e < (uint32_t)L * CB; e += 256) {
-    const uint32_t t = e / CB, b = e % CB;
-    vv[t][b] = t < n ? QKV[(size_t)(s0 + t) * 3 * d + 2 * d + h * HD + cb * CB + b] : 0.0f;
   }
   __syncthreads();
   // L2 norms: 8 lanes a token
@@ -1032,13 +897,11 @@ __global__ __launch_bounds__(256) void k_gla_sub(const float* __restrict__ QKV,
     }
   }
   __syncthreads();
-  if (cb == 0) {
-    for (uint32_t e = tid; e < n * HD; e += 256) {
-      const uint32_t t = e / HD, a = e % HD;
-      Qt[(size_t)(s0 + t) * d + h * HD + a] = qh[t][a] * __expf(cl[t][a]);
-    }
-    if (tid < (uint32_t)HD) Dj[((size_t)h * nsub + j) * HD + tid] = __expf(cl[n - 1][tid]);
+  for (uint32_t e = tid; e < n * HD; e += 256) {
+    const uint32_t t = e / HD, a = e % HD;
+    g.Qt[(size_t)(s0 + t) * d + h * HD + a] = qh[t][a] * __expf(cl[t][a]);
   }
+  if (tid < (uint32_t)HD) g.Dj[((size_t)J * heads + h) * HD + tid] = __expf(cl[n - 1][tid]);
   for (uint32_t e = tid; e < (uint32_t)L * L; e += 256) {
     const uint32_t t = e / L, s = e % L;
     float p = 0.0f;
@@ -1047,50 +910,56 @@ __global__ __launch_bounds__(256) void k_gla_sub(const float* __restrict__ QKV,
     P[t][s] = p;
   }
   __syncthreads();
-  for (uint32_t e = tid; e < (uint32_t)L * CB; e += 256) {
-    const uint32_t t = e / CB, b = e % CB;
-    if (t < n) {
-      float o = 0.0f;
-      for (uint32_t s = 0; s <= t; s++) o = fmaf(P[t][s], vv[s][b], o);
-      O[(size_t)(s0 + t) * d + h * HD + cb * CB + b] = o;
-    }
+  // kh_s e^(c_last - c_s) in place (P holds what needed kh), and the intra terms
+  for (uint32_t e = tid; e < (uint32_t)L * HD; e += 256) {
+    const uint32_t t = e / HD, a = e % HD;
+    kh[t][a] = t < n ? kh[t][a] * __expf(cl[n - 1][a] - cl[t][a]) : 0.0f;
   }
-  for (uint32_t e = tid; e < (uint32_t)HD * CB; e += 256) {
-    const uint32_t a = e / CB, b = e % CB;
-    const float cL = cl[n - 1][a];
-    float u = 0.0f;
-    for (uint32_t s = 0; s < n; s++) u = fmaf(__expf(cL - cl[s][a]) * kh[s][a], vv[s][b], u);
-    Uj[(((size_t)h * nsub + j) * HD + a) * HD + cb * CB + b] = u;
+  for (uint32_t e = tid; e < n * HD; e += 256) {
+    const uint32_t t = e / HD, b = e % HD;
+    float o = 0.0f;
+    for (uint32_t s = 0; s <= t; s++) o = fmaf(P[t][s], vv[s][b], o);
+    O[(size_t)(s0 + t) * d + h * HD + b] = o;
+  }
+  __syncthreads();
+  float* U = g.Uj + ((size_t)J * heads + h) * HD * HD;
+  for (uint32_t e = tid; e < (uint32_t)HD * HD; e += 256) {
+    const uint32_t a = e / HD, b = e % HD;
+    float s2 = 0.0f;
+    for (uint32_t s = 0; s < n; s++) s2 = fmaf(kh[s][a], vv[s][b], s2);
+    U[e] = s2;
   }
 }
 
 template <int HD>
-__global__ __launch_bounds__(256) void k_gla_carry(const float* __restrict__ Qt,
-                                                    const float* __restrict__ Dj,
-                                                    const float* __restrict__ Uj,
-                                                    const float* __restrict__ S0,
-                                                    float* __restrict__ Sbase, float* __restrict__ O,
-                                                    uint32_t d, uint32_t T) {
+__global__ __launch_bounds__(256) void k_gla_carry(GlaScratch g, StateRef S, float* __restrict__ O,
+                                                    const GlaSub* __restrict__ tab, uint32_t d) {
   constexpr int CB = 16, L = kGlaSub;
-  __shared__ float Sb[HD][CB + 1];
-  const uint32_t h = blockIdx.x, cb = blockIdx.y, j = blockIdx.z, tid = threadIdx.x;
-  const uint32_t nsub = gridDim.z, s0 = j * L, n = min((uint32_t)L, T - s0);
-  float* Sg = Sbase + (size_t)h * HD * HD + cb * CB;
-  const float* S0g = S0 + (size_t)h * HD * HD + cb * CB;
-  // S_(j-1): S_0 through the earlier sub-chunks (HD * CB / 256 elements a thread)
+  __shared__ float Sb[HD][CB + 1], qs[L][HD + 1];
+  const uint32_t h = blockIdx.x, cb = blockIdx.y, J = blockIdx.z, tid = threadIdx.x, heads = gridDim.x;
+  const GlaSub u = tab[J];
+  const uint32_t s0 = u.row, n = u.n;
+  for (uint32_t e = tid; e < n * HD; e += 256) {
+    const uint32_t t = e / HD, a = e % HD;
+    qs[t][a] = g.Qt[(size_t)(s0 + t) * d + h * HD + a];
+  }
+  // S_(j-1): the chunk's entering state through its earlier sub-chunks
+  // (table entries J - j .. J - 1), HD * CB / 256 elements a thread
+  const float* S0g = g.S0 + ((size_t)u.seg * heads + h) * HD * HD + cb * CB;
   constexpr int NE = HD * CB / 256;
-  float sv[NE > 0 ? NE : 1];
+  float sv[NE];
 #pragma unroll
   for (int i = 0; i < NE; i++) {
     const uint32_t e = tid + 256 * i, a = e / CB, b = e % CB;
     sv[i] = S0g[(size_t)a * HD + b];
   }
-  for (uint32_t i = 0; i < j; i++) {
+  for (uint32_t I = J - u.j; I < J; I++) {
+    const float* D = g.Dj + ((size_t)I * heads + h) * HD;
+    const float* U = g.Uj + ((size_t)I * heads + h) * HD * HD + cb * CB;
 #pragma unroll
     for (int q = 0; q < NE; q++) {
       const uint32_t e = tid + 256 * q, a = e / CB, b = e % CB;
-      sv[q] = fmaf(Dj[((size_t)h * nsub + i) * HD + a], sv[q],
-                   Uj[(((size_t)h * nsub + i) * HD + a) * HD + cb * CB + b]);
+      sv[q] = fmaf(D[a], sv[q], U[(size_t)a * HD + b]);
     }
   }
 #pragma unroll
@@ -1098,44 +967,55 @@ __global__ __launch_bounds__(256) void k_gla_carry(const float* __restrict__ Qt,
     const uint32_t e = tid + 256 * i;
     Sb[e / CB][e % CB] = sv[i];
   }
-  if (j == nsub - 1) {
+  if (u.j == u.nsub - 1) {
+    float* Sg = S.base + (size_t)u.seq * S.seq_stride + S.layer_off + (size_t)h * HD * HD + cb * CB;
+    const float* D = g.Dj + ((size_t)J * heads + h) * HD;
+    const float* U = g.Uj + ((size_t)J * heads + h) * HD * HD + cb * CB;
 #pragma unroll
     for (int q = 0; q < NE; q++) {
       const uint32_t e = tid + 256 * q, a = e / CB, b = e % CB;
-      Sg[(size_t)a * HD + b] = fmaf(Dj[((size_t)h * nsub + j) * HD + a], sv[q],
-                                    Uj[(((size_t)h * nsub + j) * HD + a) * HD + cb * CB + b]);
+      Sg[(size_t)a * HD + b] = fmaf(D[a], sv[q], U[(size_t)a * HD + b]);
     }
   }
   __syncthreads();
   for (uint32_t e = tid; e < n * CB; e += 256) {
     const uint32_t t = e / CB, b = e % CB;
-    const float* q = Qt + (size_t)(s0 + t) * d + h * HD;
     float o = 0.0f;
-    for (int a = 0; a < HD; a++) o = fmaf(q[a], Sb[a][b], o);
+#pragma unroll 16
+    for (int a = 0; a < HD; a++) o = fmaf(qs[t][a], Sb[a][b], o);
     O[(size_t)(s0 + t) * d + h * HD + cb * CB + b] += o;
   }
 }
 
-size_t gla_scan_floats(uint32_t T, uint32_t d, uint32_t heads) {
-  const uint32_t hd = d / heads, nsub = (T + kGlaSub - 1) / kGlaSub;
-  return (size_t)T * d + (size_t)heads * nsub * hd + (size_t)heads * nsub * hd * hd +
-         (size_t)heads * hd * hd;
+static size_t round64(size_t n) { return (n + 63) & ~(size_t)63; }
+
+size_t gla_scan_floats(uint32_t rows, uint32_t nsub, uint32_t nseg, uint32_t d, uint32_t heads) {
+  const size_t hd = d / heads;
+  return round64((size_t)rows * d) + round64((size_t)nsub * heads * hd) +
+         round64((size_t)nsub * heads * hd * hd) + round64((size_t)nseg * heads * hd * hd);
 }
 
-hipError_t launch_gla_scan(const float* QKV, const float* Z, const float* lam, float* S, float* O,
-                           float* scratch, uint32_t d, uint32_t heads, uint32_t rglru, uint32_t T,
-                           hipStream_t st) {
-  const uint32_t hd = d / heads, nsub = (T + kGlaSub - 1) / kGlaSub;
-  if (hd % 16 || hd * 16 < 256 || T == 0) return hipErrorInvalidValue;
-  float* Qt = scratch;
-  float* Dj = Qt + (size_t)T * d;
-  float* Uj = Dj + (size_t)heads * nsub * hd;
-  float* S0 = Uj + (size_t)heads * nsub * hd * hd;
-#define L_(H)                                                                                       \
-  hipLaunchKernelGGL(k_gla_sub<H>, dim3(heads, H / 16, nsub), dim3(256), 0, st, QKV, Z, lam, O, Qt, \
-                     Dj, Uj, S, S0, d, rglru, T);                                                   \
-  hipLaunchKernelGGL(k_gla_carry<H>, dim3(heads, H / 16, nsub), dim3(256), 0, st, Qt, Dj, Uj, S0,   \
-                     S, O, d, T)
+GlaScratch gla_scan_carve(float* p, uint32_t rows, uint32_t nsub, uint32_t nseg, uint32_t d,
+                          uint32_t heads) {
+  const size_t hd = d / heads;
+  GlaScratch g;
+  g.Qt = p;
+  g.Dj = g.Qt + round64((size_t)rows * d);
+  g.Uj = g.Dj + round64((size_t)nsub * heads * hd);
+  g.S0 = g.Uj + round64((size_t)nsub * heads * hd * hd);
+  (void)nseg;
+  return g;
+}
+
+hipError_t launch_gla_scan(const float* QKV, const float* Z, const float* lam, StateRef S, float* O,
+                           const GlaScratch& g, const GlaSub* tab, uint32_t nsub, uint32_t d,
+                           uint32_t heads, uint32_t rglru, hipStream_t st) {
+  const uint32_t hd = d / heads;
+  if (hd % 16 || hd * 16 < 256 || nsub == 0) return hipErrorInvalidValue;
+#define L_(H)                                                                                        \
+  hipLaunchKernelGGL(k_gla_sub<H>, dim3(heads, nsub), dim3(256), 0, st, QKV, Z, lam, O, g, S, tab, d, \
+                     rglru);                                                                         \
+  hipLaunchKernelGGL(k_gla_carry<H>, dim3(heads, H / 16, nsub), dim3(256), 0, st, g, S, O, tab, d)
   switch (hd) {
     case 64: L_(64); break;
     case 32: L_(32); break;
