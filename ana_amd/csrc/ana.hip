@@ -48,7 +48,10 @@ struct ana_ctx {
   GlaSub* d_gtab = nullptr;          // a prefill step's sub-chunk table
   uint32_t *d_rseq = nullptr, *d_rpos = nullptr;  // a prefill step's per-row sequence, position
   uint32_t seg_cap = 1, gsub_cap = 1; // chunks a prefill step holds; table entries
+  AttnTile* d_atab = nullptr;        // a prefill step's attention tiles
+  uint32_t atab_cap = 1;
   // host copies of the step tables, kept until the step's synchronize
+  std::vector<AttnTile> h_atab;
   std::vector<GlaSub> h_gtab;
   std::vector<uint32_t> h_rseq, h_rpos;
   size_t out_cap = 0;
@@ -145,7 +148,7 @@ static void release(ana_ctx* c) {
   if (c->gexec_n) (void)hipGraphExecDestroy(c->gexec_n);
   void* ps[] = {c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
-                c->d_ss, c->d_pm, c->d_gtab, c->d_rseq, c->d_rpos};
+                c->d_ss, c->d_pm, c->d_gtab, c->d_atab, c->d_rseq, c->d_rpos};
   for (void* p : ps)
     if (p) (void)hipFree(p);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
@@ -209,6 +212,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   // at most rows / kGlaSub + seg_cap sub-chunks
   c->seg_cap = std::min({c->max_seqs, c->rows, kMaxSegs});
   c->gsub_cap = c->rows / kGlaSub + c->seg_cap;
+  c->atab_cap = c->rows / kFlashQ + c->seg_cap;
   const ana_config& cf = c->cfg;
   const uint32_t d = cf.d, hd = d / cf.heads;
   uint64_t off = 0;
@@ -253,7 +257,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
     // the GLA scan's regions and tables
     if ((e = dalloc(&c->d_part, attn_fast_part_floats(c->rows, cf.heads, cf.ctx, hd))) != hipSuccess ||
         (e = dalloc(&c->d_gla, gla_scan_floats(c->rows, c->gsub_cap, c->seg_cap, d, cf.heads))) != hipSuccess ||
-        (e = dalloc(&c->d_gtab, c->gsub_cap)) != hipSuccess ||
+        (e = dalloc(&c->d_gtab, c->gsub_cap)) != hipSuccess || (e = dalloc(&c->d_atab, c->atab_cap)) != hipSuccess ||
         (e = dalloc(&c->d_rseq, c->rows)) != hipSuccess || (e = dalloc(&c->d_rpos, c->rows)) != hipSuccess)
       return bad(e);
     c->gla = gla_scan_carve(c->d_gla, c->rows, c->gsub_cap, c->seg_cap, d, cf.heads);
@@ -382,6 +386,7 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
   if (chunk && fast_mode(c)) {
     if (segs->size() > c->seg_cap) return fail(c, ANA_EINVAL, "prefill step of %zu chunks (at most %u)", segs->size(), c->seg_cap);
     c->h_gtab.clear();
+    c->h_atab.clear();
     c->h_rseq.resize(B);
     c->h_rpos.resize(B);
     uint64_t maxp = 0;
@@ -394,6 +399,8 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
         c->h_rseq[sg.row0 + t] = sg.seq;
         c->h_rpos[sg.row0 + t] = sg.pos0 + t;
       }
+      for (uint32_t t = 0; t < sg.T; t += kFlashQ)
+        c->h_atab.push_back(AttnTile{sg.seq, sg.pos0 + t, sg.row0 + t, std::min(kFlashQ, sg.T - t)});
       const uint64_t last = (uint64_t)sg.pos0 + sg.T - 1;
       if (last >= cf.ctx) fresh_all = false;
       maxp = std::max(maxp, last);
@@ -401,6 +408,9 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
     nsub = (uint32_t)c->h_gtab.size();
     if (nsub > c->gsub_cap) return fail(c, ANA_EINVAL, "prefill step of %u sub-chunks (at most %u)", nsub, c->gsub_cap);
     nsp = (uint32_t)(std::min<uint64_t>(maxp, cf.ctx - 1) / kFastTS + 1);
+    if (c->h_atab.size() > c->atab_cap) return fail(c, ANA_EINVAL, "prefill step of %zu attention tiles (at most %u)", c->h_atab.size(), c->atab_cap);
+    if (fresh_all && !c->h_atab.empty())
+      HIPCHK(c, hipMemcpyAsync(c->d_atab, c->h_atab.data(), sizeof(AttnTile) * c->h_atab.size(), hipMemcpyHostToDevice, c->st));
     HIPCHK(c, hipMemcpyAsync(c->d_gtab, c->h_gtab.data(), sizeof(GlaSub) * nsub, hipMemcpyHostToDevice, c->st));
     HIPCHK(c, hipMemcpyAsync(c->d_rseq, c->h_rseq.data(), 4 * (size_t)B, hipMemcpyHostToDevice, c->st));
     HIPCHK(c, hipMemcpyAsync(c->d_rpos, c->h_rpos.data(), 4 * (size_t)B, hipMemcpyHostToDevice, c->st));
@@ -457,9 +467,7 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
         // row's attention over the splits up to the step's last position
         a.QKV = c->QKV; a.O = c->O; a.B = B; a.seq = c->d_rseq; a.pos = c->d_rpos; a.write_kv = 0;
         HIPCHK(c, launch_kv_write(a, c->st));
-        a.part = c->d_part;
-        a.nsp = nsp;
-        HIPCHK(c, launch_attn_fast(a, c->st));
+        HIPCHK(c, launch_attn_flash(a, c->d_atab, (uint32_t)c->h_atab.size(), c->st));
       } else {
         for (const Seg& sg : *segs) {
           const bool fresh = (uint64_t)sg.pos0 + sg.T <= cf.ctx;

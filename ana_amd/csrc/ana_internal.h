@@ -271,6 +271,14 @@ hipError_t launch_gemm_mfma(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = n
 hipError_t launch_gemm_big(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nullptr,
                            hipEvent_t e1 = nullptr);
 size_t attn_fast_part_floats(uint32_t B, uint32_t heads, uint32_t ctx, uint32_t hd);
+// causal attention of fresh prefill rows on the matrix cores: one workgroup
+// per (head, tile of up to kFlashQ rows of one sequence), the rows' k and v
+// already in the ring
+constexpr uint32_t kFlashQ = 64;
+struct AttnTile {
+  uint32_t seq, pos0, row0, n;  // sequence, first row's position and workspace row, rows
+};
+hipError_t launch_attn_flash(const AttnArgs& a, const AttnTile* tab, uint32_t ntiles, hipStream_t st);
 hipError_t launch_zero_u32(uint32_t* p, uint32_t n, hipStream_t st);
 hipError_t launch_zero_u64(unsigned long long* p, uint32_t n, hipStream_t st);
 

@@ -15,6 +15,10 @@
 
 namespace ana {
 
+// MFMA operand and accumulator vectors
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
 // ------------------------------------------------------------------ weights
 
 // fp32 bits -> bfloat16, round to nearest even; NaN stays a quiet NaN
@@ -602,14 +606,184 @@ size_t attn_fast_part_floats(uint32_t B, uint32_t heads, uint32_t ctx, uint32_t 
   return (size_t)B * heads * ((ctx + kFastTS - 1) / kFastTS) * (hd + 2);
 }
 
+// ------------------------------------------------------------------ prefill attention on the matrix cores
+
+// Fresh prefill chunks (no slot past the ring's wrap): causal attention of a
+// tile of up to kFlashQ query rows of one sequence over slots 0 .. the tile's
+// last position, flash style. Per key tile of 64 slots: S = (sc q) K^T on
+// v_mfma_f32_16x16x4f32, the running max m and sum l per row,
+// O <- O e^(m_old - m_new) + P V; at the end the sink joins the max and the
+// denominator as in the split kernels: o = O e^(m - m*) / (l e^(m - m*) +
+// e^(sink - m*)). Wave w holds query rows 16 w .. 16 w + 15. Inside an MFMA
+// the 4 k-lanes of lane group g take dims (or slots) [Q g, Q g + Q), so each
+// lane reads its operands as contiguous 16-byte pieces.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_flash(AttnArgs a, const AttnTile* __restrict__ tab) {
+  constexpr int KT = 64;                 // slots per key tile
+  constexpr int DG = HD / 4;             // dims per lane group in S = Q K^T
+  constexpr int NJ = HD / 16;            // 16-dim output tiles
+  constexpr int KP = HD + 4, VP = KT + 4, PP = KT + 4;
+  __shared__ __align__(16) float Ks[KT][KP];
+  __shared__ __align__(16) float Vt[HD][VP];
+  __shared__ __align__(16) float Ps[4][16][PP];
+  const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint32_t r16 = lane & 15, g = lane >> 4;
+  const AttnTile tt = tab[blockIdx.y];
+  const uint32_t d = a.d;
+  const float* Kr = a.KV.base + (size_t)tt.seq * a.KV.seq_stride + a.KV.layer_off;
+  const float* Vr = Kr + (size_t)a.ctx * d;
+  const uint32_t last = tt.pos0 + tt.n - 1;          // the tile's last position (< ctx)
+  // this lane's query row for the S operand, dims [DG g, DG g + DG), qk-normed
+  // and scaled by 1 / sqrt(hd)
+  float q[DG];
+  {
+    const uint32_t qr = 16 * w + r16;
+    const float* x = a.QKV + (size_t)(tt.row0 + (qr < tt.n ? qr : 0)) * 3 * d + h * HD + DG * g;
+#pragma unroll
+    for (int i = 0; i < DG / 4; i++) {
+      const float4 v = *reinterpret_cast<const float4*>(x + 4 * i);
+      q[4 * i] = v.x;
+      q[4 * i + 1] = v.y;
+      q[4 * i + 2] = v.z;
+      q[4 * i + 3] = v.w;
+    }
+    float s = 1.0f / sqrtf((float)HD);
+    if (a.gq) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < DG; i++) ss = fmaf(q[i], q[i], ss);
+      ss += __shfl_xor(ss, 16, 64);
+      ss += __shfl_xor(ss, 32, 64);
+      const float rs = 1.0f / sqrtf(ss / (float)HD + 1.0e-5f);
+#pragma unroll
+      for (int i = 0; i < DG; i++) q[i] = (q[i] * rs) * (1.0f + a.gq[DG * g + i]);
+    }
+#pragma unroll
+    for (int i = 0; i < DG; i++) q[i] *= s;
+  }
+  // rows of this lane in the result layout: 16 w + 4 g + r
+  float m[4], l[4];
+  f32x4_t o[NJ];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    m[r] = -INFINITY;
+    l[r] = 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; j++) o[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t nkt = last / KT + 1;
+  for (uint32_t kt = 0; kt < nkt; kt++) {
+    const uint32_t k0 = kt * KT;
+    __syncthreads();   // the previous tile's K, V and P reads are done
+    for (uint32_t e = tid; e < (uint32_t)KT * (HD / 4); e += 256) {
+      const uint32_t s = e / (HD / 4), c4 = e % (HD / 4);
+      const uint32_t slot = k0 + s <= last ? k0 + s : 0;
+      const float4 kv = *reinterpret_cast<const float4*>(Kr + (size_t)slot * d + h * HD + 4 * c4);
+      const float4 vv = *reinterpret_cast<const float4*>(Vr + (size_t)slot * d + h * HD + 4 * c4);
+      *reinterpret_cast<float4*>(&Ks[s][4 * c4]) = kv;
+      Vt[4 * c4][s] = vv.x;
+      Vt[4 * c4 + 1][s] = vv.y;
+      Vt[4 * c4 + 2][s] = vv.z;
+      Vt[4 * c4 + 3][s] = vv.w;
+    }
+    __syncthreads();
+    // scores of the wave's 16 rows against the tile's 4 x 16 slots
+    f32x4_t sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      sc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      const float* kr = &Ks[16 * j + r16][DG * g];
+#pragma unroll
+      for (int i = 0; i < DG / 4; i++) {
+        const float4 kk = *reinterpret_cast<const float4*>(kr + 4 * i);
+        sc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(q[4 * i], kk.x, sc[j], 0, 0, 0);
+        sc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(q[4 * i + 1], kk.y, sc[j], 0, 0, 0);
+        sc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(q[4 * i + 2], kk.z, sc[j], 0, 0, 0);
+        sc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(q[4 * i + 3], kk.w, sc[j], 0, 0, 0);
+      }
+    }
+    // causal mask, running max and sum per row (a row's slots lie across the
+    // 16 lanes of its group)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint32_t row = 16 * w + 4 * g + r;
+      const uint32_t qpos = tt.pos0 + (row < tt.n ? row : tt.n - 1);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t slot = k0 + 16 * j + r16;
+        if (slot > qpos) sc[j][r] = -INFINITY;
+        mx = fmaxf(mx, sc[j][r]);
+      }
+#pragma unroll
+      for (int s2 = 1; s2 < 16; s2 <<= 1) mx = fmaxf(mx, __shfl_xor(mx, s2, 64));
+      const float mn = fmaxf(m[r], mx);   // finite: slot k0 <= qpos always
+      const float al = __expf(m[r] - mn);
+      float sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float p = __expf(sc[j][r] - mn);
+        sum += p;
+        Ps[w][4 * g + r][16 * j + r16] = p;
+      }
+#pragma unroll
+      for (int s2 = 1; s2 < 16; s2 <<= 1) sum += __shfl_xor(sum, s2, 64);
+      l[r] = l[r] * al + sum;
+      m[r] = mn;
+#pragma unroll
+      for (int j = 0; j < NJ; j++) o[j][r] *= al;
+    }
+    __syncthreads();
+    // O += P V: row r16 of the wave's P, slots [16 g, 16 g + 16)
+    const float* pr = &Ps[w][r16][16 * g];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float4 p4 = *reinterpret_cast<const float4*>(pr + 4 * i);
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const float4 v4 = *reinterpret_cast<const float4*>(&Vt[16 * j + r16][16 * g + 4 * i]);
+        o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(p4.x, v4.x, o[j], 0, 0, 0);
+        o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(p4.y, v4.y, o[j], 0, 0, 0);
+        o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(p4.z, v4.z, o[j], 0, 0, 0);
+        o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(p4.w, v4.w, o[j], 0, 0, 0);
+      }
+    }
+  }
+  // the sink, then the rows out
+  const float sink = a.sink ? a.sink[h] : -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const uint32_t row = 16 * w + 4 * g + r;
+    if (row >= tt.n) continue;
+    const float ms = fmaxf(m[r], sink);
+    const float e = __expf(m[r] - ms);
+    const float den = l[r] * e + (a.sink ? __expf(sink - ms) : 0.0f);
+    const float f = e / den;
+    float* out = a.O + (size_t)(tt.row0 + row) * d + h * HD;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) out[16 * j + r16] = o[j][r] * f;
+  }
+}
+
+hipError_t launch_attn_flash(const AttnArgs& a, const AttnTile* tab, uint32_t ntiles, hipStream_t st) {
+  const uint32_t hd = a.d / a.heads;
+  if (ntiles == 0) return hipSuccess;
+#define L_(H) hipLaunchKernelGGL(k_attn_flash<H>, dim3(a.heads, ntiles), dim3(256), 0, st, a, tab)
+  switch (hd) {
+    case 64: L_(64); break;
+    case 32: L_(32); break;
+    case 16: L_(16); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef L_
+  return hipGetLastError();
+}
+
 }  // namespace ana
 
 namespace ana {
 
 // ------------------------------------------------------------------ batched products on MFMA
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // Larger batches (prefill chunks, batched decode) in the fast modes:
 // Y[m][n] = sum_k X[m][k] W[n][k] on the matrix cores. A workgroup owns 16
