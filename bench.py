@@ -155,6 +155,41 @@ NUMERICS = {"exact": "exact_fp32: bit-exact with the reference's CPU kernels",
             "bf16": "bf16 weights, fp32 activations/accumulation/state; logits within 2e-2"}
 
 
+def run_prefill(path: str, c) -> dict:
+    """B=64 prefill on the matrix cores: 64 prompts of 512 tokens through
+    ana_feeds_n at chunk 128 (8192 rows a product), in both fast modes."""
+    extra = {}
+    for m in ("bf16", "fast_fp32"):
+        with ana_amd.Decoder(path, max_seqs=64, prefill_chunk=128, numerics=MODES[m]) as dec:
+            prs = [ckpt.prompt(1000 + b, 512, c.vocab) for b in range(64)]
+            dec.feeds_n(list(range(64)), [0] * 64, [pr[:64] for pr in prs])   # warm-up
+            for b in range(64):
+                dec.reset(b)
+            t = time.perf_counter()
+            dec.feeds_n(list(range(64)), [0] * 64, prs)
+            dt = time.perf_counter() - t
+        ntok, L = 64 * 512, 512
+        # the products, plus causal attention in the softmax layers
+        # (q k and p v over the live slots: 2 x 2 x L^2 / 2 x d per
+        # sequence and layer)
+        n_sm = sum(1 for i in range(c.layers) if i % 4 == 3)
+        flops = 2.0 * (c.params - c.vocab * c.d) * ntok + n_sm * 2.0 * 64 * L * L * c.d
+        peak = 2500.0 if m == "bf16" else 157.3
+        extra[f"prefill_b64_{m}"] = {
+            "tok_s": round(ntok / dt, 1), "seconds": round(dt, 4),
+            "tflops": round(flops / dt / 1e12, 2), "peak_tflops": peak,
+            "frac": round(flops / dt / 1e12 / peak, 4),
+            "workload": "64 prompts x 512 tokens through ana_feeds_n, chunk 128; flops = 2 x "
+                        "(P - v d) per token (the products) + causal attention 2 B L^2 d per "
+                        "softmax layer (the GLA scan not counted)",
+            "kernels": "products k_gemm_big (128 x 128 MFMA tiles"
+                       + (", bf16 weights x bf16 head+remainder activations" if m == "bf16" else ", fp32 MFMA")
+                       + "), attention k_attn_flash (fp32 MFMA), GLA k_gla_sub + k_gla_carry",
+        }
+        log(f"prefill B=64 x 512 {m}: {ntok / dt:.0f} tok/s")
+    return extra
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -166,6 +201,8 @@ def main() -> int:
     ap.add_argument("--others", type=int, default=1, help="also measure B=1 in the other modes (1/0)")
     ap.add_argument("--b64", type=int, default=1, help="also measure B=64 (1/0)")
     ap.add_argument("--prefill", type=int, default=1, help="also measure B=64 x 512 prefill (1/0)")
+    ap.add_argument("--prefill-only", type=int, default=0,
+                    help="measure only the B=64 x 512 prefill and print its figures (1/0)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--ckpt", default=os.environ.get("ANA_BENCH_CKPT", "/tmp/ana_bench_fp100m.ftc2"))
     a = ap.parse_args()
@@ -176,6 +213,9 @@ def main() -> int:
     c = cf.FP100M
     path = ensure_ckpt(c, a.ckpt)
     mode = a.numerics
+    if a.prefill_only:
+        print(json.dumps(run_prefill(path, c)), flush=True)
+        return 0
     r1 = run_batch(path, c, 1, a.prompt, a.warmup, a.steps, min(a.steps, 32), mode)
     g = r1["stats"]["gemv"]
     h = r1["stats"]["head"]
@@ -205,28 +245,7 @@ def main() -> int:
             extra[key]["workload"] = ("B=64, 128-token prompts (chunked prefill, one sequence at a "
                                       "time), 32 greedy steps at positions 128+; " + NUMERICS[m])
     if a.prefill:
-        # B=64 prefill on the matrix cores: 64 prompts of 512 tokens through
-        # ana_feeds_n at chunk 128 (8192 rows a product), bf16 weights
-        for m in ("bf16", "fast_fp32"):
-            with ana_amd.Decoder(path, max_seqs=64, prefill_chunk=128, numerics=MODES[m]) as dec:
-                prs = [ckpt.prompt(1000 + b, 512, c.vocab) for b in range(64)]
-                dec.feeds_n(list(range(64)), [0] * 64, [pr[:64] for pr in prs])   # warm-up
-                for b in range(64):
-                    dec.reset(b)
-                t = time.perf_counter()
-                dec.feeds_n(list(range(64)), [0] * 64, prs)
-                dt = time.perf_counter() - t
-            ntok = 64 * 512
-            flops = 2.0 * (c.params - c.vocab * c.d) * ntok
-            peak = 2500.0 if m == "bf16" else 157.3
-            extra[f"prefill_b64_{m}"] = {
-                "tok_s": round(ntok / dt, 1), "seconds": round(dt, 4),
-                "tflops": round(flops / dt / 1e12, 2), "peak_tflops": peak,
-                "frac": round(flops / dt / 1e12 / peak, 4),
-                "workload": "64 prompts x 512 tokens through ana_feeds_n, chunk 128; flops = 2 x "
-                            "(P - v d) per token (the products; GLA and attention not counted)",
-            }
-            log(f"prefill B=64 x 512 {m}: {ntok / dt:.0f} tok/s")
+        extra.update(run_prefill(path, c))
     cpu = cpu_baseline(path, c, a.cpu_seconds) if a.cpu_seconds > 0 else None
     kern = {k: {"launches": v[0], "ms": round(v[1], 4), "gb": round(v[2] / 1e9, 4)}
             for k, v in r1["stats"].items()}
