@@ -57,6 +57,7 @@ SIGNATURES = {
     "ana_feed": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p, _u32p]),
     "ana_feeds": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, _u32p, C.c_uint32]),
     "ana_feeds_n": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p, _u32p, _u32p]),
+    "ana_score_n": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p, _u32p, _u32p, _f32p]),
     "ana_logits": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _f32p]),
     "ana_top": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p]),
     "ana_pick": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, C.POINTER(_Sampling), _u64p, _u32p]),
@@ -220,6 +221,26 @@ class Decoder:
         self._check(lib().ana_feeds_n(self.h, s.size, _p(s, C.c_uint32), _p(p, C.c_uint32),
                                       _p(ln, C.c_uint32), _p(flat, C.c_uint32)))
 
+    def score_n(self, seqs, pos, toks) -> list:
+        """Evaluate.bend's window.go for several sequences: each feeds
+        toks[i][:-1] from pos[i]; element t of the i-th result is
+        G.lse(logits after token t) - logits[toks[i][t + 1]]."""
+        s, p = _u32(seqs), _u32(pos)
+        ts = [_u32(t) for t in toks]
+        ln = np.array([t.size for t in ts], dtype=np.uint32)
+        flat = np.ascontiguousarray(np.concatenate(ts) if ts else np.zeros(0, np.uint32), dtype=np.uint32)
+        if flat.size == 0:
+            flat = np.zeros(1, np.uint32)
+        nce = [max(int(k) - 1, 0) for k in ln]
+        out = np.zeros(max(sum(nce), 1), dtype=np.float32)
+        self._check(lib().ana_score_n(self.h, s.size, _p(s, C.c_uint32), _p(p, C.c_uint32),
+                                      _p(ln, C.c_uint32), _p(flat, C.c_uint32), _p(out, C.c_float)))
+        res, o = [], 0
+        for k in nce:
+            res.append(out[o:o + k].copy())
+            o += k
+        return res
+
     def logits(self, seqs) -> np.ndarray:
         s = _u32(seqs)
         out = np.empty((s.size, self.vocab), dtype=np.float32)
@@ -288,3 +309,12 @@ def truncate_at_eos(row: np.ndarray) -> np.ndarray:
     """Generate's stop (bend/Generate.bend:31-51): the picks through the first EOS."""
     hit = np.nonzero(row == EOS)[0]
     return row if hit.size == 0 else row[: hit[0] + 1]
+
+
+def window_mean(ce) -> np.float32:
+    """window.mean (bend/Evaluate.bend:46-48): the F32 sum of a window's
+    summands in order, over their count."""
+    acc = np.float32(0.0)
+    for v in np.asarray(ce, dtype=np.float32):
+        acc = np.float32(acc + v)
+    return np.float32(acc / np.float32(max(len(ce), 1)))

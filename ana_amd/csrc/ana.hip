@@ -43,6 +43,10 @@ struct ana_ctx {
   unsigned long long* d_amax = nullptr;  // [wb] greedy argmax keys
   float *d_ss = nullptr, *d_pm = nullptr; // split attention scratch
   float* d_part = nullptr;           // fast attention's per-split partials
+  float* SC = nullptr;               // scoring: the head's logits for up to sc_rows rows
+  uint32_t sc_rows = 1;
+  uint32_t* d_tgt = nullptr;         // scoring: each row's target token
+  float* d_ce = nullptr;             // scoring: each row's G.lse - logit[target]
   float* d_gla = nullptr;            // fast prefill's GLA scan scratch
   GlaScratch gla{};                  // its regions
   GlaSub* d_gtab = nullptr;          // a prefill step's sub-chunk table
@@ -148,7 +152,7 @@ static void release(ana_ctx* c) {
   if (c->gexec_n) (void)hipGraphExecDestroy(c->gexec_n);
   void* ps[] = {c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
-                c->d_ss, c->d_pm, c->d_gtab, c->d_atab, c->d_rseq, c->d_rpos};
+                c->d_ss, c->d_pm, c->d_gtab, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce};
   for (void* p : ps)
     if (p) (void)hipFree(p);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
@@ -213,6 +217,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   c->seg_cap = std::min({c->max_seqs, c->rows, kMaxSegs});
   c->gsub_cap = c->rows / kGlaSub + c->seg_cap;
   c->atab_cap = c->rows / kFlashQ + c->seg_cap;
+  c->sc_rows = std::min(c->rows, kScoreRows);
   const ana_config& cf = c->cfg;
   const uint32_t d = cf.d, hd = d / cf.heads;
   uint64_t off = 0;
@@ -252,6 +257,9 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = dalloc(&c->d_tok, c->rows)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_pick, wb)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_rng, 4 * wb)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->SC, (uint64_t)c->sc_rows * cf.vocab)) != hipSuccess ||
+      (e = dalloc(&c->d_tgt, c->rows)) != hipSuccess || (e = dalloc(&c->d_ce, c->rows)) != hipSuccess)
+    return bad(e);
   if (c->mode != ANA_EXACT_FP32) {
     // the fast kernels' scratch: attention partials for every row of a step,
     // the GLA scan's regions and tables
@@ -572,27 +580,52 @@ extern "C" int ana_feed(ana_ctx* c, uint32_t n, const uint32_t* seq, const uint3
 // attention chunk by chunk, so each sequence ends as n separate dd.feeds
 // would leave it (bit for bit in ANA_EXACT_FP32: products are row-wise the
 // same for any number of rows).
+// the head over rows r0 .. r0 + g of X into SC, for scoring: in exact mode
+// the exact product (row-wise the bits of ana_logits' head), in the fast
+// modes the 128 x 128 matrix-core tiles
+static int score_head(ana_ctx* c, uint32_t r0, uint32_t g) {
+  const ana_config& cf = c->cfg;
+  GemvArgs h = gemv1(c->X + (size_t)r0 * cf.d, cf.d, cf.d, c->W, cf.vocab, c->SC, cf.vocab, g);
+  h.ng = c->W + c->fin;
+  if (fast_mode(c)) {
+    h.Wh0 = c->Wh;
+    HIPCHK(c, launch_gemm_big(h, c->st));
+  } else {
+    HIPCHK(c, launch_gemv(h, c->st));
+  }
+  return ANA_OK;
+}
+
+// With ce (scoring, Evaluate.bend's window.go): sequence i feeds its first
+// len[i] - 1 tokens, and after each fed token t the head's G.lse minus the
+// logit of token t + 1 goes to ce (len[i] - 1 values a sequence, in order).
 static int feeds_n(ana_ctx* c, const char* fn, uint32_t n, const uint32_t* seq, const uint32_t* pos,
-                   const uint32_t* len, const uint32_t* toks) {
+                   const uint32_t* len, const uint32_t* toks, float* ce = nullptr) {
   if (n == 0) return ANA_OK;
   if (!seq || !pos || !len || !toks) return fail(c, ANA_EINVAL, "%s: null argument", fn);
   std::vector<uint8_t> seen(c->max_seqs, 0);
-  std::vector<uint64_t> off(n);
-  uint64_t total = 0;
+  std::vector<uint64_t> off(n), coff(n);
+  std::vector<uint32_t> flen(n);
+  uint64_t total = 0, ctot = 0;
   uint32_t maxlen = 0;
   for (uint32_t i = 0; i < n; i++) {
     if (seq[i] >= c->max_seqs) return fail(c, ANA_EINVAL, "%s: sequence %u outside 0..%u", fn, seq[i], c->max_seqs - 1);
     if (seen[seq[i]]++) return fail(c, ANA_EINVAL, "%s: sequence %u listed twice", fn, seq[i]);
     off[i] = total;
     total += len[i];
-    maxlen = std::max(maxlen, len[i]);
+    flen[i] = ce ? (len[i] ? len[i] - 1 : 0) : len[i];
+    coff[i] = ctot;
+    ctot += ce ? flen[i] : 0;
+    maxlen = std::max(maxlen, flen[i]);
   }
   for (uint64_t i = 0; i < total; i++)
     if (toks[i] >= c->cfg.vocab) return fail(c, ANA_EINVAL, "%s: token %u outside the vocabulary", fn, toks[i]);
   HIPCHK(c, hipSetDevice(c->device));
   const uint32_t d = c->cfg.d;
   std::vector<Seg> segs;
-  std::vector<uint32_t> rows;
+  std::vector<uint32_t> rows, tg;
+  std::vector<uint64_t> cix;
+  std::vector<float> hce;
   auto flush = [&]() -> int {
     if (segs.empty()) return ANA_OK;
     const uint32_t M = (uint32_t)rows.size();
@@ -602,20 +635,39 @@ static int feeds_n(ana_ctx* c, const char* fn, uint32_t n, const uint32_t* seq, 
     for (const Seg& sg : segs)
       HIPCHK(c, hipMemcpyAsync(c->xs + (uint64_t)sg.seq * d, c->X + (uint64_t)(sg.row0 + sg.T - 1) * d,
                                4 * (size_t)d, hipMemcpyDeviceToDevice, c->st));
-    // the host rows are read by the copy above before they change
+    if (ce) {
+      HIPCHK(c, hipMemcpyAsync(c->d_tgt, tg.data(), 4 * (size_t)M, hipMemcpyHostToDevice, c->st));
+      for (uint32_t r0 = 0; r0 < M; r0 += c->sc_rows) {
+        const uint32_t g = std::min(c->sc_rows, M - r0);
+        if (int r = score_head(c, r0, g)) return r;
+        HIPCHK(c, launch_ce(c->SC, c->cfg.vocab, g, c->d_tgt + r0, c->d_ce + r0, c->st));
+      }
+      hce.resize(M);
+      HIPCHK(c, hipMemcpyAsync(hce.data(), c->d_ce, 4 * (size_t)M, hipMemcpyDeviceToHost, c->st));
+    }
+    // the host rows are read by the copies above before they change
     HIPCHK(c, hipStreamSynchronize(c->st));
+    if (ce)
+      for (uint32_t r = 0; r < M; r++) ce[cix[r]] = hce[r];
     segs.clear();
     rows.clear();
+    tg.clear();
+    cix.clear();
     return ANA_OK;
   };
   for (uint32_t t0 = 0; t0 < maxlen; t0 += c->chunk) {
     for (uint32_t i = 0; i < n; i++) {
-      if (len[i] <= t0) continue;
-      const uint32_t T = std::min(c->chunk, len[i] - t0);
+      if (flen[i] <= t0) continue;
+      const uint32_t T = std::min(c->chunk, flen[i] - t0);
       if (rows.size() + T > c->rows || segs.size() == c->seg_cap)
         if (int r = flush()) return r;
       segs.push_back(Seg{seq[i], pos[i] + t0, (uint32_t)rows.size(), T});
       rows.insert(rows.end(), toks + off[i] + t0, toks + off[i] + t0 + T);
+      if (ce)
+        for (uint32_t t = t0; t < t0 + T; t++) {
+          tg.push_back(toks[off[i] + t + 1]);
+          cix.push_back(coff[i] + t);
+        }
     }
     // the next step's chunks start from the states this step leaves
     if (int r = flush()) return r;
@@ -635,6 +687,13 @@ extern "C" int ana_feeds_n(ana_ctx* c, uint32_t n, const uint32_t* seq, const ui
                            const uint32_t* len, const uint32_t* toks) {
   if (!c) return ANA_EINVAL;
   return feeds_n(c, "ana_feeds_n", n, seq, pos, len, toks);
+}
+
+extern "C" int ana_score_n(ana_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+                           const uint32_t* len, const uint32_t* toks, float* ce) {
+  if (!c) return ANA_EINVAL;
+  if (!ce && n) return fail(c, ANA_EINVAL, "ana_score_n: null output");
+  return feeds_n(c, "ana_score_n", n, seq, pos, len, toks, ce);
 }
 
 static int head_of(ana_ctx* c, const char* fn, uint32_t n, const uint32_t* seq) {

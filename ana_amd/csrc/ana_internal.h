@@ -197,6 +197,10 @@ struct PickArgs {
                         // Sample.argmax only when dd.top answers vocab
 };
 hipError_t launch_pick(const PickArgs& a, hipStream_t st);
+// per row b of B logit rows: G.lse(row) - row[tgt[b]] in the tree's order
+// (Evaluate.bend's scoring summand)
+hipError_t launch_ce(const float* logits, uint32_t vocab, uint32_t B, const uint32_t* tgt, float* ce,
+                     hipStream_t st);
 
 // small helpers for the token loop
 hipError_t launch_gather_rows(const float* src, const uint32_t* idx, uint32_t n, uint32_t d,
@@ -243,6 +247,8 @@ hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st);
 constexpr uint32_t kGlaSub = 32;
 // chunks a batched prefill step holds at most
 constexpr uint32_t kMaxSegs = 256;
+// rows the scoring head runs at once (its logits workspace)
+constexpr uint32_t kScoreRows = 512;
 struct GlaSub {
   uint32_t row;   // first workspace row
   uint32_t n;     // tokens (1 .. kGlaSub)

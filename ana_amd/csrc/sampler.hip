@@ -346,6 +346,51 @@ hipError_t launch_advance(const AdvanceArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Evaluate.bend's summand (window.go, bend/Evaluate.bend:33-44): G.lse of
+// the logits minus the target's logit, G.lse = V.max + F32.log(V.sum_exp)
+// (bend/Train/Grad.bend:795-797; bend/Tensor.bend:170-177,292-299) over the
+// logits' tree, one workgroup per row
+template <int LPT>
+__global__ __launch_bounds__(1024) void k_ce(const float* __restrict__ logits, uint32_t vocab,
+                                             const uint32_t* __restrict__ tgt, float* __restrict__ ce,
+                                             uint32_t NT) {
+  __shared__ float red[16];
+  const uint32_t b = blockIdx.x, tid = threadIdx.x, base = tid * LPT;
+  const bool active = tid < NT;
+  const float* lg = logits + (size_t)b * vocab;
+  float x[LPT], pm[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; i++) {
+    const bool in = active && base + i < vocab;
+    x[i] = in ? lg[base + i] : 0.0f;
+    pm[i] = in ? x[i] : -3.0e38f;
+  }
+  const float m = tree_up(local_reduce<LPT>(pm, Max()), Max(), red, tid, NT);
+  float e[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; i++) e[i] = (active && base + i < vocab) ? dexp(x[i] - m) : 0.0f;
+  const float s = tree_up(local_reduce<LPT>(e, Add()), Add(), red, tid, NT);
+  if (tid == 0) ce[b] = (m + dlog(s)) - lg[tgt[b]];
+}
+
+hipError_t launch_ce(const float* logits, uint32_t vocab, uint32_t B, const uint32_t* tgt, float* ce,
+                     hipStream_t st) {
+  if (B == 0) return hipSuccess;
+  uint32_t dv = 0;
+  while ((1ull << dv) < vocab) dv++;
+  const uint64_t vpad = 1ull << dv;
+  const uint32_t lpt = vpad > 1024 ? (uint32_t)(vpad / 1024) : 1u;
+  const uint32_t NT = (uint32_t)(vpad / lpt);
+  switch (lpt) {
+#define ANA_CE(L) \
+  case L: hipLaunchKernelGGL(k_ce<L>, dim3(B), dim3(1024), 0, st, logits, vocab, tgt, ce, NT); break;
+    ANA_CE(1) ANA_CE(2) ANA_CE(4) ANA_CE(8) ANA_CE(16) ANA_CE(32) ANA_CE(64)
+#undef ANA_CE
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_pick(const PickArgs& a, hipStream_t st) {
   uint32_t dv = 0;
   while ((1ull << dv) < a.vocab) dv++;

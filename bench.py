@@ -187,6 +187,23 @@ def run_prefill(path: str, c) -> dict:
                        + "), attention k_attn_flash (fp32 MFMA), GLA k_gla_sub + k_gla_carry",
         }
         log(f"prefill B=64 x 512 {m}: {ntok / dt:.0f} tok/s")
+        # window scoring (Evaluate.bend's window.go through ana_score_n): 64
+        # windows of 513 tokens, the head and G.lse after each of 512
+        with ana_amd.Decoder(path, max_seqs=64, prefill_chunk=128, numerics=MODES[m]) as dec:
+            ws = [ckpt.prompt(2000 + b, 513, c.vocab) for b in range(64)]
+            dec.score_n(list(range(64)), [0] * 64, [w[:65] for w in ws])   # warm-up
+            for b in range(64):
+                dec.reset(b)
+            t = time.perf_counter()
+            ce = dec.score_n(list(range(64)), [0] * 64, ws)
+            dt = time.perf_counter() - t
+        loss = float(np.mean([ana_amd.window_mean(x) for x in ce]))
+        extra[f"score_b64_{m}"] = {
+            "tok_s": round(ntok / dt, 1), "seconds": round(dt, 4), "mean_window_loss": round(loss, 4),
+            "workload": "64 windows x 513 tokens through ana_score_n, chunk 128: prefill plus the "
+                        "head and G.lse - logit[next] on every one of the 32768 positions",
+        }
+        log(f"score B=64 x 512 {m}: {ntok / dt:.0f} tok/s (mean window loss {loss:.4f})")
     return extra
 
 

@@ -106,6 +106,18 @@ int ana_feeds(struct ana_ctx* ctx, uint32_t seq, uint32_t pos, const uint32_t* t
 int ana_feeds_n(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, const uint32_t* pos,
                 const uint32_t* len, const uint32_t* toks);
 
+/* Window scoring, Evaluate.bend's window.go (bend/Evaluate.bend:33-44) for
+ * n sequences: sequence seq[i] feeds its first len[i] - 1 tokens from
+ * pos[i] (as ana_feeds_n would), and after each fed token t, ce receives
+ * G.lse(logits) - logits[token t + 1] (bend/Train/Grad.bend:795-797: the
+ * tree max, plus F32.log of the tree sum of F32.exp(x - max)). ce holds
+ * len[i] - 1 values per sequence, one sequence after another. In
+ * ANA_EXACT_FP32 each value has the bits of ana_feed + ana_logits + that
+ * lse; the fast modes are within their tolerance. The caller forms window
+ * means and bits per byte from them (window.mean, report). */
+int ana_score_n(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+                const uint32_t* len, const uint32_t* toks, float* ce);
+
 /* The head on each listed sequence's last fed token: n x vocab floats,
  * dd.logits (bend/Dense/Decode.bend:641-646). */
 int ana_logits(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, float* out);

@@ -667,6 +667,20 @@ static float t_max(const float* x, uint32_t n, uint32_t base, int p) {
 
 float or_tree_sum(uint32_t n, const float* x) { return t_sum(x, n, 0, tdepth(n)); }
 
+/* Evaluate.bend's summand (window.go, bend/Evaluate.bend:33-44):
+   G.lse(l) - l[y], with G.lse l = V.max l + F32.log (V.sum_exp (V.max l) l)
+   (bend/Train/Grad.bend:795-797), V.max and V.sum_exp the tree reductions
+   of bend/Tensor.bend:170-177,292-299 over the depth-dv tree of the logits */
+float or_ce(uint32_t vocab, const float* logits, uint32_t y) {
+  int dv = tdepth(vocab);
+  float m = t_max(logits, vocab, 0, dv);
+  float* e = (float*)malloc(sizeof(float) * (vocab ? vocab : 1));
+  for (uint32_t i = 0; i < vocab; i++) e[i] = f32exp(logits[i] - m);
+  float sum = t_sum(e, vocab, 0, dv);
+  free(e);
+  return (m + f32log(sum)) - logits[y];
+}
+
 static void t_matvec(const float* W, uint32_t rows, uint32_t cols, const float* x, float* y) {
   int dc = tdepth(cols);
   for (uint32_t r = 0; r < rows; r++) y[r] = t_dot(W + (size_t)r * cols, x, cols, 0, dc);

@@ -100,6 +100,8 @@ uint32_t or_pick(uint32_t vocab, const float* logits, float temp, uint32_t topk,
 float or_topk_threshold(uint32_t vocab, const float* logits, uint32_t topk);
 float or_topp_threshold(uint32_t vocab, const float* w, float topp);
 float or_tree_sum(uint32_t n, const float* x);
+/* G.lse(logits) - logits[y] in the tree's order (Evaluate.bend's summand) */
+float or_ce(uint32_t vocab, const float* logits, uint32_t y);
 
 #ifdef __cplusplus
 }

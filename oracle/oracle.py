@@ -63,6 +63,7 @@ def lib() -> C.CDLL:
             "or_topk_threshold": (C.c_float, [C.c_uint32, f32p, C.c_uint32]),
             "or_topp_threshold": (C.c_float, [C.c_uint32, f32p, C.c_float]),
             "or_tree_sum": (C.c_float, [C.c_uint32, f32p]),
+            "or_ce": (C.c_float, [C.c_uint32, f32p, C.c_uint32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -184,6 +185,12 @@ def tree_argmax(logits: np.ndarray) -> int:
 def tree_sum(x: np.ndarray) -> float:
     a = np.ascontiguousarray(x, dtype=np.float32)
     return lib().or_tree_sum(a.size, _f32p(a))
+
+
+def ce(logits: np.ndarray, y: int) -> float:
+    """G.lse(logits) - logits[y] in the reference's tree order."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    return lib().or_ce(lg.size, _f32p(lg), int(y))
 
 
 def rng_seeded(seed: int) -> np.ndarray:

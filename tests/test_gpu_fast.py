@@ -224,3 +224,27 @@ def test_fast_feeds_n(oracle, small_ckpt, mode, shape):
         worst = max(worst, rel_err(got[i], st.logits()))
     print(f"worst relative error {worst:.3e}", flush=True)
     assert worst <= TOL[mode], worst
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_fast_score_n(oracle, small_ckpt, mode):
+    """ana_score_n in a fast mode: five windows (300 rows in the first
+    step, so the head runs on the 128 x 128 matrix-core tiles); every
+    summand within 2 x tolerance x max|logit| of the oracle's."""
+    print(f"case fast score_n mode {mode}", flush=True)
+    m = oracle.Model(small_ckpt)
+    seqs, lens = [4, 0, 2, 3, 1], [64, 61, 50, 64, 65]
+    rng = np.random.default_rng(43)
+    toks = [rng.integers(0, m.vocab, size=k).astype(np.uint32) for k in lens]
+    with ana_amd.Decoder(small_ckpt, max_seqs=5, prefill_chunk=64, numerics=mode) as dec:
+        got = dec.score_n(seqs, [0] * 5, toks)
+    worst = 0.0
+    for i in range(5):
+        st = oracle.State(m)
+        for k in range(lens[i] - 1):
+            st.feed(k, int(toks[i][k]))
+            lg = st.logits()
+            want = oracle.ce(lg, int(toks[i][k + 1]))
+            worst = max(worst, abs(float(got[i][k]) - want) / float(np.abs(lg).max()))
+    print(f"worst |d ce| / max|logit| {worst:.3e}", flush=True)
+    assert worst <= 2 * TOL[mode], worst

@@ -261,3 +261,39 @@ def test_feeds_n_is_feeds(oracle, ckpts, name):
             assert np.array_equal(bits(got[i]), bits(st.logits())), (i, s)
             for l in range(m.layers):
                 assert np.array_equal(bits(dec.state(s, l)), bits(st.layer(l))), (i, l)
+
+
+@pytest.mark.parametrize("name", list(CFGS))
+def test_score_n_bit_exact(oracle, ckpts, name):
+    """ana_score_n (Evaluate.bend's window.go): four windows of ragged
+    length (one past the ring's wrap, one from a later position) scored
+    together at chunk 16; every summand is, bit for bit, the oracle's
+    G.lse - logit[next] after feeding the window token by token."""
+    path = ckpts[name]
+    print(f"case score_n {name}", flush=True)
+    m = oracle.Model(path)
+    seqs, pos, lens = [2, 0, 3, 1], [0, 0, 5, 0], [41, 2, 30, 80]
+    rng = np.random.default_rng(41)
+    toks = [rng.integers(0, m.vocab, size=n).astype(np.uint32) for n in lens]
+    pre = [rng.integers(0, m.vocab, size=p).astype(np.uint32) for p in pos]
+    with ana_amd.Decoder(path, max_seqs=4, prefill_chunk=16) as dec:
+        for s, p, pr in zip(seqs, pos, pre):
+            if p:
+                dec.feeds(s, 0, pr)
+        got = dec.score_n(seqs, pos, toks)
+    for i in range(len(seqs)):
+        assert got[i].size == lens[i] - 1
+        st = oracle.State(m)
+        for p, t in enumerate(pre[i]):
+            st.feed(p, int(t))
+        want = []
+        for k in range(lens[i] - 1):
+            st.feed(pos[i] + k, int(toks[i][k]))
+            want.append(oracle.ce(st.logits(), int(toks[i][k + 1])))
+        assert np.array_equal(bits(got[i]), bits(np.array(want, np.float32))), i
+    # window.mean over the summands: F32 in order, over their count
+    w = ana_amd.window_mean(got[3])
+    acc = np.float32(0.0)
+    for v in got[3]:
+        acc = np.float32(acc + v)
+    assert w == np.float32(acc / np.float32(got[3].size))

@@ -334,3 +334,36 @@ def test_params_formula():
     assert cf.FP100M.params == 115_435_428
     assert cf.Config(32768, 2048, 768, 3072, 12, 12, False, False, False).params == 143_739_648
     assert cf.V1.params == 12_781_824
+
+
+def _f32max(a, b):
+    # F32.max a b = (a < b ? b : a)
+    return b if a < b else a
+
+
+def test_ce_tree_order(oracle):
+    """or_ce, Evaluate.bend's summand G.lse(l) - l[y] (bend/Train/Grad.bend:
+    795-797): pinned by uniform logits (the tree sum of ones is exact, so
+    the value is log v), by a hand expansion of the depth-3 tree of 5
+    leaves (a sequential sum or another max convention fails some of the
+    random trials), and by a double-precision logsumexp at v = 32768."""
+    f32 = np.float32
+    for v in (258, 32768):
+        lg = np.full(v, 1.25, np.float32)
+        want = f32(f32(f32(1.25) + f32(np.log(np.float64(v)))) - f32(1.25))
+        assert oracle.ce(lg, 7) == want
+    rng = np.random.default_rng(31)
+    for _ in range(200):
+        x = (rng.standard_normal(5) * 3.0).astype(np.float32)
+        y = int(rng.integers(0, 5))
+        vz = f32(-3.0e38)
+        m = _f32max(_f32max(_f32max(x[0], x[1]), _f32max(x[2], x[3])),
+                    _f32max(_f32max(x[4], vz), _f32max(vz, vz)))
+        e = [f32(np.exp(np.float64(f32(xi - m)))) for xi in x]
+        s = f32(f32(f32(e[0] + e[1]) + f32(e[2] + e[3])) + f32(f32(e[4] + f32(0.0)) + f32(0.0)))
+        want = f32(f32(m + f32(np.log(np.float64(s)))) - x[y])
+        assert oracle.ce(x, y) == want, (x, y)
+    x = (rng.standard_normal(32768) * 4.0).astype(np.float32)
+    xd = x.astype(np.float64)
+    ref = np.log(np.exp(xd - xd.max()).sum()) + xd.max() - xd[123]
+    assert abs(oracle.ce(x, 123) - ref) <= 1e-5 * max(1.0, abs(ref))
