@@ -67,6 +67,16 @@ SIGNATURES = {
     "ana_state": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, _f32p, C.c_size_t]),
     "ana_prof": (C.c_int, [C.c_void_p, C.c_int]),
     "ana_prof_read": (C.c_int, [C.c_void_p, C.c_uint32, _u64p, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "ana_bpe_open": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
+    "ana_bpe_bytes": (C.c_int, [C.POINTER(C.c_void_p)]),
+    "ana_bpe_close": (None, [C.c_void_p]),
+    "ana_bpe_vocab": (C.c_uint32, [C.c_void_p]),
+    "ana_bpe_identity": (C.c_int, [C.c_void_p, C.c_char_p, C.c_size_t]),
+    "ana_bpe_encode": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint8), C.c_size_t, _u32p, C.c_size_t,
+                                 C.POINTER(C.c_size_t)]),
+    "ana_bpe_decode": (C.c_int, [C.c_void_p, _u32p, C.c_size_t, C.POINTER(C.c_uint8), C.c_size_t,
+                                 C.POINTER(C.c_size_t)]),
+    "ana_sha256_hex": (C.c_int, [C.POINTER(C.c_uint8), C.c_size_t, C.c_char_p]),
     "ana_error": (C.c_char_p, [C.c_void_p]),
     "ana_close": (None, [C.c_void_p]),
 }
@@ -318,3 +328,107 @@ def window_mean(ce) -> np.float32:
     for v in np.asarray(ce, dtype=np.float32):
         acc = np.float32(acc + v)
     return np.float32(acc / np.float32(max(len(ce), 1)))
+
+
+# ---------------------------------------------------------------- tokenizer
+
+def sha256_hex(data: bytes) -> str:
+    """H.sha256 (bend/Sha256.bend) in the library: 64 lowercase hex digits."""
+    b = (C.c_uint8 * max(len(data), 1)).from_buffer_copy(data or b"\0")
+    out = C.create_string_buffer(65)
+    if lib().ana_sha256_hex(b, len(data), out) != 0:
+        raise AnaError(1, "ana_sha256_hex failed")
+    return out.value.decode()
+
+
+class Tokenizer:
+    """The fast BPE tokenizer (bend/Tokenizer.bend) through libana: ids
+    0 = BOS, 1 = EOS, 2..257 the bytes, then one per merge."""
+
+    BOS, EOS = 0, 1
+
+    def __init__(self, path: str | None = None):
+        h = C.c_void_p()
+        if path is None:
+            rc = lib().ana_bpe_bytes(C.byref(h))
+        else:
+            rc = lib().ana_bpe_open(path.encode(), C.byref(h))
+        if rc != 0:
+            raise AnaError(rc, f"tokenizer: cannot read a BPE artifact from {path}")
+        self.h = h
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().ana_bpe_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def vocab(self) -> int:
+        return int(lib().ana_bpe_vocab(self.h))
+
+    def identity(self) -> str:
+        buf = C.create_string_buffer(512)
+        if lib().ana_bpe_identity(self.h, buf, 512) != 0:
+            raise AnaError(1, "ana_bpe_identity failed")
+        return buf.value.decode()
+
+    def encode(self, data: bytes) -> np.ndarray:
+        """Bpe.encode: the ids of a byte string (no BOS or EOS added)."""
+        b = (C.c_uint8 * max(len(data), 1)).from_buffer_copy(data or b"\0")
+        n = C.c_size_t()
+        lib().ana_bpe_encode(self.h, b, len(data), None, 0, C.byref(n))
+        out = np.zeros(max(n.value, 1), dtype=np.uint32)
+        if lib().ana_bpe_encode(self.h, b, len(data), _p(out, C.c_uint32), out.size, C.byref(n)) != 0:
+            raise AnaError(1, "ana_bpe_encode failed")
+        return out[: n.value]
+
+    def decode(self, ids) -> bytes:
+        """Bpe.decode of each id, concatenated (BOS and EOS give no bytes)."""
+        a = _u32(ids)
+        a1 = a if a.size else np.zeros(1, np.uint32)
+        n = C.c_size_t()
+        lib().ana_bpe_decode(self.h, _p(a1, C.c_uint32), a.size, None, 0, C.byref(n))
+        out = (C.c_uint8 * max(n.value, 1))()
+        if lib().ana_bpe_decode(self.h, _p(a1, C.c_uint32), a.size, out, n.value, C.byref(n)) != 0:
+            raise AnaError(1, "ana_bpe_decode failed")
+        return bytes(out[: n.value])
+
+
+# dc.candidates (bend/Decode.bend:64-66), relative to the working directory
+CANDIDATES = ["weights/enwiki-fineweb-32k.bpe", "run/enwiki-fineweb-32k.bpe",
+              "weights/code32k.bpe", "run/code32k.bpe", "run/enwiki-c4-32k.bpe"]
+BYTE_IDENTITY = "lossless-byte-v1:bos=0:eos=1:bytes=2..257"
+
+
+def find_tokenizer(want: str, pinned: str = "", candidates=None) -> Tokenizer:
+    """dc.tok.of / dc.tok.btc (bend/Decode.bend:80-145,261-270): the byte
+    tokenizer for its identity; else TOKENIZER_FILE (pinned) if set, which
+    must match; else the first candidate whose identity matches. Failures
+    carry the reference's messages."""
+    if want == BYTE_IDENTITY:
+        return Tokenizer(None)
+    if pinned:
+        try:
+            t = Tokenizer(pinned)
+        except AnaError:
+            t = None
+        if t is None or t.identity() != want:
+            raise AnaError(6, "TOKENIZER_FILE identity does not match the checkpoint\n  checkpoint: " + want)
+        return t
+    for p in (CANDIDATES if candidates is None else candidates):
+        if not os.path.exists(p):
+            continue
+        try:
+            t = Tokenizer(p)
+        except AnaError:
+            continue
+        if t.identity() == want:
+            return t
+    raise AnaError(6, "checkpoint uses BPE and no candidate tokenizer matches its identity\n  checkpoint: "
+                   + want + "\n  set TOKENIZER_FILE to the matching .bpe artifact")

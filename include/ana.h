@@ -44,6 +44,7 @@ extern "C" {
 #define ANA_EDEVICE 3    /* HIP error: "device fault" */
 #define ANA_ENOMEM 4     /* device allocation failed */
 #define ANA_EUNSUP 5     /* configuration outside what the kernels handle */
+#define ANA_ETOK 6       /* tokenizer artifact unreadable or rejected (Bpe.parse) */
 
 /* numerics modes */
 #define ANA_EXACT_FP32 0 /* bit-exact with the reference's CPU kernels */
@@ -174,6 +175,34 @@ const char* ana_error(const struct ana_ctx* ctx);
 void ana_close(struct ana_ctx* ctx);
 
 typedef struct ana_ctx ana_ctx;
+
+/* ---- the fast BPE tokenizer (bend/Tokenizer.bend), host side ----
+ * Tokens: 0 = BOS, 1 = EOS, 2..257 the bytes, then one per merge in id
+ * order. The GPU path sees ids only; these serve the prompts and the
+ * outputs around it (dc.tok.of, Bpe.encode, Bpe.decode). */
+struct ana_bpe;
+
+/* Bpe.parse of a .bpe artifact ("BPE <vocab> [v2]", then "a b new" rows,
+ * ids contiguous from 258): ANA_ETOK when unreadable or rejected. */
+int ana_bpe_open(const char* path, struct ana_bpe** out);
+/* the byte tokenizer (no merges, V2 rule; dc.tok.btc, bend/Decode.bend:264-268) */
+int ana_bpe_bytes(struct ana_bpe** out);
+void ana_bpe_close(struct ana_bpe* t);
+uint32_t ana_bpe_vocab(const struct ana_bpe* t);
+/* Bpe.identity (bend/Tokenizer.bend:330-336): "fastbpe-word-v1:bos=0:eos=1:
+ * bytes=2..257:pretoken=<rule>:vocab=<v>:sha256=<digest of the merges>",
+ * NUL-terminated into buf (ANA_EINVAL if cap is too small) */
+int ana_bpe_identity(const struct ana_bpe* t, char* buf, size_t cap);
+/* Bpe.encode (bend/Tokenizer.bend:631-634): pretokenize, then BPE per
+ * word; *nids receives the count, ids the ids when cap holds them
+ * (ANA_EINVAL otherwise, *nids still set) */
+int ana_bpe_encode(const struct ana_bpe* t, const uint8_t* bytes, size_t n, uint32_t* ids, size_t cap,
+                   size_t* nids);
+/* Bpe.decode of each id, concatenated (BOS and EOS give no bytes) */
+int ana_bpe_decode(const struct ana_bpe* t, const uint32_t* ids, size_t n, uint8_t* bytes, size_t cap,
+                   size_t* nbytes);
+/* H.sha256 (bend/Sha256.bend): 64 lowercase hex digits and a NUL */
+int ana_sha256_hex(const uint8_t* bytes, size_t n, char* out65);
 
 #ifdef __cplusplus
 }
