@@ -37,6 +37,19 @@ class _Cfg(C.Structure):
                 ("vocab", "ctx", "d", "f", "layers", "heads", "rglru", "qk", "sinks", "tied")]
 
 
+_MSTR = 1024
+
+
+class _Manifest(C.Structure):
+    _fields_ = [("version", C.c_uint32), ("cfg", _Cfg), ("count", C.c_uint32),
+                ("layout", C.c_char * _MSTR), ("layout_version", C.c_uint32),
+                ("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float), ("eps", C.c_float),
+                ("weight_decay", C.c_float), ("warmup", C.c_uint32), ("total_steps", C.c_uint32),
+                ("has_muon", C.c_uint32), ("muon", C.c_float),
+                ("model_id", C.c_char * _MSTR), ("tokenizer_id", C.c_char * _MSTR),
+                ("dataset_id", C.c_char * _MSTR), ("clip", C.c_float), ("numerics", C.c_uint32)]
+
+
 class _Opts(C.Structure):
     _fields_ = [("device", C.c_int), ("numerics", C.c_int), ("max_seqs", C.c_uint32),
                 ("prefill_chunk", C.c_uint32)]
@@ -77,6 +90,7 @@ SIGNATURES = {
     "ana_bpe_decode": (C.c_int, [C.c_void_p, _u32p, C.c_size_t, C.POINTER(C.c_uint8), C.c_size_t,
                                  C.POINTER(C.c_size_t)]),
     "ana_sha256_hex": (C.c_int, [C.POINTER(C.c_uint8), C.c_size_t, C.c_char_p]),
+    "ana_manifest_read": (C.c_int, [C.c_char_p, C.c_void_p]),
     "ana_error": (C.c_char_p, [C.c_void_p]),
     "ana_close": (None, [C.c_void_p]),
 }
@@ -432,3 +446,19 @@ def find_tokenizer(want: str, pinned: str = "", candidates=None) -> Tokenizer:
             return t
     raise AnaError(6, "checkpoint uses BPE and no candidate tokenizer matches its identity\n  checkpoint: "
                    + want + "\n  set TOKENIZER_FILE to the matching .bpe artifact")
+
+
+def read_manifest(path: str) -> dict:
+    """Load.header's Manifest (bend/Checkpoint.bend:19-136) of an FTC2 file,
+    through the library: every field, the doubles as the reference forms
+    them in F32."""
+    m = _Manifest()
+    r = lib().ana_manifest_read(path.encode(), C.byref(m))
+    if r != 0:
+        raise AnaError(r, lib().ana_error(None).decode())
+    out = {f: getattr(m, f) for f, _ in _Manifest._fields_ if f != "cfg"}
+    for k in ("layout", "model_id", "tokenizer_id", "dataset_id"):
+        out[k] = out[k].decode("utf-8")
+    out["has_muon"] = bool(out["has_muon"])
+    out["cfg"] = {f: int(getattr(m.cfg, f)) for f, _ in _Cfg._fields_}
+    return out

@@ -43,27 +43,33 @@ def _double(x: float) -> bytes:
     return b"\x00" + struct.pack(">i", int(m)) + struct.pack(">q", -k)
 
 
-def manifest_bytes(c: Config, tokenizer_id: str = "", dataset_id: str = "synthetic") -> bytes:
-    """Save.header: magic and manifest (bend/Checkpoint.bend:254-276)."""
+def manifest_bytes(c: Config, tokenizer_id: str = "", dataset_id: str = "synthetic", *,
+                   adamw=(3.0e-4, 0.9, 0.95, 1.0e-8, 0.1, 0, 0), muon=None, clip: float = 1.0,
+                   numerics: int = 0) -> bytes:
+    """Save.header: magic and manifest (bend/Checkpoint.bend:254-276).
+    adamw is (lr, beta1, beta2, eps, decay, warmup, total steps)."""
     out = [struct.pack(">I", MAGIC), struct.pack(">I", MANIFEST_VERSION)]
     out += [_nat(c.vocab), _nat(c.ctx), _nat(c.d), _nat(c.f), _nat(c.layers), _nat(c.heads)]
     out += [bytes([int(c.rglru)]), bytes([int(c.qk)]), bytes([int(c.sinks)]), bytes([int(c.tied)])]
     out += [_nat(c.params), _string(LAYOUT), struct.pack(">I", LAYOUT_VERSION)]
-    # AdamW{lr, beta1, beta2, eps, decay, warmup, total}
-    out += [_double(3.0e-4), _double(0.9), _double(0.95), _double(1.0e-8), _double(0.1), _nat(0), _nat(0)]
-    out += [b"\x00"]  # no Muon
-    out += [_string(c.model_id), _string(tokenizer_id), _string(dataset_id), _double(1.0), b"\x00"]
+    lr, b1, b2, eps, wd, warm, total = adamw
+    out += [_double(lr), _double(b1), _double(b2), _double(eps), _double(wd), _nat(warm), _nat(total)]
+    out += [b"\x00"] if muon is None else [b"\x01", _double(muon)]
+    out += [_string(c.model_id), _string(tokenizer_id), _string(dataset_id), _double(clip),
+            bytes([numerics])]
     return b"".join(out)
 
 
 def write(path: str, c: Config, params: np.ndarray, step: int = 0, tokenizer_id: str = "",
-          moments: bool = False) -> None:
-    """Write an FTC2 checkpoint holding ``params`` (P float32, namedLayout order)."""
+          moments: bool = False, **manifest) -> None:
+    """Write an FTC2 checkpoint holding ``params`` (P float32, namedLayout
+    order); ``manifest`` passes dataset_id, adamw, muon, clip, numerics to
+    manifest_bytes."""
     params = np.ascontiguousarray(params, dtype=np.float32)
     if params.size != c.params:
         raise ValueError(f"params has {params.size} floats, config needs {c.params}")
     with open(path, "wb") as fp:
-        fp.write(manifest_bytes(c, tokenizer_id))
+        fp.write(manifest_bytes(c, tokenizer_id, **manifest))
         fp.write(struct.pack(">Q", c.params))
         chunk = 1 << 24
         for i in range(0, params.size, chunk):

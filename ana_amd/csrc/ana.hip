@@ -290,6 +290,13 @@ extern "C" int ana_config_of(const ana_ctx* c, ana_config* out, uint64_t* step) 
 
 extern "C" const char* ana_error(const ana_ctx* c) { return c ? c->err.c_str() : g_open_err.c_str(); }
 
+extern "C" int ana_manifest_read(const char* path, ana_manifest* out) {
+  if (!path || !out) return fail(nullptr, ANA_EINVAL, "ana_manifest_read: null argument");
+  const std::string why = read_manifest(path, out);
+  if (!why.empty()) return fail(nullptr, ANA_ECKPT, "%s", why.c_str());
+  return ANA_OK;
+}
+
 extern "C" void ana_close(ana_ctx* c) {
   if (!c) return;
   (void)hipStreamSynchronize(c->st);

@@ -31,6 +31,8 @@ struct Ftc2 {
 };
 // Returns "" on success, else the reference's message.
 std::string read_ftc2(const char* path, Ftc2* out);
+// the manifest alone ("" or the reason it could not be read)
+std::string read_manifest(const char* path, ana_manifest* out);
 
 // ---------------------------------------------------------------- kernels
 // Every kernel computes in IEEE f32 with products and sums rounded

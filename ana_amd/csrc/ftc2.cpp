@@ -4,6 +4,7 @@
 // bend/Dense/Ckpt.bend:21-34 (u64 count, P big-endian f32, Adam step, ...).
 // Validation and messages: Manifest.problem (bend/Checkpoint.bend:162-170)
 // and dd.load (bend/Dense/Decode.bend:664-699).
+#include <math.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -93,14 +94,72 @@ struct Cur {
     }
     return s;
   }
-  void dbl() {  // Load.double: Integer (small or big), then Int64
-    if (be(1) == 0) be(4);
-    else { be(1); const uint32_t k = nat(); for (uint32_t i = 0; i < k && !bad; i++) be(1); }
-    be(8);
+  // Load.double (bend/Checkpoint.bend:54-81): an Integer (tag 0: Int32;
+  // tag 1: sign byte, byte count, little-endian bytes) times 2 to an Int64,
+  // in F32 as the reference forms it: signed.f32 and le.f32
+  // (bend/Parse.bend:71-79,171-186), then m * F32.pow(2, e)
+  float dbl() {
+    float m;
+    if (be(1) == 0) {
+      m = signed_f32((uint32_t)be(4));
+    } else {
+      const uint32_t s = (uint32_t)be(1);
+      const uint32_t k = nat();
+      std::vector<uint8_t> bs;
+      for (uint32_t i = 0; i < k && !bad; i++) bs.push_back((uint8_t)be(1));
+      float f = 0.0f;
+      for (size_t i = bs.size(); i-- > 0;) f = (float)bs[i] + 256.0f * f;
+      m = s == 1 ? f : -f;
+    }
+    const float e = signed_f32((uint32_t)be(8));
+    return m * (float)pow(2.0, (double)e);
   }
+  static float signed_f32(uint32_t x) { return x >= 2147483648u ? -(float)(~x + 1u) : (float)x; }
 };
 
+void copy_str(char* dst, const std::string& s) {
+  const size_t n = s.size() < ANA_MANIFEST_STR - 1 ? s.size() : ANA_MANIFEST_STR - 1;
+  memcpy(dst, s.data(), n);
+  dst[n] = 0;
+}
+
+// Load.header's manifest after the magic (bend/Checkpoint.bend:100-136)
+void parse_manifest(Cur& c, ana_manifest* m) {
+  memset(m, 0, sizeof *m);
+  m->version = (uint32_t)c.be(4);
+  ana_config& cf = m->cfg;
+  cf.vocab = c.nat(); cf.ctx = c.nat(); cf.d = c.nat(); cf.f = c.nat();
+  cf.layers = c.nat(); cf.heads = c.nat();
+  cf.rglru = c.be(1) != 0; cf.qk = c.be(1) != 0; cf.sinks = c.be(1) != 0; cf.tied = c.be(1) != 0;
+  m->count = c.nat();
+  copy_str(m->layout, c.str());
+  m->layout_version = (uint32_t)c.be(4);
+  m->lr = c.dbl(); m->beta1 = c.dbl(); m->beta2 = c.dbl(); m->eps = c.dbl(); m->weight_decay = c.dbl();
+  m->warmup = c.nat();
+  m->total_steps = c.nat();
+  m->has_muon = c.be(1) != 0;
+  if (m->has_muon) m->muon = c.dbl();
+  copy_str(m->model_id, c.str());
+  copy_str(m->tokenizer_id, c.str());
+  copy_str(m->dataset_id, c.str());
+  m->clip = c.dbl();
+  m->numerics = (uint32_t)c.be(1);
+}
+
 }  // namespace
+
+std::string read_manifest(const char* path, ana_manifest* out) {
+  FILE* fp = fopen(path, "rb");
+  if (!fp) return std::string("checkpoint: cannot open ") + path;
+  std::vector<uint8_t> head(1 << 16);
+  head.resize(fread(head.data(), 1, head.size(), fp));
+  fclose(fp);
+  Cur c{head.data(), head.size(), 0, false};
+  if ((uint32_t)c.be(4) != 1179927346u || c.bad) return "not a compact checkpoint (magic is not FTC2)";
+  parse_manifest(c, out);
+  if (c.bad) return "checkpoint: short read";
+  return "";
+}
 
 std::string read_ftc2(const char* path, Ftc2* out) {
   FILE* fp = fopen(path, "rb");
@@ -114,22 +173,13 @@ std::string read_ftc2(const char* path, Ftc2* out) {
     fclose(fp);
     return "not a compact checkpoint (magic is not FTC2)";
   }
-  const uint32_t version = (uint32_t)c.be(4);
-  ana_config cf{};
-  cf.vocab = c.nat(); cf.ctx = c.nat(); cf.d = c.nat(); cf.f = c.nat();
-  cf.layers = c.nat(); cf.heads = c.nat();
-  cf.rglru = c.be(1) != 0; cf.qk = c.be(1) != 0; cf.sinks = c.be(1) != 0; cf.tied = c.be(1) != 0;
-  const uint32_t count = c.nat();
-  const std::string lay = c.str();
-  const uint32_t lv = (uint32_t)c.be(4);
-  for (int i = 0; i < 5; i++) c.dbl();
-  c.nat(); c.nat();
-  if (c.be(1)) c.dbl();
-  const std::string mid = c.str();
-  c.str();
-  c.str();
-  c.dbl();
-  c.be(1);
+  ana_manifest man;
+  parse_manifest(c, &man);
+  const uint32_t version = man.version;
+  const ana_config cf = man.cfg;
+  const uint32_t count = man.count;
+  const std::string lay = man.layout, mid = man.model_id;
+  const uint32_t lv = man.layout_version;
   if (c.bad) { fclose(fp); return "checkpoint: short read"; }
   const size_t h = c.at;
   if (version != 4) { fclose(fp); return "checkpoint: unsupported checkpoint manifest version (this branch reads version 4)"; }

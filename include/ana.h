@@ -176,6 +176,32 @@ void ana_close(struct ana_ctx* ctx);
 
 typedef struct ana_ctx ana_ctx;
 
+/* ---- the FTC2 manifest (bend/Checkpoint.bend:19-136) ----
+ * Every field of Load.header's Manifest; the doubles as the reference forms
+ * them in F32 (Load.double). Strings are UTF-8, NUL-terminated, cut at
+ * ANA_MANIFEST_STR - 1 bytes. tokenizer_id names the tokenizer a caller
+ * finds by identity (dc.tok.of). */
+#define ANA_MANIFEST_STR 1024
+typedef struct ana_manifest {
+  uint32_t version;
+  ana_config cfg;
+  uint32_t count;                       /* the parameter count field */
+  char layout[ANA_MANIFEST_STR];
+  uint32_t layout_version;
+  float lr, beta1, beta2, eps, weight_decay;   /* AdamW */
+  uint32_t warmup, total_steps;
+  uint32_t has_muon;
+  float muon;
+  char model_id[ANA_MANIFEST_STR], tokenizer_id[ANA_MANIFEST_STR], dataset_id[ANA_MANIFEST_STR];
+  float clip;
+  uint32_t numerics;
+} ana_manifest;
+
+/* Load.header's manifest of an FTC2 file, without Manifest.problem's
+ * verdict (ana_open applies that): ANA_ECKPT and ana_error(NULL) on an
+ * unreadable file, a wrong magic or a short header. */
+int ana_manifest_read(const char* path, ana_manifest* out);
+
 /* ---- the fast BPE tokenizer (bend/Tokenizer.bend), host side ----
  * Tokens: 0 = BOS, 1 = EOS, 2..257 the bytes, then one per merge in id
  * order. The GPU path sees ids only; these serve the prompts and the

@@ -297,3 +297,60 @@ def test_score_n_bit_exact(oracle, ckpts, name):
     for v in got[3]:
         acc = np.float32(acc + v)
     assert w == np.float32(acc / np.float32(got[3].size))
+
+
+def test_text_end_to_end(oracle, tmp_path):
+    """Text in, text out: a checkpoint naming its tokenizer by identity
+    (a synthetic artifact of 42 merges; model vocab 300); the manifest read,
+    the tokenizer found by that identity (dc.tok.of), BOS plus the encoded
+    prompt fed, 12 greedy ids from the device loop, bit for bit the oracle's
+    greedy ids, decoded back to bytes."""
+    print("case text end to end", flush=True)
+    text = b"The history of the city of Paris"
+    # merges: the prompt's most frequent adjacent byte pairs, then pairs of those
+    xs = [b + 2 for b in text]
+    rows, nxt = [], 258
+    while nxt < 300:
+        cnt = {}
+        for i in range(len(xs) - 1):
+            cnt[(xs[i], xs[i + 1])] = cnt.get((xs[i], xs[i + 1]), 0) + 1
+        if not cnt:
+            break
+        pair = max(sorted(cnt), key=lambda p: cnt[p])
+        rows.append((pair[0], pair[1], nxt))
+        ys, i = [], 0
+        while i < len(xs):
+            if i + 1 < len(xs) and (xs[i], xs[i + 1]) == pair:
+                ys.append(nxt); i += 2
+            else:
+                ys.append(xs[i]); i += 1
+        xs, nxt = ys, nxt + 1
+    while nxt < 300:   # pad with pairs of bytes the prompt lacks
+        rows.append((200 + nxt - 258, 201, nxt)); nxt += 1
+    art = tmp_path / "t.bpe"
+    art.write_text("BPE 300 v2\n" + "".join(f"{a} {b} {n}\n" for a, b, n in rows))
+    tok = ana_amd.Tokenizer(str(art))
+    c = cf.Config(300, 64, 64, 192, 4, 4, True, True, True)
+    path = str(tmp_path / "m.ftc2")
+    ckpt.write(path, c, ckpt.init_params(c, "normal", 3), tokenizer_id=tok.identity())
+    man = ana_amd.read_manifest(path)
+    t = ana_amd.find_tokenizer(man["tokenizer_id"], candidates=[str(art)])
+    prompt = [ana_amd.Tokenizer.BOS] + [int(i) for i in t.encode(text)]
+    assert t.decode(prompt) == text and len(prompt) < len(text)
+    with ana_amd.Decoder(path, max_seqs=1, prefill_chunk=8) as dec:
+        dec.feeds(0, 0, prompt[:-1])
+        got = dec.generate([0], [len(prompt) - 1], [prompt[-1]], 12)[0]
+    m = oracle.Model(path)
+    st = oracle.State(m)
+    for p, i in enumerate(prompt):
+        st.feed(p, i)
+    want, pos = [], len(prompt)
+    nxt_id = oracle.top(st.logits())
+    for _ in range(12):
+        want.append(nxt_id)
+        st.feed(pos, nxt_id)
+        pos += 1
+        nxt_id = oracle.top(st.logits())
+    assert [int(x) for x in got] == want
+    out = t.decode(got)
+    assert isinstance(out, bytes)

@@ -238,3 +238,57 @@ def test_find_tokenizer(tmp_path):
         ana_amd.find_tokenizer(want, pinned=paths[0])
     with pytest.raises(ana_amd.AnaError, match="no candidate tokenizer matches"):
         ana_amd.find_tokenizer(want + "x", candidates=paths)
+
+
+def test_manifest_round_trip_and_discovery(tmp_path):
+    """Every manifest field through ckpt.write and ana_manifest_read (the
+    doubles as F32), and the checkpoint's tokenizer found by identity."""
+    from ana_amd import ckpt, config as cf
+    tok = ana_amd.Tokenizer(os.path.join(BPE, "code32k.bpe"))
+    p = str(tmp_path / "m.ftc2")
+    c = cf.SMALL4_V3
+    ckpt.write(p, c, ckpt.init_params(c, "hash"), tokenizer_id=tok.identity(), dataset_id="enwik8-test",
+               adamw=(6.0e-4, 0.9, 0.98, 1.0e-9, 0.05, 200, 12000), muon=0.02, clip=0.5, numerics=1)
+    m = ana_amd.read_manifest(p)
+    f32 = np.float32
+    assert (m["version"], m["count"], m["layout"], m["layout_version"]) == \
+        (4, c.params, "hybrid-gla-decoder-flat-parameters", 3)
+    assert m["cfg"] == {"vocab": 258, "ctx": 64, "d": 64, "f": 192, "layers": 4, "heads": 4,
+                        "rglru": 1, "qk": 1, "sinks": 1, "tied": 1}
+    assert [f32(m[k]) for k in ("lr", "beta1", "beta2", "eps", "weight_decay")] == \
+        [f32(6.0e-4), f32(0.9), f32(0.98), f32(1.0e-9), f32(0.05)]
+    assert (m["warmup"], m["total_steps"], m["has_muon"], f32(m["muon"])) == (200, 12000, True, f32(0.02))
+    assert (m["model_id"], m["dataset_id"], f32(m["clip"]), m["numerics"]) == \
+        (c.model_id, "enwik8-test", f32(0.5), 1)
+    assert ana_amd.find_tokenizer(m["tokenizer_id"],
+                                  candidates=[os.path.join(BPE, a) for a in ARTS]).identity() == tok.identity()
+
+
+def test_manifest_big_integer_double(tmp_path):
+    """Load.double with a big Integer mantissa (a Double's decodeFloat, as
+    the Haskell master writes it): sign byte, byte count, little-endian
+    bytes, folded in F32 by le.f32, times F32.pow(2, e)."""
+    import math
+    import struct
+    from ana_amd import ckpt, config as cf
+    c = cf.SMALL4_V3
+    base = ckpt.manifest_bytes(c)
+    lr = ckpt._double(3.0e-4)
+    i = base.index(lr)
+    fr, ex = math.frexp(3.0e-4)
+    mant, e = int(fr * (1 << 53)), ex - 53
+    bs = mant.to_bytes((mant.bit_length() + 7) // 8, "little")
+    big = b"\x01" + b"\x01" + struct.pack(">Q", len(bs)) + bs + struct.pack(">q", e)
+    p = tmp_path / "b.ftc2"
+    p.write_bytes(base[:i] + big + base[i + len(lr):])
+    want = np.float32(0.0)
+    for b in reversed(bs):
+        want = np.float32(np.float32(b) + np.float32(np.float32(256.0) * want))
+    want = np.float32(want * np.float32(2.0 ** e))
+    got = ana_amd.read_manifest(str(p))["lr"]
+    assert np.float32(got) == want
+    assert abs(got - 3.0e-4) <= 1e-6 * 3.0e-4
+    with pytest.raises(ana_amd.AnaError, match="magic"):
+        q = tmp_path / "x.ftc2"
+        q.write_bytes(b"XXXX" + base[4:])
+        ana_amd.read_manifest(str(q))
