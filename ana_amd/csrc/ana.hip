@@ -396,7 +396,7 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
   const bool chunk = segs != nullptr;
   // a fast mode's prefill step: the GLA scan's sub-chunk table and each row's
   // sequence and position, uploaded once for every layer
-  uint32_t nsub = 0, nsp = 0;
+  uint32_t nsub = 0;
   bool fresh_all = true;
   if (chunk && fast_mode(c)) {
     if (segs->size() > c->seg_cap) return fail(c, ANA_EINVAL, "prefill step of %zu chunks (at most %u)", segs->size(), c->seg_cap);
@@ -404,7 +404,6 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
     c->h_atab.clear();
     c->h_rseq.resize(B);
     c->h_rpos.resize(B);
-    uint64_t maxp = 0;
     for (uint32_t si = 0; si < segs->size(); si++) {
       const Seg& sg = (*segs)[si];
       const uint32_t ns = (sg.T + kGlaSub - 1) / kGlaSub;
@@ -418,11 +417,9 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
         c->h_atab.push_back(AttnTile{sg.seq, sg.pos0 + t, sg.row0 + t, std::min(kFlashQ, sg.T - t)});
       const uint64_t last = (uint64_t)sg.pos0 + sg.T - 1;
       if (last >= cf.ctx) fresh_all = false;
-      maxp = std::max(maxp, last);
     }
     nsub = (uint32_t)c->h_gtab.size();
     if (nsub > c->gsub_cap) return fail(c, ANA_EINVAL, "prefill step of %u sub-chunks (at most %u)", nsub, c->gsub_cap);
-    nsp = (uint32_t)(std::min<uint64_t>(maxp, cf.ctx - 1) / kFastTS + 1);
     if (c->h_atab.size() > c->atab_cap) return fail(c, ANA_EINVAL, "prefill step of %zu attention tiles (at most %u)", c->h_atab.size(), c->atab_cap);
     if (fresh_all && !c->h_atab.empty())
       HIPCHK(c, hipMemcpyAsync(c->d_atab, c->h_atab.data(), sizeof(AttnTile) * c->h_atab.size(), hipMemcpyHostToDevice, c->st));
