@@ -47,6 +47,8 @@ struct ana_ctx {
   uint32_t sc_rows = 1;
   uint32_t* d_tgt = nullptr;         // scoring: each row's target token
   float* d_ce = nullptr;             // scoring: each row's G.lse - logit[target]
+  __bf16 *d_sah = nullptr, *d_sal = nullptr;  // ANA_BF16 prefill: a product's split activations
+  float* d_rsc = nullptr;                      // and its rows' norm scales
   float* d_gla = nullptr;            // fast prefill's GLA scan scratch
   GlaScratch gla{};                  // its regions
   GlaSub* d_gtab = nullptr;          // a prefill step's sub-chunk table
@@ -152,7 +154,8 @@ static void release(ana_ctx* c) {
   if (c->gexec_n) (void)hipGraphExecDestroy(c->gexec_n);
   void* ps[] = {c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
-                c->d_ss, c->d_pm, c->d_gtab, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce};
+                c->d_ss, c->d_pm, c->d_gtab, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce,
+                c->d_sah, c->d_sal, c->d_rsc};
   for (void* p : ps)
     if (p) (void)hipFree(p);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
@@ -270,7 +273,12 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
       return bad(e);
     c->gla = gla_scan_carve(c->d_gla, c->rows, c->gsub_cap, c->seg_cap, d, cf.heads);
   }
-  if (c->mode == ANA_BF16 && (e = dalloc(&c->Wh, c->P)) != hipSuccess) return bad(e);
+  if (c->mode == ANA_BF16) {
+    const uint64_t kmax = std::max(d, cf.f);
+    if ((e = dalloc(&c->Wh, c->P)) != hipSuccess || (e = dalloc(&c->d_sah, (uint64_t)c->rows * kmax)) != hipSuccess ||
+        (e = dalloc(&c->d_sal, (uint64_t)c->rows * kmax)) != hipSuccess || (e = dalloc(&c->d_rsc, c->rows)) != hipSuccess)
+      return bad(e);
+  }
   if ((e = hipMemcpyAsync(c->W, ck.raw.data(), 4 * c->P, hipMemcpyHostToDevice, c->st)) != hipSuccess) return bad(e);
   if ((e = launch_bswap(reinterpret_cast<uint32_t*>(c->W), c->P, c->st)) != hipSuccess) return bad(e);
   if (c->Wh && (e = launch_to_bf16(c->W, c->Wh, c->P, c->st)) != hipSuccess) return bad(e);
@@ -327,18 +335,18 @@ static double gemv_bytes(const GemvArgs& g) {
 
 // The fast modes: decode steps of B <= kSmallB sequences stream bf16
 // (ANA_BF16) or fp32 rows with split-K sums and take the reassociated GLA and
-// attention kernels; prefill chunks of more than kSmallB rows run their
-// products on the matrix cores. Decode steps of more sequences, the head over
-// more than kSmallB rows and prefill chunks of kSmallB rows or fewer run the
-// exact kernels (those paths faulted the GPU in their first test and stay off
-// until the cause is found). Prefill chunks of more than kSmallB rows also
-// take the closed-form GLA chunk and the split attention.
+// attention kernels. Prefill steps of more than kSmallB rows, and the layer
+// products of decode steps of more sequences, run on the matrix cores. The
+// decode steps of more sequences keep the exact GLA, attention and head, and
+// prefill steps of kSmallB rows or fewer the exact kernels: the matrix-core
+// head and the fast GLA and attention above kSmallB decode rows faulted the
+// GPU in their first test and stay off until the cause is found.
 static bool fast_mode(const ana_ctx* c) { return c->mode != ANA_EXACT_FP32; }
 static bool fast_path(const ana_ctx* c, uint32_t B) { return fast_mode(c) && B <= kSmallB; }
 
 static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool chunk = false) {
   const bool small = g0.B <= kSmallB;
-  if (fast_mode(c) && (chunk ? !small : small)) {
+  if (fast_mode(c) && (small ? !chunk : (chunk || kind != ANA_K_HEAD))) {
     GemvArgs g = g0;
     if (c->Wh) {
       g.Wh0 = c->Wh + (g.seg[0].W - c->W);
@@ -348,6 +356,8 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
     if (c->Wh) by -= 2.0 * (g.seg[0].rows + (g.nseg > 1 ? g.seg[1].rows : 0)) * g.K;
     ProfScope ps(c, kind, by, true);
     if (small) return launch_gemv_fast(g, c->st, ps.start(), ps.stop());
+    if (g.B >= 128 && c->d_sah && g.K % 32 == 0 && g.B <= c->rows)
+      return launch_gemm_dl(g, c->d_sah, c->d_sal, c->d_rsc, c->st, ps.start(), ps.stop());
     if (g.B >= 128) return launch_gemm_big(g, c->st, ps.start(), ps.stop());
     return launch_gemm_mfma(g, c->st, ps.start(), ps.stop());
   }

@@ -1459,3 +1459,235 @@ hipError_t launch_gemm_big(const GemvArgs& a, hipStream_t st, hipEvent_t e0, hip
 }
 
 }  // namespace ana
+
+namespace ana {
+
+// ------------------------------------------------------------------ bf16 prefill products, direct to LDS
+
+// The activations of an ANA_BF16 prefill product as two bf16 arrays: each
+// value (times the norm's gain) rounded to nearest even (the head) and what
+// is left of it (the remainder); with a gain, also each row's norm scale
+// 1 / sqrt(ss / K + 1e-5) over the unscaled row. One wave a row.
+__global__ __launch_bounds__(256) void k_split(const float* __restrict__ X, uint32_t ldx, uint32_t K,
+                                                const float* __restrict__ g, uint32_t M,
+                                                __bf16* __restrict__ Ah, __bf16* __restrict__ Al,
+                                                float* __restrict__ rsc) {
+  const uint32_t m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (m >= M) return;
+  const float* x = X + (size_t)m * ldx;
+  float ss = 0.0f;
+  for (uint32_t k = 4 * lane; k < K; k += 256) {
+    float4 v = *reinterpret_cast<const float4*>(x + k);
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    if (g) {
+      const float4 gg = *reinterpret_cast<const float4*>(g + k);
+      v.x *= gg.x;
+      v.y *= gg.y;
+      v.z *= gg.z;
+      v.w *= gg.w;
+    }
+    __bf16 h[4] = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+    __bf16 l[4] = {(__bf16)(v.x - (float)h[0]), (__bf16)(v.y - (float)h[1]), (__bf16)(v.z - (float)h[2]),
+                   (__bf16)(v.w - (float)h[3])};
+    *reinterpret_cast<uint2*>(Ah + (size_t)m * K + k) = *reinterpret_cast<const uint2*>(h);
+    *reinterpret_cast<uint2*>(Al + (size_t)m * K + k) = *reinterpret_cast<const uint2*>(l);
+  }
+  if (g) {
+    ss = wave_sum(ss);
+    if (lane == 0) rsc[m] = 1.0f / sqrtf(ss / (float)K + 1.0e-5f);
+  }
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// vmcnt(n) alone (expcnt and lgkmcnt at their maxima)
+#define ANA_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
+
+// Workgroup -> (n tile, m tile) so that the workgroups one XCD runs (ids
+// equal mod 8) take consecutive tiles, n fastest: the A rows those n tiles
+// share stay in that XCD's L2.
+__device__ __forceinline__ void xcd_tile(uint32_t* nt, uint32_t* mt) {
+  const uint32_t NT = gridDim.x, total = gridDim.x * gridDim.y;
+  const uint32_t L = blockIdx.x + blockIdx.y * NT;
+  const uint32_t x = L % 8, idx = L / 8, per = total / 8, rem = total % 8;
+  const uint32_t g = (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + idx;
+  *nt = g % NT;
+  *mt = g / NT;
+}
+
+// Y[m][n] = sum_k A[m][k] W[n][k] for ANA_BF16 prefill steps of >= 128 rows,
+// A given as split head and remainder (k_split): a 128 x 128 tile per
+// workgroup, four waves of 64 x 64 (4 x 4 v_mfma_f32_16x16x32_bf16 tiles,
+// head then remainder each step). K goes in stages of 32 through a ring of
+// three LDS stages filled by global_load_lds_dwordx4 (no registers between
+// global memory and LDS): each stage holds the head, remainder and weight
+// tiles as 1 KB chunks of 16 rows, a row's four 16-byte k pieces at
+// physical slot (piece ^ ((row >> 1) & 3)), so a fragment read touches
+// eight distinct 16-byte bank groups. A wave waits on its own loads of the
+// stage it is about to read, then a barrier (no fence, which would wait on
+// every load in flight) makes the other waves' loads visible; loads of the
+// stage two ahead go out right after it. Norm scale, residual and SiLU as in
+// k_gemm_big.
+template <int NS>
+__global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __restrict__ Ahg,
+                                                  const __bf16* __restrict__ Alg,
+                                                  const float* __restrict__ rscg) {
+  constexpr int BM = 128, BN = 128, BK = 32;
+  constexpr int TILE = BM * BK;   // bf16 elements of one operand tile (8 KB)
+  __shared__ __align__(1024) __bf16 lds[NS][3][TILE];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t wm = wv >> 1, wn = wv & 1;
+  uint32_t ntile, mtile;
+  xcd_tile(&ntile, &mtile);
+  const uint32_t m0 = mtile * BM;
+  const uint32_t nb = min((uint32_t)BM, a.B - m0);
+  const uint32_t K = a.K, nst = K / BK;
+  const Segs sgs(a);
+  // this lane's piece in each of the wave's two 1 KB chunks per operand:
+  // chunk c = 2 wv + h covers tile rows 16 c .. 16 c + 15
+  const uint32_t pr = lane >> 2, pq = (lane & 3) ^ ((pr >> 1) & 3);
+  uint32_t aoff[2];
+  const uint16_t* bptr[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const uint32_t r = 16 * (2 * wv + h) + pr;
+    aoff[h] = (m0 + (r < nb ? r : 0)) * K + 8 * pq;
+    const float* w;
+    uint32_t sg, lr;
+    const bool ok = sgs.row(BN, ntile, r, &w, &sg, &lr);
+    bptr[h] = ok ? (sg ? a.Wh1 : a.Wh0) + (size_t)lr * K + 8 * pq : a.Wh0 + 8 * pq;
+  }
+  auto issue = [&](uint32_t s) {
+    const int buf = s % NS;
+    const uint32_t k0 = s * BK;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const uint32_t c = 2 * wv + h;
+      __builtin_amdgcn_global_load_lds((const void*)(Ahg + aoff[h] + k0), (lds_void*)&lds[buf][0][c * 512], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(Alg + aoff[h] + k0), (lds_void*)&lds[buf][1][c * 512], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(bptr[h] + k0), (lds_void*)&lds[buf][2][c * 512], 16, 0, 0);
+    }
+  };
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t r16 = lane & 15, g4 = lane >> 4;
+  // fragment read offset (elements) inside a 16-row chunk
+  const uint32_t foff = r16 * 32 + 8 * (g4 ^ ((r16 >> 1) & 3));
+#pragma unroll
+  for (int u = 0; u < NS - 1; u++)
+    if ((uint32_t)u < nst) issue(u);
+  for (uint32_t s = 0; s < nst; s++) {
+    // this wave's loads of stage s are done (6 loads a stage; those of the
+    // NS - 2 later stages may still fly)
+    if (s + NS - 2 < nst) ANA_VMCNT(6 * (NS - 2));
+    else ANA_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+    if (s + NS - 1 < nst) issue(s + NS - 1);
+    const int buf = s % NS;
+    const __bf16* A0 = &lds[buf][0][0];
+    const __bf16* A1 = &lds[buf][1][0];
+    const __bf16* B0 = &lds[buf][2][0];
+    bf16x8_t bfr[4], ah[4], al[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(B0 + (wn * 4 + j) * 512 + foff);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      ah[i] = *reinterpret_cast<const bf16x8_t*>(A0 + (wm * 4 + i) * 512 + foff);
+      al[i] = *reinterpret_cast<const bf16x8_t*>(A1 + (wm * 4 + i) * 512 + foff);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bfr[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bfr[j], acc[i][j], 0, 0, 0);
+      }
+  }
+  const bool norm = a.ng != nullptr;
+  // results: tile (i, j) of the wave holds rows wm*64 + 16i + 4*g4 + r,
+  // column wn*64 + 16j + r16
+  if (a.mode == GM_SILU) {
+    // up columns (wn = 1) through LDS to the gate columns (wn = 0), one
+    // 64-row half at a time
+    ANA_VMCNT(0);
+    __syncthreads();
+    float* up = reinterpret_cast<float*>(&lds[0][0][0]);
+    for (uint32_t half = 0; half < 2; half++) {
+      if (wn == 1 && wm == half) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              const uint32_t ml = 16 * i + 4 * g4 + r, n = 16 * j + r16, m = wm * 64 + ml;
+              float y = acc[i][j][r];
+              if (norm) y *= rscg[m0 + (m < nb ? m : 0)];
+              up[ml * 64 + n] = y;
+            }
+      }
+      __syncthreads();
+      if (wn == 0 && wm == half) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const uint32_t n = 16 * j + r16;
+          const float* w_;
+          uint32_t sg, lr;
+          if (!sgs.row(BN, ntile, n, &w_, &sg, &lr)) continue;
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              const uint32_t ml = 16 * i + 4 * g4 + r, m = wm * 64 + ml;
+              if (m >= nb) continue;
+              float y = acc[i][j][r];
+              if (norm) y *= rscg[m0 + m];
+              a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = fast_silu(y) * up[ml * 64 + n];
+            }
+        }
+      }
+      __syncthreads();
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t n = wn * 64 + 16 * j + r16;
+    const float* w_;
+    uint32_t sg, lr;
+    if (!sgs.row(BN, ntile, n, &w_, &sg, &lr)) continue;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r;
+        if (m >= nb) continue;
+        float y = acc[i][j][r];
+        if (norm) y *= rscg[m0 + m];
+        if (a.mode == GM_RESID) y = a.R[(size_t)(m0 + m) * a.ldr + lr] + y;
+        if (sg) a.seg[1].Y[(size_t)(m0 + m) * a.seg[1].ldy + lr] = y;
+        else a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = y;
+      }
+  }
+}
+
+hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, __bf16* Al, float* rsc, hipStream_t st,
+                          hipEvent_t e0, hipEvent_t e1) {
+  if (a.amax || (a.K % 32) || a.B == 0 || !a.Wh0 || (a.nseg > 1 && !a.Wh1)) return hipErrorInvalidValue;
+  // the split first (its time is inside the events)
+  if (e0) (void)hipEventRecord(e0, st);
+  hipLaunchKernelGGL(k_split, dim3((a.B + 3) / 4), dim3(256), 0, st, a.X, a.ldx, a.K, a.ng, a.B, Ah, Al, rsc);
+  const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
+                                          : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
+  const uint32_t per = a.mode == GM_SILU ? 64 : 128;
+  const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
+  dim3 grid(tiles, (a.B + 127) / 128);
+  hipLaunchKernelGGL(k_gemm_dl<3>, grid, dim3(256), 0, st, a, Ah, Al, rsc);
+  if (e1) (void)hipEventRecord(e1, st);
+  return hipGetLastError();
+}
+
+}  // namespace ana

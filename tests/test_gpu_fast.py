@@ -248,3 +248,38 @@ def test_fast_score_n(oracle, small_ckpt, mode):
             worst = max(worst, abs(float(got[i][k]) - want) / float(np.abs(lg).max()))
     print(f"worst |d ce| / max|logit| {worst:.3e}", flush=True)
     assert worst <= 2 * TOL[mode], worst
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_fast_decode_batch_products(oracle, small_ckpt, mode):
+    """Decode steps of more than kSmallB sequences in a fast mode: the layer
+    products on the matrix cores (the prefill kernels, one row a sequence),
+    GLA, attention and head exact. Seven sequences from ragged starts, 70
+    teacher-forced steps across the ring wrap; every sequence's logits
+    against its own oracle run at four steps."""
+    print(f"case fast decode batch products mode {mode}", flush=True)
+    m = oracle.Model(small_ckpt)
+    n, steps = 7, 70
+    starts = [3, 1, 6, 2, 8, 5, 4]
+    seqs = [2, 0, 3, 6, 5, 1, 4]
+    rng = np.random.default_rng(17)
+    toks = rng.integers(0, m.vocab, size=(n, steps + 8)).astype(np.uint32)
+    sts = [oracle.State(m) for _ in range(n)]
+    worst = 0.0
+    with ana_amd.Decoder(small_ckpt, max_seqs=n, prefill_chunk=8, numerics=mode) as dec:
+        for i in range(n):
+            dec.feeds(seqs[i], 0, toks[i, : starts[i]])
+            for p in range(starts[i]):
+                sts[i].feed(p, int(toks[i, p]))
+        for k in range(steps):
+            pos = [starts[i] + k for i in range(n)]
+            tk = [int(toks[i, pos[i]]) for i in range(n)]
+            dec.feed(seqs, pos, tk)
+            for i in range(n):
+                sts[i].feed(pos[i], tk[i])
+            if k in (0, 30, 58, steps - 1):
+                got = dec.logits(seqs)
+                for i in range(n):
+                    worst = max(worst, rel_err(got[i], sts[i].logits()))
+    print(f"worst relative error {worst:.3e}", flush=True)
+    assert worst <= TOL[mode], worst
