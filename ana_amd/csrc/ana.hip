@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "ana_internal.h"
@@ -49,6 +50,16 @@ struct ana_ctx {
   float* d_ce = nullptr;             // scoring: each row's G.lse - logit[target]
   __bf16 *d_sah = nullptr, *d_sal = nullptr;  // ANA_BF16 prefill: a product's split activations
   float* d_rsc = nullptr;                      // and its rows' norm scales
+  // fast modes: every layer product's weights packed for k_gemm_pk (fp32, or
+  // bf16 in ANA_BF16; the norm gains folded in), found by the product's first
+  // weight row; the entry keeps the segment shape and gains it was packed for
+  void* PK = nullptr;
+  struct PkEnt {
+    uint64_t off;
+    uint32_t rows0, rows1, nseg, mode, K;
+    const float* ng;
+  };
+  std::unordered_map<const float*, PkEnt> pk;
   float* d_gla = nullptr;            // fast prefill's GLA scan scratch
   GlaScratch gla{};                  // its regions
   GlaSub* d_gtab = nullptr;          // a prefill step's sub-chunk table
@@ -155,7 +166,7 @@ static void release(ana_ctx* c) {
   void* ps[] = {c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
                 c->d_ss, c->d_pm, c->d_gtab, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce,
-                c->d_sah, c->d_sal, c->d_rsc};
+                c->d_sah, c->d_sal, c->d_rsc, c->PK};
   for (void* p : ps)
     if (p) (void)hipFree(p);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
@@ -188,6 +199,8 @@ extern "C" void ana_rng_seeded(uint64_t seed, uint64_t r[4]) {
     r[i] = z ^ (z >> 31);
   }
 }
+
+static hipError_t pack_weights(ana_ctx* c);
 
 extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if (!path || !out) return fail(nullptr, ANA_EINVAL, "ana_open: null argument");
@@ -282,6 +295,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = hipMemcpyAsync(c->W, ck.raw.data(), 4 * c->P, hipMemcpyHostToDevice, c->st)) != hipSuccess) return bad(e);
   if ((e = launch_bswap(reinterpret_cast<uint32_t*>(c->W), c->P, c->st)) != hipSuccess) return bad(e);
   if (c->Wh && (e = launch_to_bf16(c->W, c->Wh, c->P, c->st)) != hipSuccess) return bad(e);
+  if (c->mode != ANA_EXACT_FP32 && (e = pack_weights(c)) != hipSuccess) return bad(e);
   if ((e = launch_zero(c->state, c->seq_stride * c->max_seqs, c->st)) != hipSuccess) return bad(e);
   if ((e = launch_zero(c->xs, (uint64_t)d * c->max_seqs, c->st)) != hipSuccess) return bad(e);
   if ((e = hipStreamSynchronize(c->st)) != hipSuccess) return bad(e);
@@ -356,6 +370,14 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
     if (c->Wh) by -= 2.0 * (g.seg[0].rows + (g.nseg > 1 ? g.seg[1].rows : 0)) * g.K;
     ProfScope ps(c, kind, by, true);
     if (small) return launch_gemv_fast(g, c->st, ps.start(), ps.stop());
+    if (g.B < 128 && gemm_pk_fits(g)) {
+      const auto it = c->pk.find(g.seg[0].W);
+      const ana_ctx::PkEnt* pe = it == c->pk.end() ? nullptr : &it->second;
+      if (pe && pe->rows0 == g.seg[0].rows && pe->nseg == g.nseg && (g.nseg < 2 || pe->rows1 == g.seg[1].rows) &&
+          pe->mode == (g.mode == GM_SILU) && pe->K == g.K && pe->ng == g.ng)
+        return launch_gemm_pk(g, static_cast<const char*>(c->PK) + pe->off, c->Wh != nullptr, c->st, ps.start(),
+                              ps.stop());
+    }
     if (g.B >= 128 && c->d_sah && g.K % 32 == 0 && g.B <= c->rows)
       return launch_gemm_dl(g, c->d_sah, c->d_sal, c->d_rsc, c->st, ps.start(), ps.stop());
     if (g.B >= 128) return launch_gemm_big(g, c->st, ps.start(), ps.stop());
@@ -374,6 +396,57 @@ static GemvArgs gemv1(const float* X, uint32_t ldx, uint32_t K, const float* W, 
   a.mode = GM_PLAIN;
   a.B = B;
   return a;
+}
+
+// The weight side of layer l's four products, with the workspaces they run
+// on (norm, then q|k|v, + the gate's z in GLA layers; Wo with the residual;
+// norm, then gate|up with SiLU; down with the residual); B left 0 for the
+// caller.
+enum { P_QKV = 0, P_WO = 1, P_GU = 2, P_WD = 3 };
+static void layer_products(const ana_ctx* c, uint32_t l, GemvArgs p[4]) {
+  const ana_config& cf = c->cfg;
+  const uint32_t d = cf.d, f = cf.f;
+  const float* W = c->W;
+  const Blk& b = c->blk[l];
+  p[P_QKV] = gemv1(c->X, d, d, W + b.wq, 3 * d, c->QKV, 3 * d, 0);
+  p[P_QKV].ng = W + b.ra;
+  if (b.gla) {
+    p[P_QKV].seg[1] = GemvSeg{W + b.wa, d, c->Z, d};
+    p[P_QKV].nseg = 2;
+  }
+  p[P_WO] = gemv1(c->O, d, d, W + b.wo, d, c->XA, d, 0);
+  p[P_WO].mode = GM_RESID; p[P_WO].R = c->X; p[P_WO].ldr = d;
+  p[P_GU] = gemv1(c->XA, d, d, W + b.wg, f, c->HH, f, 0);
+  p[P_GU].seg[1] = GemvSeg{W + b.wu, f, c->HH, f};
+  p[P_GU].nseg = 2;
+  p[P_GU].mode = GM_SILU;
+  p[P_GU].ng = W + b.rf;
+  p[P_WD] = gemv1(c->HH, f, f, W + b.wd, d, c->X, d, 0);
+  p[P_WD].mode = GM_RESID; p[P_WD].R = c->XA; p[P_WD].ldr = d;
+}
+
+// every layer product's packed weights, in one allocation
+static hipError_t pack_weights(ana_ctx* c) {
+  const int bf = c->Wh != nullptr;
+  uint64_t total = 0;
+  std::vector<GemvArgs> all;
+  for (uint32_t l = 0; l < c->cfg.layers; l++) {
+    GemvArgs p[4];
+    layer_products(c, l, p);
+    for (GemvArgs& g : p) {
+      if (g.K % 128) continue;
+      c->pk[g.seg[0].W] = ana_ctx::PkEnt{total, g.seg[0].rows, g.nseg > 1 ? g.seg[1].rows : 0u, g.nseg,
+                                         g.mode == GM_SILU ? 1u : 0u, g.K, g.ng};
+      total += (pack_bytes(g, bf) + 255) & ~255ull;
+      all.push_back(g);
+    }
+  }
+  if (all.empty()) return hipSuccess;
+  hipError_t e = hipMalloc(&c->PK, total);
+  if (e != hipSuccess) return e;
+  for (const GemvArgs& g : all)
+    if ((e = launch_pack(g, static_cast<char*>(c->PK) + c->pk[g.seg[0].W].off, bf, c->st)) != hipSuccess) return e;
+  return hipSuccess;
 }
 
 // RMSNorm(X; g) then the product: inside the product for small batches,
@@ -439,13 +512,11 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
   }
   for (uint32_t l = 0; l < cf.layers; l++) {
     const Blk& b = c->blk[l];
+    GemvArgs p[4];
+    layer_products(c, l, p);
+    for (GemvArgs& g : p) g.B = B;
     // norm, then q|k|v (+ the gate's z): dd.gla / dd.sm `pre`
-    GemvArgs g = gemv1(c->X, d, d, W + b.wq, 3 * d, c->QKV, 3 * d, B);
-    if (b.gla) {
-      g.seg[1] = GemvSeg{W + b.wa, d, c->Z, d};
-      g.nseg = 2;
-    }
-    if (int r = norm_gemv(c, c->X, W + b.ra, g, ANA_K_GEMV, chunk)) return r;
+    if (int r = norm_gemv(c, c->X, W + b.ra, p[P_QKV], ANA_K_GEMV, chunk)) return r;
     if (b.gla && !chunk) {
       // S read and written once per sequence, q|k|v|z in, o out
       ProfScope ps(c, ANA_K_GLA, (double)B * (8.0 * cf.heads * (d / cf.heads) * (d / cf.heads) + 4.0 * 5 * d));
@@ -519,17 +590,9 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
       }
     }
     // M.tail: xa = x + Wo o; hh = silu(g) * u on norm(xa); x = xa + Wd hh
-    GemvArgs wo = gemv1(c->O, d, d, W + b.wo, d, c->XA, d, B);
-    wo.mode = GM_RESID; wo.R = c->X; wo.ldr = d;
-    HIPCHK(c, gemv_timed(c, wo, ANA_K_GEMV, chunk));
-    GemvArgs gu = gemv1(c->XA, d, d, W + b.wg, f, c->HH, f, B);
-    gu.seg[1] = GemvSeg{W + b.wu, f, c->HH, f};
-    gu.nseg = 2;
-    gu.mode = GM_SILU;
-    if (int r = norm_gemv(c, c->XA, W + b.rf, gu, ANA_K_GEMV, chunk)) return r;
-    GemvArgs wd = gemv1(c->HH, f, f, W + b.wd, d, c->X, d, B);
-    wd.mode = GM_RESID; wd.R = c->XA; wd.ldr = d;
-    HIPCHK(c, gemv_timed(c, wd, ANA_K_GEMV, chunk));
+    HIPCHK(c, gemv_timed(c, p[P_WO], ANA_K_GEMV, chunk));
+    if (int r = norm_gemv(c, c->XA, W + b.rf, p[P_GU], ANA_K_GEMV, chunk)) return r;
+    HIPCHK(c, gemv_timed(c, p[P_WD], ANA_K_GEMV, chunk));
   }
   return ANA_OK;
 }
