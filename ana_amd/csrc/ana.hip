@@ -350,17 +350,29 @@ static double gemv_bytes(const GemvArgs& g) {
 // The fast modes: decode steps of B <= kSmallB sequences stream bf16
 // (ANA_BF16) or fp32 rows with split-K sums and take the reassociated GLA and
 // attention kernels. Prefill steps of more than kSmallB rows, and the layer
-// products of decode steps of more sequences, run on the matrix cores. The
-// decode steps of more sequences keep the exact GLA, attention and head, and
-// prefill steps of kSmallB rows or fewer the exact kernels: the matrix-core
-// head and the fast GLA and attention above kSmallB decode rows faulted the
-// GPU in their first test and stay off until the cause is found.
+// products and head of decode steps of more sequences, run on the matrix
+// cores (below 128 rows over packed weights). The decode steps of more
+// sequences keep the exact GLA and attention, and prefill steps of kSmallB
+// rows or fewer the exact kernels: the fast GLA and attention above kSmallB
+// decode rows were on in a first test that faulted the GPU and stay off
+// until its cause is found.
 static bool fast_mode(const ana_ctx* c) { return c->mode != ANA_EXACT_FP32; }
 static bool fast_path(const ana_ctx* c, uint32_t B) { return fast_mode(c) && B <= kSmallB; }
 
+// the packed weights of product g, when they were packed for its shape and gains
+static const ana_ctx::PkEnt* find_pk(const ana_ctx* c, const GemvArgs& g) {
+  const auto it = c->pk.find(g.seg[0].W);
+  if (it == c->pk.end()) return nullptr;
+  const ana_ctx::PkEnt& pe = it->second;
+  const bool same = pe.rows0 == g.seg[0].rows && pe.nseg == g.nseg && (g.nseg < 2 || pe.rows1 == g.seg[1].rows) &&
+                    pe.mode == (g.mode == GM_SILU ? 1u : 0u) && pe.K == g.K && pe.ng == g.ng;
+  return same ? &pe : nullptr;
+}
+
 static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool chunk = false) {
   const bool small = g0.B <= kSmallB;
-  if (fast_mode(c) && (small ? !chunk : (chunk || kind != ANA_K_HEAD))) {
+  const ana_ctx::PkEnt* pe = fast_mode(c) && !small && g0.B < 128 && gemm_pk_fits(g0) ? find_pk(c, g0) : nullptr;
+  if (pe || (fast_mode(c) && (small ? !chunk : (chunk || kind != ANA_K_HEAD)))) {
     GemvArgs g = g0;
     if (c->Wh) {
       g.Wh0 = c->Wh + (g.seg[0].W - c->W);
@@ -370,14 +382,9 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
     if (c->Wh) by -= 2.0 * (g.seg[0].rows + (g.nseg > 1 ? g.seg[1].rows : 0)) * g.K;
     ProfScope ps(c, kind, by, true);
     if (small) return launch_gemv_fast(g, c->st, ps.start(), ps.stop());
-    if (g.B < 128 && gemm_pk_fits(g)) {
-      const auto it = c->pk.find(g.seg[0].W);
-      const ana_ctx::PkEnt* pe = it == c->pk.end() ? nullptr : &it->second;
-      if (pe && pe->rows0 == g.seg[0].rows && pe->nseg == g.nseg && (g.nseg < 2 || pe->rows1 == g.seg[1].rows) &&
-          pe->mode == (g.mode == GM_SILU) && pe->K == g.K && pe->ng == g.ng)
-        return launch_gemm_pk(g, static_cast<const char*>(c->PK) + pe->off, c->Wh != nullptr, c->st, ps.start(),
-                              ps.stop());
-    }
+    if (pe)
+      return launch_gemm_pk(g, static_cast<const char*>(c->PK) + pe->off, c->Wh != nullptr, c->st, ps.start(),
+                            ps.stop());
     if (g.B >= 128 && c->d_sah && g.K % 32 == 0 && g.B <= c->rows)
       return launch_gemm_dl(g, c->d_sah, c->d_sal, c->d_rsc, c->st, ps.start(), ps.stop());
     if (g.B >= 128) return launch_gemm_big(g, c->st, ps.start(), ps.stop());
@@ -425,15 +432,25 @@ static void layer_products(const ana_ctx* c, uint32_t l, GemvArgs p[4]) {
   p[P_WD].mode = GM_RESID; p[P_WD].R = c->XA; p[P_WD].ldr = d;
 }
 
-// every layer product's packed weights, in one allocation
+// every layer product's packed weights and the head's (final norm, tied
+// embedding), in one allocation
 static hipError_t pack_weights(ana_ctx* c) {
   const int bf = c->Wh != nullptr;
+  const ana_config& cf = c->cfg;
   uint64_t total = 0;
   std::vector<GemvArgs> all;
-  for (uint32_t l = 0; l < c->cfg.layers; l++) {
+  for (uint32_t l = 0; l <= cf.layers; l++) {
     GemvArgs p[4];
-    layer_products(c, l, p);
-    for (GemvArgs& g : p) {
+    uint32_t np = 4;
+    if (l < cf.layers) {
+      layer_products(c, l, p);
+    } else {
+      p[0] = gemv1(c->X, cf.d, cf.d, c->W, cf.vocab, c->LG, cf.vocab, 0);
+      p[0].ng = c->W + c->fin;
+      np = 1;
+    }
+    for (uint32_t i = 0; i < np; i++) {
+      const GemvArgs& g = p[i];
       if (g.K % 128) continue;
       c->pk[g.seg[0].W] = ana_ctx::PkEnt{total, g.seg[0].rows, g.nseg > 1 ? g.seg[1].rows : 0u, g.nseg,
                                          g.mode == GM_SILU ? 1u : 0u, g.K, g.ng};

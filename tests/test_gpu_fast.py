@@ -253,8 +253,8 @@ def test_fast_score_n(oracle, small_ckpt, mode):
 @pytest.mark.parametrize("mode", MODES)
 def test_fast_decode_batch_products(oracle, small_ckpt, mode):
     """Decode steps of more than kSmallB sequences in a fast mode: the layer
-    products on the matrix cores (the prefill kernels, one row a sequence),
-    GLA, attention and head exact. Seven sequences from ragged starts, 70
+    products and the head on the matrix cores (packed weights, one row a
+    sequence), GLA and attention exact. Seven sequences from ragged starts, 70
     teacher-forced steps across the ring wrap; every sequence's logits
     against its own oracle run at four steps."""
     print(f"case fast decode batch products mode {mode}", flush=True)
