@@ -9,6 +9,7 @@
 #include <hip/hip_ext.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "ana_internal.h"
 #include "numerics.h"
@@ -1318,6 +1319,121 @@ __global__ __launch_bounds__(256) void k_gemm_pk(GemvArgs a, const uint4* __rest
   }
 }
 
+// f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>), in order
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_(f, std::make_integer_sequence<int, N>{});
+}
+
+// The same product with each wave on its own: K = 128 NS, and wave w's
+// quarter is NS steps of 32 k. The wave issues, per step, its weight pieces
+// (into a ring of D register sets) and two global_load_lds_dwordx4 of the 16
+// batch rows' x for that step (each one 1 KB: 8 rows x 128 bytes, the row's
+// 16-byte units at unit ^ (row & 7)) into an LDS block of its own, so its
+// loads retire in issue order: before step s it waits until only the ops of
+// steps s + 1 .. s + D - 1 are outstanding (a count fixed at compile time)
+// and reads the step's x with no barrier. Norm gains folded into the packed
+// weights; sums of squares, reduction and epilogue as k_gemm_pk.
+template <int WT, int NS, int D>
+__global__ __launch_bounds__(256) void k_gemm_pw(GemvArgs a, const uint4* __restrict__ pk) {
+  constexpr int WP = WT == 1 ? 1 : 2, OPS = WP + 2;
+  __shared__ __align__(1024) float xs[4][NS][512];
+  __shared__ f32x4_t red[3][64];
+  __shared__ float ssr[4][16];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+  const uint32_t K = 128 * NS, nsa = 4 * NS;
+  const uint32_t m0 = blockIdx.y * 16, t = blockIdx.x;
+  const bool norm = a.ng != nullptr;
+  const uint4* wsrc = pk + ((size_t)t * nsa + wv * NS) * (64 * WP) + lane;
+  // this lane's x piece in each half of a step: row 8 h + (lane >> 3), its
+  // unit (lane & 7) ^ row
+  const uint32_t dr = lane >> 3, sl = (lane & 7) ^ dr;
+  uint32_t xo[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) xo[h] = min(m0 + 8 * h + dr, a.B - 1) * a.ldx + wv * (K / 4) + 4 * sl;
+  uint4 wr[D][WP];
+  auto issue = [&](auto S) {
+    constexpr int s = decltype(S)::value;
+#pragma unroll
+    for (int p = 0; p < WP; p++) wr[s % D][p] = wsrc[s * 64 * WP + 64 * p];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+      __builtin_amdgcn_global_load_lds((const void*)(a.X + xo[h] + 32 * s), (lds_void*)&xs[wv][s][256 * h], 16, 0, 0);
+  };
+  static_for<(D < NS ? D : NS)>(issue);
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  float ss = 0.0f;
+  const uint32_t fo0 = (r16 >> 3) * 256 + (r16 & 7) * 32 + 4 * ((2 * g4) ^ (r16 & 7));
+  const uint32_t fo1 = (r16 >> 3) * 256 + (r16 & 7) * 32 + 4 * ((2 * g4 + 1) ^ (r16 & 7));
+  static_for<NS>([&](auto S) {
+    constexpr int s = decltype(S)::value;
+    constexpr int last = s + D - 1 < NS - 1 ? s + D - 1 : NS - 1;
+    ANA_VMCNT(OPS * (last - s));
+    const float4 x0 = *reinterpret_cast<const float4*>(&xs[wv][s][fo0]);
+    const float4 x1 = *reinterpret_cast<const float4*>(&xs[wv][s][fo1]);
+    const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    if (norm) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) ss += x[e] * x[e];
+    }
+    if constexpr (WT == 0) {
+      const uint4 w0 = wr[s % D][0], w1 = wr[s % D][WP - 1];
+      const float w[8] = {__uint_as_float(w0.x), __uint_as_float(w0.y), __uint_as_float(w0.z), __uint_as_float(w0.w),
+                          __uint_as_float(w1.x), __uint_as_float(w1.y), __uint_as_float(w1.z), __uint_as_float(w1.w)};
+#pragma unroll
+      for (int e = 0; e < 8; e++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[e], w[e], acc, 0, 0, 0);
+    } else {
+      bf16x8_t hi, lo;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        hi[e] = (__bf16)x[e];
+        lo[e] = (__bf16)(x[e] - (float)hi[e]);
+      }
+      const bf16x8_t wb8 = __builtin_bit_cast(bf16x8_t, wr[s % D][0]);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, wb8, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, wb8, acc, 0, 0, 0);
+    }
+    if constexpr (s + D < NS) issue(std::integral_constant<int, s + D>{});
+  });
+  if (wv > 0) red[wv - 1][lane] = acc;
+  if (norm) {
+    float v = ss;
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (g4 == 0) ssr[wv][r16] = v;
+  }
+  __syncthreads();
+  if (wv > 0) return;
+  const Segs sgs(a);
+  const float* w_;
+  uint32_t sg, lr;
+  const bool nok = sgs.row(16, t, r16, &w_, &sg, &lr);
+  f32x4_t y4 = acc;
+#pragma unroll
+  for (int p = 0; p < 3; p++) {
+    const f32x4_t o = red[p][lane];
+    y4[0] += o[0]; y4[1] += o[1]; y4[2] += o[2]; y4[3] += o[3];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const uint32_t mi = 4 * g4 + r, m = m0 + mi;
+    float y = y4[r];
+    if (norm) y *= 1.0f / sqrtf((((ssr[0][mi] + ssr[1][mi]) + ssr[2][mi]) + ssr[3][mi]) / (float)K + 1.0e-5f);
+    if (a.mode == GM_SILU) {
+      const float up = __shfl_xor(y, 8, 64);
+      if (r16 < 8 && nok && m < a.B) a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = fast_silu(y) * up;
+    } else if (nok && m < a.B) {
+      if (a.mode == GM_RESID) y = a.R[(size_t)m * a.ldr + lr] + y;
+      if (sg) a.seg[1].Y[(size_t)m * a.seg[1].ldy + lr] = y;
+      else a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = y;
+    }
+  }
+}
+
 bool gemm_pk_fits(const GemvArgs& a) {
   return !a.amax && a.B > 0 && a.K % 128 == 0 && a.K <= 2048 && (a.ldx & 3) == 0 &&
          (reinterpret_cast<uintptr_t>(a.X) & 15) == 0;
@@ -1327,10 +1443,28 @@ hipError_t launch_gemm_pk(const GemvArgs& a, const void* pk, int bf, hipStream_t
                           uint32_t mt) {
   if (!gemm_pk_fits(a) || !pk) return hipErrorInvalidValue;
   const uint32_t tiles = pk_tiles(a);
-  if (mt == 0) mt = 1;
+  const uint4* p = static_cast<const uint4*>(pk);
+  if (mt == 0) {
+    // one wave per K quarter, each on its own: the K this library meets
+    const dim3 g1(tiles, (a.B + 15) / 16);
+#define ANA_PW(NS, D)                                                                          \
+  do {                                                                                         \
+    if (bf) ANA_LAUNCH_F((k_gemm_pw<1, NS, D>), g1, dim3(256), 0, st, e0, e1, a, p);          \
+    else ANA_LAUNCH_F((k_gemm_pw<0, NS, D>), g1, dim3(256), 0, st, e0, e1, a, p);             \
+    return hipGetLastError();                                                                  \
+  } while (0)
+    switch (a.K) {
+      case 256: ANA_PW(2, 2);
+      case 768: ANA_PW(6, 6);
+      case 1024: ANA_PW(8, 8);
+      case 2048: ANA_PW(16, 8);
+      default: break;
+    }
+#undef ANA_PW
+    mt = 1;
+  }
   if (mt == 2 && a.K > 768) return hipErrorInvalidValue;
   const dim3 grid(tiles, (a.B + 16 * mt - 1) / (16 * mt));
-  const uint4* p = static_cast<const uint4*>(pk);
   if (bf) {
     if (mt == 2) ANA_LAUNCH_F((k_gemm_pk<1, 2, 768, 6>), grid, dim3(256), 0, st, e0, e1, a, p);
     else if (a.K <= 768) ANA_LAUNCH_F((k_gemm_pk<1, 1, 768, 6>), grid, dim3(256), 0, st, e0, e1, a, p);
