@@ -98,7 +98,7 @@ def run_batch(path: str, c: cf.Config, B: int, prompt: int, warmup: int, steps: 
             stats = dec.prof_read()
             dec.prof(False)
     dt = t1 - t0
-    sb = run_bytes(c, positions, steps, 2.0 if mode == "bf16" and B <= 4 else 4.0) / steps
+    sb = run_bytes(c, positions, steps, 2.0 if mode == "bf16" else 4.0) / steps
     return {
         "tok_s": B * steps / dt,
         "ms_per_step": 1000.0 * dt / steps,
@@ -182,9 +182,10 @@ def run_prefill(path: str, c) -> dict:
             "workload": "64 prompts x 512 tokens through ana_feeds_n, chunk 128; flops = 2 x "
                         "(P - v d) per token (the products) + causal attention 2 B L^2 d per "
                         "softmax layer (the GLA scan not counted)",
-            "kernels": "products k_gemm_big (128 x 128 MFMA tiles"
-                       + (", bf16 weights x bf16 head+remainder activations" if m == "bf16" else ", fp32 MFMA")
-                       + "), attention k_attn_flash (fp32 MFMA), GLA k_gla_sub + k_gla_carry",
+            "kernels": ("products k_split + k_gemm_dl (128 x 128 MFMA tiles, bf16 weights x bf16 "
+                        "head+remainder activations, both streamed straight into LDS)" if m == "bf16" else
+                        "products k_gemm_big (128 x 128 MFMA tiles, fp32 MFMA)")
+                       + ", attention k_attn_flash (fp32 MFMA), GLA k_gla_sub + k_gla_carry",
         }
         log(f"prefill B=64 x 512 {m}: {ntok / dt:.0f} tok/s")
         # window scoring (Evaluate.bend's window.go through ana_score_n): 64
