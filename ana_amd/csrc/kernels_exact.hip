@@ -635,6 +635,59 @@ __global__ __launch_bounds__(256) void k_gla(const float* __restrict__ QKV,
   }
 }
 
+// The same token step for one (head, sequence) of a decode step with
+// hd = 64, on one wave: lane b keeps column b of the head's state in
+// registers (loaded and stored one row of 64 consecutive floats at a time),
+// so nothing of S goes through LDS and the only barriers are the two that
+// publish q, k and the per-row gate values. Every value takes k_gla's
+// operations in k_gla's order: the norms' chains over q and k (each lane
+// runs them, from broadcast LDS reads), S' = (al_a * S) + (kh_a * v_b), and
+// o_b = ((0 + qh_0 S'_0b) + qh_1 S'_1b) + ..., a ascending.
+__global__ __launch_bounds__(64) void k_gla_w(const float* __restrict__ QKV, const float* __restrict__ Z,
+                                              const float* __restrict__ lam, StateRef S,
+                                              const uint32_t* __restrict__ seq, float* __restrict__ O,
+                                              uint32_t d, uint32_t rglru) {
+  constexpr int HD = 64;
+  __shared__ __align__(16) float q[HD];
+  __shared__ __align__(16) float k[HD];
+  __shared__ float al[HD], kh[HD], qh[HD];
+  const uint32_t h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  float* Sg = S.base + (size_t)seq[b] * S.seq_stride + S.layer_off + (size_t)h * HD * HD;
+  const float* x = QKV + (size_t)b * 3 * d;
+  const float qv = x[h * HD + lane], kv = x[d + h * HD + lane], vv = x[2 * d + h * HD + lane];
+  const float zv = Z[(size_t)b * d + h * HD + lane];
+  const float lv = rglru ? lam[h * HD + lane] : 0.0f;
+  float s[HD];
+#pragma unroll
+  for (int a = 0; a < HD; a++) s[a] = Sg[a * HD + lane];
+  q[lane] = qv;
+  k[lane] = kv;
+  __syncthreads();
+  const float s0 = chain_sumsq_lds(0.0f, q, HD), s1 = chain_sumsq_lds(0.0f, k, HD);
+  const float kn = kv / csqrt(1.0e-6f + s1);
+  float alv, khv;
+  if (rglru) {
+    const float la = ex_rglru_log_gate(zv, lv);
+    khv = kn * ex_rglru_write_scale(la);
+    alv = dexp(la);
+  } else {
+    alv = ex_sigmoid(zv);
+    khv = kn;
+  }
+  qh[lane] = qv / csqrt(1.0e-6f + s0);
+  al[lane] = alv;
+  kh[lane] = khv;
+  __syncthreads();
+  float acc = 0.0f;
+#pragma unroll
+  for (int a = 0; a < HD; a++) {
+    const float sa = (al[a] * s[a]) + (kh[a] * vv);
+    Sg[a * HD + lane] = sa;
+    acc = acc + qh[a] * sa;
+  }
+  O[(size_t)b * d + h * HD + lane] = acc;
+}
+
 #define ANA_HD_DISPATCH(HDV, LAUNCH) \
   switch (HDV) {                     \
     case 64: LAUNCH(64); break;      \
@@ -646,6 +699,10 @@ __global__ __launch_bounds__(256) void k_gla(const float* __restrict__ QKV,
 hipError_t launch_gla_step(const float* QKV, const float* Z, const float* lam, StateRef S,
                            const uint32_t* seq, float* O, uint32_t d, uint32_t heads,
                            uint32_t rglru, uint32_t B, hipStream_t st) {
+  if (d / heads == 64) {
+    hipLaunchKernelGGL(k_gla_w, dim3(heads, B), dim3(64), 0, st, QKV, Z, lam, S, seq, O, d, rglru);
+    return hipGetLastError();
+  }
 #define L_(H) hipLaunchKernelGGL(k_gla<H>, dim3(heads, B), dim3(256), 0, st, QKV, Z, lam, S, seq, 0u, O, d, rglru, 1u)
   ANA_HD_DISPATCH(d / heads, L_)
 #undef L_
