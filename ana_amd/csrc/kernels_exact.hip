@@ -1006,9 +1006,14 @@ __global__ __launch_bounds__(256) void k_attn_out(AttnArgs a) {
   if (tid < ATTN_CG) a.O[(size_t)b * d + h * HD + c0 + tid] = (1.0f / red[0]) * oi;
 }
 
+// From kAttnWideB rows on, one workgroup per (head, row) (k_attn) keeps
+// every CU busy, and the split kernels would dispatch ctx / kAttnTS score
+// blocks per (head, row) whatever the row's position.
+constexpr uint32_t kAttnWideB = 8;
+
 hipError_t launch_attn(const AttnArgs& a, hipStream_t st) {
   const uint32_t hd = a.d / a.heads;
-  if (a.ss && a.pm && hd % ATTN_CG == 0) {
+  if (a.ss && a.pm && hd % ATTN_CG == 0 && a.B < kAttnWideB) {
     const uint32_t ns = (a.ctx + kAttnTS - 1) / kAttnTS;
 #define L_(H)                                                                                   \
   hipLaunchKernelGGL(k_attn_scores<H>, dim3(a.heads, ns, a.B), dim3(kAttnTS), 0, st, a);      \

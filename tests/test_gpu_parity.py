@@ -124,6 +124,40 @@ def test_batched_sequences(oracle, ckpts, name):
 
 
 @pytest.mark.parametrize("name", list(CFGS))
+def test_batched_sequences_wide(oracle, ckpts, name):
+    """Nine sequences at staggered positions, 70 steps across the ring's
+    wrap (attention on one workgroup per head and row from eight rows on):
+    each one's bits are its own single-sequence run's, at four steps."""
+    path = ckpts[name]
+    print(f"case wide batch {name}", flush=True)
+    m = oracle.Model(path)
+    rng = np.random.default_rng(23)
+    n, steps = 9, 70
+    streams = rng.integers(0, m.vocab, size=(n, steps + 40)).astype(np.uint32)
+    starts = [0, 3, 17, 40, 5, 1, 29, 11, 8]
+    seqs = [8, 0, 2, 3, 7, 5, 1, 6, 4]
+    sts = [oracle.State(m) for _ in range(n)]
+    with ana_amd.Decoder(path, max_seqs=9) as dec:
+        for i, s in enumerate(seqs):
+            dec.feeds(s, 0, streams[i, : starts[i]])
+            for p in range(starts[i]):
+                sts[i].feed(p, int(streams[i, p]))
+        for k in range(steps):
+            pos = [starts[i] + k for i in range(n)]
+            tok = [int(streams[i, pos[i]]) for i in range(n)]
+            dec.feed(seqs, pos, tok)
+            for i in range(n):
+                sts[i].feed(pos[i], tok[i])
+            if k in (0, 23, 47, steps - 1):
+                got = dec.logits(seqs)
+                for i in range(n):
+                    assert np.array_equal(bits(got[i]), bits(sts[i].logits())), (k, i)
+        for i in range(n):
+            for l in range(m.layers):
+                assert np.array_equal(bits(dec.state(seqs[i], l)), bits(sts[i].layer(l))), (i, l)
+
+
+@pytest.mark.parametrize("name", list(CFGS))
 def test_token_loop_greedy(oracle, ckpts, name):
     """ana_generate's on-device loop = the host loop of Generate.bend on the
     oracle (feed, head, greedy pick on the store, feed the pick)."""
