@@ -271,24 +271,21 @@ GlaScratch gla_scan_carve(float* p, uint32_t rows, uint32_t nsub, uint32_t nseg,
 hipError_t launch_gla_scan(const float* QKV, const float* Z, const float* lam, StateRef S, float* O,
                            const GlaScratch& g, const GlaSub* tab, uint32_t nsub, uint32_t d,
                            uint32_t heads, uint32_t rglru, hipStream_t st);
-// batched products (prefill chunks, B > kSmallB) on the matrix cores: bf16
-// when Wh0 is set, else fp32; no argmax epilogue
+// batched products (B > kSmallB) on the matrix cores whose K the packed
+// GEMM does not take (K % 128 != 0 or K > 2048): bf16 when Wh0 is set, else
+// fp32; no argmax epilogue
 hipError_t launch_gemm_mfma(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nullptr,
                             hipEvent_t e1 = nullptr);
-// its register-streaming form (K % 128 == 0, K <= kSkinnyMaxK), batch tile
-// 16 mt rows (mt 1, 2 or 4; 0 picks one)
-constexpr uint32_t kSkinnyMaxK = 4096;
-hipError_t launch_gemm_skinny(const GemvArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1, uint32_t mt);
 // A product's weights packed for k_gemm_pk (fp32, or bf16 with bf; the
 // gains of ng folded in): pack_bytes of device memory at dst.
 uint64_t pack_bytes(const GemvArgs& a, int bf);
 hipError_t launch_pack(const GemvArgs& a, void* dst, int bf, hipStream_t st);
 // The decode-batch GEMM over packed weights (packed with the same ng, which
 // here only turns the norm scale on): K % 128 == 0, K <= 2048, X 16-byte
-// aligned (gemm_pk_fits); batch tile 16 mt rows (mt 1 or 2; 0 picks one)
+// aligned (gemm_pk_fits)
 bool gemm_pk_fits(const GemvArgs& a);
 hipError_t launch_gemm_pk(const GemvArgs& a, const void* pk, int bf, hipStream_t st, hipEvent_t e0,
-                          hipEvent_t e1, uint32_t mt = 0);
+                          hipEvent_t e1);
 // the same for 128 rows or more, 128 x 128 tiles
 hipError_t launch_gemm_big(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nullptr,
                            hipEvent_t e1 = nullptr);

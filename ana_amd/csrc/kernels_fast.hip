@@ -954,175 +954,9 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemvArgs a) {
   }
 }
 
-// Decode batches (5..127 rows) in the fast modes: Y[m][n] = sum_k X[m][k]
-// W[n][k] with no LDS staging in the k loop. A workgroup owns 16 weight rows
-// (n) and 16 MT batch rows (m); its four waves split K into four contiguous
-// quarters, and each wave streams its quarter of X and W straight into
-// registers, D steps of 32 k ahead, with every load issued unconditionally
-// (the step index is clamped) so the loads retire in issue order and each
-// wait covers only the step about to be used. The gains of `ng` sit in LDS;
-// each row's sum of squares is gathered from the raw x on the way. At the
-// end waves 1..3 hand their partial tiles to wave 0 through LDS, which adds
-// them in wave order and applies the norm scale and the epilogue. MFMA
-// operands: lane l holds row l % 16 of X and of W at k = 8 (l / 16) + e of
-// the step; fp32 (WT 0) takes v_mfma_f32_16x16x4f32 once per e, bf16 (WT 1)
-// one v_mfma_f32_16x16x32_bf16 on the x head and one on the remainder. The
-// result tile: lane l holds batch rows 4 (l / 16) + r, weight row l % 16.
-template <int WT, int MT, int D>
-__global__ __launch_bounds__(256) void k_gemm_skinny(GemvArgs a) {
-  constexpr uint32_t BM = 16 * MT, BN = 16, KS = 32;
-  __shared__ f32x4_t red[3][MT][64];
-  __shared__ float ssr[4][BM];
-  __shared__ __align__(16) float gs[kSkinnyMaxK];
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const uint32_t r16 = lane & 15, g4 = lane >> 4;
-  const uint32_t m0 = blockIdx.y * BM;
-  const uint32_t K = a.K, kw = K >> 2, ns = kw / KS, kb = wv * kw;
-  const bool norm = a.ng != nullptr;
-  if (norm) {
-    for (uint32_t q = tid * 4; q < K; q += 1024)
-      *reinterpret_cast<float4*>(&gs[q]) = *reinterpret_cast<const float4*>(a.ng + q);
-    __syncthreads();
-  }
-  const Segs sgs(a);
-  const float* wf;
-  uint32_t wsg, wlr;
-  const bool wok = sgs.row(BN, blockIdx.x, r16, &wf, &wsg, &wlr);
-  const uint16_t* wh = (wsg ? a.Wh1 : a.Wh0) + (size_t)wlr * K;
-  if (!wok) {  // a row past the segments: read row 0, discard its column
-    wf = sgs.W0;
-    wh = a.Wh0;
-  }
-  // X rows of this lane, clamped to the batch (rows past it are discarded)
-  uint32_t xo[MT];
-#pragma unroll
-  for (int t = 0; t < MT; t++) xo[t] = min(m0 + 16 * t + r16, a.B - 1) * a.ldx;
-  float4 xv[D][MT][2];
-  float4 wv4[D][2];
-  uint4 wb[D];
-  auto load = [&](int u, uint32_t s) {
-    const uint32_t k = kb + s * KS + 8 * g4;
-#pragma unroll
-    for (int t = 0; t < MT; t++) {
-      xv[u][t][0] = *reinterpret_cast<const float4*>(a.X + xo[t] + k);
-      xv[u][t][1] = *reinterpret_cast<const float4*>(a.X + xo[t] + k + 4);
-    }
-    if constexpr (WT == 1) {
-      wb[u] = *reinterpret_cast<const uint4*>(wh + k);
-    } else {
-      wv4[u][0] = *reinterpret_cast<const float4*>(wf + k);
-      wv4[u][1] = *reinterpret_cast<const float4*>(wf + k + 4);
-    }
-  };
-  f32x4_t acc[MT];
-  float ss[MT];
-#pragma unroll
-  for (int t = 0; t < MT; t++) {
-    acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    ss[t] = 0.0f;
-  }
-  auto step = [&](int u, uint32_t s) {
-    const uint32_t k = kb + s * KS + 8 * g4;
-    float g[8];
-    if (norm) {
-      const float4 g0 = *reinterpret_cast<const float4*>(&gs[k]);
-      const float4 g1 = *reinterpret_cast<const float4*>(&gs[k + 4]);
-      g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w;
-      g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
-    }
-    float w[8];
-    if constexpr (WT == 0) {
-      w[0] = wv4[u][0].x; w[1] = wv4[u][0].y; w[2] = wv4[u][0].z; w[3] = wv4[u][0].w;
-      w[4] = wv4[u][1].x; w[5] = wv4[u][1].y; w[6] = wv4[u][1].z; w[7] = wv4[u][1].w;
-    }
-#pragma unroll
-    for (int t = 0; t < MT; t++) {
-      float x[8] = {xv[u][t][0].x, xv[u][t][0].y, xv[u][t][0].z, xv[u][t][0].w,
-                    xv[u][t][1].x, xv[u][t][1].y, xv[u][t][1].z, xv[u][t][1].w};
-      if (norm) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          ss[t] += x[e] * x[e];
-          x[e] *= g[e];
-        }
-      }
-      if constexpr (WT == 0) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[e], w[e], acc[t], 0, 0, 0);
-      } else {
-        bf16x8_t hi, lo;
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          hi[e] = (__bf16)x[e];
-          lo[e] = (__bf16)(x[e] - (float)hi[e]);
-        }
-        const bf16x8_t wb8 = __builtin_bit_cast(bf16x8_t, wb[u]);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, wb8, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, wb8, acc[t], 0, 0, 0);
-      }
-    }
-  };
-#pragma unroll
-  for (int u = 0; u < D; u++) load(u, min((uint32_t)u, ns - 1));
-  for (uint32_t s0 = 0; s0 < ns; s0 += D) {
-#pragma unroll
-    for (int u = 0; u < D; u++) {
-      const uint32_t s = s0 + u;
-      if (s < ns) step(u, s);
-      load(u, min(s + D, ns - 1));
-    }
-  }
-  // partial tiles and sums of squares to wave 0
-  if (wv > 0) {
-#pragma unroll
-    for (int t = 0; t < MT; t++) red[wv - 1][t][lane] = acc[t];
-  }
-  if (norm) {
-#pragma unroll
-    for (int t = 0; t < MT; t++) {
-      float v = ss[t];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      if (g4 == 0) ssr[wv][16 * t + r16] = v;
-    }
-  }
-  __syncthreads();
-  if (wv > 0) return;
-  const uint32_t n = r16;
-  const float* w_;
-  uint32_t sg, lr;
-  const bool nok = sgs.row(BN, blockIdx.x, n, &w_, &sg, &lr);
-#pragma unroll
-  for (int t = 0; t < MT; t++) {
-    f32x4_t y4 = acc[t];
-#pragma unroll
-    for (int p = 0; p < 3; p++) {
-      const f32x4_t o = red[p][t][lane];
-      y4[0] += o[0]; y4[1] += o[1]; y4[2] += o[2]; y4[3] += o[3];
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const uint32_t mi = 16 * t + 4 * g4 + r, m = m0 + mi;
-      float y = y4[r];
-      if (norm) {
-        const float s = ((ssr[0][mi] + ssr[1][mi]) + ssr[2][mi]) + ssr[3][mi];
-        y *= 1.0f / sqrtf(s / (float)K + 1.0e-5f);
-      }
-      if (a.mode == GM_SILU) {
-        const float up = __shfl_xor(y, 8, 64);
-        if (n < 8 && nok && m < a.B) a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = fast_silu(y) * up;
-      } else if (nok && m < a.B) {
-        if (a.mode == GM_RESID) y = a.R[(size_t)m * a.ldr + lr] + y;
-        if (sg) a.seg[1].Y[(size_t)m * a.seg[1].ldy + lr] = y;
-        else a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = y;
-      }
-    }
-  }
-}
-
 // ------------------------------------------------------------------ packed weights
 
-// A product's weights re-laid for the decode-batch GEMM (k_gemm_pk): tile t
+// A product's weights re-laid for the decode-batch GEMM (k_gemm_pw): tile t
 // (16 weight rows in Segs order, 8 gate + 8 up rows with SiLU) and step s
 // (32 k) form one block, blocks ordered (t, s), so a wave streams its k range
 // of a tile as consecutive 1 KB pieces. In a block, lane l of a wave owns
@@ -1183,142 +1017,6 @@ hipError_t launch_pack(const GemvArgs& a, void* dst, int bf, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Decode batches (5..127 rows) in the fast modes over packed weights (the
-// norm gains folded in when `ng` is set). A workgroup owns one 16-row weight
-// tile and 16 MT batch rows. The batch rows' raw x goes to LDS once, by
-// global_load_lds_dwordx4 in whole 1 KB pieces, issued right after the
-// first D steps of the weights; a row's 16-byte units sit at
-// unit ^ (row & 7), so the MFMA fragment reads (16 rows, same k) fall in
-// distinct bank groups. The four waves split K into quarters; each streams
-// its quarter of the packed tile (coalesced 1 KB loads, D steps ahead,
-// every load unconditional) against the x fragments from LDS, and with `ng`
-// gathers its rows' sums of squares from the same fragments. Waves 1..3 hand
-// their partial tiles and sums to wave 0, which adds them in wave order and
-// applies the norm scale 1/sqrt(ss/K + 1e-5) and the epilogue (as
-// k_gemm_skinny).
-template <int WT, int MT, int KC, int D>
-__global__ __launch_bounds__(256) void k_gemm_pk(GemvArgs a, const uint4* __restrict__ pk) {
-  constexpr uint32_t BM = 16 * MT, WP = WT == 1 ? 1 : 2;
-  __shared__ __align__(1024) float xs[BM * KC];
-  __shared__ f32x4_t red[3][MT][64];
-  __shared__ float ssr[4][BM];
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
-  const uint32_t K = a.K, U = K >> 2, nsa = K >> 5, ns = K >> 7;
-  const uint32_t m0 = blockIdx.y * BM, t = blockIdx.x;
-  const bool norm = a.ng != nullptr;
-  // the wave's weight steps: tile t, steps wv ns .. wv ns + ns - 1
-  const uint4* wsrc = pk + ((size_t)t * nsa + wv * ns) * (64 * WP) + lane;
-  uint4 wr[D][WP];
-  auto wload = [&](int u, uint32_t s) {
-#pragma unroll
-    for (uint32_t p = 0; p < WP; p++) wr[u][p] = wsrc[(size_t)s * 64 * WP + 64 * p];
-  };
-#pragma unroll
-  for (int u = 0; u < D; u++) wload(u, min((uint32_t)u, ns - 1));
-  // x rows (clamped to the batch; rows past it are discarded) and gains
-  for (uint32_t q0 = wv * 64; q0 < BM * U; q0 += 256) {
-    const uint32_t q = q0 + lane, r = q / U, u = q - r * U;
-    const uint32_t m = min(m0 + r, a.B - 1);
-    __builtin_amdgcn_global_load_lds((const void*)(a.X + (size_t)m * a.ldx + 4 * (u ^ (r & 7))),
-                                     (lds_void*)(xs + 4 * q0), 16, 0, 0);
-  }
-  ANA_VMCNT(0);
-  __syncthreads();
-  f32x4_t acc[MT];
-  float ss[MT];
-#pragma unroll
-  for (int tt = 0; tt < MT; tt++) {
-    acc[tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    ss[tt] = 0.0f;
-  }
-  const uint32_t kb_u = wv * (U >> 2);
-  auto step = [&](int u, uint32_t s) {
-    const uint32_t v0 = kb_u + 8 * s + 2 * g4;
-    float w[8];
-    if constexpr (WT == 0) {
-      w[0] = __uint_as_float(wr[u][0].x); w[1] = __uint_as_float(wr[u][0].y);
-      w[2] = __uint_as_float(wr[u][0].z); w[3] = __uint_as_float(wr[u][0].w);
-      w[4] = __uint_as_float(wr[u][WP - 1].x); w[5] = __uint_as_float(wr[u][WP - 1].y);
-      w[6] = __uint_as_float(wr[u][WP - 1].z); w[7] = __uint_as_float(wr[u][WP - 1].w);
-    }
-#pragma unroll
-    for (int tt = 0; tt < MT; tt++) {
-      const uint32_t r = 16 * tt + r16, base = r * U, sw = r & 7;
-      const float4 x0 = *reinterpret_cast<const float4*>(xs + 4 * (base + (v0 ^ sw)));
-      const float4 x1 = *reinterpret_cast<const float4*>(xs + 4 * (base + ((v0 + 1) ^ sw)));
-      const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-      if (norm) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) ss[tt] += x[e] * x[e];
-      }
-      if constexpr (WT == 0) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[e], w[e], acc[tt], 0, 0, 0);
-      } else {
-        bf16x8_t hi, lo;
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          hi[e] = (__bf16)x[e];
-          lo[e] = (__bf16)(x[e] - (float)hi[e]);
-        }
-        const bf16x8_t wb8 = __builtin_bit_cast(bf16x8_t, wr[u][0]);
-        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, wb8, acc[tt], 0, 0, 0);
-        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, wb8, acc[tt], 0, 0, 0);
-      }
-    }
-  };
-  for (uint32_t s0 = 0; s0 < ns; s0 += D) {
-#pragma unroll
-    for (int u = 0; u < D; u++) {
-      const uint32_t s = s0 + u;
-      if (s < ns) step(u, s);
-      wload(u, min(s + D, ns - 1));
-    }
-  }
-  if (wv > 0) {
-#pragma unroll
-    for (int tt = 0; tt < MT; tt++) red[wv - 1][tt][lane] = acc[tt];
-  }
-  if (norm) {
-#pragma unroll
-    for (int tt = 0; tt < MT; tt++) {
-      float v = ss[tt];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      if (g4 == 0) ssr[wv][16 * tt + r16] = v;
-    }
-  }
-  __syncthreads();
-  if (wv > 0) return;
-  const Segs sgs(a);
-  const float* w_;
-  uint32_t sg, lr;
-  const bool nok = sgs.row(16, t, r16, &w_, &sg, &lr);
-#pragma unroll
-  for (int tt = 0; tt < MT; tt++) {
-    f32x4_t y4 = acc[tt];
-#pragma unroll
-    for (int p = 0; p < 3; p++) {
-      const f32x4_t o = red[p][tt][lane];
-      y4[0] += o[0]; y4[1] += o[1]; y4[2] += o[2]; y4[3] += o[3];
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const uint32_t mi = 16 * tt + 4 * g4 + r, m = m0 + mi;
-      float y = y4[r];
-      if (norm) y *= 1.0f / sqrtf((((ssr[0][mi] + ssr[1][mi]) + ssr[2][mi]) + ssr[3][mi]) / (float)K + 1.0e-5f);
-      if (a.mode == GM_SILU) {
-        const float up = __shfl_xor(y, 8, 64);
-        if (r16 < 8 && nok && m < a.B) a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = fast_silu(y) * up;
-      } else if (nok && m < a.B) {
-        if (a.mode == GM_RESID) y = a.R[(size_t)m * a.ldr + lr] + y;
-        if (sg) a.seg[1].Y[(size_t)m * a.seg[1].ldy + lr] = y;
-        else a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = y;
-      }
-    }
-  }
-}
-
 // f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>), in order
 template <typename F, int... I>
 __device__ __forceinline__ void static_for_(F&& f, std::integer_sequence<int, I...>) {
@@ -1329,15 +1027,26 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_(f, std::make_integer_sequence<int, N>{});
 }
 
-// The same product with each wave on its own: K = 128 NS, and wave w's
-// quarter is NS steps of 32 k. The wave issues, per step, its weight pieces
-// (into a ring of D register sets) and two global_load_lds_dwordx4 of the 16
-// batch rows' x for that step (each one 1 KB: 8 rows x 128 bytes, the row's
-// 16-byte units at unit ^ (row & 7)) into an LDS block of its own, so its
-// loads retire in issue order: before step s it waits until only the ops of
-// steps s + 1 .. s + D - 1 are outstanding (a count fixed at compile time)
-// and reads the step's x with no barrier. Norm gains folded into the packed
-// weights; sums of squares, reduction and epilogue as k_gemm_pk.
+// Decode batches and prefill steps of 5..127 rows in the fast modes:
+// Y[m][n] = sum_k X[m][k] W[n][k] over packed weights (the norm gains folded
+// in when `ng` is set). A workgroup owns one 16-row weight tile and 16 batch
+// rows; K = 128 NS, and its four waves take a quarter of K each (NS steps of
+// 32 k), every wave on its own. Per step a wave issues its weight pieces
+// (coalesced 1 KB loads into a ring of D register sets) and two
+// global_load_lds_dwordx4 of the 16 rows' x for that step (each 1 KB: 8 rows
+// x 128 bytes, a row's 16-byte units at unit ^ (row & 7), so the fragment
+// reads of 16 rows at one k fall in distinct bank groups) into an LDS block
+// of its own. Its loads retire in issue order: before step s it waits until
+// only the ops of steps s + 1 .. s + D - 1 are outstanding (a count fixed at
+// compile time) and reads the step's x with no barrier. MFMA operands: lane
+// l holds row l % 16 of x and of the tile at k = 8 (l / 16) + e of the step;
+// fp32 (WT 0) takes v_mfma_f32_16x16x4f32 once per e, bf16 (WT 1) one
+// v_mfma_f32_16x16x32_bf16 on the x head and one on its remainder. With `ng`
+// each wave also sums its rows' x^2 from the same fragments. Waves 1..3 hand
+// their partial tiles and sums to wave 0, which adds them in wave order and
+// applies the norm scale 1/sqrt(ss/K + 1e-5) and the epilogue (plain,
+// residual, SiLU with tile rows 0..7 gate j and 8..15 up j). The result
+// tile: lane l holds batch rows 4 (l / 16) + r, weight row l % 16.
 template <int WT, int NS, int D>
 __global__ __launch_bounds__(256) void k_gemm_pw(GemvArgs a, const uint4* __restrict__ pk) {
   constexpr int WP = WT == 1 ? 1 : 2, OPS = WP + 2;
@@ -1439,79 +1148,32 @@ bool gemm_pk_fits(const GemvArgs& a) {
          (reinterpret_cast<uintptr_t>(a.X) & 15) == 0;
 }
 
-hipError_t launch_gemm_pk(const GemvArgs& a, const void* pk, int bf, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
-                          uint32_t mt) {
+template <int NS>
+static hipError_t pw_go(const GemvArgs& a, const uint4* p, int bf, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  constexpr int D = NS < 8 ? NS : 8;
+  const dim3 grid(pk_tiles(a), (a.B + 15) / 16);
+  if (bf) ANA_LAUNCH_F((k_gemm_pw<1, NS, D>), grid, dim3(256), 0, st, e0, e1, a, p);
+  else ANA_LAUNCH_F((k_gemm_pw<0, NS, D>), grid, dim3(256), 0, st, e0, e1, a, p);
+  return hipGetLastError();
+}
+
+template <int... I>
+static hipError_t pw_dispatch(const GemvArgs& a, const uint4* p, int bf, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
+                              std::integer_sequence<int, I...>) {
+  hipError_t e = hipErrorInvalidValue;
+  ((a.K == 128u * (I + 1) ? (void)(e = pw_go<I + 1>(a, p, bf, st, e0, e1)) : (void)0), ...);
+  return e;
+}
+
+hipError_t launch_gemm_pk(const GemvArgs& a, const void* pk, int bf, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   if (!gemm_pk_fits(a) || !pk) return hipErrorInvalidValue;
-  const uint32_t tiles = pk_tiles(a);
-  const uint4* p = static_cast<const uint4*>(pk);
-  if (mt == 0) {
-    // one wave per K quarter, each on its own: the K this library meets
-    const dim3 g1(tiles, (a.B + 15) / 16);
-#define ANA_PW(NS, D)                                                                          \
-  do {                                                                                         \
-    if (bf) ANA_LAUNCH_F((k_gemm_pw<1, NS, D>), g1, dim3(256), 0, st, e0, e1, a, p);          \
-    else ANA_LAUNCH_F((k_gemm_pw<0, NS, D>), g1, dim3(256), 0, st, e0, e1, a, p);             \
-    return hipGetLastError();                                                                  \
-  } while (0)
-    switch (a.K) {
-      case 256: ANA_PW(2, 2);
-      case 768: ANA_PW(6, 6);
-      case 1024: ANA_PW(8, 8);
-      case 2048: ANA_PW(16, 8);
-      default: break;
-    }
-#undef ANA_PW
-    mt = 1;
-  }
-  if (mt == 2 && a.K > 768) return hipErrorInvalidValue;
-  const dim3 grid(tiles, (a.B + 16 * mt - 1) / (16 * mt));
-  if (bf) {
-    if (mt == 2) ANA_LAUNCH_F((k_gemm_pk<1, 2, 768, 6>), grid, dim3(256), 0, st, e0, e1, a, p);
-    else if (a.K <= 768) ANA_LAUNCH_F((k_gemm_pk<1, 1, 768, 6>), grid, dim3(256), 0, st, e0, e1, a, p);
-    else ANA_LAUNCH_F((k_gemm_pk<1, 1, 2048, 8>), grid, dim3(256), 0, st, e0, e1, a, p);
-  } else {
-    if (mt == 2) ANA_LAUNCH_F((k_gemm_pk<0, 2, 768, 6>), grid, dim3(256), 0, st, e0, e1, a, p);
-    else if (a.K <= 768) ANA_LAUNCH_F((k_gemm_pk<0, 1, 768, 6>), grid, dim3(256), 0, st, e0, e1, a, p);
-    else ANA_LAUNCH_F((k_gemm_pk<0, 1, 2048, 8>), grid, dim3(256), 0, st, e0, e1, a, p);
-  }
-  return hipGetLastError();
-}
-
-// The batch tile of k_gemm_skinny: the largest of 64, 32, 16 rows that
-// still gives a workgroup per CU (256) over the weight tiles.
-static uint32_t skinny_mt(uint32_t tiles, uint32_t B) {
-  for (uint32_t mt = 4; mt > 1; mt >>= 1)
-    if (tiles * ((B + 16 * mt - 1) / (16 * mt)) >= 256) return mt;
-  return 1;
-}
-
-hipError_t launch_gemm_skinny(const GemvArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1, uint32_t mt) {
-  if (a.amax || a.B == 0 || (a.K % 128) || a.K > kSkinnyMaxK || (a.ldx & 3)) return hipErrorInvalidValue;
-  const bool bf = a.Wh0 != nullptr;
-  if (bf && a.nseg > 1 && !a.Wh1) return hipErrorInvalidValue;
-  const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
-                                          : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
-  const uint32_t per = a.mode == GM_SILU ? 8 : 16;
-  const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
-  if (mt == 0) mt = skinny_mt(tiles, a.B);
-  dim3 grid(tiles, (a.B + 16 * mt - 1) / (16 * mt));
-  if (bf) {
-    if (mt == 4) ANA_LAUNCH_F((k_gemm_skinny<1, 4, 3>), grid, dim3(256), 0, st, e0, e1, a);
-    else if (mt == 2) ANA_LAUNCH_F((k_gemm_skinny<1, 2, 4>), grid, dim3(256), 0, st, e0, e1, a);
-    else ANA_LAUNCH_F((k_gemm_skinny<1, 1, 4>), grid, dim3(256), 0, st, e0, e1, a);
-  } else {
-    if (mt == 4) ANA_LAUNCH_F((k_gemm_skinny<0, 4, 3>), grid, dim3(256), 0, st, e0, e1, a);
-    else if (mt == 2) ANA_LAUNCH_F((k_gemm_skinny<0, 2, 4>), grid, dim3(256), 0, st, e0, e1, a);
-    else ANA_LAUNCH_F((k_gemm_skinny<0, 1, 4>), grid, dim3(256), 0, st, e0, e1, a);
-  }
-  return hipGetLastError();
+  return pw_dispatch(a, static_cast<const uint4*>(pk), bf, st, e0, e1, std::make_integer_sequence<int, 16>{});
 }
 
 hipError_t launch_gemm_mfma(const GemvArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   if (a.amax || (a.K & 7) || a.B == 0) return hipErrorInvalidValue;
   const bool bf = a.Wh0 != nullptr;
   if (bf && a.nseg > 1 && !a.Wh1) return hipErrorInvalidValue;
-  if (a.K % 128 == 0 && a.K <= kSkinnyMaxK && (a.ldx & 3) == 0) return launch_gemm_skinny(a, st, e0, e1, 0);
   const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
                                           : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
   const uint32_t per = a.mode == GM_SILU ? 8 : 16;
