@@ -1029,9 +1029,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // Decode batches and prefill steps of 5..127 rows in the fast modes:
 // Y[m][n] = sum_k X[m][k] W[n][k] over packed weights (the norm gains folded
-// in when `ng` is set). A workgroup owns one 16-row weight tile and 16 batch
-// rows; K = 128 NS, and its four waves take a quarter of K each (NS steps of
-// 32 k), every wave on its own. Per step a wave issues its weight pieces
+// in when `ng` is set). A workgroup owns NT 16-row weight tiles and 16 batch
+// rows (each x fragment serves the NT tiles); K = 128 NS, and its four
+// waves take a quarter of K each (NS steps of 32 k), every wave on its own. Per step a wave issues its weight pieces
 // (coalesced 1 KB loads into a ring of D register sets) and two
 // global_load_lds_dwordx4 of the 16 rows' x for that step (each 1 KB: 8 rows
 // x 128 bytes, a row's 16-byte units at unit ^ (row & 7), so the fragment
@@ -1047,34 +1047,43 @@ __device__ __forceinline__ void static_for(F&& f) {
 // applies the norm scale 1/sqrt(ss/K + 1e-5) and the epilogue (plain,
 // residual, SiLU with tile rows 0..7 gate j and 8..15 up j). The result
 // tile: lane l holds batch rows 4 (l / 16) + r, weight row l % 16.
-template <int WT, int NS, int D>
-__global__ __launch_bounds__(256) void k_gemm_pw(GemvArgs a, const uint4* __restrict__ pk) {
-  constexpr int WP = WT == 1 ? 1 : 2, OPS = WP + 2;
+template <int WT, int NS, int D, int NT>
+__global__ __launch_bounds__(256) void k_gemm_pw(GemvArgs a, const uint4* __restrict__ pk, uint32_t tiles) {
+  constexpr int WP = WT == 1 ? 1 : 2, OPS = NT * WP + 2;
   __shared__ __align__(1024) float xs[4][NS][512];
-  __shared__ f32x4_t red[3][64];
+  __shared__ f32x4_t red[3][NT][64];
   __shared__ float ssr[4][16];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
   const uint32_t K = 128 * NS, nsa = 4 * NS;
-  const uint32_t m0 = blockIdx.y * 16, t = blockIdx.x;
+  const uint32_t m0 = blockIdx.y * 16;
   const bool norm = a.ng != nullptr;
-  const uint4* wsrc = pk + ((size_t)t * nsa + wv * NS) * (64 * WP) + lane;
+  // the workgroup's tiles NT x .. NT x + NT - 1; one past the last reads the
+  // last tile again and stores nothing
+  const uint4* wsrc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; j++)
+    wsrc[j] = pk + ((size_t)min(NT * blockIdx.x + j, tiles - 1) * nsa + wv * NS) * (64 * WP) + lane;
   // this lane's x piece in each half of a step: row 8 h + (lane >> 3), its
   // unit (lane & 7) ^ row
   const uint32_t dr = lane >> 3, sl = (lane & 7) ^ dr;
   uint32_t xo[2];
 #pragma unroll
   for (int h = 0; h < 2; h++) xo[h] = min(m0 + 8 * h + dr, a.B - 1) * a.ldx + wv * (K / 4) + 4 * sl;
-  uint4 wr[D][WP];
+  uint4 wr[D][NT][WP];
   auto issue = [&](auto S) {
     constexpr int s = decltype(S)::value;
 #pragma unroll
-    for (int p = 0; p < WP; p++) wr[s % D][p] = wsrc[s * 64 * WP + 64 * p];
+    for (int j = 0; j < NT; j++)
+#pragma unroll
+      for (int p = 0; p < WP; p++) wr[s % D][j][p] = wsrc[j][s * 64 * WP + 64 * p];
 #pragma unroll
     for (int h = 0; h < 2; h++)
       __builtin_amdgcn_global_load_lds((const void*)(a.X + xo[h] + 32 * s), (lds_void*)&xs[wv][s][256 * h], 16, 0, 0);
   };
   static_for<(D < NS ? D : NS)>(issue);
-  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t acc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; j++) acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   float ss = 0.0f;
   const uint32_t fo0 = (r16 >> 3) * 256 + (r16 & 7) * 32 + 4 * ((2 * g4) ^ (r16 & 7));
   const uint32_t fo1 = (r16 >> 3) * 256 + (r16 & 7) * 32 + 4 * ((2 * g4 + 1) ^ (r16 & 7));
@@ -1090,11 +1099,15 @@ __global__ __launch_bounds__(256) void k_gemm_pw(GemvArgs a, const uint4* __rest
       for (int e = 0; e < 8; e++) ss += x[e] * x[e];
     }
     if constexpr (WT == 0) {
-      const uint4 w0 = wr[s % D][0], w1 = wr[s % D][WP - 1];
-      const float w[8] = {__uint_as_float(w0.x), __uint_as_float(w0.y), __uint_as_float(w0.z), __uint_as_float(w0.w),
-                          __uint_as_float(w1.x), __uint_as_float(w1.y), __uint_as_float(w1.z), __uint_as_float(w1.w)};
 #pragma unroll
-      for (int e = 0; e < 8; e++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[e], w[e], acc, 0, 0, 0);
+      for (int j = 0; j < NT; j++) {
+        const uint4 w0 = wr[s % D][j][0], w1 = wr[s % D][j][WP - 1];
+        const float w[8] = {__uint_as_float(w0.x), __uint_as_float(w0.y), __uint_as_float(w0.z),
+                            __uint_as_float(w0.w), __uint_as_float(w1.x), __uint_as_float(w1.y),
+                            __uint_as_float(w1.z), __uint_as_float(w1.w)};
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[e], w[e], acc[j], 0, 0, 0);
+      }
     } else {
       bf16x8_t hi, lo;
 #pragma unroll
@@ -1102,13 +1115,19 @@ __global__ __launch_bounds__(256) void k_gemm_pw(GemvArgs a, const uint4* __rest
         hi[e] = (__bf16)x[e];
         lo[e] = (__bf16)(x[e] - (float)hi[e]);
       }
-      const bf16x8_t wb8 = __builtin_bit_cast(bf16x8_t, wr[s % D][0]);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, wb8, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, wb8, acc, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < NT; j++) {
+        const bf16x8_t wb8 = __builtin_bit_cast(bf16x8_t, wr[s % D][j][0]);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, wb8, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, wb8, acc[j], 0, 0, 0);
+      }
     }
     if constexpr (s + D < NS) issue(std::integral_constant<int, s + D>{});
   });
-  if (wv > 0) red[wv - 1][lane] = acc;
+  if (wv > 0) {
+#pragma unroll
+    for (int j = 0; j < NT; j++) red[wv - 1][j][lane] = acc[j];
+  }
   if (norm) {
     float v = ss;
     v += __shfl_xor(v, 16, 64);
@@ -1118,27 +1137,37 @@ __global__ __launch_bounds__(256) void k_gemm_pw(GemvArgs a, const uint4* __rest
   __syncthreads();
   if (wv > 0) return;
   const Segs sgs(a);
-  const float* w_;
-  uint32_t sg, lr;
-  const bool nok = sgs.row(16, t, r16, &w_, &sg, &lr);
-  f32x4_t y4 = acc;
-#pragma unroll
-  for (int p = 0; p < 3; p++) {
-    const f32x4_t o = red[p][lane];
-    y4[0] += o[0]; y4[1] += o[1]; y4[2] += o[2]; y4[3] += o[3];
-  }
+  float rs[4];
 #pragma unroll
   for (int r = 0; r < 4; r++) {
-    const uint32_t mi = 4 * g4 + r, m = m0 + mi;
-    float y = y4[r];
-    if (norm) y *= 1.0f / sqrtf((((ssr[0][mi] + ssr[1][mi]) + ssr[2][mi]) + ssr[3][mi]) / (float)K + 1.0e-5f);
-    if (a.mode == GM_SILU) {
-      const float up = __shfl_xor(y, 8, 64);
-      if (r16 < 8 && nok && m < a.B) a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = fast_silu(y) * up;
-    } else if (nok && m < a.B) {
-      if (a.mode == GM_RESID) y = a.R[(size_t)m * a.ldr + lr] + y;
-      if (sg) a.seg[1].Y[(size_t)m * a.seg[1].ldy + lr] = y;
-      else a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = y;
+    const uint32_t mi = 4 * g4 + r;
+    rs[r] = norm ? 1.0f / sqrtf((((ssr[0][mi] + ssr[1][mi]) + ssr[2][mi]) + ssr[3][mi]) / (float)K + 1.0e-5f) : 1.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    const uint32_t t = NT * blockIdx.x + j;
+    const float* w_;
+    uint32_t sg, lr;
+    const bool nok = t < tiles && sgs.row(16, t, r16, &w_, &sg, &lr);
+    f32x4_t y4 = acc[j];
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+      const f32x4_t o = red[p][j][lane];
+      y4[0] += o[0]; y4[1] += o[1]; y4[2] += o[2]; y4[3] += o[3];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint32_t m = m0 + 4 * g4 + r;
+      float y = y4[r];
+      if (norm) y *= rs[r];
+      if (a.mode == GM_SILU) {
+        const float up = __shfl_xor(y, 8, 64);
+        if (r16 < 8 && nok && m < a.B) a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = fast_silu(y) * up;
+      } else if (nok && m < a.B) {
+        if (a.mode == GM_RESID) y = a.R[(size_t)m * a.ldr + lr] + y;
+        if (sg) a.seg[1].Y[(size_t)m * a.seg[1].ldy + lr] = y;
+        else a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = y;
+      }
     }
   }
 }
@@ -1148,12 +1177,28 @@ bool gemm_pk_fits(const GemvArgs& a) {
          (reinterpret_cast<uintptr_t>(a.X) & 15) == 0;
 }
 
+// two weight tiles a workgroup when the one-tile grid has 4 to 16
+// workgroups a CU (measured at B = 64: gate|up 10.3 -> 8.9 us fp32, 7.9 ->
+// 6.4 us bf16; with fewer, q|k|v|z and Wo lose the spread over the CUs,
+// with more, the head gains nothing), and K <= 1024 (the register ring of
+// two tiles' weights)
+constexpr uint32_t kPwTwoTileMin = 1024, kPwTwoTileMax = 4096;
+
 template <int NS>
 static hipError_t pw_go(const GemvArgs& a, const uint4* p, int bf, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   constexpr int D = NS < 8 ? NS : 8;
-  const dim3 grid(pk_tiles(a), (a.B + 15) / 16);
-  if (bf) ANA_LAUNCH_F((k_gemm_pw<1, NS, D>), grid, dim3(256), 0, st, e0, e1, a, p);
-  else ANA_LAUNCH_F((k_gemm_pw<0, NS, D>), grid, dim3(256), 0, st, e0, e1, a, p);
+  const uint32_t tiles = pk_tiles(a), mt = (a.B + 15) / 16;
+  if constexpr (NS <= 8) {
+    if (tiles * mt >= kPwTwoTileMin && tiles * mt <= kPwTwoTileMax) {
+      const dim3 grid((tiles + 1) / 2, mt);
+      if (bf) ANA_LAUNCH_F((k_gemm_pw<1, NS, D, 2>), grid, dim3(256), 0, st, e0, e1, a, p, tiles);
+      else ANA_LAUNCH_F((k_gemm_pw<0, NS, D, 2>), grid, dim3(256), 0, st, e0, e1, a, p, tiles);
+      return hipGetLastError();
+    }
+  }
+  const dim3 grid(tiles, mt);
+  if (bf) ANA_LAUNCH_F((k_gemm_pw<1, NS, D, 1>), grid, dim3(256), 0, st, e0, e1, a, p, tiles);
+  else ANA_LAUNCH_F((k_gemm_pw<0, NS, D, 1>), grid, dim3(256), 0, st, e0, e1, a, p, tiles);
   return hipGetLastError();
 }
 

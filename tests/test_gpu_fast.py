@@ -43,6 +43,20 @@ def small_ckpt(tmp_path_factory):
     return p
 
 
+# d and f multiples of 128 (the packed decode-batch products take K = 256
+# and 1024 here; gate|up at 120 rows takes two weight tiles a workgroup),
+# every arm on, hd 64
+MID = cf.Config(vocab=258, ctx=64, d=256, f=1024, layers=4, heads=4, rglru=True, qk=True, sinks=True, tied=True)
+
+
+@pytest.fixture(scope="module")
+def mid_ckpt(tmp_path_factory):
+    d = tmp_path_factory.mktemp("ckm")
+    p = str(d / "mid.ftc2")
+    ckpt.write(p, MID, ckpt.init_params(MID, "normal", 5))
+    return p
+
+
 @pytest.fixture(scope="module")
 def big_ckpt(tmp_path_factory):
     d = tmp_path_factory.mktemp("ckb")
@@ -65,6 +79,37 @@ def test_fast_small_decode(oracle, small_ckpt, mode):
             st.feed(pos, t)
             e = rel_err(dec.logits([0])[0], st.logits())
             worst = max(worst, e)
+    print(f"worst relative error {worst:.3e}", flush=True)
+    assert worst <= TOL[mode], worst
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_fast_115m_batch6(oracle, big_ckpt, mode):
+    """fp100m at ctx 2048, six sequences: decode steps of more than four
+    rows, so every layer product (K 768 and 2048) and the head run on the
+    packed matrix-core GEMM; logits against each sequence's oracle run."""
+    print(f"case fast 115m batch6 mode {mode}", flush=True)
+    oracle.set_threads(8)
+    m = oracle.Model(big_ckpt)
+    n, pre, steps = 6, [5, 9, 14, 20, 3, 11], 4
+    prompts = [[int(t) for t in ckpt.prompt(17 + i, pre[i] + steps, m.vocab)] for i in range(n)]
+    sts = [oracle.State(m) for _ in range(n)]
+    worst = 0.0
+    with ana_amd.Decoder(big_ckpt, max_seqs=n, numerics=mode) as dec:
+        for i in range(n):
+            dec.feeds(i, 0, prompts[i][: pre[i]])
+            for p in range(pre[i]):
+                sts[i].feed(p, prompts[i][p])
+        for k in range(steps):
+            pos = [pre[i] + k for i in range(n)]
+            tok = [prompts[i][pos[i]] for i in range(n)]
+            dec.feed(list(range(n)), pos, tok)
+            for i in range(n):
+                sts[i].feed(pos[i], tok[i])
+            if k in (0, steps - 1):
+                got = dec.logits(list(range(n)))
+                for i in range(n):
+                    worst = max(worst, rel_err(got[i], sts[i].logits()))
     print(f"worst relative error {worst:.3e}", flush=True)
     assert worst <= TOL[mode], worst
 
@@ -196,23 +241,27 @@ def test_fast_prefill(oracle, small_ckpt, noarms_ckpt, mode, arms, chunk):
 
 
 @pytest.mark.parametrize("mode", MODES)
-@pytest.mark.parametrize("shape", ["ragged5", "wide6"])
-def test_fast_feeds_n(oracle, small_ckpt, mode, shape):
+@pytest.mark.parametrize("shape", ["ragged5", "wide6", "rows120"])
+@pytest.mark.parametrize("model", ["small", "mid"])
+def test_fast_feeds_n(oracle, small_ckpt, mid_ckpt, mode, shape, model):
     """ana_feeds_n in a fast mode: ragged prompts prefilled together
-    (matrix-core products over all their rows: 93 rows a step, or 288 for
-    the 128 x 128 tiles), then a decode step each; logits against the
-    oracle."""
-    print(f"case fast feeds_n {shape} mode {mode}", flush=True)
-    m = oracle.Model(small_ckpt)
+    (matrix-core products over all their rows: 93 rows a step; 288 for the
+    128 x 128 tiles; 120, where gate|up takes two weight tiles a
+    workgroup), then a decode step each; logits against the oracle."""
+    print(f"case fast feeds_n {model} {shape} mode {mode}", flush=True)
+    path = small_ckpt if model == "small" else mid_ckpt
+    m = oracle.Model(path)
     if shape == "ragged5":
         seqs, lens, chunk = [3, 0, 2, 4, 1], [40, 3, 17, 70, 9], 32
+    elif shape == "rows120":
+        seqs, lens, chunk = [1, 3, 0, 2], [60, 45, 30, 90], 30
     else:
         seqs, lens, chunk = [5, 0, 2, 4, 1, 3], [60, 100, 49, 77, 90, 63], 48
     n = len(seqs)
     rng = np.random.default_rng(22)
     toks = [rng.integers(0, m.vocab, size=k + 1).astype(np.uint32) for k in lens]
     worst = 0.0
-    with ana_amd.Decoder(small_ckpt, max_seqs=n, prefill_chunk=chunk, numerics=mode) as dec:
+    with ana_amd.Decoder(path, max_seqs=n, prefill_chunk=chunk, numerics=mode) as dec:
         dec.feeds_n(seqs, [0] * n, [t[:-1] for t in toks])
         for i, s in enumerate(seqs):
             dec.feed([s], [lens[i]], [int(toks[i][-1])])
@@ -251,14 +300,17 @@ def test_fast_score_n(oracle, small_ckpt, mode):
 
 
 @pytest.mark.parametrize("mode", MODES)
-def test_fast_decode_batch_products(oracle, small_ckpt, mode):
+@pytest.mark.parametrize("model", ["small", "mid"])
+def test_fast_decode_batch_products(oracle, small_ckpt, mid_ckpt, mode, model):
     """Decode steps of more than kSmallB sequences in a fast mode: the layer
-    products and the head on the matrix cores (packed weights, one row a
-    sequence), GLA and attention exact. Seven sequences from ragged starts, 70
-    teacher-forced steps across the ring wrap; every sequence's logits
-    against its own oracle run at four steps."""
-    print(f"case fast decode batch products mode {mode}", flush=True)
-    m = oracle.Model(small_ckpt)
+    products and the head on the matrix cores (the packed GEMM where K is a
+    multiple of 128, the mid model; the tiled fallback for the small model's
+    K = 64 and 192), GLA and attention exact. Seven sequences from ragged
+    starts, 70 teacher-forced steps across the ring wrap; every sequence's
+    logits against its own oracle run at four steps."""
+    print(f"case fast decode batch products {model} mode {mode}", flush=True)
+    path = small_ckpt if model == "small" else mid_ckpt
+    m = oracle.Model(path)
     n, steps = 7, 70
     starts = [3, 1, 6, 2, 8, 5, 4]
     seqs = [2, 0, 3, 6, 5, 1, 4]
@@ -266,7 +318,7 @@ def test_fast_decode_batch_products(oracle, small_ckpt, mode):
     toks = rng.integers(0, m.vocab, size=(n, steps + 8)).astype(np.uint32)
     sts = [oracle.State(m) for _ in range(n)]
     worst = 0.0
-    with ana_amd.Decoder(small_ckpt, max_seqs=n, prefill_chunk=8, numerics=mode) as dec:
+    with ana_amd.Decoder(path, max_seqs=n, prefill_chunk=8, numerics=mode) as dec:
         for i in range(n):
             dec.feeds(seqs[i], 0, toks[i, : starts[i]])
             for p in range(starts[i]):
