@@ -235,6 +235,37 @@ def test_sampler_32k_vocab(oracle, tmp_path):
         assert np.array_equal(bits(lgs[1]), bits(st.logits()))
 
 
+def test_115m_batch8(oracle, tmp_path):
+    """fp100m, eight sequences decoded together from staggered positions:
+    the GLA step on one wave per (head, sequence) and the one-workgroup
+    attention at hd 64, bit for bit against each sequence's oracle run."""
+    c = cf.FP100M
+    path = str(tmp_path / "fp100m8.ftc2")
+    ckpt.write(path, c, ckpt.init_params(c, "normal", 2))
+    print("case 115m batch8", flush=True)
+    oracle.set_threads(8)
+    m = oracle.Model(path)
+    n, steps = 8, 3
+    pre = [1, 4, 2, 6, 3, 5, 2, 7]
+    prompts = [[int(t) for t in ckpt.prompt(30 + i, pre[i] + steps, c.vocab)] for i in range(n)]
+    sts = [oracle.State(m) for _ in range(n)]
+    with ana_amd.Decoder(path, max_seqs=n) as dec:
+        for i in range(n):
+            for p in range(pre[i]):
+                dec.feed([i], [p], [prompts[i][p]])
+                sts[i].feed(p, prompts[i][p])
+        for k in range(steps):
+            pos = [pre[i] + k for i in range(n)]
+            tok = [prompts[i][pos[i]] for i in range(n)]
+            dec.feed(list(range(n)), pos, tok)
+            for i in range(n):
+                sts[i].feed(pos[i], tok[i])
+        got = dec.logits(list(range(n)))
+    for i in range(n):
+        want = sts[i].logits()
+        assert np.array_equal(bits(got[i]), bits(want)), (i, np.abs(got[i] - want).max())
+
+
 def test_115m_shape(oracle, tmp_path):
     """fp100m's dimensions (d 768, f 2048, 12 layers, 12 heads, vocab 32768,
     all arms) at ctx 2048: a prompt through feeds, then steps, bit for bit."""
