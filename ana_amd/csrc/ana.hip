@@ -382,6 +382,9 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
     if (c->Wh) by -= 2.0 * (g.seg[0].rows + (g.nseg > 1 ? g.seg[1].rows : 0)) * g.K;
     ProfScope ps(c, kind, by, true);
     if (small) return launch_gemv_fast(g, c->st, ps.start(), ps.stop());
+    if (pe && kind == ANA_K_HEAD && head_pw_fits(g))
+      return launch_head_pw(g, static_cast<const char*>(c->PK) + pe->off, c->Wh != nullptr, c->st, ps.start(),
+                            ps.stop());
     if (pe)
       return launch_gemm_pk(g, static_cast<const char*>(c->PK) + pe->off, c->Wh != nullptr, c->st, ps.start(),
                             ps.stop());

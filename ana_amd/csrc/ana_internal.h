@@ -286,6 +286,12 @@ hipError_t launch_pack(const GemvArgs& a, void* dst, int bf, hipStream_t st);
 bool gemm_pk_fits(const GemvArgs& a);
 hipError_t launch_gemm_pk(const GemvArgs& a, const void* pk, int bf, hipStream_t st, hipEvent_t e0,
                           hipEvent_t e1);
+// The wide form for the LM head (plain products, K % 256 == 0,
+// K <= kHeadMaxK): 32 batch rows in LDS per workgroup, 16 weight tiles each
+constexpr uint32_t kHeadMaxK = 1024;
+bool head_pw_fits(const GemvArgs& a);
+hipError_t launch_head_pw(const GemvArgs& a, const void* pk, int bf, hipStream_t st, hipEvent_t e0,
+                          hipEvent_t e1);
 // the same for 128 rows or more, 128 x 128 tiles
 hipError_t launch_gemm_big(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nullptr,
                            hipEvent_t e1 = nullptr);

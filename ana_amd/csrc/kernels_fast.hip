@@ -1172,6 +1172,151 @@ __global__ __launch_bounds__(256) void k_gemm_pw(GemvArgs a, const uint4* __rest
   }
 }
 
+// Wide products over packed weights at 5..127 rows (the LM head): a
+// workgroup of NW waves owns 32 batch rows and TPW consecutive 16-row weight
+// tiles. The 32 rows' x go to LDS once (global_load_lds_dwordx4, a row's
+// 16-byte units at unit ^ (row & 7)); with `ng` the waves then share the
+// rows for their norm scales. Wave w takes tiles w, w + NW, .. of the TPW,
+// each over the whole K, its (tile, 32-k step) pieces as one stream in
+// blocks of D steps (D divides a tile's K / 32 steps, so a block never spans
+// two tiles), double-buffered in registers with every load unconditional
+// and the index clamped: the next block's weights, the next tile's too, are
+// in flight while a block computes. After a tile's last block the wave
+// scales, stores and clears its two accumulators (batch rows 0..15 and
+// 16..31). The x tile is read once per TPW weight tiles instead of once per
+// tile.
+template <int WT, int TPW, int D, int NW>
+__global__ __launch_bounds__(64 * NW) void k_head_pw(GemvArgs a, const uint4* __restrict__ pk, uint32_t tiles) {
+  constexpr int WP = WT == 1 ? 1 : 2;
+  constexpr uint32_t BM = 32;
+  __shared__ __align__(1024) float xs[BM * kHeadMaxK];
+  __shared__ float rsc[BM];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+  const uint32_t K = a.K, U = K >> 2, nsa = K >> 5;
+  const uint32_t m0 = blockIdx.y * BM, t0 = blockIdx.x * TPW;
+  const bool norm = a.ng != nullptr;
+  // this wave's blocks: tiles t0 + wv + NW i (i < TPW / NW), nsa / D blocks each
+  const uint32_t bpt = nsa / D, nb = (TPW / NW) * bpt;
+  auto block_base = [&](uint32_t k) {   // first piece of block k (clamped)
+    k = min(k, nb - 1);
+    const uint32_t i = k / bpt, s0 = (k - i * bpt) * D;
+    const uint32_t t = min(t0 + wv + NW * i, tiles - 1);
+    return pk + ((size_t)t * nsa + s0) * (64 * WP) + lane;
+  };
+  uint4 wr[D][WP];
+  auto wload = [&](const uint4* p) {
+#pragma unroll
+    for (int u = 0; u < D; u++)
+#pragma unroll
+      for (int j = 0; j < WP; j++) wr[u][j] = p[(u * WP + j) * 64];
+  };
+  wload(block_base(0));
+  for (uint32_t q0 = wv * 64; q0 < BM * U; q0 += 64 * NW) {
+    const uint32_t q = q0 + lane, r = q / U, u = q - r * U;
+    const uint32_t m = min(m0 + r, a.B - 1);
+    __builtin_amdgcn_global_load_lds((const void*)(a.X + (size_t)m * a.ldx + 4 * (u ^ (r & 7))),
+                                     (lds_void*)(xs + 4 * q0), 16, 0, 0);
+  }
+  ANA_VMCNT(0);
+  __syncthreads();
+  if (norm) {
+    for (uint32_t r = wv; r < BM; r += NW) {
+      float ss = 0.0f;
+      for (uint32_t v = lane; v < U; v += 64) {
+        const float4 x = *reinterpret_cast<const float4*>(xs + 4 * (r * U + (v ^ (r & 7))));
+        ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) rsc[r] = 1.0f / sqrtf(ss / (float)K + 1.0e-5f);
+    }
+    __syncthreads();
+  }
+  f32x4_t acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+  const Segs sgs(a);
+  for (uint32_t k = 0; k < nb; k++) {
+    const uint32_t i = k / bpt, s0 = (k - i * bpt) * D;
+    // this block's weights out of the ring, the next block's in
+    uint4 cw[D][WP];
+#pragma unroll
+    for (int u = 0; u < D; u++)
+#pragma unroll
+      for (int j = 0; j < WP; j++) cw[u][j] = wr[u][j];
+    wload(block_base(k + 1));
+#pragma unroll
+    for (int u = 0; u < D; u++) {
+      const uint32_t v0 = 8 * (s0 + u) + 2 * g4;
+      float w[8];
+      if constexpr (WT == 0) {
+        w[0] = __uint_as_float(cw[u][0].x); w[1] = __uint_as_float(cw[u][0].y);
+        w[2] = __uint_as_float(cw[u][0].z); w[3] = __uint_as_float(cw[u][0].w);
+        w[4] = __uint_as_float(cw[u][WP - 1].x); w[5] = __uint_as_float(cw[u][WP - 1].y);
+        w[6] = __uint_as_float(cw[u][WP - 1].z); w[7] = __uint_as_float(cw[u][WP - 1].w);
+      }
+#pragma unroll
+      for (int tt = 0; tt < 2; tt++) {
+        const uint32_t r = 16 * tt + r16, base = r * U, sw = r & 7;
+        const float4 x0 = *reinterpret_cast<const float4*>(xs + 4 * (base + (v0 ^ sw)));
+        const float4 x1 = *reinterpret_cast<const float4*>(xs + 4 * (base + ((v0 + 1) ^ sw)));
+        const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        if constexpr (WT == 0) {
+#pragma unroll
+          for (int e = 0; e < 8; e++) acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[e], w[e], acc[tt], 0, 0, 0);
+        } else {
+          bf16x8_t hi, lo;
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            hi[e] = (__bf16)x[e];
+            lo[e] = (__bf16)(x[e] - (float)hi[e]);
+          }
+          const bf16x8_t wb8 = __builtin_bit_cast(bf16x8_t, cw[u][0]);
+          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, wb8, acc[tt], 0, 0, 0);
+          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, wb8, acc[tt], 0, 0, 0);
+        }
+      }
+    }
+    if (s0 + D == nsa) {
+      // the tile is done: scale, store, clear
+      const uint32_t t = t0 + wv + NW * i;
+      const float* w_;
+      uint32_t sg, lr;
+      const bool nok = t < tiles && sgs.row(16, t, r16, &w_, &sg, &lr);
+#pragma unroll
+      for (int tt = 0; tt < 2; tt++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const uint32_t mi = 16 * tt + 4 * g4 + r, m = m0 + mi;
+          float y = acc[tt][r];
+          if (norm) y *= rsc[mi];
+          if (nok && m < a.B) {
+            if (sg) a.seg[1].Y[(size_t)m * a.seg[1].ldy + lr] = y;
+            else a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = y;
+          }
+        }
+        acc[tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    }
+  }
+}
+
+bool head_pw_fits(const GemvArgs& a) {
+  return !a.amax && a.mode == GM_PLAIN && a.B > 0 && a.K % 256 == 0 && a.K <= kHeadMaxK && (a.ldx & 3) == 0 &&
+         (reinterpret_cast<uintptr_t>(a.X) & 15) == 0;
+}
+
+hipError_t launch_head_pw(const GemvArgs& a, const void* pk, int bf, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  if (!head_pw_fits(a) || !pk) return hipErrorInvalidValue;
+  constexpr int TPW = 16;
+  const uint32_t tiles = pk_tiles(a);
+  const dim3 grid((tiles + TPW - 1) / TPW, (a.B + 31) / 32);
+  const uint4* p = static_cast<const uint4*>(pk);
+  // the x tile fills LDS (one workgroup a CU): sixteen waves, four a SIMD,
+  // one tile each (measured at B = 64: 55 -> 41 us fp32, 37 -> 26 us bf16
+  // from four waves to sixteen)
+  if (bf) ANA_LAUNCH_F((k_head_pw<1, TPW, 4, 16>), grid, dim3(1024), 0, st, e0, e1, a, p, tiles);
+  else ANA_LAUNCH_F((k_head_pw<0, TPW, 4, 16>), grid, dim3(1024), 0, st, e0, e1, a, p, tiles);
+  return hipGetLastError();
+}
+
 bool gemm_pk_fits(const GemvArgs& a) {
   return !a.amax && a.B > 0 && a.K % 128 == 0 && a.K <= 2048 && (a.ldx & 3) == 0 &&
          (reinterpret_cast<uintptr_t>(a.X) & 15) == 0;
