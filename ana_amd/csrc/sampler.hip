@@ -22,6 +22,31 @@ struct Add { __device__ float operator()(float a, float b) const { return a + b;
 // F32.max a b = (a < b ? b : a): a is the left subtree
 struct Max { __device__ float operator()(float a, float b) const { return a < b ? b : a; } };
 
+// x[i] = row[base + i] for i < LPT (0 past v or when inactive): a thread's
+// LPT consecutive logits, as 16-byte loads when the run is whole and
+// aligned (each load of a wave then covers whole cache-line pieces instead
+// of one float of 64 lines)
+template <int LPT>
+__device__ __forceinline__ void load_run(const float* __restrict__ row, uint32_t base, uint32_t v, bool active,
+                                         float (&x)[LPT]) {
+  if constexpr (LPT % 4 == 0) {
+    if (active && base + LPT <= v && (reinterpret_cast<uintptr_t>(row + base) & 15) == 0) {
+      const float4* r4 = reinterpret_cast<const float4*>(row + base);
+#pragma unroll
+      for (int i = 0; i < LPT / 4; i++) {
+        const float4 f = r4[i];
+        x[4 * i + 0] = f.x;
+        x[4 * i + 1] = f.y;
+        x[4 * i + 2] = f.z;
+        x[4 * i + 3] = f.w;
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < LPT; i++) x[i] = (active && base + i < v) ? row[base + i] : 0.0f;
+}
+
 template <int LPT, class Op>
 __device__ __forceinline__ float local_reduce(const float (&x)[LPT], Op op) {
   float t[LPT];
@@ -149,8 +174,7 @@ __global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t
   const bool active = tid < NT;
   const float* lg = a.logits + (size_t)b * v;
   float x[LPT];
-#pragma unroll
-  for (int i = 0; i < LPT; i++) x[i] = (active && base + i < v) ? lg[base + i] : 0.0f;
+  load_run<LPT>(lg, base, v, active, x);
 
   // greedy on the store (dc.px.top, bend/Decode.bend:407-418): dd.pick's
   // least index reaching the max; only a NaN max falls back to argmax
@@ -310,8 +334,7 @@ __global__ __launch_bounds__(1024) void k_advance(AdvanceArgs a, uint32_t NT) {
       const bool active = tid < NT;
       const float* lg = a.logits + (size_t)b * v;
       float x[LPT];
-#pragma unroll
-      for (int i = 0; i < LPT; i++) x[i] = (active && base + i < v) ? lg[base + i] : 0.0f;
+      load_run<LPT>(lg, base, v, active, x);
       t = tree_argmax<LPT>(x, base, v, red, redi, tid, NT);
     }
   } else {
@@ -359,12 +382,9 @@ __global__ __launch_bounds__(1024) void k_ce(const float* __restrict__ logits, u
   const bool active = tid < NT;
   const float* lg = logits + (size_t)b * vocab;
   float x[LPT], pm[LPT];
+  load_run<LPT>(lg, base, vocab, active, x);
 #pragma unroll
-  for (int i = 0; i < LPT; i++) {
-    const bool in = active && base + i < vocab;
-    x[i] = in ? lg[base + i] : 0.0f;
-    pm[i] = in ? x[i] : -3.0e38f;
-  }
+  for (int i = 0; i < LPT; i++) pm[i] = (active && base + i < vocab) ? x[i] : -3.0e38f;
   const float m = tree_up(local_reduce<LPT>(pm, Max()), Max(), red, tid, NT);
   float e[LPT];
 #pragma unroll
