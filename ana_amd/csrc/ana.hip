@@ -934,9 +934,12 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
       if (c->gexec) { HIPCHK(c, hipGraphExecDestroy(c->gexec)); c->gexec = nullptr; }
       if (c->gexec_n) { HIPCHK(c, hipGraphExecDestroy(c->gexec_n)); c->gexec_n = nullptr; }
       if (int r = capture(1, &c->gexec)) return r;
-      if (int r = capture(kGraphSteps, &c->gexec_n)) return r;
       c->gkey = key;
     }
+    // the kGraphSteps graph only for a call that replays it (one-step calls,
+    // an agent loop's, never do)
+    if (steps >= kGraphSteps && !c->gexec_n)
+      if (int r = capture(kGraphSteps, &c->gexec_n)) return r;
     uint32_t k = 0;
     for (; k + kGraphSteps <= steps; k += kGraphSteps) HIPCHK(c, hipGraphLaunch(c->gexec_n, c->st));
     for (; k < steps; k++) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));

@@ -155,6 +155,32 @@ NUMERICS = {"exact": "exact_fp32: bit-exact with the reference's CPU kernels",
             "bf16": "bf16 weights, fp32 activations/accumulation/state; logits within 2e-2"}
 
 
+def run_agent(path: str, c, mode: str) -> dict:
+    """Many agent episodes decoded together (ana_amd.agent): 64 episodes of
+    a 128-token prompt, the v3 sampling settings, 48 draws a stretch, two
+    calls each; a call is a drawn id = 7 mod 61 and the stand-in tool's
+    echo is 24 ids, fed as unsampled tokens."""
+    from ana_amd import agent
+    st = ana_amd.Settings(float(np.float32(0.8)), 40, float(np.float32(0.9)))
+    eps = [agent.Episode([int(x) for x in ckpt.prompt(3000 + b, 128, c.vocab)], seed=b, budget=48, calls=2)
+           for b in range(64)]
+    is_call = lambda i, t: t[-1] % 61 == 7  # noqa: E731
+    tool = lambda i, t: [2 + (t[-1] * 31 + j) % (c.vocab - 2) for j in range(24)]  # noqa: E731
+    with ana_amd.Decoder(path, max_seqs=64, prefill_chunk=128, numerics=MODES[mode]) as dec:
+        agent.run(dec, eps[:8], st, is_call, tool)   # warm-up
+        t = time.perf_counter()
+        out = agent.run(dec, eps, st, is_call, tool)
+        dt = time.perf_counter() - t
+    drawn = sum(sum(o.drawn) for o in out)
+    fed = sum(len(o.drawn) - sum(o.drawn) for o in out)
+    log(f"agent {mode}: {drawn} drawn + {fed} fed tokens over 64 episodes in {dt:.3f}s")
+    return {"episodes": 64, "seconds": round(dt, 4), "drawn": drawn, "fed": fed,
+            "drawn_tok_s": round(drawn / dt, 1), "tok_s": round((drawn + fed) / dt, 1),
+            "endings": {w: sum(1 for o in out if o.why == w) for w in ("eos", "budget", "calls", "tool")},
+            "workload": "64 episodes (128-token prompts, T 0.8 / top-k 40 / top-p 0.9, 48 draws a stretch, "
+                        "2 calls; a call: drawn id = 7 mod 61; echo 24 ids fed unsampled); " + NUMERICS[mode]}
+
+
 def run_prefill(path: str, c) -> dict:
     """B=64 prefill on the matrix cores: 64 prompts of 512 tokens through
     ana_feeds_n at chunk 128 (8192 rows a product), in both fast modes."""
@@ -221,6 +247,7 @@ def main() -> int:
     ap.add_argument("--prefill", type=int, default=1, help="also measure B=64 x 512 prefill (1/0)")
     ap.add_argument("--prefill-only", type=int, default=0,
                     help="measure only the B=64 x 512 prefill and print its figures (1/0)")
+    ap.add_argument("--agent", type=int, default=1, help="also measure 64 agent episodes (1/0)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--ckpt", default=os.environ.get("ANA_BENCH_CKPT", "/tmp/ana_bench_fp100m.ftc2"))
     a = ap.parse_args()
@@ -264,6 +291,8 @@ def main() -> int:
                                       "time), 32 greedy steps at positions 128+; " + NUMERICS[m])
     if a.prefill:
         extra.update(run_prefill(path, c))
+    if a.agent:
+        extra["agent"] = run_agent(path, c, mode)
     cpu = cpu_baseline(path, c, a.cpu_seconds) if a.cpu_seconds > 0 else None
     kern = {k: {"launches": v[0], "ms": round(v[1], 4), "gb": round(v[2] / 1e9, 4)}
             for k, v in r1["stats"].items()}
