@@ -1397,7 +1397,12 @@ namespace ana {
 // rewrites the state). Pass 2, per (head, column block, sub-chunk j): the
 // state entering j, S_(j-1) = D_(j-1) (... (D_0 S_0 + U_0) ...) + U_(j-1),
 // then o_t += qt_t^T S_(j-1); the chunk's last sub-chunk writes its final
-// state.
+// state. The matrix products run on v_mfma_f32_16x16x4f32 (lane l: row
+// l % 16 of the left operand and column l % 16 of the right at k = l / 16 of
+// each step of 4; result rows 4 (l / 16) + r): o_intra = P V, U = Kd^T V,
+// and pass 2's qt S; and P's pairs across the sub-chunk's two 16-token
+// halves (t >= 16 > s) as (qh_t e^(c_t - c_16)) . (kh_s e^(c_16 - c_s)),
+// both exponents <= 0. Pairs inside a half keep e^(c_t - c_s) per term.
 template <int HD>
 __global__ __launch_bounds__(256) void k_gla_sub(const float* __restrict__ QKV,
                                                   const float* __restrict__ Z,
@@ -1487,32 +1492,64 @@ __global__ __launch_bounds__(256) void k_gla_sub(const float* __restrict__ QKV,
     g.Qt[(size_t)(s0 + t) * d + h * HD + a] = qh[t][a] * __expf(cl[t][a]);
   }
   if (tid < (uint32_t)HD) g.Dj[((size_t)J * heads + h) * HD + tid] = __expf(cl[n - 1][tid]);
+  static_assert(L == 32 && HD % 16 == 0, "two 16-token halves, 16-wide tiles");
+  const uint32_t lane = tid & 63, wv = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+  // P inside each half, term by term; P across the halves on wave 0
   for (uint32_t e = tid; e < (uint32_t)L * L; e += 256) {
     const uint32_t t = e / L, s = e % L;
+    if (t >= 16 && s < 16) continue;
     float p = 0.0f;
     if (s <= t && t < n)
       for (int a = 0; a < HD; a++) p = fmaf(qh[t][a] * kh[s][a], __expf(cl[t][a] - cl[s][a]), p);
     P[t][s] = p;
   }
+  if (wv == 0) {
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t ti = 16 + r16, si = r16;
+    for (int k0 = 0; k0 < HD; k0 += 4) {
+      const uint32_t a = k0 + g4;
+      const float x = qh[ti][a] * __expf(cl[ti][a] - cl[16][a]);
+      const float y = kh[si][a] * __expf(cl[16][a] - cl[si][a]);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) P[16 + 4 * g4 + r][r16] = 16 + 4 * g4 + r < n ? acc[r] : 0.0f;
+  }
   __syncthreads();
-  // kh_s e^(c_last - c_s) in place (P holds what needed kh), and the intra terms
+  // kh_s e^(c_last - c_s) in place (P holds what needed kh); the intra terms
+  // o = P V, 16 x 16 tiles (t half, column block)
   for (uint32_t e = tid; e < (uint32_t)L * HD; e += 256) {
     const uint32_t t = e / HD, a = e % HD;
     kh[t][a] = t < n ? kh[t][a] * __expf(cl[n - 1][a] - cl[t][a]) : 0.0f;
   }
-  for (uint32_t e = tid; e < n * HD; e += 256) {
-    const uint32_t t = e / HD, b = e % HD;
-    float o = 0.0f;
-    for (uint32_t s = 0; s <= t; s++) o = fmaf(P[t][s], vv[s][b], o);
-    O[(size_t)(s0 + t) * d + h * HD + b] = o;
+  constexpr uint32_t CBS = HD / 16;
+  for (uint32_t tile = wv; tile < 2 * CBS; tile += 4) {
+    const uint32_t tb = tile / CBS, bb = tile % CBS;
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k0 = 0; k0 < L; k0 += 4) {
+      const uint32_t sk = k0 + g4;
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(P[16 * tb + r16][sk], vv[sk][16 * bb + r16], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint32_t t = 16 * tb + 4 * g4 + r;
+      if (t < n) O[(size_t)(s0 + t) * d + h * HD + 16 * bb + r16] = acc[r];
+    }
   }
   __syncthreads();
+  // U = Kd^T V, 16 x 16 tiles (row block of a, column block of b)
   float* U = g.Uj + ((size_t)J * heads + h) * HD * HD;
-  for (uint32_t e = tid; e < (uint32_t)HD * HD; e += 256) {
-    const uint32_t a = e / HD, b = e % HD;
-    float s2 = 0.0f;
-    for (uint32_t s = 0; s < n; s++) s2 = fmaf(kh[s][a], vv[s][b], s2);
-    U[e] = s2;
+  for (uint32_t tile = wv; tile < CBS * CBS; tile += 4) {
+    const uint32_t ab = tile / CBS, bb = tile % CBS;
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k0 = 0; k0 < L; k0 += 4) {
+      const uint32_t sk = k0 + g4;
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kh[sk][16 * ab + r16], vv[sk][16 * bb + r16], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) U[(size_t)(16 * ab + 4 * g4 + r) * HD + 16 * bb + r16] = acc[r];
   }
 }
 
@@ -1524,9 +1561,9 @@ __global__ __launch_bounds__(256) void k_gla_carry(GlaScratch g, StateRef S, flo
   const uint32_t h = blockIdx.x, cb = blockIdx.y, J = blockIdx.z, tid = threadIdx.x, heads = gridDim.x;
   const GlaSub u = tab[J];
   const uint32_t s0 = u.row, n = u.n;
-  for (uint32_t e = tid; e < n * HD; e += 256) {
+  for (uint32_t e = tid; e < (uint32_t)L * HD; e += 256) {
     const uint32_t t = e / HD, a = e % HD;
-    qs[t][a] = g.Qt[(size_t)(s0 + t) * d + h * HD + a];
+    qs[t][a] = t < n ? g.Qt[(size_t)(s0 + t) * d + h * HD + a] : 0.0f;
   }
   // S_(j-1): the chunk's entering state through its earlier sub-chunks
   // (table entries J - j .. J - 1), HD * CB / 256 elements a thread
@@ -1563,12 +1600,20 @@ __global__ __launch_bounds__(256) void k_gla_carry(GlaScratch g, StateRef S, flo
     }
   }
   __syncthreads();
-  for (uint32_t e = tid; e < n * CB; e += 256) {
-    const uint32_t t = e / CB, b = e % CB;
-    float o = 0.0f;
-#pragma unroll 16
-    for (int a = 0; a < HD; a++) o = fmaf(qs[t][a], Sb[a][b], o);
-    O[(size_t)(s0 + t) * d + h * HD + cb * CB + b] += o;
+  // o_t += qt_t^T S_(j-1) on the column block: one 16 x 16 tile per half
+  const uint32_t lane = tid & 63, wv = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+  if (wv < 2) {
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k0 = 0; k0 < HD; k0 += 4) {
+      const uint32_t a = k0 + g4;
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qs[16 * wv + r16][a], Sb[a][r16], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint32_t t = 16 * wv + 4 * g4 + r;
+      if (t < n) O[(size_t)(s0 + t) * d + h * HD + cb * CB + r16] += acc[r];
+    }
   }
 }
 
