@@ -124,6 +124,21 @@ __global__ __launch_bounds__(64) void k_gemv_fast(GemvArgs a) {
       wv[r][j] = WL::load(w, wh, k < K ? k : 0);
     }
   }
+  // the residual this lane's output adds, loaded with the weights (not after
+  // the reduction, which would add a dependent memory round trip)
+  float res = 0.0f;
+  if (a.mode == GM_RESID && lane < (uint32_t)(RW * BT)) {
+    const uint32_t rr = lane / BT, bb = lane % BT;
+    uint32_t rl = 0;
+    bool ok = false;
+#pragma unroll
+    for (int r = 0; r < RW; r++)
+      if ((uint32_t)r == rr) {
+        rl = lr[r];
+        ok = rok[r];
+      }
+    if (ok && bb < nb) res = a.R[(size_t)bb * a.ldr + rl];
+  }
   // M.norm on the lane's slices: ss over the row by a wave sum
 #pragma unroll
   for (int b = 0; b < BT; b++) {
@@ -185,7 +200,7 @@ __global__ __launch_bounds__(64) void k_gemv_fast(GemvArgs a) {
     for (int b = 0; b < BT; b++)
       if (lane == (uint32_t)(r * BT + b) && rok[r] && (uint32_t)b < nb) {
         float y = acc[r][b];
-        if (a.mode == GM_RESID) y = a.R[(size_t)b * a.ldr + lr[r]] + y;
+        if (a.mode == GM_RESID) y = res + y;
         if (sg[r]) a.seg[1].Y[(size_t)b * a.seg[1].ldy + lr[r]] = y;
         else a.seg[0].Y[(size_t)b * a.seg[0].ldy + lr[r]] = y;
       }
