@@ -61,6 +61,15 @@ __global__ __launch_bounds__(256) void k_gemv_small(GemvArgs a, uint32_t R, uint
   float4* Xf = reinterpret_cast<float4*>(rs + 4);         // [BT][K/4] when ng
 
   const Segs sgs(a);
+  // the residual a chain lane's output adds, loaded now rather than after
+  // the chain (which would add a dependent memory round trip at the end)
+  float res = 0.0f;
+  if (a.mode == GM_RESID && tid < Lc) {
+    const uint32_t b = tid / R, r = tid - b * R;
+    const float* wp;
+    uint32_t sg, lr;
+    if (b < nb && sgs.row(R, blockIdx.x, r, &wp, &sg, &lr)) res = a.R[(size_t)(b0 + b) * a.ldr + lr];
+  }
   float4 w[16];
   // weights of the chunk at q0 into w[]; item i = tid + 256 j is (row r, float4 q4)
   auto load_w = [&](uint32_t q0) {
@@ -160,7 +169,12 @@ __global__ __launch_bounds__(256) void k_gemv_small(GemvArgs a, uint32_t R, uint
   if (tid < Lc && b < nb) {
     const float* wp;
     uint32_t sg, lr;
-    if (sgs.row(R, blockIdx.x, r, &wp, &sg, &lr)) gemv_store(a, sg, lr, b0 + b, s);
+    if (sgs.row(R, blockIdx.x, r, &wp, &sg, &lr)) {
+      // plain or plus the residual (add2 of bend/Dense/Model.bend:44-45)
+      const float y = a.mode == GM_RESID ? res + s : s;
+      if (sg) a.seg[1].Y[(size_t)(b0 + b) * a.seg[1].ldy + lr] = y;
+      else a.seg[0].Y[(size_t)(b0 + b) * a.seg[0].ldy + lr] = y;
+    }
   }
   if (a.amax && tid < 64) {
     // the workgroup's best key per batch row, then one atomic each
