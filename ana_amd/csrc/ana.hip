@@ -371,7 +371,8 @@ static const ana_ctx::PkEnt* find_pk(const ana_ctx* c, const GemvArgs& g) {
 
 static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool chunk = false) {
   const bool small = g0.B <= kSmallB;
-  const ana_ctx::PkEnt* pe = fast_mode(c) && !small && g0.B < 128 && gemm_pk_fits(g0) ? find_pk(c, g0) : nullptr;
+  const bool pk_ok = gemm_pk_fits(g0) || (kind == ANA_K_HEAD && head_pw_fits(g0));
+  const ana_ctx::PkEnt* pe = fast_mode(c) && !small && g0.B < 128 && pk_ok ? find_pk(c, g0) : nullptr;
   if (pe || (fast_mode(c) && (small ? !chunk : (chunk || kind != ANA_K_HEAD)))) {
     GemvArgs g = g0;
     if (c->Wh) {
@@ -620,12 +621,31 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
 // head on B rows of src: final RMSNorm, then the tied embedding. With
 // `greedy`, small batches also leave dd.pick's argmax keys in d_amax (the
 // caller cleared them), larger ones dd.top's picks in d_pick.
-static int run_head(ana_ctx* c, const float* src, uint32_t B, bool greedy) {
+// the head's product over B rows of src (final norm, tied embedding)
+static GemvArgs head_args(const ana_ctx* c, const float* src, uint32_t B) {
   const ana_config& cf = c->cfg;
   GemvArgs h = gemv1(src, cf.d, cf.d, c->W, cf.vocab, c->LG, cf.vocab, B);
-  if (greedy && B <= kSmallB) h.amax = c->d_amax;
+  h.ng = c->W + c->fin;
+  return h;
+}
+
+// Greedy picks from the head's argmax keys (dd.pick's order, no pass over
+// the stored logits): small batches, and the fast modes' wide head over
+// packed weights (5..127 rows); else k_top over the logits.
+static bool head_keys(const ana_ctx* c, const float* src, uint32_t B) {
+  if (B <= kSmallB) return true;
+  if (!fast_mode(c) || B >= 128) return false;
+  GemvArgs h = head_args(c, src, B);
+  h.amax = c->d_amax;
+  return head_pw_fits(h) && find_pk(c, h) != nullptr;
+}
+
+static int run_head(ana_ctx* c, const float* src, uint32_t B, bool greedy) {
+  GemvArgs h = head_args(c, src, B);
+  const bool keys = greedy && head_keys(c, src, B);
+  if (keys) h.amax = c->d_amax;
   if (int r = norm_gemv(c, src, c->W + c->fin, h, ANA_K_HEAD)) return r;
-  if (greedy && B > kSmallB) HIPCHK(c, launch_top(c->LG, cf.vocab, B, c->d_pick, c->st));
+  if (greedy && !keys) HIPCHK(c, launch_top(c->LG, c->cfg.vocab, B, c->d_pick, c->st));
   return ANA_OK;
 }
 
@@ -817,7 +837,7 @@ extern "C" int ana_top(ana_ctx* c, uint32_t n, const uint32_t* seq, uint32_t* to
   if (int r = head_of(c, "ana_top", n, seq)) return r;
   HIPCHK(c, launch_zero_u64(c->d_amax, (uint32_t)(n * kAmaxPerRow), c->st));
   if (int r = run_head(c, c->X, n, true)) return r;
-  if (n <= kSmallB) HIPCHK(c, launch_keys_to_tok(c->d_amax, c->cfg.vocab, n, c->d_pick, c->st));
+  if (head_keys(c, c->X, n)) HIPCHK(c, launch_keys_to_tok(c->d_amax, c->cfg.vocab, n, c->d_pick, c->st));
   HIPCHK(c, hipMemcpyAsync(tok, c->d_pick, 4 * n, hipMemcpyDeviceToHost, c->st));
   HIPCHK(c, hipStreamSynchronize(c->st));
   return ANA_OK;
@@ -868,7 +888,7 @@ static int gen_step(ana_ctx* c, uint32_t n, uint32_t steps, const PickArgs& pa, 
   ad.vocab = c->cfg.vocab;
   ad.B = n;
   ad.steps = steps;
-  ad.amax = greedy && n <= kSmallB ? c->d_amax : nullptr;
+  ad.amax = greedy && head_keys(c, c->X, n) ? c->d_amax : nullptr;
   ad.pick = c->d_pick;
   ad.greedy = greedy;
   ad.pos = c->d_pos;

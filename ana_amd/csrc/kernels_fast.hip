@@ -1189,7 +1189,9 @@ __global__ __launch_bounds__(256) void k_gemm_pw(GemvArgs a, const uint4* __rest
 
 // Wide products over packed weights at 5..127 rows (the LM head): a
 // workgroup of NW waves owns 32 batch rows and TPW consecutive 16-row weight
-// tiles. The 32 rows' x go to LDS once (global_load_lds_dwordx4, a row's
+// tiles (with `amax` also the rows' greedy argmax keys: per tile the best of
+// its 16 columns, one atomicMax into the row's slot t % kAmaxSlots). The 32
+// rows' x go to LDS once (global_load_lds_dwordx4, a row's
 // 16-byte units at unit ^ (row & 7)); with `ng` the waves then share the
 // rows for their norm scales. Wave w takes tiles w, w + NW, .. of the TPW,
 // each over the whole K, its (tile, 32-k step) pieces as one stream in
@@ -1306,6 +1308,16 @@ __global__ __launch_bounds__(64 * NW) void k_head_pw(GemvArgs a, const uint4* __
             if (sg) a.seg[1].Y[(size_t)m * a.seg[1].ldy + lr] = y;
             else a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = y;
           }
+          if (a.amax) {
+            // the row's best key over the tile's 16 columns, one atomic
+            unsigned long long key = nok && m < a.B && sg == 0 ? argmax_key(y, lr) : 0ull;
+#pragma unroll
+            for (int sh = 1; sh < 16; sh <<= 1) {
+              const unsigned long long o = __shfl_xor(key, sh, 64);
+              key = o > key ? o : key;
+            }
+            if (r16 == 0 && key) atomicMax(&a.amax[amax_at(m, t % kAmaxSlots)], key);
+          }
         }
         acc[tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
       }
@@ -1314,7 +1326,7 @@ __global__ __launch_bounds__(64 * NW) void k_head_pw(GemvArgs a, const uint4* __
 }
 
 bool head_pw_fits(const GemvArgs& a) {
-  return !a.amax && a.mode == GM_PLAIN && a.B > 0 && a.K % 256 == 0 && a.K <= kHeadMaxK && (a.ldx & 3) == 0 &&
+  return a.mode == GM_PLAIN && a.B > 0 && a.K % 256 == 0 && a.K <= kHeadMaxK && (a.ldx & 3) == 0 &&
          (reinterpret_cast<uintptr_t>(a.X) & 15) == 0;
 }
 

@@ -335,3 +335,31 @@ def test_fast_decode_batch_products(oracle, small_ckpt, mid_ckpt, mode, model):
                     worst = max(worst, rel_err(got[i], sts[i].logits()))
     print(f"worst relative error {worst:.3e}", flush=True)
     assert worst <= TOL[mode], worst
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_fast_greedy_batch_keys(mid_ckpt, mode):
+    """Greedy picks of more than four sequences in a fast mode come from the
+    head's argmax keys (no pass over the stored logits): ana_generate's
+    tokens equal the first index of the max of the logits a twin decoder
+    reads after feeding the same tokens, and ana_top equals that argmax."""
+    print(f"case fast greedy batch keys mode {mode}", flush=True)
+    n, steps = 7, 6
+    rng = np.random.default_rng(31)
+    with ana_amd.Decoder(mid_ckpt, max_seqs=n, numerics=mode) as dec, \
+            ana_amd.Decoder(mid_ckpt, max_seqs=n, numerics=mode) as twin:
+        v = dec.vocab
+        prompts = [rng.integers(2, v, size=3 + i).astype(np.uint32) for i in range(n)]
+        for d in (dec, twin):
+            d.feeds_n(list(range(n)), [0] * n, [p[:-1] for p in prompts])
+        pos = np.array([len(p) - 1 for p in prompts], dtype=np.uint32)
+        tok = np.array([p[-1] for p in prompts], dtype=np.uint32)
+        got = dec.generate(list(range(n)), pos, tok, steps)
+        t, p = tok.copy(), pos.copy()
+        for k in range(steps):
+            twin.feed(list(range(n)), p, t)
+            lg = twin.logits(list(range(n)))
+            want = lg.argmax(axis=1).astype(np.uint32)
+            assert np.array_equal(twin.top(list(range(n))), want), k
+            assert np.array_equal(got[:, k], want), (k, got[:, k], want)
+            t, p = want, p + 1
