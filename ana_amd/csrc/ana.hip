@@ -573,6 +573,8 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
         if (fast_path(c, B)) {
           a.part = c->d_part;
           HIPCHK(c, launch_attn_fast(a, c->st));
+        } else if (fast_mode(c) && cf.ctx <= kAttnRowsMaxCtx) {
+          HIPCHK(c, launch_attn_rows(a, c->st));
         } else {
           HIPCHK(c, launch_attn(a, c->st));
         }

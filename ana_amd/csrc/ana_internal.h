@@ -243,6 +243,11 @@ hipError_t launch_gla_fast(const float* QKV, const float* Z, const float* lam, S
                            const uint32_t* seq, float* O, uint32_t d, uint32_t heads,
                            uint32_t rglru, uint32_t B, hipStream_t st);
 hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st);
+// Decode attention of more than kSmallB rows in the fast modes (hd 16, 32
+// or 64, ctx <= kAttnRowsMaxCtx: the scores stay in LDS): one workgroup per
+// (head, row)
+constexpr uint32_t kAttnRowsMaxCtx = 8192;
+hipError_t launch_attn_rows(const AttnArgs& a, hipStream_t st);
 // GLA over the prefill chunks of one step as a chunked scan: kGlaSub-token
 // sub-chunks in parallel, then their states carried across. The table holds
 // one entry per sub-chunk, those of one chunk consecutive.

@@ -622,6 +622,166 @@ hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Decode attention of more than kSmallB rows in the fast modes: one
+// workgroup per (head, row) over the row's live slots 0 .. npos. The row's
+// k (qk-normed when on) and v go to its slot first; its own slot's score
+// and product take them from LDS. A slot is L = HD / 4 lanes (a float4 of
+// its K or V row each, so a slot's row is one 16 L-byte piece), the
+// workgroup G = 256 / L slot groups, and a trip U slots a group, the next
+// trip's loads in flight while one computes. Pass 1 keeps sc*s in LDS
+// (ctx floats, dynamic); the max (with the sink) and the denominator come
+// from wave and block reductions; pass 2 sums e*V per lane over its slots
+// for its four columns, and the G slot groups meet in LDS.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
+  constexpr int L = HD / 4, G = 256 / L, U = 4;
+  extern __shared__ float ss[];   // [ctx]
+  __shared__ __align__(16) float q[HD];
+  __shared__ __align__(16) float kk[HD];
+  __shared__ __align__(16) float vs[HD];
+  __shared__ float red[4], red2[4], nrm[2];
+  __shared__ float4 op[G][L];
+  const uint32_t h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t d = a.d, ctx = a.ctx;
+  const uint32_t pos = a.pos[b];
+  const uint32_t slot = pos % ctx, npos = pos < ctx - 1 ? pos : ctx - 1;
+  float* Kr = a.KV.base + (size_t)a.seq[b] * a.KV.seq_stride + a.KV.layer_off;
+  float* Vr = Kr + (size_t)ctx * d;
+  const float* x = a.QKV + (size_t)b * 3 * d;
+  if (tid < HD) {
+    q[tid] = x[h * HD + tid];
+    kk[tid] = x[d + h * HD + tid];
+    vs[tid] = x[2 * d + h * HD + tid];
+  }
+  __syncthreads();
+  if (a.gq) {
+    // M.qkn (bend/Dense/Model.bend:39-42) on q (wave 0) and k (wave 1)
+    if (wv < 2) {
+      const float v = lane < (uint32_t)HD ? (wv == 0 ? q[lane] : kk[lane]) : 0.0f;
+      const float t = wave_sum(v * v);
+      if (lane == 0) nrm[wv] = 1.0f / sqrtf(t / (float)HD + 1.0e-5f);
+    }
+    __syncthreads();
+    if (tid < HD) {
+      q[tid] = (q[tid] * nrm[0]) * (1.0f + a.gq[tid]);
+      kk[tid] = (kk[tid] * nrm[1]) * (1.0f + a.gk[tid]);
+    }
+    __syncthreads();
+  }
+  if (tid < HD) {
+    Kr[(size_t)slot * d + h * HD + tid] = kk[tid];
+    Vr[(size_t)slot * d + h * HD + tid] = vs[tid];
+  }
+  const uint32_t li = tid % L, g = tid / L;
+  const float4 q4 = *reinterpret_cast<const float4*>(&q[4 * li]);
+  float4 k4o = *reinterpret_cast<const float4*>(&kk[4 * li]);
+  float4 v4o = *reinterpret_cast<const float4*>(&vs[4 * li]);
+  // opaque register values from here: a select between them and a ring load
+  // must stay a select (as a select of two loads it becomes one flat load
+  // through a stack copy)
+  asm volatile("" : "+v"(k4o.x), "+v"(k4o.y), "+v"(k4o.z), "+v"(k4o.w));
+  asm volatile("" : "+v"(v4o.x), "+v"(v4o.y), "+v"(v4o.z), "+v"(v4o.w));
+  const float sc = 1.0f / sqrtf((float)HD);
+  // one trip's pieces of ring `base` (own slot from `own`), index clamped
+  auto load = [&](const float* base, float4 own, uint32_t t0, float4* r) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const uint32_t t = t0 + g + u * G;
+      const float4 v = *reinterpret_cast<const float4*>(base + (size_t)(t <= npos ? t : 0) * d);
+      r[u] = t == slot ? own : v;
+    }
+  };
+  const float* kb = Kr + h * HD + 4 * li;
+  const float* vb = Vr + h * HD + 4 * li;
+  float4 cur[U], nxt[U];
+  load(kb, k4o, 0, cur);
+  for (uint32_t t0 = 0; t0 <= npos; t0 += U * G) {
+    const bool more = t0 + U * G <= npos;
+    if (more) load(kb, k4o, t0 + U * G, nxt);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const uint32_t t = t0 + g + u * G;
+      float sdot = (q4.x * cur[u].x + q4.y * cur[u].y) + (q4.z * cur[u].z + q4.w * cur[u].w);
+#pragma unroll
+      for (int mk = 1; mk < L; mk <<= 1) sdot += __shfl_xor(sdot, mk, 64);
+      if (li == 0 && t <= npos) ss[t] = sc * sdot;
+    }
+    if (more) {
+#pragma unroll
+      for (int u = 0; u < U; u++) cur[u] = nxt[u];
+    }
+  }
+  // the first V trip flies through the reductions
+  load(vb, v4o, 0, cur);
+  __syncthreads();
+  float r = -INFINITY;
+  for (uint32_t t = tid; t <= npos; t += 256) r = fmaxf(r, ss[t]);
+#pragma unroll
+  for (int mk = 32; mk >= 1; mk >>= 1) r = fmaxf(r, __shfl_xor(r, mk, 64));
+  if (lane == 0) red[wv] = r;
+  __syncthreads();
+  float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float sink = a.sink ? a.sink[h] : 0.0f;
+  if (a.sink) mx = fmaxf(mx, sink);
+  float se = 0.0f;
+  for (uint32_t t = tid; t <= npos; t += 256) {
+    const float e = expf(ss[t] - mx);
+    ss[t] = e;
+    se += e;
+  }
+  se = wave_sum(se);
+  if (lane == 0) red2[wv] = se;
+  __syncthreads();
+  float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (uint32_t t0 = 0; t0 <= npos; t0 += U * G) {
+    const bool more = t0 + U * G <= npos;
+    if (more) load(vb, v4o, t0 + U * G, nxt);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const uint32_t t = t0 + g + u * G;
+      const float e = t <= npos ? ss[t] : 0.0f;
+      o.x = fmaf(e, cur[u].x, o.x);
+      o.y = fmaf(e, cur[u].y, o.y);
+      o.z = fmaf(e, cur[u].z, o.z);
+      o.w = fmaf(e, cur[u].w, o.w);
+    }
+    if (more) {
+#pragma unroll
+      for (int u = 0; u < U; u++) cur[u] = nxt[u];
+    }
+  }
+  op[g][li] = o;
+  __syncthreads();
+  if (tid < HD) {
+    const uint32_t c = tid / 4, e = tid % 4;
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int j = 0; j < G; j++) {
+      const float4 p4 = op[j][c];
+      acc += e == 0 ? p4.x : e == 1 ? p4.y : e == 2 ? p4.z : p4.w;
+    }
+    float den = ((red2[0] + red2[1]) + red2[2]) + red2[3];
+    if (a.sink) den += expf(sink - mx);
+    a.O[(size_t)b * d + h * HD + tid] = acc / den;
+  }
+}
+
+hipError_t launch_attn_rows(const AttnArgs& a, hipStream_t st) {
+  const uint32_t hd = a.heads ? a.d / a.heads : 0;
+  if (!a.seq || !a.pos || !a.write_kv || a.ctx == 0 || a.ctx > kAttnRowsMaxCtx || hd * a.heads != a.d)
+    return hipErrorInvalidValue;
+  const size_t lds = (size_t)a.ctx * 4;
+#define L_(H) hipLaunchKernelGGL(k_attn_rows<H>, dim3(a.heads, a.B), dim3(256), lds, st, a)
+  switch (hd) {
+    case 64: L_(64); break;
+    case 32: L_(32); break;
+    case 16: L_(16); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef L_
+  return hipGetLastError();
+}
+
 size_t attn_fast_part_floats(uint32_t B, uint32_t heads, uint32_t ctx, uint32_t hd) {
   return (size_t)B * heads * ((ctx + kFastTS - 1) / kFastTS) * (hd + 2);
 }
@@ -1356,9 +1516,13 @@ bool gemm_pk_fits(const GemvArgs& a) {
 // two tiles' weights)
 constexpr uint32_t kPwTwoTileMin = 1024, kPwTwoTileMax = 4096;
 
+// The register ring holds D steps: three for K <= 1024, four above (a sweep
+// at B = 16 and 64 with the weights evicted between launches: one step
+// ahead starves the loads; six or eight ahead, every load issued at once,
+// cost 0.3-1.1 us more a product than three)
 template <int NS>
 static hipError_t pw_go(const GemvArgs& a, const uint4* p, int bf, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
-  constexpr int D = NS < 8 ? NS : 8;
+  constexpr int D = NS < 3 ? NS : NS <= 8 ? 3 : 4;
   const uint32_t tiles = pk_tiles(a), mt = (a.B + 15) / 16;
   if constexpr (NS <= 8) {
     if (tiles * mt >= kPwTwoTileMin && tiles * mt <= kPwTwoTileMax) {
