@@ -2161,14 +2161,15 @@ __device__ __forceinline__ void xcd_tile(uint32_t* nt, uint32_t* mt) {
 // A given as split head and remainder (k_split): a 128 x 128 tile per
 // workgroup, four waves of 64 x 64 (4 x 4 v_mfma_f32_16x16x32_bf16 tiles,
 // head then remainder each step). K goes in stages of 32 through a ring of
-// three LDS stages filled by global_load_lds_dwordx4 (no registers between
+// NS LDS stages filled by global_load_lds_dwordx4 (no registers between
 // global memory and LDS): each stage holds the head, remainder and weight
 // tiles as 1 KB chunks of 16 rows, a row's four 16-byte k pieces at
 // physical slot (piece ^ ((row >> 1) & 3)), so a fragment read touches
 // eight distinct 16-byte bank groups. A wave waits on its own loads of the
 // stage it is about to read, then a barrier (no fence, which would wait on
 // every load in flight) makes the other waves' loads visible; loads of the
-// stage two ahead go out right after it. Norm scale, residual and SiLU as in
+// stage NS - 1 ahead go out right after it (the barrier also says every wave
+// is done with the stage they overwrite). Norm scale, residual and SiLU as in
 // k_gemm_big.
 template <int NS>
 __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __restrict__ Ahg,
@@ -2327,7 +2328,9 @@ hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, __bf16* Al, float* rsc,
   const uint32_t per = a.mode == GM_SILU ? 64 : 128;
   const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
   dim3 grid(tiles, (a.B + 127) / 128);
-  hipLaunchKernelGGL(k_gemm_dl<3>, grid, dim3(256), 0, st, a, Ah, Al, rsc);
+  // two LDS stages (48 KB, three workgroups a CU) ran 5-12% faster than three
+  // (72 KB, two a CU) at the 8192-row prefill shapes with random operands
+  hipLaunchKernelGGL(k_gemm_dl<2>, grid, dim3(256), 0, st, a, Ah, Al, rsc);
   if (e1) (void)hipEventRecord(e1, st);
   return hipGetLastError();
 }
