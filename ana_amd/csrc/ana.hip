@@ -259,7 +259,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = dalloc(&c->X, (uint64_t)c->rows * d)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->XA, (uint64_t)c->rows * d)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->XN, (uint64_t)c->rows * d)) != hipSuccess) return bad(e);
-  if ((e = dalloc(&c->d_step, 2)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->d_step, wb)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_amax, wb * kAmaxPerRow)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_ss, wb * cf.heads * cf.ctx)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_pm, wb * cf.heads * ((cf.ctx + kAttnTS - 1) / kAttnTS))) != hipSuccess) return bad(e);
@@ -928,7 +928,7 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
   HIPCHK(c, hipMemcpyAsync(c->d_pos, pos, 4 * n, hipMemcpyHostToDevice, c->st));
   HIPCHK(c, hipMemcpyAsync(c->d_tok, tok, 4 * n, hipMemcpyHostToDevice, c->st));
   if (!greedy) HIPCHK(c, hipMemcpyAsync(c->d_rng, rng, 32 * n, hipMemcpyHostToDevice, c->st));
-  HIPCHK(c, launch_zero_u32(c->d_step, 2, c->st));
+  HIPCHK(c, launch_zero_u32(c->d_step, n, c->st));
   const PickArgs pa = pick_args(c, n, greedy ? nullptr : s, 1);
   // capture `count` steps into a graph
   auto capture = [&](uint32_t count, hipGraphExec_t* ex) -> int {

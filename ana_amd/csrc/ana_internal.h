@@ -212,9 +212,9 @@ hipError_t launch_scatter_rows(const float* src, const uint32_t* idx, uint32_t n
 // The token loop's step end for B sequences: the pick (from the sampler's
 // pick[b], or greedy: the amax key or top[b] of dd.pick, falling back to
 // Sample.argmax over the logits when there is none), recorded at
-// out[b * steps + *step], fed next (tok = pick, pos + 1); then *step + 1.
-// The step index lives in device memory, so one captured step serves every
-// iteration.
+// out[b * steps + step[b]], fed next (tok = pick, pos + 1); then step[b] + 1.
+// The step indices (one a row) live in device memory, so one captured step
+// serves every iteration.
 struct AdvanceArgs {
   const float* logits;              // [B][vocab]
   uint32_t vocab, B, steps;
@@ -224,7 +224,7 @@ struct AdvanceArgs {
   uint32_t* pos;
   uint32_t* tok;
   uint32_t* out;
-  uint32_t* step;
+  uint32_t* step;                   // [B]
   uint32_t* last;                   // [B]: the pick, for ana_top-like readers
 };
 hipError_t launch_advance(const AdvanceArgs& a, hipStream_t st);

@@ -308,24 +308,35 @@ __global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t
   }
 }
 
-// the token loop's step end (see AdvanceArgs); step[1] counts the
-// workgroups done, so the last one moves the step index on
+// the token loop's step end (see AdvanceArgs): row b's pick (from the
+// head's argmax keys, wave 0 reading a slot a lane; from the stored logits
+// when no key reaches the max, a NaN row), recorded at out[b][step[b]];
+// every row keeps its own step count, so no row waits on another
 template <int LPT>
 __global__ __launch_bounds__(1024) void k_advance(AdvanceArgs a, uint32_t NT) {
   __shared__ float red[16];
   __shared__ uint32_t redi[16];
+  __shared__ uint32_t cand_s;
   const uint32_t b = blockIdx.x, tid = threadIdx.x, v = a.vocab;
-  const uint32_t k = a.step[0];
   uint32_t t;
   if (a.greedy) {
-    uint32_t cand;
-    if (a.amax) {
-      unsigned long long key = 0;
-      for (uint32_t s = 0; s < kAmaxSlots; s++) key = a.amax[amax_at(b, s)] > key ? a.amax[amax_at(b, s)] : key;
-      cand = key ? 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull) : v;
-    } else {
-      cand = a.pick[b];
+    if (tid < 64) {
+      uint32_t cand;
+      if (a.amax) {
+        unsigned long long key = tid < kAmaxSlots ? a.amax[amax_at(b, tid)] : 0ull;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+          const unsigned long long o = __shfl_xor(key, m, 64);
+          key = o > key ? o : key;
+        }
+        cand = key ? 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull) : v;
+      } else {
+        cand = a.pick[b];
+      }
+      if (tid == 0) cand_s = cand;
     }
+    __syncthreads();
+    const uint32_t cand = cand_s;
     if (cand < v) {
       t = cand;
     } else {
@@ -341,15 +352,12 @@ __global__ __launch_bounds__(1024) void k_advance(AdvanceArgs a, uint32_t NT) {
     t = a.pick[b];
   }
   if (tid == 0) {
+    const uint32_t k = a.step[b];
     a.out[(size_t)b * a.steps + k] = t;
     a.tok[b] = t;
     a.pos[b] = a.pos[b] + 1;
     if (a.last) a.last[b] = t;
-    __threadfence();
-    if (atomicAdd(&a.step[1], 1u) == a.B - 1) {
-      a.step[1] = 0;
-      a.step[0] = k + 1;
-    }
+    a.step[b] = k + 1;
   }
 }
 
