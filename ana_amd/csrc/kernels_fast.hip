@@ -1244,6 +1244,28 @@ __global__ __launch_bounds__(256) void k_gemm_pw(GemvArgs a, const uint4* __rest
   uint32_t xo[2];
 #pragma unroll
   for (int h = 0; h < 2; h++) xo[h] = min(m0 + 8 * h + dr, a.B - 1) * a.ldx + wv * (K / 4) + 4 * sl;
+  // wave 0's residuals (its epilogue's) first: they depend on nothing, and
+  // loaded after its stores each would wait on the one before
+  float res[NT][4];
+#pragma unroll
+  for (int j = 0; j < NT; j++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) res[j][r] = 0.0f;
+  if (a.mode == GM_RESID && wv == 0) {
+    const Segs sg0(a);
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+      const uint32_t t = NT * blockIdx.x + j;
+      const float* w_;
+      uint32_t sg, lr;
+      const bool ok = t < tiles && sg0.row(16, t, r16, &w_, &sg, &lr);
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t m = m0 + 4 * g4 + r;
+        if (ok && m < a.B) res[j][r] = a.R[(size_t)m * a.ldr + lr];
+      }
+    }
+  }
   uint4 wr[D][NT][WP];
   auto issue = [&](auto S) {
     constexpr int s = decltype(S)::value;
@@ -1339,7 +1361,7 @@ __global__ __launch_bounds__(256) void k_gemm_pw(GemvArgs a, const uint4* __rest
         const float up = __shfl_xor(y, 8, 64);
         if (r16 < 8 && nok && m < a.B) a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = fast_silu(y) * up;
       } else if (nok && m < a.B) {
-        if (a.mode == GM_RESID) y = a.R[(size_t)m * a.ldr + lr] + y;
+        if (a.mode == GM_RESID) y = res[j][r] + y;
         if (sg) a.seg[1].Y[(size_t)m * a.seg[1].ldy + lr] = y;
         else a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = y;
       }
@@ -2070,12 +2092,23 @@ __global__ __launch_bounds__(256) void k_gemm_big(GemvArgs a) {
     }
     return;
   }
+  // per column block: its residuals loaded together before any store (a
+  // load after a store through another pointer would wait on it, one round
+  // trip per element)
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const uint32_t n = wn * 64 + 16 * j + r16;
     const float* w_;
     uint32_t sg, lr;
     if (!sgs.row(BN, blockIdx.x, n, &w_, &sg, &lr)) continue;
+    float res[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r;
+        res[i][r] = a.mode == GM_RESID && m < nb ? a.R[(size_t)(m0 + m) * a.ldr + lr] : 0.0f;
+      }
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -2084,7 +2117,7 @@ __global__ __launch_bounds__(256) void k_gemm_big(GemvArgs a) {
         if (m >= nb) continue;
         float y = acc[i][j][r];
         if (norm) y *= rsc[m];
-        if (a.mode == GM_RESID) y = a.R[(size_t)(m0 + m) * a.ldr + lr] + y;
+        if (a.mode == GM_RESID) y = res[i][r] + y;
         if (sg) a.seg[1].Y[(size_t)(m0 + m) * a.seg[1].ldy + lr] = y;
         else a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = y;
       }
@@ -2178,6 +2211,7 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
   constexpr int BM = 128, BN = 128, BK = 32;
   constexpr int TILE = BM * BK;   // bf16 elements of one operand tile (8 KB)
   __shared__ __align__(1024) __bf16 lds[NS][3][TILE];
+  __shared__ float rsl[BM];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint32_t wm = wv >> 1, wn = wv & 1;
   uint32_t ntile, mtile;
@@ -2251,7 +2285,14 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
   }
   const bool norm = a.ng != nullptr;
   // results: tile (i, j) of the wave holds rows wm*64 + 16i + 4*g4 + r,
-  // column wn*64 + 16j + r16
+  // column wn*64 + 16j + r16. The tile's row norm scales go to LDS before
+  // any store (a global load after a store through another pointer would
+  // wait on it, one round trip per element)
+  if (norm) {
+    if (tid < (uint32_t)BM) rsl[tid] = rscg[m0 + (tid < nb ? tid : 0)];
+    __syncthreads();
+  }
+  auto rs = [&](int i, int r) { return norm ? rsl[wm * 64 + 16 * i + 4 * g4 + r] : 1.0f; };
   if (a.mode == GM_SILU) {
     // up columns (wn = 1) through LDS to the gate columns (wn = 0), one
     // 64-row half at a time
@@ -2266,10 +2307,8 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
           for (int j = 0; j < 4; j++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-              const uint32_t ml = 16 * i + 4 * g4 + r, n = 16 * j + r16, m = wm * 64 + ml;
-              float y = acc[i][j][r];
-              if (norm) y *= rscg[m0 + (m < nb ? m : 0)];
-              up[ml * 64 + n] = y;
+              const uint32_t ml = 16 * i + 4 * g4 + r, n = 16 * j + r16;
+              up[ml * 64 + n] = acc[i][j][r] * rs(i, r);
             }
       }
       __syncthreads();
@@ -2286,8 +2325,7 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
             for (int r = 0; r < 4; r++) {
               const uint32_t ml = 16 * i + 4 * g4 + r, m = wm * 64 + ml;
               if (m >= nb) continue;
-              float y = acc[i][j][r];
-              if (norm) y *= rscg[m0 + m];
+              const float y = acc[i][j][r] * rs(i, r);
               a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = fast_silu(y) * up[ml * 64 + n];
             }
         }
@@ -2298,19 +2336,30 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
   }
 #pragma unroll
   for (int j = 0; j < 4; j++) {
+    // one column block's residuals live at a time: the compiler barrier
+    // keeps the next block's loads below this one's stores
+    asm volatile("" ::: "memory");
     const uint32_t n = wn * 64 + 16 * j + r16;
     const float* w_;
     uint32_t sg, lr;
     if (!sgs.row(BN, ntile, n, &w_, &sg, &lr)) continue;
+    // the column block's residuals together, before its stores
+    float res[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r;
+        res[i][r] = a.mode == GM_RESID && m < nb ? a.R[(size_t)(m0 + m) * a.ldr + lr] : 0.0f;
+      }
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r;
         if (m >= nb) continue;
-        float y = acc[i][j][r];
-        if (norm) y *= rscg[m0 + m];
-        if (a.mode == GM_RESID) y = a.R[(size_t)(m0 + m) * a.ldr + lr] + y;
+        float y = acc[i][j][r] * rs(i, r);
+        if (a.mode == GM_RESID) y = res[i][r] + y;
         if (sg) a.seg[1].Y[(size_t)(m0 + m) * a.seg[1].ldy + lr] = y;
         else a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = y;
       }
@@ -2328,8 +2377,9 @@ hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, __bf16* Al, float* rsc,
   const uint32_t per = a.mode == GM_SILU ? 64 : 128;
   const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
   dim3 grid(tiles, (a.B + 127) / 128);
-  // two LDS stages (48 KB, three workgroups a CU) ran 5-12% faster than three
-  // (72 KB, two a CU) at the 8192-row prefill shapes with random operands
+  // two LDS stages (48 KB) ran 5-12% faster than three (72 KB) at the
+  // 8192-row prefill shapes with random operands (two workgroups a CU
+  // either way, by registers)
   hipLaunchKernelGGL(k_gemm_dl<2>, grid, dim3(256), 0, st, a, Ah, Al, rsc);
   if (e1) (void)hipEventRecord(e1, st);
   return hipGetLastError();
