@@ -373,7 +373,9 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
   const bool small = g0.B <= kSmallB;
   const bool pk_ok = gemm_pk_fits(g0) || (kind == ANA_K_HEAD && head_pw_fits(g0));
   const ana_ctx::PkEnt* pe = fast_mode(c) && !small && g0.B < 128 && pk_ok ? find_pk(c, g0) : nullptr;
-  if (pe || (fast_mode(c) && (small ? !chunk : (chunk || kind != ANA_K_HEAD)))) {
+  // the head of a decode step of 128 rows or more takes the prefill products
+  // too (greedy picks then read the stored logits)
+  if (pe || (fast_mode(c) && (small ? !chunk : (chunk || kind != ANA_K_HEAD || g0.B >= 128)))) {
     GemvArgs g = g0;
     if (c->Wh) {
       g.Wh0 = c->Wh + (g.seg[0].W - c->W);

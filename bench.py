@@ -109,6 +109,41 @@ def run_batch(path: str, c: cf.Config, B: int, prompt: int, warmup: int, steps: 
     }
 
 
+def run_configs(path: str, c) -> dict:
+    """BASELINE's other decode configs on the same checkpoint (ctx 2048):
+    "next" (B=32, 1920-token prompts, 128 greedy steps, fast_fp32, past the
+    ring's wrap at the end), "v3" (B=64, 128-token prompts, 128 sampled steps
+    at T 0.8 / top-k 40 / top-p 0.9, seed b per sequence, fast_fp32) and
+    "bf16" (B=256, 512-token prompts, 256 greedy steps, bf16)."""
+    out = {}
+    for key, B, prompt, steps, mode, sampled in (("cfg_next", 32, 1920, 128, "fast_fp32", False),
+                                                 ("cfg_v3", 64, 128, 128, "fast_fp32", True),
+                                                 ("cfg_bf16", 256, 512, 256, "bf16", False)):
+        seqs = list(range(B))
+        with ana_amd.Decoder(path, max_seqs=B, prefill_chunk=128, numerics=MODES[mode]) as dec:
+            prs = [ckpt.prompt(5000 + b, prompt, c.vocab) for b in seqs]
+            t = time.perf_counter()
+            dec.feeds_n(seqs, [0] * B, [pr[:-1] for pr in prs])
+            t_pre = time.perf_counter() - t
+            tok = np.array([int(pr[-1]) for pr in prs], dtype=np.uint32)
+            pos = np.full(B, prompt - 1, dtype=np.uint32)
+            st = ana_amd.Settings(float(np.float32(0.8)), 40, float(np.float32(0.9))) if sampled else None
+            rng = np.ascontiguousarray(np.stack([ana_amd.rng_seeded(b) for b in seqs])) if sampled else None
+            tok = dec.generate(seqs, pos, tok, 2, st, rng)[:, -1].copy()   # graph capture, untimed
+            t0 = time.perf_counter()
+            dec.generate(seqs, pos + 2, tok, steps, st, rng)
+            dt = time.perf_counter() - t0
+        positions = [int(prompt - 1 + 2 + k) for k in range(steps) for _ in seqs]
+        sb = run_bytes(c, positions, steps, 2.0 if mode == "bf16" else 4.0) / steps
+        out[key] = {"tok_s": round(B * steps / dt, 1), "ms_per_step": round(1000.0 * dt / steps, 4),
+                    "step_gbs": round(sb * steps / dt / 1e9, 2), "prefill_tok_s": round(B * (prompt - 1) / t_pre, 1),
+                    "workload": f"B={B}, {prompt}-token prompts (ana_feeds_n, chunk 128), {steps} "
+                                f"{'sampled (T 0.8, top-k 40, top-p 0.9)' if sampled else 'greedy'} steps; "
+                                + NUMERICS[mode]}
+        log(f"{key}: {out[key]['tok_s']} tok/s, prefill {out[key]['prefill_tok_s']} tok/s")
+    return out
+
+
 def cpu_baseline(path: str, c: cf.Config, seconds: float) -> dict:
     """The oracle's dense decode on the host cores, bounded to ~`seconds`."""
     from oracle import oracle as O
@@ -248,6 +283,7 @@ def main() -> int:
     ap.add_argument("--prefill-only", type=int, default=0,
                     help="measure only the B=64 x 512 prefill and print its figures (1/0)")
     ap.add_argument("--agent", type=int, default=1, help="also measure 64 agent episodes (1/0)")
+    ap.add_argument("--configs", type=int, default=1, help="also measure BASELINE's next, v3 and bf16 decode configs (1/0)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--ckpt", default=os.environ.get("ANA_BENCH_CKPT", "/tmp/ana_bench_fp100m.ftc2"))
     a = ap.parse_args()
@@ -293,6 +329,8 @@ def main() -> int:
         extra.update(run_prefill(path, c))
     if a.agent:
         extra["agent"] = run_agent(path, c, mode)
+    if a.configs:
+        extra.update(run_configs(path, c))
     cpu = cpu_baseline(path, c, a.cpu_seconds) if a.cpu_seconds > 0 else None
     kern = {k: {"launches": v[0], "ms": round(v[1], 4), "gb": round(v[2] / 1e9, 4)}
             for k, v in r1["stats"].items()}
