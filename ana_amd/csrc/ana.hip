@@ -77,15 +77,18 @@ struct ana_ctx {
   // one step, and kGraphSteps steps back to back (a graph launch costs tens
   // of microseconds on the host side, so several steps share one)
   hipGraphExec_t gexec = nullptr, gexec_n = nullptr;
+  // what the captured steps depend on (not the step count: each row's
+  // picks go to the step-major d_out at its own step counter)
   struct GKey {
-    uint32_t n, steps;
+    uint32_t n;
     float temp, topp;
     uint32_t topk;
     const uint32_t* out;
     bool operator==(const GKey& o) const {
-      return n == o.n && steps == o.steps && temp == o.temp && topp == o.topp && topk == o.topk && out == o.out;
+      return n == o.n && temp == o.temp && topp == o.topp && topk == o.topk && out == o.out;
     }
   } gkey{};
+  std::vector<uint32_t> h_out;       // step-major picks of the last ana_generate
   // kernel timing (ana_prof)
   bool prof = false;
   double attn_bytes = 0.0;           // per softmax-layer launch of the current step
@@ -97,6 +100,8 @@ struct ana_ctx {
 };
 
 static const uint32_t kGraphSteps = 8;
+// steps of every row d_out holds at least (more when a call asks)
+static const uint32_t kOutSteps = 1024;
 
 static const size_t kProfMax = 16384;
 
@@ -879,7 +884,7 @@ extern "C" int ana_pick(ana_ctx* c, uint32_t n, const uint32_t* seq, const ana_s
 
 // one decode step of the token loop: embed the current tokens, every
 // layer, the head, the pick, then advance (pos + 1, tok = pick, record)
-static int gen_step(ana_ctx* c, uint32_t n, uint32_t steps, const PickArgs& pa, bool greedy) {
+static int gen_step(ana_ctx* c, uint32_t n, const PickArgs& pa, bool greedy) {
   HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, n, c->X, c->d_amax, c->st));
   if (int r = run_layers(c, n, c->d_seq, c->d_pos, nullptr)) return r;
   if (int r = run_head(c, c->X, n, greedy)) return r;
@@ -891,7 +896,6 @@ static int gen_step(ana_ctx* c, uint32_t n, uint32_t steps, const PickArgs& pa, 
   ad.logits = c->LG;
   ad.vocab = c->cfg.vocab;
   ad.B = n;
-  ad.steps = steps;
   ad.amax = greedy && head_keys(c, c->X, n) ? c->d_amax : nullptr;
   ad.pick = c->d_pick;
   ad.greedy = greedy;
@@ -918,13 +922,16 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
   HIPCHK(c, hipSetDevice(c->device));
   const size_t need = (size_t)n * steps;
   if (need > c->out_cap) {
+    // room for kOutSteps steps of every row at once, so calls of other
+    // step counts replay the same graphs
     if (c->gexec) { HIPCHK(c, hipGraphExecDestroy(c->gexec)); c->gexec = nullptr; }
     if (c->gexec_n) { HIPCHK(c, hipGraphExecDestroy(c->gexec_n)); c->gexec_n = nullptr; }
     if (c->d_out) HIPCHK(c, hipFree(c->d_out));
     c->d_out = nullptr;
     c->out_cap = 0;
-    HIPCHK(c, dalloc(&c->d_out, need));
-    c->out_cap = need;
+    const size_t cap = std::max(need, (size_t)c->wb * kOutSteps);
+    HIPCHK(c, dalloc(&c->d_out, cap));
+    c->out_cap = cap;
   }
   HIPCHK(c, hipMemcpyAsync(c->d_seq, seq, 4 * n, hipMemcpyHostToDevice, c->st));
   HIPCHK(c, hipMemcpyAsync(c->d_pos, pos, 4 * n, hipMemcpyHostToDevice, c->st));
@@ -937,7 +944,7 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
     hipGraph_t g = nullptr;
     HIPCHK(c, hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
     int r = 0;
-    for (uint32_t i = 0; i < count && !r; i++) r = gen_step(c, n, steps, pa, greedy);
+    for (uint32_t i = 0; i < count && !r; i++) r = gen_step(c, n, pa, greedy);
     const hipError_t ec = hipStreamEndCapture(c->st, &g);
     if (r) { if (g) (void)hipGraphDestroy(g); return r; }
     HIPCHK(c, ec);
@@ -950,10 +957,10 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
     // launch by launch, each product timed by its own start/stop events
     for (uint32_t k = 0; k < steps; k++) {
       c->attn_bytes = attn_bytes_of(c, pos, n, k);
-      if (int r = gen_step(c, n, steps, pa, greedy)) return r;
+      if (int r = gen_step(c, n, pa, greedy)) return r;
     }
   } else {
-    ana_ctx::GKey key{n, steps, pa.temp, pa.topp, pa.topk, c->d_out};
+    ana_ctx::GKey key{n, pa.temp, pa.topp, pa.topk, c->d_out};
     if (!c->gexec || !(c->gkey == key)) {
       if (c->gexec) { HIPCHK(c, hipGraphExecDestroy(c->gexec)); c->gexec = nullptr; }
       if (c->gexec_n) { HIPCHK(c, hipGraphExecDestroy(c->gexec_n)); c->gexec_n = nullptr; }
@@ -969,9 +976,13 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
     for (; k < steps; k++) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
   }
   HIPCHK(c, launch_scatter_rows(c->X, c->d_seq, n, c->cfg.d, c->xs, c->st));
-  HIPCHK(c, hipMemcpyAsync(out, c->d_out, 4 * need, hipMemcpyDeviceToHost, c->st));
+  c->h_out.resize(need);
+  HIPCHK(c, hipMemcpyAsync(c->h_out.data(), c->d_out, 4 * need, hipMemcpyDeviceToHost, c->st));
   if (!greedy) HIPCHK(c, hipMemcpyAsync(rng, c->d_rng, 32 * n, hipMemcpyDeviceToHost, c->st));
   HIPCHK(c, hipStreamSynchronize(c->st));
+  // step-major on the device, row-major for the caller
+  for (uint32_t k = 0; k < steps; k++)
+    for (uint32_t b = 0; b < n; b++) out[(size_t)b * steps + k] = c->h_out[(size_t)k * n + b];
   return ANA_OK;
 }
 

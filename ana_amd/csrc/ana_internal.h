@@ -212,12 +212,13 @@ hipError_t launch_scatter_rows(const float* src, const uint32_t* idx, uint32_t n
 // The token loop's step end for B sequences: the pick (from the sampler's
 // pick[b], or greedy: the amax key or top[b] of dd.pick, falling back to
 // Sample.argmax over the logits when there is none), recorded at
-// out[b * steps + step[b]], fed next (tok = pick, pos + 1); then step[b] + 1.
+// out[step[b] * B + b] (step-major), fed next (tok = pick, pos + 1); then
+// step[b] + 1.
 // The step indices (one a row) live in device memory, so one captured step
 // serves every iteration.
 struct AdvanceArgs {
   const float* logits;              // [B][vocab]
-  uint32_t vocab, B, steps;
+  uint32_t vocab, B;
   const unsigned long long* amax;   // greedy, keys (or nullptr)
   const uint32_t* pick;             // sampled picks, or greedy dd.pick results
   uint32_t greedy;

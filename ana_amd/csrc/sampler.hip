@@ -75,13 +75,19 @@ __device__ float tree_up(float v, Op op, float* red, uint32_t tid, uint32_t NT) 
     __syncthreads();
     return r;
   }
-  const uint32_t nw = NT >> 6;
+  const uint32_t nw = NT >> 6;   // a power of two, at most 16
   if (lane == 0 && (tid >> 6) < nw) red[tid >> 6] = v;
   __syncthreads();
+  // the wave partials' tree, unrolled over the 16 possible leaves (a
+  // runtime-bounded loop would keep w in scratch memory)
   float w[16];
-  for (uint32_t i = 0; i < nw; i++) w[i] = red[i];
-  for (uint32_t s = 1; s < nw; s *= 2)
-    for (uint32_t i = 0; i < nw; i += 2 * s) w[i] = op(w[i], w[i + s]);
+#pragma unroll
+  for (uint32_t i = 0; i < 16; i++) w[i] = i < nw ? red[i] : 0.0f;
+#pragma unroll
+  for (uint32_t s = 1; s < 16; s *= 2)
+#pragma unroll
+    for (uint32_t i = 0; i < 16; i += 2 * s)
+      if (i + s < nw) w[i] = op(w[i], w[i + s]);
   __syncthreads();
   return w[0];
 }
@@ -353,7 +359,7 @@ __global__ __launch_bounds__(1024) void k_advance(AdvanceArgs a, uint32_t NT) {
   }
   if (tid == 0) {
     const uint32_t k = a.step[b];
-    a.out[(size_t)b * a.steps + k] = t;
+    a.out[(size_t)k * a.B + b] = t;
     a.tok[b] = t;
     a.pos[b] = a.pos[b] + 1;
     if (a.last) a.last[b] = t;
