@@ -363,6 +363,10 @@ static double gemv_bytes(const GemvArgs& g) {
 // until its cause is found.
 static bool fast_mode(const ana_ctx* c) { return c->mode != ANA_EXACT_FP32; }
 static bool fast_path(const ana_ctx* c, uint32_t B) { return fast_mode(c) && B <= kSmallB; }
+// decode steps below this many rows take the products over packed weights
+// (the prefill products' 128-row tiles would leave most CUs idle: at 256
+// rows gate|up is 64 workgroups)
+static const uint32_t kPwMaxB = 1024;
 
 // the packed weights of product g, when they were packed for its shape and gains
 static const ana_ctx::PkEnt* find_pk(const ana_ctx* c, const GemvArgs& g) {
@@ -377,10 +381,11 @@ static const ana_ctx::PkEnt* find_pk(const ana_ctx* c, const GemvArgs& g) {
 static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool chunk = false) {
   const bool small = g0.B <= kSmallB;
   const bool pk_ok = gemm_pk_fits(g0) || (kind == ANA_K_HEAD && head_pw_fits(g0));
-  const ana_ctx::PkEnt* pe = fast_mode(c) && !small && g0.B < 128 && pk_ok ? find_pk(c, g0) : nullptr;
-  // the head of a decode step of 128 rows or more takes the prefill products
-  // too (greedy picks then read the stored logits)
-  if (pe || (fast_mode(c) && (small ? !chunk : (chunk || kind != ANA_K_HEAD || g0.B >= 128)))) {
+  const ana_ctx::PkEnt* pe =
+      fast_mode(c) && !small && g0.B < (chunk ? 128u : kPwMaxB) && pk_ok ? find_pk(c, g0) : nullptr;
+  // the head of a decode step of kPwMaxB rows or more takes the prefill
+  // products too (greedy picks then read the stored logits)
+  if (pe || (fast_mode(c) && (small ? !chunk : (chunk || kind != ANA_K_HEAD || g0.B >= kPwMaxB)))) {
     GemvArgs g = g0;
     if (c->Wh) {
       g.Wh0 = c->Wh + (g.seg[0].W - c->W);
@@ -640,10 +645,10 @@ static GemvArgs head_args(const ana_ctx* c, const float* src, uint32_t B) {
 
 // Greedy picks from the head's argmax keys (dd.pick's order, no pass over
 // the stored logits): small batches, and the fast modes' wide head over
-// packed weights (5..127 rows); else k_top over the logits.
+// packed weights (5 .. kPwMaxB - 1 rows); else k_top over the logits.
 static bool head_keys(const ana_ctx* c, const float* src, uint32_t B) {
   if (B <= kSmallB) return true;
-  if (!fast_mode(c) || B >= 128) return false;
+  if (!fast_mode(c) || B >= kPwMaxB) return false;
   GemvArgs h = head_args(c, src, B);
   h.amax = c->d_amax;
   return head_pw_fits(h) && find_pk(c, h) != nullptr;

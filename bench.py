@@ -20,6 +20,7 @@ decoder; the reference's Bend toolchain is absent) on a bounded sample.
 from __future__ import annotations
 
 import argparse
+import subprocess
 import json
 import os
 import sys
@@ -284,12 +285,13 @@ def main() -> int:
                     help="measure only the B=64 x 512 prefill and print its figures (1/0)")
     ap.add_argument("--agent", type=int, default=1, help="also measure 64 agent episodes (1/0)")
     ap.add_argument("--configs", type=int, default=1, help="also measure BASELINE's next, v3 and bf16 decode configs (1/0)")
+    ap.add_argument("--configs-only", type=int, default=0, help="print only those configs' JSON (the child run)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--ckpt", default=os.environ.get("ANA_BENCH_CKPT", "/tmp/ana_bench_fp100m.ftc2"))
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py: this build measures one GPU only; the decode path shards by sequence "
-              "with no collective (see DESIGN.md), so run --gpus 1.", file=sys.stderr)
+              "with no collective, so run --gpus 1.", file=sys.stderr)
         return 2
     c = cf.FP100M
     path = ensure_ckpt(c, a.ckpt)
@@ -297,6 +299,23 @@ def main() -> int:
     if a.prefill_only:
         print(json.dumps(run_prefill(path, c)), flush=True)
         return 0
+    if a.configs_only:
+        print(json.dumps(run_configs(path, c)), flush=True)
+        return 0
+    cfg_lines = {}
+    if a.configs:
+        # first, in a child process of its own (before this one touches the
+        # GPU), so a failure there costs only these lines
+        cmd = [sys.executable, os.path.abspath(__file__), "--configs-only", "1", "--ckpt", path]
+        try:
+            pr = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=600)   # its progress on stderr
+            lines = [ln for ln in pr.stdout.splitlines() if ln.startswith("{")]
+            if pr.returncode == 0 and lines:
+                cfg_lines = json.loads(lines[-1])
+            else:
+                cfg_lines = {"configs_error": f"child exited {pr.returncode}"}
+        except subprocess.TimeoutExpired:
+            cfg_lines = {"configs_error": "child timed out"}
     r1 = run_batch(path, c, 1, a.prompt, a.warmup, a.steps, min(a.steps, 32), mode)
     g = r1["stats"]["gemv"]
     h = r1["stats"]["head"]
@@ -329,8 +348,7 @@ def main() -> int:
         extra.update(run_prefill(path, c))
     if a.agent:
         extra["agent"] = run_agent(path, c, mode)
-    if a.configs:
-        extra.update(run_configs(path, c))
+    extra.update(cfg_lines)
     cpu = cpu_baseline(path, c, a.cpu_seconds) if a.cpu_seconds > 0 else None
     kern = {k: {"launches": v[0], "ms": round(v[1], 4), "gb": round(v[2] / 1e9, 4)}
             for k, v in r1["stats"].items()}

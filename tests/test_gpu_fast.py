@@ -363,3 +363,49 @@ def test_fast_greedy_batch_keys(mid_ckpt, mode):
             assert np.array_equal(twin.top(list(range(n))), want), k
             assert np.array_equal(got[:, k], want), (k, got[:, k], want)
             t, p = want, p + 1
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_fast_decode_wide_batch(oracle, mid_ckpt, mode):
+    """Decode steps of 160 sequences (above the prefill products' 128-row
+    tiles, still on the packed products, the wide head and its greedy keys):
+    ragged starts, six steps; five sequences' logits against their own oracle
+    runs, and the greedy picks of a generate step are the argmax of a twin
+    decoder's logits."""
+    print(f"case fast decode wide batch mode {mode}", flush=True)
+    m = oracle.Model(mid_ckpt)
+    n, steps = 160, 6
+    rng = np.random.default_rng(29)
+    starts = [1 + i % 5 for i in range(n)]
+    toks = rng.integers(2, m.vocab, size=(n, 16)).astype(np.uint32)
+    watch = [0, 37, 81, 128, 159]
+    sts = {i: oracle.State(m) for i in watch}
+    seqs = list(range(n))
+    worst = 0.0
+    with ana_amd.Decoder(mid_ckpt, max_seqs=n, prefill_chunk=8, numerics=mode) as dec, \
+            ana_amd.Decoder(mid_ckpt, max_seqs=n, prefill_chunk=8, numerics=mode) as twin:
+        for d_ in (dec, twin):
+            d_.feeds_n(seqs, [0] * n, [toks[i, : starts[i]] for i in range(n)])
+        for i in watch:
+            for p in range(starts[i]):
+                sts[i].feed(p, int(toks[i, p]))
+        for k in range(steps):
+            pos = [starts[i] + k for i in range(n)]
+            tk = [int(toks[i, pos[i]]) for i in range(n)]
+            dec.feed(seqs, pos, tk)
+            twin.feed(seqs, pos, tk)
+            for i in watch:
+                sts[i].feed(pos[i], tk[i])
+        got = dec.logits(seqs)
+        for i in watch:
+            worst = max(worst, rel_err(got[i], sts[i].logits()))
+        # one greedy step at the next position against the twin's argmax
+        nxt = [starts[i] + steps for i in range(n)]
+        tn = [int(toks[i, nxt[i]]) for i in range(n)]
+        picks = dec.generate(seqs, nxt, tn, 1)[:, 0]
+        twin.feed(seqs, nxt, tn)
+        lg = twin.logits(seqs)
+        want = np.argmax(lg, axis=1)
+        assert np.array_equal(picks, want.astype(np.uint32)), np.nonzero(picks != want)[0][:8]
+    print(f"worst relative error {worst:.3e}", flush=True)
+    assert worst <= TOL[mode], worst
