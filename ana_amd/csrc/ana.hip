@@ -84,10 +84,14 @@ struct ana_ctx {
     float temp, topp;
     uint32_t topk;
     const uint32_t* out;
+    bool split;
     bool operator==(const GKey& o) const {
-      return n == o.n && temp == o.temp && topp == o.topp && topk == o.topk && out == o.out;
+      return n == o.n && temp == o.temp && topp == o.topp && topk == o.topk && out == o.out && split == o.split;
     }
   } gkey{};
+  // decode steps above kSmallB rows split each row's attention over
+  // kRowsSplit-slot pieces (set per call from the rows' positions)
+  bool attn_split = false;
   std::vector<uint32_t> h_out;       // step-major picks of the last ana_generate
   // kernel timing (ana_prof)
   bool prof = false;
@@ -363,6 +367,15 @@ static double gemv_bytes(const GemvArgs& g) {
 // until its cause is found.
 static bool fast_mode(const ana_ctx* c) { return c->mode != ANA_EXACT_FP32; }
 static bool fast_path(const ana_ctx* c, uint32_t B) { return fast_mode(c) && B <= kSmallB; }
+// a decode call's attention above kSmallB rows goes in kRowsSplit-slot
+// pieces once some row reaches 2 kRowsSplit live slots (one workgroup a row
+// would stream the whole window alone: at B = 32 and 1930 slots, 96 us a
+// layer for 379 MB)
+static bool split_attention(const ana_ctx* c, uint32_t n, const uint32_t* pos, uint32_t steps) {
+  uint64_t top = 0;
+  for (uint32_t i = 0; i < n; i++) top = std::max<uint64_t>(top, (uint64_t)pos[i] + steps);
+  return n > kSmallB && top >= 2ull * kRowsSplit;
+}
 // decode steps below this many rows take the products over packed weights
 // (the prefill products' 128-row tiles would leave most CUs idle: at 256
 // rows gate|up is 64 workgroups)
@@ -585,8 +598,9 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
         if (fast_path(c, B)) {
           a.part = c->d_part;
           HIPCHK(c, launch_attn_fast(a, c->st));
-        } else if (fast_mode(c) && cf.ctx <= kAttnRowsMaxCtx) {
-          HIPCHK(c, launch_attn_rows(a, c->st));
+        } else if (fast_mode(c)) {
+          a.part = c->d_part;
+          HIPCHK(c, launch_attn_rows(a, c->attn_split || cf.ctx > kAttnRowsMaxCtx, c->st));
         } else {
           HIPCHK(c, launch_attn(a, c->st));
         }
@@ -699,6 +713,7 @@ extern "C" int ana_feed(ana_ctx* c, uint32_t n, const uint32_t* seq, const uint3
   HIPCHK(c, hipMemcpyAsync(c->d_tok, tok, 4 * n, hipMemcpyHostToDevice, c->st));
   HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, n, c->X, nullptr, c->st));
   if (c->prof) c->attn_bytes = attn_bytes_of(c, pos, n, 0);
+  c->attn_split = split_attention(c, n, pos, 1);
   if (int r = run_layers(c, n, c->d_seq, c->d_pos, nullptr)) return r;
   HIPCHK(c, launch_scatter_rows(c->X, c->d_seq, n, c->cfg.d, c->xs, c->st));
   HIPCHK(c, hipStreamSynchronize(c->st));
@@ -943,6 +958,7 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
   HIPCHK(c, hipMemcpyAsync(c->d_tok, tok, 4 * n, hipMemcpyHostToDevice, c->st));
   if (!greedy) HIPCHK(c, hipMemcpyAsync(c->d_rng, rng, 32 * n, hipMemcpyHostToDevice, c->st));
   HIPCHK(c, launch_zero_u32(c->d_step, n, c->st));
+  c->attn_split = split_attention(c, n, pos, steps);
   const PickArgs pa = pick_args(c, n, greedy ? nullptr : s, 1);
   // capture `count` steps into a graph
   auto capture = [&](uint32_t count, hipGraphExec_t* ex) -> int {
@@ -965,7 +981,7 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
       if (int r = gen_step(c, n, pa, greedy)) return r;
     }
   } else {
-    ana_ctx::GKey key{n, pa.temp, pa.topp, pa.topk, c->d_out};
+    ana_ctx::GKey key{n, pa.temp, pa.topp, pa.topk, c->d_out, c->attn_split};
     if (!c->gexec || !(c->gkey == key)) {
       if (c->gexec) { HIPCHK(c, hipGraphExecDestroy(c->gexec)); c->gexec = nullptr; }
       if (c->gexec_n) { HIPCHK(c, hipGraphExecDestroy(c->gexec_n)); c->gexec_n = nullptr; }

@@ -245,10 +245,12 @@ hipError_t launch_gla_fast(const float* QKV, const float* Z, const float* lam, S
                            uint32_t rglru, uint32_t B, hipStream_t st);
 hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st);
 // Decode attention of more than kSmallB rows in the fast modes (hd 16, 32
-// or 64, ctx <= kAttnRowsMaxCtx: the scores stay in LDS): one workgroup per
-// (head, row)
-constexpr uint32_t kAttnRowsMaxCtx = 8192;
-hipError_t launch_attn_rows(const AttnArgs& a, hipStream_t st);
+// or 64): one workgroup per (head, row) over every live slot (ctx <=
+// kAttnRowsMaxCtx: the scores stay in LDS), or with `split` one per (head,
+// row, kRowsSplit slots) and a combine (a.part holds the partials: rows x
+// heads x ctx / kRowsSplit x (hd + 2) floats)
+constexpr uint32_t kAttnRowsMaxCtx = 8192, kRowsSplit = 256;
+hipError_t launch_attn_rows(const AttnArgs& a, bool split, hipStream_t st);
 // GLA over the prefill chunks of one step as a chunked scan: kGlaSub-token
 // sub-chunks in parallel, then their states carried across. The table holds
 // one entry per sub-chunk, those of one chunk consecutive.

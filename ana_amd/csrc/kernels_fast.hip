@@ -631,11 +631,14 @@ hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st) {
 // trip's loads in flight while one computes. Pass 1 keeps sc*s in LDS
 // (ctx floats, dynamic); the max (with the sink) and the denominator come
 // from wave and block reductions; pass 2 sums e*V per lane over its slots
-// for its four columns, and the G slot groups meet in LDS.
+// for its four columns, and the G slot groups meet in LDS. With a split
+// grid (gridDim.z > 1) workgroup z takes slots z SL .. z SL + SL - 1 of the
+// live ones (SL = kRowsSplit), and leaves its max m, its sum l = sum e and
+// its o = sum e V (e = exp(sc s - m), no sink) in part for k_attn_rows_comb.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
   constexpr int L = HD / 4, G = 256 / L, U = 4;
-  extern __shared__ float ss[];   // [ctx]
+  extern __shared__ float ss[];   // [ctx] or [kRowsSplit]
   __shared__ __align__(16) float q[HD];
   __shared__ __align__(16) float kk[HD];
   __shared__ __align__(16) float vs[HD];
@@ -645,6 +648,19 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
   const uint32_t d = a.d, ctx = a.ctx;
   const uint32_t pos = a.pos[b];
   const uint32_t slot = pos % ctx, npos = pos < ctx - 1 ? pos : ctx - 1;
+  const uint32_t nsp = gridDim.z, sp = blockIdx.z;
+  const uint32_t s0 = nsp > 1 ? sp * kRowsSplit : 0u;
+  const uint32_t s1 = nsp > 1 ? min(npos + 1, s0 + kRowsSplit) : npos + 1;   // slots s0 .. s1 - 1
+  float* part = nsp > 1 ? a.part + (((size_t)b * a.heads + h) * nsp + sp) * (HD + 2) : nullptr;
+  if (s0 >= s1) {
+    // no live slot in this split
+    if (tid < HD) part[2 + tid] = 0.0f;
+    if (tid == 0) {
+      part[0] = -INFINITY;
+      part[1] = 0.0f;
+    }
+    return;
+  }
   float* Kr = a.KV.base + (size_t)a.seq[b] * a.KV.seq_stride + a.KV.layer_off;
   float* Vr = Kr + (size_t)ctx * d;
   const float* x = a.QKV + (size_t)b * 3 * d;
@@ -668,7 +684,7 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
     }
     __syncthreads();
   }
-  if (tid < HD) {
+  if (tid < HD && slot >= s0 && slot < s1) {
     Kr[(size_t)slot * d + h * HD + tid] = kk[tid];
     Vr[(size_t)slot * d + h * HD + tid] = vs[tid];
   }
@@ -687,16 +703,16 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const uint32_t t = t0 + g + u * G;
-      const float4 v = *reinterpret_cast<const float4*>(base + (size_t)(t <= npos ? t : 0) * d);
+      const float4 v = *reinterpret_cast<const float4*>(base + (size_t)(t < s1 ? t : s0) * d);
       r[u] = t == slot ? own : v;
     }
   };
   const float* kb = Kr + h * HD + 4 * li;
   const float* vb = Vr + h * HD + 4 * li;
   float4 cur[U], nxt[U];
-  load(kb, k4o, 0, cur);
-  for (uint32_t t0 = 0; t0 <= npos; t0 += U * G) {
-    const bool more = t0 + U * G <= npos;
+  load(kb, k4o, s0, cur);
+  for (uint32_t t0 = s0; t0 < s1; t0 += U * G) {
+    const bool more = t0 + U * G < s1;
     if (more) load(kb, k4o, t0 + U * G, nxt);
 #pragma unroll
     for (int u = 0; u < U; u++) {
@@ -704,7 +720,7 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
       float sdot = (q4.x * cur[u].x + q4.y * cur[u].y) + (q4.z * cur[u].z + q4.w * cur[u].w);
 #pragma unroll
       for (int mk = 1; mk < L; mk <<= 1) sdot += __shfl_xor(sdot, mk, 64);
-      if (li == 0 && t <= npos) ss[t] = sc * sdot;
+      if (li == 0 && t < s1) ss[t - s0] = sc * sdot;
     }
     if (more) {
 #pragma unroll
@@ -712,19 +728,20 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
     }
   }
   // the first V trip flies through the reductions
-  load(vb, v4o, 0, cur);
+  load(vb, v4o, s0, cur);
   __syncthreads();
+  const uint32_t ns = s1 - s0;
   float r = -INFINITY;
-  for (uint32_t t = tid; t <= npos; t += 256) r = fmaxf(r, ss[t]);
+  for (uint32_t t = tid; t < ns; t += 256) r = fmaxf(r, ss[t]);
 #pragma unroll
   for (int mk = 32; mk >= 1; mk >>= 1) r = fmaxf(r, __shfl_xor(r, mk, 64));
   if (lane == 0) red[wv] = r;
   __syncthreads();
   float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float sink = a.sink ? a.sink[h] : 0.0f;
-  if (a.sink) mx = fmaxf(mx, sink);
+  if (a.sink && nsp == 1) mx = fmaxf(mx, sink);
   float se = 0.0f;
-  for (uint32_t t = tid; t <= npos; t += 256) {
+  for (uint32_t t = tid; t < ns; t += 256) {
     const float e = expf(ss[t] - mx);
     ss[t] = e;
     se += e;
@@ -733,13 +750,13 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
   if (lane == 0) red2[wv] = se;
   __syncthreads();
   float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  for (uint32_t t0 = 0; t0 <= npos; t0 += U * G) {
-    const bool more = t0 + U * G <= npos;
+  for (uint32_t t0 = s0; t0 < s1; t0 += U * G) {
+    const bool more = t0 + U * G < s1;
     if (more) load(vb, v4o, t0 + U * G, nxt);
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const uint32_t t = t0 + g + u * G;
-      const float e = t <= npos ? ss[t] : 0.0f;
+      const float e = t < s1 ? ss[t - s0] : 0.0f;
       o.x = fmaf(e, cur[u].x, o.x);
       o.y = fmaf(e, cur[u].y, o.y);
       o.z = fmaf(e, cur[u].z, o.z);
@@ -761,17 +778,49 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
       acc += e == 0 ? p4.x : e == 1 ? p4.y : e == 2 ? p4.z : p4.w;
     }
     float den = ((red2[0] + red2[1]) + red2[2]) + red2[3];
+    if (nsp > 1) {
+      part[2 + tid] = acc;
+      if (tid == 0) {
+        part[0] = mx;
+        part[1] = den;
+      }
+      return;
+    }
     if (a.sink) den += expf(sink - mx);
     a.O[(size_t)b * d + h * HD + tid] = acc / den;
   }
 }
 
-hipError_t launch_attn_rows(const AttnArgs& a, hipStream_t st) {
+// the splits of k_attn_rows for one (head, row), with the sink:
+// M = max(m_i, sink), den = sum l_i e^(m_i - M) + e^(sink - M),
+// o = sum o_i e^(m_i - M) / den
+template <int HD>
+__global__ __launch_bounds__(64) void k_attn_rows_comb(AttnArgs a, uint32_t nsp) {
+  const uint32_t h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const float* part = a.part + ((size_t)b * a.heads + h) * nsp * (HD + 2);
+  if (tid >= (uint32_t)HD) return;
+  float M = a.sink ? a.sink[h] : -INFINITY;
+  for (uint32_t i = 0; i < nsp; i++) M = fmaxf(M, part[i * (HD + 2)]);
+  float den = a.sink ? expf(a.sink[h] - M) : 0.0f, acc = 0.0f;
+  for (uint32_t i = 0; i < nsp; i++) {
+    const float* p = part + i * (HD + 2);
+    const float w = expf(p[0] - M);
+    den = fmaf(p[1], w, den);
+    acc = fmaf(p[2 + tid], w, acc);
+  }
+  a.O[(size_t)b * a.d + h * HD + tid] = acc / den;
+}
+
+hipError_t launch_attn_rows(const AttnArgs& a, bool split, hipStream_t st) {
   const uint32_t hd = a.heads ? a.d / a.heads : 0;
-  if (!a.seq || !a.pos || !a.write_kv || a.ctx == 0 || a.ctx > kAttnRowsMaxCtx || hd * a.heads != a.d)
-    return hipErrorInvalidValue;
-  const size_t lds = (size_t)a.ctx * 4;
-#define L_(H) hipLaunchKernelGGL(k_attn_rows<H>, dim3(a.heads, a.B), dim3(256), lds, st, a)
+  if (!a.seq || !a.pos || !a.write_kv || a.ctx == 0 || hd * a.heads != a.d) return hipErrorInvalidValue;
+  if (!split && a.ctx > kAttnRowsMaxCtx) return hipErrorInvalidValue;
+  if (split && !a.part) return hipErrorInvalidValue;
+  const uint32_t nsp = split ? (a.ctx + kRowsSplit - 1) / kRowsSplit : 1u;
+  const size_t lds = (size_t)(split ? kRowsSplit : a.ctx) * 4;
+#define L_(H)                                                                                       \
+  hipLaunchKernelGGL(k_attn_rows<H>, dim3(a.heads, a.B, nsp), dim3(256), lds, st, a);              \
+  if (split) hipLaunchKernelGGL(k_attn_rows_comb<H>, dim3(a.heads, a.B), dim3(64), 0, st, a, nsp)
   switch (hd) {
     case 64: L_(64); break;
     case 32: L_(32); break;

@@ -409,3 +409,42 @@ def test_fast_decode_wide_batch(oracle, mid_ckpt, mode):
         assert np.array_equal(picks, want.astype(np.uint32)), np.nonzero(picks != want)[0][:8]
     print(f"worst relative error {worst:.3e}", flush=True)
     assert worst <= TOL[mode], worst
+
+
+LONG = cf.Config(vocab=258, ctx=1024, d=256, f=1024, layers=4, heads=4, rglru=True, qk=True, sinks=True, tied=True)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_fast_decode_long_split(oracle, tmp_path, mode):
+    """Decode steps of 6 sequences at 600+ live slots (ctx 1024): the fast
+    attention above four rows takes the window in 256-slot pieces and a
+    combine. Ragged prompts through ana_feeds_n, then teacher-forced steps
+    through ana_feed; three sequences' logits against their own oracle runs
+    after every step."""
+    print(f"case fast decode long split mode {mode}", flush=True)
+    p = str(tmp_path / "long.ftc2")
+    ckpt.write(p, LONG, ckpt.init_params(LONG, "normal", 11))
+    m = oracle.Model(p)
+    n, steps = 6, 4
+    rng = np.random.default_rng(31)
+    starts = [600 + 13 * i for i in range(n)]
+    toks = rng.integers(2, m.vocab, size=(n, max(starts) + steps + 1)).astype(np.uint32)
+    watch = [0, 3, 5]
+    sts = {i: oracle.State(m) for i in watch}
+    for i in watch:
+        for q in range(starts[i]):
+            sts[i].feed(q, int(toks[i, q]))
+    seqs = list(range(n))
+    worst = 0.0
+    with ana_amd.Decoder(p, max_seqs=n, prefill_chunk=64, numerics=mode) as dec:
+        dec.feeds_n(seqs, [0] * n, [toks[i, : starts[i]] for i in range(n)])
+        for k in range(steps):
+            pos = [starts[i] + k for i in range(n)]
+            tk = [int(toks[i, pos[i]]) for i in range(n)]
+            dec.feed(seqs, pos, tk)
+            got = dec.logits(seqs)
+            for i in watch:
+                sts[i].feed(pos[i], tk[i])
+                worst = max(worst, rel_err(got[i], sts[i].logits()))
+    print(f"worst relative error {worst:.3e}", flush=True)
+    assert worst <= TOL[mode], worst
