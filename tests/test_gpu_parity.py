@@ -419,3 +419,40 @@ def test_text_end_to_end(oracle, tmp_path):
     assert [int(x) for x in got] == want
     out = t.decode(got)
     assert isinstance(out, bytes)
+
+
+@pytest.mark.parametrize("sampled", [False, True], ids=["greedy", "v3"])
+@pytest.mark.parametrize("mode", [ana_amd.EXACT_FP32, ana_amd.FAST_FP32], ids=["exact", "fast_fp32"])
+def test_generate_calls_of_any_length(ckpts, sampled, mode):
+    """ana_generate replays its captured steps across calls of other step
+    counts (the picks are step-major on the device, each row's step count
+    its own): calls of 5, 9, 1 and 11 steps, each from where the last
+    stopped with the RNG state handed back, give the tokens of one 26-step
+    call on a twin decoder, bit for bit, greedy and sampled; so do 7 and 6
+    rows (a capture per row count)."""
+    print(f"case generate calls of any length mode {mode} sampled {sampled}", flush=True)
+    path = ckpts["v3-arms"]
+    lens = [5, 9, 1, 11]
+    total = sum(lens)
+    st = ana_amd.Settings(float(np.float32(0.8)), 40, float(np.float32(0.9))) if sampled else None
+    for n in (7, 6):
+        seqs = list(range(n))
+        rng0 = np.stack([ana_amd.rng_seeded(50 + s) for s in seqs]).astype(np.uint64) if sampled else None
+        prompts = [VEC["window"][3 * i: 3 * i + 4 + i] for i in seqs]
+        outs = []
+        for split in (True, False):
+            with ana_amd.Decoder(path, max_seqs=n, prefill_chunk=4, numerics=mode) as dec:
+                for i, pr in enumerate(prompts):
+                    dec.feeds(i, 0, pr[:-1])
+                pos = np.array([len(pr) - 1 for pr in prompts], dtype=np.uint32)
+                tok = np.array([pr[-1] for pr in prompts], dtype=np.uint32)
+                rng = np.ascontiguousarray(rng0.copy()) if sampled else None
+                got = []
+                for k in (lens if split else [total]):
+                    o = dec.generate(seqs, pos, tok, k, st, rng)
+                    got.append(o)
+                    tok, pos = o[:, -1].copy(), pos + k
+                outs.append((np.concatenate(got, axis=1), None if rng is None else rng.copy()))
+        assert np.array_equal(outs[0][0], outs[1][0]), n
+        if sampled:
+            assert np.array_equal(outs[0][1], outs[1][1]), n
