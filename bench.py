@@ -9,11 +9,16 @@ ana_generate's on-device token loop with inputs already in HBM.
 
 B = 1 (the headline `value`): a 1920-token prompt through chunked prefill,
 then W warm-up and K timed decode steps at positions 1920+ (the full
-2048-slot window). B = 64 is reported beside it (128-token prompts).
+2048-slot window); the timed call replays the graphs the warm-up captured.
+Reported beside it: B = 1 in the other modes, B = 64 (128-token prompts) in
+every mode, B = 64 x 512 prefill and window scoring, 64 agent episodes, and
+BASELINE's other decode configs (next: B = 32 at 1920+; v3: B = 64 sampled;
+bf16: B = 256), the last in a child process of their own.
 
-The roofline entry is the dominant kernel, the exact matrix-vector product:
-its algorithmic bytes (weights once, activations in and out) over its
-launches' HIP-event time on the library's stream, against 8 TB/s.
+The roofline entry is the dominant kernel of the B = 1 step, the layer
+products (with the LM head): their algorithmic bytes (weights once,
+activations in and out) over their launches' HIP-event time on the
+library's stream, against 8 TB/s.
 cpu_baseline: the CPU oracle (a restatement of the reference's dense
 decoder; the reference's Bend toolchain is absent) on a bounded sample.
 """
