@@ -1569,9 +1569,10 @@ hipError_t launch_head_pw(const GemvArgs& a, const void* pk, int bf, hipStream_t
   const uint4* p = static_cast<const uint4*>(pk);
   // the x tile fills LDS (one workgroup a CU): sixteen waves, four a SIMD,
   // one tile each (measured at B = 64: 55 -> 41 us fp32, 37 -> 26 us bf16
-  // from four waves to sixteen)
+  // from four waves to sixteen); fp32 blocks of two steps (114 -> 100 VGPRs,
+  // 43 -> 41 us at B = 64), bf16 of four
   if (bf) ANA_LAUNCH_F((k_head_pw<1, TPW, 4, 16>), grid, dim3(1024), 0, st, e0, e1, a, p, tiles);
-  else ANA_LAUNCH_F((k_head_pw<0, TPW, 4, 16>), grid, dim3(1024), 0, st, e0, e1, a, p, tiles);
+  else ANA_LAUNCH_F((k_head_pw<0, TPW, 2, 16>), grid, dim3(1024), 0, st, e0, e1, a, p, tiles);
   return hipGetLastError();
 }
 
