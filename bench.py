@@ -366,7 +366,7 @@ def main() -> int:
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": a.steps,
-        "warmup": a.warmup,
+        "warmup": max(a.warmup, 8) if a.warmup else 0,
         "ms_per_step": round(r1["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
