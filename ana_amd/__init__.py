@@ -223,9 +223,24 @@ class Decoder:
         """dd.reset / dc.en.reset."""
         self._check(lib().ana_reset(self.h, seq))
 
+    @staticmethod
+    def _rows(s, p, t, fn: str) -> None:
+        if not (p.size == t.size == s.size):
+            raise ValueError(f"{fn}: {s.size} sequences, {p.size} positions, {t.size} tokens")
+
+    @staticmethod
+    def _rng(rng, n: int, fn: str):
+        """The caller's n x 4 uint64 xoshiro words, advanced in place by the
+        library: they must be exactly that array."""
+        if not (isinstance(rng, np.ndarray) and rng.dtype == np.uint64 and rng.flags.c_contiguous
+                and rng.flags.writeable and rng.size == 4 * n):
+            raise ValueError(f"{fn}: rng must be a writable C-contiguous uint64 array of {4 * n} words")
+        return _p(rng, C.c_uint64)
+
     def feed(self, seqs, pos, toks) -> None:
         """dd.feed for each listed sequence (one token each)."""
         s, p, t = _u32(seqs), _u32(pos), _u32(toks)
+        self._rows(s, p, t, "feed")
         self._check(lib().ana_feed(self.h, s.size, _p(s, C.c_uint32), _p(p, C.c_uint32), _p(t, C.c_uint32)))
 
     def feeds(self, seq: int, pos: int, toks) -> None:
@@ -282,10 +297,7 @@ class Decoder:
         """S.pick on the device; rng (n x 4 uint64) advances in place."""
         s = _u32(seqs)
         out = np.empty(s.size, dtype=np.uint32)
-        rp = None
-        if rng is not None:
-            assert rng.dtype == np.uint64 and rng.flags.c_contiguous and rng.size == 4 * s.size
-            rp = _p(rng, C.c_uint64)
+        rp = None if rng is None else self._rng(rng, s.size, "pick")
         sc = st._c()
         self._check(lib().ana_pick(self.h, s.size, _p(s, C.c_uint32), C.byref(sc), rp, _p(out, C.c_uint32)))
         return out
@@ -294,9 +306,10 @@ class Decoder:
                  rng: np.ndarray | None = None) -> np.ndarray:
         """The token loop for each sequence: feed, head, pick, feed the pick."""
         s, p, t = _u32(seqs), _u32(pos), _u32(toks)
+        self._rows(s, p, t, "generate")
         out = np.empty((s.size, steps), dtype=np.uint32)
         sp = C.byref(st._c()) if st is not None else None
-        rp = _p(rng, C.c_uint64) if rng is not None else None
+        rp = None if rng is None else self._rng(rng, s.size, "generate")
         self._check(lib().ana_generate(self.h, s.size, _p(s, C.c_uint32), _p(p, C.c_uint32),
                                        _p(t, C.c_uint32), steps, sp, rp, _p(out, C.c_uint32)))
         return out

@@ -141,7 +141,8 @@ def _hash_noise(idx: np.ndarray) -> np.ndarray:
     return f / np.float32(9223372036854775808.0) - np.float32(1.0)
 
 
-def init_params(c: Config, kind: str = "normal", seed: int = 0, std: float = 0.02) -> np.ndarray:
+def init_params(c: Config, kind: str = "normal", seed: int = 0, std: float = 0.02,
+                trained: bool = False) -> np.ndarray:
     """Fresh parameters in namedLayout order.
 
     kind "normal": matrices and the embedding N(0, std^2) from a counter-based
@@ -150,6 +151,12 @@ def init_params(c: Config, kind: str = "normal", seed: int = 0, std: float = 0.0
     (bend/Train/Init.bend:17-35). Gains are 1, qk gains and sink logits 0, and
     the RG-LRU bases follow Griffin's init, sigmoid(lam)^8 uniform on
     [0.9, 0.999) (bend/Train/Init.bend:31-35).
+
+    trained=True gives the vectors a trained checkpoint carries instead of
+    their fresh values, so every use of them is exercised: RMSNorm gains
+    (ra, rf, final) 1 + N(0, 0.1^2), qk-norm gains (gq, gk) N(0, 0.1^2), and
+    one sink logit per head N(0, 1), each from its own counter stream of
+    ``seed``.
     """
     blocks, fin = layout(c)
     p = np.empty(c.params, dtype=np.float32)
@@ -176,10 +183,14 @@ def init_params(c: Config, kind: str = "normal", seed: int = 0, std: float = 0.0
         a = u ** 0.125
         p[o:o + n] = np.log(a / (1.0 - a)).astype(np.float32)
 
+    def vec(o: int, n: int, base: float, sd: float) -> None:
+        # a trained vector: base + N(0, sd^2), indexed by its flat offset
+        p[o:o + n] = base if not trained else np.float32(base) + _normal(seed + 0x7EA1, o, n, sd)
+
     d, f, dd = c.d, c.f, c.d * c.d
     noise(0, c.vocab * d)
     for b in blocks:
-        p[b.ra:b.ra + d] = 1.0
+        vec(b.ra, d, 1.0, 0.1)
         noise(b.wq, 4 * dd)
         if b.gla:
             noise(b.wa, dd)
@@ -187,12 +198,12 @@ def init_params(c: Config, kind: str = "normal", seed: int = 0, std: float = 0.0
                 lam(b.lam, d)
         else:
             if c.qk:
-                p[b.gq:b.gq + 2 * c.hd] = 0.0
+                vec(b.gq, 2 * c.hd, 0.0, 0.1)
             if c.sinks:
-                p[b.sink:b.sink + c.heads] = 0.0
-        p[b.rf:b.rf + d] = 1.0
+                vec(b.sink, c.heads, 0.0, 1.0)
+        vec(b.rf, d, 1.0, 0.1)
         noise(b.wg, 3 * f * d)
-    p[fin:fin + d] = 1.0
+    vec(fin, d, 1.0, 0.1)
     if not c.tied:
         noise(fin + d, c.vocab * d)
     return p

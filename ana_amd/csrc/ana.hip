@@ -44,6 +44,7 @@ struct ana_ctx {
   unsigned long long* d_amax = nullptr;  // [wb] greedy argmax keys
   float *d_ss = nullptr, *d_pm = nullptr; // split attention scratch
   float* d_part = nullptr;           // fast attention's per-split partials
+  size_t part_cap = 0;               // their floats
   float* SC = nullptr;               // scoring: the head's logits for up to sc_rows rows
   uint32_t sc_rows = 1;
   uint32_t* d_tgt = nullptr;         // scoring: each row's target token
@@ -288,7 +289,8 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if (c->mode != ANA_EXACT_FP32) {
     // the fast kernels' scratch: attention partials for every row of a step,
     // the GLA scan's regions and tables
-    if ((e = dalloc(&c->d_part, attn_fast_part_floats(c->rows, cf.heads, cf.ctx, hd))) != hipSuccess ||
+    c->part_cap = attn_fast_part_floats(c->rows, cf.heads, cf.ctx, hd);
+    if ((e = dalloc(&c->d_part, c->part_cap)) != hipSuccess ||
         (e = dalloc(&c->d_gla, gla_scan_floats(c->rows, c->gsub_cap, c->seg_cap, d, cf.heads))) != hipSuccess ||
         (e = dalloc(&c->d_gtab, c->gsub_cap)) != hipSuccess || (e = dalloc(&c->d_atab, c->atab_cap)) != hipSuccess ||
         (e = dalloc(&c->d_rseq, c->rows)) != hipSuccess || (e = dalloc(&c->d_rpos, c->rows)) != hipSuccess)
@@ -415,7 +417,7 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
       return launch_gemm_pk(g, static_cast<const char*>(c->PK) + pe->off, c->Wh != nullptr, c->st, ps.start(),
                             ps.stop());
     if (g.B >= 128 && c->d_sah && g.K % 32 == 0 && g.B <= c->rows)
-      return launch_gemm_dl(g, c->d_sah, c->d_sal, c->d_rsc, c->st, ps.start(), ps.stop());
+      return launch_gemm_dl(g, c->d_sah, c->d_sal, c->d_rsc, c->rows, c->st, ps.start(), ps.stop());
     if (g.B >= 128) return launch_gemm_big(g, c->st, ps.start(), ps.stop());
     return launch_gemm_mfma(g, c->st, ps.start(), ps.stop());
   }
@@ -590,7 +592,8 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
       a.sink = cf.sinks ? W + b.sink : nullptr;
       a.KV = sref(c, l);
       a.d = d; a.heads = cf.heads; a.ctx = cf.ctx;
-      a.ss = c->d_ss; a.pm = c->d_pm;
+      a.ss = c->d_ss; a.pm = c->d_pm; a.ss_rows = c->wb;
+      a.part_cap = c->part_cap;
       if (!chunk) {
         // each sequence's write, then its attention (dd.sm.write, dd.sm.attend)
         a.QKV = c->QKV; a.O = c->O; a.B = B; a.seq = seq; a.pos = pos; a.write_kv = 1;

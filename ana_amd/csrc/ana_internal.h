@@ -171,7 +171,9 @@ struct AttnArgs {
   uint32_t d, heads, ctx, B, write_kv;
   float* ss;            // scratch [B][heads][ctx]: sc * score
   float* pm;            // scratch [B][heads][ctx / kAttnTS]: partial maxima
+  uint32_t ss_rows;     // rows ss and pm hold
   float* part;          // fast attention: per split (m, l, o[hd])
+  size_t part_cap;      // floats at part (the launchers reject grids that need more)
   uint32_t nsp;         // fast attention: splits in the grid, those holding
                         // slots 0 .. nsp * kFastTS - 1 (0: the whole ring)
 };
@@ -236,7 +238,9 @@ hipError_t launch_zero(float* p, uint64_t n, hipStream_t st);
 
 // ---------------------------------------------------------------- fast modes
 // Reassociated (tree / fused multiply-add) versions of the decode step's
-// kernels for ANA_FAST_FP32 and ANA_BF16, B <= kSmallB rows.
+// kernels for ANA_FAST_FP32 and ANA_BF16, B <= kSmallB rows (launch_gla_fast
+// and launch_attn_fast reject decode steps of more rows: those paths are
+// off above kSmallB).
 hipError_t launch_to_bf16(const float* w, uint16_t* h, uint64_t n, hipStream_t st);
 hipError_t launch_gemv_fast(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nullptr,
                             hipEvent_t e1 = nullptr);
@@ -272,6 +276,7 @@ struct GlaSub {
 // per (chunk, head)
 struct GlaScratch {
   float *Qt, *Dj, *Uj, *S0;
+  uint32_t rows_cap, nsub_cap, nseg_cap;  // what the regions were carved for
 };
 size_t gla_scan_floats(uint32_t rows, uint32_t nsub, uint32_t nseg, uint32_t d, uint32_t heads);
 GlaScratch gla_scan_carve(float* p, uint32_t rows, uint32_t nsub, uint32_t nseg, uint32_t d,
@@ -306,8 +311,9 @@ hipError_t launch_gemm_big(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nu
 // ANA_BF16 at 128 rows or more: the activations split into bf16 head and
 // remainder (Ah, Al: B x K each; rsc: B norm scales), then the product with
 // both operands streamed straight into LDS (K a multiple of 32)
-hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, __bf16* Al, float* rsc, hipStream_t st,
-                          hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
+// (cap_rows: the rows Ah, Al and rsc hold; larger batches are rejected)
+hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, __bf16* Al, float* rsc, uint32_t cap_rows,
+                          hipStream_t st, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 size_t attn_fast_part_floats(uint32_t B, uint32_t heads, uint32_t ctx, uint32_t hd);
 // causal attention of fresh prefill rows on the matrix cores: one workgroup
 // per (head, tile of up to kFlashQ rows of one sequence), the rows' k and v

@@ -1028,6 +1028,7 @@ constexpr uint32_t kAttnWideB = 8;
 hipError_t launch_attn(const AttnArgs& a, hipStream_t st) {
   const uint32_t hd = a.d / a.heads;
   if (a.ss && a.pm && hd % ATTN_CG == 0 && a.B < kAttnWideB) {
+    if (a.B > a.ss_rows) return hipErrorInvalidValue;
     const uint32_t ns = (a.ctx + kAttnTS - 1) / kAttnTS;
 #define L_(H)                                                                                   \
   hipLaunchKernelGGL(k_attn_scores<H>, dim3(a.heads, ns, a.B), dim3(kAttnTS), 0, st, a);      \

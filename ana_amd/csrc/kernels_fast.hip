@@ -408,7 +408,8 @@ hipError_t launch_gla_fast(const float* QKV, const float* Z, const float* lam, S
                            const uint32_t* seq, float* O, uint32_t d, uint32_t heads,
                            uint32_t rglru, uint32_t B, hipStream_t st) {
   const uint32_t hd = d / heads;
-  if (hd % 16) return hipErrorInvalidValue;
+  // off above kSmallB rows (those decode steps take the exact one-wave step)
+  if (hd % 16 || B > kSmallB) return hipErrorInvalidValue;
 #define L_(H) hipLaunchKernelGGL(k_gla_fast<H>, dim3(heads, H / 16, B), dim3(256), 0, st, QKV, Z, lam, S, seq, O, d, rglru)
   switch (hd) {
     case 64: L_(64); break;
@@ -609,6 +610,10 @@ hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st) {
   const uint32_t full = (a.ctx + kFastTS - 1) / kFastTS;
   const uint32_t ns = a.nsp ? min(a.nsp, full) : full;
   if (!a.part || hd % 4 || hd > 64 || full > 64) return hipErrorInvalidValue;
+  // decode steps above kSmallB rows are off on this kernel; the partials
+  // of every (row, head, split) must fit the buffer
+  if (a.write_kv && a.B > kSmallB) return hipErrorInvalidValue;
+  if ((size_t)a.B * a.heads * ns * (hd + 2) > a.part_cap) return hipErrorInvalidValue;
 #define L_(H)                                                                                   \
   hipLaunchKernelGGL(k_attn_fast_part<H>, dim3(a.heads, ns, a.B), dim3(256), 0, st, a);        \
   hipLaunchKernelGGL(k_attn_fast_comb<H>, dim3(a.heads, a.B), dim3(64), 0, st, a, ns)
@@ -817,6 +822,7 @@ hipError_t launch_attn_rows(const AttnArgs& a, bool split, hipStream_t st) {
   if (!split && a.ctx > kAttnRowsMaxCtx) return hipErrorInvalidValue;
   if (split && !a.part) return hipErrorInvalidValue;
   const uint32_t nsp = split ? (a.ctx + kRowsSplit - 1) / kRowsSplit : 1u;
+  if (split && (size_t)a.B * a.heads * nsp * (hd + 2) > a.part_cap) return hipErrorInvalidValue;
   const size_t lds = (size_t)(split ? kRowsSplit : a.ctx) * 4;
 #define L_(H)                                                                                       \
   hipLaunchKernelGGL(k_attn_rows<H>, dim3(a.heads, a.B, nsp), dim3(256), lds, st, a);              \
@@ -1896,7 +1902,9 @@ GlaScratch gla_scan_carve(float* p, uint32_t rows, uint32_t nsub, uint32_t nseg,
   g.Dj = g.Qt + round64((size_t)rows * d);
   g.Uj = g.Dj + round64((size_t)nsub * heads * hd);
   g.S0 = g.Uj + round64((size_t)nsub * heads * hd * hd);
-  (void)nseg;
+  g.rows_cap = rows;
+  g.nsub_cap = nsub;
+  g.nseg_cap = nseg;
   return g;
 }
 
@@ -1905,6 +1913,7 @@ hipError_t launch_gla_scan(const float* QKV, const float* Z, const float* lam, S
                            uint32_t heads, uint32_t rglru, hipStream_t st) {
   const uint32_t hd = d / heads;
   if (hd % 16 || hd * 16 < 256 || nsub == 0) return hipErrorInvalidValue;
+  if (nsub > g.nsub_cap) return hipErrorInvalidValue;
 #define L_(H)                                                                                        \
   hipLaunchKernelGGL(k_gla_sub<H>, dim3(heads, nsub), dim3(256), 0, st, QKV, Z, lam, O, g, S, tab, d, \
                      rglru);                                                                         \
@@ -2416,9 +2425,10 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
   }
 }
 
-hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, __bf16* Al, float* rsc, hipStream_t st,
-                          hipEvent_t e0, hipEvent_t e1) {
+hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, __bf16* Al, float* rsc, uint32_t cap_rows,
+                          hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   if (a.amax || (a.K % 32) || a.B == 0 || !a.Wh0 || (a.nseg > 1 && !a.Wh1)) return hipErrorInvalidValue;
+  if (a.B > cap_rows) return hipErrorInvalidValue;
   // the split first (its time is inside the events)
   if (e0) (void)hipEventRecord(e0, st);
   hipLaunchKernelGGL(k_split, dim3((a.B + 3) / 4), dim3(256), 0, st, a.X, a.ldx, a.K, a.ng, a.B, Ah, Al, rsc);

@@ -437,6 +437,14 @@ or_state* or_state_new(const or_model* m) {
   return s;
 }
 
+/* a copy of s's states and residual row (workspace is scratch, not copied) */
+or_state* or_state_clone(const or_state* s) {
+  or_state* t = or_state_new(s->m);
+  for (uint32_t l = 0; l < s->m->c.layers; l++) memcpy(t->lay[l], s->lay[l], s->lay_n[l] * sizeof(float));
+  memcpy(t->x, s->x, (size_t)s->m->c.d * sizeof(float));
+  return t;
+}
+
 void or_state_free(or_state* s) {
   if (!s) return;
   for (uint32_t l = 0; l < s->m->c.layers; l++) free(s->lay[l]);

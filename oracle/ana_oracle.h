@@ -70,6 +70,7 @@ void or_set_threads(int n);
 
 /* dense engine: one sequence's states (GLA S, softmax K/V rings) + residual */
 or_state* or_state_new(const or_model* m);
+or_state* or_state_clone(const or_state* s);                 /* same states, own storage */
 void or_state_free(or_state* s);
 void or_reset(or_state* s);                                  /* dd.reset */
 void or_feed(const or_model* m, or_state* s, uint32_t pos, uint32_t tok); /* dd.feed */

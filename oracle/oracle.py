@@ -46,6 +46,7 @@ def lib() -> C.CDLL:
             "or_set_threads": (None, [C.c_int]),
             "or_state_new": (vp, [vp]),
             "or_state_free": (None, [vp]),
+            "or_state_clone": (vp, [vp]),
             "or_reset": (None, [vp]),
             "or_feed": (None, [vp, vp, C.c_uint32, C.c_uint32]),
             "or_logits": (None, [vp, vp, f32p]),
@@ -131,6 +132,13 @@ class State:
 
     def reset(self) -> None:
         lib().or_reset(self.h)
+
+    def clone(self) -> "State":
+        """An independent copy of this sequence's states."""
+        t = State.__new__(State)
+        t.m = self.m
+        t.h = lib().or_state_clone(self.h)
+        return t
 
     def feed(self, pos: int, tok: int) -> None:
         lib().or_feed(self.m.h, self.h, pos, tok)

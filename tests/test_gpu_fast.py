@@ -10,6 +10,11 @@ step, teacher-forced on the same tokens as the oracle:
 
 and check the greedy token loop's picks are argmaxes of the oracle's logits
 up to that tolerance (a near-tie may pick either side of it).
+
+Every checkpoint here carries trained-like vectors (norm gains 1 + N(0, 0.1^2),
+qk-norm gains N(0, 0.1^2), per-head sinks N(0, 1)), so the gains the fast
+modes fold into their packed weights, the (1 + g) qk factor and per-head
+sink indexing are all exercised.
 """
 import json
 import os
@@ -39,7 +44,7 @@ def rel_err(got, want):
 def small_ckpt(tmp_path_factory):
     d = tmp_path_factory.mktemp("ckf")
     p = str(d / "v3.ftc2")
-    ckpt.write(p, cf.SMALL4_V3, ckpt.init_params(cf.SMALL4_V3, "normal", 3))
+    ckpt.write(p, cf.SMALL4_V3, ckpt.init_params(cf.SMALL4_V3, "normal", 3, trained=True))
     return p
 
 
@@ -53,7 +58,7 @@ MID = cf.Config(vocab=258, ctx=64, d=256, f=1024, layers=4, heads=4, rglru=True,
 def mid_ckpt(tmp_path_factory):
     d = tmp_path_factory.mktemp("ckm")
     p = str(d / "mid.ftc2")
-    ckpt.write(p, MID, ckpt.init_params(MID, "normal", 5))
+    ckpt.write(p, MID, ckpt.init_params(MID, "normal", 5, trained=True))
     return p
 
 
@@ -61,7 +66,7 @@ def mid_ckpt(tmp_path_factory):
 def big_ckpt(tmp_path_factory):
     d = tmp_path_factory.mktemp("ckb")
     p = str(d / "fp100m.ftc2")
-    ckpt.write(p, cf.FP100M, ckpt.init_params(cf.FP100M, "normal", 0))
+    ckpt.write(p, cf.FP100M, ckpt.init_params(cf.FP100M, "normal", 0, trained=True))
     return p
 
 
@@ -209,7 +214,7 @@ def test_fast_batch8_matrix_cores(oracle, small_ckpt, mode):
 def noarms_ckpt(tmp_path_factory):
     d = tmp_path_factory.mktemp("ckn")
     p = str(d / "noarms.ftc2")
-    ckpt.write(p, cf.SMALL4_NOARMS, ckpt.init_params(cf.SMALL4_NOARMS, "normal", 4))
+    ckpt.write(p, cf.SMALL4_NOARMS, ckpt.init_params(cf.SMALL4_NOARMS, "normal", 4, trained=True))
     return p
 
 
@@ -423,7 +428,7 @@ def test_fast_decode_long_split(oracle, tmp_path, mode):
     after every step."""
     print(f"case fast decode long split mode {mode}", flush=True)
     p = str(tmp_path / "long.ftc2")
-    ckpt.write(p, LONG, ckpt.init_params(LONG, "normal", 11))
+    ckpt.write(p, LONG, ckpt.init_params(LONG, "normal", 11, trained=True))
     m = oracle.Model(p)
     n, steps = 6, 4
     rng = np.random.default_rng(31)
@@ -446,5 +451,46 @@ def test_fast_decode_long_split(oracle, tmp_path, mode):
             for i in watch:
                 sts[i].feed(pos[i], tk[i])
                 worst = max(worst, rel_err(got[i], sts[i].logits()))
+    print(f"worst relative error {worst:.3e}", flush=True)
+    assert worst <= TOL[mode], worst
+
+
+WRAP = cf.Config(vocab=258, ctx=512, d=256, f=1024, layers=4, heads=4, rglru=True, qk=True, sinks=True, tied=True)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_fast_decode_split_after_wrap(oracle, tmp_path, mode):
+    """The wide decode attention in 256-slot pieces after the ring wraps:
+    6 sequences from positions 480-515 on ctx 512 (so two pieces, every slot
+    live once the ring has wrapped), 40 teacher-forced decode steps that
+    carry every sequence past position 512; three sequences' logits against
+    their own oracle runs every fourth step."""
+    print(f"case fast decode split after wrap mode {mode}", flush=True)
+    p = str(tmp_path / "wrap.ftc2")
+    ckpt.write(p, WRAP, ckpt.init_params(WRAP, "normal", 13, trained=True))
+    m = oracle.Model(p)
+    n, steps = 6, 40
+    rng = np.random.default_rng(37)
+    starts = [480 + 7 * i for i in range(n)]
+    toks = rng.integers(2, m.vocab, size=(n, max(starts) + steps + 1)).astype(np.uint32)
+    watch = [0, 2, 5]
+    sts = {i: oracle.State(m) for i in watch}
+    for i in watch:
+        for q in range(starts[i]):
+            sts[i].feed(q, int(toks[i, q]))
+    seqs = list(range(n))
+    worst = 0.0
+    with ana_amd.Decoder(p, max_seqs=n, prefill_chunk=64, numerics=mode) as dec:
+        dec.feeds_n(seqs, [0] * n, [toks[i, : starts[i]] for i in range(n)])
+        for k in range(steps):
+            pos = [starts[i] + k for i in range(n)]
+            tk = [int(toks[i, pos[i]]) for i in range(n)]
+            dec.feed(seqs, pos, tk)
+            for i in watch:
+                sts[i].feed(pos[i], tk[i])
+            if k % 4 == 3:
+                got = dec.logits(seqs)
+                for i in watch:
+                    worst = max(worst, rel_err(got[i], sts[i].logits()))
     print(f"worst relative error {worst:.3e}", flush=True)
     assert worst <= TOL[mode], worst

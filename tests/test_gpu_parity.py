@@ -20,7 +20,11 @@ pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 VEC = json.load(open(os.path.join(HERE, "golden", "reference_vectors.json")))
-CFGS = {"v3-arms": cf.SMALL4_V3, "no-arms": cf.SMALL4_NOARMS}
+# v3-trained: small4_v3 with the vectors a trained checkpoint carries (norm
+# gains 1 + N(0, 0.1^2), qk-norm gains N(0, 0.1^2), a sink logit per head
+# N(0, 1)), so gain offsets, the (1 + g) factor and per-head sinks are live
+CFGS = {"v3-arms": cf.SMALL4_V3, "no-arms": cf.SMALL4_NOARMS, "v3-trained": cf.SMALL4_V3}
+TRAINED = {"v3-trained"}
 
 
 def bits(a):
@@ -33,7 +37,7 @@ def ckpts(tmp_path_factory):
     out = {}
     for name, c in CFGS.items():
         p = str(d / f"{name}.ftc2")
-        ckpt.write(p, c, ckpt.init_params(c, "hash"))
+        ckpt.write(p, c, ckpt.init_params(c, "hash", 1, trained=name in TRAINED))
         out[name] = p
     return out
 
@@ -206,7 +210,7 @@ def _check_pick(oracle, dec, seqs, lgs):
 
 
 def test_sampler_small_vocab(oracle, ckpts):
-    path = ckpts["v3-arms"]
+    path = ckpts["v3-trained"]
     print("case pick v258", flush=True)
     with ana_amd.Decoder(path, max_seqs=4) as dec:
         for s in range(4):
@@ -219,7 +223,7 @@ def test_sampler_32k_vocab(oracle, tmp_path):
     """The v1 config (vocab 32768: a perfect depth-15 tree)."""
     c = cf.V1
     path = str(tmp_path / "v1.ftc2")
-    ckpt.write(path, c, ckpt.init_params(c, "normal", 0))
+    ckpt.write(path, c, ckpt.init_params(c, "normal", 0, trained=True))
     print("case pick v32768", flush=True)
     oracle.set_threads(8)
     with ana_amd.Decoder(path, max_seqs=3) as dec:
@@ -241,7 +245,7 @@ def test_115m_batch8(oracle, tmp_path):
     attention at hd 64, bit for bit against each sequence's oracle run."""
     c = cf.FP100M
     path = str(tmp_path / "fp100m8.ftc2")
-    ckpt.write(path, c, ckpt.init_params(c, "normal", 2))
+    ckpt.write(path, c, ckpt.init_params(c, "normal", 2, trained=True))
     print("case 115m batch8", flush=True)
     oracle.set_threads(8)
     m = oracle.Model(path)
@@ -271,7 +275,7 @@ def test_115m_shape(oracle, tmp_path):
     all arms) at ctx 2048: a prompt through feeds, then steps, bit for bit."""
     c = cf.FP100M
     path = str(tmp_path / "fp100m.ftc2")
-    ckpt.write(path, c, ckpt.init_params(c, "normal", 0))
+    ckpt.write(path, c, ckpt.init_params(c, "normal", 0, trained=True))
     print("case 115m", flush=True)
     oracle.set_threads(8)
     m = oracle.Model(path)
@@ -397,7 +401,7 @@ def test_text_end_to_end(oracle, tmp_path):
     tok = ana_amd.Tokenizer(str(art))
     c = cf.Config(300, 64, 64, 192, 4, 4, True, True, True)
     path = str(tmp_path / "m.ftc2")
-    ckpt.write(path, c, ckpt.init_params(c, "normal", 3), tokenizer_id=tok.identity())
+    ckpt.write(path, c, ckpt.init_params(c, "normal", 3, trained=True), tokenizer_id=tok.identity())
     man = ana_amd.read_manifest(path)
     t = ana_amd.find_tokenizer(man["tokenizer_id"], candidates=[str(art)])
     prompt = [ana_amd.Tokenizer.BOS] + [int(i) for i in t.encode(text)]
@@ -431,7 +435,7 @@ def test_generate_calls_of_any_length(ckpts, sampled, mode):
     call on a twin decoder, bit for bit, greedy and sampled; so do 7 and 6
     rows (a capture per row count)."""
     print(f"case generate calls of any length mode {mode} sampled {sampled}", flush=True)
-    path = ckpts["v3-arms"]
+    path = ckpts["v3-trained"]
     lens = [5, 9, 1, 11]
     total = sum(lens)
     st = ana_amd.Settings(float(np.float32(0.8)), 40, float(np.float32(0.9))) if sampled else None
@@ -456,3 +460,48 @@ def test_generate_calls_of_any_length(ckpts, sampled, mode):
         assert np.array_equal(outs[0][0], outs[1][0]), n
         if sampled:
             assert np.array_equal(outs[0][1], outs[1][1]), n
+
+
+NAN_MID = cf.Config(vocab=258, ctx=64, d=256, f=1024, layers=4, heads=4, rglru=True, qk=True, sinks=True, tied=True)
+
+
+@pytest.mark.parametrize("n", [1, 6])
+@pytest.mark.parametrize("mode", [ana_amd.EXACT_FP32, ana_amd.FAST_FP32, ana_amd.BF16],
+                         ids=["exact", "fast_fp32", "bf16"])
+def test_nan_logits_fall_back(oracle, tmp_path, mode, n):
+    """dd.top's NaN answer and Decode.bend's fallback (bend/Dense/Decode.bend:
+    475-484, bend/Decode.bend:407-418): one final norm gain is NaN, so every
+    logit is NaN. ana_top answers vocab for every sequence, and each pick of
+    the on-device loop is Sample.argmax over the NaN logits, as the oracle's
+    host loop falls back to it (1 and 6 sequences: the small-batch head's
+    argmax keys, and above four rows the wide head's keys or dd.top's pass
+    over the stored logits)."""
+    print(f"case nan fallback mode {mode} n {n}", flush=True)
+    c = NAN_MID
+    p = ckpt.init_params(c, "normal", 9, trained=True)
+    _, fin = cf.layout(c)
+    p[fin + 5] = np.nan
+    path = str(tmp_path / "nan.ftc2")
+    ckpt.write(path, c, p)
+    m = oracle.Model(path)
+    seqs = list(range(n))
+    prompts = [[2 + 7 * i + k for k in range(3 + i)] for i in seqs]
+    with ana_amd.Decoder(path, max_seqs=n, numerics=mode) as dec:
+        dec.feeds_n(seqs, [0] * n, prompts)
+        lg = dec.logits(seqs)
+        assert np.isnan(lg).all()
+        assert list(dec.top(seqs)) == [c.vocab] * n
+        out = dec.generate(seqs, [len(pr) for pr in prompts], [1] * n, 3)
+    for i in seqs:
+        st = oracle.State(m)
+        for q, t in enumerate(prompts[i] + [1]):
+            st.feed(q, t)
+        want, pos = [], len(prompts[i]) + 1
+        for _ in range(3):
+            w = st.logits()
+            assert oracle.top(w) == c.vocab
+            t = oracle.tree_argmax(w)
+            want.append(t)
+            st.feed(pos, t)
+            pos += 1
+        assert [int(x) for x in out[i]] == want, i

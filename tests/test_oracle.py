@@ -97,19 +97,21 @@ def test_store_pick_nan_and_inf(oracle):
     assert oracle.top(lg) == 0
 
 
-def _ckpt(tmp_path, c, kind="hash", seed=0, name="m.ftc2"):
-    p = ckpt.init_params(c, kind, seed)
+def _ckpt(tmp_path, c, kind="hash", seed=0, name="m.ftc2", trained=False):
+    p = ckpt.init_params(c, kind, seed, trained=trained)
     path = str(tmp_path / name)
     ckpt.write(path, c, p)
     return path, p
 
 
-@pytest.mark.parametrize("c", [cf.SMALL4_V3, cf.SMALL4_NOARMS], ids=["v3-arms", "no-arms"])
-def test_dense_matches_meaning(oracle, tmp_path, c):
+@pytest.mark.parametrize("c,trained", [(cf.SMALL4_V3, False), (cf.SMALL4_NOARMS, False), (cf.SMALL4_V3, True)],
+                         ids=["v3-arms", "no-arms", "v3-trained"])
+def test_dense_matches_meaning(oracle, tmp_path, c, trained):
     """bend/tests/decode-dense.bend: 96 positions on ctx 64 (the ring wraps);
     dense vs tree within 1e-5 relative on each side of the wrap; a reset
-    reproduces the bits; the store pick is the tree argmax at every position."""
-    path, _ = _ckpt(tmp_path, c)
+    reproduces the bits; the store pick is the tree argmax at every position.
+    v3-trained carries non-unit norm gains, qk gains and per-head sinks."""
+    path, _ = _ckpt(tmp_path, c, trained=trained)
     m = oracle.Model(path)
     st, tr = oracle.State(m), oracle.Tree(m)
     ts = VEC["window"]
@@ -146,21 +148,121 @@ def _blank(c):
 
 def test_zero_blocks_leave_the_residual(oracle):
     """With zero matrices every block adds exactly 0, so the logits are
-    E . rmsnorm(E[tok]) (a closed form independent of summation order up to
-    rounding)."""
+    E . (rmsnorm(E[tok]) * final) (a closed form independent of summation
+    order up to rounding). The block gains ra and rf are random too: with
+    zero matrices they must change nothing, while the final gain must scale
+    the head's input column by column."""
     c = cf.Config(64, 16, 32, 48, 4, 2, True, True, True)
-    p, _, _ = _blank(c)
+    p, blocks, fin = _blank(c)
     rng = np.random.default_rng(1)
     E = rng.standard_normal((c.vocab, c.d)).astype(np.float32)
     p[: c.vocab * c.d] = E.reshape(-1)
+    for b in blocks:
+        p[b.ra:b.ra + c.d] = 1.0 + 0.3 * rng.standard_normal(c.d)
+        p[b.rf:b.rf + c.d] = 1.0 + 0.3 * rng.standard_normal(c.d)
+    g = (1.0 + 0.3 * rng.standard_normal(c.d)).astype(np.float32)
+    p[fin:fin + c.d] = g
     m = oracle.Model(cfg=c, params=p)
     st = oracle.State(m)
     for pos, tok in enumerate([3, 9, 9, 1]):
         st.feed(pos, tok)
         x = E[tok].astype(np.float64)
         assert np.array_equal(st.x(), E[tok])
-        want = E.astype(np.float64) @ (x / np.sqrt((x * x).mean() + 1e-5))
+        want = E.astype(np.float64) @ (x / np.sqrt((x * x).mean() + 1e-5) * g)
         np.testing.assert_allclose(st.logits(), want, rtol=2e-6, atol=2e-6)
+
+
+def _rms(x, g):
+    return x / np.sqrt((x * x).mean() + 1e-5) * g
+
+
+def test_softmax_layer_float64(oracle):
+    """One softmax layer with every arm on and every parameter non-trivial:
+    random Wq, Wk, Wv, Wo, norm gains ra, qk-norm gains gq and gk (one hd
+    vector each, shared by the heads, applied as 1 + g), and a different
+    sink per head; the GLA layers before it and the MLP are zero. The
+    residual after each of 13 tokens on ctx 8 (the ring wraps) is held to
+    a float64 evaluation of bend/Model.bend's sm.attend (scores scaled by
+    1/sqrt(hd), the sink in the max and the denominator only). A gain
+    without its 1 +, one gain vector used for both q and k, sink[0] for
+    every head, or a missing 1/sqrt(hd) each fail it by far more than the
+    tolerance."""
+    c = cf.Config(32, 8, 16, 8, 4, 4, False, True, True)
+    p, blocks, fin = _blank(c)
+    rng = np.random.default_rng(12)
+    d, hd, H = c.d, c.hd, c.heads
+    E = rng.standard_normal((c.vocab, d)).astype(np.float32)
+    p[: c.vocab * d] = E.reshape(-1)
+    sm = blocks[3]
+    W = {}
+    for name, o in (("q", sm.wq), ("k", sm.wk), ("v", sm.wv), ("o", sm.wo)):
+        W[name] = (rng.standard_normal((d, d)) * 0.6).astype(np.float32)
+        p[o:o + d * d] = W[name].reshape(-1)
+    ra = (1.0 + 0.3 * rng.standard_normal(d)).astype(np.float32)
+    gq = (0.4 * rng.standard_normal(hd)).astype(np.float32)
+    gk = (0.4 * rng.standard_normal(hd)).astype(np.float32)
+    sinks = (1.5 * rng.standard_normal(H)).astype(np.float32)
+    p[sm.ra:sm.ra + d] = ra
+    p[sm.gq:sm.gq + hd] = gq
+    p[sm.gk:sm.gk + hd] = gk
+    p[sm.sink:sm.sink + H] = sinks
+    m = oracle.Model(cfg=c, params=p)
+    st = oracle.State(m)
+    f8 = lambda a: np.asarray(a, dtype=np.float64)  # noqa: E731
+    Ks, Vs = [], []
+    toks = [int(t) for t in rng.integers(0, c.vocab, size=13)]
+    for pos, t in enumerate(toks):
+        st.feed(pos, t)
+        x = f8(E[t])
+        n = _rms(x, f8(ra))
+        q, k, v = f8(W["q"]) @ n, f8(W["k"]) @ n, f8(W["v"]) @ n
+        qh = np.concatenate([_rms(q[h * hd:(h + 1) * hd], 1.0 + f8(gq)) for h in range(H)])
+        kh = np.concatenate([_rms(k[h * hd:(h + 1) * hd], 1.0 + f8(gk)) for h in range(H)])
+        Ks.append(kh)
+        Vs.append(v)
+        K, V = np.array(Ks[-c.ctx:]), np.array(Vs[-c.ctx:])
+        o = np.zeros(d)
+        for h in range(H):
+            sl = slice(h * hd, (h + 1) * hd)
+            s = K[:, sl] @ qh[sl] / math.sqrt(hd)
+            mx = max(s.max(), float(sinks[h]))
+            e = np.exp(s - mx)
+            o[sl] = (e[:, None] * V[:, sl]).sum(0) / (e.sum() + math.exp(float(sinks[h]) - mx))
+        want = x + f8(W["o"]) @ o
+        np.testing.assert_allclose(st.x(), want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+
+
+def test_mlp_float64(oracle):
+    """The tail's MLP with a non-unit norm gain: one GLA layer whose mix is
+    zero (Wq = Wk = Wv = Wa = Wo = 0), so x' = x + Wd (silu(Wg n) * (Wu n))
+    with n = rmsnorm(x) * rf; rf random (ra too, which must not matter).
+    Against float64; rf applied to the wrong norm, or gate and up swapped,
+    fails it."""
+    c = cf.Config(32, 8, 16, 24, 1, 2, False, False, False)
+    p, blocks, fin = _blank(c)
+    rng = np.random.default_rng(13)
+    d, f = c.d, c.f
+    E = rng.standard_normal((c.vocab, d)).astype(np.float32)
+    p[: c.vocab * d] = E.reshape(-1)
+    b = blocks[0]
+    Wg = (rng.standard_normal((f, d)) * 0.5).astype(np.float32)
+    Wu = (rng.standard_normal((f, d)) * 0.5).astype(np.float32)
+    Wd = (rng.standard_normal((d, f)) * 0.5).astype(np.float32)
+    p[b.wg:b.wg + f * d] = Wg.reshape(-1)
+    p[b.wu:b.wu + f * d] = Wu.reshape(-1)
+    p[b.wd:b.wd + d * f] = Wd.reshape(-1)
+    rf = (1.0 + 0.3 * rng.standard_normal(d)).astype(np.float32)
+    p[b.rf:b.rf + d] = rf
+    p[b.ra:b.ra + d] = 1.0 + 0.3 * rng.standard_normal(d)
+    m = oracle.Model(cfg=c, params=p)
+    st = oracle.State(m)
+    for pos, t in enumerate([5, 1, 30, 7]):
+        st.feed(pos, t)
+        x = E[t].astype(np.float64)
+        n = _rms(x, rf.astype(np.float64))
+        g, u = Wg.astype(np.float64) @ n, Wu.astype(np.float64) @ n
+        want = x + Wd.astype(np.float64) @ (g / (1.0 + np.exp(-g)) * u)
+        np.testing.assert_allclose(st.x(), want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
 
 
 def test_attention_closed_form(oracle):
