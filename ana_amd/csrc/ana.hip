@@ -32,6 +32,11 @@ struct ana_ctx {
   int mode = ANA_EXACT_FP32;         // numerics
   float* W = nullptr;                // parameters [P]
   uint16_t* Wh = nullptr;            // ANA_BF16: the parameters as bfloat16 [P]
+  // ANA_BF16 keeps the first block's matrices in fp32: parameters in
+  // [fp32_lo, fp32_hi) are read as fp32 in every mode (the first block's
+  // rounding dominates the bf16 logits' error: alone it gives ~1.3e-2 of the
+  // ~1.4e-2 all blocks give at 115M)
+  uint64_t fp32_lo = 0, fp32_hi = 0;
   float* state = nullptr;            // [max_seqs][seq_stride]
   float* xs = nullptr;               // [max_seqs][d]
   // workspace, wb rows
@@ -59,6 +64,7 @@ struct ana_ctx {
     uint64_t off;
     uint32_t rows0, rows1, nseg, mode, K;
     const float* ng;
+    int bf;                          // packed as bf16 (else fp32)
   };
   std::unordered_map<const float*, PkEnt> pk;
   float* d_gla = nullptr;            // fast prefill's GLA scan scratch
@@ -233,6 +239,10 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   c->step = ck.step;
   c->P = params_of(ck.cfg);
   c->blk = layout_of(ck.cfg, &c->fin);
+  if (!c->blk.empty()) {
+    c->fp32_lo = c->blk[0].ra;
+    c->fp32_hi = c->blk[0].end;
+  }
   c->max_seqs = o.max_seqs;
   c->chunk = o.prefill_chunk;
   c->wb = std::max(c->max_seqs, c->chunk);
@@ -393,6 +403,13 @@ static const ana_ctx::PkEnt* find_pk(const ana_ctx* c, const GemvArgs& g) {
   return same ? &pe : nullptr;
 }
 
+// whether product g reads bfloat16 weights (ANA_BF16, outside the fp32 block)
+static bool reads_bf16(const ana_ctx* c, const GemvArgs& g) {
+  if (!c->Wh) return false;
+  const uint64_t o = (uint64_t)(g.seg[0].W - c->W);
+  return !(o >= c->fp32_lo && o < c->fp32_hi);
+}
+
 static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool chunk = false) {
   const bool small = g0.B <= kSmallB;
   const bool pk_ok = gemm_pk_fits(g0) || (kind == ANA_K_HEAD && head_pw_fits(g0));
@@ -402,21 +419,20 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
   // products too (greedy picks then read the stored logits)
   if (pe || (fast_mode(c) && (small ? !chunk : (chunk || kind != ANA_K_HEAD || g0.B >= kPwMaxB)))) {
     GemvArgs g = g0;
-    if (c->Wh) {
+    const bool bf = reads_bf16(c, g);
+    if (bf) {
       g.Wh0 = c->Wh + (g.seg[0].W - c->W);
       g.Wh1 = g.nseg > 1 ? c->Wh + (g.seg[1].W - c->W) : nullptr;
     }
     double by = gemv_bytes(g);
-    if (c->Wh) by -= 2.0 * (g.seg[0].rows + (g.nseg > 1 ? g.seg[1].rows : 0)) * g.K;
+    if (bf) by -= 2.0 * (g.seg[0].rows + (g.nseg > 1 ? g.seg[1].rows : 0)) * g.K;
     ProfScope ps(c, kind, by, true);
     if (small) return launch_gemv_fast(g, c->st, ps.start(), ps.stop());
     if (pe && kind == ANA_K_HEAD && head_pw_fits(g))
-      return launch_head_pw(g, static_cast<const char*>(c->PK) + pe->off, c->Wh != nullptr, c->st, ps.start(),
-                            ps.stop());
+      return launch_head_pw(g, static_cast<const char*>(c->PK) + pe->off, pe->bf, c->st, ps.start(), ps.stop());
     if (pe)
-      return launch_gemm_pk(g, static_cast<const char*>(c->PK) + pe->off, c->Wh != nullptr, c->st, ps.start(),
-                            ps.stop());
-    if (g.B >= 128 && c->d_sah && g.K % 32 == 0 && g.B <= c->rows)
+      return launch_gemm_pk(g, static_cast<const char*>(c->PK) + pe->off, pe->bf, c->st, ps.start(), ps.stop());
+    if (g.B >= 128 && c->d_sah && bf && g.K % 32 == 0 && g.B <= c->rows)
       return launch_gemm_dl(g, c->d_sah, c->d_sal, c->d_rsc, c->rows, c->st, ps.start(), ps.stop());
     if (g.B >= 128) return launch_gemm_big(g, c->st, ps.start(), ps.stop());
     return launch_gemm_mfma(g, c->st, ps.start(), ps.stop());
@@ -466,7 +482,6 @@ static void layer_products(const ana_ctx* c, uint32_t l, GemvArgs p[4]) {
 // every layer product's packed weights and the head's (final norm, tied
 // embedding), in one allocation
 static hipError_t pack_weights(ana_ctx* c) {
-  const int bf = c->Wh != nullptr;
   const ana_config& cf = c->cfg;
   uint64_t total = 0;
   std::vector<GemvArgs> all;
@@ -483,8 +498,9 @@ static hipError_t pack_weights(ana_ctx* c) {
     for (uint32_t i = 0; i < np; i++) {
       const GemvArgs& g = p[i];
       if (g.K % 128) continue;
+      const int bf = reads_bf16(c, g);
       c->pk[g.seg[0].W] = ana_ctx::PkEnt{total, g.seg[0].rows, g.nseg > 1 ? g.seg[1].rows : 0u, g.nseg,
-                                         g.mode == GM_SILU ? 1u : 0u, g.K, g.ng};
+                                         g.mode == GM_SILU ? 1u : 0u, g.K, g.ng, bf};
       total += (pack_bytes(g, bf) + 255) & ~255ull;
       all.push_back(g);
     }
@@ -492,8 +508,10 @@ static hipError_t pack_weights(ana_ctx* c) {
   if (all.empty()) return hipSuccess;
   hipError_t e = hipMalloc(&c->PK, total);
   if (e != hipSuccess) return e;
-  for (const GemvArgs& g : all)
-    if ((e = launch_pack(g, static_cast<char*>(c->PK) + c->pk[g.seg[0].W].off, bf, c->st)) != hipSuccess) return e;
+  for (const GemvArgs& g : all) {
+    const ana_ctx::PkEnt& pe = c->pk[g.seg[0].W];
+    if ((e = launch_pack(g, static_cast<char*>(c->PK) + pe.off, pe.bf, c->st)) != hipSuccess) return e;
+  }
   return hipSuccess;
 }
 
