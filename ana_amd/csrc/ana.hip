@@ -78,7 +78,6 @@ struct ana_ctx {
   std::vector<AttnTile> h_atab;
   std::vector<GlaSub> h_gtab;
   std::vector<uint32_t> h_rseq, h_rpos;
-  size_t out_cap = 0;
   std::string err;
   // ana_generate's decode step captured as HIP graphs, replayed per step:
   // one step, and kGraphSteps steps back to back (a graph launch costs tens
@@ -111,7 +110,7 @@ struct ana_ctx {
 };
 
 static const uint32_t kGraphSteps = 8;
-// steps of every row d_out holds at least (more when a call asks)
+// steps of every row d_out holds: ana_generate runs longer calls in pieces
 static const uint32_t kOutSteps = 1024;
 
 static const size_t kProfMax = 16384;
@@ -280,6 +279,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = dalloc(&c->XA, (uint64_t)c->rows * d)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->XN, (uint64_t)c->rows * d)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_step, wb)) != hipSuccess) return bad(e);
+  if ((e = dalloc(&c->d_out, wb * kOutSteps)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_amax, wb * kAmaxPerRow)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_ss, wb * cf.heads * cf.ctx)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_pm, wb * cf.heads * ((cf.ctx + kAttnTS - 1) / kAttnTS))) != hipSuccess) return bad(e);
@@ -924,8 +924,9 @@ extern "C" int ana_pick(ana_ctx* c, uint32_t n, const uint32_t* seq, const ana_s
 }
 
 // one decode step of the token loop: embed the current tokens, every
-// layer, the head, the pick, then advance (pos + 1, tok = pick, record)
-static int gen_step(ana_ctx* c, uint32_t n, const PickArgs& pa, bool greedy) {
+// layer, the head, the pick, then advance (pos + 1, tok = pick, record the
+// pick at out[step[b] * n + b] and count the row's step)
+static int gen_step(ana_ctx* c, uint32_t n, const PickArgs& pa, bool greedy, uint32_t* out, uint32_t* step) {
   HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, n, c->X, c->d_amax, c->st));
   if (int r = run_layers(c, n, c->d_seq, c->d_pos, nullptr)) return r;
   if (int r = run_head(c, c->X, n, greedy)) return r;
@@ -942,10 +943,42 @@ static int gen_step(ana_ctx* c, uint32_t n, const PickArgs& pa, bool greedy) {
   ad.greedy = greedy;
   ad.pos = c->d_pos;
   ad.tok = c->d_tok;
-  ad.out = c->d_out;
-  ad.step = c->d_step;
+  ad.out = out;
+  ad.step = step;
   ProfScope ps(c, ANA_K_PICK, 16.0 * n);
   HIPCHK(c, launch_advance(ad, c->st));
+  return ANA_OK;
+}
+
+// ana_generate's checks, with no heap allocation (a 64k-bit bitset on the
+// stack finds a sequence listed twice)
+static int check_generate(ana_ctx* c, const char* fn, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+                          const uint32_t* tok, uint32_t steps, const ana_sampling* s, const uint64_t* rng,
+                          const uint32_t* out) {
+  if (n == 0 || n > c->max_seqs || !seq) return fail(c, ANA_EINVAL, "%s: %u sequences (1..%u)", fn, n, c->max_seqs);
+  if (c->max_seqs > 65536) return fail(c, ANA_EUNSUP, "%s: more than 65536 sequence slots", fn);
+  uint64_t seen[1024] = {};
+  for (uint32_t i = 0; i < n; i++) {
+    const uint32_t q = seq[i];
+    if (q >= c->max_seqs) return fail(c, ANA_EINVAL, "%s: sequence %u outside 0..%u", fn, q, c->max_seqs - 1);
+    if (seen[q >> 6] >> (q & 63) & 1) return fail(c, ANA_EINVAL, "%s: sequence %u listed twice", fn, q);
+    seen[q >> 6] |= 1ull << (q & 63);
+  }
+  if (!pos || !tok || (steps && !out)) return fail(c, ANA_EINVAL, "%s: null argument", fn);
+  const bool greedy = !s || s->temperature <= 0.0f;
+  if (!greedy && !rng) return fail(c, ANA_EINVAL, "%s: sampling needs rng state", fn);
+  for (uint32_t i = 0; i < n; i++)
+    if (tok[i] >= c->cfg.vocab) return fail(c, ANA_EINVAL, "%s: token %u outside the vocabulary", fn, tok[i]);
+  return ANA_OK;
+}
+
+// the rows' sequence, position and token (and RNG words) into the context
+static int gen_inputs(ana_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* pos, const uint32_t* tok,
+                      bool greedy, const uint64_t* rng) {
+  HIPCHK(c, hipMemcpyAsync(c->d_seq, seq, 4 * n, hipMemcpyHostToDevice, c->st));
+  HIPCHK(c, hipMemcpyAsync(c->d_pos, pos, 4 * n, hipMemcpyHostToDevice, c->st));
+  HIPCHK(c, hipMemcpyAsync(c->d_tok, tok, 4 * n, hipMemcpyHostToDevice, c->st));
+  if (!greedy) HIPCHK(c, hipMemcpyAsync(c->d_rng, rng, 32 * n, hipMemcpyHostToDevice, c->st));
   return ANA_OK;
 }
 
@@ -953,32 +986,11 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
                             const uint32_t* tok, uint32_t steps, const ana_sampling* s,
                             uint64_t* rng, uint32_t* out) {
   if (!c) return ANA_EINVAL;
-  if (int r = check_seqs(c, "ana_generate", n, seq)) return r;
-  if (!pos || !tok || (steps && !out)) return fail(c, ANA_EINVAL, "ana_generate: null argument");
-  const bool greedy = !s || s->temperature <= 0.0f;
-  if (!greedy && !rng) return fail(c, ANA_EINVAL, "ana_generate: sampling needs rng state");
-  for (uint32_t i = 0; i < n; i++)
-    if (tok[i] >= c->cfg.vocab) return fail(c, ANA_EINVAL, "ana_generate: token %u outside the vocabulary", tok[i]);
+  if (int r = check_generate(c, "ana_generate", n, seq, pos, tok, steps, s, rng, out)) return r;
   if (steps == 0) return ANA_OK;
+  const bool greedy = !s || s->temperature <= 0.0f;
   HIPCHK(c, hipSetDevice(c->device));
-  const size_t need = (size_t)n * steps;
-  if (need > c->out_cap) {
-    // room for kOutSteps steps of every row at once, so calls of other
-    // step counts replay the same graphs
-    if (c->gexec) { HIPCHK(c, hipGraphExecDestroy(c->gexec)); c->gexec = nullptr; }
-    if (c->gexec_n) { HIPCHK(c, hipGraphExecDestroy(c->gexec_n)); c->gexec_n = nullptr; }
-    if (c->d_out) HIPCHK(c, hipFree(c->d_out));
-    c->d_out = nullptr;
-    c->out_cap = 0;
-    const size_t cap = std::max(need, (size_t)c->wb * kOutSteps);
-    HIPCHK(c, dalloc(&c->d_out, cap));
-    c->out_cap = cap;
-  }
-  HIPCHK(c, hipMemcpyAsync(c->d_seq, seq, 4 * n, hipMemcpyHostToDevice, c->st));
-  HIPCHK(c, hipMemcpyAsync(c->d_pos, pos, 4 * n, hipMemcpyHostToDevice, c->st));
-  HIPCHK(c, hipMemcpyAsync(c->d_tok, tok, 4 * n, hipMemcpyHostToDevice, c->st));
-  if (!greedy) HIPCHK(c, hipMemcpyAsync(c->d_rng, rng, 32 * n, hipMemcpyHostToDevice, c->st));
-  HIPCHK(c, launch_zero_u32(c->d_step, n, c->st));
+  if (int r = gen_inputs(c, n, seq, pos, tok, greedy, rng)) return r;
   c->attn_split = split_attention(c, n, pos, steps);
   const PickArgs pa = pick_args(c, n, greedy ? nullptr : s, 1);
   // capture `count` steps into a graph
@@ -986,7 +998,7 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
     hipGraph_t g = nullptr;
     HIPCHK(c, hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
     int r = 0;
-    for (uint32_t i = 0; i < count && !r; i++) r = gen_step(c, n, pa, greedy);
+    for (uint32_t i = 0; i < count && !r; i++) r = gen_step(c, n, pa, greedy, c->d_out, c->d_step);
     const hipError_t ec = hipStreamEndCapture(c->st, &g);
     if (r) { if (g) (void)hipGraphDestroy(g); return r; }
     HIPCHK(c, ec);
@@ -995,13 +1007,7 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
     HIPCHK(c, ei);
     return ANA_OK;
   };
-  if (c->prof) {
-    // launch by launch, each product timed by its own start/stop events
-    for (uint32_t k = 0; k < steps; k++) {
-      c->attn_bytes = attn_bytes_of(c, pos, n, k);
-      if (int r = gen_step(c, n, pa, greedy)) return r;
-    }
-  } else {
+  if (!c->prof) {
     ana_ctx::GKey key{n, pa.temp, pa.topp, pa.topk, c->d_out, c->attn_split};
     if (!c->gexec || !(c->gkey == key)) {
       if (c->gexec) { HIPCHK(c, hipGraphExecDestroy(c->gexec)); c->gexec = nullptr; }
@@ -1013,18 +1019,34 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
     // an agent loop's, never do)
     if (steps >= kGraphSteps && !c->gexec_n)
       if (int r = capture(kGraphSteps, &c->gexec_n)) return r;
-    uint32_t k = 0;
-    for (; k + kGraphSteps <= steps; k += kGraphSteps) HIPCHK(c, hipGraphLaunch(c->gexec_n, c->st));
-    for (; k < steps; k++) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
+  }
+  // pieces of at most kOutSteps steps: d_out (allocated at ana_open) holds
+  // one piece's picks, step-major; each piece's picks go to the caller
+  // before the next piece starts over at step 0
+  for (uint32_t k0 = 0; k0 < steps; k0 += kOutSteps) {
+    const uint32_t m = std::min(kOutSteps, steps - k0);
+    HIPCHK(c, launch_zero_u32(c->d_step, n, c->st));
+    if (c->prof) {
+      // launch by launch, each product timed by its own start/stop events
+      for (uint32_t k = 0; k < m; k++) {
+        c->attn_bytes = attn_bytes_of(c, pos, n, k0 + k);
+        if (int r = gen_step(c, n, pa, greedy, c->d_out, c->d_step)) return r;
+      }
+    } else {
+      uint32_t k = 0;
+      for (; k + kGraphSteps <= m; k += kGraphSteps) HIPCHK(c, hipGraphLaunch(c->gexec_n, c->st));
+      for (; k < m; k++) HIPCHK(c, hipGraphLaunch(c->gexec, c->st));
+    }
+    c->h_out.resize((size_t)n * m);
+    HIPCHK(c, hipMemcpyAsync(c->h_out.data(), c->d_out, 4 * (size_t)n * m, hipMemcpyDeviceToHost, c->st));
+    HIPCHK(c, hipStreamSynchronize(c->st));
+    // step-major on the device, row-major for the caller
+    for (uint32_t k = 0; k < m; k++)
+      for (uint32_t b = 0; b < n; b++) out[(size_t)b * steps + k0 + k] = c->h_out[(size_t)k * n + b];
   }
   HIPCHK(c, launch_scatter_rows(c->X, c->d_seq, n, c->cfg.d, c->xs, c->st));
-  c->h_out.resize(need);
-  HIPCHK(c, hipMemcpyAsync(c->h_out.data(), c->d_out, 4 * need, hipMemcpyDeviceToHost, c->st));
   if (!greedy) HIPCHK(c, hipMemcpyAsync(rng, c->d_rng, 32 * n, hipMemcpyDeviceToHost, c->st));
   HIPCHK(c, hipStreamSynchronize(c->st));
-  // step-major on the device, row-major for the caller
-  for (uint32_t k = 0; k < steps; k++)
-    for (uint32_t b = 0; b < n; b++) out[(size_t)b * steps + k] = c->h_out[(size_t)k * n + b];
   return ANA_OK;
 }
 
