@@ -77,6 +77,8 @@ SIGNATURES = {
     "ana_rng_seeded": (None, [C.c_uint64, _u64p]),
     "ana_generate": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p, _u32p, C.c_uint32,
                                C.POINTER(_Sampling), _u64p, _u32p]),
+    "ana_generate_noalloc": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p, _u32p, C.c_uint32,
+                                       C.POINTER(_Sampling), _u64p, _u32p]),
     "ana_state": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, _f32p, C.c_size_t]),
     "ana_prof": (C.c_int, [C.c_void_p, C.c_int]),
     "ana_prof_read": (C.c_int, [C.c_void_p, C.c_uint32, _u64p, C.POINTER(C.c_double), C.POINTER(C.c_double)]),

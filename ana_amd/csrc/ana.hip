@@ -11,6 +11,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -216,6 +217,7 @@ extern "C" void ana_rng_seeded(uint64_t seed, uint64_t r[4]) {
 }
 
 static hipError_t pack_weights(ana_ctx* c);
+static void resolve_scratch(int device);
 
 extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if (!path || !out) return fail(nullptr, ANA_EINVAL, "ana_open: null argument");
@@ -270,6 +272,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   };
   hipError_t e;
   if ((e = hipSetDevice(c->device)) != hipSuccess) return bad(e);
+  resolve_scratch(c->device);
   if ((e = hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking)) != hipSuccess) return bad(e);
   const uint64_t wb = c->wb;
   if ((e = dalloc(&c->W, c->P)) != hipSuccess) return bad(e);
@@ -1045,6 +1048,68 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
       for (uint32_t b = 0; b < n; b++) out[(size_t)b * steps + k0 + k] = c->h_out[(size_t)k * n + b];
   }
   HIPCHK(c, launch_scatter_rows(c->X, c->d_seq, n, c->cfg.d, c->xs, c->st));
+  if (!greedy) HIPCHK(c, hipMemcpyAsync(rng, c->d_rng, 32 * n, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  return ANA_OK;
+}
+
+// ------------------------------------------------------------------ no-allocation token loop
+//
+// ana_generate_noalloc's scratch: the rows' step counters, the step-major
+// picks and their row-major copy, in one file-scope device array that each
+// GPU holds for the life of the process. Host code uses its address as
+// hipGetSymbolAddress gives it on each device (g_scratch), never the
+// array's name.
+static constexpr uint32_t kNoAllocWords = 1u << 18;   // 1 MB of uint32
+static __device__ __align__(256) uint32_t scratch[kNoAllocWords];
+static constexpr int kMaxDevices = 64;
+static uint32_t* g_scratch[kMaxDevices] = {};
+static std::mutex g_scratch_mu;
+
+// once per device, with that device current (ana_open): scratch's device
+// address; an error here leaves only ana_generate_noalloc unavailable
+static void resolve_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[device]) return;
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess) g_scratch[device] = static_cast<uint32_t*>(p);
+}
+
+extern "C" int ana_generate_noalloc(ana_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+                                    const uint32_t* tok, uint32_t steps, const ana_sampling* s,
+                                    uint64_t* rng, uint32_t* out) {
+  if (!c) return ANA_EINVAL;
+  const char* fn = "ana_generate_noalloc";
+  if (int r = check_generate(c, fn, n, seq, pos, tok, steps, s, rng, out)) return r;
+  if (steps == 0) return ANA_OK;
+  const uint64_t cnt_words = ((uint64_t)n + 63) & ~63ull;
+  const uint64_t need = cnt_words + 2ull * n * steps;
+  if (need > kNoAllocWords)
+    return fail(c, ANA_EINVAL, "%s: %u sequences x %u steps need %llu scratch words, at most %u", fn, n, steps,
+                (unsigned long long)need, kNoAllocWords);
+  uint32_t* base = c->device >= 0 && c->device < kMaxDevices ? g_scratch[c->device] : nullptr;
+  if (!base) return fail(c, ANA_EDEVICE, "%s: no scratch address on device %d", fn, c->device);
+  uint32_t* d_step = base;
+  uint32_t* d_sm = base + cnt_words;
+  uint32_t* d_rm = d_sm + (size_t)n * steps;
+  const bool greedy = !s || s->temperature <= 0.0f;
+  HIPCHK(c, hipSetDevice(c->device));
+  if (int r = gen_inputs(c, n, seq, pos, tok, greedy, rng)) return r;
+  // the counters start at zero (the array keeps the last call's contents)
+  HIPCHK(c, launch_zero_u32(d_step, n, c->st));
+  c->attn_split = split_attention(c, n, pos, steps);
+  const PickArgs pa = pick_args(c, n, greedy ? nullptr : s, 1);
+  // no graphs and no timing events here: launch by launch
+  const bool prof = c->prof;
+  c->prof = false;
+  int r = ANA_OK;
+  for (uint32_t k = 0; k < steps && !r; k++) r = gen_step(c, n, pa, greedy, d_sm, d_step);
+  c->prof = prof;
+  if (r) return r;
+  HIPCHK(c, launch_scatter_rows(c->X, c->d_seq, n, c->cfg.d, c->xs, c->st));
+  HIPCHK(c, launch_picks_rows(d_sm, n, steps, d_rm, c->st));
+  HIPCHK(c, hipMemcpyAsync(out, d_rm, 4 * (size_t)n * steps, hipMemcpyDeviceToHost, c->st));
   if (!greedy) HIPCHK(c, hipMemcpyAsync(rng, c->d_rng, 32 * n, hipMemcpyDeviceToHost, c->st));
   HIPCHK(c, hipStreamSynchronize(c->st));
   return ANA_OK;

@@ -231,6 +231,8 @@ struct AdvanceArgs {
   uint32_t* last;                   // [B]: the pick, for ana_top-like readers
 };
 hipError_t launch_advance(const AdvanceArgs& a, hipStream_t st);
+// n x steps step-major picks (step k, row b at sm[k * n + b]) to row-major rm
+hipError_t launch_picks_rows(const uint32_t* sm, uint32_t n, uint32_t steps, uint32_t* rm, hipStream_t st);
 // greedy picks from amax keys (dd.top), vocab where there is none
 hipError_t launch_keys_to_tok(const unsigned long long* amax, uint32_t vocab, uint32_t B,
                               uint32_t* tok, hipStream_t st);

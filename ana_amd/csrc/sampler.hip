@@ -383,6 +383,22 @@ hipError_t launch_advance(const AdvanceArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// step-major picks (step k, row b at k * n + b) to row-major (b * steps + k)
+__global__ __launch_bounds__(256) void k_picks_rows(const uint32_t* __restrict__ sm, uint32_t n, uint32_t steps,
+                                                    uint32_t* __restrict__ rm) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (uint64_t)n * steps) return;
+  const uint32_t b = (uint32_t)(i / steps), k = (uint32_t)(i % steps);
+  rm[i] = sm[(size_t)k * n + b];
+}
+
+hipError_t launch_picks_rows(const uint32_t* sm, uint32_t n, uint32_t steps, uint32_t* rm, hipStream_t st) {
+  const uint64_t total = (uint64_t)n * steps;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_picks_rows, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, st, sm, n, steps, rm);
+  return hipGetLastError();
+}
+
 // Evaluate.bend's summand (window.go, bend/Evaluate.bend:33-44): G.lse of
 // the logits minus the target's logit, G.lse = V.max + F32.log(V.sum_exp)
 // (bend/Train/Grad.bend:795-797; bend/Tensor.bend:170-177,292-299) over the

@@ -150,6 +150,21 @@ int ana_generate(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, const uin
                  const uint32_t* tok, uint32_t steps, const ana_sampling* s, uint64_t* rng,
                  uint32_t* out);
 
+/* ana_generate for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference. Same arguments, semantics and results
+ * as ana_generate, but the call allocates nothing: it calls no hipMalloc or
+ * hipFree, captures no graph and records no timing events (kernels are
+ * launched one by one), and its scratch (the rows' step counters and
+ * picks) lives in a fixed device array of 2^18 words that each GPU holds
+ * until the process ends. A call needs 64 * ceil(n / 64) + 2 * n * steps
+ * words of it; larger calls fail with ANA_EINVAL. Every call on one GPU
+ * shares that array, whatever the context: calls that overlap on one GPU
+ * (from several threads) race. */
+int ana_generate_noalloc(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+                         const uint32_t* tok, uint32_t steps, const ana_sampling* s, uint64_t* rng,
+                         uint32_t* out);
+
 /* Copy one sequence's state out (for parity checks): layer l's GLA S
  * (heads x hd x hd floats) or K ring then V ring (2 x ctx x d floats); l ==
  * layers gives the residual row (d floats). n is the float count of out. */
