@@ -316,7 +316,7 @@ class Decoder:
                                        _p(t, C.c_uint32), steps, sp, rp, _p(out, C.c_uint32)))
         return out
 
-    KINDS = ("gemv", "head", "attn", "gla", "pick")
+    KINDS = ("gemv", "head", "attn", "gla", "pick", "step")
 
     def prof(self, on: bool) -> None:
         """Start (and clear) or stop per-launch event timing."""

@@ -7,6 +7,7 @@
 // row of its last fed token, which the head reads (the store's x cell in
 // bend/Dense/Decode.bend).
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -68,6 +69,16 @@ struct ana_ctx {
     int bf;                          // packed as bf16 (else fp32)
   };
   std::unordered_map<const float*, PkEnt> pk;
+  // the persistent one-sequence decode (ANA_FAST_FP32): its layer table,
+  // exchange entries (two sets of ll_par), control words, grid and the
+  // epoch its next launch starts from
+  bool persist = false, persist_off = false;
+  uint32_t pG = 0, pnp = 0;
+  PLayer* d_play = nullptr;
+  unsigned long long* d_ll = nullptr;
+  uint64_t ll_par = 0, e_key = 0;
+  uint32_t* d_ctl = nullptr;
+  uint32_t epoch = 0;
   float* d_gla = nullptr;            // fast prefill's GLA scan scratch
   GlaScratch gla{};                  // its regions
   GlaSub* d_gtab = nullptr;          // a prefill step's sub-chunk table
@@ -179,7 +190,7 @@ static void release(ana_ctx* c) {
   (void)hipSetDevice(c->device);
   if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
   if (c->gexec_n) (void)hipGraphExecDestroy(c->gexec_n);
-  void* ps[] = {c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
+  void* ps[] = {c->d_play, c->d_ll, c->d_ctl, c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
                 c->d_ss, c->d_pm, c->d_gtab, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce,
                 c->d_sah, c->d_sal, c->d_rsc, c->PK};
@@ -217,6 +228,7 @@ extern "C" void ana_rng_seeded(uint64_t seed, uint64_t r[4]) {
 }
 
 static hipError_t pack_weights(ana_ctx* c);
+static hipError_t persist_setup(ana_ctx* c);
 static void resolve_scratch(int device);
 
 extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
@@ -320,6 +332,9 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = launch_bswap(reinterpret_cast<uint32_t*>(c->W), c->P, c->st)) != hipSuccess) return bad(e);
   if (c->Wh && (e = launch_to_bf16(c->W, c->Wh, c->P, c->st)) != hipSuccess) return bad(e);
   if (c->mode != ANA_EXACT_FP32 && (e = pack_weights(c)) != hipSuccess) return bad(e);
+  if (c->mode == ANA_FAST_FP32 && (e = persist_setup(c)) != hipSuccess) return bad(e);
+  // ANA_PERSIST=0 keeps one-sequence decode on the captured graphs
+  if (const char* pv = getenv("ANA_PERSIST")) c->persist_off = strcmp(pv, "0") == 0;
   if ((e = launch_zero(c->state, c->seq_stride * c->max_seqs, c->st)) != hipSuccess) return bad(e);
   if ((e = launch_zero(c->xs, (uint64_t)d * c->max_seqs, c->st)) != hipSuccess) return bad(e);
   if ((e = hipStreamSynchronize(c->st)) != hipSuccess) return bad(e);
@@ -480,6 +495,63 @@ static void layer_products(const ana_ctx* c, uint32_t l, GemvArgs p[4]) {
   p[P_GU].ng = W + b.rf;
   p[P_WD] = gemv1(c->HH, f, f, W + b.wd, d, c->X, d, 0);
   p[P_WD].mode = GM_RESID; p[P_WD].R = c->XA; p[P_WD].ldr = d;
+}
+
+// The persistent one-sequence decode's tables, when the kernel takes this
+// model on this device's CUs (one workgroup a CU): each layer's parameter
+// offsets and exchange slots, two sets of exchange entries, control words.
+static hipError_t persist_setup(ana_ctx* c) {
+  const ana_config& cf = c->cfg;
+  hipDeviceProp_t pr;
+  hipError_t e = hipGetDeviceProperties(&pr, c->device);
+  if (e != hipSuccess) return e;
+  int coop = 0;
+  if ((e = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->device)) != hipSuccess) return e;
+  const uint32_t G = (uint32_t)std::min(pr.multiProcessorCount, 256);
+  if (!coop || !decode1_fits(cf, G)) return hipSuccess;
+  const uint32_t d = cf.d, f = cf.f, hd = d / cf.heads, np = decode1_pieces(cf, G);
+  std::vector<PLayer> t(cf.layers);
+  uint64_t en = 0;
+  for (uint32_t l = 0; l < cf.layers; l++) {
+    const Blk& b = c->blk[l];
+    PLayer& P = t[l];
+    P.ra = b.ra; P.wq = b.wq; P.wa = b.wa; P.lam = b.lam; P.gq = b.gq; P.gk = b.gk; P.sink = b.sink;
+    P.wo = b.wo; P.rf = b.rf; P.wg = b.wg; P.wd = b.wd;
+    P.soff = c->layer_off[l];
+    P.gla = b.gla ? 1u : 0u;
+    P.e_qkv = en; en += (b.gla ? 4ull : 3ull) * d;
+    if (!b.gla) { P.e_part = en; en += (uint64_t)cf.heads * np * (hd + 2); }
+    P.e_o = en; en += d;
+    P.e_xa = en; en += d;
+    P.e_hh = en; en += f;
+    P.e_x = en; en += d;
+  }
+  c->e_key = en;
+  en += G;
+  c->ll_par = (en + 63) & ~63ull;
+  if ((e = dalloc(&c->d_play, cf.layers)) != hipSuccess) return e;
+  if ((e = dalloc(&c->d_ll, 2 * c->ll_par)) != hipSuccess) return e;
+  if ((e = dalloc(&c->d_ctl, 4)) != hipSuccess) return e;
+  if ((e = hipMemcpyAsync(c->d_play, t.data(), sizeof(PLayer) * t.size(), hipMemcpyHostToDevice, c->st)) != hipSuccess)
+    return e;
+  if ((e = launch_zero_u64(c->d_ll, (uint32_t)(2 * c->ll_par), c->st)) != hipSuccess) return e;
+  c->pG = G;
+  c->pnp = np;
+  c->persist = true;
+  return hipSuccess;
+}
+
+// algorithmic bytes of one decode step of one sequence: every weight once
+// (the head reads all of the tied embedding), the GLA states read and
+// written, the live K and V rows read and the new ones written
+static double step_bytes(const ana_ctx* c, uint64_t pos) {
+  const ana_config& cf = c->cfg;
+  const double hd = (double)cf.d / cf.heads;
+  double b = 4.0 * (double)(c->P - (uint64_t)cf.vocab * cf.d + cf.d) + 4.0 * cf.vocab * cf.d;
+  const uint64_t live = std::min<uint64_t>(pos, cf.ctx - 1) + 1;
+  for (uint32_t l = 0; l < cf.layers; l++)
+    b += c->blk[l].gla ? 8.0 * cf.heads * hd * hd : 4.0 * cf.d * (2.0 * live + 2.0);
+  return b;
 }
 
 // every layer product's packed weights and the head's (final norm, tied
@@ -985,6 +1057,82 @@ static int gen_inputs(ana_ctx* c, uint32_t n, const uint32_t* seq, const uint32_
   return ANA_OK;
 }
 
+// ana_generate of one greedy sequence in the fast fp32 mode: the token
+// loop as persistent launches (pieces of kOutSteps steps; a step whose
+// logits have no maximum ends a launch, and k_advance picks it by
+// Sample.argmax before the next). Returns ANA_EUNSUP, having run nothing,
+// when the launch itself is refused (the caller then takes the graphs).
+static int generate_persist(ana_ctx* c, const uint32_t* pos, uint32_t steps, uint32_t* out) {
+  uint32_t ctl[4];
+  for (uint32_t k0 = 0; k0 < steps; k0 += kOutSteps) {
+    const uint32_t m = std::min(kOutSteps, steps - k0);
+    HIPCHK(c, launch_zero_u32(c->d_step, 1, c->st));
+    uint32_t done = 0;
+    while (done < m) {
+      HIPCHK(c, launch_zero_u32(c->d_ctl, 4, c->st));
+      PersistArgs pa{};
+      pa.W = c->W;
+      pa.lay = c->d_play;
+      pa.L = c->cfg.layers; pa.d = c->cfg.d; pa.f = c->cfg.f; pa.heads = c->cfg.heads; pa.ctx = c->cfg.ctx;
+      pa.vocab = c->cfg.vocab; pa.rglru = c->cfg.rglru; pa.qk = c->cfg.qk; pa.sinks = c->cfg.sinks;
+      pa.np = c->pnp;
+      pa.fin = c->fin;
+      pa.state = c->state; pa.seq_stride = c->seq_stride;
+      pa.X = c->X; pa.LG = c->LG;
+      pa.seq = c->d_seq; pa.pos = c->d_pos; pa.tok = c->d_tok; pa.out = c->d_out; pa.step = c->d_step;
+      pa.pick = c->d_pick;
+      pa.steps = m - done;
+      pa.ll = c->d_ll; pa.ll_par = c->ll_par; pa.e_key = c->e_key;
+      pa.epoch0 = c->epoch;
+      pa.ctl = c->d_ctl;
+      hipError_t e;
+      {
+        double by = 0.0;
+        if (c->prof)
+          for (uint32_t k = done; k < m; k++) by += step_bytes(c, (uint64_t)pos[0] + k0 + k);
+        ProfScope ps(c, ANA_K_STEP, by);
+        e = launch_decode1(pa, c->pG, c->st);
+      }
+      if (e != hipSuccess) {
+        if (k0 == 0 && done == 0) {
+          (void)hipGetLastError();
+          return ANA_EUNSUP;
+        }
+        return fail(c, ANA_EDEVICE, "device fault: %s (persistent decode launch)", hipGetErrorString(e));
+      }
+      HIPCHK(c, hipMemcpyAsync(ctl, c->d_ctl, sizeof ctl, hipMemcpyDeviceToHost, c->st));
+      HIPCHK(c, hipStreamSynchronize(c->st));
+      // the next launch's entries never carry an epoch this one wrote
+      c->epoch += (m - done) + 2;
+      if (ctl[0] || ctl[1])
+        return fail(c, ANA_EDEVICE, "device fault: a persistent decode wait ran out (step %u of the call)", k0 + done + ctl[2]);
+      done += ctl[2];
+      if (ctl[3]) {
+        // no logit reached the maximum: Sample.argmax over the stored logits
+        AdvanceArgs ad{};
+        ad.logits = c->LG;
+        ad.vocab = c->cfg.vocab;
+        ad.B = 1;
+        ad.pick = c->d_pick;
+        ad.greedy = 1;
+        ad.pos = c->d_pos;
+        ad.tok = c->d_tok;
+        ad.out = c->d_out;
+        ad.step = c->d_step;
+        HIPCHK(c, launch_advance(ad, c->st));
+        done += 1;
+      }
+    }
+    c->h_out.resize(m);
+    HIPCHK(c, hipMemcpyAsync(c->h_out.data(), c->d_out, 4 * (size_t)m, hipMemcpyDeviceToHost, c->st));
+    HIPCHK(c, hipStreamSynchronize(c->st));
+    for (uint32_t k = 0; k < m; k++) out[k0 + k] = c->h_out[k];
+  }
+  HIPCHK(c, launch_scatter_rows(c->X, c->d_seq, 1, c->cfg.d, c->xs, c->st));
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  return ANA_OK;
+}
+
 extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* pos,
                             const uint32_t* tok, uint32_t steps, const ana_sampling* s,
                             uint64_t* rng, uint32_t* out) {
@@ -994,6 +1142,11 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
   const bool greedy = !s || s->temperature <= 0.0f;
   HIPCHK(c, hipSetDevice(c->device));
   if (int r = gen_inputs(c, n, seq, pos, tok, greedy, rng)) return r;
+  if (n == 1 && greedy && c->persist && !c->persist_off) {
+    const int r = generate_persist(c, pos, steps, out);
+    if (r != ANA_EUNSUP) return r;
+    c->persist = false;   // refused (resources): the graphs from now on
+  }
   c->attn_split = split_attention(c, n, pos, steps);
   const PickArgs pa = pick_args(c, n, greedy ? nullptr : s, 1);
   // capture `count` steps into a graph

@@ -328,4 +328,39 @@ hipError_t launch_attn_flash(const AttnArgs& a, const AttnTile* tab, uint32_t nt
 hipError_t launch_zero_u32(uint32_t* p, uint32_t n, hipStream_t st);
 hipError_t launch_zero_u64(unsigned long long* p, uint32_t n, hipStream_t st);
 
+// ---------------------------------------------------------------- persistent B = 1 decode
+// The fast fp32 token loop of one sequence in one cooperative launch: one
+// workgroup a CU runs every phase of every step, phases exchanging their
+// outputs as 8-byte (value, epoch) entries. Per layer: parameter offsets
+// (floats into the parameter vector), the layer's offset in a sequence's
+// state, and its exchange slots (entries into one parity's set).
+struct PLayer {
+  uint64_t ra, wq, wa, lam, gq, gk, sink, wo, rf, wg, wd;
+  uint64_t soff;
+  uint64_t e_qkv, e_part, e_o, e_xa, e_hh, e_x;
+  uint32_t gla, pad;
+};
+struct PersistArgs {
+  const float* W;
+  const PLayer* lay;        // [L], device
+  uint32_t L, d, f, heads, ctx, vocab, rglru, qk, sinks, np;  // np: attention pieces a head
+  uint64_t fin;             // the final norm's gains
+  float* state;
+  uint64_t seq_stride;
+  float* X;                 // out: the last fed token's residual row
+  float* LG;                // out: the last step's logits
+  const uint32_t* seq;      // [1]
+  uint32_t *pos, *tok, *out, *step, *pick;   // as ana_generate's step (out step-major)
+  uint32_t steps;
+  unsigned long long* ll;   // two sets of ll_par entries
+  uint64_t ll_par, e_key;   // entries a set; the head's keys (one a workgroup)
+  uint32_t epoch0;          // step k of the launch tags its entries epoch0 + k + 1
+  uint32_t* ctl;            // [0] a wait ran out, [1] abort, [2] steps picked, [3] stopped on NaN
+};
+// pieces of the ring a head's attention takes (one workgroup each)
+uint32_t decode1_pieces(const ana_config& c, uint32_t G);
+// whether the persistent kernel takes this configuration on G workgroups
+bool decode1_fits(const ana_config& c, uint32_t G);
+hipError_t launch_decode1(const PersistArgs& a, uint32_t G, hipStream_t st);
+
 }  // namespace ana

@@ -433,13 +433,14 @@ def test_generate_calls_of_any_length(ckpts, sampled, mode):
     its own): calls of 5, 9, 1 and 11 steps, each from where the last
     stopped with the RNG state handed back, give the tokens of one 26-step
     call on a twin decoder, bit for bit, greedy and sampled; so do 7 and 6
-    rows (a capture per row count)."""
+    rows (a capture per row count), and one row (in fast_fp32 the persistent
+    one-sequence loop, whose state and exchange epochs carry across calls)."""
     print(f"case generate calls of any length mode {mode} sampled {sampled}", flush=True)
     path = ckpts["v3-trained"]
     lens = [5, 9, 1, 11]
     total = sum(lens)
     st = ana_amd.Settings(float(np.float32(0.8)), 40, float(np.float32(0.9))) if sampled else None
-    for n in (7, 6):
+    for n in (7, 6, 1):
         seqs = list(range(n))
         rng0 = np.stack([ana_amd.rng_seeded(50 + s) for s in seqs]).astype(np.uint64) if sampled else None
         prompts = [VEC["window"][3 * i: 3 * i + 4 + i] for i in seqs]
