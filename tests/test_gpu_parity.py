@@ -368,6 +368,40 @@ def test_score_n_bit_exact(oracle, ckpts, name):
     assert w == np.float32(acc / np.float32(got[3].size))
 
 
+@pytest.mark.parametrize("name", list(CFGS))
+def test_score_n_tree_engine(oracle, ckpts, name):
+    """ana_score_n against the engine Evaluate.bend really scores with:
+    window.go calls Md.decode, the tree meaning (bend/Evaluate.bend:33-42),
+    while ana_score_n is bit-exact with the dense engine. One window of 90
+    tokens (past the ring's wrap at ctx 64) scored on the device, against
+    G.lse - logit[next] on the oracle's tree step (or_tree_step) at every
+    position. The dense and tree logits agree within 1e-5 of the largest
+    |logit| (decode-dense.bend's law), and a summand moves by at most twice
+    that (lse and logit[next] each by at most the logits' difference), so
+    each summand is held within 2e-5 of that position's largest |logit|,
+    and the window means within the largest of those bounds."""
+    path = ckpts[name]
+    print(f"case score_n tree engine {name}", flush=True)
+    m = oracle.Model(path)
+    toks = np.array(VEC["window"][:90], np.uint32)
+    with ana_amd.Decoder(path, max_seqs=1, prefill_chunk=16) as dec:
+        got = dec.score_n([0], [0], [toks])[0]
+    tr = oracle.Tree(m)
+    worst, bounds, want = 0.0, [], []
+    for k in range(toks.size - 1):
+        lg = tr.step(k, int(toks[k]))
+        want.append(oracle.ce(lg, int(toks[k + 1])))
+        bound = 2e-5 * float(np.abs(lg).max())
+        bounds.append(bound)
+        d = abs(float(got[k]) - want[-1])
+        worst = max(worst, d / bound)
+        assert d <= bound, (k, float(got[k]), want[-1], bound)
+    print(f"worst summand difference {worst:.3f} of its bound", flush=True)
+    # window.mean on each engine's summands (F32 in order, over the count)
+    d = abs(float(ana_amd.window_mean(got)) - float(ana_amd.window_mean(np.array(want, np.float32))))
+    assert d <= max(bounds), (d, max(bounds))
+
+
 def test_text_end_to_end(oracle, tmp_path):
     """Text in, text out: a checkpoint naming its tokenizer by identity
     (a synthetic artifact of 42 merges; model vocab 300); the manifest read,
