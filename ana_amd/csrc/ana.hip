@@ -56,7 +56,7 @@ struct ana_ctx {
   uint32_t sc_rows = 1;
   uint32_t* d_tgt = nullptr;         // scoring: each row's target token
   float* d_ce = nullptr;             // scoring: each row's G.lse - logit[target]
-  __bf16 *d_sah = nullptr, *d_sal = nullptr;  // ANA_BF16 prefill: a product's split activations
+  __bf16* d_sah = nullptr;   // ANA_BF16 prefill: a product's activations in bf16
   float* d_rsc = nullptr;                      // and its rows' norm scales
   // fast modes: every layer product's weights packed for k_gemm_pk (fp32, or
   // bf16 in ANA_BF16; the norm gains folded in), found by the product's first
@@ -193,7 +193,7 @@ static void release(ana_ctx* c) {
   void* ps[] = {c->d_play, c->d_ll, c->d_ctl, c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
                 c->d_ss, c->d_pm, c->d_gtab, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce,
-                c->d_sah, c->d_sal, c->d_rsc, c->PK};
+                c->d_sah, c->d_rsc, c->PK};
   for (void* p : ps)
     if (p) (void)hipFree(p);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
@@ -325,7 +325,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if (c->mode == ANA_BF16) {
     const uint64_t kmax = std::max(d, cf.f);
     if ((e = dalloc(&c->Wh, c->P)) != hipSuccess || (e = dalloc(&c->d_sah, (uint64_t)c->rows * kmax)) != hipSuccess ||
-        (e = dalloc(&c->d_sal, (uint64_t)c->rows * kmax)) != hipSuccess || (e = dalloc(&c->d_rsc, c->rows)) != hipSuccess)
+        (e = dalloc(&c->d_rsc, c->rows)) != hipSuccess)
       return bad(e);
   }
   if ((e = hipMemcpyAsync(c->W, ck.raw.data(), 4 * c->P, hipMemcpyHostToDevice, c->st)) != hipSuccess) return bad(e);
@@ -451,7 +451,7 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
     if (pe)
       return launch_gemm_pk(g, static_cast<const char*>(c->PK) + pe->off, pe->bf, c->st, ps.start(), ps.stop());
     if (g.B >= 128 && c->d_sah && bf && g.K % 32 == 0 && g.B <= c->rows)
-      return launch_gemm_dl(g, c->d_sah, c->d_sal, c->d_rsc, c->rows, c->st, ps.start(), ps.stop());
+      return launch_gemm_dl(g, c->d_sah, c->d_rsc, c->rows, c->st, ps.start(), ps.stop());
     if (g.B >= 128) return launch_gemm_big(g, c->st, ps.start(), ps.stop());
     return launch_gemm_mfma(g, c->st, ps.start(), ps.stop());
   }

@@ -310,11 +310,11 @@ hipError_t launch_head_pw(const GemvArgs& a, const void* pk, int bf, hipStream_t
 // the same for 128 rows or more, 128 x 128 tiles
 hipError_t launch_gemm_big(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nullptr,
                            hipEvent_t e1 = nullptr);
-// ANA_BF16 at 128 rows or more: the activations split into bf16 head and
-// remainder (Ah, Al: B x K each; rsc: B norm scales), then the product with
+// ANA_BF16 at 128 rows or more: the activations (times the norm's gain)
+// rounded to bf16 (Ah: B x K; rsc: B norm scales), then the product with
 // both operands streamed straight into LDS (K a multiple of 32)
-// (cap_rows: the rows Ah, Al and rsc hold; larger batches are rejected)
-hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, __bf16* Al, float* rsc, uint32_t cap_rows,
+// (cap_rows: the rows Ah and rsc hold; larger batches are rejected)
+hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t cap_rows,
                           hipStream_t st, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 size_t attn_fast_part_floats(uint32_t B, uint32_t heads, uint32_t ctx, uint32_t hd);
 // causal attention of fresh prefill rows on the matrix cores: one workgroup

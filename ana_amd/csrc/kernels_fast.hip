@@ -1024,8 +1024,7 @@ namespace ana {
 // Y[m][n] = sum_k X[m][k] W[n][k] on the matrix cores. A workgroup owns 16
 // weight rows (n) and 64 batch rows (m); wave w computes the 16 x 16 tile
 // of batch rows 16w.. with v_mfma_f32_16x16x32_bf16 (ANA_BF16: bf16
-// weights; each activation split into a bf16 head and a bf16 remainder,
-// x = hi + lo to ~16 bits, two products per step) or v_mfma_f32_16x16x4f32
+// weights and activations rounded to bf16) or v_mfma_f32_16x16x4f32
 // (ANA_FAST_FP32). K goes in
 // chunks of 64 through a ring of D register sets (D - 1 chunks in flight)
 // and two LDS buffers. With `ng` the chunk is staged as x * g and each
@@ -1038,7 +1037,6 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemvArgs a) {
   constexpr int XP = BK + 8;             // LDS row pitch (elements), bf16 or f32
   using E = typename std::conditional<WT == 1, __bf16, float>::type;
   __shared__ __align__(16) E Xs[2][BM][XP];
-  __shared__ __align__(16) __bf16 Xl[WT == 1 ? 2 : 1][WT == 1 ? BM : 1][WT == 1 ? XP : 8];
   __shared__ __align__(16) E Ws[2][BN][XP];
   __shared__ float ssp[4][BM];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -1096,13 +1094,6 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemvArgs a) {
       dst[1] = (E)x.y;
       dst[2] = (E)x.z;
       dst[3] = (E)x.w;
-      if constexpr (WT == 1) {
-        __bf16* lo = &Xl[buf][xm][xk + 4 * j];
-        lo[0] = (__bf16)(x.x - (float)dst[0]);
-        lo[1] = (__bf16)(x.y - (float)dst[1]);
-        lo[2] = (__bf16)(x.z - (float)dst[2]);
-        lo[3] = (__bf16)(x.w - (float)dst[3]);
-      }
     }
     const uint32_t q = q0 + wk;
     if constexpr (WT == 1) {
@@ -1134,9 +1125,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemvArgs a) {
 #pragma unroll
           for (int ks = 0; ks < BK; ks += 32) {
             const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(&Xs[buf][am][ks + 8 * g4]);
-            const bf16x8_t al = *reinterpret_cast<const bf16x8_t*>(&Xl[buf][am][ks + 8 * g4]);
             const bf16x8_t bv = *reinterpret_cast<const bf16x8_t*>(&Ws[buf][lane & 15][ks + 8 * g4]);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bv, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
           }
         } else {
@@ -1271,7 +1260,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 // compile time) and reads the step's x with no barrier. MFMA operands: lane
 // l holds row l % 16 of x and of the tile at k = 8 (l / 16) + e of the step;
 // fp32 (WT 0) takes v_mfma_f32_16x16x4f32 once per e, bf16 (WT 1) one
-// v_mfma_f32_16x16x32_bf16 on the x head and one on its remainder. With `ng`
+// v_mfma_f32_16x16x32_bf16 on x rounded to bf16. With `ng`
 // each wave also sums its rows' x^2 from the same fragments. Waves 1..3 hand
 // their partial tiles and sums to wave 0, which adds them in wave order and
 // applies the norm scale 1/sqrt(ss/K + 1e-5) and the epilogue (plain,
@@ -1361,16 +1350,12 @@ __global__ __launch_bounds__(256) void k_gemm_pw(GemvArgs a, const uint4* __rest
         for (int e = 0; e < 8; e++) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[e], w[e], acc[j], 0, 0, 0);
       }
     } else {
-      bf16x8_t hi, lo;
+      bf16x8_t hi;
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        hi[e] = (__bf16)x[e];
-        lo[e] = (__bf16)(x[e] - (float)hi[e]);
-      }
+      for (int e = 0; e < 8; e++) hi[e] = (__bf16)x[e];
 #pragma unroll
       for (int j = 0; j < NT; j++) {
         const bf16x8_t wb8 = __builtin_bit_cast(bf16x8_t, wr[s % D][j][0]);
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, wb8, acc[j], 0, 0, 0);
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, wb8, acc[j], 0, 0, 0);
       }
     }
@@ -1516,14 +1501,10 @@ __global__ __launch_bounds__(64 * NW) void k_head_pw(GemvArgs a, const uint4* __
 #pragma unroll
           for (int e = 0; e < 8; e++) acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[e], w[e], acc[tt], 0, 0, 0);
         } else {
-          bf16x8_t hi, lo;
+          bf16x8_t hi;
 #pragma unroll
-          for (int e = 0; e < 8; e++) {
-            hi[e] = (__bf16)x[e];
-            lo[e] = (__bf16)(x[e] - (float)hi[e]);
-          }
+          for (int e = 0; e < 8; e++) hi[e] = (__bf16)x[e];
           const bf16x8_t wb8 = __builtin_bit_cast(bf16x8_t, cw[u][0]);
-          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, wb8, acc[tt], 0, 0, 0);
           acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, wb8, acc[tt], 0, 0, 0);
         }
       }
@@ -1938,8 +1919,8 @@ namespace ana {
 // 128 tile per workgroup, four waves in 2 x 2 each computing 64 x 64 as
 // 4 x 4 MFMA 16 x 16 tiles. K goes in stages of BK through two LDS buffers,
 // the next stage's global loads in registers while the current one is
-// multiplied. ANA_BF16: v_mfma_f32_16x16x32_bf16 on the bf16 weights with
-// each activation as a bf16 head and remainder (two products a step);
+// multiplied. ANA_BF16: v_mfma_f32_16x16x32_bf16 on the bf16 weights and
+// the activations rounded to bf16;
 // ANA_FAST_FP32: v_mfma_f32_16x16x4f32. Norm, residual and SiLU as in
 // k_gemm_mfma (SiLU: tile rows 0..63 gate j, 64..127 up j).
 template <int WT>
@@ -1948,7 +1929,6 @@ __global__ __launch_bounds__(256) void k_gemm_big(GemvArgs a) {
   constexpr int AP = BK + 8;                      // LDS row pitch (elements)
   using E = typename std::conditional<WT == 1, __bf16, float>::type;
   __shared__ __align__(16) E As[2][BM][AP];
-  __shared__ __align__(16) __bf16 Al[WT == 1 ? 2 : 1][WT == 1 ? BM : 1][WT == 1 ? AP : 8];
   __shared__ __align__(16) E Bs[2][BN][AP];
   __shared__ float rsc[BM];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -2026,13 +2006,6 @@ __global__ __launch_bounds__(256) void k_gemm_big(GemvArgs a) {
       dst[1] = (E)x.y;
       dst[2] = (E)x.z;
       dst[3] = (E)x.w;
-      if constexpr (WT == 1) {
-        __bf16* lo = &Al[buf][am_[j]][ak_[j]];
-        lo[0] = (__bf16)(x.x - (float)dst[0]);
-        lo[1] = (__bf16)(x.y - (float)dst[1]);
-        lo[2] = (__bf16)(x.z - (float)dst[2]);
-        lo[3] = (__bf16)(x.w - (float)dst[3]);
-      }
     }
 #pragma unroll
     for (int j = 0; j < BV; j++) {
@@ -2061,21 +2034,16 @@ __global__ __launch_bounds__(256) void k_gemm_big(GemvArgs a) {
     const int buf = s & 1;
     if (s + 1 < nst) load(s + 1);
     if constexpr (WT == 1) {
-      bf16x8_t bfr[4], ah[4], al[4];
+      bf16x8_t bfr[4], ah[4];
 #pragma unroll
       for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[buf][wn * 64 + 16 * j + r16][8 * g4]);
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        ah[i] = *reinterpret_cast<const bf16x8_t*>(&As[buf][wm * 64 + 16 * i + r16][8 * g4]);
-        al[i] = *reinterpret_cast<const bf16x8_t*>(&Al[buf][wm * 64 + 16 * i + r16][8 * g4]);
-      }
+      for (int i = 0; i < 4; i++) ah[i] = *reinterpret_cast<const bf16x8_t*>(&As[buf][wm * 64 + 16 * i + r16][8 * g4]);
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bfr[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 4; j++)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bfr[j], acc[i][j], 0, 0, 0);
-        }
     } else {
       float4 bfr[4], afr[4];
 #pragma unroll
@@ -2203,14 +2171,13 @@ namespace ana {
 
 // ------------------------------------------------------------------ bf16 prefill products, direct to LDS
 
-// The activations of an ANA_BF16 prefill product as two bf16 arrays: each
-// value (times the norm's gain) rounded to nearest even (the head) and what
-// is left of it (the remainder); with a gain, also each row's norm scale
-// 1 / sqrt(ss / K + 1e-5) over the unscaled row. One wave a row.
+// The activations of an ANA_BF16 prefill product as bf16: each value
+// (times the norm's gain) rounded to nearest even; with a gain, also each
+// row's norm scale 1 / sqrt(ss / K + 1e-5) over the unscaled row. One wave
+// a row.
 __global__ __launch_bounds__(256) void k_split(const float* __restrict__ X, uint32_t ldx, uint32_t K,
                                                 const float* __restrict__ g, uint32_t M,
-                                                __bf16* __restrict__ Ah, __bf16* __restrict__ Al,
-                                                float* __restrict__ rsc) {
+                                                __bf16* __restrict__ Ah, float* __restrict__ rsc) {
   const uint32_t m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (m >= M) return;
   const float* x = X + (size_t)m * ldx;
@@ -2226,10 +2193,7 @@ __global__ __launch_bounds__(256) void k_split(const float* __restrict__ X, uint
       v.w *= gg.w;
     }
     __bf16 h[4] = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
-    __bf16 l[4] = {(__bf16)(v.x - (float)h[0]), (__bf16)(v.y - (float)h[1]), (__bf16)(v.z - (float)h[2]),
-                   (__bf16)(v.w - (float)h[3])};
     *reinterpret_cast<uint2*>(Ah + (size_t)m * K + k) = *reinterpret_cast<const uint2*>(h);
-    *reinterpret_cast<uint2*>(Al + (size_t)m * K + k) = *reinterpret_cast<const uint2*>(l);
   }
   if (g) {
     ss = wave_sum(ss);
@@ -2250,12 +2214,11 @@ __device__ __forceinline__ void xcd_tile(uint32_t* nt, uint32_t* mt) {
 }
 
 // Y[m][n] = sum_k A[m][k] W[n][k] for ANA_BF16 prefill steps of >= 128 rows,
-// A given as split head and remainder (k_split): a 128 x 128 tile per
-// workgroup, four waves of 64 x 64 (4 x 4 v_mfma_f32_16x16x32_bf16 tiles,
-// head then remainder each step). K goes in stages of 32 through a ring of
-// NS LDS stages filled by global_load_lds_dwordx4 (no registers between
-// global memory and LDS): each stage holds the head, remainder and weight
-// tiles as 1 KB chunks of 16 rows, a row's four 16-byte k pieces at
+// A given as bf16 (k_split): a 128 x 128 tile per workgroup, four waves of
+// 64 x 64 (4 x 4 v_mfma_f32_16x16x32_bf16 tiles). K goes in stages of 32
+// through a ring of NS LDS stages filled by global_load_lds_dwordx4 (no
+// registers between global memory and LDS): each stage holds the A and
+// weight tiles as 1 KB chunks of 16 rows, a row's four 16-byte k pieces at
 // physical slot (piece ^ ((row >> 1) & 3)), so a fragment read touches
 // eight distinct 16-byte bank groups. A wave waits on its own loads of the
 // stage it is about to read, then a barrier (no fence, which would wait on
@@ -2265,11 +2228,10 @@ __device__ __forceinline__ void xcd_tile(uint32_t* nt, uint32_t* mt) {
 // k_gemm_big.
 template <int NS>
 __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __restrict__ Ahg,
-                                                  const __bf16* __restrict__ Alg,
                                                   const float* __restrict__ rscg) {
   constexpr int BM = 128, BN = 128, BK = 32;
   constexpr int TILE = BM * BK;   // bf16 elements of one operand tile (8 KB)
-  __shared__ __align__(1024) __bf16 lds[NS][3][TILE];
+  __shared__ __align__(1024) __bf16 lds[NS][2][TILE];
   __shared__ float rsl[BM];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint32_t wm = wv >> 1, wn = wv & 1;
@@ -2300,8 +2262,7 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
     for (int h = 0; h < 2; h++) {
       const uint32_t c = 2 * wv + h;
       __builtin_amdgcn_global_load_lds((const void*)(Ahg + aoff[h] + k0), (lds_void*)&lds[buf][0][c * 512], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(Alg + aoff[h] + k0), (lds_void*)&lds[buf][1][c * 512], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(bptr[h] + k0), (lds_void*)&lds[buf][2][c * 512], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(bptr[h] + k0), (lds_void*)&lds[buf][1][c * 512], 16, 0, 0);
     }
   };
   f32x4_t acc[4][4];
@@ -2316,31 +2277,25 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
   for (int u = 0; u < NS - 1; u++)
     if ((uint32_t)u < nst) issue(u);
   for (uint32_t s = 0; s < nst; s++) {
-    // this wave's loads of stage s are done (6 loads a stage; those of the
+    // this wave's loads of stage s are done (4 loads a stage; those of the
     // NS - 2 later stages may still fly)
-    if (s + NS - 2 < nst) ANA_VMCNT(6 * (NS - 2));
+    if (s + NS - 2 < nst) ANA_VMCNT(4 * (NS - 2));
     else ANA_VMCNT(0);
     __builtin_amdgcn_s_barrier();
     if (s + NS - 1 < nst) issue(s + NS - 1);
     const int buf = s % NS;
     const __bf16* A0 = &lds[buf][0][0];
-    const __bf16* A1 = &lds[buf][1][0];
-    const __bf16* B0 = &lds[buf][2][0];
-    bf16x8_t bfr[4], ah[4], al[4];
+    const __bf16* B0 = &lds[buf][1][0];
+    bf16x8_t bfr[4], ah[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(B0 + (wn * 4 + j) * 512 + foff);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      ah[i] = *reinterpret_cast<const bf16x8_t*>(A0 + (wm * 4 + i) * 512 + foff);
-      al[i] = *reinterpret_cast<const bf16x8_t*>(A1 + (wm * 4 + i) * 512 + foff);
-    }
+    for (int i = 0; i < 4; i++) ah[i] = *reinterpret_cast<const bf16x8_t*>(A0 + (wm * 4 + i) * 512 + foff);
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bfr[j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < 4; j++)
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bfr[j], acc[i][j], 0, 0, 0);
-      }
   }
   const bool norm = a.ng != nullptr;
   // results: tile (i, j) of the wave holds rows wm*64 + 16i + 4*g4 + r,
@@ -2425,13 +2380,13 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
   }
 }
 
-hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, __bf16* Al, float* rsc, uint32_t cap_rows,
+hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t cap_rows,
                           hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   if (a.amax || (a.K % 32) || a.B == 0 || !a.Wh0 || (a.nseg > 1 && !a.Wh1)) return hipErrorInvalidValue;
   if (a.B > cap_rows) return hipErrorInvalidValue;
   // the split first (its time is inside the events)
   if (e0) (void)hipEventRecord(e0, st);
-  hipLaunchKernelGGL(k_split, dim3((a.B + 3) / 4), dim3(256), 0, st, a.X, a.ldx, a.K, a.ng, a.B, Ah, Al, rsc);
+  hipLaunchKernelGGL(k_split, dim3((a.B + 3) / 4), dim3(256), 0, st, a.X, a.ldx, a.K, a.ng, a.B, Ah, rsc);
   const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
                                           : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
   const uint32_t per = a.mode == GM_SILU ? 64 : 128;
@@ -2440,7 +2395,7 @@ hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, __bf16* Al, float* rsc,
   // two LDS stages (48 KB) ran 5-12% faster than three (72 KB) at the
   // 8192-row prefill shapes with random operands (two workgroups a CU
   // either way, by registers)
-  hipLaunchKernelGGL(k_gemm_dl<2>, grid, dim3(256), 0, st, a, Ah, Al, rsc);
+  hipLaunchKernelGGL(k_gemm_dl<2>, grid, dim3(256), 0, st, a, Ah, rsc);
   if (e1) (void)hipEventRecord(e1, st);
   return hipGetLastError();
 }

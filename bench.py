@@ -269,7 +269,7 @@ def run_prefill(path: str, c) -> dict:
                         "(P - v d) per token (the products) + causal attention 2 B L^2 d per "
                         "softmax layer (the GLA scan not counted)",
             "kernels": ("products k_split + k_gemm_dl (128 x 128 MFMA tiles, bf16 weights x bf16 "
-                        "head+remainder activations, both streamed straight into LDS)" if m == "bf16" else
+                        "activations, both streamed straight into LDS; block 0 in fp32)" if m == "bf16" else
                         "products k_gemm_big (128 x 128 MFMA tiles, fp32 MFMA)")
                        + ", attention k_attn_flash (fp32 MFMA), GLA k_gla_sub + k_gla_carry",
         }

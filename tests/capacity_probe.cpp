@@ -79,7 +79,7 @@ int main() {
   p.X = buf; p.ldx = 64; p.K = 64; p.seg[0] = GemvSeg{buf, 64, buf, 64}; p.nseg = 1;
   p.B = 200; p.Wh0 = reinterpret_cast<const uint16_t*>(buf);
   expect("gemm_dl: 200 rows, split buffers for 199",
-         launch_gemm_dl(p, reinterpret_cast<__bf16*>(buf), reinterpret_cast<__bf16*>(buf), buf, 199, nullptr),
+         launch_gemm_dl(p, reinterpret_cast<__bf16*>(buf), buf, 199, nullptr),
          true);
 
   printf("%d failed\n", fails);
