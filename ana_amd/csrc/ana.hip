@@ -437,7 +437,9 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
   // products too (greedy picks then read the stored logits)
   if (pe || (fast_mode(c) && (small ? !chunk : (chunk || kind != ANA_K_HEAD || g0.B >= kPwMaxB)))) {
     GemvArgs g = g0;
-    const bool bf = reads_bf16(c, g);
+    // prefill steps on the big tiles read every block's weights in bf16
+    // (decode keeps the first block in fp32)
+    const bool bf = reads_bf16(c, g) || (c->Wh && chunk && g.B >= 128);
     if (bf) {
       g.Wh0 = c->Wh + (g.seg[0].W - c->W);
       g.Wh1 = g.nseg > 1 ? c->Wh + (g.seg[1].W - c->W) : nullptr;
