@@ -387,6 +387,41 @@ def test_sampler_thresholds_and_draw(oracle):
         assert np.array_equal(r, r0)
 
 
+def test_bisections_take_forty_steps(oracle):
+    """Sample.bend's thresholds bisect 40 times: top-k over [peak - 100,
+    peak] (a final width of 100 / 2^40 = 9.09e-11) and top-p over [0, 1]
+    (2^-40 = 9.09e-13). So when the value just below the boundary sits
+    further below it than that width, exactly the true set survives; with
+    a gap between one and two widths, a bisection of 39 steps (twice the
+    width) keeps the value below the boundary for some placements. Values
+    near zero keep float32 spacing far below either width."""
+    rng = np.random.default_rng(40)
+    v, k = 64, 3
+    for trial in range(64):
+        # top-k: the peak at 0, the k-th largest at -x, the next 1.35 widths
+        # below it, every other logit far below
+        x = float(rng.uniform(1e-10, 3e-9))
+        gap = 1.35 * 100.0 * 2.0 ** -40
+        lg = np.full(v, -60.0, np.float32)
+        lg[5], lg[17] = 0.0, -1e-11
+        lg[30] = -x
+        lg[41] = -(x + gap)
+        assert np.float32(-(x + gap)) < np.float32(-x)
+        t = oracle.topk_threshold(lg, k)
+        assert (lg >= t).sum() == k, (trial, x, t)
+        # top-p: weights of magnitude 1e-11, the boundary weight b and the
+        # next 1.35 widths below it; the mass needed lies between the top
+        # two's and the top three's
+        b = float(rng.uniform(3e-12, 6e-12))
+        w = np.full(v, 1e-14, np.float32)
+        w[7], w[20] = 9e-12, b
+        w[33] = b - 1.35 * 2.0 ** -40
+        total = float(w.astype(np.float64).sum())
+        need = 9e-12 + 0.5 * b
+        t = oracle.topp_threshold(w, np.float32(need / total))
+        assert (w >= t).sum() == 2, (trial, b, t)
+
+
 def test_draw_follows_cumulative_mass(oracle):
     """With top-k and top-p off the draw is inverse CDF over index order:
     the pick i satisfies cum[i-1] <= u*total < cum[i] up to rounding."""
