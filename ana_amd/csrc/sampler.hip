@@ -150,6 +150,25 @@ __device__ uint32_t tree_argmax(const float (&x)[LPT], uint32_t base, uint32_t v
   return wi[0];
 }
 
+// a whole number summed over the workgroup's 16 waves (every thread gets it)
+__device__ uint32_t block_count(uint32_t c, uint32_t* redu, uint32_t tid) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) c += __shfl_xor(c, m, 64);
+  if ((tid & 63) == 0) redu[tid >> 6] = c;
+  __syncthreads();
+  uint32_t t = 0;
+#pragma unroll
+  for (int w = 0; w < 16; w++) t += redu[w];
+  __syncthreads();
+  return t;
+}
+
+__device__ __forceinline__ uint32_t wave_count(uint32_t c) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) c += __shfl_xor(c, m, 64);
+  return c;
+}
+
 __device__ __forceinline__ uint64_t rotl64(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
 
 // Rng.next (bend/Sample.bend:57-66): the file's transition, which is not
@@ -167,6 +186,11 @@ __device__ uint64_t rng_next(uint64_t* r) {
 
 }  // namespace
 
+// candidates a wave finishes the top-k bisection on; survivors of a top-k
+// the top-p bisection takes in one wave, and its fold's stack depth (the
+// tree's levels, at most 16 for a vocabulary of 65536, plus one)
+constexpr int kCand = 1024, kSurv = 64, kSurvDepth = 18;
+
 template <int LPT>
 __global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t dv) {
   __shared__ float red[16];
@@ -174,6 +198,11 @@ __global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t
   __shared__ float heap[2048];
   __shared__ float leaf[LPT];
   __shared__ uint32_t who;
+  __shared__ uint32_t redu[16], nc_s, off_s[16];
+  __shared__ float lo_s;
+  __shared__ uint32_t sidx[kSurv];
+  __shared__ float sw[kSurv], stk[kSurvDepth][64];
+  __shared__ uint32_t ops[kSurvDepth];
   const uint32_t b = blockIdx.x, tid = threadIdx.x;
   const uint32_t v = a.vocab;
   const uint32_t base = tid * LPT;
@@ -229,28 +258,173 @@ __global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t
   const float peak = tree_up(local_reduce<LPT>(pm, Max()), Max(), red, tid, NT);
 
   // top-k: the largest t in [peak-100, peak] (40 bisection steps) keeping
-  // at least k logits >= t; the rest go to -3e38 (sample.topk)
+  // at least k logits >= t; the rest go to -3e38 (sample.topk). A count is
+  // a whole number below 2^24, so its tree sum is exact and may be formed
+  // in any order: the steps run over the whole row while more than kCand
+  // logits lie in [lo, hi), then those candidates go to LDS and wave 0 takes
+  // the remaining steps (count(x >= mid) = count(x >= hi0) + the candidates
+  // >= mid) with no barrier. nsurv = count(x >= lo) after the last step.
+  uint32_t nsurv = 0;
   if (a.topk < v) {
     const float need = (float)a.topk;
     float lo = peak - 100.0f, hi = peak;
-    for (int it = 0; it < 40; it++) {
-      const float mid = 0.5f * (lo + hi);
-      float c[LPT];
+    auto cnt_ge = [&](float t) {
+      uint32_t c = 0;
 #pragma unroll
-      for (int i = 0; i < LPT; i++) c[i] = (active && base + i < v && x[i] >= mid) ? 1.0f : 0.0f;
-      const float cnt = tree_up(local_reduce<LPT>(c, Add()), Add(), red, tid, NT);
-      if (cnt >= need) lo = mid; else hi = mid;
+      for (int i = 0; i < LPT; i++) c += (active && base + i < v && x[i] >= t) ? 1u : 0u;
+      return c;
+    };
+    uint32_t c_lo = block_count(cnt_ge(lo), redu, tid), c_hi = block_count(cnt_ge(hi), redu, tid);
+    int it = 0;
+    for (; it < 40 && c_lo - c_hi > kCand; it++) {
+      const float mid = 0.5f * (lo + hi);
+      const uint32_t c = block_count(cnt_ge(mid), redu, tid);
+      if ((float)c >= need) { lo = mid; c_lo = c; } else { hi = mid; c_hi = c; }
+    }
+    if (it < 40) {
+      float* cand = heap;   // (the draw's heap is filled only later)
+      if (tid == 0) nc_s = 0;
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < LPT; i++)
+        if (active && base + i < v && x[i] >= lo && x[i] < hi) cand[atomicAdd(&nc_s, 1u)] = x[i];
+      __syncthreads();
+      if (tid < 64) {
+        const uint32_t nc = nc_s;
+        float cv[kCand / 64];
+#pragma unroll
+        for (int e = 0; e < kCand / 64; e++) cv[e] = tid + 64 * e < nc ? cand[tid + 64 * e] : 0.0f;
+        for (; it < 40; it++) {
+          const float mid = 0.5f * (lo + hi);
+          uint32_t c = 0;
+#pragma unroll
+          for (int e = 0; e < kCand / 64; e++) c += (tid + 64 * e < nc && cv[e] >= mid) ? 1u : 0u;
+          c = c_hi + wave_count(c);
+          if ((float)c >= need) { lo = mid; c_lo = c; } else { hi = mid; }
+        }
+        if (tid == 0) {
+          lo_s = lo;
+          nc_s = c_lo;
+        }
+      }
+      __syncthreads();
+      lo = lo_s;
+      c_lo = nc_s;
+      __syncthreads();
     }
 #pragma unroll
     for (int i = 0; i < LPT; i++) x[i] = x[i] >= lo ? x[i] : -3.0e38f;
+    nsurv = c_lo;
   }
   // w = exp((x - peak) / temp) (exp.at); absent leaves stay 0
   float w[LPT];
 #pragma unroll
   for (int i = 0; i < LPT; i++) w[i] = (active && base + i < v) ? dexp((x[i] - peak) / a.temp) : 0.0f;
 
-  // top-p: the largest t in [0, 1] whose kept mass reaches p of the total
-  if (a.topp < 1.0f) {
+  // top-p: the largest t in [0, 1] whose kept mass reaches p of the total.
+  // After a top-k that kept 1..kSurv logits only those weights are not 0,
+  // and a 0 leaf leaves every sum of the reference's tree unchanged, so
+  // each mass is the tree sum over the survivors alone: wave 0 forms, per
+  // survivor L, the tree-ordered mass of {w >= w_L} once, and each step's
+  // mass is the one of the least w_L >= mid (0 when there is none).
+  // (every logit the top-k dropped now weighs dexp((-3e38 - peak) / temp),
+  // which must be 0 for the survivors to be the only leaves that count)
+  if (a.topp < 1.0f && a.topk < v && nsurv >= 1 && nsurv <= (uint32_t)kSurv &&
+      dexp((-3.0e38f - peak) / a.temp) == 0.0f) {
+    // the leaves of non-zero weight (at most the survivors) in index order:
+    // a thread's own, after those of the threads before it
+    uint32_t mine = 0;
+#pragma unroll
+    for (int i = 0; i < LPT; i++) mine += w[i] > 0.0f ? 1u : 0u;
+    const uint32_t lane = tid & 63;
+    uint32_t incl = mine;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      const uint32_t o = __shfl_up(incl, m, 64);
+      if (lane >= (uint32_t)m) incl += o;
+    }
+    if (lane == 63) off_s[tid >> 6] = incl;
+    __syncthreads();
+    uint32_t off = incl - mine;
+    for (uint32_t w2 = 0; w2 < (tid >> 6); w2++) off += off_s[w2];
+#pragma unroll
+    for (int i = 0; i < LPT; i++)
+      if (w[i] > 0.0f) {
+        sidx[off] = base + i;
+        sw[off] = w[i];
+        off++;
+      }
+    uint32_t n = 0;
+#pragma unroll
+    for (int w2 = 0; w2 < 16; w2++) n += off_s[w2];
+    __syncthreads();
+    if (tid < 64 && n == 0) {
+      // no weight above 0: every mass is 0, which reaches need = 0, so lo
+      // climbs to the last midpoint
+      float lo = 0.0f, hi = 1.0f;
+      for (int it = 0; it < 40; it++) {
+        const float mid = 0.5f * (lo + hi);
+        if (0.0f >= a.topp * 0.0f) lo = mid; else hi = mid;
+      }
+      if (tid == 0) lo_s = lo;
+    } else if (tid < 64) {
+      const bool valid = tid < n;
+      const float wl = valid ? sw[tid] : 0.0f;
+      // lane L's mass: the leaves in index order with w < w_L as 0, summed
+      // as the tree nests them. Consecutive leaves meet at level
+      // h = 32 - clz(i ^ j); a smaller h binds first, so a stack of pending
+      // levels (uniform across the wave) folds them left to right
+      // (ops: the pending levels, the same in every lane, which all write them)
+      int sp = 0;   // values on the stack; sp - 1 pending levels
+      uint32_t prev = 0;
+      for (uint32_t j = 0; j < n; j++) {
+        const uint32_t ij = sidx[j];
+        const float wj = sw[j];
+        const float val = wj >= wl ? wj : 0.0f;
+        if (j > 0) {
+          const uint32_t h = 32u - __builtin_clz(prev ^ ij);
+          while (sp > 1 && ops[sp - 2] < h) {
+            stk[sp - 2][tid] = stk[sp - 2][tid] + stk[sp - 1][tid];
+            sp--;
+          }
+          ops[sp - 1] = h;
+        }
+        stk[sp][tid] = val;
+        sp++;
+        prev = ij;
+      }
+      while (sp > 1) {
+        stk[sp - 2][tid] = stk[sp - 2][tid] + stk[sp - 1][tid];
+        sp--;
+      }
+      const float ml = stk[0][tid];
+      // the total: the mass of the least weight (every survivor)
+      float mn = valid ? wl : INFINITY;
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) mn = fminf(mn, __shfl_xor(mn, m, 64));
+      const unsigned long long at0 = __ballot(valid && wl == mn);
+      const float total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml), __builtin_ctzll(at0)));
+      const float need = a.topp * total;
+      float lo = 0.0f, hi = 1.0f;
+      for (int it = 0; it < 40; it++) {
+        const float mid = 0.5f * (lo + hi);
+        float k2 = valid && wl >= mid ? wl : INFINITY;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) k2 = fminf(k2, __shfl_xor(k2, m, 64));
+        float mass = 0.0f;
+        if (k2 != INFINITY) {
+          const unsigned long long at = __ballot(valid && wl == k2);
+          mass = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml), __builtin_ctzll(at)));
+        }
+        if (mass >= need) lo = mid; else hi = mid;
+      }
+      if (tid == 0) lo_s = lo;
+    }
+    __syncthreads();
+    const float lo = lo_s;
+#pragma unroll
+    for (int i = 0; i < LPT; i++) w[i] = w[i] >= lo ? w[i] : 0.0f;
+  } else if (a.topp < 1.0f) {
     const float need = a.topp * tree_up(local_reduce<LPT>(w, Add()), Add(), red, tid, NT);
     float lo = 0.0f, hi = 1.0f;
     for (int it = 0; it < 40; it++) {

@@ -194,8 +194,12 @@ def test_token_loop_greedy(oracle, ckpts, name):
         assert list(out[i]) == want, i
 
 
+# (the device's top-k finishes its bisection in one wave once 1024 or fewer
+# logits lie in the interval, and its top-p takes one wave after a top-k
+# that kept 64 or fewer: 64 and 200 sit either side of that, 1000 keeps the
+# whole-row steps going longer)
 SETTINGS = [(0.8, 40, 0.9), (1.0, 0xFFFFFFFF, 0.95), (0.5, 5, 1.0), (0.8, 0xFFFFFFFF, 1.0),
-            (1.5, 3, 0.5), (0.0, 40, 0.9)]
+            (1.5, 3, 0.5), (0.0, 40, 0.9), (0.7, 64, 0.95), (0.9, 200, 0.8), (1.2, 1000, 0.7)]
 
 
 def _check_pick(oracle, dec, seqs, lgs):
