@@ -9,6 +9,8 @@
 // reference's tree, so the results are its bits. Absent leaves (index >=
 // vocab, the tree's VZ) count 0.0 in sums and -3e38 in the max, as V.sum and
 // V.max give VZ; Sample.argmax gives VZ the pair (-3e38, 0).
+#include <type_traits>
+
 #include "ana_internal.h"
 #include "numerics.h"
 
@@ -150,23 +152,55 @@ __device__ uint32_t tree_argmax(const float (&x)[LPT], uint32_t base, uint32_t v
   return wi[0];
 }
 
-// a whole number summed over the workgroup's 16 waves (every thread gets it)
-__device__ uint32_t block_count(uint32_t c, uint32_t* redu, uint32_t tid) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) c += __shfl_xor(c, m, 64);
-  if ((tid & 63) == 0) redu[tid >> 6] = c;
-  __syncthreads();
-  uint32_t t = 0;
-#pragma unroll
-  for (int w = 0; w < 16; w++) t += redu[w];
-  __syncthreads();
-  return t;
+// wave reductions by DPP within rows of 16 lanes (lane ^ 1, lane ^ 2, the
+// mirrored quad, the mirrored half-row), then the four rows by lane reads:
+// a few cycles a step where a lane shuffle waits on LDS
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+// a whole number over the wave (every lane gets it)
+__device__ __forceinline__ uint32_t wave_count(uint32_t c) {
+  int v = (int)c;
+  v += dpp_i<0xB1>(v);
+  v += dpp_i<0x4E>(v);
+  v += dpp_i<0x141>(v);
+  v += dpp_i<0x140>(v);
+  return (uint32_t)((__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+                    (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48)));
+}
+// the least of a wave's floats (every lane gets it)
+__device__ __forceinline__ float wave_minf(float x) {
+  auto mn = [](float a, float b) { return b < a ? b : a; };
+  auto d = [](float a, auto c) {
+    return __builtin_bit_cast(float, dpp_i<decltype(c)::value>(__builtin_bit_cast(int, a)));
+  };
+  x = mn(x, d(x, std::integral_constant<int, 0xB1>{}));
+  x = mn(x, d(x, std::integral_constant<int, 0x4E>{}));
+  x = mn(x, d(x, std::integral_constant<int, 0x141>{}));
+  x = mn(x, d(x, std::integral_constant<int, 0x140>{}));
+  auto rl = [](float a, int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), l)); };
+  return mn(mn(rl(x, 0), rl(x, 16)), mn(rl(x, 32), rl(x, 48)));
 }
 
-__device__ __forceinline__ uint32_t wave_count(uint32_t c) {
+// N whole numbers, each summed over the workgroup's 16 waves (every thread
+// gets them)
+template <int N>
+__device__ void block_counts(uint32_t (&c)[N], uint32_t (*redn)[16], uint32_t tid) {
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) c += __shfl_xor(c, m, 64);
-  return c;
+  for (int i = 0; i < N; i++) c[i] = wave_count(c[i]);
+  if ((tid & 63) == 0)
+#pragma unroll
+    for (int i = 0; i < N; i++) redn[tid >> 6][i] = c[i];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < N; i++) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int w = 0; w < 16; w++) t += redn[w][i];
+    c[i] = t;
+  }
+  __syncthreads();
 }
 
 __device__ __forceinline__ uint64_t rotl64(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
@@ -190,15 +224,17 @@ __device__ uint64_t rng_next(uint64_t* r) {
 // the top-p bisection takes in one wave, and its fold's stack depth (the
 // tree's levels, at most 16 for a vocabulary of 65536, plus one)
 constexpr int kCand = 1024, kSurv = 64, kSurvDepth = 18;
+// top-k steps a pass over the whole row resolves, and its midpoints
+constexpr int kPass = 2, kNodes = (1 << kPass) - 1;
 
 template <int LPT>
 __global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t dv) {
   __shared__ float red[16];
   __shared__ uint32_t redi[16];
   __shared__ float heap[2048];
-  __shared__ float leaf[LPT];
+  __shared__ float leafh[2 * LPT];
   __shared__ uint32_t who;
-  __shared__ uint32_t redu[16], nc_s, off_s[16];
+  __shared__ uint32_t redn[16][16], nc_s, off_s[16];
   __shared__ float lo_s;
   __shared__ uint32_t sidx[kSurv];
   __shared__ float sw[kSurv], stk[kSurvDepth][64];
@@ -274,20 +310,69 @@ __global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t
       for (int i = 0; i < LPT; i++) c += (active && base + i < v && x[i] >= t) ? 1u : 0u;
       return c;
     };
-    uint32_t c_lo = block_count(cnt_ge(lo), redu, tid), c_hi = block_count(cnt_ge(hi), redu, tid);
+    uint32_t c0[2] = {cnt_ge(lo), cnt_ge(hi)};
+    block_counts<2>(c0, redn, tid);
+    uint32_t c_lo = c0[0], c_hi = c0[1];
     int it = 0;
-    for (; it < 40 && c_lo - c_hi > kCand; it++) {
-      const float mid = 0.5f * (lo + hi);
-      const uint32_t c = block_count(cnt_ge(mid), redu, tid);
-      if ((float)c >= need) { lo = mid; c_lo = c; } else { hi = mid; c_hi = c; }
+    // kPass steps a pass over the row: the kNodes midpoints the next kPass
+    // steps could take (node i's lower child 2 i + 1 halves [lo, mid], its
+    // upper child 2 i + 2 halves [mid, hi], each midpoint the same float
+    // 0.5 (lo + hi) the step itself forms), all counted at once, then the path
+    while (it + kPass <= 40 && c_lo - c_hi > kCand) {
+      float mids[kNodes], los[kNodes], his[kNodes];
+      los[0] = lo;
+      his[0] = hi;
+#pragma unroll
+      for (int n = 0; n < kNodes; n++) {
+        mids[n] = 0.5f * (los[n] + his[n]);
+        if (2 * n + 2 < kNodes) {
+          los[2 * n + 1] = los[n];
+          his[2 * n + 1] = mids[n];
+          los[2 * n + 2] = mids[n];
+          his[2 * n + 2] = his[n];
+        }
+      }
+      uint32_t cs[kNodes];
+#pragma unroll
+      for (int n = 0; n < kNodes; n++) cs[n] = cnt_ge(mids[n]);
+      block_counts<kNodes>(cs, redn, tid);
+      int node = 0;
+#pragma unroll
+      for (int st = 0; st < kPass; st++) {
+        // (a uniform walk: select by index without dynamic register indexing)
+        float mid = 0.0f;
+        uint32_t c = 0;
+#pragma unroll
+        for (int n = 0; n < kNodes; n++)
+          if (n == node) { mid = mids[n]; c = cs[n]; }
+        if ((float)c >= need) { lo = mid; c_lo = c; node = 2 * node + 2; } else { hi = mid; c_hi = c; node = 2 * node + 1; }
+      }
+      it += kPass;
     }
     if (it < 40) {
       float* cand = heap;   // (the draw's heap is filled only later)
       if (tid == 0) nc_s = 0;
       __syncthreads();
+      {
+        // one atomic a wave for its candidates' places, then each thread's
+        // after the lanes before it
+        uint32_t mine = 0;
 #pragma unroll
-      for (int i = 0; i < LPT; i++)
-        if (active && base + i < v && x[i] >= lo && x[i] < hi) cand[atomicAdd(&nc_s, 1u)] = x[i];
+        for (int i = 0; i < LPT; i++) mine += (active && base + i < v && x[i] >= lo && x[i] < hi) ? 1u : 0u;
+        const uint32_t lane = tid & 63;
+        uint32_t incl = mine;
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) {
+          const uint32_t o = __shfl_up(incl, m, 64);
+          if (lane >= (uint32_t)m) incl += o;
+        }
+        uint32_t at = 0;
+        if (lane == 63) at = atomicAdd(&nc_s, incl);
+        at = (uint32_t)__builtin_amdgcn_readlane((int)at, 63) + incl - mine;
+#pragma unroll
+        for (int i = 0; i < LPT; i++)
+          if (active && base + i < v && x[i] >= lo && x[i] < hi) cand[at++] = x[i];
+      }
       __syncthreads();
       if (tid < 64) {
         const uint32_t nc = nc_s;
@@ -299,7 +384,7 @@ __global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t
           uint32_t c = 0;
 #pragma unroll
           for (int e = 0; e < kCand / 64; e++) c += (tid + 64 * e < nc && cv[e] >= mid) ? 1u : 0u;
-          c = c_hi + wave_count(c);
+          c = c_hi + wave_count(c);   // (c_hi: count(x >= hi) when the candidates were taken)
           if ((float)c >= need) { lo = mid; c_lo = c; } else { hi = mid; }
         }
         if (tid == 0) {
@@ -316,10 +401,13 @@ __global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t
     for (int i = 0; i < LPT; i++) x[i] = x[i] >= lo ? x[i] : -3.0e38f;
     nsurv = c_lo;
   }
-  // w = exp((x - peak) / temp) (exp.at); absent leaves stay 0
+  // w = exp((x - peak) / temp) (exp.at); absent leaves stay 0. Every logit
+  // the top-k dropped is -3e38 now, so its weight is one value, formed once
+  const float wz = dexp((-3.0e38f - peak) / a.temp);
   float w[LPT];
 #pragma unroll
-  for (int i = 0; i < LPT; i++) w[i] = (active && base + i < v) ? dexp((x[i] - peak) / a.temp) : 0.0f;
+  for (int i = 0; i < LPT; i++)
+    w[i] = (active && base + i < v) ? (x[i] == -3.0e38f ? wz : dexp((x[i] - peak) / a.temp)) : 0.0f;
 
   // top-p: the largest t in [0, 1] whose kept mass reaches p of the total.
   // After a top-k that kept 1..kSurv logits only those weights are not 0,
@@ -329,8 +417,7 @@ __global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t
   // mass is the one of the least w_L >= mid (0 when there is none).
   // (every logit the top-k dropped now weighs dexp((-3e38 - peak) / temp),
   // which must be 0 for the survivors to be the only leaves that count)
-  if (a.topp < 1.0f && a.topk < v && nsurv >= 1 && nsurv <= (uint32_t)kSurv &&
-      dexp((-3.0e38f - peak) / a.temp) == 0.0f) {
+  if (a.topp < 1.0f && a.topk < v && nsurv >= 1 && nsurv <= (uint32_t)kSurv && wz == 0.0f) {
     // the leaves of non-zero weight (at most the survivors) in index order:
     // a thread's own, after those of the threads before it
     uint32_t mine = 0;
@@ -374,43 +461,43 @@ __global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t
       // as the tree nests them. Consecutive leaves meet at level
       // h = 32 - clz(i ^ j); a smaller h binds first, so a stack of pending
       // levels (uniform across the wave) folds them left to right
-      // (ops: the pending levels, the same in every lane, which all write them)
+      // (ops: the pending levels, the same in every lane, which all write
+      // them; the stack's top value stays in a register, the rest in stk)
+      const uint32_t myi = valid ? sidx[tid] : 0u;
       int sp = 0;   // values on the stack; sp - 1 pending levels
       uint32_t prev = 0;
+      float cur = 0.0f;
       for (uint32_t j = 0; j < n; j++) {
-        const uint32_t ij = sidx[j];
-        const float wj = sw[j];
+        const uint32_t ij = (uint32_t)__builtin_amdgcn_readlane((int)myi, (int)j);
+        const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), (int)j));
         const float val = wj >= wl ? wj : 0.0f;
         if (j > 0) {
           const uint32_t h = 32u - __builtin_clz(prev ^ ij);
           while (sp > 1 && ops[sp - 2] < h) {
-            stk[sp - 2][tid] = stk[sp - 2][tid] + stk[sp - 1][tid];
+            cur = stk[sp - 2][tid] + cur;
             sp--;
           }
           ops[sp - 1] = h;
+          stk[sp - 1][tid] = cur;
         }
-        stk[sp][tid] = val;
+        cur = val;
         sp++;
         prev = ij;
       }
       while (sp > 1) {
-        stk[sp - 2][tid] = stk[sp - 2][tid] + stk[sp - 1][tid];
+        cur = stk[sp - 2][tid] + cur;
         sp--;
       }
-      const float ml = stk[0][tid];
+      const float ml = cur;
       // the total: the mass of the least weight (every survivor)
-      float mn = valid ? wl : INFINITY;
-#pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) mn = fminf(mn, __shfl_xor(mn, m, 64));
+      const float mn = wave_minf(valid ? wl : INFINITY);
       const unsigned long long at0 = __ballot(valid && wl == mn);
       const float total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml), __builtin_ctzll(at0)));
       const float need = a.topp * total;
       float lo = 0.0f, hi = 1.0f;
       for (int it = 0; it < 40; it++) {
         const float mid = 0.5f * (lo + hi);
-        float k2 = valid && wl >= mid ? wl : INFINITY;
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) k2 = fminf(k2, __shfl_xor(k2, m, 64));
+        const float k2 = wave_minf(valid && wl >= mid ? wl : INFINITY);
         float mass = 0.0f;
         if (k2 != INFINITY) {
           const unsigned long long at = __ballot(valid && wl == k2);
@@ -439,12 +526,25 @@ __global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t
     for (int i = 0; i < LPT; i++) w[i] = w[i] >= lo ? w[i] : 0.0f;
   }
 
-  // the draw: thread sums into a heap of the tree above the threads, then
-  // draw.go walks from the root (left iff u < sum(left) or the right is VZ)
-  if (active) heap[NT + tid] = local_reduce<LPT>(w, Add());
-  __syncthreads();
-  for (uint32_t n = NT >> 1; n >= 1; n >>= 1) {
-    for (uint32_t i = tid; i < n; i += 1024) heap[n + i] = heap[2 * (n + i)] + heap[2 * (n + i) + 1];
+  // the draw: thread sums into a heap of the tree above the threads (node n
+  // = node 2 n + node 2 n + 1), then draw.go walks from the root (left iff
+  // u < sum(left) or the right is VZ). The levels inside a wave join lanes
+  // by xor partners, left + right; those above, wave 0 alone
+  {
+    float hv = active ? local_reduce<LPT>(w, Add()) : 0.0f;
+    if (active) heap[NT + tid] = hv;
+    const uint32_t lane = tid & 63;
+    for (uint32_t m = 1; m < 64 && m < NT; m <<= 1) {
+      const float o = __shfl_xor(hv, m, 64);
+      hv = (lane & m) ? o + hv : hv + o;
+      if (active && (lane & (2 * m - 1)) == 0) heap[(NT + tid) / (2 * m)] = hv;
+    }
+    __syncthreads();
+    if (NT > 64 && tid < 64)
+      for (uint32_t n = NT >> 7; n >= 1; n >>= 1) {
+        if (tid < n) heap[n + tid] = heap[2 * (n + tid)] + heap[2 * (n + tid) + 1];
+        __builtin_amdgcn_wave_barrier();   // (one wave: its LDS ops keep their order)
+      }
     __syncthreads();
   }
   uint32_t pbase = 0;
@@ -467,21 +567,26 @@ __global__ __launch_bounds__(1024) void k_pick(PickArgs a, uint32_t NT, uint32_t
   }
   __syncthreads();
   if (tid == who) {
+    // the run's own tree in LDS: leaves at LPT + i, node n = node 2 n +
+    // node 2 n + 1 (the pairs local_reduce forms)
 #pragma unroll
-    for (int i = 0; i < LPT; i++) leaf[i] = w[i];
+    for (int i = 0; i < LPT; i++) leafh[LPT + i] = w[i];
+#pragma unroll
+    for (int st = 1; st < LPT; st *= 2)
+#pragma unroll
+      for (int i = 0; i < LPT; i += 2 * st) {
+        w[i] = w[i] + w[i + st];
+        leafh[(LPT + i) / (2 * st)] = w[i];
+      }
   }
   __syncthreads();
   if (tid == 0) {
-    float tmp[LPT];
+    uint32_t n = 1;
     while (p > 0) {
       const uint32_t half = 1u << (p - 1);
-      const uint32_t off = pbase % LPT;
-      for (uint32_t i = 0; i < half; i++) tmp[i] = leaf[off + i];
-      for (uint32_t s = 1; s < half; s *= 2)
-        for (uint32_t i = 0; i < half; i += 2 * s) tmp[i] = tmp[i] + tmp[i + s];
-      const float ml = tmp[0];
+      const float ml = leafh[2 * n];
       const bool left = (u < ml) || (pbase + half >= v);
-      if (!left) { u = u - ml; pbase += half; }
+      if (!left) { u = u - ml; pbase += half; n = 2 * n + 1; } else { n = 2 * n; }
       p--;
     }
     a.tok[b] = pbase;
