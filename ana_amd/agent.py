@@ -1,27 +1,34 @@
 """Many agent episodes decoded together on one Decoder.
 
-The engine's side of the agent tool loop (bend/Agent/Loop.bend):
-- an episode feeds BOS and its prompt, then draws from the prompt's last
-  logits (al.episode, Loop.bend:681-690, through dc.en.prefill.pick);
-- it draws one token a step (al.gen, through dc.en.step.pick);
-- when a stretch ends a tool call, the tool's echo is fed as unsampled
-  tokens, prefilled, and drawing resumes from the echo's last logits
-  (al.called then al.resume, Loop.bend:561-567);
-- tokens given as if the model had written them (AGENT_FIRST: al.start and
-  al.forced.first, Loop.bend:275-277, 338-343) take the same route.
+The engine's side of the agent tool loop (bend/Agent/Loop.bend), stretch by
+stretch as al.gen runs it (Loop.bend:480-505):
+- an episode feeds BOS and its prompt and draws a pick from the prompt's
+  last logits (al.episode, Loop.bend:681-690, through dc.en.prefill.pick);
+- given tokens to write first (AGENT_FIRST), that pick is drawn and set
+  aside: the RNG moves past it, and the given tokens stand in as picks not
+  drawn (al.start and al.forced.first, Loop.bend:275-277, 338-343);
+- a stretch of budget N: a pick that is EOS ends the episode ("eos", the EOS
+  not written); with N picks written, the next one ends it ("budget"); a
+  pick that ends a call line is written, the call's token fed in its place
+  (al.called, Loop.bend:403-411: the newline token, `call_token`) and the
+  tool asked; any other pick is written, fed, and the next one drawn (or,
+  while given tokens remain, taken from them: al.next, Loop.bend:375-383);
+- a tool's echo is fed as unsampled tokens and a new stretch starts from a
+  pick drawn from the echo's last logits (al.resume, Loop.bend:561-567);
+  tokens still to be given are dropped there, as al.resume starts afresh.
 
-Forced tokens leave the episode's RNG where it was ("a pick not drawn",
-Loop.bend:275). What a call is and what the tool answers stay with the
-caller (`is_call`, `tool`), as do the transcript, the repetition cut and the
-retry settings after a failed check.
+What a call is and what the tool answers stay with the caller (`is_call`,
+`tool`), as do the transcript, the repetition cut and the retry settings
+after a failed check.
 
 What this module adds is the batching: every live episode shares each engine
-call. A round is one ana_feeds_n for every episode with a forced run (the
-pending token and the run but its last token, at each episode's own
-position), then one ana_generate step for every live episode, each with its
-own RNG words. An episode's tokens do not depend on which others share its
-calls (`test_agent` and `test_gpu_agent` check that, the GPU one bit for
-bit in exact mode).
+call. A round feeds, for each episode, the tokens written since its last
+draw but the last one (ana_feeds_n), then takes one ana_generate step for
+every episode that draws (the last token fed there, each episode with its
+own RNG words). An episode's tokens do not depend on which others share its
+calls; `test_agent` holds the batching to a one-episode restatement of the
+loop on a stand-in decoder, and `test_gpu_agent` to the same restatement on
+the CPU oracle, bit for bit in exact mode.
 """
 from __future__ import annotations
 
@@ -44,23 +51,25 @@ class Episode:
 
 @dataclass
 class Outcome:
-    tokens: list = field(default_factory=list)   # after the prompt: drawn and fed, in order
-    drawn: list = field(default_factory=list)    # per token: drawn (True) or fed (False)
+    tokens: list = field(default_factory=list)   # written after the prompt: drawn and given, in order (no EOS)
+    drawn: list = field(default_factory=list)    # per token: drawn (True) or given (False)
     why: str = ""                                 # "eos", "budget", "calls" or "tool"
 
 
 def run(dec, eps: Sequence[Episode], st, is_call: Callable[[int, list], bool],
-        tool: Callable[[int, list], Sequence[int] | None], slots: Sequence[int] | None = None) -> list:
+        tool: Callable[[int, list], Sequence[int] | None], slots: Sequence[int] | None = None,
+        call_token: int | None = None) -> list:
     """Decode episodes eps together on dec (sequence slots `slots`, default
     0..n-1; each is reset first) with sampling settings st (None: greedy).
 
-    After every drawn token t of episode i (tokens = everything after its
-    prompt so far): t == EOS ends it ("eos"); else is_call(i, tokens) asks
-    for the tool: with calls left, tool(i, tokens) either ends the episode
-    (None: "tool", the caller's verdict, as a passed check ends al.round) or
-    gives the ids fed next, after which a new stretch begins with a new
-    budget (al.resume); without calls left the episode ends ("calls"); else
-    the stretch's budget of draws ends it ("budget")."""
+    Each pick of episode i (tokens = everything it wrote so far): EOS ends
+    it ("eos"); with the stretch's budget of picks written, it ends it
+    ("budget"); else it is written, and is_call(i, tokens) asks whether it
+    ends a call line. Then, with calls left, tool(i, tokens) either ends the
+    episode (None: "tool", the caller's verdict, as a passed check ends
+    al.round) or gives the echo: call_token (None: the written pick) is fed
+    at the call's place, the echo after it, and a new stretch starts with a
+    new budget; without calls left the episode ends ("calls")."""
     n = len(eps)
     slots = list(range(n)) if slots is None else [int(s) for s in slots]
     if len(slots) != n or len(set(slots)) != n:
@@ -72,54 +81,76 @@ def run(dec, eps: Sequence[Episode], st, is_call: Callable[[int, list], bool],
     from . import rng_seeded
     out = [Outcome() for _ in eps]
     rng = np.ascontiguousarray(np.stack([rng_seeded(e.seed) for e in eps]).astype(np.uint64))
-    pos = [len(e.prompt) - 1 for e in eps]        # where the pending token goes
-    nxt = [int(e.prompt[-1]) for e in eps]        # the pending token (fed, not yet)
-    forced = [list(e.first) for e in eps]
-    draws = [0] * n
+    pos = [0] * n                                 # where the next fed token goes
+    pick = [(0, True)] * n                        # the pick in hand: (token, drawn)
+    given = [list(e.first) for e in eps]          # given tokens after the one in hand
+    left = [e.budget for e in eps]                # picks the stretch may still write
     calls = [e.calls for e in eps]
-    live = set(range(n))
     for s in slots:
         dec.reset(s)
-    dec.feeds_n(slots, [0] * n, [list(e.prompt[:-1]) for e in eps])
+
+    def draw(idx, feeds):
+        """For each episode idx[k]: feed feeds[k] from its position, the
+        last token through one ana_generate step, whose pick comes back."""
+        pre = [k for k in range(len(idx)) if len(feeds[k]) > 1]
+        if pre:
+            dec.feeds_n([slots[idx[k]] for k in pre], [pos[idx[k]] for k in pre], [feeds[k][:-1] for k in pre])
+        r = np.ascontiguousarray(rng[idx])
+        got = dec.generate([slots[i] for i in idx], [pos[i] + len(f) - 1 for i, f in zip(idx, feeds)],
+                           [f[-1] for f in feeds], 1, st, r)
+        rng[idx] = r
+        for k, i in enumerate(idx):
+            pos[i] += len(feeds[k])
+        return [int(got[k, 0]) for k in range(len(idx))]
+
+    # the prompts fed and each first pick drawn; given tokens set it aside
+    first = draw(list(range(n)), [list(e.prompt) for e in eps])
+    for i in range(n):
+        pick[i] = (given[i].pop(0), False) if given[i] else (first[i], True)
+    live = set(range(n))
     while live:
-        fr = sorted(i for i in live if forced[i])
-        if fr:
-            dec.feeds_n([slots[i] for i in fr], [pos[i] for i in fr], [[nxt[i]] + forced[i][:-1] for i in fr])
-            for i in fr:
-                f, forced[i] = forced[i], []
-                out[i].tokens += f
-                out[i].drawn += [False] * len(f)
-                pos[i] += len(f)
-                nxt[i] = f[-1]
-        dr = sorted(live)
-        r = np.ascontiguousarray(rng[dr])
-        got = dec.generate([slots[i] for i in dr], [pos[i] for i in dr], [nxt[i] for i in dr], 1, st, r)
-        rng[dr] = r
-        for k, i in enumerate(dr):
-            t = int(got[k, 0])
-            out[i].tokens.append(t)
-            out[i].drawn.append(True)
-            pos[i] += 1
-            nxt[i] = t
-            draws[i] += 1
-            if t == EOS:
-                out[i].why = "eos"
-            elif is_call(i, out[i].tokens):
-                if calls[i] == 0:
-                    out[i].why = "calls"
-                else:
+        idx, feeds = [], []
+        for i in sorted(live):
+            fed = []
+            while True:
+                t, drawn = pick[i]
+                if t == EOS:
+                    out[i].why = "eos"
+                    break
+                if left[i] == 0:
+                    out[i].why = "budget"
+                    break
+                out[i].tokens.append(t)
+                out[i].drawn.append(drawn)
+                if is_call(i, out[i].tokens):
+                    if calls[i] == 0:
+                        out[i].why = "calls"
+                        break
                     calls[i] -= 1
                     ans = tool(i, out[i].tokens)
                     if ans is None:
                         out[i].why = "tool"
-                    else:
-                        echo = [int(x) for x in ans]
-                        if EOS in echo:
-                            raise ValueError("agent.run: EOS in a tool's echo")
-                        forced[i] = echo
-                        draws[i] = 0
-            elif draws[i] >= eps[i].budget:
-                out[i].why = "budget"
+                        break
+                    echo = [int(x) for x in ans]
+                    if EOS in echo:
+                        raise ValueError("agent.run: EOS in a tool's echo")
+                    fed += [t if call_token is None else int(call_token)] + echo
+                    given[i] = []
+                    left[i] = eps[i].budget
+                    idx.append(i)
+                    feeds.append(fed)
+                    break
+                left[i] -= 1
+                fed.append(t)
+                if given[i]:
+                    pick[i] = (given[i].pop(0), False)
+                    continue
+                idx.append(i)
+                feeds.append(fed)
+                break
             if out[i].why:
                 live.discard(i)
+        if idx:
+            for i, t in zip(idx, draw(idx, feeds)):
+                pick[i] = (t, True)
     return out

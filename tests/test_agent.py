@@ -1,5 +1,7 @@
-"""ana_amd.agent's bookkeeping on a stand-in decoder (no GPU): positions,
-forced runs, RNG words and endings, batched against one episode at a time."""
+"""ana_amd.agent's batching on a stand-in decoder (no GPU): every episode's
+tokens, flags and ending are those of the one-episode restatement of
+bend/Agent/Loop.bend (agent_loop_ref) on a stand-in engine with the same
+rule for picks: positions, given tokens, RNG words, budgets and calls."""
 import numpy as np
 import pytest
 
@@ -55,18 +57,38 @@ EPS = [agent.Episode([0, 5, 9, 12], seed=3, budget=30, calls=3),
        agent.Episode([0], seed=11, budget=12, calls=1, first=[40, 41]),
        agent.Episode([0, 7, 7, 7, 7, 7, 2], seed=5, budget=25, calls=0),
        agent.Episode([0, 88, 3], seed=8, budget=40, calls=5, first=[17]),
-       agent.Episode([0, 1 + 1, 60], seed=0, budget=5, calls=2)]
+       agent.Episode([0, 1 + 1, 60], seed=0, budget=5, calls=2),
+       agent.Episode([0, 3], seed=2, budget=40, calls=2)]
 
 
-def test_batched_is_alone():
-    dec = FakeDecoder(len(EPS))
-    together = agent.run(dec, EPS, None, is_call, tool)
-    for i, e in enumerate(EPS):
-        d1 = FakeDecoder(1)
-        alone = agent.run(d1, [e], None, lambda _, t: is_call(i, t), lambda _, t: tool(i, t))[0]
-        assert alone == together[i], i
-        # every token but the last drawn one was fed at its position
-        assert dec.hist[i] == list(e.prompt) + together[i].tokens[:-1]
+def fake_engine(vocab=97, seed_rng=None):
+    """One episode's stand-in engine: FakeDecoder's rule for one slot."""
+    hist, rng = [], seed_rng.copy()
+
+    def feed(t):
+        hist.append(int(t))
+
+    def pick():
+        h = (sum((i + 1) * x for i, x in enumerate(hist)) + int(rng[0] % 1000003)) % vocab
+        rng[0] += np.uint64(7919)
+        rng[3] ^= np.uint64(h + 1)
+        return h
+    return feed, pick, hist
+
+
+def test_batched_matches_loop():
+    from ana_amd import rng_seeded
+    from agent_loop_ref import episode
+    for ct in (None, 11):
+        dec = FakeDecoder(len(EPS))
+        together = agent.run(dec, EPS, None, is_call, tool, call_token=ct)
+        for i, e in enumerate(EPS):
+            feed, pick, hist = fake_engine(seed_rng=rng_seeded(e.seed).astype(np.uint64))
+            want = episode(feed, pick, e, lambda t, i=i: is_call(i, t), lambda t, i=i: tool(i, t), call_token=ct)
+            assert together[i] == want, (ct, i)
+            # the slot saw exactly the restatement's feeds (the last pick's
+            # token is fed only when drawn)
+            assert dec.hist[i] == hist, (ct, i)
 
 
 def test_endings_and_flags():
@@ -74,13 +96,20 @@ def test_endings_and_flags():
     for e, o in zip(EPS, out):
         assert o.why in ("eos", "budget", "calls", "tool")
         assert len(o.tokens) == len(o.drawn)
-        assert o.tokens[: len(e.first)] == list(e.first) and not any(o.drawn[: len(e.first)])
-        assert o.drawn[-1]
-        # a stretch never draws more than its budget
+        assert agent.EOS not in o.tokens
+        # the given tokens lead, up to a call among them (al.resume drops
+        # the rest), and are not drawn
+        g = 0
+        while g < len(o.tokens) and not o.drawn[g]:
+            g += 1
+        assert o.tokens[:g] == list(e.first)[:g] and (g == len(e.first) or is_call(0, [o.tokens[g - 1]]))
+        # a stretch writes at most its budget of picks (given ones count)
         run_ = 0
-        for d in o.drawn:
-            run_ = run_ + 1 if d else 0
+        for t, d in zip(o.tokens, o.drawn):
+            run_ += 1
             assert run_ <= e.budget
+            if is_call(0, [t]):
+                run_ = 0
     assert out[2].why in ("eos", "budget", "calls")
     # the scenario reaches every ending
     assert {o.why for o in out} == {"eos", "budget", "calls", "tool"}
