@@ -452,7 +452,7 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
       return launch_head_pw(g, static_cast<const char*>(c->PK) + pe->off, pe->bf, c->st, ps.start(), ps.stop());
     if (pe)
       return launch_gemm_pk(g, static_cast<const char*>(c->PK) + pe->off, pe->bf, c->st, ps.start(), ps.stop());
-    if (g.B >= 128 && c->d_sah && bf && g.K % 32 == 0 && g.B <= c->rows)
+    if (g.B >= 128 && c->d_sah && bf && g.K % 64 == 0 && g.B <= c->rows)
       return launch_gemm_dl(g, c->d_sah, c->d_rsc, c->rows, c->st, ps.start(), ps.stop());
     if (g.B >= 128) return launch_gemm_big(g, c->st, ps.start(), ps.stop());
     return launch_gemm_mfma(g, c->st, ps.start(), ps.stop());

@@ -312,7 +312,7 @@ hipError_t launch_gemm_big(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nu
                            hipEvent_t e1 = nullptr);
 // ANA_BF16 at 128 rows or more: the activations (times the norm's gain)
 // rounded to bf16 (Ah: B x K; rsc: B norm scales), then the product with
-// both operands streamed straight into LDS (K a multiple of 32)
+// both operands streamed straight into LDS (K a multiple of 64)
 // (cap_rows: the rows Ah and rsc hold; larger batches are rejected)
 hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t cap_rows,
                           hipStream_t st, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);

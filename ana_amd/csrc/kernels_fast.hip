@@ -2215,10 +2215,12 @@ __device__ __forceinline__ void xcd_tile(uint32_t* nt, uint32_t* mt) {
 
 // Y[m][n] = sum_k A[m][k] W[n][k] for ANA_BF16 prefill steps of >= 128 rows,
 // A given as bf16 (k_split): a 128 x 128 tile per workgroup, four waves of
-// 64 x 64 (4 x 4 v_mfma_f32_16x16x32_bf16 tiles). K goes in stages of 32
-// through a ring of NS LDS stages filled by global_load_lds_dwordx4 (no
-// registers between global memory and LDS): each stage holds the A and
-// weight tiles as 1 KB chunks of 16 rows, a row's four 16-byte k pieces at
+// 64 x 64 (4 x 4 v_mfma_f32_16x16x32_bf16 tiles). K goes in stages of 64
+// (a whole 128-byte line of each row; stages of 32 took 6% longer, one
+// barrier per half the work) through a ring of NS LDS stages filled by
+// global_load_lds_dwordx4 (no registers between global memory and LDS):
+// each stage holds the A and weight tiles, each k half as 1 KB chunks of
+// 16 rows, a row's four 16-byte k pieces at
 // physical slot (piece ^ ((row >> 1) & 3)), so a fragment read touches
 // eight distinct 16-byte bank groups. A wave waits on its own loads of the
 // stage it is about to read, then a barrier (no fence, which would wait on
@@ -2229,9 +2231,9 @@ __device__ __forceinline__ void xcd_tile(uint32_t* nt, uint32_t* mt) {
 template <int NS>
 __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __restrict__ Ahg,
                                                   const float* __restrict__ rscg) {
-  constexpr int BM = 128, BN = 128, BK = 32;
-  constexpr int TILE = BM * BK;   // bf16 elements of one operand tile (8 KB)
-  __shared__ __align__(1024) __bf16 lds[NS][2][TILE];
+  constexpr int BM = 128, BN = 128, BK = 64;
+  constexpr int TILE = BM * 32;   // bf16 elements of one operand tile half (8 KB)
+  __shared__ __align__(1024) __bf16 lds[NS][2][2][TILE];
   __shared__ float rsl[BM];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint32_t wm = wv >> 1, wn = wv & 1;
@@ -2261,8 +2263,11 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
 #pragma unroll
     for (int h = 0; h < 2; h++) {
       const uint32_t c = 2 * wv + h;
-      __builtin_amdgcn_global_load_lds((const void*)(Ahg + aoff[h] + k0), (lds_void*)&lds[buf][0][c * 512], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(bptr[h] + k0), (lds_void*)&lds[buf][1][c * 512], 16, 0, 0);
+#pragma unroll
+      for (int kh = 0; kh < 2; kh++) {
+        __builtin_amdgcn_global_load_lds((const void*)(Ahg + aoff[h] + k0 + 32 * kh), (lds_void*)&lds[buf][0][kh][c * 512], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(bptr[h] + k0 + 32 * kh), (lds_void*)&lds[buf][1][kh][c * 512], 16, 0, 0);
+      }
     }
   };
   f32x4_t acc[4][4];
@@ -2277,25 +2282,28 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
   for (int u = 0; u < NS - 1; u++)
     if ((uint32_t)u < nst) issue(u);
   for (uint32_t s = 0; s < nst; s++) {
-    // this wave's loads of stage s are done (4 loads a stage; those of the
+    // this wave's loads of stage s are done (8 loads a stage; those of the
     // NS - 2 later stages may still fly)
-    if (s + NS - 2 < nst) ANA_VMCNT(4 * (NS - 2));
+    if (s + NS - 2 < nst) ANA_VMCNT(8 * (NS - 2));
     else ANA_VMCNT(0);
     __builtin_amdgcn_s_barrier();
     if (s + NS - 1 < nst) issue(s + NS - 1);
     const int buf = s % NS;
-    const __bf16* A0 = &lds[buf][0][0];
-    const __bf16* B0 = &lds[buf][1][0];
-    bf16x8_t bfr[4], ah[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(B0 + (wn * 4 + j) * 512 + foff);
+    for (int kh = 0; kh < 2; kh++) {
+      const __bf16* A0 = &lds[buf][0][kh][0];
+      const __bf16* B0 = &lds[buf][1][kh][0];
+      bf16x8_t bfr[4], ah[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) ah[i] = *reinterpret_cast<const bf16x8_t*>(A0 + (wm * 4 + i) * 512 + foff);
+      for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(B0 + (wn * 4 + j) * 512 + foff);
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+      for (int i = 0; i < 4; i++) ah[i] = *reinterpret_cast<const bf16x8_t*>(A0 + (wm * 4 + i) * 512 + foff);
 #pragma unroll
-      for (int j = 0; j < 4; j++)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bfr[j], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
   }
   const bool norm = a.ng != nullptr;
   // results: tile (i, j) of the wave holds rows wm*64 + 16i + 4*g4 + r,
@@ -2312,7 +2320,7 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
     // 64-row half at a time
     ANA_VMCNT(0);
     __syncthreads();
-    float* up = reinterpret_cast<float*>(&lds[0][0][0]);
+    float* up = reinterpret_cast<float*>(&lds[0][0][0][0]);
     for (uint32_t half = 0; half < 2; half++) {
       if (wn == 1 && wm == half) {
 #pragma unroll
@@ -2382,7 +2390,7 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
 
 hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t cap_rows,
                           hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
-  if (a.amax || (a.K % 32) || a.B == 0 || !a.Wh0 || (a.nseg > 1 && !a.Wh1)) return hipErrorInvalidValue;
+  if (a.amax || (a.K % 64) || a.B == 0 || !a.Wh0 || (a.nseg > 1 && !a.Wh1)) return hipErrorInvalidValue;
   if (a.B > cap_rows) return hipErrorInvalidValue;
   // the split first (its time is inside the events)
   if (e0) (void)hipEventRecord(e0, st);
