@@ -2388,6 +2388,154 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
   }
 }
 
+// The same product on a 256 x 256 tile per workgroup of sixteen waves
+// (wave w: rows 64 (w / 4) .., columns 64 (w % 4) .., 4 x 4 MFMA tiles),
+// for products of 2048 output rows or more at prefill shapes: each staged
+// byte feeds twice the flops it feeds in the 128 x 128 tile. Stages of 64
+// k (both operands, 64 KB) through two LDS buffers, loaded as k_gemm_dl
+// loads them (wave w the rows 16 w .. 16 w + 15 of A and of the weights).
+// SiLU: the tile's columns 0..127 are gate rows j, 128..255 the matching up
+// rows; the up waves hand their results to the gate waves through LDS.
+__global__ __launch_bounds__(1024) void k_gemm_dl2(GemvArgs a, const __bf16* __restrict__ Ahg,
+                                                    const float* __restrict__ rscg) {
+  constexpr int BM = 256, BN = 256, BK = 64, NS = 2;
+  constexpr int TILE = BM * 32;   // bf16 elements of one operand's k half (16 KB)
+  __shared__ __align__(1024) __bf16 lds[NS][2][2][TILE];
+  __shared__ float rsl[BM];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t wm = wv >> 2, wn = wv & 3;
+  uint32_t ntile, mtile;
+  xcd_tile(&ntile, &mtile);
+  const uint32_t m0 = mtile * BM;
+  const uint32_t nb = min((uint32_t)BM, a.B - m0);
+  const uint32_t K = a.K, nst = K / BK;
+  const Segs sgs(a);
+  // this lane's piece of the wave's 1 KB chunk per operand and k half
+  // (chunk wv: tile rows 16 wv .. 16 wv + 15)
+  const uint32_t pr = lane >> 2, pq = (lane & 3) ^ ((pr >> 1) & 3);
+  const uint32_t r0 = 16 * wv + pr;
+  const uint32_t aoff = (m0 + (r0 < nb ? r0 : 0)) * K + 8 * pq;
+  const uint16_t* bptr;
+  {
+    const float* w;
+    uint32_t sg, lr;
+    const bool ok = sgs.row(BN, ntile, r0, &w, &sg, &lr);
+    bptr = ok ? (sg ? a.Wh1 : a.Wh0) + (size_t)lr * K + 8 * pq : a.Wh0 + 8 * pq;
+  }
+  auto issue = [&](uint32_t s) {
+    const int buf = s % NS;
+    const uint32_t k0 = s * BK;
+#pragma unroll
+    for (int kh = 0; kh < 2; kh++) {
+      __builtin_amdgcn_global_load_lds((const void*)(Ahg + aoff + k0 + 32 * kh), (lds_void*)&lds[buf][0][kh][wv * 512], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(bptr + k0 + 32 * kh), (lds_void*)&lds[buf][1][kh][wv * 512], 16, 0, 0);
+    }
+  };
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t r16 = lane & 15, g4 = lane >> 4;
+  const uint32_t foff = r16 * 32 + 8 * (g4 ^ ((r16 >> 1) & 3));
+  issue(0);
+  for (uint32_t s = 0; s < nst; s++) {
+    // this wave's loads of stage s are done, then every wave's; the
+    // barrier also says every wave is done with the buffer stage s + 1 fills
+    ANA_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+    if (s + 1 < nst) issue(s + 1);
+    const int buf = s % NS;
+#pragma unroll
+    for (int kh = 0; kh < 2; kh++) {
+      const __bf16* A0 = &lds[buf][0][kh][0];
+      const __bf16* B0 = &lds[buf][1][kh][0];
+      bf16x8_t bfr[4], ah[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(B0 + (wn * 4 + j) * 512 + foff);
+#pragma unroll
+      for (int i = 0; i < 4; i++) ah[i] = *reinterpret_cast<const bf16x8_t*>(A0 + (wm * 4 + i) * 512 + foff);
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  const bool norm = a.ng != nullptr;
+  // results: tile (i, j) of the wave holds rows wm*64 + 16i + 4*g4 + r,
+  // column wn*64 + 16j + r16; the row norm scales go to LDS first
+  ANA_VMCNT(0);
+  __syncthreads();
+  if (norm) {
+    if (tid < (uint32_t)BM) rsl[tid] = rscg[m0 + (tid < nb ? tid : 0)];
+    __syncthreads();
+  }
+  auto rs = [&](int i, int r) { return norm ? rsl[wm * 64 + 16 * i + 4 * g4 + r] : 1.0f; };
+  if (a.mode == GM_SILU) {
+    // up columns (wn 2, 3) through LDS to the gate columns (wn 0, 1)
+    float* up = reinterpret_cast<float*>(&lds[0][0][0][0]);   // [256][128]
+    if (wn >= 2) {
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r, n = (wn - 2) * 64 + 16 * j + r16;
+            up[m * 128 + n] = acc[i][j][r] * rs(i, r);
+          }
+    }
+    __syncthreads();
+    if (wn < 2) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t n = wn * 64 + 16 * j + r16;
+        const float* w_;
+        uint32_t sg, lr;
+        if (!sgs.row(BN, ntile, n, &w_, &sg, &lr)) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r;
+            if (m >= nb) continue;
+            const float y = acc[i][j][r] * rs(i, r);
+            a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = fast_silu(y) * up[m * 128 + n];
+          }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    // one column block's residuals live at a time
+    asm volatile("" ::: "memory");
+    const uint32_t n = wn * 64 + 16 * j + r16;
+    const float* w_;
+    uint32_t sg, lr;
+    if (!sgs.row(BN, ntile, n, &w_, &sg, &lr)) continue;
+    float res[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r;
+        res[i][r] = a.mode == GM_RESID && m < nb ? a.R[(size_t)(m0 + m) * a.ldr + lr] : 0.0f;
+      }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r;
+        if (m >= nb) continue;
+        float y = acc[i][j][r] * rs(i, r);
+        if (a.mode == GM_RESID) y = res[i][r] + y;
+        if (sg) a.seg[1].Y[(size_t)(m0 + m) * a.seg[1].ldy + lr] = y;
+        else a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = y;
+      }
+  }
+}
+
 hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t cap_rows,
                           hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   if (a.amax || (a.K % 64) || a.B == 0 || !a.Wh0 || (a.nseg > 1 && !a.Wh1)) return hipErrorInvalidValue;
@@ -2397,6 +2545,17 @@ hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t ca
   hipLaunchKernelGGL(k_split, dim3((a.B + 3) / 4), dim3(256), 0, st, a.X, a.ldx, a.K, a.ng, a.B, Ah, rsc);
   const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
                                           : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
+  // the 256 x 256 tiles where they still give every CU a workgroup
+  {
+    const uint32_t per2 = a.mode == GM_SILU ? 128 : 256;
+    const uint32_t tiles2 = a.mode == GM_SILU ? (a.seg[0].rows + per2 - 1) / per2 : (rows + per2 - 1) / per2;
+    const uint32_t mt2 = (a.B + 255) / 256;
+    if (rows >= 2048 && tiles2 * mt2 >= 256) {
+      hipLaunchKernelGGL(k_gemm_dl2, dim3(tiles2, mt2), dim3(1024), 0, st, a, Ah, rsc);
+      if (e1) (void)hipEventRecord(e1, st);
+      return hipGetLastError();
+    }
+  }
   const uint32_t per = a.mode == GM_SILU ? 64 : 128;
   const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
   dim3 grid(tiles, (a.B + 127) / 128);
