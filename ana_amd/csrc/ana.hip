@@ -57,6 +57,8 @@ struct ana_ctx {
   uint32_t* d_tgt = nullptr;         // scoring: each row's target token
   float* d_ce = nullptr;             // scoring: each row's G.lse - logit[target]
   __bf16* d_sah = nullptr;   // ANA_BF16 prefill: a product's activations in bf16
+  __bf16* d_hh = nullptr;    // ANA_BF16 prefill: gate|up's outputs in bf16, down's input
+  bool hh_bf = false;        // d_hh holds the last gate|up's outputs
   float* d_rsc = nullptr;                      // and its rows' norm scales
   // fast modes: every layer product's weights packed for k_gemm_pk (fp32, or
   // bf16 in ANA_BF16; the norm gains folded in), found by the product's first
@@ -83,6 +85,7 @@ struct ana_ctx {
   GlaScratch gla{};                  // its regions
   GlaSub* d_gtab = nullptr;          // a prefill step's sub-chunk table
   uint32_t *d_rseq = nullptr, *d_rpos = nullptr;  // a prefill step's per-row sequence, position
+  uint32_t* d_rcp = nullptr;   // a prefill step's (last row, sequence) pairs for the residual rows
   uint32_t seg_cap = 1, gsub_cap = 1; // chunks a prefill step holds; table entries
   AttnTile* d_atab = nullptr;        // a prefill step's attention tiles
   uint32_t atab_cap = 1;
@@ -192,8 +195,8 @@ static void release(ana_ctx* c) {
   if (c->gexec_n) (void)hipGraphExecDestroy(c->gexec_n);
   void* ps[] = {c->d_play, c->d_ll, c->d_ctl, c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
-                c->d_ss, c->d_pm, c->d_gtab, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce,
-                c->d_sah, c->d_rsc, c->PK};
+                c->d_ss, c->d_pm, c->d_gtab, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce, c->d_rcp,
+                c->d_sah, c->d_hh, c->d_rsc, c->PK};
   for (void* p : ps)
     if (p) (void)hipFree(p);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
@@ -311,6 +314,8 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = dalloc(&c->SC, (uint64_t)c->sc_rows * cf.vocab)) != hipSuccess ||
       (e = dalloc(&c->d_tgt, c->rows)) != hipSuccess || (e = dalloc(&c->d_ce, c->rows)) != hipSuccess)
     return bad(e);
+  // a prefill step's residual-row pairs (every mode)
+  if ((e = dalloc(&c->d_rcp, 2 * (uint64_t)c->rows)) != hipSuccess) return bad(e);
   if (c->mode != ANA_EXACT_FP32) {
     // the fast kernels' scratch: attention partials for every row of a step,
     // the GLA scan's regions and tables
@@ -325,7 +330,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if (c->mode == ANA_BF16) {
     const uint64_t kmax = std::max(d, cf.f);
     if ((e = dalloc(&c->Wh, c->P)) != hipSuccess || (e = dalloc(&c->d_sah, (uint64_t)c->rows * kmax)) != hipSuccess ||
-        (e = dalloc(&c->d_rsc, c->rows)) != hipSuccess)
+        (e = dalloc(&c->d_hh, (uint64_t)c->rows * cf.f)) != hipSuccess || (e = dalloc(&c->d_rsc, c->rows)) != hipSuccess)
       return bad(e);
   }
   if ((e = hipMemcpyAsync(c->W, ck.raw.data(), 4 * c->P, hipMemcpyHostToDevice, c->st)) != hipSuccess) return bad(e);
@@ -430,6 +435,9 @@ static bool reads_bf16(const ana_ctx* c, const GemvArgs& g) {
 
 static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool chunk = false) {
   const bool small = g0.B <= kSmallB;
+  // (d_hh holds this gate|up's outputs only if the path below writes them)
+  const bool hh_was = c->hh_bf;
+  if (g0.mode == GM_SILU) c->hh_bf = false;
   const bool pk_ok = gemm_pk_fits(g0) || (kind == ANA_K_HEAD && head_pw_fits(g0));
   const ana_ctx::PkEnt* pe =
       fast_mode(c) && !small && g0.B < (chunk ? 128u : kPwMaxB) && pk_ok ? find_pk(c, g0) : nullptr;
@@ -452,8 +460,15 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
       return launch_head_pw(g, static_cast<const char*>(c->PK) + pe->off, pe->bf, c->st, ps.start(), ps.stop());
     if (pe)
       return launch_gemm_pk(g, static_cast<const char*>(c->PK) + pe->off, pe->bf, c->st, ps.start(), ps.stop());
-    if (g.B >= 128 && c->d_sah && bf && g.K % 64 == 0 && g.B <= c->rows)
-      return launch_gemm_dl(g, c->d_sah, c->d_rsc, c->rows, c->st, ps.start(), ps.stop());
+    if (g.B >= 128 && c->d_sah && bf && g.K % 64 == 0 && g.B <= c->rows) {
+      // gate|up also leaves its outputs in bf16, and down reads them
+      // there instead of splitting them again
+      if (g.mode == GM_SILU && c->d_hh && gemm_dl2_takes(g)) g.Yh = c->d_hh;
+      if (g.X == c->HH && hh_was && !g.ng && g.K == c->cfg.f) g.Xh = c->d_hh;
+      const hipError_t e = launch_gemm_dl(g, c->d_sah, c->d_rsc, c->rows, c->st, ps.start(), ps.stop());
+      if (g.mode == GM_SILU) c->hh_bf = g.Yh != nullptr && e == hipSuccess;
+      return e;
+    }
     if (g.B >= 128) return launch_gemm_big(g, c->st, ps.start(), ps.stop());
     return launch_gemm_mfma(g, c->st, ps.start(), ps.stop());
   }
@@ -867,18 +882,26 @@ static int feeds_n(ana_ctx* c, const char* fn, uint32_t n, const uint32_t* seq, 
   HIPCHK(c, hipSetDevice(c->device));
   const uint32_t d = c->cfg.d;
   std::vector<Seg> segs;
-  std::vector<uint32_t> rows, tg;
+  std::vector<uint32_t> rows, tg, rcp;
   std::vector<uint64_t> cix;
   std::vector<float> hce;
   auto flush = [&]() -> int {
     if (segs.empty()) return ANA_OK;
     const uint32_t M = (uint32_t)rows.size();
+    // each sequence's residual row is its last row of the step: the
+    // (row, sequence) pairs go up with the step's tokens, and one copy
+    // kernel moves every row after the layers
+    rcp.clear();
+    if (segs.size() > c->rows) return fail(c, ANA_EINVAL, "%s: %zu sequences in one step", fn, segs.size());
+    for (const Seg& sg : segs) {
+      rcp.push_back(sg.row0 + sg.T - 1);
+      rcp.push_back(sg.seq);
+    }
     HIPCHK(c, hipMemcpyAsync(c->d_tok, rows.data(), 4 * (size_t)M, hipMemcpyHostToDevice, c->st));
+    HIPCHK(c, hipMemcpyAsync(c->d_rcp, rcp.data(), 4 * rcp.size(), hipMemcpyHostToDevice, c->st));
     HIPCHK(c, launch_embed(c->W, c->d_tok, d, M, c->X, nullptr, c->st));
     if (int r = run_layers(c, M, nullptr, nullptr, &segs)) return r;
-    for (const Seg& sg : segs)
-      HIPCHK(c, hipMemcpyAsync(c->xs + (uint64_t)sg.seq * d, c->X + (uint64_t)(sg.row0 + sg.T - 1) * d,
-                               4 * (size_t)d, hipMemcpyDeviceToDevice, c->st));
+    HIPCHK(c, launch_copy_rows(c->X, c->d_rcp, (uint32_t)segs.size(), d, c->xs, c->st));
     if (ce) {
       HIPCHK(c, hipMemcpyAsync(c->d_tgt, tg.data(), 4 * (size_t)M, hipMemcpyHostToDevice, c->st));
       for (uint32_t r0 = 0; r0 < M; r0 += c->sc_rows) {

@@ -67,6 +67,8 @@ struct GemvArgs {
                              // (small batches only)
   const uint16_t* Wh0;       // fast products: the segments' rows as bfloat16
   const uint16_t* Wh1;       // (nullptr: read the fp32 rows)
+  __bf16* Yh;                // ANA_BF16 prefill, SiLU: the outputs in bf16 too, [B][seg0.rows]
+  const __bf16* Xh;          // ANA_BF16 prefill, no norm: X already in bf16, [B][K]
 };
 // The two row segments as plain values (a runtime index into GemvArgs.seg
 // would send every lookup through memory).
@@ -211,6 +213,9 @@ hipError_t launch_gather_rows(const float* src, const uint32_t* idx, uint32_t n,
                               float* dst, hipStream_t st);
 hipError_t launch_scatter_rows(const float* src, const uint32_t* idx, uint32_t n, uint32_t d,
                                float* dst, hipStream_t st);
+// dst row pairs[2 b + 1] = src row pairs[2 b] for b < n (pairs on the device)
+hipError_t launch_copy_rows(const float* src, const uint32_t* pairs, uint32_t n, uint32_t d, float* dst,
+                            hipStream_t st);
 // The token loop's step end for B sequences: the pick (from the sampler's
 // pick[b], or greedy: the amax key or top[b] of dd.pick, falling back to
 // Sample.argmax over the logits when there is none), recorded at
@@ -314,6 +319,9 @@ hipError_t launch_gemm_big(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nu
 // rounded to bf16 (Ah: B x K; rsc: B norm scales), then the product with
 // both operands streamed straight into LDS (K a multiple of 64)
 // (cap_rows: the rows Ah and rsc hold; larger batches are rejected)
+// whether launch_gemm_dl takes product a on its 256 x 256 tiles (the only
+// ones that write Yh)
+bool gemm_dl2_takes(const GemvArgs& a);
 hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t cap_rows,
                           hipStream_t st, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 size_t attn_fast_part_floats(uint32_t B, uint32_t heads, uint32_t ctx, uint32_t hd);

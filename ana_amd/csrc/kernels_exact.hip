@@ -1137,6 +1137,22 @@ hipError_t launch_scatter_rows(const float* src, const uint32_t* idx, uint32_t n
   return hipGetLastError();
 }
 
+// dst row pairs[2 b + 1] = src row pairs[2 b], for every b < n
+__global__ void k_copy_rows(const float* __restrict__ src, const uint32_t* __restrict__ pairs, uint32_t d,
+                            float* __restrict__ dst) {
+  const uint32_t b = blockIdx.x;
+  const float* s = src + (size_t)pairs[2 * b] * d;
+  float* t = dst + (size_t)pairs[2 * b + 1] * d;
+  for (uint32_t j = threadIdx.x; j < d; j += blockDim.x) t[j] = s[j];
+}
+
+hipError_t launch_copy_rows(const float* src, const uint32_t* pairs, uint32_t n, uint32_t d, float* dst,
+                            hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_copy_rows, dim3(n), dim3(256), 0, st, src, pairs, d, dst);
+  return hipGetLastError();
+}
+
 __global__ void k_zero(float* p, uint64_t n) {
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (uint64_t)gridDim.x * blockDim.x)

@@ -2500,7 +2500,9 @@ __global__ __launch_bounds__(1024) void k_gemm_dl2(GemvArgs a, const __bf16* __r
             const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r;
             if (m >= nb) continue;
             const float y = acc[i][j][r] * rs(i, r);
-            a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = fast_silu(y) * up[m * 128 + n];
+            const float hv = fast_silu(y) * up[m * 128 + n];
+            a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = hv;
+            if (a.Yh) a.Yh[(size_t)(m0 + m) * a.seg[0].rows + lr] = (__bf16)hv;
           }
       }
     }
@@ -2536,26 +2538,32 @@ __global__ __launch_bounds__(1024) void k_gemm_dl2(GemvArgs a, const __bf16* __r
   }
 }
 
+bool gemm_dl2_takes(const GemvArgs& a) {
+  const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
+                                          : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
+  const uint32_t tiles2 = a.mode == GM_SILU ? (a.seg[0].rows + 127) / 128 : (rows + 255) / 256;
+  return rows >= 2048 && tiles2 * ((a.B + 255) / 256) >= 256;
+}
+
 hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t cap_rows,
                           hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   if (a.amax || (a.K % 64) || a.B == 0 || !a.Wh0 || (a.nseg > 1 && !a.Wh1)) return hipErrorInvalidValue;
   if (a.B > cap_rows) return hipErrorInvalidValue;
-  // the split first (its time is inside the events)
+  if (a.Xh && a.ng) return hipErrorInvalidValue;   // (bf16 input takes no norm)
+  // the split first (its time is inside the events), unless X came in bf16
   if (e0) (void)hipEventRecord(e0, st);
-  hipLaunchKernelGGL(k_split, dim3((a.B + 3) / 4), dim3(256), 0, st, a.X, a.ldx, a.K, a.ng, a.B, Ah, rsc);
+  if (a.Xh) Ah = const_cast<__bf16*>(a.Xh);
+  else hipLaunchKernelGGL(k_split, dim3((a.B + 3) / 4), dim3(256), 0, st, a.X, a.ldx, a.K, a.ng, a.B, Ah, rsc);
   const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
                                           : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
   // the 256 x 256 tiles where they still give every CU a workgroup
-  {
-    const uint32_t per2 = a.mode == GM_SILU ? 128 : 256;
-    const uint32_t tiles2 = a.mode == GM_SILU ? (a.seg[0].rows + per2 - 1) / per2 : (rows + per2 - 1) / per2;
-    const uint32_t mt2 = (a.B + 255) / 256;
-    if (rows >= 2048 && tiles2 * mt2 >= 256) {
-      hipLaunchKernelGGL(k_gemm_dl2, dim3(tiles2, mt2), dim3(1024), 0, st, a, Ah, rsc);
-      if (e1) (void)hipEventRecord(e1, st);
-      return hipGetLastError();
-    }
+  if (gemm_dl2_takes(a)) {
+    const uint32_t tiles2 = a.mode == GM_SILU ? (a.seg[0].rows + 127) / 128 : (rows + 255) / 256;
+    hipLaunchKernelGGL(k_gemm_dl2, dim3(tiles2, (a.B + 255) / 256), dim3(1024), 0, st, a, Ah, rsc);
+    if (e1) (void)hipEventRecord(e1, st);
+    return hipGetLastError();
   }
+  if (a.Yh) return hipErrorInvalidValue;   // (only the 256 x 256 tiles write bf16 outputs)
   const uint32_t per = a.mode == GM_SILU ? 64 : 128;
   const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
   dim3 grid(tiles, (a.B + 127) / 128);

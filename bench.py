@@ -241,19 +241,24 @@ def run_agent(path: str, c, mode: str) -> dict:
                         "2 calls; a call: drawn id = 7 mod 61; echo 24 ids fed unsampled); " + NUMERICS[mode]}
 
 
-def run_prefill(path: str, c) -> dict:
+def run_prefill(path: str, c, reps: int = 5) -> dict:
     """B=64 prefill on the matrix cores: 64 prompts of 512 tokens through
-    ana_feeds_n at chunk 128 (8192 rows a product), in both fast modes."""
+    ana_feeds_n at chunk 128 (8192 rows a product), in both fast modes; the
+    median of `reps` timed passes (one pass is about 25 ms, short enough for
+    clock ramps to move it by a fifth)."""
     extra = {}
     for m in ("bf16", "fast_fp32"):
         with ana_amd.Decoder(path, max_seqs=64, prefill_chunk=128, numerics=MODES[m]) as dec:
             prs = [ckpt.prompt(1000 + b, 512, c.vocab) for b in range(64)]
             dec.feeds_n(list(range(64)), [0] * 64, [pr[:64] for pr in prs])   # warm-up
-            for b in range(64):
-                dec.reset(b)
-            t = time.perf_counter()
-            dec.feeds_n(list(range(64)), [0] * 64, prs)
-            dt = time.perf_counter() - t
+            runs = []
+            for _ in range(reps):
+                for b in range(64):
+                    dec.reset(b)
+                t = time.perf_counter()
+                dec.feeds_n(list(range(64)), [0] * 64, prs)
+                runs.append(time.perf_counter() - t)
+            dt = float(np.median(runs))
         ntok, L = 64 * 512, 512
         # the products, plus causal attention in the softmax layers
         # (q k and p v over the live slots: 2 x 2 x L^2 / 2 x d per
@@ -263,13 +268,14 @@ def run_prefill(path: str, c) -> dict:
         peak = 2500.0 if m == "bf16" else 157.3
         extra[f"prefill_b64_{m}"] = {
             "tok_s": round(ntok / dt, 1), "seconds": round(dt, 4),
+            "runs_s": [round(x, 4) for x in runs],
             "tflops": round(flops / dt / 1e12, 2), "peak_tflops": peak,
             "frac": round(flops / dt / 1e12 / peak, 4),
             "workload": "64 prompts x 512 tokens through ana_feeds_n, chunk 128; flops = 2 x "
                         "(P - v d) per token (the products) + causal attention 2 B L^2 d per "
                         "softmax layer (the GLA scan not counted)",
-            "kernels": ("products k_split + k_gemm_dl (128 x 128 MFMA tiles, bf16 weights x bf16 "
-                        "activations, both streamed straight into LDS; block 0 in fp32)" if m == "bf16" else
+            "kernels": ("products k_split + k_gemm_dl2 / k_gemm_dl (256 x 256 and 128 x 128 MFMA tiles, "
+                        "bf16 weights x bf16 activations, both streamed straight into LDS)" if m == "bf16" else
                         "products k_gemm_big (128 x 128 MFMA tiles, fp32 MFMA)")
                        + ", attention k_attn_flash (fp32 MFMA), GLA k_gla_sub + k_gla_carry",
         }
@@ -279,14 +285,18 @@ def run_prefill(path: str, c) -> dict:
         with ana_amd.Decoder(path, max_seqs=64, prefill_chunk=128, numerics=MODES[m]) as dec:
             ws = [ckpt.prompt(2000 + b, 513, c.vocab) for b in range(64)]
             dec.score_n(list(range(64)), [0] * 64, [w[:65] for w in ws])   # warm-up
-            for b in range(64):
-                dec.reset(b)
-            t = time.perf_counter()
-            ce = dec.score_n(list(range(64)), [0] * 64, ws)
-            dt = time.perf_counter() - t
+            runs = []
+            for _ in range(reps):
+                for b in range(64):
+                    dec.reset(b)
+                t = time.perf_counter()
+                ce = dec.score_n(list(range(64)), [0] * 64, ws)
+                runs.append(time.perf_counter() - t)
+            dt = float(np.median(runs))
         loss = float(np.mean([ana_amd.window_mean(x) for x in ce]))
         extra[f"score_b64_{m}"] = {
             "tok_s": round(ntok / dt, 1), "seconds": round(dt, 4), "mean_window_loss": round(loss, 4),
+            "runs_s": [round(x, 4) for x in runs],
             "workload": "64 windows x 513 tokens through ana_score_n, chunk 128: prefill plus the "
                         "head and G.lse - logit[next] on every one of the 32768 positions",
         }
@@ -307,6 +317,7 @@ def main() -> int:
     ap.add_argument("--prefill", type=int, default=1, help="also measure B=64 x 512 prefill (1/0)")
     ap.add_argument("--prefill-only", type=int, default=0,
                     help="measure only the B=64 x 512 prefill and print its figures (1/0)")
+    ap.add_argument("--reps", type=int, default=5, help="timed passes of each prefill and scoring figure (the median is reported)")
     ap.add_argument("--agent", type=int, default=1, help="also measure 64 agent episodes (1/0)")
     ap.add_argument("--configs", type=int, default=1, help="also measure BASELINE's next, v3 and bf16 decode configs (1/0)")
     ap.add_argument("--configs-only", type=int, default=0, help="print only those configs' JSON (the child run)")
@@ -321,7 +332,7 @@ def main() -> int:
     path = ensure_ckpt(c, a.ckpt)
     mode = a.numerics
     if a.prefill_only:
-        print(json.dumps(run_prefill(path, c)), flush=True)
+        print(json.dumps(run_prefill(path, c, a.reps)), flush=True)
         release_device()
         return 0
     if a.configs_only:
@@ -384,7 +395,7 @@ def main() -> int:
             extra[key]["workload"] = ("B=64, 128-token prompts (ana_feeds_n, chunk 64), 8 untimed then 32 "
                                       "timed greedy steps at positions 135+; " + NUMERICS[m])
     if a.prefill:
-        extra.update(run_prefill(path, c))
+        extra.update(run_prefill(path, c, a.reps))
     if a.agent:
         extra["agent"] = run_agent(path, c, mode)
     extra.update(cfg_lines)
