@@ -84,6 +84,7 @@ struct ana_ctx {
   float* d_gla = nullptr;            // fast prefill's GLA scan scratch
   GlaScratch gla{};                  // its regions
   GlaSub* d_gtab = nullptr;          // a prefill step's sub-chunk table
+  GlaRun* d_grun = nullptr;          // and its chunk table
   uint32_t *d_rseq = nullptr, *d_rpos = nullptr;  // a prefill step's per-row sequence, position
   uint32_t* d_rcp = nullptr;   // a prefill step's (last row, sequence) pairs for the residual rows
   uint32_t seg_cap = 1, gsub_cap = 1; // chunks a prefill step holds; table entries
@@ -92,6 +93,7 @@ struct ana_ctx {
   // host copies of the step tables, kept until the step's synchronize
   std::vector<AttnTile> h_atab;
   std::vector<GlaSub> h_gtab;
+  std::vector<GlaRun> h_grun;
   std::vector<uint32_t> h_rseq, h_rpos;
   std::string err;
   // ana_generate's decode step captured as HIP graphs, replayed per step:
@@ -195,7 +197,7 @@ static void release(ana_ctx* c) {
   if (c->gexec_n) (void)hipGraphExecDestroy(c->gexec_n);
   void* ps[] = {c->d_play, c->d_ll, c->d_ctl, c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
-                c->d_ss, c->d_pm, c->d_gtab, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce, c->d_rcp,
+                c->d_ss, c->d_pm, c->d_gtab, c->d_grun, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce, c->d_rcp,
                 c->d_sah, c->d_hh, c->d_rsc, c->PK};
   for (void* p : ps)
     if (p) (void)hipFree(p);
@@ -322,7 +324,8 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
     c->part_cap = attn_fast_part_floats(c->rows, cf.heads, cf.ctx, hd);
     if ((e = dalloc(&c->d_part, c->part_cap)) != hipSuccess ||
         (e = dalloc(&c->d_gla, gla_scan_floats(c->rows, c->gsub_cap, c->seg_cap, d, cf.heads))) != hipSuccess ||
-        (e = dalloc(&c->d_gtab, c->gsub_cap)) != hipSuccess || (e = dalloc(&c->d_atab, c->atab_cap)) != hipSuccess ||
+        (e = dalloc(&c->d_gtab, c->gsub_cap)) != hipSuccess || (e = dalloc(&c->d_grun, c->seg_cap)) != hipSuccess ||
+        (e = dalloc(&c->d_atab, c->atab_cap)) != hipSuccess ||
         (e = dalloc(&c->d_rseq, c->rows)) != hipSuccess || (e = dalloc(&c->d_rpos, c->rows)) != hipSuccess)
       return bad(e);
     c->gla = gla_scan_carve(c->d_gla, c->rows, c->gsub_cap, c->seg_cap, d, cf.heads);
@@ -638,10 +641,11 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
   // a fast mode's prefill step: the GLA scan's sub-chunk table and each row's
   // sequence and position, uploaded once for every layer
   uint32_t nsub = 0;
-  bool fresh_all = true;
+  bool fresh_all = true, gla_run = true;
   if (chunk && fast_mode(c)) {
     if (segs->size() > c->seg_cap) return fail(c, ANA_EINVAL, "prefill step of %zu chunks (at most %u)", segs->size(), c->seg_cap);
     c->h_gtab.clear();
+    c->h_grun.clear();
     c->h_atab.clear();
     c->h_rseq.resize(B);
     c->h_rpos.resize(B);
@@ -650,6 +654,8 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
       const uint32_t ns = (sg.T + kGlaSub - 1) / kGlaSub;
       for (uint32_t j = 0; j < ns; j++)
         c->h_gtab.push_back(GlaSub{sg.row0 + j * kGlaSub, std::min(kGlaSub, sg.T - j * kGlaSub), j, ns, sg.seq, si, 0, 0});
+      c->h_grun.push_back(GlaRun{sg.row0, sg.T, sg.seq, 0});
+      if (sg.T > kGlaRunMaxT) gla_run = false;
       for (uint32_t t = 0; t < sg.T; t++) {
         c->h_rseq[sg.row0 + t] = sg.seq;
         c->h_rpos[sg.row0 + t] = sg.pos0 + t;
@@ -664,7 +670,10 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
     if (c->h_atab.size() > c->atab_cap) return fail(c, ANA_EINVAL, "prefill step of %zu attention tiles (at most %u)", c->h_atab.size(), c->atab_cap);
     if (fresh_all && !c->h_atab.empty())
       HIPCHK(c, hipMemcpyAsync(c->d_atab, c->h_atab.data(), sizeof(AttnTile) * c->h_atab.size(), hipMemcpyHostToDevice, c->st));
-    HIPCHK(c, hipMemcpyAsync(c->d_gtab, c->h_gtab.data(), sizeof(GlaSub) * nsub, hipMemcpyHostToDevice, c->st));
+    if (gla_run)
+      HIPCHK(c, hipMemcpyAsync(c->d_grun, c->h_grun.data(), sizeof(GlaRun) * c->h_grun.size(), hipMemcpyHostToDevice, c->st));
+    else
+      HIPCHK(c, hipMemcpyAsync(c->d_gtab, c->h_gtab.data(), sizeof(GlaSub) * nsub, hipMemcpyHostToDevice, c->st));
     HIPCHK(c, hipMemcpyAsync(c->d_rseq, c->h_rseq.data(), 4 * (size_t)B, hipMemcpyHostToDevice, c->st));
     HIPCHK(c, hipMemcpyAsync(c->d_rpos, c->h_rpos.data(), 4 * (size_t)B, hipMemcpyHostToDevice, c->st));
   }
@@ -685,9 +694,14 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
         HIPCHK(c, launch_gla_step(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), seq,
                                   c->O, d, cf.heads, cf.rglru, B, c->st));
     } else if (b.gla && fast_mode(c)) {
-      // every chunk of the step at once: the closed-form chunked scan
-      HIPCHK(c, launch_gla_scan(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), c->O, c->gla,
-                                c->d_gtab, nsub, d, cf.heads, cf.rglru, c->st));
+      // every chunk of the step at once: a workgroup per (head, chunk)
+      // through its sub-chunks, or the closed-form chunked scan
+      if (gla_run)
+        HIPCHK(c, launch_gla_run(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), c->O, c->d_grun,
+                                 (uint32_t)c->h_grun.size(), c->rows, d, cf.heads, cf.rglru, c->st));
+      else
+        HIPCHK(c, launch_gla_scan(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), c->O, c->gla,
+                                  c->d_gtab, nsub, d, cf.heads, cf.rglru, c->st));
     } else if (b.gla) {
       for (const Seg& sg : *segs) {
         float* S = c->state + (uint64_t)sg.seq * c->seq_stride + c->layer_off[l];

@@ -285,6 +285,21 @@ struct GlaScratch {
   float *Qt, *Dj, *Uj, *S0;
   uint32_t rows_cap, nsub_cap, nseg_cap;  // what the regions were carved for
 };
+// One chunk of a prefill step for k_gla_run: one workgroup per (head,
+// chunk) walks its sub-chunks in order, the state in LDS. Chunks of at most
+// kGlaRunMaxT tokens take it (a few sequential sub-chunks, and a tenth of
+// the scan's traffic); longer ones the scan.
+struct GlaRun {
+  uint32_t row;   // first workspace row
+  uint32_t T;     // tokens
+  uint32_t seq;   // state slot
+  uint32_t pad;
+};
+constexpr uint32_t kGlaRunMaxT = 8 * kGlaSub;
+// (rows: the workspace rows QKV and Z hold)
+hipError_t launch_gla_run(const float* QKV, const float* Z, const float* lam, StateRef S, float* O,
+                          const GlaRun* runs, uint32_t nrun, uint32_t rows, uint32_t d, uint32_t heads,
+                          uint32_t rglru, hipStream_t st);
 size_t gla_scan_floats(uint32_t rows, uint32_t nsub, uint32_t nseg, uint32_t d, uint32_t heads);
 GlaScratch gla_scan_carve(float* p, uint32_t rows, uint32_t nsub, uint32_t nseg, uint32_t d,
                           uint32_t heads);

@@ -26,6 +26,7 @@
 
 #include "ana_internal.h"
 #include "numerics.h"
+#include "wave.h"
 
 namespace ana {
 
@@ -35,38 +36,6 @@ constexpr uint32_t kPT = 256;           // threads per workgroup
 constexpr uint32_t kMaxPLayers = 64;    // layers the persistent kernel takes
 constexpr uint32_t kPollMax = 1u << 20; // polls before a wait gives up
 
-// a DPP move of v (lane permutation dpp_ctrl within each row of 16 lanes)
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
-}
-// the sum over each row of 16 lanes, in every lane of the row: lane ^ 1 and
-// lane ^ 2 (quad_perm), then the mirrored quad (row_half_mirror), then the
-// mirrored half-row (row_mirror)
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp<0xB1>(v);
-  v += dpp<0x4E>(v);
-  v += dpp<0x141>(v);
-  v += dpp<0x140>(v);
-  return v;
-}
-__device__ __forceinline__ float lane_f(float v, int l) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
-}
-// the sum over the wave (every lane gets it): the rows' sums by DPP, then
-// the four rows' by lane reads
-__device__ __forceinline__ float wsum(float v) {
-  v = row16_sum(v);
-  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
-}
-// the maximum over the wave, the same way
-__device__ __forceinline__ float wmax(float v) {
-  v = fmaxf(v, dpp<0xB1>(v));
-  v = fmaxf(v, dpp<0x4E>(v));
-  v = fmaxf(v, dpp<0x141>(v));
-  v = fmaxf(v, dpp<0x140>(v));
-  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
-}
 
 __device__ __forceinline__ void ll_put(unsigned long long* p, float v, uint32_t ep) {
   __hip_atomic_store(p, ((unsigned long long)ep << 32) | __float_as_uint(v), __ATOMIC_RELAXED,

@@ -13,6 +13,7 @@
 
 #include "ana_internal.h"
 #include "numerics.h"
+#include "wave.h"
 
 namespace ana {
 
@@ -1630,6 +1631,69 @@ namespace ana {
 
 // ------------------------------------------------------------------ GLA over prefill chunks
 
+// The pair weights of a kGlaSub-token sub-chunk: P[t][s] =
+// sum_a qh_t[a] kh_s[a] e^(c_t[a] - c_s[a]) for s <= t < n, zero elsewhere
+// (c the running sum of log a inside the sub-chunk, non-increasing). A pair
+// s < t goes by the highest bit in which t and s differ: at level l they sit
+// in one 2^(l+1)-token block, t in its upper half, s in its lower one, and
+// with r the first token of the upper half
+//   e^(c_t - c_s) = e^(c_t - c_r) e^(c_r - c_s), both exponents <= 0,
+// so the pairs of a level are the in-block entries of one 16 x 16 product of
+// the 16 upper-half rows qh_t e^(c_t - c_r) by the 16 lower-half columns
+// kh_s e^(c_r - c_s) (v_mfma_f32_16x16x4f32; lane l: row l % 16 and column
+// l % 16 at k = l / 16 of each step of 4; result rows 4 (l / 16) + r).
+// Levels 1-4 take one wave each; the diagonal (exponent 0) and level 0's 16
+// neighbour pairs are sums over a on lane groups. Reads qh, kh, cl; writes
+// every entry of P once; the caller synchronises after.
+template <int HD>
+__device__ __forceinline__ void gla_pairs(const float (*qh)[HD + 1], const float (*kh)[HD + 1],
+                                          const float (*cl)[HD + 1], float (*P)[kGlaSub + 1],
+                                          uint32_t n, uint32_t tid) {
+  constexpr int L = kGlaSub;
+  static_assert(L == 32 && HD % 16 == 0, "five levels of 16 x 16 tiles");
+  // above the diagonal and past the last token: zero
+  for (uint32_t e = tid; e < (uint32_t)L * L; e += 256) {
+    const uint32_t t = e / L, s = e % L;
+    if (s > t || t >= n) P[t][s] = 0.0f;
+  }
+  {  // the diagonal, 8 lanes a token
+    const uint32_t t = tid >> 3, l = tid & 7;
+    float p = 0.0f;
+    for (uint32_t a = l; a < (uint32_t)HD; a += 8) p = fmaf(qh[t][a], kh[t][a], p);
+#pragma unroll
+    for (int m = 4; m >= 1; m >>= 1) p += __shfl_xor(p, m, 64);
+    if (l == 0 && t < n) P[t][t] = p;
+  }
+  {  // level 0: (2i + 1, 2i), 16 lanes a pair
+    const uint32_t i = tid >> 4, l = tid & 15, t = 2 * i + 1, s2 = 2 * i;
+    float p = 0.0f;
+    for (uint32_t a = l; a < (uint32_t)HD; a += 16)
+      p = fmaf(qh[t][a] * kh[s2][a], __expf(cl[t][a] - cl[s2][a]), p);
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) p += __shfl_xor(p, m, 64);
+    if (l == 0 && t < n) P[t][s2] = p;
+  }
+  // levels 1-4 on the matrix cores
+  const uint32_t lane = tid & 63, lv = (tid >> 6) + 1, r16 = lane & 15, g4 = lane >> 4;
+  const uint32_t lo = (1u << lv) - 1;
+  const uint32_t ti = ((r16 >> lv) << (lv + 1)) | (1u << lv) | (r16 & lo), rt = ti & ~lo;
+  const uint32_t si = ((r16 >> lv) << (lv + 1)) | (r16 & lo), rs = (si & ~lo) | (1u << lv);
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int k0 = 0; k0 < HD; k0 += 4) {
+    const uint32_t a = k0 + g4;
+    const float x = qh[ti][a] * __expf(cl[ti][a] - cl[rt][a]);
+    const float y = kh[si][a] * __expf(cl[rs][a] - cl[si][a]);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc, 0, 0, 0);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const uint32_t i = 4 * g4 + r;
+    const uint32_t t = ((i >> lv) << (lv + 1)) | (1u << lv) | (i & lo);
+    if ((i >> lv) == (r16 >> lv) && t < n) P[t][si] = acc[r];
+  }
+}
+
 // T tokens of one sequence through one head's GLA (bend/Dense/Decode.bend
 // dd.gla over a chunk): the recurrence S_t = diag(a_t) S_(t-1) + kh_t v_t^T,
 // o_t = qh_t^T S_t, taken kGlaSub tokens at a time in closed form. With c_t
@@ -1650,9 +1714,7 @@ namespace ana {
 // state. The matrix products run on v_mfma_f32_16x16x4f32 (lane l: row
 // l % 16 of the left operand and column l % 16 of the right at k = l / 16 of
 // each step of 4; result rows 4 (l / 16) + r): o_intra = P V, U = Kd^T V,
-// and pass 2's qt S; and P's pairs across the sub-chunk's two 16-token
-// halves (t >= 16 > s) as (qh_t e^(c_t - c_16)) . (kh_s e^(c_16 - c_s)),
-// both exponents <= 0. Pairs inside a half keep e^(c_t - c_s) per term.
+// and pass 2's qt S; P itself by gla_pairs.
 template <int HD>
 __global__ __launch_bounds__(256) void k_gla_sub(const float* __restrict__ QKV,
                                                   const float* __restrict__ Z,
@@ -1742,30 +1804,9 @@ __global__ __launch_bounds__(256) void k_gla_sub(const float* __restrict__ QKV,
     g.Qt[(size_t)(s0 + t) * d + h * HD + a] = qh[t][a] * __expf(cl[t][a]);
   }
   if (tid < (uint32_t)HD) g.Dj[((size_t)J * heads + h) * HD + tid] = __expf(cl[n - 1][tid]);
-  static_assert(L == 32 && HD % 16 == 0, "two 16-token halves, 16-wide tiles");
-  const uint32_t lane = tid & 63, wv = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
-  // P inside each half, term by term; P across the halves on wave 0
-  for (uint32_t e = tid; e < (uint32_t)L * L; e += 256) {
-    const uint32_t t = e / L, s = e % L;
-    if (t >= 16 && s < 16) continue;
-    float p = 0.0f;
-    if (s <= t && t < n)
-      for (int a = 0; a < HD; a++) p = fmaf(qh[t][a] * kh[s][a], __expf(cl[t][a] - cl[s][a]), p);
-    P[t][s] = p;
-  }
-  if (wv == 0) {
-    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    const uint32_t ti = 16 + r16, si = r16;
-    for (int k0 = 0; k0 < HD; k0 += 4) {
-      const uint32_t a = k0 + g4;
-      const float x = qh[ti][a] * __expf(cl[ti][a] - cl[16][a]);
-      const float y = kh[si][a] * __expf(cl[16][a] - cl[si][a]);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc, 0, 0, 0);
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++) P[16 + 4 * g4 + r][r16] = 16 + 4 * g4 + r < n ? acc[r] : 0.0f;
-  }
+  gla_pairs<HD>(qh, kh, cl, P, n, tid);
   __syncthreads();
+  const uint32_t lane = tid & 63, wv = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
   // kh_s e^(c_last - c_s) in place (P holds what needed kh); the intra terms
   // o = P V, 16 x 16 tiles (t half, column block)
   for (uint32_t e = tid; e < (uint32_t)L * HD; e += 256) {
@@ -1865,6 +1906,165 @@ __global__ __launch_bounds__(256) void k_gla_carry(GlaScratch g, StateRef S, flo
       if (t < n) O[(size_t)(s0 + t) * d + h * HD + cb * CB + r16] += acc[r];
     }
   }
+}
+
+// Every chunk of a prefill step through one head's GLA in one workgroup:
+// its kGlaSub-token sub-chunks in order (the host gives it chunks of at most
+// kGlaRunMaxT tokens; longer ones take the scan, whose sub-chunks run in
+// parallel). Per sub-chunk, with c, P, qt and Kd as in k_gla_sub,
+//   o_t = sum_(s<=t) P_ts v_s + qt_t^T S,   S <- diag(e^(c_last)) S + Kd^T V.
+// The state lives in the waves' MFMA accumulators: wave w holds column block
+// w % (HD / 16) of S, every row block, as the 16 x 16 result tiles of
+// Kd^T V (lane l: rows 16 ab + 4 (l / 16) + y, column l % 16), and the qt S
+// product takes its k steps in that same order (step (ab, y): k = 16 ab +
+// 4 (l / 16) + y), so the accumulators are its right operand as they stand.
+// S is read and written once per chunk and never passes through LDS; with
+// HD < 64 the waves past the column blocks hold copies. Thread (a, token
+// block) holds column a of TPT consecutive tokens: the L2 norms are sums
+// over the HD lanes of its group, the running sums of log a run in
+// registers and only the block totals pass through LDS.
+template <int HD, int TPT>
+__device__ __forceinline__ void gla_run_load(const float* __restrict__ QKV, const float* __restrict__ Z,
+                                             uint32_t row, uint32_t T, uint32_t j0, uint32_t tb, uint32_t col,
+                                             uint32_t d, float (&q)[TPT], float (&k)[TPT], float (&v)[TPT],
+                                             float (&z)[TPT]) {
+#pragma unroll
+  for (int i = 0; i < TPT; i++) {
+    const uint32_t t = j0 + tb * TPT + i;
+    q[i] = k[i] = v[i] = z[i] = 0.0f;
+    if (t < T) {
+      const uint32_t o = (row + t) * 3 * d + col;  // (the launcher checks rows x 3 d < 2^32)
+      q[i] = QKV[o];
+      k[i] = QKV[o + d];
+      v[i] = QKV[o + 2 * d];
+      z[i] = Z[(row + t) * d + col];
+    }
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256, 3) void k_gla_run(const float* __restrict__ QKV,
+                                                     const float* __restrict__ Z,
+                                                     const float* __restrict__ lam, float* __restrict__ O,
+                                                     StateRef S, const GlaRun* __restrict__ runs, uint32_t d,
+                                                     uint32_t rglru) {
+  constexpr int L = kGlaSub, TPA = 256 / HD, TPT = L / TPA, CBS = HD / 16, R = 4 / CBS;
+  static_assert(TPT >= 1 && TPA * TPT == L && CBS * R == 4, "whole tokens a thread, a column block a wave");
+  __shared__ float qh[L][HD + 1], kh[L][HD + 1], cl[L][HD + 1], vv[L][HD + 1];
+  __shared__ float P[L][L + 1], tot[TPA][HD];
+  const uint32_t h = blockIdx.x, tid = threadIdx.x;
+  const GlaRun r = runs[blockIdx.y];
+  const uint32_t a = tid % HD, tb = tid / HD, col = h * HD + a;
+  const uint32_t lane = tid & 63, wv = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+  const uint32_t bw = wv % CBS, rep = wv / CBS;
+  float* Sg = S.base + (size_t)r.seq * S.seq_stride + S.layer_off + (size_t)h * HD * HD;
+  f32x4_t Sr[CBS];
+#pragma unroll
+  for (int ab = 0; ab < CBS; ab++)
+#pragma unroll
+    for (int y = 0; y < 4; y++) Sr[ab][y] = Sg[(16 * ab + 4 * g4 + y) * HD + 16 * bw + r16];
+  const float lv = rglru ? f_log_sigmoid(lam[col]) : 0.0f;
+  for (uint32_t j0 = 0; j0 < r.T; j0 += L) {
+    const uint32_t n = min((uint32_t)L, r.T - j0);
+    float q[TPT], k[TPT], v[TPT], z[TPT], lq[TPT], lk[TPT], c[TPT];
+    gla_run_load<HD, TPT>(QKV, Z, r.row, r.T, j0, tb, col, d, q, k, v, z);
+    // norms, gates (dd.gate) and the running sum inside the token block
+#pragma unroll
+    for (int i = 0; i < TPT; i++) {
+      const float sq = group_sum<HD>(q[i] * q[i]), sk = group_sum<HD>(k[i] * k[i]);
+      float la = 0.0f;
+      lq[i] = lk[i] = 0.0f;
+      if (tb * TPT + i < n) {
+        // (the hardware's reciprocal square root, exp and log, ~1 ulp; 1 -
+        // e^(2 la) keeps expf, as la ends near the cap of -1e-4 there)
+        lq[i] = q[i] * __builtin_amdgcn_rsqf(1.0e-6f + sq);
+        const float kn = k[i] * __builtin_amdgcn_rsqf(1.0e-6f + sk);
+        if (rglru) {
+          la = fminf(ANA_CAP, (8.0f * __builtin_amdgcn_rcpf(1.0f + __expf(-z[i]))) * lv);
+          lk[i] = kn * sqrtf(1.0f - expf(2.0f * la));
+        } else {
+          la = -(fmaxf(-z[i], 0.0f) + __logf(1.0f + __expf(-fabsf(z[i]))));
+          lk[i] = kn;
+        }
+      }
+      c[i] = (i ? c[i - 1] : 0.0f) + la;
+    }
+    tot[tb][a] = c[TPT - 1];
+    __syncthreads();
+    float off = 0.0f;
+    for (uint32_t b = 0; b < tb; b++) off += tot[b][a];
+#pragma unroll
+    for (int i = 0; i < TPT; i++) {
+      qh[tb * TPT + i][a] = lq[i];
+      kh[tb * TPT + i][a] = lk[i];
+      cl[tb * TPT + i][a] = c[i] + off;
+      vv[tb * TPT + i][a] = v[i];
+    }
+    __syncthreads();
+    gla_pairs<HD>(qh, kh, cl, P, n, tid);
+    __syncthreads();
+    // qt = qh e^(c) and Kd = kh e^(c_last - c) in place (zero past n: the
+    // gates there are zero)
+    const float clast = cl[n - 1][a];
+#pragma unroll
+    for (int i = 0; i < TPT; i++) {
+      const uint32_t t = tb * TPT + i;
+      const float ct = cl[t][a];
+      qh[t][a] *= __expf(ct);
+      kh[t][a] *= __expf(clast - ct);
+    }
+    __syncthreads();
+    // o = P V + qt S on column block bw, token halves th (split over the
+    // copies)
+    for (uint32_t th = rep; th < 2; th += R) {
+      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int k0 = 0; k0 < L; k0 += 4)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(P[16 * th + r16][k0 + g4], vv[k0 + g4][16 * bw + r16], acc,
+                                                   0, 0, 0);
+#pragma unroll
+      for (int ab = 0; ab < CBS; ab++)
+#pragma unroll
+        for (int y = 0; y < 4; y++)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qh[16 * th + r16][16 * ab + 4 * g4 + y], Sr[ab][y], acc,
+                                                     0, 0, 0);
+#pragma unroll
+      for (int x = 0; x < 4; x++) {
+        const uint32_t t = 16 * th + 4 * g4 + x;
+        if (t < n) O[(size_t)(r.row + j0 + t) * d + h * HD + 16 * bw + r16] = acc[x];
+      }
+    }
+    // S' = D S + Kd^T V on the wave's own tiles (the next sub-chunk writes
+    // LDS only after its first barrier)
+#pragma unroll
+    for (int ab = 0; ab < CBS; ab++) {
+#pragma unroll
+      for (int y = 0; y < 4; y++) Sr[ab][y] *= __expf(cl[n - 1][16 * ab + 4 * g4 + y]);
+#pragma unroll
+      for (int k0 = 0; k0 < L; k0 += 4)
+        Sr[ab] = __builtin_amdgcn_mfma_f32_16x16x4f32(kh[k0 + g4][16 * ab + r16], vv[k0 + g4][16 * bw + r16],
+                                                      Sr[ab], 0, 0, 0);
+    }
+  }
+  if (rep == 0)
+#pragma unroll
+    for (int ab = 0; ab < CBS; ab++)
+#pragma unroll
+      for (int y = 0; y < 4; y++) Sg[(16 * ab + 4 * g4 + y) * HD + 16 * bw + r16] = Sr[ab][y];
+}
+
+hipError_t launch_gla_run(const float* QKV, const float* Z, const float* lam, StateRef S, float* O,
+                          const GlaRun* runs, uint32_t nrun, uint32_t rows, uint32_t d, uint32_t heads,
+                          uint32_t rglru, hipStream_t st) {
+  const uint32_t hd = d / heads;
+  if (nrun == 0 || hd * heads != d || (uint64_t)rows * 3 * d >= (1ull << 32)) return hipErrorInvalidValue;
+  switch (hd) {
+    case 64: hipLaunchKernelGGL(k_gla_run<64>, dim3(heads, nrun), dim3(256), 0, st, QKV, Z, lam, O, S, runs, d, rglru); break;
+    case 32: hipLaunchKernelGGL(k_gla_run<32>, dim3(heads, nrun), dim3(256), 0, st, QKV, Z, lam, O, S, runs, d, rglru); break;
+    case 16: hipLaunchKernelGGL(k_gla_run<16>, dim3(heads, nrun), dim3(256), 0, st, QKV, Z, lam, O, S, runs, d, rglru); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 static size_t round64(size_t n) { return (n + 63) & ~(size_t)63; }

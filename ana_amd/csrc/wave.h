@@ -1,0 +1,57 @@
+// Wave-level helpers shared by the kernels: DPP lane moves and the sums
+// and maxima they build (gfx950, 64-lane waves of four 16-lane rows).
+#pragma once
+#include <hip/hip_runtime.h>
+
+namespace ana {
+
+// a DPP move of v (lane permutation dpp_ctrl within each row of 16 lanes)
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+// the sum over each row of 16 lanes, in every lane of the row: lane ^ 1 and
+// lane ^ 2 (quad_perm), then the mirrored quad (row_half_mirror), then the
+// mirrored half-row (row_mirror)
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  return v;
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+// the sum over the wave (every lane gets it): the rows' sums by DPP, then
+// the four rows' by lane reads
+__device__ __forceinline__ float wsum(float v) {
+  v = row16_sum(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+// the maximum over the wave, the same way
+__device__ __forceinline__ float wmax(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
+// the sum over each group of G consecutive lanes (G = 16, 32 or 64), in
+// every lane of the group
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(G == 16 || G == 32 || G == 64, "rows, half waves or the wave");
+  v = row16_sum(v);
+  if constexpr (G == 16) {
+    return v;
+  } else if constexpr (G == 32) {
+    const float lo = lane_f(v, 0) + lane_f(v, 16), hi = lane_f(v, 32) + lane_f(v, 48);
+    return (threadIdx.x & 32) ? hi : lo;
+  } else {
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+  }
+}
+
+}  // namespace ana

@@ -420,13 +420,15 @@ LONG = cf.Config(vocab=258, ctx=1024, d=256, f=1024, layers=4, heads=4, rglru=Tr
 
 
 @pytest.mark.parametrize("mode", MODES)
-def test_fast_decode_long_split(oracle, tmp_path, mode):
+@pytest.mark.parametrize("chunk", [64, 320])
+def test_fast_decode_long_split(oracle, tmp_path, mode, chunk):
     """Decode steps of 6 sequences at 600+ live slots (ctx 1024): the fast
     attention above four rows takes the window in 256-slot pieces and a
-    combine. Ragged prompts through ana_feeds_n, then teacher-forced steps
-    through ana_feed; three sequences' logits against their own oracle runs
-    after every step."""
-    print(f"case fast decode long split mode {mode}", flush=True)
+    combine. Ragged prompts through ana_feeds_n (chunks of 64 tokens take
+    the GLA a workgroup per chunk, chunks of 320 the scan over sub-chunks),
+    then teacher-forced steps through ana_feed; three sequences' logits
+    against their own oracle runs after every step."""
+    print(f"case fast decode long split chunk {chunk} mode {mode}", flush=True)
     p = str(tmp_path / "long.ftc2")
     ckpt.write(p, LONG, ckpt.init_params(LONG, "normal", 11, trained=True))
     m = oracle.Model(p)
@@ -441,7 +443,7 @@ def test_fast_decode_long_split(oracle, tmp_path, mode):
             sts[i].feed(q, int(toks[i, q]))
     seqs = list(range(n))
     worst = 0.0
-    with ana_amd.Decoder(p, max_seqs=n, prefill_chunk=64, numerics=mode) as dec:
+    with ana_amd.Decoder(p, max_seqs=n, prefill_chunk=chunk, numerics=mode) as dec:
         dec.feeds_n(seqs, [0] * n, [toks[i, : starts[i]] for i in range(n)])
         for k in range(steps):
             pos = [starts[i] + k for i in range(n)]
