@@ -2429,12 +2429,21 @@ __device__ __forceinline__ void xcd_tile(uint32_t* nt, uint32_t* mt) {
 // is done with the stage they overwrite). Norm scale, residual and SiLU as in
 // k_gemm_big.
 template <int NS>
-__global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __restrict__ Ahg,
+__global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __restrict__ Ahg,
                                                   const float* __restrict__ rscg) {
   constexpr int BM = 128, BN = 128, BK = 64;
   constexpr int TILE = BM * 32;   // bf16 elements of one operand tile half (8 KB)
-  __shared__ __align__(1024) __bf16 lds[NS][2][2][TILE];
+  static_assert(NS == 2, "two stage objects");
+  // one LDS object per stage: a stage's fragment reads then provably miss
+  // the loads in flight into the other, and the compiler does not wait for
+  // them (one array indexed by stage made it drain every load before each
+  // stage's reads, and the loads never overlapped the MFMAs)
+  __shared__ __align__(1024) __bf16 st0[2][2][TILE], st1[2][2][TILE];
   __shared__ float rsl[BM];
+  auto stage = [&](auto B) -> __bf16(*)[2][TILE] {
+    if constexpr (decltype(B)::value == 0) return st0;
+    else return st1;
+  };
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint32_t wm = wv >> 1, wn = wv & 1;
   uint32_t ntile, mtile;
@@ -2457,16 +2466,15 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
     const bool ok = sgs.row(BN, ntile, r, &w, &sg, &lr);
     bptr[h] = ok ? (sg ? a.Wh1 : a.Wh0) + (size_t)lr * K + 8 * pq : a.Wh0 + 8 * pq;
   }
-  auto issue = [&](uint32_t s) {
-    const int buf = s % NS;
+  auto issue = [&](uint32_t s, auto B) {
     const uint32_t k0 = s * BK;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
       const uint32_t c = 2 * wv + h;
 #pragma unroll
       for (int kh = 0; kh < 2; kh++) {
-        __builtin_amdgcn_global_load_lds((const void*)(Ahg + aoff[h] + k0 + 32 * kh), (lds_void*)&lds[buf][0][kh][c * 512], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(bptr[h] + k0 + 32 * kh), (lds_void*)&lds[buf][1][kh][c * 512], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(Ahg + aoff[h] + k0 + 32 * kh), (lds_void*)&stage(B)[0][kh][c * 512], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(bptr[h] + k0 + 32 * kh), (lds_void*)&stage(B)[1][kh][c * 512], 16, 0, 0);
       }
     }
   };
@@ -2478,21 +2486,11 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
   const uint32_t r16 = lane & 15, g4 = lane >> 4;
   // fragment read offset (elements) inside a 16-row chunk
   const uint32_t foff = r16 * 32 + 8 * (g4 ^ ((r16 >> 1) & 3));
-#pragma unroll
-  for (int u = 0; u < NS - 1; u++)
-    if ((uint32_t)u < nst) issue(u);
-  for (uint32_t s = 0; s < nst; s++) {
-    // this wave's loads of stage s are done (8 loads a stage; those of the
-    // NS - 2 later stages may still fly)
-    if (s + NS - 2 < nst) ANA_VMCNT(8 * (NS - 2));
-    else ANA_VMCNT(0);
-    __builtin_amdgcn_s_barrier();
-    if (s + NS - 1 < nst) issue(s + NS - 1);
-    const int buf = s % NS;
+  auto compute = [&](auto B) {
 #pragma unroll
     for (int kh = 0; kh < 2; kh++) {
-      const __bf16* A0 = &lds[buf][0][kh][0];
-      const __bf16* B0 = &lds[buf][1][kh][0];
+      const __bf16* A0 = &stage(B)[0][kh][0];
+      const __bf16* B0 = &stage(B)[1][kh][0];
       bf16x8_t bfr[4], ah[4];
 #pragma unroll
       for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(B0 + (wn * 4 + j) * 512 + foff);
@@ -2503,6 +2501,24 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
 #pragma unroll
         for (int j = 0; j < 4; j++)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+  };
+  constexpr std::integral_constant<int, 0> S0{};
+  constexpr std::integral_constant<int, 1> S1{};
+  issue(0, S0);
+  // stage s: this wave's loads of it are done (the only ones in flight),
+  // then every wave's (the barrier, which also says every wave is done with
+  // the other stage object); the next stage's loads go out, then s's MFMAs
+  for (uint32_t s = 0; s < nst; s += 2) {
+    ANA_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+    if (s + 1 < nst) issue(s + 1, S1);
+    compute(S0);
+    if (s + 1 < nst) {
+      ANA_VMCNT(0);
+      __builtin_amdgcn_s_barrier();
+      if (s + 2 < nst) issue(s + 2, S0);
+      compute(S1);
     }
   }
   const bool norm = a.ng != nullptr;
@@ -2520,7 +2536,8 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
     // 64-row half at a time
     ANA_VMCNT(0);
     __syncthreads();
-    float* up = reinterpret_cast<float*>(&lds[0][0][0][0]);
+    float* up = reinterpret_cast<float*>(&st0[0][0][0]);
+    static_assert(sizeof(st0) >= 64 * 64 * sizeof(float), "exchange buffer");
     for (uint32_t half = 0; half < 2; half++) {
       if (wn == 1 && wm == half) {
 #pragma unroll
@@ -2598,10 +2615,15 @@ __global__ __launch_bounds__(256) void k_gemm_dl(GemvArgs a, const __bf16* __res
 // rows; the up waves hand their results to the gate waves through LDS.
 __global__ __launch_bounds__(1024) void k_gemm_dl2(GemvArgs a, const __bf16* __restrict__ Ahg,
                                                     const float* __restrict__ rscg) {
-  constexpr int BM = 256, BN = 256, BK = 64, NS = 2;
+  constexpr int BM = 256, BN = 256, BK = 64;
   constexpr int TILE = BM * 32;   // bf16 elements of one operand's k half (16 KB)
-  __shared__ __align__(1024) __bf16 lds[NS][2][2][TILE];
+  // one LDS object per stage, as in k_gemm_dl
+  __shared__ __align__(1024) __bf16 st0[2][2][TILE], st1[2][2][TILE];
   __shared__ float rsl[BM];
+  auto stage = [&](auto B) -> __bf16(*)[2][TILE] {
+    if constexpr (decltype(B)::value == 0) return st0;
+    else return st1;
+  };
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint32_t wm = wv >> 2, wn = wv & 3;
   uint32_t ntile, mtile;
@@ -2622,13 +2644,12 @@ __global__ __launch_bounds__(1024) void k_gemm_dl2(GemvArgs a, const __bf16* __r
     const bool ok = sgs.row(BN, ntile, r0, &w, &sg, &lr);
     bptr = ok ? (sg ? a.Wh1 : a.Wh0) + (size_t)lr * K + 8 * pq : a.Wh0 + 8 * pq;
   }
-  auto issue = [&](uint32_t s) {
-    const int buf = s % NS;
+  auto issue = [&](uint32_t s, auto B) {
     const uint32_t k0 = s * BK;
 #pragma unroll
     for (int kh = 0; kh < 2; kh++) {
-      __builtin_amdgcn_global_load_lds((const void*)(Ahg + aoff + k0 + 32 * kh), (lds_void*)&lds[buf][0][kh][wv * 512], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(bptr + k0 + 32 * kh), (lds_void*)&lds[buf][1][kh][wv * 512], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(Ahg + aoff + k0 + 32 * kh), (lds_void*)&stage(B)[0][kh][wv * 512], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(bptr + k0 + 32 * kh), (lds_void*)&stage(B)[1][kh][wv * 512], 16, 0, 0);
     }
   };
   f32x4_t acc[4][4];
@@ -2638,18 +2659,11 @@ __global__ __launch_bounds__(1024) void k_gemm_dl2(GemvArgs a, const __bf16* __r
     for (int j = 0; j < 4; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   const uint32_t r16 = lane & 15, g4 = lane >> 4;
   const uint32_t foff = r16 * 32 + 8 * (g4 ^ ((r16 >> 1) & 3));
-  issue(0);
-  for (uint32_t s = 0; s < nst; s++) {
-    // this wave's loads of stage s are done, then every wave's; the
-    // barrier also says every wave is done with the buffer stage s + 1 fills
-    ANA_VMCNT(0);
-    __builtin_amdgcn_s_barrier();
-    if (s + 1 < nst) issue(s + 1);
-    const int buf = s % NS;
+  auto compute = [&](auto B) {
 #pragma unroll
     for (int kh = 0; kh < 2; kh++) {
-      const __bf16* A0 = &lds[buf][0][kh][0];
-      const __bf16* B0 = &lds[buf][1][kh][0];
+      const __bf16* A0 = &stage(B)[0][kh][0];
+      const __bf16* B0 = &stage(B)[1][kh][0];
       bf16x8_t bfr[4], ah[4];
 #pragma unroll
       for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(B0 + (wn * 4 + j) * 512 + foff);
@@ -2659,6 +2673,23 @@ __global__ __launch_bounds__(1024) void k_gemm_dl2(GemvArgs a, const __bf16* __r
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+  };
+  constexpr std::integral_constant<int, 0> S0{};
+  constexpr std::integral_constant<int, 1> S1{};
+  issue(0, S0);
+  // this wave's loads of stage s are done, then every wave's; the barrier
+  // also says every wave is done with the object stage s + 1 fills
+  for (uint32_t s = 0; s < nst; s += 2) {
+    ANA_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+    if (s + 1 < nst) issue(s + 1, S1);
+    compute(S0);
+    if (s + 1 < nst) {
+      ANA_VMCNT(0);
+      __builtin_amdgcn_s_barrier();
+      if (s + 2 < nst) issue(s + 2, S0);
+      compute(S1);
     }
   }
   const bool norm = a.ng != nullptr;
@@ -2672,8 +2703,10 @@ __global__ __launch_bounds__(1024) void k_gemm_dl2(GemvArgs a, const __bf16* __r
   }
   auto rs = [&](int i, int r) { return norm ? rsl[wm * 64 + 16 * i + 4 * g4 + r] : 1.0f; };
   if (a.mode == GM_SILU) {
-    // up columns (wn 2, 3) through LDS to the gate columns (wn 0, 1)
-    float* up = reinterpret_cast<float*>(&lds[0][0][0][0]);   // [256][128]
+    // up columns (wn 2, 3) through LDS to the gate columns (wn 0, 1): rows
+    // 0..127 in the first stage object, 128..255 in the second (64 KB each)
+    static_assert(sizeof(st0) == 128 * 128 * sizeof(float), "exchange halves");
+    float* up = reinterpret_cast<float*>(wm < 2 ? &st0[0][0][0] : &st1[0][0][0]);   // [m & 127][128]
     if (wn >= 2) {
 #pragma unroll
       for (int i = 0; i < 4; i++)
@@ -2682,7 +2715,7 @@ __global__ __launch_bounds__(1024) void k_gemm_dl2(GemvArgs a, const __bf16* __r
 #pragma unroll
           for (int r = 0; r < 4; r++) {
             const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r, n = (wn - 2) * 64 + 16 * j + r16;
-            up[m * 128 + n] = acc[i][j][r] * rs(i, r);
+            up[(m & 127) * 128 + n] = acc[i][j][r] * rs(i, r);
           }
     }
     __syncthreads();
@@ -2700,7 +2733,7 @@ __global__ __launch_bounds__(1024) void k_gemm_dl2(GemvArgs a, const __bf16* __r
             const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r;
             if (m >= nb) continue;
             const float y = acc[i][j][r] * rs(i, r);
-            const float hv = fast_silu(y) * up[m * 128 + n];
+            const float hv = fast_silu(y) * up[(m & 127) * 128 + n];
             a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = hv;
             if (a.Yh) a.Yh[(size_t)(m0 + m) * a.seg[0].rows + lr] = (__bf16)hv;
           }
