@@ -862,7 +862,13 @@ static int score_head(ana_ctx* c, uint32_t r0, uint32_t g) {
   h.ng = c->W + c->fin;
   if (fast_mode(c)) {
     h.Wh0 = c->Wh;
-    HIPCHK(c, launch_gemm_big(h, c->st));
+    // ANA_BF16 at 128 rows or more: the bf16 matrix-core tiles, as the
+    // layer products of a prefill step (activations rounded to bf16 with
+    // the final norm's gain, as the decode head rounds them)
+    if (c->Wh && c->d_sah && g >= 128 && cf.d % 64 == 0)
+      HIPCHK(c, launch_gemm_dl(h, c->d_sah, c->d_rsc, c->rows, c->st));
+    else
+      HIPCHK(c, launch_gemm_big(h, c->st));
   } else {
     HIPCHK(c, launch_gemv(h, c->st));
   }
