@@ -127,7 +127,7 @@ def run_batch(path: str, c: cf.Config, B: int, prompt: int, warmup: int, steps: 
     }
 
 
-def run_configs(path: str, c) -> dict:
+def run_configs(path: str, c, only: str = "") -> dict:
     """BASELINE's other decode configs on the same checkpoint (ctx 2048):
     "next" (B=32, 1920-token prompts, 128 greedy steps, fast_fp32, past the
     ring's wrap at the end), "v3" (B=64, 128-token prompts, 128 sampled steps
@@ -137,6 +137,8 @@ def run_configs(path: str, c) -> dict:
     for key, B, prompt, steps, mode, sampled in (("cfg_next", 32, 1920, 128, "fast_fp32", False),
                                                  ("cfg_v3", 64, 128, 128, "fast_fp32", True),
                                                  ("cfg_bf16", 256, 512, 256, "bf16", False)):
+        if only and key != "cfg_" + only:
+            continue
         seqs = list(range(B))
         with ana_amd.Decoder(path, max_seqs=B, prefill_chunk=128, numerics=MODES[mode]) as dec:
             prs = [ckpt.prompt(5000 + b, prompt, c.vocab) for b in seqs]
@@ -321,6 +323,8 @@ def main() -> int:
     ap.add_argument("--agent", type=int, default=1, help="also measure 64 agent episodes (1/0)")
     ap.add_argument("--configs", type=int, default=1, help="also measure BASELINE's next, v3 and bf16 decode configs (1/0)")
     ap.add_argument("--configs-only", type=int, default=0, help="print only those configs' JSON (the child run)")
+    ap.add_argument("--config", choices=["", "next", "v3", "bf16"], default="",
+                    help="with --configs-only: just this one config")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--ckpt", default=os.environ.get("ANA_BENCH_CKPT", "/tmp/ana_bench_fp100m.ftc2"))
     a = ap.parse_args()
@@ -336,7 +340,7 @@ def main() -> int:
         release_device()
         return 0
     if a.configs_only:
-        print(json.dumps(run_configs(path, c)), flush=True)
+        print(json.dumps(run_configs(path, c, a.config)), flush=True)
         release_device()
         return 0
     cfg_lines = {}
