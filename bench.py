@@ -227,20 +227,27 @@ def run_agent(path: str, c, mode: str) -> dict:
     eps = [agent.Episode([int(x) for x in ckpt.prompt(3000 + b, 128, c.vocab)], seed=b, budget=48, calls=2)
            for b in range(64)]
     is_call = lambda i, t: t[-1] % 61 == 7  # noqa: E731
-    tool = lambda i, t: [2 + (t[-1] * 31 + j) % (c.vocab - 2) for j in range(24)]  # noqa: E731
+    echoed = [0]   # the echoes' tokens (fed, and not among an outcome's tokens)
+
+    def tool(i, t):
+        e = [2 + (t[-1] * 31 + j) % (c.vocab - 2) for j in range(24)]
+        echoed[0] += len(e)
+        return e
     with ana_amd.Decoder(path, max_seqs=64, prefill_chunk=128, numerics=MODES[mode]) as dec:
         agent.run(dec, eps[:8], st, is_call, tool)   # warm-up
+        echoed[0] = 0
         t = time.perf_counter()
         out = agent.run(dec, eps, st, is_call, tool)
         dt = time.perf_counter() - t
     drawn = sum(sum(o.drawn) for o in out)
-    fed = sum(len(o.drawn) - sum(o.drawn) for o in out)
+    fed = sum(len(o.drawn) - sum(o.drawn) for o in out) + echoed[0]
     log(f"agent {mode}: {drawn} drawn + {fed} fed tokens over 64 episodes in {dt:.3f}s")
-    return {"episodes": 64, "seconds": round(dt, 4), "drawn": drawn, "fed": fed,
+    return {"episodes": 64, "seconds": round(dt, 4), "drawn": drawn, "fed": fed, "echoed": echoed[0],
             "drawn_tok_s": round(drawn / dt, 1), "tok_s": round((drawn + fed) / dt, 1),
             "endings": {w: sum(1 for o in out if o.why == w) for w in ("eos", "budget", "calls", "tool")},
             "workload": "64 episodes (128-token prompts, T 0.8 / top-k 40 / top-p 0.9, 48 draws a stretch, "
-                        "2 calls; a call: drawn id = 7 mod 61; echo 24 ids fed unsampled); " + NUMERICS[mode]}
+                        "2 calls; a call: drawn id = 7 mod 61; echo 24 ids fed unsampled; fed counts given "
+                        "tokens and echoes); " + NUMERICS[mode]}
 
 
 def run_prefill(path: str, c, reps: int = 5) -> dict:
