@@ -64,6 +64,8 @@ struct ana_ctx {
   // bf16 in ANA_BF16; the norm gains folded in), found by the product's first
   // weight row; the entry keeps the segment shape and gains it was packed for
   void* PK = nullptr;
+  unsigned long long* d_hpc = nullptr;  // the fused head and sampler's arrival counters
+  uint32_t* d_hpctl = nullptr;          // and its ran-out flag
   struct PkEnt {
     uint64_t off;
     uint32_t rows0, rows1, nseg, mode, K;
@@ -198,7 +200,7 @@ static void release(ana_ctx* c) {
   void* ps[] = {c->d_play, c->d_ll, c->d_ctl, c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
                 c->d_ss, c->d_pm, c->d_gtab, c->d_grun, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce, c->d_rcp,
-                c->d_sah, c->d_hh, c->d_rsc, c->PK};
+                c->d_sah, c->d_hh, c->d_rsc, c->PK, c->d_hpc, c->d_hpctl};
   for (void* p : ps)
     if (p) (void)hipFree(p);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
@@ -340,6 +342,15 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = launch_bswap(reinterpret_cast<uint32_t*>(c->W), c->P, c->st)) != hipSuccess) return bad(e);
   if (c->Wh && (e = launch_to_bf16(c->W, c->Wh, c->P, c->st)) != hipSuccess) return bad(e);
   if (c->mode != ANA_EXACT_FP32 && (e = pack_weights(c)) != hipSuccess) return bad(e);
+  if (c->mode != ANA_EXACT_FP32) {
+    // the fused head and sampler's counters (one per 32-row block, only
+    // ever added to) and flag start at zero
+    const size_t blocks = (c->max_seqs + 31) / 32;
+    if ((e = dalloc(&c->d_hpc, blocks)) != hipSuccess || (e = dalloc(&c->d_hpctl, 1)) != hipSuccess ||
+        (e = hipMemsetAsync(c->d_hpc, 0, 8 * blocks, c->st)) != hipSuccess ||
+        (e = hipMemsetAsync(c->d_hpctl, 0, 4, c->st)) != hipSuccess)
+      return bad(e);
+  }
   if (c->mode == ANA_FAST_FP32 && (e = persist_setup(c)) != hipSuccess) return bad(e);
   // ANA_PERSIST=0 keeps one-sequence decode on the captured graphs
   if (const char* pv = getenv("ANA_PERSIST")) c->persist_off = strcmp(pv, "0") == 0;
@@ -1046,13 +1057,46 @@ extern "C" int ana_pick(ana_ctx* c, uint32_t n, const uint32_t* seq, const ana_s
 // one decode step of the token loop: embed the current tokens, every
 // layer, the head, the pick, then advance (pos + 1, tok = pick, record the
 // pick at out[step[b] * n + b] and count the row's step)
+// A sampled step's LM head and pick as one launch (launch_head_pick) where
+// the fused form applies: the fast modes' head over packed weights, a grid
+// the GPU holds at once. 1: launched; 0: run them apart; < 0: an error.
+static int head_pick(ana_ctx* c, uint32_t n, const PickArgs& pa) {
+  if (!fast_mode(c) || !c->d_hpc) return 0;
+  GemvArgs h = head_args(c, c->X, n);
+  const ana_ctx::PkEnt* pe = head_pw_fits(h) ? find_pk(c, h) : nullptr;
+  if (!pe) return 0;
+  double by = gemv_bytes(h);
+  if (pe->bf) by -= 2.0 * h.seg[0].rows * h.K;
+  ProfScope ps(c, ANA_K_HEAD, by, true);
+  const hipError_t e = launch_head_pick(h, static_cast<const char*>(c->PK) + pe->off, pe->bf,
+                                        HeadPick{pa, c->d_hpc, c->d_hpctl}, c->st, ps.start(), ps.stop());
+  if (e == hipErrorNotSupported) return 0;
+  if (e != hipSuccess) return -fail(c, ANA_EDEVICE, "launch_head_pick: %s", hipGetErrorString(e));
+  return 1;
+}
+
+// after a sampled call's last synchronisation: whether a fused sampler's
+// wait for its head ran out (its picks then never landed)
+static int head_pick_check(ana_ctx* c, const char* fn) {
+  if (!c->d_hpctl) return ANA_OK;
+  uint32_t f = 0;
+  HIPCHK(c, hipMemcpy(&f, c->d_hpctl, 4, hipMemcpyDeviceToHost));
+  if (!f) return ANA_OK;
+  HIPCHK(c, hipMemset(c->d_hpctl, 0, 4));
+  return fail(c, ANA_EDEVICE, "%s: a sampler's wait for the LM head ran out", fn);
+}
+
 static int gen_step(ana_ctx* c, uint32_t n, const PickArgs& pa, bool greedy, uint32_t* out, uint32_t* step) {
   HIPCHK(c, launch_embed(c->W, c->d_tok, c->cfg.d, n, c->X, c->d_amax, c->st));
   if (int r = run_layers(c, n, c->d_seq, c->d_pos, nullptr)) return r;
-  if (int r = run_head(c, c->X, n, greedy)) return r;
-  if (!greedy) {
-    ProfScope ps(c, ANA_K_PICK, 4.0 * n * c->cfg.vocab);
-    HIPCHK(c, launch_pick(pa, c->st));
+  const int fused = greedy ? 0 : head_pick(c, n, pa);
+  if (fused < 0) return -fused;
+  if (!fused) {
+    if (int r = run_head(c, c->X, n, greedy)) return r;
+    if (!greedy) {
+      ProfScope ps(c, ANA_K_PICK, 4.0 * n * c->cfg.vocab);
+      HIPCHK(c, launch_pick(pa, c->st));
+    }
   }
   AdvanceArgs ad{};
   ad.logits = c->LG;
@@ -1248,6 +1292,7 @@ extern "C" int ana_generate(ana_ctx* c, uint32_t n, const uint32_t* seq, const u
   HIPCHK(c, launch_scatter_rows(c->X, c->d_seq, n, c->cfg.d, c->xs, c->st));
   if (!greedy) HIPCHK(c, hipMemcpyAsync(rng, c->d_rng, 32 * n, hipMemcpyDeviceToHost, c->st));
   HIPCHK(c, hipStreamSynchronize(c->st));
+  if (!greedy) return head_pick_check(c, "ana_generate");
   return ANA_OK;
 }
 
@@ -1310,6 +1355,7 @@ extern "C" int ana_generate_noalloc(ana_ctx* c, uint32_t n, const uint32_t* seq,
   HIPCHK(c, hipMemcpyAsync(out, d_rm, 4 * (size_t)n * steps, hipMemcpyDeviceToHost, c->st));
   if (!greedy) HIPCHK(c, hipMemcpyAsync(rng, c->d_rng, 32 * n, hipMemcpyDeviceToHost, c->st));
   HIPCHK(c, hipStreamSynchronize(c->st));
+  if (!greedy) return head_pick_check(c, "ana_generate_noalloc");
   return ANA_OK;
 }
 

@@ -321,6 +321,21 @@ hipError_t launch_pack(const GemvArgs& a, void* dst, int bf, hipStream_t st);
 bool gemm_pk_fits(const GemvArgs& a);
 hipError_t launch_gemm_pk(const GemvArgs& a, const void* pk, int bf, hipStream_t st, hipEvent_t e0,
                           hipEvent_t e1);
+// The LM head fused with the seeded sampler (k_head_pw with PICK): the
+// head's workgroups write their logits through to the level every XCD
+// reads and count themselves in per 32-row block; the last `rows` of a
+// block to arrive wait for the rest and run S.pick on one row each. Only
+// for grids the GPU holds at once with at least as many workgroups a block
+// as rows (launch_head_pick answers hipErrorNotSupported otherwise, and for
+// vocabularies whose sampler geometry has no fused form).
+struct HeadPick {
+  PickArgs pa;                // pa.logits: the head's output rows
+  unsigned long long* cnt;    // per 32-row block: arrivals, only ever added to
+  uint32_t* ctl;              // set when a wait ran out
+};
+constexpr uint32_t kPickPollMax = 1u << 20;   // polls before a sampler's wait gives up
+hipError_t launch_head_pick(const GemvArgs& a, const void* pk, int bf, const HeadPick& hp, hipStream_t st,
+                            hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 // The wide form for the LM head (plain products, K % 256 == 0,
 // K <= kHeadMaxK): 32 batch rows in LDS per workgroup, 16 weight tiles each
 constexpr uint32_t kHeadMaxK = 1024;

@@ -13,6 +13,7 @@
 
 #include "ana_internal.h"
 #include "numerics.h"
+#include "pick_row.h"
 #include "wave.h"
 
 namespace ana {
@@ -1425,8 +1426,19 @@ __global__ __launch_bounds__(256) void k_gemm_pw(GemvArgs a, const uint4* __rest
 // scales, stores and clears its two accumulators (batch rows 0..15 and
 // 16..31). The x tile is read once per TPW weight tiles instead of once per
 // tile.
-template <int WT, int TPW, int D, int NW>
-__global__ __launch_bounds__(64 * NW) void k_head_pw(GemvArgs a, const uint4* __restrict__ pk, uint32_t tiles) {
+// With PICK = LPT (the sampler's leaves a thread), the fused form of the
+// head and the sampler: the logits are stored with agent-scope stores
+// (written through to the level every XCD reads), and once its stores are
+// complete the workgroup counts itself in on its row block's counter (a
+// running total, so no reset between launches); the last `rows` arrivals
+// wait (bounded) until every workgroup of the block has counted in, then
+// each copies one of the block's rows into LDS with agent-scope loads and
+// runs pick_row on it. The host launches it only when the whole grid is resident at
+// once (so no waiting workgroup holds a slot another needs) and a block has
+// at least as many workgroups as rows.
+template <int WT, int TPW, int D, int NW, int PICK>
+__global__ __launch_bounds__(64 * NW) void k_head_pw(GemvArgs a, const uint4* __restrict__ pk, uint32_t tiles,
+                                                     HeadPick hp) {
   constexpr int WP = WT == 1 ? 1 : 2;
   constexpr uint32_t BM = 32;
   __shared__ __align__(1024) float xs[BM * kHeadMaxK];
@@ -1524,8 +1536,9 @@ __global__ __launch_bounds__(64 * NW) void k_head_pw(GemvArgs a, const uint4* __
           float y = acc[tt][r];
           if (norm) y *= rsc[mi];
           if (nok && m < a.B) {
-            if (sg) a.seg[1].Y[(size_t)m * a.seg[1].ldy + lr] = y;
-            else a.seg[0].Y[(size_t)m * a.seg[0].ldy + lr] = y;
+            float* yp = sg ? a.seg[1].Y + (size_t)m * a.seg[1].ldy + lr : a.seg[0].Y + (size_t)m * a.seg[0].ldy + lr;
+            if constexpr (PICK != 0) __hip_atomic_store(yp, y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else *yp = y;
           }
           if (a.amax) {
             // the row's best key over the tile's 16 columns, one atomic
@@ -1541,6 +1554,49 @@ __global__ __launch_bounds__(64 * NW) void k_head_pw(GemvArgs a, const uint4* __
         acc[tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
       }
     }
+  }
+  if constexpr (PICK != 0) {
+    __shared__ uint32_t samp_s;
+    ANA_VMCNT(0);   // this wave's stores are complete, then every wave's
+    __syncthreads();
+    if (tid == 0) {
+      // (the host launches this form with at least as many workgroups a
+      // block as rows in it: one row a sampler)
+      const uint32_t per = gridDim.x, ns = min(BM, a.B - m0);
+      const unsigned long long old =
+          __hip_atomic_fetch_add(hp.cnt + blockIdx.y, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t ai = (uint32_t)(old % per);
+      uint32_t j = ~0u;
+      if (ai >= per - ns) {
+        j = ai - (per - ns);
+        const unsigned long long target = old - ai + per;
+        for (uint32_t polls = 0;
+             __hip_atomic_load(hp.cnt + blockIdx.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target; polls++) {
+          if (polls >= kPickPollMax) {
+            __hip_atomic_store(hp.ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            j = ~0u;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+        }
+      }
+      samp_s = j;
+    }
+    __syncthreads();
+    const uint32_t j = samp_s;
+    if (j == ~0u) return;
+    static_assert(BM * kHeadMaxK >= 32768, "the x tile holds a row of the fused forms' vocabularies");
+    // the row into the x tile's LDS (dead now, and as large as the
+    // vocabulary the fused forms take): agent-scope loads, lane t of
+    // consecutive floats so each load of a wave is one 256-byte piece
+    const uint32_t v = hp.pa.vocab;
+    const float* lg = hp.pa.logits + (size_t)(m0 + j) * v;
+    for (uint32_t i = tid; i < v; i += 64 * NW)
+      xs[i] = __hip_atomic_load(const_cast<float*>(lg) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    uint32_t dv = 0;
+    while ((1u << dv) < v) dv++;
+    pick_row<PICK>(hp.pa, m0 + j, (1u << dv) / PICK, dv, xs);
   }
 }
 
@@ -1559,9 +1615,54 @@ hipError_t launch_head_pw(const GemvArgs& a, const void* pk, int bf, hipStream_t
   // one tile each (measured at B = 64: 55 -> 41 us fp32, 37 -> 26 us bf16
   // from four waves to sixteen); fp32 blocks of two steps (114 -> 100 VGPRs,
   // 43 -> 41 us at B = 64), bf16 of four
-  if (bf) ANA_LAUNCH_F((k_head_pw<1, TPW, 4, 16>), grid, dim3(1024), 0, st, e0, e1, a, p, tiles);
-  else ANA_LAUNCH_F((k_head_pw<0, TPW, 2, 16>), grid, dim3(1024), 0, st, e0, e1, a, p, tiles);
+  const HeadPick none{};
+  if (bf) ANA_LAUNCH_F((k_head_pw<1, TPW, 4, 16, 0>), grid, dim3(1024), 0, st, e0, e1, a, p, tiles, none);
+  else ANA_LAUNCH_F((k_head_pw<0, TPW, 2, 16, 0>), grid, dim3(1024), 0, st, e0, e1, a, p, tiles, none);
   return hipGetLastError();
+}
+
+// workgroups of kernel k the GPU holds at once (1024 threads each)
+template <class Kern>
+static uint64_t resident_wgs(Kern k) {
+  int dev = 0, cus = 0, per = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, 1024, 0) != hipSuccess)
+    return 0;
+  return (uint64_t)cus * (uint64_t)per;
+}
+
+template <int WT, int D, int L>
+static hipError_t head_pick_go(const GemvArgs& a, const uint4* p, uint32_t tiles, const dim3& grid,
+                               const HeadPick& hp, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  static const uint64_t cap = resident_wgs(k_head_pw<WT, 16, D, 16, L>);
+  if ((uint64_t)grid.x * grid.y > cap) return hipErrorNotSupported;
+  ANA_LAUNCH_F((k_head_pw<WT, 16, D, 16, L>), grid, dim3(1024), 0, st, e0, e1, a, p, tiles, hp);
+  return hipGetLastError();
+}
+
+hipError_t launch_head_pick(const GemvArgs& a, const void* pk, int bf, const HeadPick& hp, hipStream_t st,
+                            hipEvent_t e0, hipEvent_t e1) {
+  if (!head_pw_fits(a) || !pk || !hp.cnt || !hp.ctl || hp.pa.logits != a.seg[0].Y || a.nseg != 1 ||
+      hp.pa.B != a.B || hp.pa.vocab != a.seg[0].rows)
+    return hipErrorInvalidValue;
+  // the sampler's geometry (as launch_pick's): 1024 threads of LPT leaves
+  // over the vocabulary padded to a power of two; fused forms for LPT 1
+  // (up to 1024 entries) and 32 (16385 .. 32768)
+  uint32_t dv = 0;
+  while ((1ull << dv) < a.seg[0].rows) dv++;
+  const uint64_t vpad = 1ull << dv;
+  const uint32_t lpt = vpad > 1024 ? (uint32_t)(vpad / 1024) : 1u;
+  constexpr int TPW = 16;
+  const uint32_t tiles = pk_tiles(a);
+  const dim3 grid((tiles + TPW - 1) / TPW, (a.B + 31) / 32);
+  if (grid.x < std::min(a.B, 32u)) return hipErrorNotSupported;   // one row a sampler
+  const uint4* p = static_cast<const uint4*>(pk);
+  if (lpt == 1) return bf ? head_pick_go<1, 4, 1>(a, p, tiles, grid, hp, st, e0, e1)
+                          : head_pick_go<0, 2, 1>(a, p, tiles, grid, hp, st, e0, e1);
+  if (lpt == 32) return bf ? head_pick_go<1, 4, 32>(a, p, tiles, grid, hp, st, e0, e1)
+                           : head_pick_go<0, 2, 32>(a, p, tiles, grid, hp, st, e0, e1);
+  return hipErrorNotSupported;
 }
 
 bool gemm_pk_fits(const GemvArgs& a) {

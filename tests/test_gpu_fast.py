@@ -537,3 +537,59 @@ def test_fast_persistent_decode(oracle, small_ckpt, mid_ckpt, big_ckpt, model):
         e = rel_err(lg, want)
         print(f"persist {persist}: final relative error {e:.3e}", flush=True)
         assert e <= TOL[ana_amd.FAST_FP32], (persist, e)
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("model,n", [("v1", 40), ("v1", 1), ("mid", 2)])
+def test_fast_fused_head_sampler(oracle, mid_ckpt, tmp_path, mode, model, n):
+    """Sampled steps of ana_generate in a fast mode run the LM head fused with
+    the sampler (vocab 32768: 128 head workgroups a 32-row block, 40 rows
+    being two blocks; vocab 258 at two rows: two workgroups, one sampler
+    each). Every step's picks, and the RNG words at the end, equal S.pick's
+    (the oracle's) on the logits of a twin decoder fed the same tokens, and
+    the unfused sampler's (ana_pick on the twin); the event timing shows
+    one pick-kind launch a step (the step end), none for the sampler."""
+    print(f"case fused head sampler {model} n {n} mode {mode}", flush=True)
+    if model == "v1":
+        c = cf.V1
+        path = str(tmp_path / "v1f.ftc2")
+        ckpt.write(path, c, ckpt.init_params(c, "normal", 5, trained=True))
+    else:
+        path, c = mid_ckpt, MID
+    oracle.set_threads(8)
+    st = ana_amd.Settings(float(np.float32(0.8)), 40, float(np.float32(0.9)))
+    steps = 3
+    seqs = list(range(n))
+    r = np.random.default_rng(41)
+    prompts = [r.integers(2, c.vocab, size=2 + b % 5).astype(np.uint32) for b in range(n)]
+    rng0 = np.ascontiguousarray(np.stack([ana_amd.rng_seeded(100 + b) for b in range(n)]))
+    with ana_amd.Decoder(path, max_seqs=n, numerics=mode) as dec, \
+            ana_amd.Decoder(path, max_seqs=n, numerics=mode) as twin:
+        for d_ in (dec, twin):
+            d_.feeds_n(seqs, [0] * n, [p[:-1] for p in prompts])
+        pos = np.array([len(p) - 1 for p in prompts], dtype=np.uint32)
+        tok = np.array([int(p[-1]) for p in prompts], dtype=np.uint32)
+        rng = rng0.copy()
+        out = dec.generate(seqs, pos, tok, steps, st, rng)
+        r_or = [oracle.rng_seeded(100 + b) for b in range(n)]
+        r_tw = rng0.copy()
+        t, p = tok.copy(), pos.copy()
+        for k in range(steps):
+            twin.feed(seqs, p, t)
+            lg = twin.logits(seqs)
+            tw = twin.pick(seqs, st, r_tw)
+            for b in range(n):
+                want = oracle.pick(lg[b], st.temperature, st.top_k, st.top_p, r_or[b])
+                assert int(out[b, k]) == int(want), (k, b)
+            assert np.array_equal(tw, out[:, k]), k
+            t, p = out[:, k].copy(), p + 1
+        for b in range(n):
+            assert np.array_equal(rng[b], r_or[b]), b
+        assert np.array_equal(rng, r_tw)
+        # one more step with event timing: the sampler ran inside the head
+        dec.prof(True)
+        dec.generate(seqs, p, t, 1, st, rng)
+        stats = dec.prof_read()
+        dec.prof(False)
+        assert stats["pick"][0] == 1, stats["pick"]
+        assert stats["head"][0] == 1, stats["head"]
