@@ -1058,10 +1058,13 @@ extern "C" int ana_pick(ana_ctx* c, uint32_t n, const uint32_t* seq, const ana_s
 // layer, the head, the pick, then advance (pos + 1, tok = pick, record the
 // pick at out[step[b] * n + b] and count the row's step)
 // A sampled step's LM head and pick as one launch (launch_head_pick) where
-// the fused form applies: the fast modes' head over packed weights, a grid
-// the GPU holds at once. 1: launched; 0: run them apart; < 0: an error.
+// the fused form applies: above kSmallB rows (at or below it the head is
+// the one-wave GEMV over every CU, 27 us a step faster at B = 1 than the
+// fused form's head on 128 workgroups), the fast modes' head over packed
+// weights, a grid the GPU holds at once. 1: launched; 0: run them apart;
+// < 0: an error.
 static int head_pick(ana_ctx* c, uint32_t n, const PickArgs& pa) {
-  if (!fast_mode(c) || !c->d_hpc) return 0;
+  if (!fast_mode(c) || !c->d_hpc || n <= kSmallB) return 0;
   GemvArgs h = head_args(c, c->X, n);
   const ana_ctx::PkEnt* pe = head_pw_fits(h) ? find_pk(c, h) : nullptr;
   if (!pe) return 0;

@@ -540,15 +540,16 @@ def test_fast_persistent_decode(oracle, small_ckpt, mid_ckpt, big_ckpt, model):
 
 
 @pytest.mark.parametrize("mode", MODES)
-@pytest.mark.parametrize("model,n", [("v1", 40), ("v1", 1), ("mid", 2)])
+@pytest.mark.parametrize("model,n", [("v1", 40), ("v1", 5), ("v1", 3)])
 def test_fast_fused_head_sampler(oracle, mid_ckpt, tmp_path, mode, model, n):
     """Sampled steps of ana_generate in a fast mode run the LM head fused with
-    the sampler (vocab 32768: 128 head workgroups a 32-row block, 40 rows
-    being two blocks; vocab 258 at two rows: two workgroups, one sampler
-    each). Every step's picks, and the RNG words at the end, equal S.pick's
-    (the oracle's) on the logits of a twin decoder fed the same tokens, and
-    the unfused sampler's (ana_pick on the twin); the event timing shows
-    one pick-kind launch a step (the step end), none for the sampler."""
+    the sampler above four rows (vocab 32768: 128 head workgroups a 32-row
+    block, 40 rows being two blocks, 5 one); at three rows the head and
+    k_pick run apart. Every step's picks, and the RNG words at the end,
+    equal S.pick's (the oracle's) on the logits of a twin decoder fed the
+    same tokens, and the unfused sampler's (ana_pick on the twin); the event
+    timing shows the fused form's one pick-kind launch a step (the step
+    end), or two apart."""
     print(f"case fused head sampler {model} n {n} mode {mode}", flush=True)
     if model == "v1":
         c = cf.V1
@@ -591,5 +592,5 @@ def test_fast_fused_head_sampler(oracle, mid_ckpt, tmp_path, mode, model, n):
         dec.generate(seqs, p, t, 1, st, rng)
         stats = dec.prof_read()
         dec.prof(False)
-        assert stats["pick"][0] == 1, stats["pick"]
+        assert stats["pick"][0] == (1 if n > 4 else 2), stats["pick"]
         assert stats["head"][0] == 1, stats["head"]
