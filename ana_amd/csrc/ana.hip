@@ -746,7 +746,7 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
         // no chunk reaches the ring's wrap: every row's write, then every
         // row's attention over the splits up to the step's last position
         a.QKV = c->QKV; a.O = c->O; a.B = B; a.seq = c->d_rseq; a.pos = c->d_rpos; a.write_kv = 0;
-        HIPCHK(c, launch_kv_write(a, c->st));
+        HIPCHK(c, launch_kv_write_fast(a, c->st));
         HIPCHK(c, launch_attn_flash(a, c->d_atab, (uint32_t)c->h_atab.size(), c->st));
       } else {
         for (const Seg& sg : *segs) {

@@ -2168,6 +2168,45 @@ hipError_t launch_gla_run(const float* QKV, const float* Z, const float* lam, St
   return hipGetLastError();
 }
 
+// A fast-mode prefill step's K and V rows into the rings (dd.sm.write over
+// every row): thread t of workgroup (x, b) takes column 256 x + t of row b,
+// so a head's HD columns are HD consecutive lanes; the qk-norm's sum of
+// squares is their group sum (reassociated), k = (k * s) * (1 + gk), and K
+// and V go to slot pos mod ctx. One workgroup a 256 columns of a row,
+// where the exact kernel takes one a (head, row) with an in-order chain.
+template <int HD>
+__global__ __launch_bounds__(256) void k_kv_write_fast(AttnArgs a) {
+  const uint32_t b = blockIdx.y, col = blockIdx.x * 256 + threadIdx.x, d = a.d;
+  const bool in = col < d;
+  const float* x = a.QKV + (size_t)b * 3 * d;
+  float k = in ? x[d + col] : 0.0f;
+  const float v = in ? x[2 * d + col] : 0.0f;
+  if (a.gk) {
+    const float ss = group_sum<HD>(k * k);
+    k = (k * (1.0f / sqrtf(ss / (float)HD + 1.0e-5f))) * (1.0f + a.gk[col % HD]);
+  }
+  if (!in) return;
+  const uint32_t pos = a.pos ? a.pos[b] : a.pos0 + b;
+  const uint32_t slot = pos % a.ctx;
+  const uint32_t sl = a.seq ? a.seq[b] : a.seq0;
+  float* Kr = a.KV.base + (size_t)sl * a.KV.seq_stride + a.KV.layer_off;
+  Kr[(size_t)slot * d + col] = k;
+  Kr[(size_t)a.ctx * d + (size_t)slot * d + col] = v;
+}
+
+hipError_t launch_kv_write_fast(const AttnArgs& a, hipStream_t st) {
+  const uint32_t hd = a.d / a.heads;
+  if (a.B == 0 || hd * a.heads != a.d) return hipErrorInvalidValue;
+  const dim3 grid((a.d + 255) / 256, a.B);
+  switch (hd) {
+    case 64: hipLaunchKernelGGL(k_kv_write_fast<64>, grid, dim3(256), 0, st, a); break;
+    case 32: hipLaunchKernelGGL(k_kv_write_fast<32>, grid, dim3(256), 0, st, a); break;
+    case 16: hipLaunchKernelGGL(k_kv_write_fast<16>, grid, dim3(256), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 static size_t round64(size_t n) { return (n + 63) & ~(size_t)63; }
 
 size_t gla_scan_floats(uint32_t rows, uint32_t nsub, uint32_t nseg, uint32_t d, uint32_t heads) {
