@@ -15,8 +15,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libana.so")
-SOURCES = ["ana.hip", "kernels_exact.hip", "kernels_fast.hip", "sampler.hip", "decode_persist.hip", "ftc2.cpp",
-           "bpe.cpp"]
+SOURCES = ["ana.hip", "kernels_exact.hip", "kernels_fast.hip", "gemm_wide.hip", "sampler.hip", "decode_persist.hip",
+           "ftc2.cpp", "bpe.cpp"]
 OBJDIR = os.path.join(HERE, "_build")
 
 

@@ -452,6 +452,9 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
   // (d_hh holds this gate|up's outputs only if the path below writes them)
   const bool hh_was = c->hh_bf;
   if (g0.mode == GM_SILU) c->hh_bf = false;
+  // the hidden rows exist only in bf16 after a gate|up that wrote d_hh, so
+  // down must take the path that reads them there
+  const bool hh_only = g0.X == c->HH && hh_was;
   const bool pk_ok = gemm_pk_fits(g0) || (kind == ANA_K_HEAD && head_pw_fits(g0));
   const ana_ctx::PkEnt* pe =
       fast_mode(c) && !small && g0.B < (chunk ? 128u : kPwMaxB) && pk_ok ? find_pk(c, g0) : nullptr;
@@ -468,6 +471,7 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
     }
     double by = gemv_bytes(g);
     if (bf) by -= 2.0 * (g.seg[0].rows + (g.nseg > 1 ? g.seg[1].rows : 0)) * g.K;
+    if (hh_only && (small || pe)) return hipErrorInvalidValue;
     ProfScope ps(c, kind, by, true);
     if (small) return launch_gemv_fast(g, c->st, ps.start(), ps.stop());
     if (pe && kind == ANA_K_HEAD && head_pw_fits(g))
@@ -475,17 +479,19 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
     if (pe)
       return launch_gemm_pk(g, static_cast<const char*>(c->PK) + pe->off, pe->bf, c->st, ps.start(), ps.stop());
     if (g.B >= 128 && c->d_sah && bf && g.K % 64 == 0 && g.B <= c->rows) {
-      // gate|up also leaves its outputs in bf16, and down reads them
-      // there instead of splitting them again
-      if (g.mode == GM_SILU && c->d_hh && gemm_dl2_takes(g)) g.Yh = c->d_hh;
+      // gate|up leaves its outputs in bf16 only, and down reads them there
+      // instead of splitting them again
+      if (g.mode == GM_SILU && c->d_hh && gemm_wide_takes(g)) g.Yh = c->d_hh;
       if (g.X == c->HH && hh_was && !g.ng && g.K == c->cfg.f) g.Xh = c->d_hh;
       const hipError_t e = launch_gemm_dl(g, c->d_sah, c->d_rsc, c->rows, c->st, ps.start(), ps.stop());
       if (g.mode == GM_SILU) c->hh_bf = g.Yh != nullptr && e == hipSuccess;
       return e;
     }
+    if (hh_only) return hipErrorInvalidValue;
     if (g.B >= 128) return launch_gemm_big(g, c->st, ps.start(), ps.stop());
     return launch_gemm_mfma(g, c->st, ps.start(), ps.stop());
   }
+  if (hh_only) return hipErrorInvalidValue;
   ProfScope ps(c, kind, gemv_bytes(g0), true);
   return launch_gemv(g0, c->st, ps.start(), ps.stop());
 }

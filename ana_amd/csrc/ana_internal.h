@@ -67,7 +67,8 @@ struct GemvArgs {
                              // (small batches only)
   const uint16_t* Wh0;       // fast products: the segments' rows as bfloat16
   const uint16_t* Wh1;       // (nullptr: read the fp32 rows)
-  __bf16* Yh;                // ANA_BF16 prefill, SiLU: the outputs in bf16 too, [B][seg0.rows]
+  __bf16* Yh;                // ANA_BF16 prefill, SiLU: the outputs in bf16 only (seg0.Y not
+                             // written), [B][seg0.rows]
   const __bf16* Xh;          // ANA_BF16 prefill, no norm: X already in bf16, [B][K]
 };
 // The two row segments as plain values (a runtime index into GemvArgs.seg
@@ -352,9 +353,11 @@ hipError_t launch_gemm_big(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nu
 // rounded to bf16 (Ah: B x K; rsc: B norm scales), then the product with
 // both operands streamed straight into LDS (K a multiple of 64)
 // (cap_rows: the rows Ah and rsc hold; larger batches are rejected)
-// whether launch_gemm_dl takes product a on its 256 x 256 tiles (the only
-// ones that write Yh)
-bool gemm_dl2_takes(const GemvArgs& a);
+// whether launch_gemm_dl takes product a on the 256 x 256 wide-wave tiles
+// (gemm_wide.hip), the only ones that write Yh
+bool gemm_wide_takes(const GemvArgs& a);
+// the wide-wave tiles alone (A in bf16, rsc the norm scales with a gain)
+hipError_t launch_gemm_wide(const GemvArgs& a, const __bf16* Ah, const float* rsc, hipStream_t st);
 hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t cap_rows,
                           hipStream_t st, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 size_t attn_fast_part_floats(uint32_t B, uint32_t heads, uint32_t ctx, uint32_t hd);

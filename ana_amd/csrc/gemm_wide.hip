@@ -1,0 +1,379 @@
+// ANA_BF16 prefill products on wide wave tiles (gfx950).
+//
+// Y[m][n] = sum_k A[m][k] W[n][k] for the layer products of a prefill step
+// of thousands of rows: A the activations in bf16 (k_split, or the bf16
+// hidden rows gate|up leaves), W the bf16 weights; norm scale, SiLU and
+// residual in the epilogue.
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+#include <utility>
+
+#include "ana_internal.h"
+#include "mfma.h"
+
+namespace ana {
+
+namespace {
+
+constexpr int kWideBK = 32;
+
+// A (WM * NI * 16) x (WN * NJ * 16) tile of WM x WN waves, each
+// (NI * 16) x (NJ * 16) (NI x NJ v_mfma_f32_16x16x32_bf16 tiles). K goes
+// through a ring of four 32-k stages (the A and weight tiles as 1 KB chunks
+// of 16 rows, a row's four 16-byte k pieces at slot piece ^ ((row >> 1) &
+// 3), so a fragment read touches eight distinct 16-byte bank groups),
+// filled by global_load_lds four stages ahead; each wave reads stage s + 1's
+// fragments from LDS into its second register set while its MFMAs run on
+// stage s's. Norm scale, residual and SiLU in the epilogue (SiLU: the
+// tile's first half of columns are gate rows, the second half the matching
+// up rows).
+template <int WM, int WN, int NI, int NJ>
+__global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArgs a, const __bf16* __restrict__ Ahg,
+                                                                         const float* __restrict__ rscg) {
+  constexpr int NW = WM * WN, NT = NW * 64;
+  constexpr int BM = WM * NI * 16, BN = WN * NJ * 16, BK = kWideBK;
+  constexpr int ACH = BM / 16, WCH = BN / 16;     // 1 KB chunks a stage
+  constexpr int AW = ACH / NW, BW = WCH / NW;     // of them a wave fills
+  static_assert(AW * NW == ACH && BW * NW == WCH, "chunks split evenly over the waves");
+  static_assert(BM == 256, "one norm scale a thread of the first 256");
+  constexpr int SO = (ACH + WCH) * 512;           // bf16 elements of a stage object
+  static_assert(SO * 2 >= 64 * (BN / 2) * 4, "a stage object holds 64 rows of the SiLU exchange");
+  __shared__ __align__(1024) __bf16 st0[SO], st1[SO], st2[SO], st3[SO];
+  __shared__ float rsl[BM];
+  auto stage = [&](auto B) -> __bf16* {
+    if constexpr (decltype(B)::value == 0) return st0;
+    else if constexpr (decltype(B)::value == 1) return st1;
+    else if constexpr (decltype(B)::value == 2) return st2;
+    else return st3;
+  };
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t wm = wv / WN, wn = wv % WN;
+  uint32_t ntile, mtile;
+  xcd_tile(&ntile, &mtile);
+  const uint32_t m0 = mtile * BM;
+  const uint32_t nb = min((uint32_t)BM, a.B - m0);
+  const uint32_t K = a.K, nst = K / BK;
+  const Segs sgs(a);
+  // wave wv fills A chunks AW wv .. and weight chunks BW wv .. of each
+  // stage (chunk c: tile rows 16 c .. 16 c + 15), this lane's 16-byte piece
+  // of each
+  // (as 32-bit byte offsets from a uniform base, so each load is the
+  // base in SGPRs plus one VGPR: the weights' base is the lower of the two
+  // segments', which lie in one buffer)
+  const uint32_t pr = lane >> 2, pq = (lane & 3) ^ ((pr >> 1) & 3);
+  const char* const abase = reinterpret_cast<const char*>(Ahg);
+  const uint16_t* const wlo = a.nseg > 1 && a.Wh1 < a.Wh0 ? a.Wh1 : a.Wh0;
+  const char* const wbase = reinterpret_cast<const char*>(wlo);
+  uint32_t aoff[AW], boff[BW];
+#pragma unroll
+  for (int h = 0; h < AW; h++) {
+    const uint32_t r = 16 * (AW * wv + h) + pr;
+    aoff[h] = 2 * ((m0 + (r < nb ? r : 0)) * K + 8 * pq);
+  }
+#pragma unroll
+  for (int h = 0; h < BW; h++) {
+    const uint32_t r = 16 * (BW * wv + h) + pr;
+    const float* w;
+    uint32_t sg, lr;
+    const bool ok = sgs.row(BN, ntile, r, &w, &sg, &lr);
+    const uint16_t* p = ok ? (sg ? a.Wh1 : a.Wh0) + (size_t)lr * K + 8 * pq : a.Wh0 + 8 * pq;
+    boff[h] = (uint32_t)(reinterpret_cast<const char*>(p) - wbase);
+  }
+  // AW + BW loads a wave a stage
+  auto issue = [&](uint32_t s, auto B) {
+    const uint32_t kb = s * BK * 2;
+#pragma unroll
+    for (int h = 0; h < AW; h++)
+      __builtin_amdgcn_global_load_lds((const void*)(abase + (aoff[h] + kb)), (lds_void*)(stage(B) + (AW * wv + h) * 512), 16, 0, 0);
+#pragma unroll
+    for (int h = 0; h < BW; h++)
+      __builtin_amdgcn_global_load_lds((const void*)(wbase + (boff[h] + kb)), (lds_void*)(stage(B) + (ACH + BW * wv + h) * 512), 16, 0, 0);
+  };
+  f32x4_t acc[NI][NJ];
+#pragma unroll
+  for (int i = 0; i < NI; i++)
+#pragma unroll
+    for (int j = 0; j < NJ; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t r16 = lane & 15, g4 = lane >> 4;
+  const uint32_t foff = r16 * 32 + 8 * (g4 ^ ((r16 >> 1) & 3));
+  bf16x8_t fa0[NI], fb0[NJ], fa1[NI], fb1[NJ];
+  auto lread = [&](auto B, bf16x8_t* fa, bf16x8_t* fb) {
+    const __bf16* S = stage(B);
+#pragma unroll
+    for (int i = 0; i < NI; i++) fa[i] = *reinterpret_cast<const bf16x8_t*>(S + (wm * NI + i) * 512 + foff);
+#pragma unroll
+    for (int j = 0; j < NJ; j++) fb[j] = *reinterpret_cast<const bf16x8_t*>(S + (ACH + wn * NJ + j) * 512 + foff);
+  };
+  auto mma = [&](const bf16x8_t* fa, const bf16x8_t* fb) {
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+#pragma unroll
+      for (int j = 0; j < NJ; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+  };
+  // the waits and the barrier, with nothing moved across them: a memory
+  // clobber so no LDS access crosses (the barrier builtin alone orders no
+  // memory), and scheduling barriers so no MFMA does (the scheduler would
+  // otherwise pull the next step's MFMAs up to the fragments they read and
+  // wait on those reads there)
+  auto step_barrier = [&](auto W) {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    ANA_LGKMCNT0();
+    ANA_VMCNT(decltype(W)::value);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // step s (object B, its fragments already in register set P): this
+  // wave's reads of them are done, and its loads of stage s + 1 (W younger
+  // loads may still be in flight); the barrier makes every wave's loads of
+  // s + 1 visible and says every wave is done reading object B, which stage
+  // s + 4 then fills; then s + 1's fragments into set Q, issued before s's
+  // MFMAs, which do not wait on them. Every wait is unconditional and K is
+  // a multiple of 128 (stages in fours, the last four peeled), so the
+  // compiler adds no wait of its own.
+  auto step = [&](uint32_t s, auto B, auto Bn, auto W, bool more, bf16x8_t* pa, bf16x8_t* pb, bf16x8_t* qa,
+                  bf16x8_t* qb) {
+    step_barrier(W);
+    if (more) issue(s + 4, B);
+    lread(Bn, qa, qb);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(pa, pb);
+  };
+  constexpr std::integral_constant<int, 0> S0{};
+  constexpr std::integral_constant<int, 1> S1{};
+  constexpr std::integral_constant<int, 2> S2{};
+  constexpr std::integral_constant<int, 3> S3{};
+  constexpr std::integral_constant<int, 3 * (AW + BW)> W3{};
+  constexpr std::integral_constant<int, 2 * (AW + BW)> W2{};   // two stages' loads
+  constexpr std::integral_constant<int, AW + BW> W1{};
+  constexpr std::integral_constant<int, 0> W0{};
+  issue(0, S0);
+  issue(1, S1);
+  issue(2, S2);
+  issue(3, S3);
+  step_barrier(W3);
+  lread(S0, fa0, fb0);
+  uint32_t s = 0;
+  for (; s + 4 < nst; s += 4) {
+    step(s, S0, S1, W2, true, fa0, fb0, fa1, fb1);
+    step(s + 1, S1, S2, W2, true, fa1, fb1, fa0, fb0);
+    step(s + 2, S2, S3, W2, true, fa0, fb0, fa1, fb1);
+    step(s + 3, S3, S0, W2, true, fa1, fb1, fa0, fb0);
+  }
+  step(s, S0, S1, W2, false, fa0, fb0, fa1, fb1);
+  step(s + 1, S1, S2, W1, false, fa1, fb1, fa0, fb0);
+  step(s + 2, S2, S3, W0, false, fa0, fb0, fa1, fb1);
+  mma(fa1, fb1);
+  const bool norm = a.ng != nullptr;
+  // results: tile (i, j) of the wave holds rows wm*NI*16 + 16i + 4*g4 + r,
+  // column wn*NJ*16 + 16j + r16; the row norm scales go to LDS first (every
+  // wave's fragment reads and loads are done at the barrier)
+  ANA_VMCNT(0);
+  __syncthreads();
+  if (norm) {
+    for (uint32_t t = tid; t < (uint32_t)BM; t += NT) rsl[t] = rscg[m0 + (t < nb ? t : 0)];
+    __syncthreads();
+  }
+  auto rs = [&](int i, int r) { return norm ? rsl[wm * NI * 16 + 16 * i + 4 * g4 + r] : 1.0f; };
+  // full tiles (every row and column valid; every tile of the 8192-row
+  // prefill products) store without a check or a load among the stores:
+  // with per-element bounds checks, per-element scale lookups and loads
+  // between the stores, the compiler drained the stores (vmcnt(0)) again
+  // and again, and the epilogue took longer than the k loop
+  const uint32_t wrows = a.mode == GM_SILU ? a.seg[0].rows : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
+  const uint32_t wper = a.mode == GM_SILU ? BN / 2 : BN;
+  const bool full = nb == (uint32_t)BM && (ntile + 1) * wper <= wrows && a.mode != GM_RESID;
+  if (full) {
+    float sc[NI][4];
+    if (norm) {
+#pragma unroll
+      for (int i = 0; i < NI; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) sc[i][r] = rsl[wm * NI * 16 + 16 * i + 4 * g4 + r];
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) sc[i][r] = 1.0f;
+    }
+    const size_t mrow = m0 + wm * NI * 16 + 4 * g4;   // this lane's first row
+    if (a.mode == GM_SILU) {
+      constexpr int HB = BN / 2;
+      auto upat = [&](uint32_t m) -> float* {
+        const uint32_t q = m >> 6;
+        return reinterpret_cast<float*>(q == 0 ? st0 : q == 1 ? st1 : q == 2 ? st2 : st3) + (m & 63) * HB;
+      };
+      if (wn >= (uint32_t)(WN / 2)) {
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            float* up = upat(wm * NI * 16 + 16 * i + 4 * g4 + r) + (wn - WN / 2) * NJ * 16 + r16;
+#pragma unroll
+            for (int j = 0; j < NJ; j++) up[16 * j] = acc[i][j][r] * sc[i][r];
+          }
+      }
+      __syncthreads();
+      if (wn < (uint32_t)(WN / 2)) {
+        // gate row j of this lane's columns: the tile's column n is gate
+        // row ntile * HB + n
+        const uint32_t lr0 = ntile * HB + wn * NJ * 16 + r16;
+        float hv[NI][4][NJ];
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const float* up = upat(wm * NI * 16 + 16 * i + 4 * g4 + r) + wn * NJ * 16 + r16;
+#pragma unroll
+            for (int j = 0; j < NJ; j++) hv[i][r][j] = fast_silu(acc[i][j][r] * sc[i][r]) * up[16 * j];
+          }
+        if (a.Yh) {
+          __bf16* yb = a.Yh + mrow * a.seg[0].rows + lr0;
+#pragma unroll
+          for (int i = 0; i < NI; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+              for (int j = 0; j < NJ; j++) yb[(size_t)(16 * i + r) * a.seg[0].rows + 16 * j] = (__bf16)hv[i][r][j];
+        } else {
+          float* yb = a.seg[0].Y + mrow * a.seg[0].ldy + lr0;
+#pragma unroll
+          for (int i = 0; i < NI; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+              for (int j = 0; j < NJ; j++) yb[(size_t)(16 * i + r) * a.seg[0].ldy + 16 * j] = hv[i][r][j];
+        }
+      }
+      return;
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      // this lane's column: the segment and row it falls in, by selects
+      const uint32_t v = ntile * BN + wn * NJ * 16 + 16 * j + r16;
+      const bool s1 = v >= a.seg[0].rows;
+      float* const Yb = s1 ? a.seg[1].Y : a.seg[0].Y;
+      const uint32_t ld = s1 ? a.seg[1].ldy : a.seg[0].ldy;
+      float* yb = Yb + mrow * ld + (s1 ? v - a.seg[0].rows : v);
+#pragma unroll
+      for (int i = 0; i < NI; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) yb[(size_t)(16 * i + r) * ld] = acc[i][j][r] * sc[i][r];
+    }
+    return;
+  }
+  if (a.mode == GM_SILU) {
+    // up columns (the second half of the waves' columns) through LDS to the
+    // gate columns: tile rows 64 q .. 64 q + 63 in stage object q
+    constexpr int HB = BN / 2;
+    auto upat = [&](uint32_t m) -> float* {
+      const uint32_t q = m >> 6;
+      return reinterpret_cast<float*>(q == 0 ? st0 : q == 1 ? st1 : q == 2 ? st2 : st3) + (m & 63) * HB;
+    };
+    if (wn >= (uint32_t)(WN / 2)) {
+#pragma unroll
+      for (int i = 0; i < NI; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const uint32_t m = wm * NI * 16 + 16 * i + 4 * g4 + r;
+          float* up = upat(m);
+          const float sc = rs(i, r);
+#pragma unroll
+          for (int j = 0; j < NJ; j++) up[(wn - WN / 2) * NJ * 16 + 16 * j + r16] = acc[i][j][r] * sc;
+        }
+    }
+    __syncthreads();
+    if (wn < (uint32_t)(WN / 2)) {
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const uint32_t n = wn * NJ * 16 + 16 * j + r16;
+        const float* w_;
+        uint32_t sg, lr;
+        if (!sgs.row(BN, ntile, n, &w_, &sg, &lr)) continue;
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const uint32_t m = wm * NI * 16 + 16 * i + 4 * g4 + r;
+            if (m >= nb) continue;
+            const float y = acc[i][j][r] * rs(i, r);
+            const float hv = fast_silu(y) * upat(m)[n];
+            if (a.Yh) a.Yh[(size_t)(m0 + m) * a.seg[0].rows + lr] = (__bf16)hv;
+            else a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = hv;
+          }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    // one column block's residuals live at a time
+    asm volatile("" ::: "memory");
+    const uint32_t n = wn * NJ * 16 + 16 * j + r16;
+    const float* w_;
+    uint32_t sg, lr;
+    if (!sgs.row(BN, ntile, n, &w_, &sg, &lr)) continue;
+    float res[NI][4];
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t m = wm * NI * 16 + 16 * i + 4 * g4 + r;
+        res[i][r] = a.mode == GM_RESID && m < nb ? a.R[(size_t)(m0 + m) * a.ldr + lr] : 0.0f;
+      }
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t m = wm * NI * 16 + 16 * i + 4 * g4 + r;
+        if (m >= nb) continue;
+        float y = acc[i][j][r] * rs(i, r);
+        if (a.mode == GM_RESID) y = res[i][r] + y;
+        if (sg) a.seg[1].Y[(size_t)(m0 + m) * a.seg[1].ldy + lr] = y;
+        else a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = y;
+      }
+  }
+}
+
+// the configuration launched: 2 x 4 waves of 128 x 64 on a 256 x 256 tile,
+// two waves a SIMD (128 accumulators and two fragment sets of 12 in 256
+// registers); each wave reads 12 KB of fragments a 32-k stage for 32 MFMAs,
+// against 8 KB for 16 in sixteen waves of 64 x 64. Four waves of 128 x 96
+// ran at two thirds of this rate: with one wave a SIMD nothing covered a
+// stall, and their 192 accumulators sat in AGPRs, where the allocator moved
+// them between MFMAs
+constexpr int kWM = 2, kWN = 4, kNI = 8, kNJ = 4;
+constexpr int kWideBM = kWM * kNI * 16, kWideBN = kWN * kNJ * 16;
+
+uint32_t wide_tiles(const GemvArgs& a) {
+  const uint32_t rows = a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
+  return a.mode == GM_SILU ? (a.seg[0].rows + kWideBN / 2 - 1) / (kWideBN / 2) : (rows + kWideBN - 1) / kWideBN;
+}
+
+}  // namespace
+
+bool gemm_wide_takes(const GemvArgs& a) {
+  const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
+                                          : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
+  return rows >= 2048 && wide_tiles(a) * ((a.B + kWideBM - 1) / kWideBM) >= 256 && a.K % 128 == 0;
+}
+
+hipError_t launch_gemm_wide(const GemvArgs& a, const __bf16* Ah, const float* rsc, hipStream_t st) {
+  if (!gemm_wide_takes(a) || a.amax || !a.Wh0 || (a.nseg > 1 && !a.Wh1)) return hipErrorInvalidValue;
+  // the A and weight offsets are 32-bit byte offsets
+  if (2ull * a.B * a.K >= (1ull << 32)) return hipErrorInvalidValue;
+  {
+    const uint16_t* lo = a.nseg > 1 && a.Wh1 < a.Wh0 ? a.Wh1 : a.Wh0;
+    const uint16_t* e0 = a.Wh0 + (size_t)a.seg[0].rows * a.K;
+    const uint16_t* e1 = a.nseg > 1 ? a.Wh1 + (size_t)a.seg[1].rows * a.K : e0;
+    const uint16_t* hi = e1 > e0 ? e1 : e0;
+    if ((uint64_t)(hi - lo) * 2 >= (1ull << 32)) return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL((k_gemm_wide<kWM, kWN, kNI, kNJ>), dim3(wide_tiles(a), (a.B + kWideBM - 1) / kWideBM),
+                     dim3(kWM * kWN * 64), 0, st, a, Ah, rsc);
+  return hipGetLastError();
+}
+
+}  // namespace ana

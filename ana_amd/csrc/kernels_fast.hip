@@ -12,19 +12,12 @@
 #include <utility>
 
 #include "ana_internal.h"
+#include "mfma.h"
 #include "numerics.h"
 #include "pick_row.h"
 #include "wave.h"
 
 namespace ana {
-
-// MFMA operand and accumulator vectors
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-// an LDS address for global_load_lds
-typedef __attribute__((address_space(3))) void lds_void;
-// vmcnt(n) alone (expcnt and lgkmcnt at their maxima)
-#define ANA_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
 
 // ------------------------------------------------------------------ weights
 
@@ -70,8 +63,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
   return v;
 }
-
-__device__ __forceinline__ float fast_silu(float z) { return z / (1.0f + __expf(-z)); }
 
 // ------------------------------------------------------------------ products
 
@@ -2541,18 +2532,6 @@ __global__ __launch_bounds__(256) void k_split(const float* __restrict__ X, uint
   }
 }
 
-// Workgroup -> (n tile, m tile) so that the workgroups one XCD runs (ids
-// equal mod 8) take consecutive tiles, n fastest: the A rows those n tiles
-// share stay in that XCD's L2.
-__device__ __forceinline__ void xcd_tile(uint32_t* nt, uint32_t* mt) {
-  const uint32_t NT = gridDim.x, total = gridDim.x * gridDim.y;
-  const uint32_t L = blockIdx.x + blockIdx.y * NT;
-  const uint32_t x = L % 8, idx = L / 8, per = total / 8, rem = total % 8;
-  const uint32_t g = (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + idx;
-  *nt = g % NT;
-  *mt = g / NT;
-}
-
 // Y[m][n] = sum_k A[m][k] W[n][k] for ANA_BF16 prefill steps of >= 128 rows,
 // A given as bf16 (k_split): a 128 x 128 tile per workgroup, four waves of
 // 64 x 64 (4 x 4 v_mfma_f32_16x16x32_bf16 tiles). K goes in stages of 64
@@ -2671,6 +2650,59 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
     __syncthreads();
   }
   auto rs = [&](int i, int r) { return norm ? rsl[wm * 64 + 16 * i + 4 * g4 + r] : 1.0f; };
+  // full tiles (every row and column valid) of plain and residual products
+  // store without a check among the stores, the residuals all loaded first:
+  // with per-element checks and each column block's residual loads after
+  // the previous block's stores, the compiler drained the stores
+  // (vmcnt(0)) before every block
+  const uint32_t wrows = a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
+  if (a.mode != GM_SILU && nb == (uint32_t)BM && (ntile + 1) * BN <= wrows) {
+    float sc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) sc[i][r] = norm ? rsl[wm * 64 + 16 * i + 4 * g4 + r] : 1.0f;
+    const size_t mrow = m0 + wm * 64 + 4 * g4;   // this lane's first row
+    uint32_t col[4];
+    bool s1[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t v = ntile * BN + wn * 64 + 16 * j + r16;
+      s1[j] = v >= a.seg[0].rows;
+      col[j] = s1[j] ? v - a.seg[0].rows : v;
+    }
+    float res[4][4][4];
+    if (a.mode == GM_RESID) {
+      const float* rb = a.R + mrow * a.ldr;
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) res[j][i][r] = rb[(size_t)(16 * i + r) * a.ldr + col[j]];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) res[j][i][r] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float* const Yb = s1[j] ? a.seg[1].Y : a.seg[0].Y;
+      const uint32_t ld = s1[j] ? a.seg[1].ldy : a.seg[0].ldy;
+      float* yb = Yb + mrow * ld + col[j];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float y = acc[i][j][r] * sc[i][r];
+          yb[(size_t)(16 * i + r) * ld] = a.mode == GM_RESID ? res[j][i][r] + y : y;
+        }
+    }
+    return;
+  }
   if (a.mode == GM_SILU) {
     // up columns (wn = 1) through LDS to the gate columns (wn = 0), one
     // 64-row half at a time
@@ -2745,179 +2777,6 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
   }
 }
 
-// The same product on a 256 x 256 tile per workgroup of sixteen waves
-// (wave w: rows 64 (w / 4) .., columns 64 (w % 4) .., 4 x 4 MFMA tiles),
-// for products of 2048 output rows or more at prefill shapes: each staged
-// byte feeds twice the flops it feeds in the 128 x 128 tile. Stages of 64
-// k (both operands, 64 KB) through two LDS buffers, loaded as k_gemm_dl
-// loads them (wave w the rows 16 w .. 16 w + 15 of A and of the weights).
-// SiLU: the tile's columns 0..127 are gate rows j, 128..255 the matching up
-// rows; the up waves hand their results to the gate waves through LDS.
-__global__ __launch_bounds__(1024) void k_gemm_dl2(GemvArgs a, const __bf16* __restrict__ Ahg,
-                                                    const float* __restrict__ rscg) {
-  constexpr int BM = 256, BN = 256, BK = 64;
-  constexpr int TILE = BM * 32;   // bf16 elements of one operand's k half (16 KB)
-  // one LDS object per stage, as in k_gemm_dl
-  __shared__ __align__(1024) __bf16 st0[2][2][TILE], st1[2][2][TILE];
-  __shared__ float rsl[BM];
-  auto stage = [&](auto B) -> __bf16(*)[2][TILE] {
-    if constexpr (decltype(B)::value == 0) return st0;
-    else return st1;
-  };
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const uint32_t wm = wv >> 2, wn = wv & 3;
-  uint32_t ntile, mtile;
-  xcd_tile(&ntile, &mtile);
-  const uint32_t m0 = mtile * BM;
-  const uint32_t nb = min((uint32_t)BM, a.B - m0);
-  const uint32_t K = a.K, nst = K / BK;
-  const Segs sgs(a);
-  // this lane's piece of the wave's 1 KB chunk per operand and k half
-  // (chunk wv: tile rows 16 wv .. 16 wv + 15)
-  const uint32_t pr = lane >> 2, pq = (lane & 3) ^ ((pr >> 1) & 3);
-  const uint32_t r0 = 16 * wv + pr;
-  const uint32_t aoff = (m0 + (r0 < nb ? r0 : 0)) * K + 8 * pq;
-  const uint16_t* bptr;
-  {
-    const float* w;
-    uint32_t sg, lr;
-    const bool ok = sgs.row(BN, ntile, r0, &w, &sg, &lr);
-    bptr = ok ? (sg ? a.Wh1 : a.Wh0) + (size_t)lr * K + 8 * pq : a.Wh0 + 8 * pq;
-  }
-  auto issue = [&](uint32_t s, auto B) {
-    const uint32_t k0 = s * BK;
-#pragma unroll
-    for (int kh = 0; kh < 2; kh++) {
-      __builtin_amdgcn_global_load_lds((const void*)(Ahg + aoff + k0 + 32 * kh), (lds_void*)&stage(B)[0][kh][wv * 512], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(bptr + k0 + 32 * kh), (lds_void*)&stage(B)[1][kh][wv * 512], 16, 0, 0);
-    }
-  };
-  f32x4_t acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  const uint32_t r16 = lane & 15, g4 = lane >> 4;
-  const uint32_t foff = r16 * 32 + 8 * (g4 ^ ((r16 >> 1) & 3));
-  auto compute = [&](auto B) {
-#pragma unroll
-    for (int kh = 0; kh < 2; kh++) {
-      const __bf16* A0 = &stage(B)[0][kh][0];
-      const __bf16* B0 = &stage(B)[1][kh][0];
-      bf16x8_t bfr[4], ah[4];
-#pragma unroll
-      for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(B0 + (wn * 4 + j) * 512 + foff);
-#pragma unroll
-      for (int i = 0; i < 4; i++) ah[i] = *reinterpret_cast<const bf16x8_t*>(A0 + (wm * 4 + i) * 512 + foff);
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bfr[j], acc[i][j], 0, 0, 0);
-    }
-  };
-  constexpr std::integral_constant<int, 0> S0{};
-  constexpr std::integral_constant<int, 1> S1{};
-  issue(0, S0);
-  // this wave's loads of stage s are done, then every wave's; the barrier
-  // also says every wave is done with the object stage s + 1 fills
-  for (uint32_t s = 0; s < nst; s += 2) {
-    ANA_VMCNT(0);
-    __builtin_amdgcn_s_barrier();
-    if (s + 1 < nst) issue(s + 1, S1);
-    compute(S0);
-    if (s + 1 < nst) {
-      ANA_VMCNT(0);
-      __builtin_amdgcn_s_barrier();
-      if (s + 2 < nst) issue(s + 2, S0);
-      compute(S1);
-    }
-  }
-  const bool norm = a.ng != nullptr;
-  // results: tile (i, j) of the wave holds rows wm*64 + 16i + 4*g4 + r,
-  // column wn*64 + 16j + r16; the row norm scales go to LDS first
-  ANA_VMCNT(0);
-  __syncthreads();
-  if (norm) {
-    if (tid < (uint32_t)BM) rsl[tid] = rscg[m0 + (tid < nb ? tid : 0)];
-    __syncthreads();
-  }
-  auto rs = [&](int i, int r) { return norm ? rsl[wm * 64 + 16 * i + 4 * g4 + r] : 1.0f; };
-  if (a.mode == GM_SILU) {
-    // up columns (wn 2, 3) through LDS to the gate columns (wn 0, 1): rows
-    // 0..127 in the first stage object, 128..255 in the second (64 KB each)
-    static_assert(sizeof(st0) == 128 * 128 * sizeof(float), "exchange halves");
-    float* up = reinterpret_cast<float*>(wm < 2 ? &st0[0][0][0] : &st1[0][0][0]);   // [m & 127][128]
-    if (wn >= 2) {
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r, n = (wn - 2) * 64 + 16 * j + r16;
-            up[(m & 127) * 128 + n] = acc[i][j][r] * rs(i, r);
-          }
-    }
-    __syncthreads();
-    if (wn < 2) {
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const uint32_t n = wn * 64 + 16 * j + r16;
-        const float* w_;
-        uint32_t sg, lr;
-        if (!sgs.row(BN, ntile, n, &w_, &sg, &lr)) continue;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r;
-            if (m >= nb) continue;
-            const float y = acc[i][j][r] * rs(i, r);
-            const float hv = fast_silu(y) * up[(m & 127) * 128 + n];
-            a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = hv;
-            if (a.Yh) a.Yh[(size_t)(m0 + m) * a.seg[0].rows + lr] = (__bf16)hv;
-          }
-      }
-    }
-    return;
-  }
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    // one column block's residuals live at a time
-    asm volatile("" ::: "memory");
-    const uint32_t n = wn * 64 + 16 * j + r16;
-    const float* w_;
-    uint32_t sg, lr;
-    if (!sgs.row(BN, ntile, n, &w_, &sg, &lr)) continue;
-    float res[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r;
-        res[i][r] = a.mode == GM_RESID && m < nb ? a.R[(size_t)(m0 + m) * a.ldr + lr] : 0.0f;
-      }
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const uint32_t m = wm * 64 + 16 * i + 4 * g4 + r;
-        if (m >= nb) continue;
-        float y = acc[i][j][r] * rs(i, r);
-        if (a.mode == GM_RESID) y = res[i][r] + y;
-        if (sg) a.seg[1].Y[(size_t)(m0 + m) * a.seg[1].ldy + lr] = y;
-        else a.seg[0].Y[(size_t)(m0 + m) * a.seg[0].ldy + lr] = y;
-      }
-  }
-}
-
-bool gemm_dl2_takes(const GemvArgs& a) {
-  const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
-                                          : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
-  const uint32_t tiles2 = a.mode == GM_SILU ? (a.seg[0].rows + 127) / 128 : (rows + 255) / 256;
-  return rows >= 2048 && tiles2 * ((a.B + 255) / 256) >= 256;
-}
-
 hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t cap_rows,
                           hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   if (a.amax || (a.K % 64) || a.B == 0 || !a.Wh0 || (a.nseg > 1 && !a.Wh1)) return hipErrorInvalidValue;
@@ -2929,14 +2788,14 @@ hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t ca
   else hipLaunchKernelGGL(k_split, dim3((a.B + 3) / 4), dim3(256), 0, st, a.X, a.ldx, a.K, a.ng, a.B, Ah, rsc);
   const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
                                           : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
-  // the 256 x 256 tiles where they still give every CU a workgroup
-  if (gemm_dl2_takes(a)) {
-    const uint32_t tiles2 = a.mode == GM_SILU ? (a.seg[0].rows + 127) / 128 : (rows + 255) / 256;
-    hipLaunchKernelGGL(k_gemm_dl2, dim3(tiles2, (a.B + 255) / 256), dim3(1024), 0, st, a, Ah, rsc);
+  // the 256 x 256 wide-wave tiles (gemm_wide.hip) where they still give
+  // every CU a workgroup
+  if (gemm_wide_takes(a)) {
+    const hipError_t e = launch_gemm_wide(a, Ah, rsc, st);
     if (e1) (void)hipEventRecord(e1, st);
-    return hipGetLastError();
+    return e;
   }
-  if (a.Yh) return hipErrorInvalidValue;   // (only the 256 x 256 tiles write bf16 outputs)
+  if (a.Yh) return hipErrorInvalidValue;   // (only the large tiles write bf16 outputs)
   const uint32_t per = a.mode == GM_SILU ? 64 : 128;
   const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
   dim3 grid(tiles, (a.B + 127) / 128);

@@ -283,7 +283,7 @@ def run_prefill(path: str, c, reps: int = 5) -> dict:
             "workload": "64 prompts x 512 tokens through ana_feeds_n, chunk 128; flops = 2 x "
                         "(P - v d) per token (the products) + causal attention 2 B L^2 d per "
                         "softmax layer (the GLA scan not counted)",
-            "kernels": ("products k_split + k_gemm_dl2 / k_gemm_dl (256 x 256 and 128 x 128 MFMA tiles, "
+            "kernels": ("products k_split + k_gemm_wide / k_gemm_dl (256 x 256 and 128 x 128 MFMA tiles, "
                         "bf16 weights x bf16 activations, both streamed straight into LDS)" if m == "bf16" else
                         "products k_gemm_big (128 x 128 MFMA tiles, fp32 MFMA)")
                        + ", attention k_attn_flash (fp32 MFMA), GLA k_gla_sub + k_gla_carry",
