@@ -34,8 +34,12 @@ __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArg
   constexpr int NW = WM * WN, NT = NW * 64;
   constexpr int BM = WM * NI * 16, BN = WN * NJ * 16, BK = kWideBK;
   constexpr int ACH = BM / 16, WCH = BN / 16;     // 1 KB chunks a stage
-  constexpr int AW = ACH / NW, BW = WCH / NW;     // of them a wave fills
-  static_assert(AW * NW == ACH && BW * NW == WCH, "chunks split evenly over the waves");
+  // of them a wave fills: the A chunks split evenly; the weight chunks
+  // round up, the spare slots loading chunks 0, 1, .. again (the same
+  // bytes to the same place), so every wave issues the same count and the
+  // compile-time waits hold for each
+  constexpr int AW = ACH / NW, BW = (WCH + NW - 1) / NW;
+  static_assert(AW * NW == ACH, "A chunks split evenly over the waves");
   static_assert(BM == 256, "one norm scale a thread of the first 256");
   constexpr int SO = (ACH + WCH) * 512;           // bf16 elements of a stage object
   static_assert(SO * 2 >= 64 * (BN / 2) * 4, "a stage object holds 64 rows of the SiLU exchange");
@@ -73,7 +77,7 @@ __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArg
   }
 #pragma unroll
   for (int h = 0; h < BW; h++) {
-    const uint32_t r = 16 * (BW * wv + h) + pr;
+    const uint32_t r = 16 * ((BW * wv + h) % WCH) + pr;
     const float* w;
     uint32_t sg, lr;
     const bool ok = sgs.row(BN, ntile, r, &w, &sg, &lr);
@@ -88,7 +92,7 @@ __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArg
       __builtin_amdgcn_global_load_lds((const void*)(abase + (aoff[h] + kb)), (lds_void*)(stage(B) + (AW * wv + h) * 512), 16, 0, 0);
 #pragma unroll
     for (int h = 0; h < BW; h++)
-      __builtin_amdgcn_global_load_lds((const void*)(wbase + (boff[h] + kb)), (lds_void*)(stage(B) + (ACH + BW * wv + h) * 512), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(wbase + (boff[h] + kb)), (lds_void*)(stage(B) + (ACH + (BW * wv + h) % WCH) * 512), 16, 0, 0);
   };
   f32x4_t acc[NI][NJ];
 #pragma unroll
@@ -337,19 +341,28 @@ __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArg
   }
 }
 
-// the configuration launched: 2 x 4 waves of 128 x 64 on a 256 x 256 tile,
+// the configurations launched: 2 x 4 waves of 128 x 64 on a 256 x 256 tile,
 // two waves a SIMD (128 accumulators and two fragment sets of 12 in 256
 // registers); each wave reads 12 KB of fragments a 32-k stage for 32 MFMAs,
 // against 8 KB for 16 in sixteen waves of 64 x 64. Four waves of 128 x 96
 // ran at two thirds of this rate: with one wave a SIMD nothing covered a
 // stall, and their 192 accumulators sat in AGPRs, where the allocator moved
-// them between MFMAs
-constexpr int kWM = 2, kWN = 4, kNI = 8, kNJ = 4;
-constexpr int kWideBM = kWM * kNI * 16, kWideBN = kWN * kNJ * 16;
+// them between MFMAs. And 4 x 2 waves of 64 x 96 on a 256 x 192 tile, for
+// products whose 256-wide tiles leave the last round of workgroups part
+// empty (q|k|v|z at 3072 output rows: 384 tiles, a round and a half on 256
+// CUs, against 512 of three quarters the work)
+constexpr int kWideBM = 256;
+constexpr int kBN256 = 256, kBN192 = 192;
 
-uint32_t wide_tiles(const GemvArgs& a) {
+uint32_t wide_tiles(const GemvArgs& a, uint32_t BN) {
   const uint32_t rows = a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
-  return a.mode == GM_SILU ? (a.seg[0].rows + kWideBN / 2 - 1) / (kWideBN / 2) : (rows + kWideBN - 1) / kWideBN;
+  return a.mode == GM_SILU ? (a.seg[0].rows + BN / 2 - 1) / (BN / 2) : (rows + BN - 1) / BN;
+}
+
+// rounds of one workgroup a CU times the work of a tile, in 64-column units
+uint32_t wide_cost(const GemvArgs& a, uint32_t BN, uint32_t cus) {
+  const uint32_t t = wide_tiles(a, BN) * ((a.B + kWideBM - 1) / kWideBM);
+  return (t + cus - 1) / cus * (BN / 64);
 }
 
 }  // namespace
@@ -357,7 +370,7 @@ uint32_t wide_tiles(const GemvArgs& a) {
 bool gemm_wide_takes(const GemvArgs& a) {
   const uint32_t rows = a.mode == GM_SILU ? 2 * a.seg[0].rows
                                           : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
-  return rows >= 2048 && wide_tiles(a) * ((a.B + kWideBM - 1) / kWideBM) >= 256 && a.K % 128 == 0;
+  return rows >= 2048 && wide_tiles(a, kBN256) * ((a.B + kWideBM - 1) / kWideBM) >= 256 && a.K % 128 == 0;
 }
 
 hipError_t launch_gemm_wide(const GemvArgs& a, const __bf16* Ah, const float* rsc, hipStream_t st) {
@@ -371,8 +384,18 @@ hipError_t launch_gemm_wide(const GemvArgs& a, const __bf16* Ah, const float* rs
     const uint16_t* hi = e1 > e0 ? e1 : e0;
     if ((uint64_t)(hi - lo) * 2 >= (1ull << 32)) return hipErrorInvalidValue;
   }
-  hipLaunchKernelGGL((k_gemm_wide<kWM, kWN, kNI, kNJ>), dim3(wide_tiles(a), (a.B + kWideBM - 1) / kWideBM),
-                     dim3(kWM * kWN * 64), 0, st, a, Ah, rsc);
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return hipErrorInvalidDevice;
+    cus = n;
+  }
+  const uint32_t mt = (a.B + kWideBM - 1) / kWideBM;
+  if (wide_cost(a, kBN192, cus) < wide_cost(a, kBN256, cus))
+    hipLaunchKernelGGL((k_gemm_wide<4, 2, 4, 6>), dim3(wide_tiles(a, kBN192), mt), dim3(512), 0, st, a, Ah, rsc);
+  else
+    hipLaunchKernelGGL((k_gemm_wide<2, 4, 8, 4>), dim3(wide_tiles(a, kBN256), mt), dim3(512), 0, st, a, Ah, rsc);
   return hipGetLastError();
 }
 
