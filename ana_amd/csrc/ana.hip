@@ -753,7 +753,7 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
         // row's attention over the splits up to the step's last position
         a.QKV = c->QKV; a.O = c->O; a.B = B; a.seq = c->d_rseq; a.pos = c->d_rpos; a.write_kv = 0;
         HIPCHK(c, launch_kv_write_fast(a, c->st));
-        HIPCHK(c, launch_attn_flash(a, c->d_atab, (uint32_t)c->h_atab.size(), c->st));
+        HIPCHK(c, launch_attn_flash(a, c->d_atab, (uint32_t)c->h_atab.size(), c->mode == ANA_BF16, c->st));
       } else {
         for (const Seg& sg : *segs) {
           const bool fresh = (uint64_t)sg.pos0 + sg.T <= cf.ctx;

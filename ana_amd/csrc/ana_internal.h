@@ -368,7 +368,9 @@ constexpr uint32_t kFlashQ = 64;
 struct AttnTile {
   uint32_t seq, pos0, row0, n;  // sequence, first row's position and workspace row, rows
 };
-hipError_t launch_attn_flash(const AttnArgs& a, const AttnTile* tab, uint32_t ntiles, hipStream_t st);
+// bf: the products on the bf16 matrix cores (ANA_BF16; hd 32 or 64, else
+// the fp32 ones)
+hipError_t launch_attn_flash(const AttnArgs& a, const AttnTile* tab, uint32_t ntiles, bool bf, hipStream_t st);
 hipError_t launch_zero_u32(uint32_t* p, uint32_t n, hipStream_t st);
 hipError_t launch_zero_u64(unsigned long long* p, uint32_t n, hipStream_t st);
 

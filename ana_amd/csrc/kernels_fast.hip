@@ -993,9 +993,171 @@ __global__ __launch_bounds__(256) void k_attn_flash(AttnArgs a, const AttnTile* 
   }
 }
 
-hipError_t launch_attn_flash(const AttnArgs& a, const AttnTile* tab, uint32_t ntiles, hipStream_t st) {
+// k_attn_flash with its two products on the bf16 matrix cores (ANA_BF16,
+// hd a multiple of 32): q (qk-normed and scaled), the K and V tiles and
+// the probabilities rounded to bf16, S = q K^T and O += P V accumulated in
+// fp32 on v_mfma_f32_16x16x32_bf16 (two instructions a 16 x 16 tile where
+// the fp32 kernel takes sixteen); mask, online max and sum, sink and output
+// as in k_attn_flash. A lane's fragments: query row r16 of its wave's 16
+// (or slot r16 of a 16-slot group, or output column r16), k elements
+// 32 kk + 8 g4 .. + 7.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_flash_bf(AttnArgs a, const AttnTile* __restrict__ tab) {
+  constexpr int KT = 64;                 // slots per key tile
+  constexpr int NK = HD / 32;            // 32-dim k steps of S = q K^T
+  constexpr int NJ = HD / 16;            // 16-dim output tiles
+  constexpr int KP = HD + 8, VP = KT + 8, PP = KT + 8;   // bf16 row pitches (16-byte multiples)
+  static_assert(HD % 32 == 0, "hd a multiple of 32");
+  __shared__ __align__(16) __bf16 Ks[KT][KP];
+  __shared__ __align__(16) __bf16 Vt[HD][VP];
+  __shared__ __align__(16) __bf16 Ps[4][16][PP];
+  const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint32_t r16 = lane & 15, g = lane >> 4;
+  const AttnTile tt = tab[blockIdx.y];
+  const uint32_t d = a.d;
+  const float* Kr = a.KV.base + (size_t)tt.seq * a.KV.seq_stride + a.KV.layer_off;
+  const float* Vr = Kr + (size_t)a.ctx * d;
+  const uint32_t last = tt.pos0 + tt.n - 1;          // the tile's last position (< ctx)
+  bf16x8_t qf[NK];
+  {
+    const uint32_t qr = 16 * w + r16;
+    const float* x = a.QKV + (size_t)(tt.row0 + (qr < tt.n ? qr : 0)) * 3 * d + h * HD;
+    float qv[NK][8];
+#pragma unroll
+    for (int kk = 0; kk < NK; kk++) {
+      const float4 v0 = *reinterpret_cast<const float4*>(x + 32 * kk + 8 * g);
+      const float4 v1 = *reinterpret_cast<const float4*>(x + 32 * kk + 8 * g + 4);
+      qv[kk][0] = v0.x; qv[kk][1] = v0.y; qv[kk][2] = v0.z; qv[kk][3] = v0.w;
+      qv[kk][4] = v1.x; qv[kk][5] = v1.y; qv[kk][6] = v1.z; qv[kk][7] = v1.w;
+    }
+    const float s = 1.0f / sqrtf((float)HD);
+    if (a.gq) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int kk = 0; kk < NK; kk++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) ss = fmaf(qv[kk][e], qv[kk][e], ss);
+      ss += __shfl_xor(ss, 16, 64);
+      ss += __shfl_xor(ss, 32, 64);
+      const float rs = 1.0f / sqrtf(ss / (float)HD + 1.0e-5f);
+#pragma unroll
+      for (int kk = 0; kk < NK; kk++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) qv[kk][e] = (qv[kk][e] * rs) * (1.0f + a.gq[32 * kk + 8 * g + e]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < NK; kk++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) qf[kk][e] = (__bf16)(qv[kk][e] * s);
+  }
+  // rows of this lane in the result layout: 16 w + 4 g + r
+  float m[4], l[4];
+  f32x4_t o[NJ];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    m[r] = -INFINITY;
+    l[r] = 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; j++) o[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t nkt = last / KT + 1;
+  for (uint32_t kt = 0; kt < nkt; kt++) {
+    const uint32_t k0 = kt * KT;
+    __syncthreads();   // the previous tile's K, V and P reads are done
+    for (uint32_t e = tid; e < (uint32_t)KT * (HD / 4); e += 256) {
+      const uint32_t s = e / (HD / 4), c4 = e % (HD / 4);
+      const uint32_t slot = k0 + s <= last ? k0 + s : 0;
+      const float4 kv = *reinterpret_cast<const float4*>(Kr + (size_t)slot * d + h * HD + 4 * c4);
+      const float4 vv = *reinterpret_cast<const float4*>(Vr + (size_t)slot * d + h * HD + 4 * c4);
+      __bf16 kb[4] = {(__bf16)kv.x, (__bf16)kv.y, (__bf16)kv.z, (__bf16)kv.w};
+      *reinterpret_cast<uint2*>(&Ks[s][4 * c4]) = *reinterpret_cast<const uint2*>(kb);
+      Vt[4 * c4][s] = (__bf16)vv.x;
+      Vt[4 * c4 + 1][s] = (__bf16)vv.y;
+      Vt[4 * c4 + 2][s] = (__bf16)vv.z;
+      Vt[4 * c4 + 3][s] = (__bf16)vv.w;
+    }
+    __syncthreads();
+    // scores of the wave's 16 rows against the tile's 4 x 16 slots
+    f32x4_t sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      sc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kk = 0; kk < NK; kk++) {
+        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(&Ks[16 * j + r16][32 * kk + 8 * g]);
+        sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[kk], kf, sc[j], 0, 0, 0);
+      }
+    }
+    // causal mask, running max and sum per row (a row's slots lie across the
+    // 16 lanes of its group)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint32_t row = 16 * w + 4 * g + r;
+      const uint32_t qpos = tt.pos0 + (row < tt.n ? row : tt.n - 1);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t slot = k0 + 16 * j + r16;
+        if (slot > qpos) sc[j][r] = -INFINITY;
+        mx = fmaxf(mx, sc[j][r]);
+      }
+#pragma unroll
+      for (int s2 = 1; s2 < 16; s2 <<= 1) mx = fmaxf(mx, __shfl_xor(mx, s2, 64));
+      const float mn = fmaxf(m[r], mx);   // finite: slot k0 <= qpos always
+      const float al = __expf(m[r] - mn);
+      float sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float p = __expf(sc[j][r] - mn);
+        sum += p;
+        Ps[w][4 * g + r][16 * j + r16] = (__bf16)p;
+      }
+#pragma unroll
+      for (int s2 = 1; s2 < 16; s2 <<= 1) sum += __shfl_xor(sum, s2, 64);
+      l[r] = l[r] * al + sum;
+      m[r] = mn;
+#pragma unroll
+      for (int j = 0; j < NJ; j++) o[j][r] *= al;
+    }
+    __syncthreads();
+    // O += P V: row r16 of the wave's P, slots 32 kk + 8 g ..
+#pragma unroll
+    for (int kk = 0; kk < KT / 32; kk++) {
+      const bf16x8_t pf = *reinterpret_cast<const bf16x8_t*>(&Ps[w][r16][32 * kk + 8 * g]);
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const bf16x8_t vf = *reinterpret_cast<const bf16x8_t*>(&Vt[16 * j + r16][32 * kk + 8 * g]);
+        o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf, vf, o[j], 0, 0, 0);
+      }
+    }
+  }
+  // the sink, then the rows out
+  const float sink = a.sink ? a.sink[h] : -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const uint32_t row = 16 * w + 4 * g + r;
+    if (row >= tt.n) continue;
+    const float ms = fmaxf(m[r], sink);
+    const float e = __expf(m[r] - ms);
+    const float den = l[r] * e + (a.sink ? __expf(sink - ms) : 0.0f);
+    const float f = e / den;
+    float* out = a.O + (size_t)(tt.row0 + row) * d + h * HD;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) out[16 * j + r16] = o[j][r] * f;
+  }
+}
+
+hipError_t launch_attn_flash(const AttnArgs& a, const AttnTile* tab, uint32_t ntiles, bool bf, hipStream_t st) {
   const uint32_t hd = a.d / a.heads;
   if (ntiles == 0) return hipSuccess;
+  if (bf && hd == 64) {
+    hipLaunchKernelGGL(k_attn_flash_bf<64>, dim3(a.heads, ntiles), dim3(256), 0, st, a, tab);
+    return hipGetLastError();
+  }
+  if (bf && hd == 32) {
+    hipLaunchKernelGGL(k_attn_flash_bf<32>, dim3(a.heads, ntiles), dim3(256), 0, st, a, tab);
+    return hipGetLastError();
+  }
 #define L_(H) hipLaunchKernelGGL(k_attn_flash<H>, dim3(a.heads, ntiles), dim3(256), 0, st, a, tab)
   switch (hd) {
     case 64: L_(64); break;
