@@ -60,6 +60,18 @@ struct ana_ctx {
   __bf16* d_hh = nullptr;    // ANA_BF16 prefill: gate|up's outputs in bf16, down's input
   bool hh_bf = false;        // d_hh holds the last gate|up's outputs
   float* d_rsc = nullptr;                      // and its rows' norm scales
+  // ANA_BF16 prefill, the operands producers leave for the next product
+  // (k_split's work done in their epilogues): d_oh the mixes' outputs in
+  // bf16 (Wo's operand) when oh_ok; d_nxh a residual product's outputs times
+  // the next norm's gain in bf16, with d_ssp its rows' partial sums of
+  // squares (nx_n a row), for the product that reads nx_of with gain nx_g
+  __bf16* d_oh = nullptr;
+  bool oh_ok = false;
+  __bf16* d_nxh = nullptr;
+  float* d_ssp = nullptr;
+  const float* nx_of = nullptr;
+  const float* nx_g = nullptr;
+  uint32_t nx_n = 0;
   // fast modes: every layer product's weights packed for k_gemm_pk (fp32, or
   // bf16 in ANA_BF16; the norm gains folded in), found by the product's first
   // weight row; the entry keeps the segment shape and gains it was packed for
@@ -200,7 +212,7 @@ static void release(ana_ctx* c) {
   void* ps[] = {c->d_play, c->d_ll, c->d_ctl, c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
                 c->d_ss, c->d_pm, c->d_gtab, c->d_grun, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce, c->d_rcp,
-                c->d_sah, c->d_hh, c->d_rsc, c->PK, c->d_hpc, c->d_hpctl};
+                c->d_sah, c->d_hh, c->d_rsc, c->PK, c->d_hpc, c->d_hpctl, c->d_oh, c->d_nxh, c->d_ssp};
   for (void* p : ps)
     if (p) (void)hipFree(p);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
@@ -335,7 +347,10 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if (c->mode == ANA_BF16) {
     const uint64_t kmax = std::max(d, cf.f);
     if ((e = dalloc(&c->Wh, c->P)) != hipSuccess || (e = dalloc(&c->d_sah, (uint64_t)c->rows * kmax)) != hipSuccess ||
-        (e = dalloc(&c->d_hh, (uint64_t)c->rows * cf.f)) != hipSuccess || (e = dalloc(&c->d_rsc, c->rows)) != hipSuccess)
+        (e = dalloc(&c->d_hh, (uint64_t)c->rows * cf.f)) != hipSuccess || (e = dalloc(&c->d_rsc, c->rows)) != hipSuccess ||
+        (e = dalloc(&c->d_oh, (uint64_t)c->rows * d)) != hipSuccess ||
+        (e = dalloc(&c->d_nxh, (uint64_t)c->rows * d)) != hipSuccess ||
+        (e = dalloc(&c->d_ssp, (uint64_t)c->rows * (d / 64 + 1))) != hipSuccess)
       return bad(e);
   }
   if ((e = hipMemcpyAsync(c->W, ck.raw.data(), 4 * c->P, hipMemcpyHostToDevice, c->st)) != hipSuccess) return bad(e);
@@ -447,14 +462,23 @@ static bool reads_bf16(const ana_ctx* c, const GemvArgs& g) {
   return !(o >= c->fp32_lo && o < c->fp32_hi);
 }
 
-static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool chunk = false) {
+// next_gain: the norm gain of the product that reads this one's outputs
+// next (a prefill step's residual products), for a producer-side bf16 copy
+static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool chunk = false,
+                             const float* next_gain = nullptr) {
   const bool small = g0.B <= kSmallB;
+  // the operands producers left: each serves the one product it was made
+  // for, and goes stale when that product (or another) has run
+  const bool nx_here = c->nx_of && g0.X == c->nx_of && g0.ng == c->nx_g;
+  const bool oh_here = c->oh_ok && g0.X == c->O && !g0.ng;
+  c->nx_of = nullptr;
+  c->oh_ok = false;
   // (d_hh holds this gate|up's outputs only if the path below writes them)
   const bool hh_was = c->hh_bf;
   if (g0.mode == GM_SILU) c->hh_bf = false;
   // the hidden rows exist only in bf16 after a gate|up that wrote d_hh, so
   // down must take the path that reads them there
-  const bool hh_only = g0.X == c->HH && hh_was;
+  const bool hh_only = (g0.X == c->HH && hh_was) || oh_here;   // (or O, when the mix left it in bf16 only)
   const bool pk_ok = gemm_pk_fits(g0) || (kind == ANA_K_HEAD && head_pw_fits(g0));
   const ana_ctx::PkEnt* pe =
       fast_mode(c) && !small && g0.B < (chunk ? 128u : kPwMaxB) && pk_ok ? find_pk(c, g0) : nullptr;
@@ -483,8 +507,31 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
       // instead of splitting them again
       if (g.mode == GM_SILU && c->d_hh && gemm_wide_takes(g)) g.Yh = c->d_hh;
       if (g.X == c->HH && hh_was && !g.ng && g.K == c->cfg.f) g.Xh = c->d_hh;
+      if (nx_here && g.K == c->cfg.d) {
+        g.Xh = c->d_nxh;
+        g.sspi = c->d_ssp;
+        g.nspi = c->nx_n;
+      }
+      if (oh_here) {
+        if (g.K != c->cfg.d) return hipErrorInvalidValue;
+        g.Xh = c->d_oh;
+      }
+      // a residual product of one segment on k_gemm_dl's full tiles also
+      // leaves the next product's operand
+      const bool fold = next_gain && g.Xh != c->d_nxh && g.nseg == 1 && g.mode != GM_SILU && g.B % 128 == 0 &&
+                        g.seg[0].rows == c->cfg.d && g.seg[0].rows % 128 == 0 && !gemm_wide_takes(g);
+      if (fold) {
+        g.Yn = c->d_nxh;
+        g.gn = next_gain;
+        g.ssp = c->d_ssp;
+      }
       const hipError_t e = launch_gemm_dl(g, c->d_sah, c->d_rsc, c->rows, c->st, ps.start(), ps.stop());
       if (g.mode == GM_SILU) c->hh_bf = g.Yh != nullptr && e == hipSuccess;
+      if (fold && e == hipSuccess) {
+        c->nx_of = g.seg[0].Y;
+        c->nx_g = next_gain;
+        c->nx_n = g.seg[0].rows / 64;
+      }
       return e;
     }
     if (hh_only) return hipErrorInvalidValue;
@@ -655,6 +702,11 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
   const uint32_t d = cf.d, f = cf.f;
   const float* W = c->W;
   const bool chunk = segs != nullptr;
+  // ANA_BF16 prefill steps whose products run on the bf16 tiles: the mixes
+  // write Wo's operand in bf16 and the residual products the next norm's
+  c->nx_of = nullptr;
+  c->oh_ok = false;
+  const bool bf_ops = c->d_oh && chunk && B >= 128 && B <= c->rows && d % 64 == 0;
   // a fast mode's prefill step: the GLA scan's sub-chunk table and each row's
   // sequence and position, uploaded once for every layer
   uint32_t nsub = 0;
@@ -713,10 +765,12 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
     } else if (b.gla && fast_mode(c)) {
       // every chunk of the step at once: a workgroup per (head, chunk)
       // through its sub-chunks, or the closed-form chunked scan
-      if (gla_run)
-        HIPCHK(c, launch_gla_run(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), c->O, c->d_grun,
-                                 (uint32_t)c->h_grun.size(), c->rows, d, cf.heads, cf.rglru, c->st));
-      else
+      if (gla_run) {
+        HIPCHK(c, launch_gla_run(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), c->O,
+                                 bf_ops ? c->d_oh : nullptr, c->d_grun, (uint32_t)c->h_grun.size(), c->rows, d,
+                                 cf.heads, cf.rglru, c->st));
+        c->oh_ok = bf_ops;
+      } else
         HIPCHK(c, launch_gla_scan(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), c->O, c->gla,
                                   c->d_gtab, nsub, d, cf.heads, cf.rglru, c->st));
     } else if (b.gla) {
@@ -753,7 +807,9 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
         // row's attention over the splits up to the step's last position
         a.QKV = c->QKV; a.O = c->O; a.B = B; a.seq = c->d_rseq; a.pos = c->d_rpos; a.write_kv = 0;
         HIPCHK(c, launch_kv_write_fast(a, c->st));
+        a.Oh = bf_ops ? c->d_oh : nullptr;
         HIPCHK(c, launch_attn_flash(a, c->d_atab, (uint32_t)c->h_atab.size(), c->mode == ANA_BF16, c->st));
+        c->oh_ok = bf_ops;
       } else {
         for (const Seg& sg : *segs) {
           const bool fresh = (uint64_t)sg.pos0 + sg.T <= cf.ctx;
@@ -783,9 +839,9 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
       }
     }
     // M.tail: xa = x + Wo o; hh = silu(g) * u on norm(xa); x = xa + Wd hh
-    HIPCHK(c, gemv_timed(c, p[P_WO], ANA_K_GEMV, chunk));
+    HIPCHK(c, gemv_timed(c, p[P_WO], ANA_K_GEMV, chunk, bf_ops ? W + b.rf : nullptr));
     if (int r = norm_gemv(c, c->XA, W + b.rf, p[P_GU], ANA_K_GEMV, chunk)) return r;
-    HIPCHK(c, gemv_timed(c, p[P_WD], ANA_K_GEMV, chunk));
+    HIPCHK(c, gemv_timed(c, p[P_WD], ANA_K_GEMV, chunk, bf_ops && l + 1 < cf.layers ? W + c->blk[l + 1].ra : nullptr));
   }
   return ANA_OK;
 }

@@ -69,7 +69,16 @@ struct GemvArgs {
   const uint16_t* Wh1;       // (nullptr: read the fp32 rows)
   __bf16* Yh;                // ANA_BF16 prefill, SiLU: the outputs in bf16 only (seg0.Y not
                              // written), [B][seg0.rows]
-  const __bf16* Xh;          // ANA_BF16 prefill, no norm: X already in bf16, [B][K]
+  const __bf16* Xh;          // ANA_BF16 prefill: X already in bf16, [B][K] (with a norm: the
+                             // gain applied, the scales from sspi)
+  __bf16* Yn;                // ANA_BF16 prefill, k_gemm_dl on full tiles, one segment: the
+                             // outputs times gn in bf16 too, [B][seg0.rows] (the next
+                             // product's operand, k_split's work done here)
+  const float* gn;           // that next product's norm gain
+  float* ssp;                // the rows' partial sums of the outputs' squares, [B][nsp]: one
+                             // a (128-column tile, 64-column half), nsp = seg0.rows / 64
+  const float* sspi;         // with Xh and a norm: the producer's partials, nspi a row, the
+  uint32_t nspi;             // norm scale 1 / sqrt(their sum / K + 1e-5)
 };
 // The two row segments as plain values (a runtime index into GemvArgs.seg
 // would send every lookup through memory).
@@ -171,6 +180,7 @@ struct AttnArgs {
   const uint32_t* pos;  // per row position (device)
   uint32_t pos0;        // when pos is nullptr: row b is at pos0 + b
   float* O;             // [B][d]
+  __bf16* Oh;           // k_attn_flash(_bf): the outputs in bf16 only (nullptr: O)
   uint32_t d, heads, ctx, B, write_kv;
   float* ss;            // scratch [B][heads][ctx]: sc * score
   float* pm;            // scratch [B][heads][ctx / kAttnTS]: partial maxima
@@ -301,7 +311,8 @@ struct GlaRun {
 };
 constexpr uint32_t kGlaRunMaxT = 8 * kGlaSub;
 // (rows: the workspace rows QKV and Z hold)
-hipError_t launch_gla_run(const float* QKV, const float* Z, const float* lam, StateRef S, float* O,
+// (Oh: the outputs in bf16 only, for a bf16 Wo operand)
+hipError_t launch_gla_run(const float* QKV, const float* Z, const float* lam, StateRef S, float* O, __bf16* Oh,
                           const GlaRun* runs, uint32_t nrun, uint32_t rows, uint32_t d, uint32_t heads,
                           uint32_t rglru, hipStream_t st);
 size_t gla_scan_floats(uint32_t rows, uint32_t nsub, uint32_t nseg, uint32_t d, uint32_t heads);

@@ -177,7 +177,10 @@ __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArg
   ANA_VMCNT(0);
   __syncthreads();
   if (norm) {
-    for (uint32_t t = tid; t < (uint32_t)BM; t += NT) rsl[t] = rscg[m0 + (t < nb ? t : 0)];
+    for (uint32_t t = tid; t < (uint32_t)BM; t += NT) {
+      const uint32_t m = m0 + (t < nb ? t : 0);
+      rsl[t] = a.sspi ? norm_from_partials(a.sspi + (size_t)m * a.nspi, a.nspi, K) : rscg[m];
+    }
     __syncthreads();
   }
   auto rs = [&](int i, int r) { return norm ? rsl[wm * NI * 16 + 16 * i + 4 * g4 + r] : 1.0f; };

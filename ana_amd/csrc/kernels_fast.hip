@@ -987,9 +987,14 @@ __global__ __launch_bounds__(256) void k_attn_flash(AttnArgs a, const AttnTile* 
     const float e = __expf(m[r] - ms);
     const float den = l[r] * e + (a.sink ? __expf(sink - ms) : 0.0f);
     const float f = e / den;
-    float* out = a.O + (size_t)(tt.row0 + row) * d + h * HD;
+    const size_t ob = (size_t)(tt.row0 + row) * d + h * HD;
+    if (a.Oh) {
 #pragma unroll
-    for (int j = 0; j < NJ; j++) out[16 * j + r16] = o[j][r] * f;
+      for (int j = 0; j < NJ; j++) a.Oh[ob + 16 * j + r16] = (__bf16)(o[j][r] * f);
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; j++) a.O[ob + 16 * j + r16] = o[j][r] * f;
+    }
   }
 }
 
@@ -1141,9 +1146,14 @@ __global__ __launch_bounds__(256) void k_attn_flash_bf(AttnArgs a, const AttnTil
     const float e = __expf(m[r] - ms);
     const float den = l[r] * e + (a.sink ? __expf(sink - ms) : 0.0f);
     const float f = e / den;
-    float* out = a.O + (size_t)(tt.row0 + row) * d + h * HD;
+    const size_t ob = (size_t)(tt.row0 + row) * d + h * HD;
+    if (a.Oh) {
 #pragma unroll
-    for (int j = 0; j < NJ; j++) out[16 * j + r16] = o[j][r] * f;
+      for (int j = 0; j < NJ; j++) a.Oh[ob + 16 * j + r16] = (__bf16)(o[j][r] * f);
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; j++) a.O[ob + 16 * j + r16] = o[j][r] * f;
+    }
   }
 }
 
@@ -2200,8 +2210,8 @@ template <int HD>
 __global__ __launch_bounds__(256, 3) void k_gla_run(const float* __restrict__ QKV,
                                                      const float* __restrict__ Z,
                                                      const float* __restrict__ lam, float* __restrict__ O,
-                                                     StateRef S, const GlaRun* __restrict__ runs, uint32_t d,
-                                                     uint32_t rglru) {
+                                                     __bf16* __restrict__ Oh, StateRef S,
+                                                     const GlaRun* __restrict__ runs, uint32_t d, uint32_t rglru) {
   constexpr int L = kGlaSub, TPA = 256 / HD, TPT = L / TPA, CBS = HD / 16, R = 4 / CBS;
   static_assert(TPT >= 1 && TPA * TPT == L && CBS * R == 4, "whole tokens a thread, a column block a wave");
   __shared__ float qh[L][HD + 1], kh[L][HD + 1], cl[L][HD + 1], vv[L][HD + 1];
@@ -2285,7 +2295,11 @@ __global__ __launch_bounds__(256, 3) void k_gla_run(const float* __restrict__ QK
 #pragma unroll
       for (int x = 0; x < 4; x++) {
         const uint32_t t = 16 * th + 4 * g4 + x;
-        if (t < n) O[(size_t)(r.row + j0 + t) * d + h * HD + 16 * bw + r16] = acc[x];
+        if (t < n) {
+          const size_t o = (size_t)(r.row + j0 + t) * d + h * HD + 16 * bw + r16;
+          if (Oh) Oh[o] = (__bf16)acc[x];
+          else O[o] = acc[x];
+        }
       }
     }
     // S' = D S + Kd^T V on the wave's own tiles (the next sub-chunk writes
@@ -2307,15 +2321,15 @@ __global__ __launch_bounds__(256, 3) void k_gla_run(const float* __restrict__ QK
       for (int y = 0; y < 4; y++) Sg[(16 * ab + 4 * g4 + y) * HD + 16 * bw + r16] = Sr[ab][y];
 }
 
-hipError_t launch_gla_run(const float* QKV, const float* Z, const float* lam, StateRef S, float* O,
+hipError_t launch_gla_run(const float* QKV, const float* Z, const float* lam, StateRef S, float* O, __bf16* Oh,
                           const GlaRun* runs, uint32_t nrun, uint32_t rows, uint32_t d, uint32_t heads,
                           uint32_t rglru, hipStream_t st) {
   const uint32_t hd = d / heads;
   if (nrun == 0 || hd * heads != d || (uint64_t)rows * 3 * d >= (1ull << 32)) return hipErrorInvalidValue;
   switch (hd) {
-    case 64: hipLaunchKernelGGL(k_gla_run<64>, dim3(heads, nrun), dim3(256), 0, st, QKV, Z, lam, O, S, runs, d, rglru); break;
-    case 32: hipLaunchKernelGGL(k_gla_run<32>, dim3(heads, nrun), dim3(256), 0, st, QKV, Z, lam, O, S, runs, d, rglru); break;
-    case 16: hipLaunchKernelGGL(k_gla_run<16>, dim3(heads, nrun), dim3(256), 0, st, QKV, Z, lam, O, S, runs, d, rglru); break;
+    case 64: hipLaunchKernelGGL(k_gla_run<64>, dim3(heads, nrun), dim3(256), 0, st, QKV, Z, lam, O, Oh, S, runs, d, rglru); break;
+    case 32: hipLaunchKernelGGL(k_gla_run<32>, dim3(heads, nrun), dim3(256), 0, st, QKV, Z, lam, O, Oh, S, runs, d, rglru); break;
+    case 16: hipLaunchKernelGGL(k_gla_run<16>, dim3(heads, nrun), dim3(256), 0, st, QKV, Z, lam, O, Oh, S, runs, d, rglru); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -2808,7 +2822,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
   // any store (a global load after a store through another pointer would
   // wait on it, one round trip per element)
   if (norm) {
-    if (tid < (uint32_t)BM) rsl[tid] = rscg[m0 + (tid < nb ? tid : 0)];
+    if (tid < (uint32_t)BM) {
+      const uint32_t m = m0 + (tid < nb ? tid : 0);
+      rsl[tid] = a.sspi ? norm_from_partials(a.sspi + (size_t)m * a.nspi, a.nspi, K) : rscg[m];
+    }
     __syncthreads();
   }
   auto rs = [&](int i, int r) { return norm ? rsl[wm * 64 + 16 * i + 4 * g4 + r] : 1.0f; };
@@ -2850,17 +2867,43 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
 #pragma unroll
           for (int r = 0; r < 4; r++) res[j][i][r] = 0.0f;
     }
+    // with Yn (one segment): the outputs times the next norm's gain in bf16
+    // too, and each row's sum of squares over the wave's 64 columns (the
+    // 16 lanes of a row group by DPP, then one partial a row)
+    float ss[4][4], gn[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) ss[i][r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) gn[j] = a.Yn ? a.gn[col[j]] : 0.0f;   // (loaded before any store)
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       float* const Yb = s1[j] ? a.seg[1].Y : a.seg[0].Y;
       const uint32_t ld = s1[j] ? a.seg[1].ldy : a.seg[0].ldy;
       float* yb = Yb + mrow * ld + col[j];
+      const float gj = gn[j];
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          const float y = acc[i][j][r] * sc[i][r];
-          yb[(size_t)(16 * i + r) * ld] = a.mode == GM_RESID ? res[j][i][r] + y : y;
+          float y = acc[i][j][r] * sc[i][r];
+          if (a.mode == GM_RESID) y = res[j][i][r] + y;
+          yb[(size_t)(16 * i + r) * ld] = y;
+          if (a.Yn) {
+            a.Yn[(mrow + 16 * i + r) * a.seg[0].rows + col[j]] = (__bf16)(y * gj);
+            ss[i][r] = fmaf(y, y, ss[i][r]);
+          }
+        }
+    }
+    if (a.Yn) {
+      const uint32_t nsp = a.seg[0].rows / 64;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float t = row16_sum(ss[i][r]);
+          if (r16 == 0) a.ssp[(mrow + 16 * i + r) * nsp + 2 * ntile + wn] = t;
         }
     }
     return;
@@ -2943,7 +2986,11 @@ hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t ca
                           hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   if (a.amax || (a.K % 64) || a.B == 0 || !a.Wh0 || (a.nseg > 1 && !a.Wh1)) return hipErrorInvalidValue;
   if (a.B > cap_rows) return hipErrorInvalidValue;
-  if (a.Xh && a.ng) return hipErrorInvalidValue;   // (bf16 input takes no norm)
+  if (a.Xh && a.ng && !a.sspi) return hipErrorInvalidValue;   // (bf16 input with a norm: its partials)
+  // Yn: k_gemm_dl's full tiles only (its epilogue writes it), one segment
+  if (a.Yn && (a.nseg != 1 || a.mode == GM_SILU || a.B % 128 || a.seg[0].rows % 128 || !a.gn || !a.ssp ||
+               gemm_wide_takes(a)))
+    return hipErrorInvalidValue;
   // the split first (its time is inside the events), unless X came in bf16
   if (e0) (void)hipEventRecord(e0, st);
   if (a.Xh) Ah = const_cast<__bf16*>(a.Xh);

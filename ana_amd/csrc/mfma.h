@@ -20,6 +20,14 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ float fast_silu(float z) { return z / (1.0f + __expf(-z)); }
 
+// a row's RMSNorm scale from its producer's n partial sums of squares, in
+// order (K: the row's length)
+__device__ __forceinline__ float norm_from_partials(const float* p, uint32_t n, uint32_t K) {
+  float s = 0.0f;
+  for (uint32_t i = 0; i < n; i++) s += p[i];
+  return 1.0f / sqrtf(s / (float)K + 1.0e-5f);
+}
+
 // Workgroup -> (n tile, m tile) so that the workgroups one XCD runs (ids
 // equal mod 8) take consecutive tiles, n fastest: the A rows those n tiles
 // share stay in that XCD's L2.
