@@ -16,40 +16,41 @@ namespace ana {
 
 namespace {
 
-constexpr int kWideBK = 32;
+constexpr int kWideBK = 64;
 
 // A (WM * NI * 16) x (WN * NJ * 16) tile of WM x WN waves, each
 // (NI * 16) x (NJ * 16) (NI x NJ v_mfma_f32_16x16x32_bf16 tiles). K goes
-// through a ring of four 32-k stages (the A and weight tiles as 1 KB chunks
-// of 16 rows, a row's four 16-byte k pieces at slot piece ^ ((row >> 1) &
-// 3), so a fragment read touches eight distinct 16-byte bank groups),
-// filled by global_load_lds four stages ahead; each wave reads stage s + 1's
-// fragments from LDS into its second register set while its MFMAs run on
-// stage s's. Norm scale, residual and SiLU in the epilogue (SiLU: the
-// tile's first half of columns are gate rows, the second half the matching
-// up rows).
+// through two LDS stages of 64 k, each filled by global_load_lds one stage
+// ahead: the A and weight tiles as 1 KB chunks of 8 rows, each row's whole
+// 128-byte line, its eight 16-byte k pieces at slot piece ^ (row & 7), so
+// the 16 rows of a fragment read touch distinct 16-byte bank groups eight
+// at a time. (Loads of 16 rows x 64 bytes, half lines, for stages of 32 k
+// moved the same bytes at two thirds the rate: 652 against 434 ns a 32-k
+// step for a round of 256 tiles, no MFMAs.) Each wave reads one 32-k
+// half's fragments of a stage, then runs its MFMAs, then the other half;
+// the other wave of its SIMD computes meanwhile. Norm scale, residual and
+// SiLU in the
+// epilogue (SiLU: the tile's first half of columns are gate rows, the
+// second half the matching up rows).
 template <int WM, int WN, int NI, int NJ>
 __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArgs a, const __bf16* __restrict__ Ahg,
                                                                          const float* __restrict__ rscg) {
   constexpr int NW = WM * WN, NT = NW * 64;
   constexpr int BM = WM * NI * 16, BN = WN * NJ * 16, BK = kWideBK;
-  constexpr int ACH = BM / 16, WCH = BN / 16;     // 1 KB chunks a stage
+  constexpr int ACH = BM / 8, WCH = BN / 8;       // 1 KB chunks a stage
   // of them a wave fills: the A chunks split evenly; the weight chunks
   // round up, the spare slots loading chunks 0, 1, .. again (the same
-  // bytes to the same place), so every wave issues the same count and the
-  // compile-time waits hold for each
+  // bytes to the same place), so every wave issues the same count
   constexpr int AW = ACH / NW, BW = (WCH + NW - 1) / NW;
   static_assert(AW * NW == ACH, "A chunks split evenly over the waves");
   static_assert(BM == 256, "one norm scale a thread of the first 256");
   constexpr int SO = (ACH + WCH) * 512;           // bf16 elements of a stage object
-  static_assert(SO * 2 >= 64 * (BN / 2) * 4, "a stage object holds 64 rows of the SiLU exchange");
-  __shared__ __align__(1024) __bf16 st0[SO], st1[SO], st2[SO], st3[SO];
+  static_assert(SO >= 64 * (BN / 2) * 4, "half a stage object holds 64 rows of the SiLU exchange");
+  __shared__ __align__(1024) __bf16 st0[SO], st1[SO];
   __shared__ float rsl[BM];
   auto stage = [&](auto B) -> __bf16* {
     if constexpr (decltype(B)::value == 0) return st0;
-    else if constexpr (decltype(B)::value == 1) return st1;
-    else if constexpr (decltype(B)::value == 2) return st2;
-    else return st3;
+    else return st1;
   };
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint32_t wm = wv / WN, wn = wv % WN;
@@ -60,24 +61,24 @@ __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArg
   const uint32_t K = a.K, nst = K / BK;
   const Segs sgs(a);
   // wave wv fills A chunks AW wv .. and weight chunks BW wv .. of each
-  // stage (chunk c: tile rows 16 c .. 16 c + 15), this lane's 16-byte piece
-  // of each
-  // (as 32-bit byte offsets from a uniform base, so each load is the
-  // base in SGPRs plus one VGPR: the weights' base is the lower of the two
-  // segments', which lie in one buffer)
-  const uint32_t pr = lane >> 2, pq = (lane & 3) ^ ((pr >> 1) & 3);
+  // stage (chunk c: tile rows 8 c .. 8 c + 7), this lane's 16-byte piece of
+  // each: row lane / 8 of the chunk, slot lane % 8 holding k piece
+  // (lane % 8) ^ row (as 32-bit byte offsets from a uniform base, so each
+  // load is the base in SGPRs plus one VGPR: the weights' base is the lower
+  // of the two segments', which lie in one buffer)
+  const uint32_t pr = lane >> 3, pq = (lane & 7) ^ pr;
   const char* const abase = reinterpret_cast<const char*>(Ahg);
   const uint16_t* const wlo = a.nseg > 1 && a.Wh1 < a.Wh0 ? a.Wh1 : a.Wh0;
   const char* const wbase = reinterpret_cast<const char*>(wlo);
   uint32_t aoff[AW], boff[BW];
 #pragma unroll
   for (int h = 0; h < AW; h++) {
-    const uint32_t r = 16 * (AW * wv + h) + pr;
+    const uint32_t r = 8 * (AW * wv + h) + pr;
     aoff[h] = 2 * ((m0 + (r < nb ? r : 0)) * K + 8 * pq);
   }
 #pragma unroll
   for (int h = 0; h < BW; h++) {
-    const uint32_t r = 16 * ((BW * wv + h) % WCH) + pr;
+    const uint32_t r = 8 * ((BW * wv + h) % WCH) + pr;
     const float* w;
     uint32_t sg, lr;
     const bool ok = sgs.row(BN, ntile, r, &w, &sg, &lr);
@@ -100,16 +101,19 @@ __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArg
 #pragma unroll
     for (int j = 0; j < NJ; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   const uint32_t r16 = lane & 15, g4 = lane >> 4;
-  const uint32_t foff = r16 * 32 + 8 * (g4 ^ ((r16 >> 1) & 3));
-  bf16x8_t fa0[NI], fb0[NJ], fa1[NI], fb1[NJ];
-  auto lread = [&](auto B, bf16x8_t* fa, bf16x8_t* fb) {
+  // a 16-row MFMA tile is two chunks; this lane's row r16 and 32-k half kh
+  // (k piece 4 kh + g4)
+  const uint32_t fbase = (r16 >> 3) * 512 + (r16 & 7) * 64;
+  const uint32_t foff0 = fbase + 8 * (g4 ^ (r16 & 7)), foff1 = fbase + 8 * ((4 + g4) ^ (r16 & 7));
+  bf16x8_t fa[NI], fb[NJ];
+  auto lread = [&](auto B, uint32_t foff) {
     const __bf16* S = stage(B);
 #pragma unroll
-    for (int i = 0; i < NI; i++) fa[i] = *reinterpret_cast<const bf16x8_t*>(S + (wm * NI + i) * 512 + foff);
+    for (int i = 0; i < NI; i++) fa[i] = *reinterpret_cast<const bf16x8_t*>(S + (wm * NI + i) * 1024 + foff);
 #pragma unroll
-    for (int j = 0; j < NJ; j++) fb[j] = *reinterpret_cast<const bf16x8_t*>(S + (ACH + wn * NJ + j) * 512 + foff);
+    for (int j = 0; j < NJ; j++) fb[j] = *reinterpret_cast<const bf16x8_t*>(S + ACH * 512 + (wn * NJ + j) * 1024 + foff);
   };
-  auto mma = [&](const bf16x8_t* fa, const bf16x8_t* fb) {
+  auto mma = [&]() {
 #pragma unroll
     for (int i = 0; i < NI; i++)
 #pragma unroll
@@ -117,59 +121,37 @@ __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArg
   };
   // the waits and the barrier, with nothing moved across them: a memory
   // clobber so no LDS access crosses (the barrier builtin alone orders no
-  // memory), and scheduling barriers so no MFMA does (the scheduler would
-  // otherwise pull the next step's MFMAs up to the fragments they read and
-  // wait on those reads there)
-  auto step_barrier = [&](auto W) {
+  // memory), and scheduling barriers so no MFMA does
+  auto step_barrier = [&]() {
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
     ANA_LGKMCNT0();
-    ANA_VMCNT(decltype(W)::value);
+    ANA_VMCNT(0);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   };
-  // step s (object B, its fragments already in register set P): this
-  // wave's reads of them are done, and its loads of stage s + 1 (W younger
-  // loads may still be in flight); the barrier makes every wave's loads of
-  // s + 1 visible and says every wave is done reading object B, which stage
-  // s + 4 then fills; then s + 1's fragments into set Q, issued before s's
-  // MFMAs, which do not wait on them. Every wait is unconditional and K is
-  // a multiple of 128 (stages in fours, the last four peeled), so the
-  // compiler adds no wait of its own.
-  auto step = [&](uint32_t s, auto B, auto Bn, auto W, bool more, bf16x8_t* pa, bf16x8_t* pb, bf16x8_t* qa,
-                  bf16x8_t* qb) {
-    step_barrier(W);
-    if (more) issue(s + 4, B);
-    lread(Bn, qa, qb);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(pa, pb);
+  // stage s (object B): this wave's loads of it (the only ones in flight)
+  // and its fragment reads of the other object are done; the barrier makes
+  // every wave's loads of s visible and says every wave is done reading the
+  // other object, which stage s + 1 then fills; then each 32-k half's
+  // fragments and MFMAs (the SIMD's other wave computes while this one
+  // waits on its reads)
+  auto step = [&](uint32_t s, auto B, auto Bn) {
+    step_barrier();
+    if (s + 1 < nst) issue(s + 1, Bn);
+    lread(B, foff0);
+    mma();
+    lread(B, foff1);
+    mma();
   };
   constexpr std::integral_constant<int, 0> S0{};
   constexpr std::integral_constant<int, 1> S1{};
-  constexpr std::integral_constant<int, 2> S2{};
-  constexpr std::integral_constant<int, 3> S3{};
-  constexpr std::integral_constant<int, 3 * (AW + BW)> W3{};
-  constexpr std::integral_constant<int, 2 * (AW + BW)> W2{};   // two stages' loads
-  constexpr std::integral_constant<int, AW + BW> W1{};
-  constexpr std::integral_constant<int, 0> W0{};
   issue(0, S0);
-  issue(1, S1);
-  issue(2, S2);
-  issue(3, S3);
-  step_barrier(W3);
-  lread(S0, fa0, fb0);
-  uint32_t s = 0;
-  for (; s + 4 < nst; s += 4) {
-    step(s, S0, S1, W2, true, fa0, fb0, fa1, fb1);
-    step(s + 1, S1, S2, W2, true, fa1, fb1, fa0, fb0);
-    step(s + 2, S2, S3, W2, true, fa0, fb0, fa1, fb1);
-    step(s + 3, S3, S0, W2, true, fa1, fb1, fa0, fb0);
+  for (uint32_t s = 0; s < nst; s += 2) {
+    step(s, S0, S1);
+    step(s + 1, S1, S0);
   }
-  step(s, S0, S1, W2, false, fa0, fb0, fa1, fb1);
-  step(s + 1, S1, S2, W1, false, fa1, fb1, fa0, fb0);
-  step(s + 2, S2, S3, W0, false, fa0, fb0, fa1, fb1);
-  mma(fa1, fb1);
   const bool norm = a.ng != nullptr;
   // results: tile (i, j) of the wave holds rows wm*NI*16 + 16i + 4*g4 + r,
   // column wn*NJ*16 + 16j + r16; the row norm scales go to LDS first (every
@@ -208,9 +190,10 @@ __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArg
     const size_t mrow = m0 + wm * NI * 16 + 4 * g4;   // this lane's first row
     if (a.mode == GM_SILU) {
       constexpr int HB = BN / 2;
+      // tile rows 64 q .. 64 q + 63 in half q & 1 of stage object q >> 1
       auto upat = [&](uint32_t m) -> float* {
         const uint32_t q = m >> 6;
-        return reinterpret_cast<float*>(q == 0 ? st0 : q == 1 ? st1 : q == 2 ? st2 : st3) + (m & 63) * HB;
+        return reinterpret_cast<float*>((q >> 1 ? st1 : st0) + (q & 1) * (SO / 2)) + (m & 63) * HB;
       };
       if (wn >= (uint32_t)(WN / 2)) {
 #pragma unroll
@@ -277,7 +260,7 @@ __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArg
     constexpr int HB = BN / 2;
     auto upat = [&](uint32_t m) -> float* {
       const uint32_t q = m >> 6;
-      return reinterpret_cast<float*>(q == 0 ? st0 : q == 1 ? st1 : q == 2 ? st2 : st3) + (m & 63) * HB;
+      return reinterpret_cast<float*>((q >> 1 ? st1 : st0) + (q & 1) * (SO / 2)) + (m & 63) * HB;
     };
     if (wn >= (uint32_t)(WN / 2)) {
 #pragma unroll
