@@ -2711,31 +2711,30 @@ __global__ __launch_bounds__(256) void k_split(const float* __restrict__ X, uint
 // Y[m][n] = sum_k A[m][k] W[n][k] for ANA_BF16 prefill steps of >= 128 rows,
 // A given as bf16 (k_split): a 128 x 128 tile per workgroup, four waves of
 // 64 x 64 (4 x 4 v_mfma_f32_16x16x32_bf16 tiles). K goes in stages of 64
-// (a whole 128-byte line of each row; stages of 32 took 6% longer, one
-// barrier per half the work) through a ring of NS LDS stages filled by
-// global_load_lds_dwordx4 (no registers between global memory and LDS):
-// each stage holds the A and weight tiles, each k half as 1 KB chunks of
-// 16 rows, a row's four 16-byte k pieces at
-// physical slot (piece ^ ((row >> 1) & 3)), so a fragment read touches
-// eight distinct 16-byte bank groups. A wave waits on its own loads of the
-// stage it is about to read, then a barrier (no fence, which would wait on
-// every load in flight) makes the other waves' loads visible; loads of the
-// stage NS - 1 ahead go out right after it (the barrier also says every wave
-// is done with the stage they overwrite). Norm scale, residual and SiLU as in
-// k_gemm_big.
+// through a ring of NS LDS stages filled by global_load_lds_dwordx4 (no
+// registers between global memory and LDS): each stage holds the A and
+// weight tiles as 1 KB chunks of 8 rows, each row's whole 128-byte line, its
+// eight 16-byte k pieces at slot piece ^ (row & 7), so a fragment read
+// touches eight distinct 16-byte bank groups at a time (loads of half
+// lines, 16 rows x 64 bytes, moved the same bytes at two thirds the rate).
+// A wave waits on its own loads of the stage it is about to read, then a
+// barrier (no fence, which would wait on every load in flight) makes the
+// other waves' loads visible; loads of the next stage go out right after
+// it (the barrier also says every wave is done with the stage they
+// overwrite). Norm scale, residual and SiLU as in k_gemm_big.
 template <int NS>
 __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __restrict__ Ahg,
                                                   const float* __restrict__ rscg) {
   constexpr int BM = 128, BN = 128, BK = 64;
-  constexpr int TILE = BM * 32;   // bf16 elements of one operand tile half (8 KB)
+  constexpr int OPE = BM * BK;   // bf16 elements of one operand's stage (16 KB, 16 chunks)
   static_assert(NS == 2, "two stage objects");
   // one LDS object per stage: a stage's fragment reads then provably miss
   // the loads in flight into the other, and the compiler does not wait for
   // them (one array indexed by stage made it drain every load before each
   // stage's reads, and the loads never overlapped the MFMAs)
-  __shared__ __align__(1024) __bf16 st0[2][2][TILE], st1[2][2][TILE];
+  __shared__ __align__(1024) __bf16 st0[2][OPE], st1[2][OPE];
   __shared__ float rsl[BM];
-  auto stage = [&](auto B) -> __bf16(*)[2][TILE] {
+  auto stage = [&](auto B) -> __bf16(*)[OPE] {
     if constexpr (decltype(B)::value == 0) return st0;
     else return st1;
   };
@@ -2747,14 +2746,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
   const uint32_t nb = min((uint32_t)BM, a.B - m0);
   const uint32_t K = a.K, nst = K / BK;
   const Segs sgs(a);
-  // this lane's piece in each of the wave's two 1 KB chunks per operand:
-  // chunk c = 2 wv + h covers tile rows 16 c .. 16 c + 15
-  const uint32_t pr = lane >> 2, pq = (lane & 3) ^ ((pr >> 1) & 3);
-  uint32_t aoff[2];
-  const uint16_t* bptr[2];
+  // this lane's piece of the wave's four 1 KB chunks per operand (chunk
+  // c = 4 wv + h: tile rows 8 c .. 8 c + 7): row lane / 8 of the chunk,
+  // slot lane % 8 holding k piece (lane % 8) ^ row
+  const uint32_t pr = lane >> 3, pq = (lane & 7) ^ pr;
+  uint32_t aoff[4];
+  const uint16_t* bptr[4];
 #pragma unroll
-  for (int h = 0; h < 2; h++) {
-    const uint32_t r = 16 * (2 * wv + h) + pr;
+  for (int h = 0; h < 4; h++) {
+    const uint32_t r = 8 * (4 * wv + h) + pr;
     aoff[h] = (m0 + (r < nb ? r : 0)) * K + 8 * pq;
     const float* w;
     uint32_t sg, lr;
@@ -2764,13 +2764,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
   auto issue = [&](uint32_t s, auto B) {
     const uint32_t k0 = s * BK;
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const uint32_t c = 2 * wv + h;
-#pragma unroll
-      for (int kh = 0; kh < 2; kh++) {
-        __builtin_amdgcn_global_load_lds((const void*)(Ahg + aoff[h] + k0 + 32 * kh), (lds_void*)&stage(B)[0][kh][c * 512], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(bptr[h] + k0 + 32 * kh), (lds_void*)&stage(B)[1][kh][c * 512], 16, 0, 0);
-      }
+    for (int h = 0; h < 4; h++) {
+      const uint32_t c = 4 * wv + h;
+      __builtin_amdgcn_global_load_lds((const void*)(Ahg + aoff[h] + k0), (lds_void*)&stage(B)[0][c * 512], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(bptr[h] + k0), (lds_void*)&stage(B)[1][c * 512], 16, 0, 0);
     }
   };
   f32x4_t acc[4][4];
@@ -2779,24 +2776,34 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   const uint32_t r16 = lane & 15, g4 = lane >> 4;
-  // fragment read offset (elements) inside a 16-row chunk
-  const uint32_t foff = r16 * 32 + 8 * (g4 ^ ((r16 >> 1) & 3));
+  // fragment read offsets (elements) in a 16-row MFMA tile (two chunks):
+  // row r16, k piece 4 kh + g4
+  const uint32_t fbase = (r16 >> 3) * 512 + (r16 & 7) * 64;
+  const uint32_t foff[2] = {fbase + 8 * (g4 ^ (r16 & 7)), fbase + 8 * ((4 + g4) ^ (r16 & 7))};
   auto compute = [&](auto B) {
 #pragma unroll
     for (int kh = 0; kh < 2; kh++) {
-      const __bf16* A0 = &stage(B)[0][kh][0];
-      const __bf16* B0 = &stage(B)[1][kh][0];
+      const __bf16* A0 = &stage(B)[0][0];
+      const __bf16* B0 = &stage(B)[1][0];
       bf16x8_t bfr[4], ah[4];
 #pragma unroll
-      for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(B0 + (wn * 4 + j) * 512 + foff);
+      for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(B0 + (wn * 4 + j) * 1024 + foff[kh]);
 #pragma unroll
-      for (int i = 0; i < 4; i++) ah[i] = *reinterpret_cast<const bf16x8_t*>(A0 + (wm * 4 + i) * 512 + foff);
+      for (int i = 0; i < 4; i++) ah[i] = *reinterpret_cast<const bf16x8_t*>(A0 + (wm * 4 + i) * 1024 + foff[kh]);
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bfr[j], acc[i][j], 0, 0, 0);
     }
+  };
+  // the wait and the barrier, with no LDS access moved across them (the
+  // barrier builtin alone orders no memory)
+  auto step_barrier = [&]() {
+    asm volatile("" ::: "memory");
+    ANA_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   };
   constexpr std::integral_constant<int, 0> S0{};
   constexpr std::integral_constant<int, 1> S1{};
@@ -2805,13 +2812,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
   // then every wave's (the barrier, which also says every wave is done with
   // the other stage object); the next stage's loads go out, then s's MFMAs
   for (uint32_t s = 0; s < nst; s += 2) {
-    ANA_VMCNT(0);
-    __builtin_amdgcn_s_barrier();
+    step_barrier();
     if (s + 1 < nst) issue(s + 1, S1);
     compute(S0);
     if (s + 1 < nst) {
-      ANA_VMCNT(0);
-      __builtin_amdgcn_s_barrier();
+      step_barrier();
       if (s + 2 < nst) issue(s + 2, S0);
       compute(S1);
     }
@@ -2913,7 +2918,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
     // 64-row half at a time
     ANA_VMCNT(0);
     __syncthreads();
-    float* up = reinterpret_cast<float*>(&st0[0][0][0]);
+    float* up = reinterpret_cast<float*>(&st0[0][0]);
     static_assert(sizeof(st0) >= 64 * 64 * sizeof(float), "exchange buffer");
     for (uint32_t half = 0; half < 2; half++) {
       if (wn == 1 && wm == half) {
