@@ -2807,6 +2807,38 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
   };
   constexpr std::integral_constant<int, 0> S0{};
   constexpr std::integral_constant<int, 1> S1{};
+  // full tiles (every row and column valid) of plain and residual products
+  // take the epilogue without checks; their residuals are loaded here,
+  // before the k loop, so those loads overlap the MFMAs instead of waiting
+  // in the epilogue with every other workgroup's
+  const uint32_t wrows = a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
+  const bool full = a.mode != GM_SILU && nb == (uint32_t)BM && (ntile + 1) * BN <= wrows;
+  uint32_t col[4];
+  bool s1[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t v = ntile * BN + wn * 64 + 16 * j + r16;
+    s1[j] = v >= a.seg[0].rows;
+    col[j] = s1[j] ? v - a.seg[0].rows : v;
+  }
+  const size_t mrow = m0 + wm * 64 + 4 * g4;   // this lane's first row
+  float res[4][4][4];
+  if (full && a.mode == GM_RESID) {
+    const float* rb = a.R + mrow * a.ldr;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) res[j][i][r] = rb[(size_t)(16 * i + r) * a.ldr + col[j]];
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) res[j][i][r] = 0.0f;
+  }
   issue(0, S0);
   // stage s: this wave's loads of it are done (the only ones in flight),
   // then every wave's (the barrier, which also says every wave is done with
@@ -2834,44 +2866,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
     __syncthreads();
   }
   auto rs = [&](int i, int r) { return norm ? rsl[wm * 64 + 16 * i + 4 * g4 + r] : 1.0f; };
-  // full tiles (every row and column valid) of plain and residual products
-  // store without a check among the stores, the residuals all loaded first:
-  // with per-element checks and each column block's residual loads after
-  // the previous block's stores, the compiler drained the stores
-  // (vmcnt(0)) before every block
-  const uint32_t wrows = a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
-  if (a.mode != GM_SILU && nb == (uint32_t)BM && (ntile + 1) * BN <= wrows) {
+  // full tiles store without a check among the stores (the residuals came
+  // in before the k loop): with per-element checks and each column block's
+  // residual loads after the previous block's stores, the compiler drained
+  // the stores (vmcnt(0)) before every block
+  if (full) {
     float sc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int r = 0; r < 4; r++) sc[i][r] = norm ? rsl[wm * 64 + 16 * i + 4 * g4 + r] : 1.0f;
-    const size_t mrow = m0 + wm * 64 + 4 * g4;   // this lane's first row
-    uint32_t col[4];
-    bool s1[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const uint32_t v = ntile * BN + wn * 64 + 16 * j + r16;
-      s1[j] = v >= a.seg[0].rows;
-      col[j] = s1[j] ? v - a.seg[0].rows : v;
-    }
-    float res[4][4][4];
-    if (a.mode == GM_RESID) {
-      const float* rb = a.R + mrow * a.ldr;
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-          for (int r = 0; r < 4; r++) res[j][i][r] = rb[(size_t)(16 * i + r) * a.ldr + col[j]];
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-          for (int r = 0; r < 4; r++) res[j][i][r] = 0.0f;
-    }
     // with Yn (one segment): the outputs times the next norm's gain in bf16
     // too, and each row's sum of squares over the wave's 64 columns (the
     // 16 lanes of a row group by DPP, then one partial a row)
