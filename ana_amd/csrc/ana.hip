@@ -716,6 +716,8 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
     c->h_gtab.clear();
     c->h_grun.clear();
     c->h_atab.clear();
+    // attention tile rows: 128 on the bf16 flash kernel, else 64
+    const uint32_t fq = attn_flash_tile_rows(c->mode == ANA_BF16, d / cf.heads);
     c->h_rseq.resize(B);
     c->h_rpos.resize(B);
     for (uint32_t si = 0; si < segs->size(); si++) {
@@ -729,8 +731,8 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
         c->h_rseq[sg.row0 + t] = sg.seq;
         c->h_rpos[sg.row0 + t] = sg.pos0 + t;
       }
-      for (uint32_t t = 0; t < sg.T; t += kFlashQ)
-        c->h_atab.push_back(AttnTile{sg.seq, sg.pos0 + t, sg.row0 + t, std::min(kFlashQ, sg.T - t)});
+      for (uint32_t t = 0; t < sg.T; t += fq)
+        c->h_atab.push_back(AttnTile{sg.seq, sg.pos0 + t, sg.row0 + t, std::min(fq, sg.T - t)});
       const uint64_t last = (uint64_t)sg.pos0 + sg.T - 1;
       if (last >= cf.ctx) fresh_all = false;
     }

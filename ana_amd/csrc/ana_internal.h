@@ -375,12 +375,14 @@ size_t attn_fast_part_floats(uint32_t B, uint32_t heads, uint32_t ctx, uint32_t 
 // causal attention of fresh prefill rows on the matrix cores: one workgroup
 // per (head, tile of up to kFlashQ rows of one sequence), the rows' k and v
 // already in the ring
-constexpr uint32_t kFlashQ = 64;
+constexpr uint32_t kFlashQ = 64, kFlashQBf = 128;
 struct AttnTile {
   uint32_t seq, pos0, row0, n;  // sequence, first row's position and workspace row, rows
 };
 // bf: the products on the bf16 matrix cores (ANA_BF16; hd 32 or 64, else
-// the fp32 ones)
+// the fp32 ones); the tiles hold up to attn_flash_tile_rows(bf, hd) rows
+// (kFlashQBf on the bf16 kernel, else kFlashQ)
+uint32_t attn_flash_tile_rows(bool bf, uint32_t hd);
 hipError_t launch_attn_flash(const AttnArgs& a, const AttnTile* tab, uint32_t ntiles, bool bf, hipStream_t st);
 hipError_t launch_zero_u32(uint32_t* p, uint32_t n, hipStream_t st);
 hipError_t launch_zero_u64(unsigned long long* p, uint32_t n, hipStream_t st);

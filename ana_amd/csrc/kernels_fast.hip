@@ -1003,11 +1003,14 @@ __global__ __launch_bounds__(256) void k_attn_flash(AttnArgs a, const AttnTile* 
 // the probabilities rounded to bf16, S = q K^T and O += P V accumulated in
 // fp32 on v_mfma_f32_16x16x32_bf16 (two instructions a 16 x 16 tile where
 // the fp32 kernel takes sixteen); mask, online max and sum, sink and output
-// as in k_attn_flash. A lane's fragments: query row r16 of its wave's 16
+// as in k_attn_flash. Eight waves take a tile of up to kFlashQBf = 128
+// query rows, so each staged K and V tile serves twice the rows of the
+// fp32 kernel's 64 (each workgroup of a sequence restages every tile up to
+// its last position). A lane's fragments: query row r16 of its wave's 16
 // (or slot r16 of a 16-slot group, or output column r16), k elements
 // 32 kk + 8 g4 .. + 7.
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_flash_bf(AttnArgs a, const AttnTile* __restrict__ tab) {
+__global__ __launch_bounds__(512) void k_attn_flash_bf(AttnArgs a, const AttnTile* __restrict__ tab) {
   constexpr int KT = 64;                 // slots per key tile
   constexpr int NK = HD / 32;            // 32-dim k steps of S = q K^T
   constexpr int NJ = HD / 16;            // 16-dim output tiles
@@ -1015,7 +1018,7 @@ __global__ __launch_bounds__(256) void k_attn_flash_bf(AttnArgs a, const AttnTil
   static_assert(HD % 32 == 0, "hd a multiple of 32");
   __shared__ __align__(16) __bf16 Ks[KT][KP];
   __shared__ __align__(16) __bf16 Vt[HD][VP];
-  __shared__ __align__(16) __bf16 Ps[4][16][PP];
+  __shared__ __align__(16) __bf16 Ps[8][16][PP];
   const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const uint32_t r16 = lane & 15, g = lane >> 4;
   const AttnTile tt = tab[blockIdx.y];
@@ -1069,7 +1072,7 @@ __global__ __launch_bounds__(256) void k_attn_flash_bf(AttnArgs a, const AttnTil
   for (uint32_t kt = 0; kt < nkt; kt++) {
     const uint32_t k0 = kt * KT;
     __syncthreads();   // the previous tile's K, V and P reads are done
-    for (uint32_t e = tid; e < (uint32_t)KT * (HD / 4); e += 256) {
+    for (uint32_t e = tid; e < (uint32_t)KT * (HD / 4); e += 512) {
       const uint32_t s = e / (HD / 4), c4 = e % (HD / 4);
       const uint32_t slot = k0 + s <= last ? k0 + s : 0;
       const float4 kv = *reinterpret_cast<const float4*>(Kr + (size_t)slot * d + h * HD + 4 * c4);
@@ -1157,15 +1160,14 @@ __global__ __launch_bounds__(256) void k_attn_flash_bf(AttnArgs a, const AttnTil
   }
 }
 
+uint32_t attn_flash_tile_rows(bool bf, uint32_t hd) { return bf && (hd == 64 || hd == 32) ? kFlashQBf : kFlashQ; }
+
 hipError_t launch_attn_flash(const AttnArgs& a, const AttnTile* tab, uint32_t ntiles, bool bf, hipStream_t st) {
   const uint32_t hd = a.d / a.heads;
   if (ntiles == 0) return hipSuccess;
-  if (bf && hd == 64) {
-    hipLaunchKernelGGL(k_attn_flash_bf<64>, dim3(a.heads, ntiles), dim3(256), 0, st, a, tab);
-    return hipGetLastError();
-  }
-  if (bf && hd == 32) {
-    hipLaunchKernelGGL(k_attn_flash_bf<32>, dim3(a.heads, ntiles), dim3(256), 0, st, a, tab);
+  if (attn_flash_tile_rows(bf, hd) == kFlashQBf) {
+    if (hd == 64) hipLaunchKernelGGL(k_attn_flash_bf<64>, dim3(a.heads, ntiles), dim3(512), 0, st, a, tab);
+    else hipLaunchKernelGGL(k_attn_flash_bf<32>, dim3(a.heads, ntiles), dim3(512), 0, st, a, tab);
     return hipGetLastError();
   }
 #define L_(H) hipLaunchKernelGGL(k_attn_flash<H>, dim3(a.heads, ntiles), dim3(256), 0, st, a, tab)
