@@ -30,9 +30,10 @@ constexpr int kWideBK = 64;
 // half's fragments of a stage, then runs its MFMAs, then the other half;
 // the other wave of its SIMD computes meanwhile. Norm scale, residual and
 // SiLU in the
-// epilogue (SiLU: the tile's first half of columns are gate rows, the
-// second half the matching up rows).
-template <int WM, int WN, int NI, int NJ>
+// epilogue (SiLU, a compile-time choice so the other products' code and
+// its schedule do not carry it: the tile's first half of columns are gate
+// rows, the second half the matching up rows).
+template <int WM, int WN, int NI, int NJ, bool SILU>
 __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArgs a, const __bf16* __restrict__ Ahg,
                                                                          const float* __restrict__ rscg) {
   constexpr int NW = WM * WN, NT = NW * 64;
@@ -171,8 +172,8 @@ __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArg
   // with per-element bounds checks, per-element scale lookups and loads
   // between the stores, the compiler drained the stores (vmcnt(0)) again
   // and again, and the epilogue took longer than the k loop
-  const uint32_t wrows = a.mode == GM_SILU ? a.seg[0].rows : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
-  const uint32_t wper = a.mode == GM_SILU ? BN / 2 : BN;
+  const uint32_t wrows = SILU ? a.seg[0].rows : a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
+  const uint32_t wper = SILU ? BN / 2 : BN;
   const bool full = nb == (uint32_t)BM && (ntile + 1) * wper <= wrows && a.mode != GM_RESID;
   if (full) {
     float sc[NI][4];
@@ -188,54 +189,64 @@ __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArg
         for (int r = 0; r < 4; r++) sc[i][r] = 1.0f;
     }
     const size_t mrow = m0 + wm * NI * 16 + 4 * g4;   // this lane's first row
-    if (a.mode == GM_SILU) {
+    if constexpr (SILU) {
       constexpr int HB = BN / 2;
       // tile rows 64 q .. 64 q + 63 in half q & 1 of stage object q >> 1
       auto upat = [&](uint32_t m) -> float* {
         const uint32_t q = m >> 6;
         return reinterpret_cast<float*>((q >> 1 ? st1 : st0) + (q & 1) * (SO / 2)) + (m & 63) * HB;
       };
-      if (wn >= (uint32_t)(WN / 2)) {
+      // each gate wave and its up wave (same rows, matching columns) swap
+      // half their rows: the gate wave hands over its gate values of rows
+      // i >= NI / 2, the up wave its up values of rows i < NI / 2; then each
+      // forms silu(gate) * up and stores for its own half of the rows
+      const bool gate = wn < (uint32_t)(WN / 2);
+      const uint32_t cw = (gate ? wn : wn - WN / 2) * NJ * 16 + r16;   // column in the half
 #pragma unroll
-        for (int i = 0; i < NI; i++)
+      for (int i = 0; i < NI; i++) {
+        if ((i >= NI / 2) != gate) continue;
 #pragma unroll
-          for (int r = 0; r < 4; r++) {
-            float* up = upat(wm * NI * 16 + 16 * i + 4 * g4 + r) + (wn - WN / 2) * NJ * 16 + r16;
+        for (int r = 0; r < 4; r++) {
+          float* x = upat(wm * NI * 16 + 16 * i + 4 * g4 + r) + cw;
 #pragma unroll
-            for (int j = 0; j < NJ; j++) up[16 * j] = acc[i][j][r] * sc[i][r];
-          }
+          for (int j = 0; j < NJ; j++) x[16 * j] = acc[i][j][r] * sc[i][r];
+        }
       }
       __syncthreads();
-      if (wn < (uint32_t)(WN / 2)) {
-        // gate row j of this lane's columns: the tile's column n is gate
-        // row ntile * HB + n
-        const uint32_t lr0 = ntile * HB + wn * NJ * 16 + r16;
-        float hv[NI][4][NJ];
+      // the gate row of this lane's columns: the tile's column n is gate
+      // row ntile * HB + n
+      const uint32_t lr0 = ntile * HB + cw;
+      float hv[NI / 2][4][NJ];
 #pragma unroll
-        for (int i = 0; i < NI; i++)
+      for (int ii = 0; ii < NI / 2; ii++) {
+        const int i = gate ? ii : ii + NI / 2;
 #pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const float* up = upat(wm * NI * 16 + 16 * i + 4 * g4 + r) + wn * NJ * 16 + r16;
+        for (int r = 0; r < 4; r++) {
+          const float* x = upat(wm * NI * 16 + 16 * i + 4 * g4 + r) + cw;
 #pragma unroll
-            for (int j = 0; j < NJ; j++) hv[i][r][j] = fast_silu(acc[i][j][r] * sc[i][r]) * up[16 * j];
+          for (int j = 0; j < NJ; j++) {
+            const float own = acc[i][j][r] * sc[i][r], other = x[16 * j];
+            hv[ii][r][j] = gate ? fast_silu(own) * other : fast_silu(other) * own;
           }
-        if (a.Yh) {
-          __bf16* yb = a.Yh + mrow * a.seg[0].rows + lr0;
-#pragma unroll
-          for (int i = 0; i < NI; i++)
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-#pragma unroll
-              for (int j = 0; j < NJ; j++) yb[(size_t)(16 * i + r) * a.seg[0].rows + 16 * j] = (__bf16)hv[i][r][j];
-        } else {
-          float* yb = a.seg[0].Y + mrow * a.seg[0].ldy + lr0;
-#pragma unroll
-          for (int i = 0; i < NI; i++)
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-#pragma unroll
-              for (int j = 0; j < NJ; j++) yb[(size_t)(16 * i + r) * a.seg[0].ldy + 16 * j] = hv[i][r][j];
         }
+      }
+      const size_t mh = mrow + (gate ? 0 : 16 * (NI / 2));   // this lane's first row of its half
+      if (a.Yh) {
+        __bf16* yb = a.Yh + mh * a.seg[0].rows + lr0;
+#pragma unroll
+        for (int ii = 0; ii < NI / 2; ii++)
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++) yb[(size_t)(16 * ii + r) * a.seg[0].rows + 16 * j] = (__bf16)hv[ii][r][j];
+      } else {
+        float* yb = a.seg[0].Y + mh * a.seg[0].ldy + lr0;
+#pragma unroll
+        for (int ii = 0; ii < NI / 2; ii++)
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++) yb[(size_t)(16 * ii + r) * a.seg[0].ldy + 16 * j] = hv[ii][r][j];
       }
       return;
     }
@@ -254,7 +265,7 @@ __global__ __launch_bounds__(WM * WN * 64, WM * WN / 4) void k_gemm_wide(GemvArg
     }
     return;
   }
-  if (a.mode == GM_SILU) {
+  if constexpr (SILU) {
     // up columns (the second half of the waves' columns) through LDS to the
     // gate columns: tile rows 64 q .. 64 q + 63 in stage object q
     constexpr int HB = BN / 2;
@@ -379,9 +390,11 @@ hipError_t launch_gemm_wide(const GemvArgs& a, const __bf16* Ah, const float* rs
   }
   const uint32_t mt = (a.B + kWideBM - 1) / kWideBM;
   if (wide_cost(a, kBN192, cus) < wide_cost(a, kBN256, cus))
-    hipLaunchKernelGGL((k_gemm_wide<4, 2, 4, 6>), dim3(wide_tiles(a, kBN192), mt), dim3(512), 0, st, a, Ah, rsc);
+    if (a.mode == GM_SILU) hipLaunchKernelGGL((k_gemm_wide<4, 2, 4, 6, true>), dim3(wide_tiles(a, kBN192), mt), dim3(512), 0, st, a, Ah, rsc);
+    else hipLaunchKernelGGL((k_gemm_wide<4, 2, 4, 6, false>), dim3(wide_tiles(a, kBN192), mt), dim3(512), 0, st, a, Ah, rsc);
   else
-    hipLaunchKernelGGL((k_gemm_wide<2, 4, 8, 4>), dim3(wide_tiles(a, kBN256), mt), dim3(512), 0, st, a, Ah, rsc);
+    if (a.mode == GM_SILU) hipLaunchKernelGGL((k_gemm_wide<2, 4, 8, 4, true>), dim3(wide_tiles(a, kBN256), mt), dim3(512), 0, st, a, Ah, rsc);
+    else hipLaunchKernelGGL((k_gemm_wide<2, 4, 8, 4, false>), dim3(wide_tiles(a, kBN256), mt), dim3(512), 0, st, a, Ah, rsc);
   return hipGetLastError();
 }
 
