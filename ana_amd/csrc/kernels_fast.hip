@@ -2724,7 +2724,7 @@ __global__ __launch_bounds__(256) void k_split(const float* __restrict__ X, uint
 // other waves' loads visible; loads of the next stage go out right after
 // it (the barrier also says every wave is done with the stage they
 // overwrite). Norm scale, residual and SiLU as in k_gemm_big.
-template <int NS>
+template <int NS, bool SILU>
 __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __restrict__ Ahg,
                                                   const float* __restrict__ rscg) {
   constexpr int BM = 128, BN = 128, BK = 64;
@@ -2814,7 +2814,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
   // before the k loop, so those loads overlap the MFMAs instead of waiting
   // in the epilogue with every other workgroup's
   const uint32_t wrows = a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
-  const bool full = a.mode != GM_SILU && nb == (uint32_t)BM && (ntile + 1) * BN <= wrows;
+  const bool full = !SILU && nb == (uint32_t)BM && (ntile + 1) * BN <= wrows;
   uint32_t col[4];
   bool s1[4];
 #pragma unroll
@@ -2919,7 +2919,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
     }
     return;
   }
-  if (a.mode == GM_SILU) {
+  if constexpr (SILU) {
     // up columns (wn = 1) through LDS to the gate columns (wn = 0), one
     // 64-row half at a time
     ANA_VMCNT(0);
@@ -3022,7 +3022,10 @@ hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t ca
   // two LDS stages (48 KB) ran 5-12% faster than three (72 KB) at the
   // 8192-row prefill shapes with random operands (two workgroups a CU
   // either way, by registers)
-  hipLaunchKernelGGL(k_gemm_dl<2>, grid, dim3(256), 0, st, a, Ah, rsc);
+  // (SiLU a compile-time choice: its code in the other products' kernel
+  // changes how the compiler schedules their k loop)
+  if (a.mode == GM_SILU) hipLaunchKernelGGL((k_gemm_dl<2, true>), grid, dim3(256), 0, st, a, Ah, rsc);
+  else hipLaunchKernelGGL((k_gemm_dl<2, false>), grid, dim3(256), 0, st, a, Ah, rsc);
   if (e1) (void)hipEventRecord(e1, st);
   return hipGetLastError();
 }
