@@ -66,75 +66,82 @@ __device__ __forceinline__ float ex_rms_scale(float ss, float n) {
 
 namespace ana {
 
-// s = (((s + p[0]) + p[1]) + ...) + p[n-1]: one in-order chain over LDS
-// (p 16-byte aligned), with the next 8 float4 loads in flight
-// while the current 32 adds run.
-__device__ __forceinline__ float chain_sum_lds(float s, const float* __restrict__ p, uint32_t n) {
+// s = (((s + f(b[0].x)) + f(b[0].y)) + ...) + f(b[7].w), in order
+template <class F>
+__device__ __forceinline__ float chain_add8(float s, const float4 (&b)[8], F f) {
+#pragma unroll
+  for (int u = 0; u < 8; u++) {
+    s = s + f(b[u].x);
+    s = s + f(b[u].y);
+    s = s + f(b[u].z);
+    s = s + f(b[u].w);
+  }
+  return s;
+}
+
+// s = (((s + f(p[0])) + f(p[1])) + ...) + f(p[n-1]): one in-order chain
+// over LDS (p 16-byte aligned). Two sets of 8 float4 take turns: a set is
+// loaded again as soon as its 32 adds are issued, so its loads are in
+// flight while the other set's 32 adds run, and no set is copied into
+// another (a rotation through copies put the next loads behind a wait for
+// the current ones).
+template <class F>
+__device__ __forceinline__ float chain_lds(float s, const float* __restrict__ p, uint32_t n, F f) {
   const float4* q = reinterpret_cast<const float4*>(p);
   const uint32_t n4 = n >> 2;
   uint32_t i = 0;
-  if (n4 >= 8) {
-    float4 a[8];
+  if (n4 >= 16) {
+    float4 a[8], b[8];
 #pragma unroll
     for (int u = 0; u < 8; u++) a[u] = q[u];
-    for (i = 8; i + 8 <= n4; i += 8) {
-      float4 b[8];
 #pragma unroll
-      for (int u = 0; u < 8; u++) b[u] = q[i + u];
+    for (int u = 0; u < 8; u++) b[u] = q[8 + u];
+    // a holds float4s i - 16 .. i - 9, b i - 8 .. i - 1
+    for (i = 16; i + 16 <= n4; i += 16) {
+      s = chain_add8(s, a, f);
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        s = s + a[u].x;
-        s = s + a[u].y;
-        s = s + a[u].z;
-        s = s + a[u].w;
-      }
+      for (int u = 0; u < 8; u++) a[u] = q[i + u];
+      s = chain_add8(s, b, f);
 #pragma unroll
-      for (int u = 0; u < 8; u++) a[u] = b[u];
+      for (int u = 0; u < 8; u++) b[u] = q[i + 8 + u];
     }
+    s = chain_add8(s, a, f);
+    if (i + 8 <= n4) {
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-      s = s + a[u].x;
-      s = s + a[u].y;
-      s = s + a[u].z;
-      s = s + a[u].w;
+      for (int u = 0; u < 8; u++) a[u] = q[i + u];
+      s = chain_add8(s, b, f);
+      s = chain_add8(s, a, f);
+      i += 8;
+    } else {
+      s = chain_add8(s, b, f);
     }
+  }
+  if (i + 8 <= n4) {
+    float4 a[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) a[u] = q[i + u];
+    s = chain_add8(s, a, f);
+    i += 8;
   }
   for (; i < n4; i++) {
     const float4 v = q[i];
-    s = s + v.x;
-    s = s + v.y;
-    s = s + v.z;
-    s = s + v.w;
+    s = s + f(v.x);
+    s = s + f(v.y);
+    s = s + f(v.z);
+    s = s + f(v.w);
   }
-  for (uint32_t j = n4 << 2; j < n; j++) s = s + p[j];
+  for (uint32_t j = n4 << 2; j < n; j++) s = s + f(p[j]);
   return s;
+}
+
+// s = (((s + p[0]) + p[1]) + ...) + p[n-1]
+__device__ __forceinline__ float chain_sum_lds(float s, const float* __restrict__ p, uint32_t n) {
+  return chain_lds(s, p, n, [](float x) { return x; });
 }
 
 // s = s + x0*x0 + x1*x1 ... in order (M.norm's sum of squares)
 __device__ __forceinline__ float chain_sumsq_lds(float s, const float* __restrict__ p, uint32_t n) {
-  const float4* q = reinterpret_cast<const float4*>(p);
-  const uint32_t n4 = n >> 2;
-  uint32_t i = 0;
-  for (; i + 8 <= n4; i += 8) {
-    float4 a[8];
-#pragma unroll
-    for (int u = 0; u < 8; u++) a[u] = q[i + u];
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-      s = s + a[u].x * a[u].x;
-      s = s + a[u].y * a[u].y;
-      s = s + a[u].z * a[u].z;
-      s = s + a[u].w * a[u].w;
-    }
-  }
-  for (; i < n4; i++) {
-    const float4 v = q[i];
-    s = s + v.x * v.x;
-    s = s + v.y * v.y;
-    s = s + v.z * v.z;
-    s = s + v.w * v.w;
-  }
-  return s;
+  return chain_lds(s, p, n, [](float x) { return x * x; });
 }
 
 }  // namespace ana
