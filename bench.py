@@ -405,6 +405,13 @@ def main() -> int:
             extra[key] = {k: round(r64[k], 3) for k in ("tok_s", "ms_per_step", "step_gbs", "prefill_tok_s")}
             extra[key]["workload"] = ("B=64, 128-token prompts (ana_feeds_n, chunk 64), 8 untimed then 32 "
                                       "timed greedy steps at positions 135+; " + NUMERICS[m])
+        # the same batch deep in the window: every step's attention reads
+        # ~1940 live slots a sequence instead of ~150
+        r = run_batch(path, c, 64, 1920, 8, 32, 0, mode, chunk=128)
+        extra["b64_ctx2048"] = {k: round(r[k], 3) for k in ("tok_s", "ms_per_step", "step_gbs", "prefill_tok_s")}
+        extra["b64_ctx2048"]["workload"] = (f"B=64, 1920-token prompts (ana_feeds_n, chunk 128), {PRIME} + 8 untimed "
+                                            f"then 32 timed greedy steps at positions {1919 + PRIME + 8}+; "
+                                            + NUMERICS[mode])
     if a.prefill:
         extra.update(run_prefill(path, c, a.reps))
     if a.agent:
