@@ -350,7 +350,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
         (e = dalloc(&c->d_hh, (uint64_t)c->rows * cf.f)) != hipSuccess || (e = dalloc(&c->d_rsc, c->rows)) != hipSuccess ||
         (e = dalloc(&c->d_oh, (uint64_t)c->rows * d)) != hipSuccess ||
         (e = dalloc(&c->d_nxh, (uint64_t)c->rows * d)) != hipSuccess ||
-        (e = dalloc(&c->d_ssp, (uint64_t)c->rows * (d / 64 + 1))) != hipSuccess)
+        (e = dalloc(&c->d_ssp, (uint64_t)c->rows * (d / 48 + 1))) != hipSuccess)
       return bad(e);
   }
   if ((e = hipMemcpyAsync(c->W, ck.raw.data(), 4 * c->P, hipMemcpyHostToDevice, c->st)) != hipSuccess) return bad(e);
@@ -519,7 +519,7 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
       // a residual product of one segment on k_gemm_dl's full tiles also
       // leaves the next product's operand
       const bool fold = next_gain && g.Xh != c->d_nxh && g.nseg == 1 && g.mode != GM_SILU && g.B % 128 == 0 &&
-                        g.seg[0].rows == c->cfg.d && g.seg[0].rows % 128 == 0 && !gemm_wide_takes(g);
+                        g.seg[0].rows == c->cfg.d && g.seg[0].rows % gemm_dl_cols(g) == 0 && !gemm_wide_takes(g);
       if (fold) {
         g.Yn = c->d_nxh;
         g.gn = next_gain;
@@ -530,7 +530,7 @@ static hipError_t gemv_timed(ana_ctx* c, const GemvArgs& g0, uint32_t kind, bool
       if (fold && e == hipSuccess) {
         c->nx_of = g.seg[0].Y;
         c->nx_g = next_gain;
-        c->nx_n = g.seg[0].rows / 64;
+        c->nx_n = g.seg[0].rows / (gemm_dl_cols(g) / 2);
       }
       return e;
     }

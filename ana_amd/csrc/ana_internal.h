@@ -369,6 +369,9 @@ hipError_t launch_gemm_big(const GemvArgs& a, hipStream_t st, hipEvent_t e0 = nu
 bool gemm_wide_takes(const GemvArgs& a);
 // the wide-wave tiles alone (A in bf16, rsc the norm scales with a gain)
 hipError_t launch_gemm_wide(const GemvArgs& a, const __bf16* Ah, const float* rsc, hipStream_t st);
+// k_gemm_dl's tile width for a product (96 or 128 columns); a row's
+// partial sums of squares from its epilogue (Yn) come one per half tile
+uint32_t gemm_dl_cols(const GemvArgs& a);
 hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t cap_rows,
                           hipStream_t st, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 size_t attn_fast_part_floats(uint32_t B, uint32_t heads, uint32_t ctx, uint32_t hd);

@@ -2724,10 +2724,11 @@ __global__ __launch_bounds__(256) void k_split(const float* __restrict__ X, uint
 // other waves' loads visible; loads of the next stage go out right after
 // it (the barrier also says every wave is done with the stage they
 // overwrite). Norm scale, residual and SiLU as in k_gemm_big.
-template <int NS, bool SILU>
+template <int NS, bool SILU, int BN>
 __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __restrict__ Ahg,
                                                   const float* __restrict__ rscg) {
-  constexpr int BM = 128, BN = 128, BK = 64;
+  constexpr int BM = 128, BK = 64, NJ = BN / 32, HN = BN / 2;   // (NJ 16-column MFMA tiles a wave, HN its columns)
+  static_assert(BN == 128 || (BN == 96 && !SILU), "tile width");
   constexpr int OPE = BM * BK;   // bf16 elements of one operand's stage (16 KB, 16 chunks)
   static_assert(NS == 2, "two stage objects");
   // one LDS object per stage: a stage's fragment reads then provably miss
@@ -2753,11 +2754,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
   // slot lane % 8 holding k piece (lane % 8) ^ row
   const uint32_t pr = lane >> 3, pq = (lane & 7) ^ pr;
   uint32_t aoff[4];
-  const uint16_t* bptr[4];
+  const uint16_t* bptr[NJ];
 #pragma unroll
   for (int h = 0; h < 4; h++) {
     const uint32_t r = 8 * (4 * wv + h) + pr;
     aoff[h] = (m0 + (r < nb ? r : 0)) * K + 8 * pq;
+  }
+  // the weight tile's BN / 8 chunks: NJ a wave (chunk NJ wv + h)
+#pragma unroll
+  for (int h = 0; h < NJ; h++) {
+    const uint32_t r = 8 * (NJ * wv + h) + pr;
     const float* w;
     uint32_t sg, lr;
     const bool ok = sgs.row(BN, ntile, r, &w, &sg, &lr);
@@ -2767,16 +2773,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
     const uint32_t k0 = s * BK;
 #pragma unroll
     for (int h = 0; h < 4; h++) {
-      const uint32_t c = 4 * wv + h;
-      __builtin_amdgcn_global_load_lds((const void*)(Ahg + aoff[h] + k0), (lds_void*)&stage(B)[0][c * 512], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(bptr[h] + k0), (lds_void*)&stage(B)[1][c * 512], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(Ahg + aoff[h] + k0), (lds_void*)&stage(B)[0][(4 * wv + h) * 512], 16, 0, 0);
+      if (h < NJ)
+        __builtin_amdgcn_global_load_lds((const void*)(bptr[h] + k0), (lds_void*)&stage(B)[1][(NJ * wv + h) * 512], 16, 0, 0);
     }
   };
-  f32x4_t acc[4][4];
+  f32x4_t acc[4][NJ];
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < NJ; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   const uint32_t r16 = lane & 15, g4 = lane >> 4;
   // fragment read offsets (elements) in a 16-row MFMA tile (two chunks):
   // row r16, k piece 4 kh + g4
@@ -2787,15 +2793,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
     for (int kh = 0; kh < 2; kh++) {
       const __bf16* A0 = &stage(B)[0][0];
       const __bf16* B0 = &stage(B)[1][0];
-      bf16x8_t bfr[4], ah[4];
+      bf16x8_t bfr[NJ], ah[4];
 #pragma unroll
-      for (int j = 0; j < 4; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(B0 + (wn * 4 + j) * 1024 + foff[kh]);
+      for (int j = 0; j < NJ; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(B0 + (wn * NJ + j) * 1024 + foff[kh]);
 #pragma unroll
       for (int i = 0; i < 4; i++) ah[i] = *reinterpret_cast<const bf16x8_t*>(A0 + (wm * 4 + i) * 1024 + foff[kh]);
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int j = 0; j < NJ; j++)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bfr[j], acc[i][j], 0, 0, 0);
     }
   };
@@ -2815,27 +2821,27 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
   // in the epilogue with every other workgroup's
   const uint32_t wrows = a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
   const bool full = !SILU && nb == (uint32_t)BM && (ntile + 1) * BN <= wrows;
-  uint32_t col[4];
-  bool s1[4];
+  uint32_t col[NJ];
+  bool s1[NJ];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const uint32_t v = ntile * BN + wn * 64 + 16 * j + r16;
+  for (int j = 0; j < NJ; j++) {
+    const uint32_t v = ntile * BN + wn * HN + 16 * j + r16;
     s1[j] = v >= a.seg[0].rows;
     col[j] = s1[j] ? v - a.seg[0].rows : v;
   }
   const size_t mrow = m0 + wm * 64 + 4 * g4;   // this lane's first row
-  float res[4][4][4];
+  float res[NJ][4][4];
   if (full && a.mode == GM_RESID) {
     const float* rb = a.R + mrow * a.ldr;
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int j = 0; j < NJ; j++)
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) res[j][i][r] = rb[(size_t)(16 * i + r) * a.ldr + col[j]];
   } else {
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int j = 0; j < NJ; j++)
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -2857,7 +2863,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
   }
   const bool norm = a.ng != nullptr;
   // results: tile (i, j) of the wave holds rows wm*64 + 16i + 4*g4 + r,
-  // column wn*64 + 16j + r16. The tile's row norm scales go to LDS before
+  // column wn*HN + 16j + r16. The tile's row norm scales go to LDS before
   // any store (a global load after a store through another pointer would
   // wait on it, one round trip per element)
   if (norm) {
@@ -2879,17 +2885,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
 #pragma unroll
       for (int r = 0; r < 4; r++) sc[i][r] = norm ? rsl[wm * 64 + 16 * i + 4 * g4 + r] : 1.0f;
     // with Yn (one segment): the outputs times the next norm's gain in bf16
-    // too, and each row's sum of squares over the wave's 64 columns (the
+    // too, and each row's sum of squares over the wave's HN columns (the
     // 16 lanes of a row group by DPP, then one partial a row)
-    float ss[4][4], gn[4];
+    float ss[4][4], gn[NJ];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int r = 0; r < 4; r++) ss[i][r] = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; j++) gn[j] = a.Yn ? a.gn[col[j]] : 0.0f;   // (loaded before any store)
+    for (int j = 0; j < NJ; j++) gn[j] = a.Yn ? a.gn[col[j]] : 0.0f;   // (loaded before any store)
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < NJ; j++) {
       float* const Yb = s1[j] ? a.seg[1].Y : a.seg[0].Y;
       const uint32_t ld = s1[j] ? a.seg[1].ldy : a.seg[0].ldy;
       float* yb = Yb + mrow * ld + col[j];
@@ -2908,7 +2914,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
         }
     }
     if (a.Yn) {
-      const uint32_t nsp = a.seg[0].rows / 64;
+      const uint32_t nsp = a.seg[0].rows / HN;
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -2919,7 +2925,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
     }
     return;
   }
-  if constexpr (SILU) {
+  if constexpr (SILU && BN == 128) {
     // up columns (wn = 1) through LDS to the gate columns (wn = 0), one
     // 64-row half at a time
     ANA_VMCNT(0);
@@ -2962,11 +2968,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
     return;
   }
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
+  for (int j = 0; j < NJ; j++) {
     // one column block's residuals live at a time: the compiler barrier
     // keeps the next block's loads below this one's stores
     asm volatile("" ::: "memory");
-    const uint32_t n = wn * 64 + 16 * j + r16;
+    const uint32_t n = wn * HN + 16 * j + r16;
     const float* w_;
     uint32_t sg, lr;
     if (!sgs.row(BN, ntile, n, &w_, &sg, &lr)) continue;
@@ -2993,13 +2999,35 @@ __global__ __launch_bounds__(256, 2) void k_gemm_dl(GemvArgs a, const __bf16* __
   }
 }
 
+// k_gemm_dl's tile width: 96 where its tiles fill the workgroup slots (two
+// a CU) at less tile width a CU than 128-wide ones do. At N = 768 and 8192
+// rows, 128-wide tiles are 384 workgroups on 512 slots, so half the CUs
+// take two and set the time while the rest take one; 96-wide tiles are
+// 512, two on every CU, each CU a quarter fewer columns.
+uint32_t gemm_dl_cols(const GemvArgs& a) {
+  if (a.mode == GM_SILU) return 128;
+  static uint32_t slots = 0;
+  if (slots == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    slots = 2 * (uint32_t)n;
+  }
+  const uint32_t rows = a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0), mt = (a.B + 127) / 128;
+  auto cost = [&](uint32_t bn) { return ((rows + bn - 1) / bn * mt + slots - 1) / slots * bn; };
+  return cost(96) < cost(128) ? 96 : 128;
+}
+
 hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t cap_rows,
                           hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   if (a.amax || (a.K % 64) || a.B == 0 || !a.Wh0 || (a.nseg > 1 && !a.Wh1)) return hipErrorInvalidValue;
   if (a.B > cap_rows) return hipErrorInvalidValue;
   if (a.Xh && a.ng && !a.sspi) return hipErrorInvalidValue;   // (bf16 input with a norm: its partials)
-  // Yn: k_gemm_dl's full tiles only (its epilogue writes it), one segment
-  if (a.Yn && (a.nseg != 1 || a.mode == GM_SILU || a.B % 128 || a.seg[0].rows % 128 || !a.gn || !a.ssp ||
+  const uint32_t BN = gemm_dl_cols(a);
+  // Yn: k_gemm_dl's full tiles only (its epilogue writes it), one segment;
+  // its partial sums of squares go a row per BN / 2 columns
+  if (a.Yn && (a.nseg != 1 || a.mode == GM_SILU || a.B % 128 || a.seg[0].rows % BN || !a.gn || !a.ssp ||
                gemm_wide_takes(a)))
     return hipErrorInvalidValue;
   // the split first (its time is inside the events), unless X came in bf16
@@ -3016,7 +3044,7 @@ hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t ca
     return e;
   }
   if (a.Yh) return hipErrorInvalidValue;   // (only the large tiles write bf16 outputs)
-  const uint32_t per = a.mode == GM_SILU ? 64 : 128;
+  const uint32_t per = a.mode == GM_SILU ? 64 : BN;
   const uint32_t tiles = a.mode == GM_SILU ? (a.seg[0].rows + per - 1) / per : (rows + per - 1) / per;
   dim3 grid(tiles, (a.B + 127) / 128);
   // two LDS stages (48 KB) ran 5-12% faster than three (72 KB) at the
@@ -3024,8 +3052,9 @@ hipError_t launch_gemm_dl(const GemvArgs& a, __bf16* Ah, float* rsc, uint32_t ca
   // either way, by registers)
   // (SiLU a compile-time choice: its code in the other products' kernel
   // changes how the compiler schedules their k loop)
-  if (a.mode == GM_SILU) hipLaunchKernelGGL((k_gemm_dl<2, true>), grid, dim3(256), 0, st, a, Ah, rsc);
-  else hipLaunchKernelGGL((k_gemm_dl<2, false>), grid, dim3(256), 0, st, a, Ah, rsc);
+  if (a.mode == GM_SILU) hipLaunchKernelGGL((k_gemm_dl<2, true, 128>), grid, dim3(256), 0, st, a, Ah, rsc);
+  else if (BN == 96) hipLaunchKernelGGL((k_gemm_dl<2, false, 96>), grid, dim3(256), 0, st, a, Ah, rsc);
+  else hipLaunchKernelGGL((k_gemm_dl<2, false, 128>), grid, dim3(256), 0, st, a, Ah, rsc);
   if (e1) (void)hipEventRecord(e1, st);
   return hipGetLastError();
 }
