@@ -434,11 +434,16 @@ static bool fast_path(const ana_ctx* c, uint32_t B) { return fast_mode(c) && B <
 // a decode call's attention above kSmallB rows goes in kRowsSplit-slot
 // pieces once some row reaches 2 kRowsSplit live slots (one workgroup a row
 // would stream the whole window alone: at B = 32 and 1930 slots, 96 us a
-// layer for 379 MB)
+// layer for 379 MB), while its (head, row) pairs are fewer than
+// kRowsSplitPairs. With more pairs than that, one workgroup each already
+// gives every CU two or more, and the pieces only add partials and the
+// combine: at B = 64 and ~1950 live slots the whole-window grid ran the step
+// 0.991 -> 0.944 ms, and B = 256 at 512-767 slots 157.8k -> 161.7k tok/s
+constexpr uint64_t kRowsSplitPairs = 512;
 static bool split_attention(const ana_ctx* c, uint32_t n, const uint32_t* pos, uint32_t steps) {
   uint64_t top = 0;
   for (uint32_t i = 0; i < n; i++) top = std::max<uint64_t>(top, (uint64_t)pos[i] + steps);
-  return n > kSmallB && top >= 2ull * kRowsSplit;
+  return n > kSmallB && top >= 2ull * kRowsSplit && (uint64_t)n * c->cfg.heads < kRowsSplitPairs;
 }
 // decode steps below this many rows take the products over packed weights
 // (the prefill products' 128-row tiles would leave most CUs idle: at 256
