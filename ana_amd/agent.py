@@ -9,9 +9,9 @@ stretch as al.gen runs it (Loop.bend:480-505):
   drawn (al.start and al.forced.first, Loop.bend:275-277, 338-343);
 - a stretch of budget N: a pick that is EOS ends the episode ("eos", the EOS
   not written); with N picks written, the next one ends it ("budget"); a
-  pick that ends a call line is written, the call's token fed in its place
-  (al.called, Loop.bend:403-411: the newline token, `call_token`) and the
-  tool asked; any other pick is written, fed, and the next one drawn (or,
+  pick that ends a call line is replaced by the call's token, written and
+  fed in its place (al.called, Loop.bend:403-411, writes the newline and
+  feeds the newline token, `call_token`), and the tool asked; any other pick is written, fed, and the next one drawn (or,
   while given tokens remain, taken from them: al.next, Loop.bend:375-383);
 - a tool's echo is fed as unsampled tokens and a new stretch starts from a
   pick drawn from the echo's last logits (al.resume, Loop.bend:561-567);
@@ -65,9 +65,11 @@ def run(dec, eps: Sequence[Episode], st, is_call: Callable[[int, list], bool],
     Each pick of episode i (tokens = everything it wrote so far): EOS ends
     it ("eos"); with the stretch's budget of picks written, it ends it
     ("budget"); else it is written, and is_call(i, tokens) asks whether it
-    ends a call line. Then, with calls left, tool(i, tokens) either ends the
-    episode (None: "tool", the caller's verdict, as a passed check ends
-    al.round) or gives the echo: call_token (None: the written pick) is fed
+    ends a call line. If it does, call_token (None: the pick itself) takes
+    the pick's place among the tokens written, as al.called writes the
+    newline in place of the pick's bytes; then, with calls left, tool(i,
+    tokens) either ends the episode (None: "tool", the caller's verdict, as
+    a passed check ends al.round) or gives the echo: the call's token is fed
     at the call's place, the echo after it, and a new stretch starts with a
     new budget; without calls left the episode ends ("calls")."""
     n = len(eps)
@@ -123,6 +125,8 @@ def run(dec, eps: Sequence[Episode], st, is_call: Callable[[int, list], bool],
                 out[i].tokens.append(t)
                 out[i].drawn.append(drawn)
                 if is_call(i, out[i].tokens):
+                    if call_token is not None:
+                        t = out[i].tokens[-1] = int(call_token)
                     if calls[i] == 0:
                         out[i].why = "calls"
                         break
@@ -134,7 +138,7 @@ def run(dec, eps: Sequence[Episode], st, is_call: Callable[[int, list], bool],
                     echo = [int(x) for x in ans]
                     if EOS in echo:
                         raise ValueError("agent.run: EOS in a tool's echo")
-                    fed += [t if call_token is None else int(call_token)] + echo
+                    fed += [t] + echo
                     given[i] = []
                     left[i] = eps[i].budget
                     idx.append(i)

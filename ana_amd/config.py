@@ -131,3 +131,6 @@ FP100M = Config(32768, 2048, 768, 2048, 12, 12, True, True, True)
 # 115M at ctx 256 with sigmoid gates, no qk-norm, no sinks)
 V1 = Config(32768, 256, 256, 1024, 4, 4, False, False, False)
 V2 = Config(32768, 256, 768, 2048, 12, 12, False, False, False)
+# v2 as BASELINE.json writes it (MLP 3072: 143,739,648 parameters, not the
+# reference's 115M, whose MLP is 2048)
+V2_F3072 = Config(32768, 256, 768, 3072, 12, 12, False, False, False)

@@ -1380,6 +1380,10 @@ static __device__ __align__(256) uint32_t scratch[kNoAllocWords];
 static constexpr int kMaxDevices = 64;
 static uint32_t* g_scratch[kMaxDevices] = {};
 static std::mutex g_scratch_mu;
+// held by a call for its whole use of a device's array, from clearing the
+// counters to the final synchronisation, so calls on one GPU from several
+// threads (several contexts) take the array in turn instead of racing
+static std::mutex g_scratch_use[kMaxDevices];
 
 // once per device, with that device current (ana_open): scratch's device
 // address; an error here leaves only ana_generate_noalloc unavailable
@@ -1409,6 +1413,7 @@ extern "C" int ana_generate_noalloc(ana_ctx* c, uint32_t n, const uint32_t* seq,
   uint32_t* d_sm = base + cnt_words;
   uint32_t* d_rm = d_sm + (size_t)n * steps;
   const bool greedy = !s || s->temperature <= 0.0f;
+  std::lock_guard<std::mutex> use(g_scratch_use[c->device]);
   HIPCHK(c, hipSetDevice(c->device));
   if (int r = gen_inputs(c, n, seq, pos, tok, greedy, rng)) return r;
   // the counters start at zero (the array keeps the last call's contents)

@@ -159,8 +159,9 @@ int ana_generate(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, const uin
  * picks) lives in a fixed device array of 2^18 words that each GPU holds
  * until the process ends. A call needs 64 * ceil(n / 64) + 2 * n * steps
  * words of it; larger calls fail with ANA_EINVAL. Every call on one GPU
- * shares that array, whatever the context: calls that overlap on one GPU
- * (from several threads) race. */
+ * shares that array, whatever the context, so calls on one GPU from several
+ * threads run one at a time: each holds a per-device lock from clearing its
+ * counters to its final synchronisation. */
 int ana_generate_noalloc(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, const uint32_t* pos,
                          const uint32_t* tok, uint32_t steps, const ana_sampling* s, uint64_t* rng,
                          uint32_t* out);

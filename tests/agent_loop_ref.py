@@ -35,14 +35,17 @@ def episode(feed, pick, ep, is_call, tool, call_token=None):
             out.tokens.append(t)
             out.drawn.append(drawn)
             if is_call(out.tokens):
-                break                  # al.called
+                # al.called (Loop.bend:403-411) writes the newline (10 <> out)
+                # in place of the pick's bytes and feeds the newline token
+                if call_token is not None:
+                    out.tokens[-1] = t = call_token
+                break
             n -= 1
             # al.next (Loop.bend:375-383): t fed; a given token next, else a
             # pick drawn
             feed(t)
             cur = (force.pop(0), False) if force else (pick(), True)
-        # al.called (Loop.bend:403-411): the call's token fed in its place;
-        # al.round answers it while calls are left
+        # al.round answers the call while calls are left
         if calls == 0:
             out.why = "calls"
             return out
@@ -51,7 +54,7 @@ def episode(feed, pick, ep, is_call, tool, call_token=None):
         if echo is None:
             out.why = "tool"
             return out
-        feed(t if call_token is None else call_token)
+        feed(t)
         # al.resume (Loop.bend:561-567): the echo fed, a pick drawn, a new
         # stretch, nothing left to give
         for e in echo:

@@ -89,6 +89,33 @@ def test_batched_matches_loop():
             # the slot saw exactly the restatement's feeds (the last pick's
             # token is fed only when drawn)
             assert dec.hist[i] == hist, (ct, i)
+        if ct is not None:
+            # the call-ending picks (4 mod 9, never 11) were written as the
+            # call's token: no written token ends a call, and some calls
+            # were made
+            assert not any(is_call(0, [t]) for o in together for t in o.tokens)
+            assert sum(o.tokens.count(ct) for o in together) >= 3
+
+
+def test_call_token_written_and_fed():
+    """al.called: the pick that ends a call line is written as the newline
+    and the newline token is fed in its place, so the tool and the engine
+    both see call_token, never the pick."""
+    seen = []
+
+    def tool1(i, toks):
+        seen.append(list(toks))
+        return [5, 6] if len(seen) == 1 else None
+
+    ep = agent.Episode([0, 3], seed=0, budget=40, calls=2)
+    dec = FakeDecoder(1)
+    out = agent.run(dec, [ep], None, is_call, tool1, call_token=11)[0]
+    assert seen and all(s[-1] == 11 for s in seen)
+    k = len(seen[0])
+    assert out.tokens[k - 1] == 11
+    # fed: the prompt, then the written tokens up to the call, with 11 at the
+    # call's place, then the echo
+    assert dec.hist[0][:len(ep.prompt) + k + 2] == list(ep.prompt) + out.tokens[:k] + [5, 6]
 
 
 def test_endings_and_flags():
