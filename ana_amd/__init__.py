@@ -19,7 +19,7 @@ from .config import Config
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libana.so")
 
-ANA_OK, ANA_EINVAL, ANA_ECKPT, ANA_EDEVICE, ANA_ENOMEM, ANA_EUNSUP = range(6)
+ANA_OK, ANA_EINVAL, ANA_ECKPT, ANA_EDEVICE, ANA_ENOMEM, ANA_EUNSUP, ANA_ETOK, ANA_ETIME = range(8)
 EXACT_FP32 = 0
 FAST_FP32 = 1
 BF16 = 2
@@ -82,6 +82,8 @@ SIGNATURES = {
     "ana_state": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, _f32p, C.c_size_t]),
     "ana_prof": (C.c_int, [C.c_void_p, C.c_int]),
     "ana_prof_read": (C.c_int, [C.c_void_p, C.c_uint32, _u64p, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "ana_trace": (C.c_int, [C.c_void_p, C.c_uint32]),
+    "ana_trace_read": (C.c_int, [C.c_void_p, _u32p, C.c_size_t, _u32p]),
     "ana_bpe_open": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
     "ana_bpe_bytes": (C.c_int, [C.POINTER(C.c_void_p)]),
     "ana_bpe_close": (None, [C.c_void_p]),
@@ -330,6 +332,23 @@ class Decoder:
             self._check(lib().ana_prof_read(self.h, k, C.byref(n), C.byref(ms), C.byref(b)))
             out[name] = (n.value, ms.value, b.value)
         return out
+
+    def trace(self, steps: int) -> None:
+        """Arm (steps >= 1) or disarm (0) the persistent decode kernel's
+        phase stamps."""
+        self._check(lib().ana_trace(self.h, steps))
+
+    def trace_read(self) -> np.ndarray:
+        """The last persistent launch's stamps: [steps, phases, workgroups, 4]
+        ticks of the device's constant-rate clock, its low 32 bits (start,
+        inputs seen, weights landed, outputs published)."""
+        dims = np.zeros(3, dtype=np.uint32)
+        self._check(lib().ana_trace_read(self.h, None, 0, _p(dims, C.c_uint32)))
+        n = int(np.prod(dims.astype(np.int64))) * 4
+        out = np.zeros(n, dtype=np.uint32)
+        if n:
+            self._check(lib().ana_trace_read(self.h, _p(out, C.c_uint32), n, _p(dims, C.c_uint32)))
+        return out.reshape(int(dims[0]), int(dims[1]), int(dims[2]), 4)
 
     def state(self, seq: int, layer: int) -> np.ndarray:
         c = self.config

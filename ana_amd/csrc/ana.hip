@@ -95,6 +95,9 @@ struct ana_ctx {
   uint64_t ll_par = 0, e_key = 0;
   uint32_t* d_ctl = nullptr;
   uint32_t epoch = 0;
+  uint64_t p_tmo = 0;                // a wait's limit in the device clock's ticks (2 s)
+  uint32_t* d_trace = nullptr;       // ana_trace's phase stamps, when armed
+  uint32_t trace_steps = 0, trace_phases = 0;
   float* d_gla = nullptr;            // fast prefill's GLA scan scratch
   GlaScratch gla{};                  // its regions
   GlaSub* d_gtab = nullptr;          // a prefill step's sub-chunk table
@@ -209,7 +212,7 @@ static void release(ana_ctx* c) {
   (void)hipSetDevice(c->device);
   if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
   if (c->gexec_n) (void)hipGraphExecDestroy(c->gexec_n);
-  void* ps[] = {c->d_play, c->d_ll, c->d_ctl, c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
+  void* ps[] = {c->d_play, c->d_ll, c->d_ctl, c->d_trace, c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
                 c->d_ss, c->d_pm, c->d_gtab, c->d_grun, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce, c->d_rcp,
                 c->d_sah, c->d_hh, c->d_rsc, c->PK, c->d_hpc, c->d_hpctl, c->d_oh, c->d_nxh, c->d_ssp};
@@ -598,6 +601,10 @@ static hipError_t persist_setup(ana_ctx* c) {
   if ((e = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->device)) != hipSuccess) return e;
   const uint32_t G = (uint32_t)std::min(pr.multiProcessorCount, 256);
   if (!coop || !decode1_fits(cf, G)) return hipSuccess;
+  int rate_khz = 0;   // the constant-rate clock the kernel's waits are timed by
+  if ((e = hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, c->device)) != hipSuccess) return e;
+  if (rate_khz <= 0) return hipSuccess;
+  c->p_tmo = (uint64_t)rate_khz * 2000ull;
   const uint32_t d = cf.d, f = cf.f, hd = d / cf.heads, np = decode1_pieces(cf, G);
   std::vector<PLayer> t(cf.layers);
   uint64_t en = 0;
@@ -1246,6 +1253,10 @@ static int generate_persist(ana_ctx* c, const uint32_t* pos, uint32_t steps, uin
       pa.ll = c->d_ll; pa.ll_par = c->ll_par; pa.e_key = c->e_key;
       pa.epoch0 = c->epoch;
       pa.ctl = c->d_ctl;
+      pa.tmo = c->p_tmo;
+      pa.trace = c->d_trace;
+      pa.trace_steps = c->trace_steps;
+      pa.trace_phases = c->trace_phases;
       hipError_t e;
       {
         double by = 0.0;
@@ -1266,7 +1277,10 @@ static int generate_persist(ana_ctx* c, const uint32_t* pos, uint32_t steps, uin
       // the next launch's entries never carry an epoch this one wrote
       c->epoch += (m - done) + 2;
       if (ctl[0] || ctl[1])
-        return fail(c, ANA_EDEVICE, "device fault: a persistent decode wait ran out (step %u of the call)", k0 + done + ctl[2]);
+        return fail(c, ANA_ETIME,
+                    "persistent decode: a wait between workgroups passed its 2 s limit at step %u of the call; "
+                    "the sequence's state is partly advanced: reset it before feeding it again",
+                    k0 + done + ctl[2]);
       done += ctl[2];
       if (ctl[3]) {
         // no logit reached the maximum: Sample.argmax over the stored logits
@@ -1466,6 +1480,45 @@ extern "C" int ana_prof_read(ana_ctx* c, uint32_t kind, uint64_t* launches, doub
   if (launches) *launches = n;
   if (ms) *ms = t;
   if (bytes) *bytes = by;
+  return ANA_OK;
+}
+
+extern "C" int ana_trace(ana_ctx* c, uint32_t steps) {
+  if (!c) return ANA_EINVAL;
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  if (c->d_trace) (void)hipFree(c->d_trace);
+  c->d_trace = nullptr;
+  c->trace_steps = c->trace_phases = 0;
+  if (steps == 0) return ANA_OK;
+  if (!c->persist) return fail(c, ANA_EUNSUP, "ana_trace: this context has no persistent decode kernel");
+  if (steps > 64) return fail(c, ANA_EINVAL, "ana_trace: %u steps, at most 64", steps);
+  const uint32_t ph = decode1_phases(c->cfg);
+  const size_t n = (size_t)steps * ph * c->pG * 4;
+  if (c->cfg.layers > 32) return fail(c, ANA_EUNSUP, "ana_trace: %u layers, at most 32", c->cfg.layers);
+  if (hipMalloc(&c->d_trace, 4 * n) != hipSuccess) {
+    (void)hipGetLastError();
+    c->d_trace = nullptr;
+    return fail(c, ANA_ENOMEM, "ana_trace: out of device memory");
+  }
+  HIPCHK(c, launch_zero_u32(c->d_trace, (uint32_t)n, c->st));
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  c->trace_steps = steps;
+  c->trace_phases = ph;
+  return ANA_OK;
+}
+
+extern "C" int ana_trace_read(ana_ctx* c, uint32_t* out, size_t cap, uint32_t dims[3]) {
+  if (!c || !dims) return ANA_EINVAL;
+  dims[0] = c->trace_steps;
+  dims[1] = c->trace_phases;
+  dims[2] = c->trace_steps ? c->pG : 0;
+  const size_t n = (size_t)dims[0] * dims[1] * dims[2] * 4;
+  if (n == 0 || !out) return ANA_OK;   // (no buffer: the extents only)
+  if (cap < n) return fail(c, ANA_EINVAL, "ana_trace_read: %zu stamps, room for %zu", n, cap);
+  HIPCHK(c, hipSetDevice(c->device));
+  HIPCHK(c, hipMemcpyAsync(out, c->d_trace, 4 * n, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(c, hipStreamSynchronize(c->st));
   return ANA_OK;
 }
 

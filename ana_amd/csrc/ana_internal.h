@@ -417,12 +417,17 @@ struct PersistArgs {
   unsigned long long* ll;   // two sets of ll_par entries
   uint64_t ll_par, e_key;   // entries a set; the head's keys (one a workgroup)
   uint32_t epoch0;          // step k of the launch tags its entries epoch0 + k + 1
-  uint32_t* ctl;            // [0] a wait ran out, [1] abort, [2] steps picked, [3] stopped on NaN
+  uint32_t* ctl;            // [0] a wait timed out, [1] abort, [2] steps picked, [3] stopped on NaN
+  uint64_t tmo;             // a wait's limit, in ticks of the device's constant-rate clock
+  uint32_t* trace;          // phase stamps [trace_steps][trace_phases][G][4], or null
+  uint32_t trace_steps, trace_phases;
 };
 // pieces of the ring a head's attention takes (one workgroup each)
 uint32_t decode1_pieces(const ana_config& c, uint32_t G);
 // whether the persistent kernel takes this configuration on G workgroups
 bool decode1_fits(const ana_config& c, uint32_t G);
 hipError_t launch_decode1(const PersistArgs& a, uint32_t G, hipStream_t st);
+// phases a step of the persistent kernel takes (the trace's second extent)
+uint32_t decode1_phases(const ana_config& c);
 
 }  // namespace ana

@@ -18,8 +18,10 @@
 // s + 2 after every workgroup has produced for step s + 1, so no consumer
 // of step s still reads a slot it overwrites.
 //
-// Every wait is bounded: a workgroup that polls too long, or sees another
-// one give up, raises the abort word and leaves, and the host reports it.
+// Every wait is bounded in time (the device's constant-rate clock, against a
+// limit the host passes): a workgroup that waits too long, or sees another
+// one give up, raises the abort word and leaves, and the host reports a
+// time-out (the sequence's state is then partly advanced).
 // A step whose logits have no maximum (NaN) stops the launch before its
 // pick; the host picks by Sample.argmax and launches again.
 #include <hip/hip_runtime.h>
@@ -34,7 +36,10 @@ namespace {
 
 constexpr uint32_t kPT = 256;           // threads per workgroup
 constexpr uint32_t kMaxPLayers = 64;    // layers the persistent kernel takes
-constexpr uint32_t kPollMax = 1u << 20; // polls before a wait gives up
+constexpr uint32_t kMaxTracePhases = 6 * 32 + 2;       // phases a traced step may have (32 layers)
+
+// the device's constant-rate clock (s_memrealtime: 100 MHz on gfx950)
+__device__ __forceinline__ uint64_t rtc() { return __builtin_amdgcn_s_memrealtime(); }
 
 
 __device__ __forceinline__ void ll_put(unsigned long long* p, float v, uint32_t ep) {
@@ -54,8 +59,9 @@ __device__ __forceinline__ bool aborted(uint32_t* ctl) {
 // was aborted (and raises the abort word).
 template <int PE, class Map, class Tag>
 __device__ bool ll_gather(const unsigned long long* base, uint32_t n, uint32_t ep, Map map, Tag tag, float* dst,
-                          uint32_t* ctl, uint32_t* bad_s) {
+                          uint32_t* ctl, uint32_t* bad_s, uint64_t tmo) {
   const uint32_t tid = threadIdx.x;
+  const uint64_t t0 = rtc();
   unsigned long long v[PE];
 #pragma unroll
   for (int e = 0; e < PE; e++) {
@@ -74,7 +80,7 @@ __device__ bool ll_gather(const unsigned long long* base, uint32_t n, uint32_t e
       }
     }
     if (all) break;
-    if ((it & 127) == 0 && (it >= kPollMax || aborted(ctl))) {
+    if ((it & 127) == 0 && (rtc() - t0 > tmo || aborted(ctl))) {
       ok = false;
       break;
     }
@@ -88,7 +94,7 @@ __device__ bool ll_gather(const unsigned long long* base, uint32_t n, uint32_t e
   __syncthreads();
   if (*bad_s) {
     if (tid == 0) {
-      if (!aborted(ctl)) atomicOr(&ctl[0], 1u);   // this workgroup's wait ran out
+      if (!aborted(ctl)) atomicOr(&ctl[0], 1u);   // this workgroup's wait timed out
       __hip_atomic_store(&ctl[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __builtin_amdgcn_s_waitcnt(0);   // no load into LDS outlives the workgroup
@@ -148,7 +154,12 @@ typedef __attribute__((address_space(3))) void lds_void;
 // 4 (l + 64 j). Loads retire in issue order, so a phase waits for all of
 // its wave's loads (vmcnt 0) before it reads its buffer: the next phase's
 // pieces, issued before this phase's input polls, have landed by then too.
-template <int HD, int NFD, int NFF>
+//
+// TR: the trace build. Wave 0's first lane stamps four clock readings a
+// phase (the clock's low 32 bits) into LDS (the phase's start; its inputs all seen; its weights
+// landed; its outputs published) and the workgroup copies a step's stamps
+// to a.trace after the pick, for the first a.trace_steps steps.
+template <int HD, int NFD, int NFF, bool TR>
 __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   constexpr int QD = HD / 4;            // attention: dims a score lane holds (4 lanes a slot)
   constexpr int C4 = HD / 4;            // float4 columns of a head
@@ -165,6 +176,19 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   __shared__ float o16[4][4][4];
   __shared__ uint32_t bad_s;
   __shared__ unsigned long long key_s[4];
+  __shared__ uint32_t tr_s[TR ? kMaxTracePhases : 1][4];
+  uint32_t ph = 0;   // the step's phase (trace)
+#define TS(i)                                       \
+  do {                                              \
+    if constexpr (TR) {                             \
+      if (tid == 0) tr_s[ph][i] = (uint32_t)rtc();  \
+    }                                               \
+  } while (0)
+#define TS_END()                                    \
+  do {                                              \
+    TS(3);                                          \
+    ph++;                                           \
+  } while (0)
   const uint32_t w = blockIdx.x, G = gridDim.x, tid = threadIdx.x, lane = tid & 63;
   const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // (a scalar: the wave's branches are uniform)
   const uint32_t d = a.d, f = a.f, H = a.heads, ctx = a.ctx, L = a.L;
@@ -325,6 +349,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   for (; k < a.steps; k++) {
     const uint32_t ep = a.epoch0 + k + 1;
     unsigned long long* LL = a.ll + (size_t)(ep & 1) * a.ll_par;
+    ph = 0;
     // layer 0's residual input is the token's embedding row
     if (orow_ok) x_own = W[(size_t)tok * d + orow];
     for (uint32_t l = 0; l < L; l++) {
@@ -333,6 +358,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       float svr = 0.0f, lamr = 0.0f, gqr = 0.0f, gkr = 0.0f, sinkr = 0.0f;
       // ---- norm, then q|k|v (|z): rows w RQ .. w RQ + RQ - 1
       __syncthreads();
+      TS(0);
       dma_kv(P, pb ^ 1);
       load_gain(gra, P.ra);
       // the mix's own inputs that do not depend on this token
@@ -351,10 +377,12 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       }
       if (l == 0) {
         for (uint32_t i = tid; i < d; i += kPT) xs[i] = W[(size_t)tok * d + i];
-      } else if (!ll_gather<4>(LL, d, ep, Ident{Ls[l - 1].e_x}, Tag32{}, xs, a.ctl, &bad_s)) {
+      } else if (!ll_gather<4>(LL, d, ep, Ident{Ls[l - 1].e_x}, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) {
         return;
       }
+      TS(1);
       land();
+      TS(2);
       norm_xs(d, gra);
       {
         float4 xr[NFD];
@@ -373,9 +401,11 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
           }
         }
       }
+      TS_END();
       pb ^= 1;
       // ---- the mix (pieces: an attention unit's K and V, in pb)
       __syncthreads();
+      TS(0);
       dma_wo(P, pb ^ 1);
       if (P.gla) {
         if (w < H * C4) {
@@ -388,7 +418,9 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
             if (i < 3u * HD) return base + 3 * d + h * HD + (i - 2 * HD);
             return base + 2 * d + h * HD + 4 * cb + (i - 3 * HD);
           };
-          if (!ll_gather<1>(LL, 3 * HD + 4, ep, map, Tag32{}, xs, a.ctl, &bad_s)) return;
+          if (!ll_gather<1>(LL, 3 * HD + 4, ep, map, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) return;
+          TS(1);
+          TS(2);
           const uint32_t ar = tid >> 2, c = tid & 3;
           const float q = (int)tid < HD ? xs[tid] : 0.0f, kk = (int)tid < HD ? xs[HD + tid] : 0.0f;
           const float q2 = block_sum(q * q, red);
@@ -427,7 +459,11 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
             for (int q = 0; q < 16; q++) acc += o16[q >> 2][q & 3][tid];
             ll_put(LL + P.e_o + h * HD + 4 * cb + tid, acc, ep);
           }
+        } else {
+          TS(1);
+          TS(2);
         }
+        TS_END();
         land();
       } else {
         const uint32_t npos = pos < ctx - 1 ? pos : ctx - 1, slot = pos % ctx;
@@ -439,8 +475,10 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
             if (i < 2u * HD) return base + d + h * HD + (i - HD);
             return base + 2 * d + h * HD + (i - 2 * HD);
           };
-          if (!ll_gather<1>(LL, 3 * HD, ep, map, Tag32{}, xs, a.ctl, &bad_s)) return;
+          if (!ll_gather<1>(LL, 3 * HD, ep, map, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) return;
+          TS(1);
           land();
+          TS(2);
           float q = (int)tid < HD ? xs[tid] : 0.0f, kx = (int)tid < HD ? xs[HD + tid] : 0.0f;
           if (a.qk) {
             // M.qkn (bend/Dense/Model.bend:39-42): gains 1 + g
@@ -536,8 +574,12 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
             ll_put(out + 1, lsum, ep);
           }
         } else {
+          TS(1);
           land();
+          TS(2);
         }
+        TS_END();
+        TS(0);
         // ---- the pieces and the sink combined: o of head h, columns 4 cb ..
         if (w < H * C4) {
           const uint32_t h = w / C4, cb = w % C4;
@@ -549,7 +591,9 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
             const uint32_t j = i - 2 * np;
             return base + (uint64_t)(j / 4) * (HD + 2) + 2 + 4 * cb + (j % 4);
           };
-          if (!ll_gather<1>(LL, 6 * np, ep, map, Tag32{}, xs, a.ctl, &bad_s)) return;
+          if (!ll_gather<1>(LL, 6 * np, ep, map, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) return;
+          TS(1);
+          TS(2);
           if (tid < 4) {
             float M = -INFINITY;
             for (uint32_t i = 0; i < np; i++) M = fmaxf(M, xs[i]);
@@ -564,15 +608,22 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
             if (a.sinks) den += __expf(sinkr - M);
             ll_put(LL + P.e_o + h * HD + 4 * cb + tid, acc / den, ep);
           }
+        } else {
+          TS(1);
+          TS(2);
         }
+        TS_END();
       }
       pb ^= 1;
       // ---- xa = x + Wo o
       __syncthreads();
+      TS(0);
       dma_gu(P, pb ^ 1);
       load_gain(grf, P.rf);
-      if (!ll_gather<4>(LL, d, ep, Ident{P.e_o}, Tag32{}, xs, a.ctl, &bad_s)) return;
+      if (!ll_gather<4>(LL, d, ep, Ident{P.e_o}, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) return;
+      TS(1);
       land();
+      TS(2);
       {
         float acc = 0.0f;
         if (orow_ok) {
@@ -583,12 +634,16 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         xa_own = x_own + acc;
         if (lane == 0 && orow_ok) ll_put(LL + P.e_xa + orow, xa_own, ep);
       }
+      TS_END();
       pb ^= 1;
       // ---- hh = silu(g) u on norm(xa)
       __syncthreads();
+      TS(0);
       dma_wd(P, pb ^ 1);
-      if (!ll_gather<4>(LL, d, ep, Ident{P.e_xa}, Tag32{}, xs, a.ctl, &bad_s)) return;
+      if (!ll_gather<4>(LL, d, ep, Ident{P.e_xa}, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) return;
+      TS(1);
       land();
+      TS(2);
       norm_xs(d, grf);
       {
         float4 xr[NFD];
@@ -610,13 +665,17 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
           }
         }
       }
+      TS_END();
       pb ^= 1;
       // ---- x = xa + Wd hh
       __syncthreads();
+      TS(0);
       if (l + 1 < L) dma_qkv(Ls[l + 1], pb ^ 1);
       else dma_head(0, pb ^ 1);
-      if (!ll_gather<NFF>(LL, f, ep, Ident{P.e_hh}, Tag32{}, xs, a.ctl, &bad_s)) return;
+      if (!ll_gather<NFF>(LL, f, ep, Ident{P.e_hh}, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) return;
+      TS(1);
       land();
+      TS(2);
       {
         float acc = 0.0f;
         if (orow_ok) {
@@ -627,15 +686,19 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         x_own = xa_own + acc;
         if (lane == 0 && orow_ok) ll_put(LL + P.e_x + orow, x_own, ep);
       }
+      TS_END();
       pb ^= 1;
     }
     // ---- the head: logits of rows h0 .. h1 - 1 (wave wv: rows h0 + wv + 4 i),
     // batch b (rows h0 + wv + 4 (b HBR + i)) in buffer pb ^ (b & 1)
     {
+      TS(0);
       float gfin[4];
       load_gain(gfin, a.fin);
-      if (!ll_gather<4>(LL, d, ep, Ident{Ls[L - 1].e_x}, Tag32{}, xs, a.ctl, &bad_s)) return;
+      if (!ll_gather<4>(LL, d, ep, Ident{Ls[L - 1].e_x}, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) return;
+      TS(1);
       land();
+      TS(2);
       norm_xs(d, gfin);
       float4 xr[NFD];
 #pragma unroll
@@ -682,19 +745,22 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         __hip_atomic_store(LL + a.e_key + w, (k48 << 16) | (ep & 0xFFFFu), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
       }
+      TS_END();
       pb ^= (nhb & 1);
     }
     // ---- the pick (dd.pick's order): every workgroup reads every key; the
     // next step's first product loads meanwhile
     {
       __syncthreads();
+      TS(0);
       dma_qkv(Ls[0], pb);
       unsigned long long kv = 0ull;
       bool ok = true;
       if (tid < G) {
+        const uint64_t t0 = rtc();
         kv = ll_ld(LL + a.e_key + tid);
         for (uint32_t it = 1; (uint32_t)(kv & 0xFFFFu) != (ep & 0xFFFFu); it++) {
-          if ((it & 127) == 0 && (it >= kPollMax || aborted(a.ctl))) {
+          if ((it & 127) == 0 && (rtc() - t0 > a.tmo || aborted(a.ctl))) {
             ok = false;
             break;
           }
@@ -719,6 +785,16 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       mk = key_s[0];
       for (int i = 1; i < 4; i++) mk = key_s[i] > mk ? key_s[i] : mk;
       __syncthreads();
+      TS(1);
+      TS(2);
+      TS_END();
+      if constexpr (TR) {
+        // this step's stamps: [step][phase][workgroup][4]
+        if (k < a.trace_steps) {
+          for (uint32_t i = tid; i < ph * 4; i += kPT)
+            a.trace[(((size_t)k * a.trace_phases + i / 4) * G + w) * 4 + i % 4] = tr_s[i / 4][i % 4];
+        }
+      }
       if (mk == 0ull) {
         // no logit reaches the maximum (NaN): the host picks by Sample.argmax
         nan_stop = true;
@@ -742,6 +818,8 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     a.ctl[2] = k;
     a.ctl[3] = nan_stop ? 1u : 0u;
   }
+#undef TS
+#undef TS_END
 }
 
 
@@ -768,11 +846,20 @@ bool decode1_fits(const ana_config& c, uint32_t G) {
   return true;
 }
 
+uint32_t decode1_phases(const ana_config& c) {
+  const uint32_t sm = c.layers / 4;
+  return 5 * (c.layers - sm) + 6 * sm + 2;
+}
+
 hipError_t launch_decode1(const PersistArgs& a, uint32_t G, hipStream_t st) {
   void* args[] = {const_cast<PersistArgs*>(&a)};
   const uint32_t hd = a.d / a.heads;
   if (a.f > 2048) return hipErrorInvalidValue;
-#define L_(H) return hipLaunchCooperativeKernel((const void*)k_decode1<H, 3, 8>, dim3(G), dim3(kPT), args, 0, st)
+  const bool tr = a.trace && a.trace_steps;
+  if (tr && a.trace_phases > kMaxTracePhases) return hipErrorInvalidValue;
+#define L_(H)                                                                                                     \
+  return hipLaunchCooperativeKernel(tr ? (const void*)k_decode1<H, 3, 8, true> : (const void*)k_decode1<H, 3, 8, false>, \
+                                    dim3(G), dim3(kPT), args, 0, st)
   if (hd == 64) L_(64);
   if (hd == 32) L_(32);
   if (hd == 16) L_(16);

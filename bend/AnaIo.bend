@@ -24,6 +24,11 @@ import Base
 def ana.open(path: String, numerics: U32, max_seqs: U32, chunk: U32) -> IO(U32):
   import "./effs/ana.c"
 
+# the Adam step the checkpoint was saved at (ana_config_of's step; the
+# Model's step, as dd.load reads it)
+def ana.step(h: U32) -> IO(U32):
+  import "./effs/ana.c"
+
 # dd.reset (Dense/Decode.bend:534-538): the sequence's states to zero
 def ana.reset(h: U32, seq: U32) -> IO(U32):
   import "./effs/ana.c"

@@ -178,6 +178,23 @@ static void __attribute__((constructor)) ana_open_use(void) {
 }
 #endif
 
+#ifdef CID(ana.step)
+Term ana_step_run(Env e, Term* f, IoWork* w) {
+  (void)e;
+  (void)w;
+  ana_config k;
+  uint64_t step = 0;
+  pthread_mutex_lock(&an_mu);
+  struct ana_ctx* c = an_ctx(f[0]);
+  an_check(c, AN.config_of(c, &k, &step));
+  pthread_mutex_unlock(&an_mu);
+  return (Term)(u32)step;
+}
+static void __attribute__((constructor)) ana_step_use(void) {
+  io_eff(CID(ana.step), ana_step_run);
+}
+#endif
+
 #ifdef CID(ana.reset)
 Term ana_reset_run(Env e, Term* f, IoWork* w) {
   (void)e;

@@ -45,6 +45,10 @@ extern "C" {
 #define ANA_ENOMEM 4     /* device allocation failed */
 #define ANA_EUNSUP 5     /* configuration outside what the kernels handle */
 #define ANA_ETOK 6       /* tokenizer artifact unreadable or rejected (Bpe.parse) */
+#define ANA_ETIME 7      /* a wait between the persistent decode kernel's workgroups passed
+                            its time limit (a stalled or heavily shared GPU): the call's
+                            sequence is partly advanced and must be reset (ana_reset)
+                            before it is fed again */
 
 /* numerics modes */
 #define ANA_EXACT_FP32 0 /* bit-exact with the reference's CPU kernels */
@@ -186,6 +190,24 @@ int ana_state(struct ana_ctx* ctx, uint32_t seq, uint32_t layer, float* out, siz
 int ana_prof(struct ana_ctx* ctx, int on);
 int ana_prof_read(struct ana_ctx* ctx, uint32_t kind, uint64_t* launches, double* ms,
                   double* bytes);
+
+/* Phase stamps of the persistent one-sequence decode kernel (no counterpart
+ * in the reference; for profiling the exchange between its workgroups).
+ * ana_trace(ctx, steps) with 1 <= steps <= 64 arms it (allocating the
+ * stamps' buffer; ANA_EUNSUP where the context has no persistent kernel or
+ * more than 32 layers); steps == 0 disarms it. While armed, each persistent
+ * launch records its first `steps` steps: per (step, phase, workgroup), four
+ * readings of the device's constant-rate clock (100 MHz on gfx950; its low
+ * 32 bits, so differences are taken modulo 2^32) taken by the
+ * workgroup's first thread: the phase's start, all of its inputs seen, its
+ * weights landed in LDS, its outputs published. A step's phases are, per
+ * layer, q|k|v(|z), the mix (GLA; or the attention pieces, then their
+ * combination), Wo, gate|up and down, then the head and the pick.
+ * ana_trace_read copies the last launch's stamps, [steps][phases]
+ * [workgroups][4], into out (cap entries) and their extents into dims;
+ * with out NULL it gives the extents only. */
+int ana_trace(struct ana_ctx* ctx, uint32_t steps);
+int ana_trace_read(struct ana_ctx* ctx, uint32_t* out, size_t cap, uint32_t dims[3]);
 
 /* The last error on ctx, or of the last failed ana_open when ctx is NULL. */
 const char* ana_error(const struct ana_ctx* ctx);

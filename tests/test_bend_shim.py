@@ -20,10 +20,10 @@ HDR = open(os.path.join(ROOT, "include", "ana.h")).read()
 DEFS = re.findall(r"^def (ana\.[a-z_]+)\((.*?)\) -> IO\((.*?)\):\n  import \"\./effs/ana\.c\"", BEND, re.M)
 
 
-def test_eight_effects_declared():
+def test_nine_effects_declared():
     names = [d[0] for d in DEFS]
-    assert names == ["ana.open", "ana.reset", "ana.feed", "ana.feeds", "ana.logits", "ana.top", "ana.pick",
-                     "ana.score"], names
+    assert names == ["ana.open", "ana.step", "ana.reset", "ana.feed", "ana.feeds", "ana.logits", "ana.top",
+                     "ana.pick", "ana.score"], names
 
 
 @pytest.mark.parametrize("name,args,ret", DEFS)
@@ -59,3 +59,103 @@ def test_resolved_symbols_are_the_abi():
     lib = ctypes.CDLL(so)
     for s in syms:
         assert hasattr(lib, s), s
+
+
+# ---- the engine arm: bend/Decode.bend.ana.patch
+PATCH_PATH = os.path.join(ROOT, "bend", "Decode.bend.ana.patch")
+PATCH = open(PATCH_PATH).read()
+REF_DECODE = "/root/reference/bend/Decode.bend"
+
+# each seam function of Decode.bend (En's cases, bend/Decode.bend:304-470)
+# and what its EAna arm must reach: the library effect, or the engine
+# helper that reaches it
+SEAM = {
+    "dc.en.step": ["AI.ana.feed(", "dc.en.ana.io("],
+    "dc.en.feed": ["AI.ana.feed("],
+    "dc.en.feeds": ["dc.en.ana.ids("],
+    "dc.en.prefill": ["dc.en.ana.prefill("],
+    "dc.en.step.pick": ["AI.ana.feed(", "dc.en.ana.pick("],
+    "dc.en.prefill.pick": ["dc.en.ana.prefill.pick("],
+    "dc.en.reset": ["AI.ana.reset("],
+    "dc.en.name": ['"ana"'],
+}
+# the engine's helpers and the effects they reach
+HELPERS = {
+    "dc.en.ana.io": ["AI.ana.logits("],
+    "dc.en.ana.ids": ["AI.ana.feeds(", "DIo.put.u32("],
+    "dc.en.ana.prefill": ["dc.en.ana.ids(", "dc.en.ana.io("],
+    "dc.en.ana.pick": ["AI.ana.top(", "dc.en.ana.io("],
+    "dc.en.ana.prefill.pick": ["dc.en.ana.ids(", "dc.en.ana.pick("],
+    "dc.loaded.ana": ["AI.ana.open(", "AI.ana.step(", "EAna{"],
+    "dc.load.eng.of": ["dc.loaded.ana(", "dc.load.fmt("],
+}
+
+
+def _defs(text):
+    """{name: body} of every top-level def in text"""
+    out, cur, body = {}, None, []
+    for line in text.split("\n"):
+        m = re.match(r"def ([a-z_.]+)\(", line)
+        if m:
+            if cur:
+                out[cur] = "\n".join(body)
+            cur, body = m.group(1), [line]
+        elif cur is not None:
+            if line and not line.startswith(" "):
+                out[cur] = "\n".join(body)
+                cur, body = None, []
+            else:
+                body.append(line)
+    if cur:
+        out[cur] = "\n".join(body)
+    return out
+
+
+def test_patch_adds_only_its_own_lines():
+    """A zero-context diff: every hunk inserts, except the one line of
+    dc.load that now asks dc.load.eng."""
+    minus = [l for l in PATCH.split("\n") if l.startswith("-") and not l.startswith("---")]
+    assert minus == ['-    dc.load.fmt(String.ends_with(path, ".btc"), String.eq(eng, "tree"), path, pinned)'], minus
+    assert "+    dc.load.eng(eng, path, pinned)" in PATCH
+    assert "+  EAna{h: U32, q: U32, dv: Nat, v: U32, x: Array<F32>}" in PATCH
+    assert "+import ./AnaIo.bend as AI" in PATCH
+
+
+def test_patch_effects_are_declared():
+    used = set(re.findall(r"AI\.(ana\.[a-z_]+)\(", PATCH))
+    declared = {d[0] for d in DEFS}
+    assert used and used <= declared, used - declared
+
+
+def _patched():
+    import shutil
+    import subprocess
+    import tempfile
+    if not os.path.exists(REF_DECODE):
+        pytest.skip("the reference tree is not here")
+    d = tempfile.mkdtemp()
+    os.makedirs(os.path.join(d, "bend"))
+    shutil.copy(REF_DECODE, os.path.join(d, "bend", "Decode.bend"))
+    r = subprocess.run(["git", "apply", "--unidiff-zero", PATCH_PATH], cwd=d, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    return open(os.path.join(d, "bend", "Decode.bend")).read()
+
+
+def test_patch_applies_and_every_seam_case_has_its_arm():
+    text = _patched()
+    defs = _defs(text)
+    for fn, calls in SEAM.items():
+        body = defs[fn]
+        assert "case EAna{" in body, fn
+        arm = body[body.index("case EAna{"):]
+        for c in calls:
+            assert c in arm, (fn, c)
+    for fn, calls in HELPERS.items():
+        assert fn in defs, fn
+        for c in calls:
+            assert c in defs[fn], (fn, c)
+    # the engines' other arms are untouched, and dc.load chooses by ANA_DECODER
+    for fn in SEAM:
+        assert "case EDense{" in defs[fn] and "case ETree{" in defs[fn], fn
+    assert 'String.eq(eng, "hip")' in defs["dc.load.eng"]
+    assert "dc.load.eng(eng, path, pinned)" in defs["dc.load"]

@@ -33,9 +33,12 @@ def is_call_len(i, toks):
 
 
 def tool(i, toks):
-    if toks[-1] >= 240:
+    # (keyed on every token written: with a call token, the last one is
+    # always that token)
+    key = sum(toks) % 251
+    if key >= 190:
         return None
-    return [2 + (toks[-1] * 5 + j + i) % 250 for j in range(1 + (i + len(toks)) % 5)]
+    return [2 + (key * 5 + j + i) % 250 for j in range(1 + (i + len(toks)) % 5)]
 
 
 def episodes(vocab):
