@@ -9,9 +9,19 @@
 // its outputs as 8-byte entries (the value's bits, the step's epoch above)
 // with device-coherent stores, and each consumer polls the entries it needs
 // with device-coherent loads until every one carries the epoch it waits
-// for. There is no grid barrier. Each workgroup loads the weights of the
-// phase after the current one into registers before it waits, so the weight
-// stream runs under the exchanges instead of after them.
+// for. There is no grid barrier.
+//
+// Each wave first issues its share of the next phase's weights (1 KB pieces
+// streamed into LDS by global_load_lds), then polls its share of the
+// current phase's inputs. A wave's loads retire in issue order, so its polls
+// return only after its pieces have landed: the first poll then usually
+// finds the inputs already published (polling at once, in waves of their
+// own beside the stream, took a second round trip and ran slower), and when
+// the inputs are in, both buffers are ready. The two 64 KB weight buffers
+// are separate LDS objects and every phase knows at compile time which one
+// it reads and which one its loads fill (a layer is compiled for each
+// starting buffer), so the compiler never holds a read of one buffer behind
+// the loads filling the other.
 //
 // Entries of one (layer, phase) have their own slots, and slots alternate
 // between two sets by the epoch's parity: a producer can only reach step
@@ -25,6 +35,8 @@
 // A step whose logits have no maximum (NaN) stops the launch before its
 // pick; the host picks by Sample.argmax and launches again.
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "ana_internal.h"
 #include "numerics.h"
@@ -41,7 +53,6 @@ constexpr uint32_t kMaxTracePhases = 6 * 32 + 2;       // phases a traced step m
 // the device's constant-rate clock (s_memrealtime: 100 MHz on gfx950)
 __device__ __forceinline__ uint64_t rtc() { return __builtin_amdgcn_s_memrealtime(); }
 
-
 __device__ __forceinline__ void ll_put(unsigned long long* p, float v, uint32_t ep) {
   __hip_atomic_store(p, ((unsigned long long)ep << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
@@ -53,62 +64,52 @@ __device__ __forceinline__ bool aborted(uint32_t* ctl) {
   return __hip_atomic_load(&ctl[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 
-// Poll n entries (entry i at base[map(i)]) until each carries epoch ep
-// (tag(entry) == ep), then dst[i] = the value. PE entries a thread at most.
-// Returns false for the whole workgroup when a wait ran out or the launch
-// was aborted (and raises the abort word).
-template <int PE, class Map, class Tag>
-__device__ bool ll_gather(const unsigned long long* base, uint32_t n, uint32_t ep, Map map, Tag tag, float* dst,
-                          uint32_t* ctl, uint32_t* bad_s, uint64_t tmo) {
-  const uint32_t tid = threadIdx.x;
-  const uint64_t t0 = rtc();
+// s_waitcnt with vmcnt = k (expcnt and lgkmcnt not waited on)
+#define ANA_VM(k) (((k) & 15) | (((k) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+// The workgroup's threads poll n entries (entry i at base[map(i)]; thread t
+// takes i = t + 256 e, e < PE) until each carries epoch ep in its upper
+// half, then dst[i] = the value. False (for this wave) when the wait passed
+// tmo ticks or another workgroup gave up.
+template <int PE, class Map>
+__device__ __forceinline__ bool poll_gather(const unsigned long long* base, uint32_t n, uint32_t ep, Map map, float* dst,
+                                            uint32_t* ctl, uint64_t tmo) {
+  const uint32_t pt = threadIdx.x;
   unsigned long long v[PE];
 #pragma unroll
   for (int e = 0; e < PE; e++) {
-    const uint32_t i = tid + kPT * e;
+    const uint32_t i = pt + kPT * e;
     v[e] = i < n ? ll_ld(base + map(i)) : 0ull;
   }
+  const uint64_t t0 = rtc();
   bool ok = true;
   for (uint32_t it = 1;; it++) {
     bool all = true;
 #pragma unroll
     for (int e = 0; e < PE; e++) {
-      const uint32_t i = tid + kPT * e;
-      if (i < n && tag(v[e]) != ep) {
+      const uint32_t i = pt + kPT * e;
+      if (i < n && (uint32_t)(v[e] >> 32) != ep) {
         all = false;
         v[e] = ll_ld(base + map(i));
       }
     }
-    if (all) break;
-    if ((it & 127) == 0 && (rtc() - t0 > tmo || aborted(ctl))) {
+    if (__all(all)) break;
+    if ((it & 31) == 0 && (rtc() - t0 > tmo || aborted(ctl))) {
       ok = false;
       break;
     }
   }
 #pragma unroll
   for (int e = 0; e < PE; e++) {
-    const uint32_t i = tid + kPT * e;
+    const uint32_t i = pt + kPT * e;
     if (i < n) dst[i] = __uint_as_float((uint32_t)v[e]);
   }
-  if (!ok) *bad_s = 1;
-  __syncthreads();
-  if (*bad_s) {
-    if (tid == 0) {
-      if (!aborted(ctl)) atomicOr(&ctl[0], 1u);   // this workgroup's wait timed out
-      __hip_atomic_store(&ctl[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __builtin_amdgcn_s_waitcnt(0);   // no load into LDS outlives the workgroup
-    return false;
-  }
-  return true;
+  return ok;
 }
 
 struct Ident {
   uint64_t o;
   __device__ uint64_t operator()(uint32_t i) const { return o + i; }
-};
-struct Tag32 {
-  __device__ uint32_t operator()(unsigned long long v) const { return (uint32_t)(v >> 32); }
 };
 
 // block-wide sum of one value per thread (all threads get it)
@@ -126,7 +127,9 @@ __device__ __forceinline__ float dot4(float4 a, float4 b, float acc) {
   acc = fmaf(a.z, b.z, acc);
   return fmaf(a.w, b.w, acc);
 }
-
+__device__ __forceinline__ float4 mul4(float4 a, float4 b) {
+  return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
+}
 
 __device__ __forceinline__ float p_sigmoid(float z) {
   if (0.0f <= z) return 1.0f / (1.0f + expf(-z));
@@ -134,6 +137,14 @@ __device__ __forceinline__ float p_sigmoid(float z) {
   return e / (1.0f + e);
 }
 __device__ __forceinline__ float p_log_sigmoid(float z) { return -(fmaxf(-z, 0.0f) + log1pf(expf(-fabsf(z)))); }
+
+template <int B>
+using IC = std::integral_constant<int, B>;
+
+// the hardware's reciprocal and reciprocal square root (about 1 ulp): the
+// fast mode's norms, gates and sums take them in place of IEEE division
+__device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float rsq(float x) { return __builtin_amdgcn_rsqf(x); }
 
 }  // namespace
 
@@ -145,37 +156,35 @@ typedef __attribute__((address_space(3))) void lds_void;
 // NFD); NFF of a K = f row (f <= 256 NFF). One workgroup of kPT threads
 // (four waves) a CU.
 //
-// A phase's weights (and an attention unit's K and V rows) go from HBM
-// straight into one of two 64 KB LDS buffers (global_load_lds_dwordx4: a
-// wave instruction moves one 1 KB piece, lane l's 16 bytes to byte 16 l),
-// issued at the start of the phase before; the other buffer holds the
-// current phase's. A wave's weight pieces are laid out as it reads them
-// back: (row, k chunk j) at piece (row_i NF + j), lane l's float4 at k =
-// 4 (l + 64 j). Loads retire in issue order, so a phase waits for all of
-// its wave's loads (vmcnt 0) before it reads its buffer: the next phase's
-// pieces, issued before this phase's input polls, have landed by then too.
+// A weight piece is 1 KB: a wave's global_load_lds_dwordx4 moves lane l's
+// 16 bytes to byte 16 l of the piece. A row of K = d is NFD pieces, lane
+// l's float4 of piece j at k = 4 (l + 64 j). Each phase's pieces are
+// numbered 0 .. P - 1 and wave u issues pieces u, u + 4, ....
 //
-// TR: the trace build. Wave 0's first lane stamps four clock readings a
-// phase (the clock's low 32 bits) into LDS (the phase's start; its inputs all seen; its weights
-// landed; its outputs published) and the workgroup copies a step's stamps
-// to a.trace after the pick, for the first a.trace_steps steps.
+// TR: the trace build. Four clock readings a phase (the clock's low 32
+// bits) go into LDS by thread 0: the phase's start; its inputs all seen;
+// all waves met after their waits; its outputs published. The workgroup copies a step's stamps to a.trace
+// after the pick, for the first a.trace_steps steps.
 template <int HD, int NFD, int NFF, bool TR>
 __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   constexpr int QD = HD / 4;            // attention: dims a score lane holds (4 lanes a slot)
   constexpr int C4 = HD / 4;            // float4 columns of a head
   constexpr int GS = kPT / C4;          // attention V lanes: slot groups
   constexpr int KPASS = 2;              // 64 slots a pass: pieces of up to 128 slots
-  constexpr int MAXP = 2;               // gate|up pairs a wave (f <= 8 G)
-  constexpr int HBR = 4;                // head rows a wave a batch
+  constexpr int HBR = 5;                // head rows a wave a batch
   constexpr uint32_t WB = 4096;         // float4s a weight buffer (64 KB)
-  constexpr uint32_t KV_V = KPASS * 64 * C4;   // V's float4 offset in an attention buffer
-  __shared__ __align__(16) float4 wbuf[2][WB];
+  constexpr uint32_t KVQ = KPASS * C4;  // pieces of an attention unit's K (and of its V)
+  constexpr uint32_t KV_V = KVQ * 64;   // V's float4 offset in an attention buffer
+  constexpr int PEX = NFD;              // entries a thread polls of a d vector
+  constexpr int PEF = NFF;              // of an f vector
+  constexpr int PES = 1;                // of up to 256 entries
+  __shared__ __align__(16) float4 wbA[WB];
+  __shared__ __align__(16) float4 wbB[WB];
   __shared__ __align__(16) float xs[256 * NFF];
-  __shared__ float red[8], qv[HD], kvv[HD], vvv[HD], al[HD], kh[HD], es[KPASS * 64], lgs[4][32];
+  __shared__ float red[8], qv[HD], kvv[HD], vvv[HD], es[KPASS * 64], lgs[4][40];
   __shared__ float4 part4[4][C4];
-  __shared__ float o16[4][4][4];
   __shared__ uint32_t bad_s;
-  __shared__ unsigned long long key_s[4];
+  __shared__ unsigned long long key_s[4], pick_s[4];
   __shared__ uint32_t tr_s[TR ? kMaxTracePhases : 1][4];
   uint32_t ph = 0;   // the step's phase (trace)
 #define TS(i)                                       \
@@ -184,16 +193,11 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       if (tid == 0) tr_s[ph][i] = (uint32_t)rtc();  \
     }                                               \
   } while (0)
-#define TS_END()                                    \
-  do {                                              \
-    TS(3);                                          \
-    ph++;                                           \
-  } while (0)
   const uint32_t w = blockIdx.x, G = gridDim.x, tid = threadIdx.x, lane = tid & 63;
   const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // (a scalar: the wave's branches are uniform)
+
   const uint32_t d = a.d, f = a.f, H = a.heads, ctx = a.ctx, L = a.L;
   if (tid == 0) bad_s = 0;
-  __syncthreads();
   const float* W = a.W;
   float* Sseq = a.state + (size_t)a.seq[0] * a.seq_stride;
   uint32_t pos = a.pos[0], tok = a.tok[0];
@@ -203,10 +207,11 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   const uint32_t orow = w * RO + wv;            // this wave's Wo / down row
   const bool orow_ok = wv < RO && orow < d;
   float x_own = 0.0f, xa_own = 0.0f;            // this wave's rows of x and xa
-  const float sc = 1.0f / sqrtf((float)HD);
+  const float sc = 1.0f / sqrtf((float)HD), invd = 1.0f / (float)d;
   const uint32_t np = a.np, PL = (ctx + np - 1) / np;
   const uint32_t v = a.vocab, RH = (v + G - 1) / G, h0 = w * RH, h1 = min(v, h0 + RH);
   const uint32_t nhb = (RH + 4 * HBR - 1) / (4 * HBR);   // head batches (each wave HBR rows a batch)
+  const bool gla_unit = w < H * C4, att_unit = w < H * np;
   // the layer table in LDS: its fields are read there (a global copy would
   // be re-read after every store the compiler cannot tell apart from it)
   __shared__ PLayer lays[kMaxPLayers];
@@ -215,84 +220,84 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   __syncthreads();
   const PLayer* Ls = lays;
   auto zero4 = []() { return make_float4(0.f, 0.f, 0.f, 0.f); };
-  auto piece = [&](const float* src, uint32_t buf, uint32_t at) {
-    // one 1 KB piece: lane l's 16 bytes from src (this lane's address) to
-    // float4 at * 64 + l of the buffer
-    __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)&wbuf[buf][at * 64], 16, 0, 0);
+  // the buffer of parity B
+  auto bufp = [&](auto B) -> float4* {
+    if constexpr (decltype(B)::value) return wbB;
+    else return wbA;
   };
-  // ---- the pieces of each phase (this wave's)
+  // one 1 KB piece: lane l's 16 bytes from src (this lane's address) to
+  // float4 at * 64 + l of the buffer
+  auto piece = [&](const float* src, float4* buf, uint32_t at) {
+    __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)&buf[at * 64], 16, 0, 0);
+  };
+  // ---- the pieces of each phase (issued by the loading waves)
   auto qkv_rows = [&](const PLayer& P) { return P.gla ? 4 * d : 3 * d; };
-  auto dma_qkv = [&](const PLayer& P, uint32_t buf) {
-    const uint32_t R = qkv_rows(P), RQ = (R + G - 1) / G;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t r = w * RQ + wv + 4 * i;
-      if ((uint32_t)(wv + 4 * i) < RQ && r < R) {
-        const float* row = W + (r < 3 * d ? P.wq + (size_t)r * d : P.wa + (size_t)(r - 3 * d) * d);
-#pragma unroll
-        for (int j = 0; j < NFD; j++) {
-          const uint32_t k = 4 * (lane + 64 * j);
-          piece(row + (k < d ? k : 0), buf, (wv * 4 + i) * NFD + j);
-        }
-      }
-    }
-  };
-  auto dma_wo = [&](const PLayer& P, uint32_t buf) {
-    if (!orow_ok) return;
-    const float* row = W + P.wo + (size_t)orow * d;
-#pragma unroll
-    for (int j = 0; j < NFD; j++) {
+  auto dma_qkv = [&](const PLayer& P, float4* buf) {
+    const uint32_t R = qkv_rows(P), RQ = (R + G - 1) / G, NP = RQ * NFD;
+    for (uint32_t q = wv; q < NP; q += 4) {
+      const uint32_t i = q / NFD, j = q % NFD, r = min(w * RQ + i, R - 1);
+      const float* row = W + (r < 3 * d ? P.wq + (size_t)r * d : P.wa + (size_t)(r - 3 * d) * d);
       const uint32_t k = 4 * (lane + 64 * j);
-      piece(row + (k < d ? k : 0), buf, wv * NFD + j);
-    }
-  };
-  auto dma_gu = [&](const PLayer& P, uint32_t buf) {
-#pragma unroll
-    for (int i = 0; i < MAXP; i++) {
-      const uint32_t jp = w * RGp + wv + 4 * i;
-      if ((uint32_t)(wv + 4 * i) < RGp && jp < f) {
-        const float* g = W + P.wg + (size_t)jp * d;
-        const float* u = g + (size_t)f * d;
-#pragma unroll
-        for (int j = 0; j < NFD; j++) {
-          const uint32_t k = 4 * (lane + 64 * j), kk = k < d ? k : 0;
-          piece(g + kk, buf, ((wv * MAXP + i) * 2 + 0) * NFD + j);
-          piece(u + kk, buf, ((wv * MAXP + i) * 2 + 1) * NFD + j);
-        }
-      }
-    }
-  };
-  auto dma_wd = [&](const PLayer& P, uint32_t buf) {
-    if (!orow_ok) return;
-    const float* row = W + P.wd + (size_t)orow * f;
-#pragma unroll
-    for (int j = 0; j < NFF; j++) {
-      const uint32_t k = 4 * (lane + 64 * j);
-      piece(row + (k < f ? k : 0), buf, wv * NFF + j);
+      piece(row + (k < d ? k : 0), buf, q);
     }
   };
   // an attention unit's K rows then V rows of its piece of the ring: slot i
   // of the piece at float4 i C4 .. (V from KV_V); slots past the ring or the
   // piece read slot t0 (never used)
-  auto dma_kv = [&](const PLayer& P, uint32_t buf) {
-    if (P.gla || w >= H * np) return;
+  auto dma_kv = [&](const PLayer& P, float4* buf) {
+    if (P.gla || !att_unit) return;
     const uint32_t h = w / np, t0 = (w % np) * PL;
     const float* Kr = Sseq + P.soff;
     const float* Vr = Kr + (size_t)ctx * d;
-    const uint32_t nq = KPASS * 64 * C4 / 64;   // pieces of K (and of V)
-    for (uint32_t q = wv; q < nq; q += 4) {
-      const uint32_t i = q * (64 / C4) + lane / C4, t = t0 + i;
+    for (uint32_t q = wv; q < 2 * KVQ; q += 4) {
+      const uint32_t qq = q < KVQ ? q : q - KVQ;
+      const uint32_t i = qq * (64 / C4) + lane / C4, t = t0 + i;
       const uint32_t tt = (i < PL && t < ctx) ? t : t0;
       const size_t off = (size_t)tt * d + h * HD + 4 * (lane % C4);
-      piece(Kr + off, buf, q);
-      piece(Vr + off, buf, KV_V / 64 + q);
+      piece((q < KVQ ? Kr : Vr) + off, buf, q);
     }
   };
-  auto dma_head = [&](uint32_t batch, uint32_t buf) {
+  auto dma_wo = [&](const PLayer& P, float4* buf) {
+    const uint32_t NP = RO * NFD;
+    for (uint32_t q = wv; q < NP; q += 4) {
+      const uint32_t i = q / NFD, j = q % NFD, r = min(w * RO + i, d - 1);
+      const uint32_t k = 4 * (lane + 64 * j);
+      piece(W + P.wo + (size_t)r * d + (k < d ? k : 0), buf, q);
+    }
+  };
+  auto dma_gu = [&](const PLayer& P, float4* buf) {
+    const uint32_t NP = RGp * 2 * NFD;
+    for (uint32_t q = wv; q < NP; q += 4) {
+      const uint32_t pi = q / (2 * NFD), gu = (q / NFD) & 1, j = q % NFD, jp = min(w * RGp + pi, f - 1);
+      const uint32_t k = 4 * (lane + 64 * j);
+      piece(W + P.wg + (gu ? (size_t)f * d : 0) + (size_t)jp * d + (k < d ? k : 0), buf, q);
+    }
+  };
+  auto dma_wd = [&](const PLayer& P, float4* buf) {
+    const uint32_t NP = RO * NFF;
+    for (uint32_t q = wv; q < NP; q += 4) {
+      const uint32_t i = q / NFF, j = q % NFF, r = min(w * RO + i, d - 1);
+      const uint32_t k = 4 * (lane + 64 * j);
+      piece(W + P.wd + (size_t)r * f + (k < f ? k : 0), buf, q);
+    }
+  };
+  // the head's rows of batch b for wave u: h0 + u + 4 (b HBR + i), at
+  // pieces (u HBR + i) NFD + j (row 0 stands in past h1; its result is not
+  // used). Batch 0 of every wave, by the loading waves:
+  auto dma_head0 = [&](float4* buf) {
+    const uint32_t NP = 4 * HBR * NFD;
+    for (uint32_t q = wv; q < NP; q += 4) {
+      const uint32_t rl = q / NFD, j = q % NFD, u = rl / HBR, i = rl % HBR;
+      const uint32_t r = h0 + u + 4 * i, rr = r < h1 ? r : 0u;
+      const uint32_t k = 4 * (lane + 64 * j);
+      piece(W + (size_t)rr * d + (k < d ? k : 0), buf, q);
+    }
+  };
+  // ... and batch b of this wave's own rows, by the wave itself
+  auto dma_head_own = [&](uint32_t b, float4* buf) {
 #pragma unroll
     for (int i = 0; i < HBR; i++) {
-      const uint32_t r = h0 + wv + 4 * (batch * HBR + i);
-      const uint32_t rr = r < h1 ? r : 0u;   // (row 0 stands in; its result is not used)
+      const uint32_t r = h0 + wv + 4 * (b * HBR + i), rr = r < h1 ? r : 0u;
 #pragma unroll
       for (int j = 0; j < NFD; j++) {
         const uint32_t k = 4 * (lane + 64 * j);
@@ -300,40 +305,32 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       }
     }
   };
-  auto wb4 = [&](uint32_t buf, uint32_t at) { return wbuf[buf][at * 64 + lane]; };
-  auto land = [&]() {
-    __builtin_amdgcn_s_waitcnt(0);   // every load of this wave retired (LDS written)
-    __syncthreads();
-  };
-  // xs[0..n) times the RMSNorm scale and the gains at gain[] (thread tid owns
-  // entries tid + 256 e)
-  auto norm_xs = [&](uint32_t n, const float (&g)[4]) {
-    float ss = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const uint32_t i = tid + kPT * e;
-      if (i < n) ss += xs[i] * xs[i];
-    }
-    ss = block_sum(ss, red);
-    const float rs = 1.0f / sqrtf(ss / (float)n + 1.0e-5f);
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const uint32_t i = tid + kPT * e;
-      if (i < n) xs[i] = (xs[i] * rs) * g[e];
-    }
-    __syncthreads();
-  };
-  auto load_gain = [&](float (&g)[4], uint64_t off) {
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const uint32_t i = tid + kPT * e;
-      g[e] = i < d ? W[off + i] : 0.0f;
-    }
-  };
   // this lane's float4 j of xs[0..n) (zero past n)
   auto xs4 = [&](uint32_t j, uint32_t n) {
     const uint32_t k = 4 * (lane + 64 * j);
     return k < n ? *reinterpret_cast<const float4*>(&xs[k]) : zero4();
+  };
+  // this lane's float4s of a gain vector at W + off (d entries)
+  auto load_g4 = [&](float4 (&g)[NFD], uint64_t off) {
+#pragma unroll
+    for (int j = 0; j < NFD; j++) {
+      const uint32_t k = 4 * (lane + 64 * j);
+      g[j] = k < d ? *reinterpret_cast<const float4*>(W + off + k) : zero4();
+    }
+  };
+  // the RMSNorm of xs[0..d) folded into the products: xg = x g (this
+  // lane's float4s), and the scale 1 / sqrt(mean(x^2) + 1e-5), which every
+  // wave forms from the whole row itself
+  auto norm_fold = [&](const float4 (&g)[NFD], float4 (&xg)[NFD]) -> float {
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NFD; j++) {
+      const float4 x = xs4(j, d);
+      ss = dot4(x, x, ss);
+      xg[j] = mul4(x, g[j]);
+    }
+    ss = wsum(ss);
+    return rsq(ss * invd + 1.0e-5f);
   };
   auto fail_wg = [&]() {
     if (tid == 0) {
@@ -341,74 +338,102 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       __hip_atomic_store(&a.ctl[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   };
+  // the meeting after the polls: the phase's inputs are in xs and its
+  // pieces in LDS (each wave's polls retired after its pieces). False
+  // (every wave) when a wait failed.
+  auto meet = [&]() -> bool {
+    __syncthreads();
+    TS(2);
+    if (bad_s) {
+      fail_wg();
+      __builtin_amdgcn_s_waitcnt(0);   // no load into LDS outlives the workgroup
+      return false;
+    }
+    return true;
+  };
+  // a wave's poll verdict, before the meeting
+  auto gathered = [&](bool ok) {
+    if (!ok && lane == 0) bad_s = 1;
+    if constexpr (TR) {
+      if (tid == 0) tr_s[ph][1] = (uint32_t)rtc();
+    }
+  };
+  auto pub = [&]() {
+    TS(3);
+    ph++;
+  };
 
-  uint32_t pb = 0;          // the buffer holding the current phase's pieces
-  dma_qkv(Ls[0], pb);
-  uint32_t k = 0;
-  bool nan_stop = false;
-  for (; k < a.steps; k++) {
-    const uint32_t ep = a.epoch0 + k + 1;
-    unsigned long long* LL = a.ll + (size_t)(ep & 1) * a.ll_par;
-    ph = 0;
-    // layer 0's residual input is the token's embedding row
-    if (orow_ok) x_own = W[(size_t)tok * d + orow];
-    for (uint32_t l = 0; l < L; l++) {
-      const PLayer P = Ls[l];
-      float gra[4], grf[4];
-      float svr = 0.0f, lamr = 0.0f, gqr = 0.0f, gkr = 0.0f, sinkr = 0.0f;
-      // ---- norm, then q|k|v (|z): rows w RQ .. w RQ + RQ - 1
-      __syncthreads();
-      TS(0);
-      dma_kv(P, pb ^ 1);
-      load_gain(gra, P.ra);
-      // the mix's own inputs that do not depend on this token
-      if (P.gla) {
-        if (w < H * C4) {
-          const uint32_t h = w / C4, cb = w % C4, ar = tid >> 2, c = tid & 3;
-          if ((int)ar < HD) svr = Sseq[P.soff + (size_t)h * HD * HD + (size_t)ar * HD + 4 * cb + c];
-          if (a.rglru && (int)tid < HD) lamr = W[P.lam + h * HD + tid];
-        }
-      } else {
-        if (a.qk && w < H * np && (int)tid < HD) {
-          gqr = W[P.gq + tid];
-          gkr = W[P.gk + tid];
-        }
-        if (a.sinks && w < H * C4) sinkr = W[P.sink + w / C4];
+  // one layer, compiled for the buffer parity its first phase reads (B);
+  // false when a wait failed
+  auto layer = [&](auto B, uint32_t l, uint32_t ep, unsigned long long* LL) -> bool {
+    constexpr int PB = decltype(B)::value;
+    float4* bufB = bufp(IC<PB>{});
+    float4* bufN = bufp(IC<1 - PB>{});
+    const PLayer P = Ls[l];
+    // ---- norm, then q|k|v (|z) (in bufB): rows w RQ .. w RQ + RQ - 1,
+    // wave wv the rows wv + 4 i
+    __syncthreads();
+    TS(0);
+    float4 g4[NFD];
+    load_g4(g4, P.ra);
+    float svr = 0.0f, lamr = 0.0f, gqr = 0.0f, gkr = 0.0f, sinkr = 0.0f;
+    // the mix's own inputs that do not depend on this token: GLA column
+    // 4 cb + wv of head h (lane a: row a of S) and the RG-LRU lambdas; the
+    // attention's qk gains and sink
+    if (P.gla) {
+      if (gla_unit && (int)lane < HD) {
+        const uint32_t h = w / C4, cb = w % C4;
+        svr = Sseq[P.soff + (size_t)h * HD * HD + (size_t)lane * HD + 4 * cb + wv];
+        if (a.rglru) lamr = W[P.lam + h * HD + lane];
       }
+    } else {
+      if (a.qk && att_unit && (int)tid < HD) {
+        gqr = W[P.gq + tid];
+        gkr = W[P.gk + tid];
+      }
+      if (a.sinks && gla_unit) sinkr = W[P.sink + w / C4];
+    }
+    if (l == 0 && orow_ok) x_own = W[(size_t)tok * d + orow];
+    dma_kv(P, bufN);
+    {
+      bool ok = true;
       if (l == 0) {
+        // layer 0's input is the token's embedding row
         for (uint32_t i = tid; i < d; i += kPT) xs[i] = W[(size_t)tok * d + i];
-      } else if (!ll_gather<4>(LL, d, ep, Ident{Ls[l - 1].e_x}, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) {
-        return;
+      } else {
+        ok = poll_gather<PEX>(LL, d, ep, Ident{Ls[l - 1].e_x}, xs, a.ctl, a.tmo);
       }
-      TS(1);
-      land();
-      TS(2);
-      norm_xs(d, gra);
+      gathered(ok);
+    }
+    if (!meet()) return false;
+    {
+      float4 xg[NFD];
+      const float rs = norm_fold(g4, xg);
+      const uint32_t R = qkv_rows(P), RQ = (R + G - 1) / G;
+      float res[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; kk++) {
+        const uint32_t i = min(wv + 4 * kk, RQ - 1);
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NFD; j++) acc = dot4(bufB[(i * NFD + j) * 64 + lane], xg[j], acc);
+        res[kk] = wsum(acc) * rs;
+      }
+      if (lane < 4) {
+        const uint32_t i = wv + 4 * lane, r = w * RQ + i;
+        const float val = lane == 0 ? res[0] : lane == 1 ? res[1] : lane == 2 ? res[2] : res[3];
+        if (i < RQ && r < R) ll_put(LL + P.e_qkv + r, val, ep);
+      }
+    }
+    pub();
+    // ---- the mix (an attention unit's K and V pieces in bufN)
+    __syncthreads();
+    TS(0);
+    dma_wo(P, bufB);
+    if (P.gla) {
       {
-        float4 xr[NFD];
-#pragma unroll
-        for (int j = 0; j < NFD; j++) xr[j] = xs4(j, d);
-        const uint32_t R = qkv_rows(P), RQ = (R + G - 1) / G;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const uint32_t r = w * RQ + wv + 4 * i;
-          if ((uint32_t)(wv + 4 * i) < RQ && r < R) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int j = 0; j < NFD; j++) acc = dot4(wb4(pb, (wv * 4 + i) * NFD + j), xr[j], acc);
-            acc = wsum(acc);
-            if (lane == 0) ll_put(LL + P.e_qkv + r, acc, ep);
-          }
-        }
-      }
-      TS_END();
-      pb ^= 1;
-      // ---- the mix (pieces: an attention unit's K and V, in pb)
-      __syncthreads();
-      TS(0);
-      dma_wo(P, pb ^ 1);
-      if (P.gla) {
-        if (w < H * C4) {
+        bool ok = true;
+        if (gla_unit) {
           const uint32_t h = w / C4, cb = w % C4;
           // q, k, z of head h, then v's four columns of this block
           const uint64_t base = P.e_qkv;
@@ -418,170 +443,158 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
             if (i < 3u * HD) return base + 3 * d + h * HD + (i - 2 * HD);
             return base + 2 * d + h * HD + 4 * cb + (i - 3 * HD);
           };
-          if (!ll_gather<1>(LL, 3 * HD + 4, ep, map, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) return;
-          TS(1);
-          TS(2);
-          const uint32_t ar = tid >> 2, c = tid & 3;
-          const float q = (int)tid < HD ? xs[tid] : 0.0f, kk = (int)tid < HD ? xs[HD + tid] : 0.0f;
-          const float q2 = block_sum(q * q, red);
-          const float k2 = block_sum(kk * kk, red);
-          if ((int)tid < HD) {
-            qv[tid] = q / sqrtf(1.0e-6f + q2);
-            const float kn = kk / sqrtf(1.0e-6f + k2);
-            const float z = xs[2 * HD + tid];
-            if (a.rglru) {
-              // dd.gate's RG-LRU arm (bend/Dense/Ex.bend:158-162), in float
-              const float la = fminf(ANA_CAP, (8.0f * p_sigmoid(z)) * p_log_sigmoid(lamr));
-              kh[tid] = kn * sqrtf(1.0f - expf(2.0f * la));
-              al[tid] = expf(la);
-            } else {
-              al[tid] = p_sigmoid(z);
-              kh[tid] = kn;
-            }
-          }
-          __syncthreads();
-          float o = 0.0f;
-          if ((int)ar < HD) {
-            const float s = fmaf(al[ar], svr, kh[ar] * xs[3 * HD + c]);
-            Sseq[P.soff + (size_t)h * HD * HD + (size_t)ar * HD + 4 * cb + c] = s;
-            o = qv[ar] * s;
-          }
-          // over the rows: lanes of one column (lane & 3) in a row of 16 by
-          // rotations of 4 and 8, then the wave's four rows and the four
-          // waves through LDS
-          o += dpp<0x124>(o);   // row_ror:4
-          o += dpp<0x128>(o);   // row_ror:8
-          if ((lane & 15) < 4) o16[wv][lane >> 4][lane & 3] = o;
-          __syncthreads();
-          if (tid < 4) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 16; q++) acc += o16[q >> 2][q & 3][tid];
-            ll_put(LL + P.e_o + h * HD + 4 * cb + tid, acc, ep);
-          }
-        } else {
-          TS(1);
-          TS(2);
+          ok = poll_gather<PES>(LL, 3 * HD + 4, ep, map, xs, a.ctl, a.tmo);
         }
-        TS_END();
-        land();
-      } else {
-        const uint32_t npos = pos < ctx - 1 ? pos : ctx - 1, slot = pos % ctx;
-        if (w < H * np) {
-          const uint32_t h = w / np, p = w % np, t0 = p * PL;
+        gathered(ok);
+      }
+      if (!meet()) return false;
+      if (gla_unit) {
+        // wave wv: column c = 4 cb + wv of head h's state, lane a its row a
+        const uint32_t h = w / C4, cb = w % C4, c = 4 * cb + wv;
+        const bool on = (int)lane < HD;
+        const float qa = on ? xs[lane] : 0.0f, ka = on ? xs[HD + lane] : 0.0f;
+        const float q2 = wsum(qa * qa), k2 = wsum(ka * ka);
+        const float qn = qa * rsq(1.0e-6f + q2), kn = ka * rsq(1.0e-6f + k2);
+        const float z = on ? xs[2 * HD + lane] : 0.0f, vc = xs[3 * HD + wv];
+        float al, kh;
+        if (a.rglru) {
+          // dd.gate's RG-LRU arm (bend/Dense/Ex.bend:158-162), in float
+          const float la = fminf(ANA_CAP, (8.0f * p_sigmoid(z)) * p_log_sigmoid(lamr));
+          kh = kn * sqrtf(1.0f - expf(2.0f * la));
+          al = expf(la);
+        } else {
+          al = p_sigmoid(z);
+          kh = kn;
+        }
+        const float s = fmaf(al, svr, kh * vc);
+        if (on) Sseq[P.soff + (size_t)h * HD * HD + (size_t)lane * HD + c] = s;
+        const float o = wsum(on ? qn * s : 0.0f);
+        if (lane == 0) ll_put(LL + P.e_o + h * HD + c, o, ep);
+      }
+      pub();
+    } else {
+      const uint32_t npos = pos < ctx - 1 ? pos : ctx - 1, slot = pos % ctx;
+      {
+        bool ok = true;
+        if (att_unit) {
+          const uint32_t h = w / np;
           const uint64_t base = P.e_qkv;
           auto map = [&](uint32_t i) -> uint64_t {
             if (i < (uint32_t)HD) return base + h * HD + i;
             if (i < 2u * HD) return base + d + h * HD + (i - HD);
             return base + 2 * d + h * HD + (i - 2 * HD);
           };
-          if (!ll_gather<1>(LL, 3 * HD, ep, map, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) return;
-          TS(1);
-          land();
-          TS(2);
-          float q = (int)tid < HD ? xs[tid] : 0.0f, kx = (int)tid < HD ? xs[HD + tid] : 0.0f;
-          if (a.qk) {
-            // M.qkn (bend/Dense/Model.bend:39-42): gains 1 + g
-            const float q2 = block_sum(q * q, red), k2 = block_sum(kx * kx, red);
-            q = (q * (1.0f / sqrtf(q2 / (float)HD + 1.0e-5f))) * (1.0f + gqr);
-            kx = (kx * (1.0f / sqrtf(k2 / (float)HD + 1.0e-5f))) * (1.0f + gkr);
-          }
-          if ((int)tid < HD) {
-            qv[tid] = q;
-            kvv[tid] = kx;
-            vvv[tid] = xs[2 * HD + tid];
-          }
-          __syncthreads();
-          // dd.sm.write: the piece holding this step's slot writes k and v
-          if (slot >= t0 && slot < t0 + PL && (int)tid < HD) {
-            float* Kr = Sseq + P.soff;
-            Kr[(size_t)slot * d + h * HD + tid] = kvv[tid];
-            Kr[(size_t)ctx * d + (size_t)slot * d + h * HD + tid] = vvv[tid];
-          }
-          // scores, 4 lanes a slot; the step's own slot from kvv
-          float mloc = -INFINITY;
-#pragma unroll
-          for (int ps = 0; ps < KPASS; ps++) {
-            const uint32_t i = (tid >> 2) + 64 * ps, t = t0 + i, qq = tid & 3;
-            float acc = 0.0f;
-            if (t == slot) {
-#pragma unroll
-              for (int c = 0; c < QD; c++) acc = fmaf(qv[qq * QD + c], kvv[qq * QD + c], acc);
-            } else {
-#pragma unroll
-              for (int u = 0; u < QD / 4; u++) {
-                const float4 k4 = wbuf[pb][i * C4 + qq * (QD / 4) + u];
-                const uint32_t c = qq * QD + 4 * u;
-                acc = fmaf(qv[c], k4.x, acc);
-                acc = fmaf(qv[c + 1], k4.y, acc);
-                acc = fmaf(qv[c + 2], k4.z, acc);
-                acc = fmaf(qv[c + 3], k4.w, acc);
-              }
-            }
-            acc += dpp<0xB1>(acc);
-            acc += dpp<0x4E>(acc);
-            const bool live = i < PL && t <= npos;
-            const float y = live ? sc * acc : -INFINITY;
-            if ((tid & 3) == 0) es[i] = y;
-            mloc = fmaxf(mloc, y);
-          }
-          mloc = wmax(mloc);
-          if (lane == 0) red[4 + wv] = mloc;
-          __syncthreads();
-          const float m = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
-          float e = 0.0f;
-          if (tid < KPASS * 64) {
-            const float y = es[tid];
-            e = y == -INFINITY ? 0.0f : __expf(y - m);
-          }
-          const float lsum = block_sum(e, red);   // (its first barrier orders the reads of es above)
-          if (tid < KPASS * 64) es[tid] = e;
-          __syncthreads();
-          // o over the piece: thread (c4, g) takes slots g, g + GS, ...
-          const uint32_t c4 = tid % C4, g = tid / C4;
-          float4 o = zero4();
-          for (uint32_t i = g; i < PL && i < KPASS * 64; i += GS) {
-            float4 v4 = wbuf[pb][KV_V + i * C4 + c4];
-            if (t0 + i == slot) v4 = make_float4(vvv[4 * c4], vvv[4 * c4 + 1], vvv[4 * c4 + 2], vvv[4 * c4 + 3]);
-            const float ev = es[i];
-            o.x = fmaf(ev, v4.x, o.x);
-            o.y = fmaf(ev, v4.y, o.y);
-            o.z = fmaf(ev, v4.z, o.z);
-            o.w = fmaf(ev, v4.w, o.w);
-          }
-#pragma unroll
-          for (int s2 = C4; s2 < 64; s2 <<= 1) {
-            o.x += __shfl_xor(o.x, s2, 64);
-            o.y += __shfl_xor(o.y, s2, 64);
-            o.z += __shfl_xor(o.z, s2, 64);
-            o.w += __shfl_xor(o.w, s2, 64);
-          }
-          if (lane < (uint32_t)C4) part4[wv][lane] = o;
-          __syncthreads();
-          unsigned long long* out = LL + P.e_part + (size_t)(h * np + p) * (HD + 2);
-          if ((int)tid < HD) {
-            const uint32_t c = tid / 4, e4 = tid % 4;
-            float s2 = 0.0f;
-#pragma unroll
-            for (int q4 = 0; q4 < 4; q4++) {
-              const float4 p4 = part4[q4][c];
-              s2 += e4 == 0 ? p4.x : e4 == 1 ? p4.y : e4 == 2 ? p4.z : p4.w;
-            }
-            ll_put(out + 2 + tid, s2, ep);
-          }
-          if (tid == 0) {
-            ll_put(out, m, ep);
-            ll_put(out + 1, lsum, ep);
-          }
-        } else {
-          TS(1);
-          land();
-          TS(2);
+          ok = poll_gather<PES>(LL, 3 * HD, ep, map, xs, a.ctl, a.tmo);
         }
-        TS_END();
-        TS(0);
-        // ---- the pieces and the sink combined: o of head h, columns 4 cb ..
-        if (w < H * C4) {
+        gathered(ok);
+      }
+      if (!meet()) return false;
+      if (att_unit) {
+        const uint32_t h = w / np, p = w % np, t0 = p * PL;
+        float q = (int)tid < HD ? xs[tid] : 0.0f, kx = (int)tid < HD ? xs[HD + tid] : 0.0f;
+        if (a.qk) {
+          // M.qkn (bend/Dense/Model.bend:39-42): gains 1 + g (wave 0 holds
+          // the head's dims)
+          const float q2 = wsum(q * q), k2 = wsum(kx * kx);
+          q = (q * rsq(q2 * (1.0f / HD) + 1.0e-5f)) * (1.0f + gqr);
+          kx = (kx * rsq(k2 * (1.0f / HD) + 1.0e-5f)) * (1.0f + gkr);
+        }
+        if ((int)tid < HD) {
+          qv[tid] = q;
+          kvv[tid] = kx;
+          vvv[tid] = xs[2 * HD + tid];
+        }
+        __syncthreads();
+        // dd.sm.write: the piece holding this step's slot writes k and v
+        if (slot >= t0 && slot < t0 + PL && (int)tid < HD) {
+          float* Kr = Sseq + P.soff;
+          Kr[(size_t)slot * d + h * HD + tid] = kvv[tid];
+          Kr[(size_t)ctx * d + (size_t)slot * d + h * HD + tid] = vvv[tid];
+        }
+        // scores, 4 lanes a slot; the step's own slot from kvv
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int ps = 0; ps < KPASS; ps++) {
+          const uint32_t i = (tid >> 2) + 64 * ps, t = t0 + i, qq = tid & 3;
+          float acc = 0.0f;
+          if (t == slot) {
+#pragma unroll
+            for (int c = 0; c < QD; c++) acc = fmaf(qv[qq * QD + c], kvv[qq * QD + c], acc);
+          } else {
+#pragma unroll
+            for (int u = 0; u < QD / 4; u++) {
+              const float4 k4 = bufN[i * C4 + qq * (QD / 4) + u];
+              const uint32_t c = qq * QD + 4 * u;
+              acc = fmaf(qv[c], k4.x, acc);
+              acc = fmaf(qv[c + 1], k4.y, acc);
+              acc = fmaf(qv[c + 2], k4.z, acc);
+              acc = fmaf(qv[c + 3], k4.w, acc);
+            }
+          }
+          acc += dpp<0xB1>(acc);
+          acc += dpp<0x4E>(acc);
+          const bool live = i < PL && t <= npos;
+          const float y = live ? sc * acc : -INFINITY;
+          if ((tid & 3) == 0) es[i] = y;
+          mloc = fmaxf(mloc, y);
+        }
+        mloc = wmax(mloc);
+        if (lane == 0) red[4 + wv] = mloc;
+        __syncthreads();
+        const float m = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
+        float e = 0.0f;
+        if (tid < KPASS * 64) {
+          const float y = es[tid];
+          e = y == -INFINITY ? 0.0f : __expf(y - m);
+        }
+        const float lsum = block_sum(e, red);   // (its first barrier orders the reads of es above)
+        if (tid < KPASS * 64) es[tid] = e;
+        __syncthreads();
+        // o over the piece: thread (c4, g) takes slots g, g + GS, ...
+        const uint32_t c4 = tid % C4, g = tid / C4;
+        float4 o = zero4();
+        for (uint32_t i = g; i < PL && i < KPASS * 64; i += GS) {
+          float4 v4 = bufN[KV_V + i * C4 + c4];
+          if (t0 + i == slot) v4 = make_float4(vvv[4 * c4], vvv[4 * c4 + 1], vvv[4 * c4 + 2], vvv[4 * c4 + 3]);
+          const float ev = es[i];
+          o.x = fmaf(ev, v4.x, o.x);
+          o.y = fmaf(ev, v4.y, o.y);
+          o.z = fmaf(ev, v4.z, o.z);
+          o.w = fmaf(ev, v4.w, o.w);
+        }
+#pragma unroll
+        for (int s2 = C4; s2 < 64; s2 <<= 1) {
+          o.x += __shfl_xor(o.x, s2, 64);
+          o.y += __shfl_xor(o.y, s2, 64);
+          o.z += __shfl_xor(o.z, s2, 64);
+          o.w += __shfl_xor(o.w, s2, 64);
+        }
+        if (lane < (uint32_t)C4) part4[wv][lane] = o;
+        __syncthreads();
+        unsigned long long* out = LL + P.e_part + (size_t)(h * np + p) * (HD + 2);
+        if ((int)tid < HD) {
+          const uint32_t c = tid / 4, e4 = tid % 4;
+          float s2 = 0.0f;
+#pragma unroll
+          for (int q4 = 0; q4 < 4; q4++) {
+            const float4 p4 = part4[q4][c];
+            s2 += e4 == 0 ? p4.x : e4 == 1 ? p4.y : e4 == 2 ? p4.z : p4.w;
+          }
+          ll_put(out + 2 + tid, s2, ep);
+        }
+        if (tid == 0) {
+          ll_put(out, m, ep);
+          ll_put(out + 1, lsum, ep);
+        }
+      }
+      pub();
+      // ---- the pieces and the sink combined: o of head h, columns 4 cb ..
+      // (no loads of its own: the Wo pieces stay in flight)
+      __syncthreads();
+      TS(0);
+      {
+        bool ok = true;
+        if (gla_unit) {
           const uint32_t h = w / C4, cb = w % C4;
           const uint64_t base = P.e_part + (uint64_t)h * np * (HD + 2);
           // entries: np maxima, np sums, then np x 4 columns
@@ -591,220 +604,260 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
             const uint32_t j = i - 2 * np;
             return base + (uint64_t)(j / 4) * (HD + 2) + 2 + 4 * cb + (j % 4);
           };
-          if (!ll_gather<1>(LL, 6 * np, ep, map, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) return;
-          TS(1);
-          TS(2);
-          if (tid < 4) {
-            float M = -INFINITY;
-            for (uint32_t i = 0; i < np; i++) M = fmaxf(M, xs[i]);
-            if (a.sinks) M = fmaxf(M, sinkr);
-            float den = 0.0f, acc = 0.0f;
-            for (uint32_t i = 0; i < np; i++) {
-              const float mi = xs[i];
-              const float wgt = mi == -INFINITY ? 0.0f : __expf(mi - M);
-              den = fmaf(xs[np + i], wgt, den);
-              acc = fmaf(xs[2 * np + 4 * i + tid], wgt, acc);
-            }
-            if (a.sinks) den += __expf(sinkr - M);
-            ll_put(LL + P.e_o + h * HD + 4 * cb + tid, acc / den, ep);
-          }
-        } else {
-          TS(1);
-          TS(2);
+          ok = poll_gather<PES>(LL, 6 * np, ep, map, xs, a.ctl, a.tmo);
         }
-        TS_END();
+        gathered(ok);
       }
-      pb ^= 1;
-      // ---- xa = x + Wo o
-      __syncthreads();
-      TS(0);
-      dma_gu(P, pb ^ 1);
-      load_gain(grf, P.rf);
-      if (!ll_gather<4>(LL, d, ep, Ident{P.e_o}, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) return;
-      TS(1);
-      land();
-      TS(2);
-      {
-        float acc = 0.0f;
-        if (orow_ok) {
+      if (!meet()) return false;
+      if (gla_unit && wv == 0) {
+        // lane i: piece i (np <= 64)
+        const uint32_t h = w / C4, cb = w % C4;
+        const bool on = lane < np;
+        const float mi = on ? xs[lane] : -INFINITY;
+        float M = wmax(mi);
+        if (a.sinks) M = fmaxf(M, sinkr);
+        const float wgt = on && mi != -INFINITY ? __expf(mi - M) : 0.0f;
+        float den = wsum(on ? xs[np + lane] * wgt : 0.0f);
+        if (a.sinks) den += __expf(sinkr - M);
+        float acc[4];
 #pragma unroll
-          for (int j = 0; j < NFD; j++) acc = dot4(wb4(pb, wv * NFD + j), xs4(j, d), acc);
-        }
-        acc = wsum(acc);
-        xa_own = x_own + acc;
-        if (lane == 0 && orow_ok) ll_put(LL + P.e_xa + orow, xa_own, ep);
-      }
-      TS_END();
-      pb ^= 1;
-      // ---- hh = silu(g) u on norm(xa)
-      __syncthreads();
-      TS(0);
-      dma_wd(P, pb ^ 1);
-      if (!ll_gather<4>(LL, d, ep, Ident{P.e_xa}, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) return;
-      TS(1);
-      land();
-      TS(2);
-      norm_xs(d, grf);
-      {
-        float4 xr[NFD];
-#pragma unroll
-        for (int j = 0; j < NFD; j++) xr[j] = xs4(j, d);
-#pragma unroll
-        for (int i = 0; i < MAXP; i++) {
-          const uint32_t jp = w * RGp + wv + 4 * i;
-          if ((uint32_t)(wv + 4 * i) < RGp && jp < f) {
-            float g = 0.0f, u = 0.0f;
-#pragma unroll
-            for (int j = 0; j < NFD; j++) {
-              g = dot4(wb4(pb, ((wv * MAXP + i) * 2 + 0) * NFD + j), xr[j], g);
-              u = dot4(wb4(pb, ((wv * MAXP + i) * 2 + 1) * NFD + j), xr[j], u);
-            }
-            g = wsum(g);
-            u = wsum(u);
-            if (lane == 0) ll_put(LL + P.e_hh + jp, g / (1.0f + __expf(-g)) * u, ep);
-          }
+        for (int c = 0; c < 4; c++) acc[c] = wsum(on ? xs[2 * np + 4 * lane + c] * wgt : 0.0f);
+        if (lane < 4) {
+          const float val = lane == 0 ? acc[0] : lane == 1 ? acc[1] : lane == 2 ? acc[2] : acc[3];
+          ll_put(LL + P.e_o + h * HD + 4 * cb + lane, val * rcp(den), ep);
         }
       }
-      TS_END();
-      pb ^= 1;
-      // ---- x = xa + Wd hh
-      __syncthreads();
-      TS(0);
-      if (l + 1 < L) dma_qkv(Ls[l + 1], pb ^ 1);
-      else dma_head(0, pb ^ 1);
-      if (!ll_gather<NFF>(LL, f, ep, Ident{P.e_hh}, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) return;
-      TS(1);
-      land();
-      TS(2);
-      {
-        float acc = 0.0f;
-        if (orow_ok) {
-#pragma unroll
-          for (int j = 0; j < NFF; j++) acc = dot4(wb4(pb, wv * NFF + j), xs4(j, f), acc);
-        }
-        acc = wsum(acc);
-        x_own = xa_own + acc;
-        if (lane == 0 && orow_ok) ll_put(LL + P.e_x + orow, x_own, ep);
-      }
-      TS_END();
-      pb ^= 1;
+      pub();
     }
-    // ---- the head: logits of rows h0 .. h1 - 1 (wave wv: rows h0 + wv + 4 i),
-    // batch b (rows h0 + wv + 4 (b HBR + i)) in buffer pb ^ (b & 1)
-    {
-      TS(0);
-      float gfin[4];
-      load_gain(gfin, a.fin);
-      if (!ll_gather<4>(LL, d, ep, Ident{Ls[L - 1].e_x}, Tag32{}, xs, a.ctl, &bad_s, a.tmo)) return;
-      TS(1);
-      land();
-      TS(2);
-      norm_xs(d, gfin);
-      float4 xr[NFD];
+    // ---- xa = x + Wo o (Wo in bufB)
+    __syncthreads();
+    TS(0);
+    float4 gf[NFD];
+    load_g4(gf, P.rf);
+    dma_gu(P, bufN);
+    gathered(poll_gather<PEX>(LL, d, ep, Ident{P.e_o}, xs, a.ctl, a.tmo));
+    if (!meet()) return false;
+    if (orow_ok) {
+      float acc = 0.0f;
 #pragma unroll
-      for (int j = 0; j < NFD; j++) xr[j] = xs4(j, d);
-      unsigned long long best = 0ull;
-      for (uint32_t b = 0; b < nhb; b++) {
-        const uint32_t cur = pb ^ (b & 1);
-        if (b + 1 < nhb) {
-          dma_head(b + 1, cur ^ 1);
-          // batch b retired, batch b + 1 (HBR NFD pieces) may be in flight
-          __builtin_amdgcn_s_waitcnt((HBR * NFD & 15) | (((HBR * NFD) >> 4) << 14) | (7 << 4) | (15 << 8));
+      for (int j = 0; j < NFD; j++) acc = dot4(bufB[(wv * NFD + j) * 64 + lane], xs4(j, d), acc);
+      xa_own = x_own + wsum(acc);
+      if (lane == 0) ll_put(LL + P.e_xa + orow, xa_own, ep);
+    }
+    pub();
+    // ---- hh = silu(g) u on norm(xa) (gate|up in bufN): wave wv the pairs
+    // wv + 4 i
+    __syncthreads();
+    TS(0);
+    dma_wd(P, bufB);
+    gathered(poll_gather<PEX>(LL, d, ep, Ident{P.e_xa}, xs, a.ctl, a.tmo));
+    if (!meet()) return false;
+    {
+      float4 xg[NFD];
+      const float rs = norm_fold(gf, xg);
+      float hv[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const uint32_t pi = min(wv + 4 * i, RGp - 1);
+        float g = 0.0f, u = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NFD; j++) {
+          g = dot4(bufN[((pi * 2 + 0) * NFD + j) * 64 + lane], xg[j], g);
+          u = dot4(bufN[((pi * 2 + 1) * NFD + j) * 64 + lane], xg[j], u);
+        }
+        g = wsum(g) * rs;
+        u = wsum(u) * rs;
+        hv[i] = g * rcp(1.0f + __expf(-g)) * u;
+      }
+      if (lane < 2) {
+        const uint32_t pi = wv + 4 * lane, jp = w * RGp + pi;
+        if (pi < RGp && jp < f) ll_put(LL + P.e_hh + jp, lane == 0 ? hv[0] : hv[1], ep);
+      }
+    }
+    pub();
+    // ---- x = xa + Wd hh (Wd in bufB)
+    __syncthreads();
+    TS(0);
+    l + 1 < L ? dma_qkv(Ls[l + 1], bufN) : dma_head0(bufN);
+    gathered(poll_gather<PEF>(LL, f, ep, Ident{P.e_hh}, xs, a.ctl, a.tmo));
+    if (!meet()) return false;
+    if (orow_ok) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NFF; j++) acc = dot4(bufB[(wv * NFF + j) * 64 + lane], xs4(j, f), acc);
+      x_own = xa_own + wsum(acc);
+      if (lane == 0) ll_put(LL + P.e_x + orow, x_own, ep);
+    }
+    pub();
+    return true;
+  };
+
+  // the head: logits of rows h0 .. h1 - 1 (wave wv: rows h0 + wv + 4 i),
+  // batch b (rows h0 + wv + 4 (b HBR + i)) in the buffer of parity B ^ (b &
+  // 1); batch 0 came from the loading waves, the rest each wave loads itself
+  auto head = [&](auto B, uint32_t ep, unsigned long long* LL) -> bool {
+    constexpr int PB = decltype(B)::value;
+    float4* b0 = bufp(IC<PB>{});
+    float4* b1 = bufp(IC<1 - PB>{});
+    __syncthreads();
+    TS(0);
+    float4 gf[NFD];
+    load_g4(gf, a.fin);
+    gathered(poll_gather<PEX>(LL, d, ep, Ident{Ls[L - 1].e_x}, xs, a.ctl, a.tmo));
+    if (!meet()) return false;
+    float4 xg[NFD];
+    const float rs = norm_fold(gf, xg);
+    unsigned long long best = 0ull;
+    auto rows = [&](float4* cur, uint32_t b) {
+#pragma unroll
+      for (int i = 0; i < HBR; i++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NFD; j++) acc = dot4(cur[((wv * HBR + i) * NFD + j) * 64 + lane], xg[j], acc);
+        acc = wsum(acc) * rs;
+        const uint32_t r = h0 + wv + 4 * (b * HBR + i);
+        if (lane == 0 && r < h1) {
+          lgs[wv][b * HBR + i] = acc;
+          const unsigned long long kk = argmax_key(acc, r);
+          best = kk > best ? kk : best;
+        }
+      }
+    };
+    // batch b in b0 and b + 1 in b1, each issued one batch ahead (this
+    // wave's rows, which it alone reads: its own count suffices, no
+    // barrier)
+    for (uint32_t b = 0; b < nhb; b += 2) {
+      if (b + 1 < nhb) {
+        dma_head_own(b + 1, b1);
+        if (b > 0) __builtin_amdgcn_s_waitcnt(ANA_VM(HBR * NFD));
+      } else if (b > 0) {
+        __builtin_amdgcn_s_waitcnt(0);
+      }
+      rows(b0, b);
+      if (b + 1 < nhb) {
+        if (b + 2 < nhb) {
+          dma_head_own(b + 2, b0);
+          __builtin_amdgcn_s_waitcnt(ANA_VM(HBR * NFD));
         } else {
           __builtin_amdgcn_s_waitcnt(0);
         }
-#pragma unroll
-        for (int i = 0; i < HBR; i++) {
-          float acc = 0.0f;
-#pragma unroll
-          for (int j = 0; j < NFD; j++) acc = dot4(wb4(cur, (wv * HBR + i) * NFD + j), xr[j], acc);
-          acc = wsum(acc);
-          const uint32_t r = h0 + wv + 4 * (b * HBR + i);
-          if (lane == 0 && r < h1) {
-            lgs[wv][b * HBR + i] = acc;
-            const unsigned long long kk = argmax_key(acc, r);
-            best = kk > best ? kk : best;
-          }
-        }
+        rows(b1, b + 1);
       }
-      if (lane == 0) key_s[wv] = best;
-      __syncthreads();
-      // the rows' logits, then (once they are stored) the key
-      for (uint32_t i = tid; i < RH; i += kPT) {
-        const uint32_t r = h0 + i;
-        if (r < h1) __hip_atomic_store(a.LG + r, lgs[i & 3][i >> 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      if (tid == 0) {
-        unsigned long long b2 = key_s[0];
-        for (int i = 1; i < 4; i++) b2 = key_s[i] > b2 ? key_s[i] : b2;
-        // (value bits, 0xFFFF - index) in 48 bits, over a 16-bit epoch tag
-        const uint32_t ix = 0xFFFFFFFFu - (uint32_t)(b2 & 0xFFFFFFFFull);
-        const unsigned long long k48 = b2 ? ((b2 >> 32) << 16) | (0xFFFFull - ix) : 0ull;
-        __hip_atomic_store(LL + a.e_key + w, (k48 << 16) | (ep & 0xFFFFu), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      }
-      TS_END();
-      pb ^= (nhb & 1);
     }
-    // ---- the pick (dd.pick's order): every workgroup reads every key; the
-    // next step's first product loads meanwhile
+    if (lane == 0) key_s[wv] = best;
+    __syncthreads();
+    // the rows' logits, then (once they are stored) the key
+    for (uint32_t i = tid; i < RH; i += kPT) {
+      const uint32_t r = h0 + i;
+      if (r < h1) __hip_atomic_store(a.LG + r, lgs[i & 3][i >> 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      unsigned long long b2 = key_s[0];
+      for (int i = 1; i < 4; i++) b2 = key_s[i] > b2 ? key_s[i] : b2;
+      // (value bits, 0xFFFF - index) in 48 bits, over a 16-bit epoch tag
+      const uint32_t ix = 0xFFFFFFFFu - (uint32_t)(b2 & 0xFFFFFFFFull);
+      const unsigned long long k48 = b2 ? ((b2 >> 32) << 16) | (0xFFFFull - ix) : 0ull;
+      __hip_atomic_store(LL + a.e_key + w, (k48 << 16) | (ep & 0xFFFFu), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    pub();
+    return true;
+  };
+
+  // the pick (dd.pick's order): the poll wave reads every workgroup's key
+  // while the loading waves load the next step's first product into the
+  // buffer of parity B; the best key (0: no logit reached the maximum)
+  auto pick = [&](auto B, uint32_t ep, unsigned long long* LL, bool& ok) -> unsigned long long {
+    constexpr int PB = decltype(B)::value;
+    __syncthreads();
+    TS(0);
+    dma_qkv(Ls[0], bufp(IC<PB>{}));
     {
-      __syncthreads();
-      TS(0);
-      dma_qkv(Ls[0], pb);
-      unsigned long long kv = 0ull;
-      bool ok = true;
-      if (tid < G) {
-        const uint64_t t0 = rtc();
-        kv = ll_ld(LL + a.e_key + tid);
-        for (uint32_t it = 1; (uint32_t)(kv & 0xFFFFu) != (ep & 0xFFFFu); it++) {
-          if ((it & 127) == 0 && (rtc() - t0 > a.tmo || aborted(a.ctl))) {
-            ok = false;
-            break;
+      const uint32_t pt = tid;
+      unsigned long long kv[PES];
+      bool good = true;
+#pragma unroll
+      for (int e = 0; e < PES; e++) {
+        const uint32_t i = pt + kPT * e;
+        kv[e] = i < G ? ll_ld(LL + a.e_key + i) : 0ull;
+      }
+      const uint64_t t0 = rtc();
+      for (uint32_t it = 1;; it++) {
+        bool all = true;
+#pragma unroll
+        for (int e = 0; e < PES; e++) {
+          const uint32_t i = pt + kPT * e;
+          if (i < G && (uint32_t)(kv[e] & 0xFFFFu) != (ep & 0xFFFFu)) {
+            all = false;
+            kv[e] = ll_ld(LL + a.e_key + i);
           }
-          kv = ll_ld(LL + a.e_key + tid);
+        }
+        if (__all(all)) break;
+        if ((it & 31) == 0 && (rtc() - t0 > a.tmo || aborted(a.ctl))) {
+          good = false;
+          break;
         }
       }
-      if (!ok) bad_s = 1;
-      unsigned long long mk = tid < G ? kv >> 16 : 0ull;
+      unsigned long long mk = 0ull;
+#pragma unroll
+      for (int e = 0; e < PES; e++) {
+        const uint32_t i = pt + kPT * e;
+        const unsigned long long k = i < G ? kv[e] >> 16 : 0ull;
+        mk = k > mk ? k : mk;
+      }
 #pragma unroll
       for (int m = 32; m >= 1; m >>= 1) {
         const unsigned long long o = __shfl_xor(mk, m, 64);
         mk = o > mk ? o : mk;
       }
-      __syncthreads();
-      if (bad_s) {
-        fail_wg();
-        __builtin_amdgcn_s_waitcnt(0);
-        return;
-      }
-      if (lane == 0) key_s[wv] = mk;
-      __syncthreads();
-      mk = key_s[0];
-      for (int i = 1; i < 4; i++) mk = key_s[i] > mk ? key_s[i] : mk;
-      __syncthreads();
-      TS(1);
-      TS(2);
-      TS_END();
-      if constexpr (TR) {
-        // this step's stamps: [step][phase][workgroup][4]
-        if (k < a.trace_steps) {
-          for (uint32_t i = tid; i < ph * 4; i += kPT)
-            a.trace[(((size_t)k * a.trace_phases + i / 4) * G + w) * 4 + i % 4] = tr_s[i / 4][i % 4];
-        }
-      }
-      if (mk == 0ull) {
-        // no logit reaches the maximum (NaN): the host picks by Sample.argmax
-        nan_stop = true;
-        break;
-      }
-      const uint32_t t = 0xFFFFu - (uint32_t)(mk & 0xFFFFull);
-      if (w == 0 && tid == 0) a.out[(size_t)(st0 + k)] = t;
-      tok = t;
-      pos = pos + 1;
+      if (lane == 0) pick_s[wv] = mk;
+      gathered(good);
     }
+    ok = meet();
+    unsigned long long r = 0ull;
+    for (uint32_t u = 0; u < 4; u++) r = pick_s[u] > r ? pick_s[u] : r;
+    pub();
+    return r;
+  };
+
+  dma_qkv(Ls[0], wbA);
+  __builtin_amdgcn_s_waitcnt(0);
+  uint32_t pb = 0;          // the buffer parity the next phase reads
+  uint32_t k = 0;
+  bool nan_stop = false;
+  for (; k < a.steps; k++) {
+    const uint32_t ep = a.epoch0 + k + 1;
+    unsigned long long* LL = a.ll + (size_t)(ep & 1) * a.ll_par;
+    ph = 0;
+    for (uint32_t l = 0; l < L; l++) {
+      const bool ok = pb ? layer(IC<1>{}, l, ep, LL) : layer(IC<0>{}, l, ep, LL);
+      if (!ok) return;
+      pb ^= 1;   // five buffer phases a layer
+    }
+    if (!(pb ? head(IC<1>{}, ep, LL) : head(IC<0>{}, ep, LL))) return;
+    pb ^= (nhb & 1);
+    bool ok = true;
+    const unsigned long long mk = pb ? pick(IC<1>{}, ep, LL, ok) : pick(IC<0>{}, ep, LL, ok);
+    if (!ok) return;
+    if constexpr (TR) {
+      // this step's stamps: [step][phase][workgroup][4]
+      __syncthreads();
+      if (k < a.trace_steps) {
+        for (uint32_t i = tid; i < ph * 4; i += kPT)
+          a.trace[(((size_t)k * a.trace_phases + i / 4) * G + w) * 4 + i % 4] = tr_s[i / 4][i % 4];
+      }
+    }
+    if (mk == 0ull) {
+      // no logit reaches the maximum (NaN): the host picks by Sample.argmax
+      nan_stop = true;
+      break;
+    }
+    const uint32_t t = 0xFFFFu - (uint32_t)(mk & 0xFFFFull);
+    if (w == 0 && tid == 0) a.out[(size_t)(st0 + k)] = t;
+    tok = t;
+    pos = pos + 1;
   }
   // after the launch: the last fed token's residual row (this workgroup's
   // rows), and (workgroup 0) the loop's position, token, step and stop
@@ -819,7 +872,6 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     a.ctl[3] = nan_stop ? 1u : 0u;
   }
 #undef TS
-#undef TS_END
 }
 
 
@@ -868,4 +920,3 @@ hipError_t launch_decode1(const PersistArgs& a, uint32_t G, hipStream_t st) {
 }
 
 }  // namespace ana
-
