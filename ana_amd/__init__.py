@@ -73,6 +73,7 @@ SIGNATURES = {
     "ana_score_n": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p, _u32p, _u32p, _f32p]),
     "ana_logits": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _f32p]),
     "ana_top": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p]),
+    "ana_stats": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p, _f32p, _u32p, _f32p]),
     "ana_pick": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, C.POINTER(_Sampling), _u64p, _u32p]),
     "ana_rng_seeded": (None, [C.c_uint64, _u64p]),
     "ana_generate": (C.c_int, [C.c_void_p, C.c_uint32, _u32p, _u32p, _u32p, C.c_uint32,
@@ -296,6 +297,19 @@ class Decoder:
         out = np.empty(s.size, dtype=np.uint32)
         self._check(lib().ana_top(self.h, s.size, _p(s, C.c_uint32), _p(out, C.c_uint32)))
         return out
+
+    def stats(self, seqs, toks):
+        """dc.prob.of and al.stat after each sequence's last fed token: the
+        token's probability, the likeliest other token and its probability."""
+        s, t = _u32(seqs), _u32(toks)
+        if s.size != t.size:
+            raise ValueError("stats: one token per sequence")
+        p = np.empty(s.size, dtype=np.float32)
+        a = np.empty(s.size, dtype=np.uint32)
+        pa = np.empty(s.size, dtype=np.float32)
+        self._check(lib().ana_stats(self.h, s.size, _p(s, C.c_uint32), _p(t, C.c_uint32), _p(p, C.c_float),
+                                    _p(a, C.c_uint32), _p(pa, C.c_float)))
+        return p, a, pa
 
     def pick(self, seqs, st: Settings, rng: np.ndarray | None = None) -> np.ndarray:
         """S.pick on the device; rng (n x 4 uint64) advances in place."""

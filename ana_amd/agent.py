@@ -15,11 +15,21 @@ stretch as al.gen runs it (Loop.bend:480-505):
   while given tokens remain, taken from them: al.next, Loop.bend:375-383);
 - a tool's echo is fed as unsampled tokens and a new stretch starts from a
   pick drawn from the echo's last logits (al.resume, Loop.bend:561-567);
-  tokens still to be given are dropped there, as al.resume starts afresh.
+  tokens still to be given are dropped there, as al.resume starts afresh;
+- a failed check (the tool answers `Retry(echo, term)`, al.round's AlFail,
+  Loop.bend:622-627) resumes the same way, from then on with the retry
+  settings, and with the failed term to avoid: when the caller's
+  `term_start` says the token just written starts the new stretch's term,
+  the next tokens come from the product rule instead of a draw (al.next.free
+  and al.product, Loop.bend:284-357, `product` below): the model's
+  probability of writing the failed term again is read step by step along
+  it, the engine is emptied and every token fed so far replayed, and the
+  failed term up to the first step where another token outweighs it, then
+  that token, are given as if drawn.
 
-What a call is and what the tool answers stay with the caller (`is_call`,
-`tool`), as do the transcript, the repetition cut and the retry settings
-after a failed check.
+What a call is, where a term starts and what the tool answers stay with
+the caller (`is_call`, `term_start`, `tool`), as do the transcript and the
+repetition cut.
 
 What this module adds is the batching: every live episode shares each engine
 call. A round feeds, for each episode, the tokens written since its last
@@ -50,6 +60,73 @@ class Episode:
 
 
 @dataclass
+class Retry:
+    """A tool's failed check: its echo, and the failed term (the term's
+    tokens, then the call's) the next stretch's term is to avoid."""
+    echo: Sequence[int]
+    term: Sequence[int]
+
+
+@dataclass
+class Cut:
+    """al.product's verdict (AlC, Loop.bend:289-310): q, the model's
+    probability of writing the whole failed term again from its start; d,
+    the failed term's tokens kept; a, the token put at step d and b its
+    probability; given, the failed term's first d tokens then a."""
+    q: np.float32
+    d: int
+    a: int
+    b: np.float32
+    given: list
+
+
+def cut_of(steps) -> tuple:
+    """The pass along the failed term from its end back (al.cut.last and
+    al.cut.step, Loop.bend:297-310, F32 arithmetic): steps[j] = (p, a, b),
+    the model's probability of the term's token j at step j, the likeliest
+    other token and its probability. T's own token weighs p (1 - q') (q' the
+    rest's probability, after it), another its own probability; the first
+    step where another outweighs T's is where T is left."""
+    f32 = np.float32
+    p, a, b = steps[-1]
+    q, d, aa, bb = f32(p), 0, int(a), f32(b)
+    for p, a, b in reversed(steps[:-1]):
+        p, b = f32(p), f32(b)
+        if b > f32(p * f32(f32(1.0) - q)):
+            q, d, aa, bb = f32(p * q), 0, int(a), b
+        else:
+            q, d = f32(p * q), d + 1
+    return q, d, aa, bb
+
+
+def product(dec, slot: int, fed: Sequence[int], term: Sequence[int]) -> Cut:
+    """al.product (Loop.bend:345-357) on one sequence slot: fed is every
+    token the slot has taken so far, in order, with the term's first token
+    (the pick that starts the new term) last and not yet fed; term is the
+    failed term to avoid (at least one token). That token is fed, then
+    along the failed term: at each step its token's probability and its
+    likeliest rival (ana_stats: al.stat), each token fed but the last
+    (al.pass). Then the slot is emptied and fed replayed (al.product.fin:
+    the dense store has no rewind), so it stands after fed, and the cut
+    says which tokens come next (given as if drawn; the RNG untouched)."""
+    term = [int(x) for x in term]
+    if not term:
+        raise ValueError("agent.product: an empty failed term")
+    pos = len(fed) - 1
+    dec.feed([slot], [pos], [int(fed[-1])])
+    steps = []
+    for j, x in enumerate(term):
+        p, a, b = dec.stats([slot], [x])
+        steps.append((p[0], int(a[0]), b[0]))
+        if j + 1 < len(term):
+            dec.feed([slot], [pos + 1 + j], [x])
+    q, d, a, b = cut_of(steps)
+    dec.reset(slot)
+    dec.feeds(slot, 0, [int(t) for t in fed])
+    return Cut(q, d, a, b, term[:d] + [a])
+
+
+@dataclass
 class Outcome:
     tokens: list = field(default_factory=list)   # written after the prompt: drawn and given, in order (no EOS)
     drawn: list = field(default_factory=list)    # per token: drawn (True) or given (False)
@@ -57,8 +134,9 @@ class Outcome:
 
 
 def run(dec, eps: Sequence[Episode], st, is_call: Callable[[int, list], bool],
-        tool: Callable[[int, list], Sequence[int] | None], slots: Sequence[int] | None = None,
-        call_token: int | None = None) -> list:
+        tool: Callable[[int, list], Sequence[int] | Retry | None], slots: Sequence[int] | None = None,
+        call_token: int | None = None, term_start: Callable[[int, list], bool] | None = None,
+        retry=None) -> list:
     """Decode episodes eps together on dec (sequence slots `slots`, default
     0..n-1; each is reset first) with sampling settings st (None: greedy).
 
@@ -71,7 +149,12 @@ def run(dec, eps: Sequence[Episode], st, is_call: Callable[[int, list], bool],
     tokens) either ends the episode (None: "tool", the caller's verdict, as
     a passed check ends al.round) or gives the echo: the call's token is fed
     at the call's place, the echo after it, and a new stretch starts with a
-    new budget; without calls left the episode ends ("calls")."""
+    new budget; without calls left the episode ends ("calls"). A
+    Retry(echo, term) answer is a failed check: the same, and from then on
+    the episode draws with the settings `retry` (None: st) and, when
+    term_start(i, tokens) says the token just written starts the stretch's
+    term (no given tokens pending), takes its next tokens from product()
+    against that term."""
     n = len(eps)
     slots = list(range(n)) if slots is None else [int(s) for s in slots]
     if len(slots) != n or len(set(slots)) != n:
@@ -88,28 +171,42 @@ def run(dec, eps: Sequence[Episode], st, is_call: Callable[[int, list], bool],
     given = [list(e.first) for e in eps]          # given tokens after the one in hand
     left = [e.budget for e in eps]                # picks the stretch may still write
     calls = [e.calls for e in eps]
+    hist = [[] for _ in eps]                      # every token fed, in order (al.k.fed)
+    avoid = [None] * n                            # the failed term the next term avoids
+    retried = [False] * n                         # drawing with the retry settings
     for s in slots:
         dec.reset(s)
 
     def draw(idx, feeds):
         """For each episode idx[k]: feed feeds[k] from its position, the
-        last token through one ana_generate step, whose pick comes back."""
+        last token through one ana_generate step, whose pick comes back
+        (episodes after a failed check with the retry settings)."""
         pre = [k for k in range(len(idx)) if len(feeds[k]) > 1]
         if pre:
             dec.feeds_n([slots[idx[k]] for k in pre], [pos[idx[k]] for k in pre], [feeds[k][:-1] for k in pre])
-        r = np.ascontiguousarray(rng[idx])
-        got = dec.generate([slots[i] for i in idx], [pos[i] + len(f) - 1 for i, f in zip(idx, feeds)],
-                           [f[-1] for f in feeds], 1, st, r)
-        rng[idx] = r
+        got = {}
+        for sett, grp in ((st, [k for k, i in enumerate(idx) if not retried[i]]),
+                          (st if retry is None else retry, [k for k, i in enumerate(idx) if retried[i]])):
+            if not grp:
+                continue
+            ii = [idx[k] for k in grp]
+            r = np.ascontiguousarray(rng[ii])
+            o = dec.generate([slots[i] for i in ii], [pos[i] + len(feeds[k]) - 1 for i, k in zip(ii, grp)],
+                             [feeds[k][-1] for k in grp], 1, sett, r)
+            rng[ii] = r
+            for j, k in enumerate(grp):
+                got[k] = int(o[j, 0])
         for k, i in enumerate(idx):
             pos[i] += len(feeds[k])
-        return [int(got[k, 0]) for k in range(len(idx))]
+            hist[i] += [int(t) for t in feeds[k]]
+        return [got[k] for k in range(len(idx))]
 
     # the prompts fed and each first pick drawn; given tokens set it aside
     first = draw(list(range(n)), [list(e.prompt) for e in eps])
     for i in range(n):
         pick[i] = (given[i].pop(0), False) if given[i] else (first[i], True)
     live = set(range(n))
+    tail = []
     while live:
         idx, feeds = [], []
         for i in sorted(live):
@@ -135,6 +232,10 @@ def run(dec, eps: Sequence[Episode], st, is_call: Callable[[int, list], bool],
                     if ans is None:
                         out[i].why = "tool"
                         break
+                    if isinstance(ans, Retry):
+                        avoid[i] = [int(x) for x in ans.term] or None
+                        retried[i] = True
+                        ans = ans.echo
                     echo = [int(x) for x in ans]
                     if EOS in echo:
                         raise ValueError("agent.run: EOS in a tool's echo")
@@ -149,11 +250,36 @@ def run(dec, eps: Sequence[Episode], st, is_call: Callable[[int, list], bool],
                 if given[i]:
                     pick[i] = (given[i].pop(0), False)
                     continue
+                if avoid[i] is not None and term_start is not None and term_start(i, out[i].tokens):
+                    # al.next.free's product: what was written before t goes
+                    # in, then t through the pass, the replay and the cut
+                    if len(fed) > 1:
+                        dec.feeds_n([slots[i]], [pos[i]], [fed[:-1]])
+                        pos[i] += len(fed) - 1
+                        hist[i] += [int(x) for x in fed[:-1]]
+                    c = product(dec, slots[i], hist[i] + [int(t)], avoid[i])
+                    hist[i].append(int(t))
+                    pos[i] += 1
+                    avoid[i] = None
+                    fed = []
+                    pick[i] = (c.given[0], False)
+                    given[i] = c.given[1:]
+                    continue
                 idx.append(i)
                 feeds.append(fed)
                 break
             if out[i].why:
                 live.discard(i)
+                if fed:
+                    # given tokens written before the end: fed, as al.next
+                    # feeds each before the next one stands in
+                    tail.append((i, fed))
+        if tail:
+            dec.feeds_n([slots[i] for i, _ in tail], [pos[i] for i, _ in tail], [f for _, f in tail])
+            for i, f in tail:
+                pos[i] += len(f)
+                hist[i] += [int(t) for t in f]
+            tail = []
         if idx:
             for i, t in zip(idx, draw(idx, feeds)):
                 pick[i] = (t, True)

@@ -55,6 +55,7 @@ struct ana_ctx {
   float* SC = nullptr;               // scoring: the head's logits for up to sc_rows rows
   uint32_t sc_rows = 1;
   uint32_t* d_tgt = nullptr;         // scoring: each row's target token
+  float* d_stat = nullptr;           // ana_stats: each row's p and rival p, then the rivals
   float* d_ce = nullptr;             // scoring: each row's G.lse - logit[target]
   __bf16* d_sah = nullptr;   // ANA_BF16 prefill: a product's activations in bf16
   __bf16* d_hh = nullptr;    // ANA_BF16 prefill: gate|up's outputs in bf16, down's input
@@ -214,7 +215,7 @@ static void release(ana_ctx* c) {
   if (c->gexec_n) (void)hipGraphExecDestroy(c->gexec_n);
   void* ps[] = {c->d_play, c->d_ll, c->d_ctl, c->d_trace, c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
-                c->d_ss, c->d_pm, c->d_gtab, c->d_grun, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce, c->d_rcp,
+                c->d_ss, c->d_pm, c->d_gtab, c->d_grun, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce, c->d_stat, c->d_rcp,
                 c->d_sah, c->d_hh, c->d_rsc, c->PK, c->d_hpc, c->d_hpctl, c->d_oh, c->d_nxh, c->d_ssp};
   for (void* p : ps)
     if (p) (void)hipFree(p);
@@ -331,7 +332,8 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
   if ((e = dalloc(&c->d_pick, wb)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->d_rng, 4 * wb)) != hipSuccess) return bad(e);
   if ((e = dalloc(&c->SC, (uint64_t)c->sc_rows * cf.vocab)) != hipSuccess ||
-      (e = dalloc(&c->d_tgt, c->rows)) != hipSuccess || (e = dalloc(&c->d_ce, c->rows)) != hipSuccess)
+      (e = dalloc(&c->d_tgt, c->rows)) != hipSuccess || (e = dalloc(&c->d_ce, c->rows)) != hipSuccess ||
+      (e = dalloc(&c->d_stat, 3 * (uint64_t)c->max_seqs)) != hipSuccess)
     return bad(e);
   // a prefill step's residual-row pairs (every mode)
   if ((e = dalloc(&c->d_rcp, 2 * (uint64_t)c->rows)) != hipSuccess) return bad(e);
@@ -1084,6 +1086,26 @@ extern "C" int ana_logits(ana_ctx* c, uint32_t n, const uint32_t* seq, float* ou
   if (int r = head_of(c, "ana_logits", n, seq)) return r;
   if (int r = run_head(c, c->X, n, false)) return r;
   HIPCHK(c, hipMemcpyAsync(out, c->LG, (size_t)4 * n * c->cfg.vocab, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(c, hipStreamSynchronize(c->st));
+  return ANA_OK;
+}
+
+extern "C" int ana_stats(ana_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* tok, float* prob,
+                         uint32_t* alt, float* alt_prob) {
+  if (!c) return ANA_EINVAL;
+  if (!tok || !prob || !alt || !alt_prob) return fail(c, ANA_EINVAL, "ana_stats: null argument");
+  if (int r = head_of(c, "ana_stats", n, seq)) return r;
+  for (uint32_t i = 0; i < n; i++)
+    if (tok[i] >= c->cfg.vocab) return fail(c, ANA_EINVAL, "ana_stats: token %u outside the vocabulary", tok[i]);
+  if (int r = run_head(c, c->X, n, false)) return r;
+  float* dp = c->d_stat;
+  float* dpa = dp + c->max_seqs;
+  uint32_t* dalt = reinterpret_cast<uint32_t*>(dp + 2 * (size_t)c->max_seqs);
+  HIPCHK(c, hipMemcpyAsync(c->d_tgt, tok, 4 * n, hipMemcpyHostToDevice, c->st));
+  HIPCHK(c, launch_stats(c->LG, c->cfg.vocab, n, c->d_tgt, dp, dalt, dpa, c->st));
+  HIPCHK(c, hipMemcpyAsync(prob, dp, 4 * n, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(c, hipMemcpyAsync(alt, dalt, 4 * n, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(c, hipMemcpyAsync(alt_prob, dpa, 4 * n, hipMemcpyDeviceToHost, c->st));
   HIPCHK(c, hipStreamSynchronize(c->st));
   return ANA_OK;
 }

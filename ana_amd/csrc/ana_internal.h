@@ -216,6 +216,10 @@ struct PickArgs {
 hipError_t launch_pick(const PickArgs& a, hipStream_t st);
 // per row b of B logit rows: G.lse(row) - row[tgt[b]] in the tree's order
 // (Evaluate.bend's scoring summand)
+// dc.prob.of and al.stat for B rows of logits: each row's token probability,
+// its likeliest rival and the rival's probability
+hipError_t launch_stats(const float* logits, uint32_t vocab, uint32_t B, const uint32_t* tok, float* p,
+                        uint32_t* alt, float* palt, hipStream_t st);
 hipError_t launch_ce(const float* logits, uint32_t vocab, uint32_t B, const uint32_t* tgt, float* ce,
                      hipStream_t st);
 

@@ -131,12 +131,14 @@ __device__ __forceinline__ float4 mul4(float4 a, float4 b) {
   return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
 }
 
+// the gates in the fast mode's float: exp and log on the hardware's
+// base-2 units, the division as a reciprocal
 __device__ __forceinline__ float p_sigmoid(float z) {
-  if (0.0f <= z) return 1.0f / (1.0f + expf(-z));
-  const float e = expf(z);
-  return e / (1.0f + e);
+  const float e = __expf(-fabsf(z));
+  const float r = __builtin_amdgcn_rcpf(1.0f + e);
+  return 0.0f <= z ? r : e * r;
 }
-__device__ __forceinline__ float p_log_sigmoid(float z) { return -(fmaxf(-z, 0.0f) + log1pf(expf(-fabsf(z)))); }
+__device__ __forceinline__ float p_log_sigmoid(float z) { return -(fmaxf(-z, 0.0f) + __logf(1.0f + __expf(-fabsf(z)))); }
 
 template <int B>
 using IC = std::integral_constant<int, B>;
@@ -460,8 +462,8 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         if (a.rglru) {
           // dd.gate's RG-LRU arm (bend/Dense/Ex.bend:158-162), in float
           const float la = fminf(ANA_CAP, (8.0f * p_sigmoid(z)) * p_log_sigmoid(lamr));
-          kh = kn * sqrtf(1.0f - expf(2.0f * la));
-          al = expf(la);
+          kh = kn * sqrtf(1.0f - expf(2.0f * la));   // (1 - e^2la cancels: the exact exp)
+          al = __expf(la);
         } else {
           al = p_sigmoid(z);
           kh = kn;

@@ -125,6 +125,60 @@ __global__ __launch_bounds__(1024) void k_ce(const float* __restrict__ logits, u
   if (tid == 0) ce[b] = (m + dlog(s)) - lg[tgt[b]];
 }
 
+// The model's own probability of a token and its likeliest rival, from one
+// row of logits: dc.prob.of (bend/Decode.bend:199-202; SAMPLE_STATS's prob)
+// and al.stat (bend/Agent/Loop.bend:284-288). With m the tree max and z the
+// tree sum of F32.exp(x - m): p = exp(l[t] - m) / z, a = Sample.argmax of
+// the row with l[t] set to -3e38, pa = exp(l[a] - m) / z. One workgroup per
+// row, the reductions in the logits' tree order.
+template <int LPT>
+__global__ __launch_bounds__(1024) void k_stats(const float* __restrict__ logits, uint32_t vocab,
+                                                const uint32_t* __restrict__ tok, float* __restrict__ p,
+                                                uint32_t* __restrict__ alt, float* __restrict__ palt, uint32_t NT) {
+  __shared__ float red[16];
+  __shared__ uint32_t redi[16];
+  const uint32_t b = blockIdx.x, tid = threadIdx.x, base = tid * LPT;
+  const bool active = tid < NT;
+  const float* lg = logits + (size_t)b * vocab;
+  const uint32_t t = tok[b];
+  float x[LPT], pm[LPT];
+  load_run<LPT>(lg, base, vocab, active, x);
+#pragma unroll
+  for (int i = 0; i < LPT; i++) pm[i] = (active && base + i < vocab) ? x[i] : -3.0e38f;
+  const float m = tree_up(local_reduce<LPT>(pm, Max()), Max(), red, tid, NT);
+  float e[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; i++) e[i] = (active && base + i < vocab) ? dexp(x[i] - m) : 0.0f;
+  const float z = tree_up(local_reduce<LPT>(e, Add()), Add(), red, tid, NT);
+#pragma unroll
+  for (int i = 0; i < LPT; i++)
+    if (base + i == t) x[i] = -3.0e38f;
+  const uint32_t a = tree_argmax<LPT>(x, base, vocab, red, redi, tid, NT);
+  if (tid == 0) {
+    p[b] = dexp(lg[t] - m) / z;
+    alt[b] = a;
+    palt[b] = dexp(lg[a] - m) / z;
+  }
+}
+
+hipError_t launch_stats(const float* logits, uint32_t vocab, uint32_t B, const uint32_t* tok, float* p,
+                        uint32_t* alt, float* palt, hipStream_t st) {
+  if (B == 0) return hipSuccess;
+  uint32_t dv = 0;
+  while ((1ull << dv) < vocab) dv++;
+  const uint64_t vpad = 1ull << dv;
+  const uint32_t lpt = vpad > 1024 ? (uint32_t)(vpad / 1024) : 1u;
+  const uint32_t NT = (uint32_t)(vpad / lpt);
+  switch (lpt) {
+#define ANA_ST(L) \
+  case L: hipLaunchKernelGGL(k_stats<L>, dim3(B), dim3(1024), 0, st, logits, vocab, tok, p, alt, palt, NT); break;
+    ANA_ST(1) ANA_ST(2) ANA_ST(4) ANA_ST(8) ANA_ST(16) ANA_ST(32) ANA_ST(64)
+#undef ANA_ST
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_ce(const float* logits, uint32_t vocab, uint32_t B, const uint32_t* tgt, float* ce,
                      hipStream_t st) {
   if (B == 0) return hipSuccess;

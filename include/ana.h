@@ -127,6 +127,19 @@ int ana_score_n(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, const uint
  * dd.logits (bend/Dense/Decode.bend:641-646). */
 int ana_logits(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, float* out);
 
+/* The model's own probability of a token after each listed sequence's
+ * last fed token, and its likeliest rival: dc.prob.of
+ * (bend/Decode.bend:199-202, the prob= of SAMPLE_STATS's lines,
+ * bend/Generate.bend:40-49) and al.stat (bend/Agent/Loop.bend:284-288, the
+ * agent's pass along a failed term). The head runs on the device and only
+ * the three answers come back: with m the logits' tree max and z the tree
+ * sum of F32.exp(x - m), prob[i] = exp(l[tok[i]] - m) / z; alt[i] is
+ * Sample.argmax of the logits with l[tok[i]] set to -3e38, and alt_prob[i]
+ * its probability the same way. Bit-exact with those formulas on the
+ * reference's logits in ANA_EXACT_FP32. */
+int ana_stats(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, const uint32_t* tok, float* prob,
+              uint32_t* alt, float* alt_prob);
+
 /* Greedy's pick on the device: dd.top (bend/Dense/Decode.bend:475-484,
  * 648-660), the least index reaching the maximum logit; vocab when no logit
  * does (a NaN maximum), where the caller falls back to ana_pick. */

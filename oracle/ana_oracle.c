@@ -913,6 +913,25 @@ static best t_argmax(const float* x, uint32_t n, uint32_t base, int p) {
 }
 uint32_t or_tree_argmax(uint32_t v, const float* lg) { return t_argmax(lg, v, 0, tdepth(v)).i; }
 
+/* dc.prob.of (bend/Decode.bend:199-202) and al.stat (bend/Agent/Loop.bend:
+ * 284-288): m = T.V.max, z = T.V.sum_exp(m, lg) (bend/Tensor.bend:292-299),
+ * p = F32.exp(l[x] - m) / z; a = Sample.argmax of lg with l[x] set to
+ * -3e38 (T.V.set), pa = F32.exp(l[a] - m) / z */
+void or_stat(uint32_t vocab, const float* logits, uint32_t x, float* p, uint32_t* a, float* pa) {
+  int dv = tdepth(vocab);
+  float m = t_max(logits, vocab, 0, dv);
+  float* e = (float*)calloc(vocab ? vocab : 1, sizeof(float));
+  for (uint32_t i = 0; i < vocab; i++) e[i] = f32exp(logits[i] - m);
+  float z = t_sum(e, vocab, 0, dv);
+  for (uint32_t i = 0; i < vocab; i++) e[i] = i == x ? -3.0e38f : logits[i];
+  uint32_t r = t_argmax(e, vocab, 0, dv).i;
+  free(e);
+  *p = f32exp(logits[x] - m) / z;
+  *a = r;
+  *pa = f32exp(logits[r] - m) / z;
+}
+
+
 static float t_count_ge(const float* x, uint32_t n, uint32_t base, int p, float t) {
   if (base >= n) return 0.0f;
   if (p == 0) return x[base] >= t ? 1.0f : 0.0f;

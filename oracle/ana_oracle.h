@@ -103,6 +103,9 @@ float or_topp_threshold(uint32_t vocab, const float* w, float topp);
 float or_tree_sum(uint32_t n, const float* x);
 /* G.lse(logits) - logits[y] in the tree's order (Evaluate.bend's summand) */
 float or_ce(uint32_t vocab, const float* logits, uint32_t y);
+/* dc.prob.of and al.stat: token x's probability, its likeliest rival a
+ * (Sample.argmax with l[x] = -3e38) and a's probability */
+void or_stat(uint32_t vocab, const float* logits, uint32_t x, float* p, uint32_t* a, float* pa);
 
 #ifdef __cplusplus
 }

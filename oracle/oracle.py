@@ -65,6 +65,7 @@ def lib() -> C.CDLL:
             "or_topp_threshold": (C.c_float, [C.c_uint32, f32p, C.c_float]),
             "or_tree_sum": (C.c_float, [C.c_uint32, f32p]),
             "or_ce": (C.c_float, [C.c_uint32, f32p, C.c_uint32]),
+            "or_stat": (None, [C.c_uint32, f32p, C.c_uint32, f32p, C.POINTER(C.c_uint32), f32p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -193,6 +194,14 @@ def tree_argmax(logits: np.ndarray) -> int:
 def tree_sum(x: np.ndarray) -> float:
     a = np.ascontiguousarray(x, dtype=np.float32)
     return lib().or_tree_sum(a.size, _f32p(a))
+
+
+def stat(logits: np.ndarray, x: int):
+    """dc.prob.of / al.stat: (p, a, pa) in the reference's tree order."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    p, a, pa = C.c_float(), C.c_uint32(), C.c_float()
+    lib().or_stat(lg.size, _f32p(lg), int(x), C.byref(p), C.byref(a), C.byref(pa))
+    return np.float32(p.value), int(a.value), np.float32(pa.value)
 
 
 def ce(logits: np.ndarray, y: int) -> float:

@@ -30,6 +30,19 @@ class FakeDecoder:
         for s, p, t in zip(seqs, pos, toks):
             self._put(s, p, t)
 
+    def feed(self, seqs, pos, toks):
+        for s, p, t in zip(seqs, pos, toks):
+            self._put(s, p, [t])
+
+    def feeds(self, seq, pos, toks):
+        self._put(seq, pos, toks)
+
+    def stats(self, seqs, toks):
+        """a stand-in al.stat: a function of the slot's fed tokens"""
+        out = [fake_stat(self.hist[s], int(x), self.vocab) for s, x in zip(seqs, toks)]
+        return (np.array([o[0] for o in out], np.float32), np.array([o[1] for o in out], np.uint32),
+                np.array([o[2] for o in out], np.float32))
+
     def generate(self, seqs, pos, toks, steps, st, rng):
         assert steps == 1 and rng.shape == (len(seqs), 4) and rng.dtype == np.uint64
         self.calls.append(("generate", len(seqs)))
@@ -41,6 +54,13 @@ class FakeDecoder:
             rng[k, 3] ^= np.uint64(h + 1)
             out[k, 0] = h
         return out
+
+
+def fake_stat(hist, x, vocab=97):
+    h = sum((i + 1) * t for i, t in enumerate(hist)) + 13 * x
+    a = (h * 7 + 3) % vocab
+    a = a if a != x else (a + 1) % vocab
+    return np.float32((h % 89 + 1) / 100.0), a, np.float32(((h // 3) % 53 + 1) / 120.0)
 
 
 def is_call(i, toks):
@@ -151,3 +171,62 @@ def test_slots_and_errors():
         agent.run(dec, EPS[:2], None, is_call, tool, slots=[1, 1])
     with pytest.raises(ValueError):
         agent.run(dec, [agent.Episode([0], 1, 4, first=[1])], None, is_call, tool)
+
+
+def test_cut_by_hand():
+    """al.cut.last / al.cut.step (Loop.bend:297-310) on hand cases: a
+    one-token failed term is always left at its only token; at a step where
+    the rival's b exceeds p (1 - q) (q the rest's probability) the term is
+    left there, else kept."""
+    f32 = np.float32
+    q, d, a, b = agent.cut_of([(0.9, 5, 0.05)])
+    assert (d, a) == (0, 5) and q == f32(0.9)
+    # step 0: b0 = 0.5 > p0 (1 - p1) = 0.6 * 0.2 = 0.12: left at step 0
+    q, d, a, b = agent.cut_of([(0.6, 11, 0.5), (0.8, 12, 0.1)])
+    assert (d, a) == (0, 11) and q == f32(f32(0.6) * f32(0.8)) and b == f32(0.5)
+    # step 0: b0 = 0.1 < 0.9 (1 - 0.3) = 0.63: kept, left at step 1's rival
+    q, d, a, b = agent.cut_of([(0.9, 11, 0.1), (0.3, 12, 0.2)])
+    assert (d, a, b) == (1, 12, f32(0.2))
+    # three steps, left at the middle one: q folds every step's p
+    q, d, a, b = agent.cut_of([(0.95, 1, 0.01), (0.4, 2, 0.55), (0.99, 3, 0.005)])
+    assert (d, a) == (1, 2) and q == f32(f32(0.95) * f32(f32(0.4) * f32(0.99)))
+
+
+def test_product_and_retry_match_the_loop():
+    """agent.run with failed checks (Retry) and term starts, on the stand-in
+    decoder, against the restatement: al.product's pass along the failed
+    term, the replay and the given tokens, and the retry settings' draws."""
+    from ana_amd import rng_seeded
+    from agent_loop_ref import episode, product_ref
+
+    def tool_r(i, toks):
+        if toks[-1] >= 70:
+            return None
+        echo = [2 + (toks[-1] * 5 + j + i) % 80 for j in range(1 + (i + len(toks)) % 3)]
+        return agent.Retry(echo, toks[-4:]) if (i + len(toks)) % 3 else echo
+
+    def term_start(i, toks):
+        return toks[-1] % 3 == 1
+
+    dec = FakeDecoder(len(EPS))
+    together = agent.run(dec, EPS, None, is_call, tool_r, term_start=term_start)
+    n_products = 0
+    for i, e in enumerate(EPS):
+        feed, pick, hist = fake_engine(seed_rng=rng_seeded(e.seed).astype(np.uint64))
+
+        def feed_at(pos, t, hist=hist):
+            assert pos == len(hist)
+            hist.append(int(t))
+
+        def replay(fed, hist=hist):
+            hist[:] = [int(t) for t in fed]
+
+        def product(fed, term, hist=hist, feed_at=feed_at, replay=replay):
+            nonlocal n_products
+            n_products += 1
+            return product_ref(feed_at, lambda x: fake_stat(hist, x), replay, fed, term)
+        want = episode(feed, pick, e, lambda t, i=i: is_call(i, t), lambda t, i=i: tool_r(i, t),
+                       term_start=lambda t, i=i: term_start(i, t), product=product)
+        assert together[i] == want, i
+        assert dec.hist[i] == hist, i
+    assert n_products >= 3

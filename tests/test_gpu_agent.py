@@ -86,3 +86,125 @@ def test_batched_episodes_are_the_loop(oracle, path, sampling, call_token):
     whys = {o.why for o in together}
     print(f"endings {sorted(whys)}; tokens {[len(o.tokens) for o in together]}", flush=True)
     assert len(whys) >= 2
+
+
+class OracleEngine:
+    """One episode's engine on the CPU oracle: feed, the picks (the base
+    settings and the retry ones share the episode's RNG words), al.stat on
+    the last logits, and the replay after emptying the state."""
+
+    def __init__(self, oracle, m, seed, st, rs):
+        self.o, self.m, self.st, self.rs = oracle, m, st, rs
+        self.s = oracle.State(m)
+        self.at = 0
+        self.r = oracle.rng_seeded(seed)
+
+    def feed(self, t):
+        self.s.feed(self.at, int(t))
+        self.at += 1
+
+    def feed_at(self, pos, t):
+        assert pos == self.at
+        self.feed(t)
+
+    def _pick(self, st):
+        lg = self.s.logits()
+        if st is None:
+            return self.o.top(lg)
+        return self.o.pick(lg, st.temperature, st.top_k, st.top_p, self.r)
+
+    def pick(self):
+        return self._pick(self.st)
+
+    def retry_pick(self):
+        return self._pick(self.rs)
+
+    def stat(self, x):
+        return self.o.stat(self.s.logits(), x)
+
+    def replay(self, fed):
+        self.s = self.o.State(self.m)
+        self.at = 0
+        for t in fed:
+            self.feed(t)
+
+
+def test_product_is_the_reference(oracle, path):
+    """agent.product (al.product: the pass along a failed term with
+    ana_stats, the replay, the cut) bit for bit against its restatement on
+    the oracle, in exact mode: the verdict (q, d, a, b), the given tokens,
+    and the logits after the replay. The failed terms are the model's own
+    greedy continuation with one token changed at different places, so the
+    cut falls at the start and at several places along the term."""
+    from agent_loop_ref import product_ref
+    m = oracle.Model(path)
+    rng = np.random.default_rng(11)
+    with ana_amd.Decoder(path, max_seqs=2, prefill_chunk=8, numerics=ana_amd.EXACT_FP32) as dec:
+        v = dec.vocab
+        prompt = [0] + [int(x) for x in rng.integers(2, v, size=9)]
+        eng = OracleEngine(oracle, m, 0, None, None)
+        for t in prompt:
+            eng.feed(t)
+        greedy = []
+        for _ in range(7):
+            t = oracle.top(eng.s.logits())
+            greedy.append(int(t))
+            eng.feed(t)
+        seen = set()
+        for case, (k, length) in enumerate([(0, 1), (0, 6), (3, 6), (5, 6), (6, 6), (2, 3)]):
+            term = list(greedy[1:1 + length])
+            if k < length:
+                term[k] = int(rng.integers(2, v))
+            fed = prompt + [greedy[0]]
+            print(f"case product {case}: term length {length}, changed at {k}", flush=True)
+            dec.reset(1)
+            dec.feeds(1, 0, prompt)
+            got = agent.product(dec, 1, fed, term)
+            e2 = OracleEngine(oracle, m, 0, None, None)
+            for t in prompt:
+                e2.feed(t)
+            given, (q, d, a, b) = product_ref(e2.feed_at, e2.stat, e2.replay, fed, term)
+            assert (got.q, got.d, got.a, got.b) == (q, d, a, b), (case, got, (q, d, a, b))
+            assert got.given == given
+            lg = dec.logits([1])[0]
+            assert np.array_equal(lg.view(np.uint32), e2.s.logits().view(np.uint32)), case
+            seen.add(d)
+        assert len(seen) >= 3 and 0 in seen, seen
+
+
+def test_retry_episodes_are_the_loop(oracle, path):
+    """agent.run with failed checks (Retry answers with the term to avoid),
+    term starts and retry settings, on the GPU in exact mode, bit for bit
+    against the one-episode restatement driven by the oracle."""
+    from agent_loop_ref import episode, product_ref
+    st = ana_amd.Settings(float(np.float32(0.8)), 40, float(np.float32(0.9)))
+    rs = ana_amd.Settings(float(np.float32(0.5)), 20, float(np.float32(0.95)))
+
+    def tool_r(i, toks):
+        key = sum(toks) % 251
+        if key >= 215:
+            return None
+        echo = [2 + (key * 5 + j + i) % 250 for j in range(1 + (i + len(toks)) % 4)]
+        return agent.Retry(echo, toks[-5:]) if (i + len(toks)) % 3 else echo
+
+    def term_start(i, toks):
+        return toks[-1] % 4 == 1
+
+    m = oracle.Model(path)
+    with ana_amd.Decoder(path, max_seqs=8, prefill_chunk=8, numerics=ana_amd.EXACT_FP32) as dec:
+        eps = episodes(dec.vocab)
+        print("case agent retry: 7 episodes, v3 then retry sampling", flush=True)
+        together = agent.run(dec, eps, st, is_call, tool_r, term_start=term_start, retry=rs)
+        products = 0
+        for i, e in enumerate(eps):
+            eng = OracleEngine(oracle, m, e.seed, st, rs)
+
+            def product(fed, term, eng=eng):
+                nonlocal products
+                products += 1
+                return product_ref(eng.feed_at, eng.stat, eng.replay, fed, term)
+            want = episode(eng.feed, eng.pick, e, lambda t, i=i: is_call(i, t), lambda t, i=i: tool_r(i, t),
+                           term_start=lambda t, i=i: term_start(i, t), product=product, retry_pick=eng.retry_pick)
+            assert together[i] == want, i
+    print(f"products {products}; endings {sorted({o.why for o in together})}", flush=True)
+    assert products >= 2

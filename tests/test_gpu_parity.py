@@ -544,3 +544,46 @@ def test_nan_logits_fall_back(oracle, tmp_path, mode, n):
             st.feed(pos, t)
             pos += 1
         assert [int(x) for x in out[i]] == want, i
+
+
+@pytest.mark.parametrize("mode", [ana_amd.EXACT_FP32, ana_amd.FAST_FP32, ana_amd.BF16], ids=["exact", "fast_fp32", "bf16"])
+def test_stats_prob_and_rival(oracle, tmp_path, mode):
+    """ana_stats (dc.prob.of and al.stat) after feeds, against the oracle's
+    or_stat on its own logits: bit for bit in exact mode (with trained-like
+    vectors at v = 32768 too), within the mode's tolerance in the fast ones
+    (the rival then must be within tolerance of the best other logit)."""
+    for name, c, trained in (("small", cf.SMALL4_V3, False), ("115m", cf.BPE100M_V3, True)):
+        path = str(tmp_path / f"{name}.ftc2")
+        ckpt.write(path, c, ckpt.init_params(c, "normal", 3, trained=trained))
+        m = oracle.Model(path)
+        rng = np.random.default_rng(5)
+        n = 3
+        prompts = [[0] + [int(x) for x in rng.integers(2, c.vocab, size=6 + 2 * b)] for b in range(n)]
+        print(f"case stats {name} mode {mode}", flush=True)
+        with ana_amd.Decoder(path, max_seqs=n, numerics=mode) as dec:
+            dec.feeds_n(list(range(n)), [0] * n, prompts)
+            want = []
+            toks = []
+            for b in range(n):
+                st = oracle.State(m)
+                for p_, t in enumerate(prompts[b]):
+                    st.feed(p_, t)
+                lg = st.logits()
+                # the token: the best, a mid-ranked one, a random one
+                x = [int(np.argmax(lg)), int(np.argsort(lg)[c.vocab // 2]), int(rng.integers(0, c.vocab))][b]
+                toks.append(x)
+                want.append((oracle.stat(lg, x), lg))
+            p, a, pa = dec.stats(list(range(n)), toks)
+        for b in range(n):
+            (wp, wa, wpa), lg = want[b]
+            if mode == ana_amd.EXACT_FP32:
+                assert (p[b], int(a[b]), pa[b]) == (wp, wa, wpa), (name, b)
+            else:
+                tol = 1e-4 if mode == ana_amd.FAST_FP32 else 2e-2
+                scale = float(np.abs(lg).max())
+                # probabilities move by at most e^(2 tol scale) - 1 relative
+                bound = np.expm1(2.5 * tol * scale)
+                assert abs(float(p[b]) - float(wp)) <= bound * float(wp) + 1e-30, (name, b, p[b], wp)
+                other = lg.copy()
+                other[toks[b]] = -3e38
+                assert lg[int(a[b])] >= other.max() - 2 * tol * scale and int(a[b]) != toks[b], (name, b)

@@ -504,3 +504,48 @@ def test_ce_tree_order(oracle):
     xd = x.astype(np.float64)
     ref = np.log(np.exp(xd - xd.max()).sum()) + xd.max() - xd[123]
     assert abs(oracle.ce(x, 123) - ref) <= 1e-5 * max(1.0, abs(ref))
+
+
+
+def test_stat_prob_and_rival(oracle):
+    """or_stat, dc.prob.of (bend/Decode.bend:199-202) and al.stat
+    (bend/Agent/Loop.bend:284-288): p = exp(l[x] - m) / z over the tree
+    sum z, the rival a = Sample.argmax with l[x] set to -3e38 (least index
+    on a tie), pa its probability. Pinned by uniform logits (z = v exactly,
+    so p = 1/v and the rival is index 0, or 1 when x is 0), by the 5-leaf
+    depth-3 tree expanded by hand (the sum's order and the max's
+    convention), by logits near 1e4 (the sum overflows unless the max comes
+    off first), and by a double-precision softmax at v = 32768."""
+    f32 = np.float32
+    for v in (256, 32768):
+        lg = np.full(v, 2.5, np.float32)
+        for x in (0, 5):
+            p, a, pa = oracle.stat(lg, x)
+            assert p == f32(1.0) / f32(v) and pa == p
+            assert a == (1 if x == 0 else 0)
+    rng = np.random.default_rng(7)
+    vz = f32(-3.0e38)
+    for _ in range(200):
+        lg = (rng.standard_normal(5) * 3.0).astype(np.float32)
+        x = int(rng.integers(0, 5))
+        m = _f32max(_f32max(_f32max(lg[0], lg[1]), _f32max(lg[2], lg[3])),
+                    _f32max(_f32max(lg[4], vz), _f32max(vz, vz)))
+        e = [f32(np.exp(np.float64(f32(xi - m)))) for xi in lg]
+        z = f32(f32(f32(e[0] + e[1]) + f32(e[2] + e[3])) + f32(f32(e[4] + f32(0.0)) + f32(0.0)))
+        others = [(float(lg[i]) if i != x else -3.0e38, -i) for i in range(5)]
+        a_want = -max(others)[1]
+        p, a, pa = oracle.stat(lg, x)
+        assert p == f32(e[x] / z) and a == a_want and pa == f32(e[a_want] / z), (lg, x)
+    big = np.full(300, 1.0e4, np.float32)
+    big[17] = 1.0e4 + 2.0
+    p, a, pa = oracle.stat(big, 17)
+    assert np.isfinite(p) and abs(float(p) - np.exp(2.0) / (np.exp(2.0) + 299)) < 1e-6 and a == 0
+    lg = (rng.standard_normal(32768) * 4.0).astype(np.float32)
+    x = int(np.argsort(lg)[-1])
+    d = lg.astype(np.float64)
+    sm = np.exp(d - d.max())
+    sm /= sm.sum()
+    p, a, pa = oracle.stat(lg, x)
+    second = int(np.argsort(lg)[-2])
+    assert a == second
+    assert abs(float(p) - sm[x]) <= 1e-6 * sm[x] and abs(float(pa) - sm[second]) <= 1e-6 * sm[second]
