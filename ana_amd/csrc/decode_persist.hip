@@ -16,8 +16,9 @@
 // current phase's inputs. A wave's loads retire in issue order, so its polls
 // return only after its pieces have landed: the first poll then usually
 // finds the inputs already published (polling at once, in waves of their
-// own beside the stream, took a second round trip and ran slower), and when
-// the inputs are in, both buffers are ready. The two 64 KB weight buffers
+// own beside the stream, took a second round trip and ran slower; issuing
+// the pieces after the inputs were in, before the compute, ran slower too),
+// and when the inputs are in, both buffers are ready. The two 64 KB weight buffers
 // are separate LDS objects and every phase knows at compile time which one
 // it reads and which one its loads fill (a layer is compiled for each
 // starting buffer), so the compiler never holds a read of one buffer behind
@@ -67,6 +68,18 @@ __device__ __forceinline__ bool aborted(uint32_t* ctl) {
 // s_waitcnt with vmcnt = k (expcnt and lgkmcnt not waited on)
 #define ANA_VM(k) (((k) & 15) | (((k) >> 4) << 14) | (7 << 4) | (15 << 8))
 
+// a workgroup barrier that waits for this wave's LDS operations only: the
+// weight pieces streaming into the other LDS buffer stay in flight (a
+// __syncthreads() fence would wait for them), and no LDS access moves
+// across it. Global memory is ordered where it matters by explicit waits
+// (a wave's polls retire after its pieces; the head's logit stores).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt and expcnt not waited on
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // The workgroup's threads poll n entries (entry i at base[map(i)]; thread t
 // takes i = t + 256 e, e < PE) until each carries epoch ep in its upper
 // half, then dst[i] = the value. False (for this wave) when the wait passed
@@ -115,9 +128,9 @@ struct Ident {
 // block-wide sum of one value per thread (all threads get it)
 __device__ __forceinline__ float block_sum(float v, float* red) {
   v = wsum(v);
-  __syncthreads();
+  lds_barrier();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
+  lds_barrier();
   return red[0] + red[1] + red[2] + red[3];
 }
 
@@ -344,7 +357,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   // pieces in LDS (each wave's polls retired after its pieces). False
   // (every wave) when a wait failed.
   auto meet = [&]() -> bool {
-    __syncthreads();
+    lds_barrier();
     TS(2);
     if (bad_s) {
       fail_wg();
@@ -374,7 +387,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     const PLayer P = Ls[l];
     // ---- norm, then q|k|v (|z) (in bufB): rows w RQ .. w RQ + RQ - 1,
     // wave wv the rows wv + 4 i
-    __syncthreads();
+    lds_barrier();
     TS(0);
     float4 g4[NFD];
     load_g4(g4, P.ra);
@@ -429,7 +442,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     }
     pub();
     // ---- the mix (an attention unit's K and V pieces in bufN)
-    __syncthreads();
+    lds_barrier();
     TS(0);
     dma_wo(P, bufB);
     if (P.gla) {
@@ -506,7 +519,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
           kvv[tid] = kx;
           vvv[tid] = xs[2 * HD + tid];
         }
-        __syncthreads();
+        lds_barrier();
         // dd.sm.write: the piece holding this step's slot writes k and v
         if (slot >= t0 && slot < t0 + PL && (int)tid < HD) {
           float* Kr = Sseq + P.soff;
@@ -542,7 +555,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         }
         mloc = wmax(mloc);
         if (lane == 0) red[4 + wv] = mloc;
-        __syncthreads();
+        lds_barrier();
         const float m = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
         float e = 0.0f;
         if (tid < KPASS * 64) {
@@ -551,7 +564,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         }
         const float lsum = block_sum(e, red);   // (its first barrier orders the reads of es above)
         if (tid < KPASS * 64) es[tid] = e;
-        __syncthreads();
+        lds_barrier();
         // o over the piece: thread (c4, g) takes slots g, g + GS, ...
         const uint32_t c4 = tid % C4, g = tid / C4;
         float4 o = zero4();
@@ -572,7 +585,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
           o.w += __shfl_xor(o.w, s2, 64);
         }
         if (lane < (uint32_t)C4) part4[wv][lane] = o;
-        __syncthreads();
+        lds_barrier();
         unsigned long long* out = LL + P.e_part + (size_t)(h * np + p) * (HD + 2);
         if ((int)tid < HD) {
           const uint32_t c = tid / 4, e4 = tid % 4;
@@ -592,7 +605,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       pub();
       // ---- the pieces and the sink combined: o of head h, columns 4 cb ..
       // (no loads of its own: the Wo pieces stay in flight)
-      __syncthreads();
+      lds_barrier();
       TS(0);
       {
         bool ok = true;
@@ -632,7 +645,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       pub();
     }
     // ---- xa = x + Wo o (Wo in bufB)
-    __syncthreads();
+    lds_barrier();
     TS(0);
     float4 gf[NFD];
     load_g4(gf, P.rf);
@@ -649,7 +662,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     pub();
     // ---- hh = silu(g) u on norm(xa) (gate|up in bufN): wave wv the pairs
     // wv + 4 i
-    __syncthreads();
+    lds_barrier();
     TS(0);
     dma_wd(P, bufB);
     gathered(poll_gather<PEX>(LL, d, ep, Ident{P.e_xa}, xs, a.ctl, a.tmo));
@@ -678,9 +691,10 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     }
     pub();
     // ---- x = xa + Wd hh (Wd in bufB)
-    __syncthreads();
+    lds_barrier();
     TS(0);
-    l + 1 < L ? dma_qkv(Ls[l + 1], bufN) : dma_head0(bufN);
+    if (l + 1 < L) dma_qkv(Ls[l + 1], bufN);
+    else dma_head0(bufN);
     gathered(poll_gather<PEF>(LL, f, ep, Ident{P.e_hh}, xs, a.ctl, a.tmo));
     if (!meet()) return false;
     if (orow_ok) {
@@ -701,7 +715,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     constexpr int PB = decltype(B)::value;
     float4* b0 = bufp(IC<PB>{});
     float4* b1 = bufp(IC<1 - PB>{});
-    __syncthreads();
+    lds_barrier();
     TS(0);
     float4 gf[NFD];
     load_g4(gf, a.fin);
@@ -773,7 +787,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   // buffer of parity B; the best key (0: no logit reached the maximum)
   auto pick = [&](auto B, uint32_t ep, unsigned long long* LL, bool& ok) -> unsigned long long {
     constexpr int PB = decltype(B)::value;
-    __syncthreads();
+    lds_barrier();
     TS(0);
     dma_qkv(Ls[0], bufp(IC<PB>{}));
     {
@@ -845,7 +859,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     if (!ok) return;
     if constexpr (TR) {
       // this step's stamps: [step][phase][workgroup][4]
-      __syncthreads();
+      lds_barrier();
       if (k < a.trace_steps) {
         for (uint32_t i = tid; i < ph * 4; i += kPT)
           a.trace[(((size_t)k * a.trace_phases + i / 4) * G + w) * 4 + i % 4] = tr_s[i / 4][i % 4];
