@@ -1911,10 +1911,9 @@ namespace ana {
 // Levels 1-4 take one wave each; the diagonal (exponent 0) and level 0's 16
 // neighbour pairs are sums over a on lane groups. Reads qh, kh, cl; writes
 // every entry of P once; the caller synchronises after.
-template <int HD>
-__device__ __forceinline__ void gla_pairs(const float (*qh)[HD + 1], const float (*kh)[HD + 1],
-                                          const float (*cl)[HD + 1], float (*P)[kGlaSub + 1],
-                                          uint32_t n, uint32_t tid) {
+template <int HD, typename TQ, typename TK, typename TC, typename TP>
+__device__ __forceinline__ void gla_pairs(const TQ* qh, const TK* kh, const TC* cl, TP* P, uint32_t n,
+                                          uint32_t tid) {
   constexpr int L = kGlaSub;
   static_assert(L == 32 && HD % 16 == 0, "five levels of 16 x 16 tiles");
   // above the diagonal and past the last token: zero
@@ -2185,27 +2184,62 @@ __global__ __launch_bounds__(256) void k_gla_carry(GlaScratch g, StateRef S, flo
 // product takes its k steps in that same order (step (ab, y): k = 16 ab +
 // 4 (l / 16) + y), so the accumulators are its right operand as they stand.
 // S is read and written once per chunk and never passes through LDS; with
-// HD < 64 the waves past the column blocks hold copies. Thread (a, token
-// block) holds column a of TPT consecutive tokens: the L2 norms are sums
-// over the HD lanes of its group, the running sums of log a run in
-// registers and only the block totals pass through LDS.
-template <int HD, int TPT>
+// HD < 64 the waves past the column blocks hold copies. The gate pass is
+// token-major: eight lanes a token, HD / 8 columns a lane, loaded as
+// float4s a sub-chunk ahead, so a token's L2 norms are a lane's own sum
+// and three DPP adds; the running sums of log a then go down each column
+// (thread (a, token block): TPT tokens in registers, the block totals
+// through LDS).
+// CPT consecutive columns c0 .. c0 + CPT - 1 of q, k, v (QKV) and z (Z) for
+// token row + t (t clamped to T - 1: a token past T reads the last one, and
+// its values are discarded where used), as 16- or 8-byte loads; branch-free,
+// so the loads stay in flight while the caller works on
+template <int CPT>
 __device__ __forceinline__ void gla_run_load(const float* __restrict__ QKV, const float* __restrict__ Z,
-                                             uint32_t row, uint32_t T, uint32_t j0, uint32_t tb, uint32_t col,
-                                             uint32_t d, float (&q)[TPT], float (&k)[TPT], float (&v)[TPT],
-                                             float (&z)[TPT]) {
+                                             uint32_t row, uint32_t t, uint32_t T, uint32_t c0, uint32_t d,
+                                             float (&q)[CPT], float (&k)[CPT], float (&v)[CPT],
+                                             float (&z)[CPT]) {
+  static_assert(CPT % 4 == 0 || CPT == 2, "whole float4s or one float2");
+  const uint32_t tt = min(t, T - 1);
+  const float* x = QKV + (size_t)(row + tt) * 3 * d + c0;
+  const float* zz = Z + (size_t)(row + tt) * d + c0;
+  if constexpr (CPT == 2) {
+    const float2 a = *reinterpret_cast<const float2*>(x), b = *reinterpret_cast<const float2*>(x + d),
+                 c = *reinterpret_cast<const float2*>(x + 2 * d), e = *reinterpret_cast<const float2*>(zz);
+    q[0] = a.x; q[1] = a.y; k[0] = b.x; k[1] = b.y; v[0] = c.x; v[1] = c.y; z[0] = e.x; z[1] = e.y;
+  } else {
 #pragma unroll
-  for (int i = 0; i < TPT; i++) {
-    const uint32_t t = j0 + tb * TPT + i;
-    q[i] = k[i] = v[i] = z[i] = 0.0f;
-    if (t < T) {
-      const uint32_t o = (row + t) * 3 * d + col;  // (the launcher checks rows x 3 d < 2^32)
-      q[i] = QKV[o];
-      k[i] = QKV[o + d];
-      v[i] = QKV[o + 2 * d];
-      z[i] = Z[(row + t) * d + col];
+    for (int u = 0; u < CPT; u += 4) {
+      const float4 a = *reinterpret_cast<const float4*>(x + u), b = *reinterpret_cast<const float4*>(x + d + u),
+                   c = *reinterpret_cast<const float4*>(x + 2 * d + u),
+                   e = *reinterpret_cast<const float4*>(zz + u);
+      q[u] = a.x; q[u + 1] = a.y; q[u + 2] = a.z; q[u + 3] = a.w;
+      k[u] = b.x; k[u + 1] = b.y; k[u + 2] = b.z; k[u + 3] = b.w;
+      v[u] = c.x; v[u + 1] = c.y; v[u + 2] = c.z; v[u + 3] = c.w;
+      z[u] = e.x; z[u + 1] = e.y; z[u + 2] = e.z; z[u + 3] = e.w;
     }
   }
+}
+
+// the sum over each group of 8 consecutive lanes (a quad, then the
+// mirrored quad), in every lane of the group
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  return v;
+}
+
+// 1 - e^x for x <= 0 without cancellation near 0: the series to x^7 where
+// x > -1/2 (truncation below 2e-7 of the result), the hardware exp elsewhere
+__device__ __forceinline__ float one_minus_exp(float x) {
+  float p = fmaf(x, 1.0f / 5040.0f, 1.0f / 720.0f);
+  p = fmaf(x, p, 1.0f / 120.0f);
+  p = fmaf(x, p, 1.0f / 24.0f);
+  p = fmaf(x, p, 1.0f / 6.0f);
+  p = fmaf(x, p, 0.5f);
+  p = fmaf(x, p, 1.0f);
+  return x > -0.5f ? -x * p : 1.0f - __expf(x);
 }
 
 template <int HD>
@@ -2216,11 +2250,21 @@ __global__ __launch_bounds__(256, 3) void k_gla_run(const float* __restrict__ QK
                                                      const GlaRun* __restrict__ runs, uint32_t d, uint32_t rglru) {
   constexpr int L = kGlaSub, TPA = 256 / HD, TPT = L / TPA, CBS = HD / 16, R = 4 / CBS;
   static_assert(TPT >= 1 && TPA * TPT == L && CBS * R == 4, "whole tokens a thread, a column block a wave");
-  __shared__ float qh[L][HD + 1], kh[L][HD + 1], cl[L][HD + 1], vv[L][HD + 1];
-  __shared__ float P[L][L + 1], tot[TPA][HD];
+  // the gate pass: TPK threads a token, CPT columns a thread
+  constexpr int TPK = 256 / L, CPT = HD / TPK;
+  static_assert(TPK == 8 && CPT * TPK == HD, "a token's columns over 8 lanes");
+  // row strides (floats) picked by a model of the 64 lanes' bank use for
+  // each read pattern at HD = 64: the pair levels' 16 rows x 4 k and the
+  // diagonal's 8 x 8 on qh, kh and cl; qt S's 16 rows x 4 columns 4 apart
+  // on qh; Kd^T V's and P V's 4 rows x 16 columns on kh and vv (stride 16
+  // mod 64 spreads those over all 64 banks); P V's 16 rows x 4 k on P
+  constexpr int SQ = HD + 5, SK = HD + 10, SC = HD + 6, SV = HD + 16, SP = L + 4;
+  __shared__ float qh[L][SQ], kh[L][SK], cl[L][SC], vv[L][SV];
+  __shared__ float P[L][SP], tot[TPA][HD];
   const uint32_t h = blockIdx.x, tid = threadIdx.x;
   const GlaRun r = runs[blockIdx.y];
-  const uint32_t a = tid % HD, tb = tid / HD, col = h * HD + a;
+  const uint32_t a = tid % HD, tb = tid / HD;
+  const uint32_t tk = tid / TPK, c0 = h * HD + (tid % TPK) * CPT, e0 = (tid % TPK) * CPT;
   const uint32_t lane = tid & 63, wv = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
   const uint32_t bw = wv % CBS, rep = wv / CBS;
   float* Sg = S.base + (size_t)r.seq * S.seq_stride + S.layer_off + (size_t)h * HD * HD;
@@ -2229,42 +2273,66 @@ __global__ __launch_bounds__(256, 3) void k_gla_run(const float* __restrict__ QK
   for (int ab = 0; ab < CBS; ab++)
 #pragma unroll
     for (int y = 0; y < 4; y++) Sr[ab][y] = Sg[(16 * ab + 4 * g4 + y) * HD + 16 * bw + r16];
-  const float lv = rglru ? f_log_sigmoid(lam[col]) : 0.0f;
+  float lv[CPT];
+#pragma unroll
+  for (int e = 0; e < CPT; e++) lv[e] = rglru ? f_log_sigmoid(lam[c0 + e]) : 0.0f;
+  float q[CPT], k[CPT], v[CPT], z[CPT];
+  gla_run_load<CPT>(QKV, Z, r.row, tk, r.T, c0, d, q, k, v, z);
   for (uint32_t j0 = 0; j0 < r.T; j0 += L) {
     const uint32_t n = min((uint32_t)L, r.T - j0);
-    float q[TPT], k[TPT], v[TPT], z[TPT], lq[TPT], lk[TPT], c[TPT];
-    gla_run_load<HD, TPT>(QKV, Z, r.row, r.T, j0, tb, col, d, q, k, v, z);
-    // norms, gates (dd.gate) and the running sum inside the token block
+    // token tk's norms (sums over its 8 lanes) and gates (dd.gate), token
+    // by token: the hardware's reciprocal square root, exp, log and square
+    // root (~1 ulp), and 1 - e^(2 la) by one_minus_exp, as la ends near the
+    // cap of -1e-4 there
+    float lqr[CPT], lkr[CPT], lar[CPT], vr[CPT];
+    {
+      const bool ok = tk < n;
+      float sq = 0.0f, sk = 0.0f;
 #pragma unroll
-    for (int i = 0; i < TPT; i++) {
-      const float sq = group_sum<HD>(q[i] * q[i]), sk = group_sum<HD>(k[i] * k[i]);
-      float la = 0.0f;
-      lq[i] = lk[i] = 0.0f;
-      if (tb * TPT + i < n) {
-        // (the hardware's reciprocal square root, exp and log, ~1 ulp; 1 -
-        // e^(2 la) keeps expf, as la ends near the cap of -1e-4 there)
-        lq[i] = q[i] * __builtin_amdgcn_rsqf(1.0e-6f + sq);
-        const float kn = k[i] * __builtin_amdgcn_rsqf(1.0e-6f + sk);
-        if (rglru) {
-          la = fminf(ANA_CAP, (8.0f * __builtin_amdgcn_rcpf(1.0f + __expf(-z[i]))) * lv);
-          lk[i] = kn * sqrtf(1.0f - expf(2.0f * la));
-        } else {
-          la = -(fmaxf(-z[i], 0.0f) + __logf(1.0f + __expf(-fabsf(z[i]))));
-          lk[i] = kn;
-        }
+      for (int e = 0; e < CPT; e++) {
+        sq = fmaf(q[e], q[e], sq);
+        sk = fmaf(k[e], k[e], sk);
       }
-      c[i] = (i ? c[i - 1] : 0.0f) + la;
-    }
-    tot[tb][a] = c[TPT - 1];
-    __syncthreads();
-    float off = 0.0f;
-    for (uint32_t b = 0; b < tb; b++) off += tot[b][a];
+      const float rq = __builtin_amdgcn_rsqf(1.0e-6f + sum8(sq)), rk = __builtin_amdgcn_rsqf(1.0e-6f + sum8(sk));
 #pragma unroll
-    for (int i = 0; i < TPT; i++) {
-      qh[tb * TPT + i][a] = lq[i];
-      kh[tb * TPT + i][a] = lk[i];
-      cl[tb * TPT + i][a] = c[i] + off;
-      vv[tb * TPT + i][a] = v[i];
+      for (int e = 0; e < CPT; e++) {
+        float la, lk;
+        if (rglru) {
+          la = fminf(ANA_CAP, (8.0f * __builtin_amdgcn_rcpf(1.0f + __expf(-z[e]))) * lv[e]);
+          lk = (k[e] * rk) * __builtin_amdgcn_sqrtf(one_minus_exp(2.0f * la));
+        } else {
+          la = -(fmaxf(-z[e], 0.0f) + __logf(1.0f + __expf(-fabsf(z[e]))));
+          lk = k[e] * rk;
+        }
+        lqr[e] = ok ? q[e] * rq : 0.0f;
+        lkr[e] = ok ? lk : 0.0f;
+        lar[e] = ok ? la : 0.0f;
+        vr[e] = ok ? v[e] : 0.0f;
+      }
+    }
+    // the next sub-chunk's inputs, in flight through this one's work
+    if (j0 + L < r.T) gla_run_load<CPT>(QKV, Z, r.row, j0 + L + tk, r.T, c0, d, q, k, v, z);
+    __syncthreads();   // (the previous sub-chunk's reads of the arrays are done)
+#pragma unroll
+    for (int e = 0; e < CPT; e++) {
+      qh[tk][e0 + e] = lqr[e];
+      kh[tk][e0 + e] = lkr[e];
+      cl[tk][e0 + e] = lar[e];
+      vv[tk][e0 + e] = vr[e];
+    }
+    __syncthreads();
+    // the running sums of log a down each column: thread (a, tb) over its
+    // TPT tokens, then the earlier blocks' totals
+    {
+      float c[TPT];
+#pragma unroll
+      for (int i = 0; i < TPT; i++) c[i] = (i ? c[i - 1] : 0.0f) + cl[tb * TPT + i][a];
+      tot[tb][a] = c[TPT - 1];
+      __syncthreads();
+      float off = 0.0f;
+      for (uint32_t b = 0; b < tb; b++) off += tot[b][a];
+#pragma unroll
+      for (int i = 0; i < TPT; i++) cl[tb * TPT + i][a] = c[i] + off;
     }
     __syncthreads();
     gla_pairs<HD>(qh, kh, cl, P, n, tid);
@@ -2338,35 +2406,57 @@ hipError_t launch_gla_run(const float* QKV, const float* Z, const float* lam, St
 }
 
 // A fast-mode prefill step's K and V rows into the rings (dd.sm.write over
-// every row): thread t of workgroup (x, b) takes column 256 x + t of row b,
-// so a head's HD columns are HD consecutive lanes; the qk-norm's sum of
-// squares is their group sum (reassociated), k = (k * s) * (1 + gk), and K
-// and V go to slot pos mod ctx. One workgroup a 256 columns of a row,
-// where the exact kernel takes one a (head, row) with an in-order chain.
+// every row): wave w of workgroup x takes row 4 x + w, lane l its float4
+// columns 4 (l + 64 j), so a head's HD columns are HD / 4 consecutive lanes;
+// the qk-norm's sum of squares is their group sum (reassociated),
+// k = (k * s) * (1 + gk), and K and V go to slot pos mod ctx. The exact
+// kernel takes one workgroup a (head, row) with an in-order chain instead.
 template <int HD>
 __global__ __launch_bounds__(256) void k_kv_write_fast(AttnArgs a) {
-  const uint32_t b = blockIdx.y, col = blockIdx.x * 256 + threadIdx.x, d = a.d;
-  const bool in = col < d;
-  const float* x = a.QKV + (size_t)b * 3 * d;
-  float k = in ? x[d + col] : 0.0f;
-  const float v = in ? x[2 * d + col] : 0.0f;
-  if (a.gk) {
-    const float ss = group_sum<HD>(k * k);
-    k = (k * (1.0f / sqrtf(ss / (float)HD + 1.0e-5f))) * (1.0f + a.gk[col % HD]);
-  }
-  if (!in) return;
+  // a wave a row, four columns a lane (float4), so each lane's loads and
+  // stores are 16 bytes and a workgroup moves four whole rows; a head's
+  // HD / 4 lanes sum its squares by DPP within their 16-lane row
+  constexpr int G = HD / 4;
+  static_assert(G == 4 || G == 8 || G == 16, "a head's lanes inside one DPP row");
+  const uint32_t lane = threadIdx.x & 63, b = blockIdx.x * 4 + (threadIdx.x >> 6), d = a.d, d4 = d >> 2;
+  if (b >= a.B) return;
   const uint32_t pos = a.pos ? a.pos[b] : a.pos0 + b;
   const uint32_t slot = pos % a.ctx;
   const uint32_t sl = a.seq ? a.seq[b] : a.seq0;
-  float* Kr = a.KV.base + (size_t)sl * a.KV.seq_stride + a.KV.layer_off;
-  Kr[(size_t)slot * d + col] = k;
-  Kr[(size_t)a.ctx * d + (size_t)slot * d + col] = v;
+  const float4* x = reinterpret_cast<const float4*>(a.QKV + (size_t)b * 3 * d);
+  float4* Kr = reinterpret_cast<float4*>(a.KV.base + (size_t)sl * a.KV.seq_stride + a.KV.layer_off +
+                                         (size_t)slot * d);
+  float4* Vr = Kr + (size_t)a.ctx * d4;
+  // (d4 is a multiple of 64 lanes' worth or the tail lanes sit out whole
+  // groups: d is heads x HD, so a group never straddles the end)
+  for (uint32_t q = lane; q < ((d4 + 63) & ~63u); q += 64) {
+    const bool in = q < d4;
+    float4 k = in ? x[d4 + q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 v = in ? x[2 * d4 + q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (a.gk) {
+      float ss = k.x * k.x + k.y * k.y + k.z * k.z + k.w * k.w;
+      ss += dpp<0xB1>(ss);
+      ss += dpp<0x4E>(ss);
+      if constexpr (G >= 8) ss += dpp<0x141>(ss);
+      if constexpr (G >= 16) ss += dpp<0x140>(ss);
+      const float r = 1.0f / sqrtf(ss / (float)HD + 1.0e-5f);
+      // (the gains one float at a time: their offset in the parameters need
+      // not be a multiple of four)
+      const float* g = a.gk + (4 * q) % HD;
+      k = make_float4((k.x * r) * (1.0f + g[0]), (k.y * r) * (1.0f + g[1]), (k.z * r) * (1.0f + g[2]),
+                      (k.w * r) * (1.0f + g[3]));
+    }
+    if (in) {
+      Kr[q] = k;
+      Vr[q] = v;
+    }
+  }
 }
 
 hipError_t launch_kv_write_fast(const AttnArgs& a, hipStream_t st) {
   const uint32_t hd = a.d / a.heads;
   if (a.B == 0 || hd * a.heads != a.d) return hipErrorInvalidValue;
-  const dim3 grid((a.d + 255) / 256, a.B);
+  const dim3 grid((a.B + 3) / 4);
   switch (hd) {
     case 64: hipLaunchKernelGGL(k_kv_write_fast<64>, grid, dim3(256), 0, st, a); break;
     case 32: hipLaunchKernelGGL(k_kv_write_fast<32>, grid, dim3(256), 0, st, a); break;

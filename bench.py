@@ -217,6 +217,79 @@ NUMERICS = {"exact": "exact_fp32: bit-exact with the reference's CPU kernels",
             "bf16": "bf16 weights, fp32 activations/accumulation/state; logits within 2e-2"}
 
 
+def phase_names(c) -> list:
+    """k_decode1's phases of a step, in order: per layer q|k|v(|z), the mix
+    (GLA; or the attention pieces, then their combination), Wo, gate|up,
+    down; then the LM head and the pick."""
+    names = []
+    for i in range(c.layers):
+        if c.is_softmax(i):
+            names += [(i, "qkv"), (i, "att"), (i, "comb"), (i, "wo"), (i, "gu"), (i, "down")]
+        else:
+            names += [(i, "qkvz"), (i, "gla"), (i, "wo"), (i, "gu"), (i, "down")]
+    return names + [(-1, "head"), (-1, "pick")]
+
+
+def run_phase_trace(path: str, c, steps: int) -> str:
+    """The bench's B=1 fast_fp32 workload (1920-token prompt, decode from
+    1919) with k_decode1's phase stamps armed for `steps` steps of one
+    call; returns a markdown summary. Per (phase, workgroup) the stamps
+    split a phase into: wait (start to every input seen: the exchange, and
+    the weight loads issued before it, which retire first), land (to the
+    phase's weights in LDS), compute (to the outputs published), and the gap
+    to the next phase's start. Figures are means over workgroups and over
+    the traced steps after the first two."""
+    TICK_US = 0.01   # the constant-rate clock runs at 100 MHz
+    pr = ckpt.prompt(0, 1920, c.vocab)
+    with ana_amd.Decoder(path, max_seqs=1, numerics=ana_amd.FAST_FP32) as dec:
+        dec.feeds(0, 0, pr[:-1])
+        pos, tok = 1919, int(pr[-1])
+        o = dec.generate([0], [pos], [tok], PRIME)[0]
+        pos, tok = pos + PRIME, int(o[-1])
+        t = time.perf_counter()
+        o = dec.generate([0], [pos], [tok], 64)[0]
+        untraced = (time.perf_counter() - t) / 64 * 1e6
+        pos, tok = pos + 64, int(o[-1])
+        dec.trace(steps)
+        t = time.perf_counter()
+        o = dec.generate([0], [pos], [tok], 64)[0]
+        traced = (time.perf_counter() - t) / 64 * 1e6
+        tr = dec.trace_read().astype(np.int64)
+    S, P, G, _ = tr.shape
+    names = phase_names(c)
+    if len(names) != P:
+        raise RuntimeError(f"phase trace: {P} phases, expected {len(names)}")
+    # ticks relative to each step's first stamp (the low 32 bits wrap)
+    t = (tr - tr[:, 0:1, :, 0:1]) % (1 << 32)
+    t = np.where(t > (1 << 31), t - (1 << 32), t) * TICK_US
+    ss = list(range(2, S)) if S > 2 else list(range(S))
+    a = t[ss]                                        # [s, P, G, 4]
+    wait = a[..., 1] - a[..., 0]
+    land = a[..., 2] - a[..., 1]
+    comp = a[..., 3] - a[..., 2]
+    gap = np.concatenate([a[:, 1:, :, 0] - a[:, :-1, :, 3], np.zeros_like(a[:, :1, :, 0])], axis=1)
+    span = [float(a[i, -1, :, 3].max() - a[i, 0, :, 0].min()) for i in range(len(ss))]
+    out = [f"k_decode1 phase stamps: {len(ss)} steps (of {S} traced) x {P} phases x {G} workgroups; "
+           f"one step {np.mean(span):.1f} us from its first phase's start to its pick's last publish "
+           f"(ana_generate: {untraced:.1f} us a step untraced, {traced:.1f} traced)", "",
+           "| phase | count | wait us | land us | compute us | gap us | total us | x count |",
+           "|---|---|---|---|---|---|---|---|"]
+    kinds = []
+    for _, k in names:
+        if k not in kinds:
+            kinds.append(k)
+    tot = np.zeros(5)
+    for k in kinds:
+        idx = [p for p, (_, kk) in enumerate(names) if kk == k]
+        w, la, co, g = (float(x[:, idx].mean()) for x in (wait, land, comp, gap))
+        n = len(idx)
+        tot += np.array([w, la, co, g, w + la + co + g]) * n
+        out.append(f"| {k} | {n} | {w:.2f} | {la:.2f} | {co:.2f} | {g:.2f} | {w + la + co + g:.2f} | "
+                   f"{(w + la + co + g) * n:.1f} |")
+    out.append(f"| step | {P} | {tot[0]:.1f} | {tot[1]:.1f} | {tot[2]:.1f} | {tot[3]:.1f} | {tot[4]:.1f} | |")
+    return "\n".join(out)
+
+
 def run_agent(path: str, c, mode: str) -> dict:
     """Many agent episodes decoded together (ana_amd.agent): 64 episodes of
     a 128-token prompt, the v3 sampling settings, 48 draws a stretch, two
@@ -334,6 +407,8 @@ def main() -> int:
                     help="with --configs-only: just this one config")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--ckpt", default=os.environ.get("ANA_BENCH_CKPT", "/tmp/ana_bench_fp100m.ftc2"))
+    ap.add_argument("--phase-trace", type=int, default=0,
+                    help="only print k_decode1's per-phase stamp summary over this many traced steps (1..64)")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py: this build measures one GPU only; the decode path shards by sequence "
@@ -342,6 +417,10 @@ def main() -> int:
     c = cf.FP100M
     path = ensure_ckpt(c, a.ckpt)
     mode = a.numerics
+    if a.phase_trace:
+        print(run_phase_trace(path, c, a.phase_trace), flush=True)
+        release_device()
+        return 0
     if a.prefill_only:
         print(json.dumps(run_prefill(path, c, a.reps)), flush=True)
         release_device()
