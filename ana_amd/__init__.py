@@ -85,6 +85,7 @@ SIGNATURES = {
     "ana_prof_read": (C.c_int, [C.c_void_p, C.c_uint32, _u64p, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "ana_trace": (C.c_int, [C.c_void_p, C.c_uint32]),
     "ana_trace_read": (C.c_int, [C.c_void_p, _u32p, C.c_size_t, _u32p]),
+    "ana_probe_reread": (C.c_int, [C.c_int, C.c_uint64, C.c_uint32, C.POINTER(C.c_double)]),
     "ana_bpe_open": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
     "ana_bpe_bytes": (C.c_int, [C.POINTER(C.c_void_p)]),
     "ana_bpe_close": (None, [C.c_void_p]),
@@ -375,6 +376,15 @@ class Decoder:
         out = np.empty(n, dtype=np.float32)
         self._check(lib().ana_state(self.h, seq, layer, _p(out, C.c_float), n))
         return out
+
+
+def probe_reread(nbytes: int, reps: int = 20, device: int = 0) -> float:
+    """ana_probe_reread: GB/s of re-reading one device buffer of nbytes."""
+    g = C.c_double()
+    r = lib().ana_probe_reread(device, nbytes, reps, C.byref(g))
+    if r != 0:
+        raise AnaError(r, f"ana_probe_reread: {nbytes} bytes")
+    return g.value
 
 
 def truncate_at_eos(row: np.ndarray) -> np.ndarray:

@@ -1544,6 +1544,60 @@ extern "C" int ana_trace_read(ana_ctx* c, uint32_t* out, size_t cap, uint32_t di
   return ANA_OK;
 }
 
+// a streaming read of n4 float4s, grid-stride (16-byte loads, a wave's
+// loads 1 KB contiguous); the sum keeps the loads, and the store never
+// happens for the zero-filled buffer the probe reads
+__global__ __launch_bounds__(256) void k_stream_read(const float4* __restrict__ p, size_t n4, float* sink) {
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+    const float4 v = p[i];
+    acc.x += v.x;
+    acc.y += v.y;
+    acc.z += v.z;
+    acc.w += v.w;
+  }
+  const float sum = (acc.x + acc.y) + (acc.z + acc.w);
+  if (sum != 0.0f) sink[0] = sum;
+}
+
+extern "C" int ana_probe_reread(int device, uint64_t bytes, uint32_t reps, double* gbs) {
+  if (!gbs || reps == 0 || bytes < 4096 || bytes % 16) return ANA_EINVAL;
+  if (hipSetDevice(device) != hipSuccess) return ANA_EDEVICE;
+  void* buf = nullptr;
+  float* sink = nullptr;
+  hipStream_t st = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int r = ANA_EDEVICE;
+  if (hipMalloc(&buf, bytes) != hipSuccess) return ANA_ENOMEM;
+  if (hipMalloc(reinterpret_cast<void**>(&sink), 16) == hipSuccess && hipStreamCreate(&st) == hipSuccess &&
+      hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess &&
+      hipMemsetAsync(buf, 0, bytes, st) == hipSuccess) {
+    const size_t n4 = bytes / 16;
+    // one untimed pass brings the buffer into whatever cache holds it
+    hipLaunchKernelGGL(k_stream_read, dim3(8192), dim3(256), 0, st, static_cast<const float4*>(buf), n4, sink);
+    bool ok = hipGetLastError() == hipSuccess && hipEventRecord(e0, st) == hipSuccess;
+    for (uint32_t i = 0; ok && i < reps; i++) {
+      hipLaunchKernelGGL(k_stream_read, dim3(8192), dim3(256), 0, st, static_cast<const float4*>(buf), n4, sink);
+      ok = hipGetLastError() == hipSuccess;
+    }
+    float ms = 0.0f;
+    if (ok && hipEventRecord(e1, st) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
+        hipEventElapsedTime(&ms, e0, e1) == hipSuccess && ms > 0.0f) {
+      *gbs = (double)bytes * reps / (ms * 1e-3) / 1e9;
+      r = ANA_OK;
+    }
+  }
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (st) {
+    (void)hipStreamSynchronize(st);
+    (void)hipStreamDestroy(st);
+  }
+  if (sink) (void)hipFree(sink);
+  (void)hipFree(buf);
+  return r;
+}
+
 extern "C" int ana_state(ana_ctx* c, uint32_t seq, uint32_t layer, float* out, size_t n) {
   if (!c || !out) return ANA_EINVAL;
   if (seq >= c->max_seqs || layer > c->cfg.layers) return fail(c, ANA_EINVAL, "ana_state: no such sequence or layer");

@@ -407,6 +407,8 @@ def main() -> int:
                     help="with --configs-only: just this one config")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--ckpt", default=os.environ.get("ANA_BENCH_CKPT", "/tmp/ana_bench_fp100m.ftc2"))
+    ap.add_argument("--mall-probe", type=int, default=0,
+                    help="only print the re-read rate of device buffers from 32 MiB to 1 GiB (1/0)")
     ap.add_argument("--phase-trace", type=int, default=0,
                     help="only print k_decode1's per-phase stamp summary over this many traced steps (1..64)")
     a = ap.parse_args()
@@ -417,6 +419,13 @@ def main() -> int:
     c = cf.FP100M
     path = ensure_ckpt(c, a.ckpt)
     mode = a.numerics
+    if a.mall_probe:
+        # the cache levels by their re-read rates: eight 4 MB L2s (one an
+        # XCD), the 256 MB Infinity Cache, then HBM
+        print("| buffer | re-read rate |\n|---|---|")
+        for mib in (16, 32, 64, 128, 192, 256, 320, 512, 1024):
+            print(f"| {mib} MiB | {ana_amd.probe_reread(mib << 20, 20) / 1e3:.2f} TB/s |", flush=True)
+        return 0
     if a.phase_trace:
         print(run_phase_trace(path, c, a.phase_trace), flush=True)
         release_device()

@@ -222,6 +222,14 @@ int ana_prof_read(struct ana_ctx* ctx, uint32_t kind, uint64_t* launches, double
 int ana_trace(struct ana_ctx* ctx, uint32_t steps);
 int ana_trace_read(struct ana_ctx* ctx, uint32_t* out, size_t cap, uint32_t dims[3]);
 
+/* A measurement probe with no counterpart in the reference (no context):
+ * the rate of re-reading one zero-filled device buffer of `bytes` (at least
+ * 4096, a multiple of 16) `reps` times with a streaming float4 read over
+ * 8192 x 256 threads, after one untimed pass, in GB/s (HIP events). Where
+ * the buffer fits a cache level (the XCDs' L2s, the Infinity Cache), the
+ * rate is that level's; past it, HBM's. It allocates and frees its buffer. */
+int ana_probe_reread(int device, uint64_t bytes, uint32_t reps, double* gbs);
+
 /* The last error on ctx, or of the last failed ana_open when ctx is NULL. */
 const char* ana_error(const struct ana_ctx* ctx);
 

@@ -13,7 +13,10 @@ sequences to the oracle:
   step graphs instead of the persistent kernel, and K = 3072 products.
 - v3 (the 115M, arms on, ctx 256): B = 64, 128-token prompts, 128 sampled
   steps at temperature 0.8, top-k 40, top-p 0.9, seed 0 + b; exact mode, four
-  watched sequences' ids and final RNG words bit for bit. Its checkpoint
+  watched sequences' ids and final RNG words bit for bit; and fast_fp32
+  (the bench's cfg_v3: the head fused with the sampler), every row's picks
+  equal to S.pick's on a twin decoder's logits with the final RNG words,
+  and two watched sequences' logits within 1e-4. Its checkpoint
   carries trained-like vectors (norm gains 1 + N(0, 0.1^2), qk gains
   N(0, 0.1^2), sinks N(0, 1)) so the arms the config names are live.
 - next (the 115M, ctx 2048): B = 32, 1920-token prompts, 128 greedy steps
@@ -186,6 +189,62 @@ def test_config_v3_sampled(oracle, tmp_path):
                 o.pos += 1
         assert [int(t) for t in out[b]] == want, b
         assert np.array_equal(rng[b], r), b
+
+
+def test_config_v3_sampled_fast(oracle, tmp_path):
+    """BASELINE v3 as bench.py's cfg_v3 times it: fast_fp32, B = 64, 128
+    sampled steps (T 0.8, top-k 40, top-p 0.9) in one ana_generate call,
+    whose sampled steps run the LM head fused with the sampler (64 rows:
+    two 32-row blocks, every head workgroup resident). A twin decoder fed
+    the same tokens gives each step's logits: every one of the 64 rows'
+    128 picks equals S.pick's (the oracle's) on them with the row's own RNG,
+    and the final RNG words match bit for bit; two watched sequences'
+    logits are within 1e-4 of the oracle's, teacher-forced, after 32, 64
+    and 128 steps."""
+    c = cf.BPE100M_V3
+    path = _ckpt(tmp_path, c, "v3f", trained=True)
+    _threads(oracle)
+    m = oracle.Model(path)
+    n, plen, steps = 64, 128, 128
+    st = ana_amd.Settings(float(np.float32(0.8)), 40, float(np.float32(0.9)))
+    prompts = _prompts(c, n, plen)
+    seqs = list(range(n))
+    rng0 = np.ascontiguousarray(np.stack([ana_amd.rng_seeded(b) for b in range(n)]).astype(np.uint64))
+    watch = (0, 63)
+    checks = (31, 63, 127)
+    print(f"case config v3 fast_fp32: B {n}, prompt {plen}, {steps} sampled steps", flush=True)
+    with ana_amd.Decoder(path, max_seqs=n, numerics=ana_amd.FAST_FP32) as dec, \
+            ana_amd.Decoder(path, max_seqs=n, numerics=ana_amd.FAST_FP32) as twin:
+        for d_ in (dec, twin):
+            d_.feeds_n(seqs, [0] * n, [p[:-1] for p in prompts])
+        pos = np.full(n, plen - 1, dtype=np.uint32)
+        tok = np.array([int(p[-1]) for p in prompts], dtype=np.uint32)
+        rng = rng0.copy()
+        out = dec.generate(seqs, pos, tok, steps, st, rng)
+        r_or = [oracle.rng_seeded(b) for b in range(n)]
+        sts = {b: _oracle_prompt(oracle, m, prompts[b]) for b in watch}
+        t, p = tok.copy(), pos.copy()
+        worst = 0.0
+        for k in range(steps):
+            twin.feed(seqs, p, t)
+            lg = twin.logits(seqs)
+            for b in range(n):
+                want = oracle.pick(lg[b], st.temperature, st.top_k, st.top_p, r_or[b])
+                assert int(out[b, k]) == int(want), (k, b)
+            if k in checks:
+                for i, b in enumerate(watch):
+                    ref = sts[b].logits()
+                    e = rel_err(lg[b], ref)
+                    worst = max(worst, e)
+                    assert e <= TOL[ana_amd.FAST_FP32], (k, b, e)
+            for b in watch:
+                if k + 1 < steps:
+                    sts[b].feed(sts[b].pos, int(out[b, k]))
+                    sts[b].pos += 1
+            t, p = out[:, k].copy(), p + 1
+        for b in range(n):
+            assert np.array_equal(rng[b], r_or[b]), b
+    print(f"worst relative error {worst:.3e}", flush=True)
 
 
 @pytest.fixture(scope="module")
