@@ -1069,14 +1069,28 @@ __global__ __launch_bounds__(512) void k_attn_flash_bf(AttnArgs a, const AttnTil
 #pragma unroll
   for (int j = 0; j < NJ; j++) o[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   const uint32_t nkt = last / KT + 1;
-  for (uint32_t kt = 0; kt < nkt; kt++) {
-    const uint32_t k0 = kt * KT;
-    __syncthreads();   // the previous tile's K, V and P reads are done
-    for (uint32_t e = tid; e < (uint32_t)KT * (HD / 4); e += 512) {
-      const uint32_t s = e / (HD / 4), c4 = e % (HD / 4);
+  // this thread's float4s of a key tile's K and V rows (e = tid + 512 i:
+  // slot e / (HD / 4), columns 4 (e % (HD / 4)) ..), loaded a tile ahead so
+  // they are in flight through the tile before
+  constexpr int NE = KT * (HD / 4) / 512;
+  static_assert(NE >= 1 && NE * 512 == KT * (HD / 4), "whole float4s a thread");
+  float4 kr[NE], vr[NE];
+  auto load_tile = [&](uint32_t k0) {
+#pragma unroll
+    for (int i = 0; i < NE; i++) {
+      const uint32_t e = tid + 512 * i, s = e / (HD / 4), c4 = e % (HD / 4);
       const uint32_t slot = k0 + s <= last ? k0 + s : 0;
-      const float4 kv = *reinterpret_cast<const float4*>(Kr + (size_t)slot * d + h * HD + 4 * c4);
-      const float4 vv = *reinterpret_cast<const float4*>(Vr + (size_t)slot * d + h * HD + 4 * c4);
+      kr[i] = *reinterpret_cast<const float4*>(Kr + (size_t)slot * d + h * HD + 4 * c4);
+      vr[i] = *reinterpret_cast<const float4*>(Vr + (size_t)slot * d + h * HD + 4 * c4);
+    }
+  };
+  load_tile(0);
+  for (uint32_t kt = 0; kt < nkt; kt++) {
+    __syncthreads();   // the previous tile's K, V and P reads are done
+#pragma unroll
+    for (int i = 0; i < NE; i++) {
+      const uint32_t e = tid + 512 * i, s = e / (HD / 4), c4 = e % (HD / 4);
+      const float4 kv = kr[i], vv = vr[i];
       __bf16 kb[4] = {(__bf16)kv.x, (__bf16)kv.y, (__bf16)kv.z, (__bf16)kv.w};
       *reinterpret_cast<uint2*>(&Ks[s][4 * c4]) = *reinterpret_cast<const uint2*>(kb);
       Vt[4 * c4][s] = (__bf16)vv.x;
@@ -1084,6 +1098,8 @@ __global__ __launch_bounds__(512) void k_attn_flash_bf(AttnArgs a, const AttnTil
       Vt[4 * c4 + 2][s] = (__bf16)vv.z;
       Vt[4 * c4 + 3][s] = (__bf16)vv.w;
     }
+    if (kt + 1 < nkt) load_tile((kt + 1) * KT);
+    const uint32_t k0 = kt * KT;
     __syncthreads();
     // scores of the wave's 16 rows against the tile's 4 x 16 slots
     f32x4_t sc[4];
@@ -1109,8 +1125,7 @@ __global__ __launch_bounds__(512) void k_attn_flash_bf(AttnArgs a, const AttnTil
         if (slot > qpos) sc[j][r] = -INFINITY;
         mx = fmaxf(mx, sc[j][r]);
       }
-#pragma unroll
-      for (int s2 = 1; s2 < 16; s2 <<= 1) mx = fmaxf(mx, __shfl_xor(mx, s2, 64));
+      mx = row16_max(mx);
       const float mn = fmaxf(m[r], mx);   // finite: slot k0 <= qpos always
       const float al = __expf(m[r] - mn);
       float sum = 0.0f;
@@ -1120,8 +1135,7 @@ __global__ __launch_bounds__(512) void k_attn_flash_bf(AttnArgs a, const AttnTil
         sum += p;
         Ps[w][4 * g + r][16 * j + r16] = (__bf16)p;
       }
-#pragma unroll
-      for (int s2 = 1; s2 < 16; s2 <<= 1) sum += __shfl_xor(sum, s2, 64);
+      sum = row16_sum(sum);
       l[r] = l[r] * al + sum;
       m[r] = mn;
 #pragma unroll

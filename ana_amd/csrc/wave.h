@@ -20,6 +20,14 @@ __device__ __forceinline__ float row16_sum(float v) {
   v += dpp<0x140>(v);
   return v;
 }
+// the maximum over each row of 16 lanes, in every lane of the row
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  return v;
+}
 __device__ __forceinline__ float lane_f(float v, int l) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
