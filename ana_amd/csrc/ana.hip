@@ -34,6 +34,7 @@ struct ana_ctx {
   int mode = ANA_EXACT_FP32;         // numerics
   float* W = nullptr;                // parameters [P]
   uint16_t* Wh = nullptr;            // ANA_BF16: the parameters as bfloat16 [P]
+  uint16_t* Wp = nullptr;            // ANA_BF16: the persistent kernel's bf16 matrices that start off 16 bytes in Wh, on 16 bytes
   // ANA_BF16 keeps the first block's matrices in fp32: parameters in
   // [fp32_lo, fp32_hi) are read as fp32 in every mode (the first block's
   // rounding dominates the bf16 logits' error: alone it gives ~1.3e-2 of the
@@ -86,7 +87,7 @@ struct ana_ctx {
     int bf;                          // packed as bf16 (else fp32)
   };
   std::unordered_map<const float*, PkEnt> pk;
-  // the persistent one-sequence decode (ANA_FAST_FP32): its layer table,
+  // the persistent one-sequence decode (ANA_FAST_FP32, ANA_BF16): its layer table,
   // exchange entries (two sets of ll_par), control words, grid and the
   // epoch its next launch starts from
   bool persist = false, persist_off = false;
@@ -213,7 +214,7 @@ static void release(ana_ctx* c) {
   (void)hipSetDevice(c->device);
   if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
   if (c->gexec_n) (void)hipGraphExecDestroy(c->gexec_n);
-  void* ps[] = {c->d_play, c->d_ll, c->d_ctl, c->d_trace, c->W, c->Wh, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
+  void* ps[] = {c->d_play, c->d_ll, c->d_ctl, c->d_trace, c->W, c->Wh, c->Wp, c->d_part, c->d_gla, c->state, c->xs, c->X, c->XA, c->XN, c->QKV, c->Z, c->O, c->HH, c->LG,
                 c->d_seq, c->d_pos, c->d_tok, c->d_pick, c->d_out, c->d_step, c->d_rng, c->d_amax,
                 c->d_ss, c->d_pm, c->d_gtab, c->d_grun, c->d_atab, c->d_rseq, c->d_rpos, c->SC, c->d_tgt, c->d_ce, c->d_stat, c->d_rcp,
                 c->d_sah, c->d_hh, c->d_rsc, c->PK, c->d_hpc, c->d_hpctl, c->d_oh, c->d_nxh, c->d_ssp};
@@ -371,7 +372,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
         (e = hipMemsetAsync(c->d_hpctl, 0, 4, c->st)) != hipSuccess)
       return bad(e);
   }
-  if (c->mode == ANA_FAST_FP32 && (e = persist_setup(c)) != hipSuccess) return bad(e);
+  if ((c->mode == ANA_FAST_FP32 || c->mode == ANA_BF16) && (e = persist_setup(c)) != hipSuccess) return bad(e);
   // ANA_PERSIST=0 keeps one-sequence decode on the captured graphs
   if (const char* pv = getenv("ANA_PERSIST")) c->persist_off = strcmp(pv, "0") == 0;
   if ((e = launch_zero(c->state, c->seq_stride * c->max_seqs, c->st)) != hipSuccess) return bad(e);
@@ -608,6 +609,9 @@ static hipError_t persist_setup(ana_ctx* c) {
   if (rate_khz <= 0) return hipSuccess;
   c->p_tmo = (uint64_t)rate_khz * 2000ull;
   const uint32_t d = cf.d, f = cf.f, hd = d / cf.heads, np = decode1_pieces(cf, G);
+  // bf16 pieces are 16 bytes of eight values: rows start on 16 bytes when
+  // d and f are multiples of 8 and the matrix does
+  if (c->Wh && (d % 8 || f % 8)) return hipSuccess;
   std::vector<PLayer> t(cf.layers);
   uint64_t en = 0;
   for (uint32_t l = 0; l < cf.layers; l++) {
@@ -623,6 +627,37 @@ static hipError_t persist_setup(ana_ctx* c) {
     P.e_xa = en; en += d;
     P.e_hh = en; en += f;
     P.e_x = en; en += d;
+  }
+  if (c->Wh) {
+    // the bf16 matrices past the first layer: in place where they start on
+    // 16 bytes, else copied into Wp on 16 bytes (in the 115M's layout the
+    // attention layers' 12 sinks shift every later matrix by 8 bytes)
+    struct Mat { uint64_t off, n, *at; };
+    std::vector<Mat> ms;
+    for (uint32_t l = 1; l < cf.layers; l++) {
+      const Blk& b = c->blk[l];
+      PLayer& P = t[l];
+      ms.push_back({b.wq, 3ull * d * d, &P.hq});
+      if (b.gla) ms.push_back({b.wa, (uint64_t)d * d, &P.ha});
+      ms.push_back({b.wo, (uint64_t)d * d, &P.ho});
+      ms.push_back({b.wg, 2ull * f * d, &P.hg});
+      ms.push_back({b.wd, (uint64_t)d * f, &P.hd});
+    }
+    uint64_t need = 0;
+    for (const Mat& m : ms)
+      if (m.off % 8) need += (m.n + 7) & ~7ull;
+    if (need && (e = dalloc(&c->Wp, need)) != hipSuccess) return e;
+    uint64_t at = 0;
+    for (const Mat& m : ms) {
+      if (m.off % 8 == 0) {
+        *m.at = (uint64_t)(uintptr_t)(c->Wh + m.off);
+        continue;
+      }
+      if ((e = hipMemcpyAsync(c->Wp + at, c->Wh + m.off, 2 * m.n, hipMemcpyDeviceToDevice, c->st)) != hipSuccess)
+        return e;
+      *m.at = (uint64_t)(uintptr_t)(c->Wp + at);
+      at += (m.n + 7) & ~7ull;
+    }
   }
   c->e_key = en;
   en += G;
@@ -640,12 +675,14 @@ static hipError_t persist_setup(ana_ctx* c) {
 }
 
 // algorithmic bytes of one decode step of one sequence: every weight once
-// (the head reads all of the tied embedding), the GLA states read and
-// written, the live K and V rows read and the new ones written
+// (the head reads all of the tied embedding; in ANA_BF16 two bytes a weight
+// outside the fp32 block), the GLA states read and written, the live K and
+// V rows read and the new ones written
 static double step_bytes(const ana_ctx* c, uint64_t pos) {
   const ana_config& cf = c->cfg;
   const double hd = (double)cf.d / cf.heads;
-  double b = 4.0 * (double)(c->P - (uint64_t)cf.vocab * cf.d + cf.d) + 4.0 * cf.vocab * cf.d;
+  double b = c->Wh ? 2.0 * (double)(c->P + cf.d) + 2.0 * (double)(c->fp32_hi - c->fp32_lo)
+                   : 4.0 * (double)(c->P + cf.d);
   const uint64_t live = std::min<uint64_t>(pos, cf.ctx - 1) + 1;
   for (uint32_t l = 0; l < cf.layers; l++)
     b += c->blk[l].gla ? 8.0 * cf.heads * hd * hd : 4.0 * cf.d * (2.0 * live + 2.0);
@@ -1262,6 +1299,7 @@ static int generate_persist(ana_ctx* c, const uint32_t* pos, uint32_t steps, uin
       HIPCHK(c, launch_zero_u32(c->d_ctl, 4, c->st));
       PersistArgs pa{};
       pa.W = c->W;
+      pa.Wh = c->Wh;
       pa.lay = c->d_play;
       pa.L = c->cfg.layers; pa.d = c->cfg.d; pa.f = c->cfg.f; pa.heads = c->cfg.heads; pa.ctx = c->cfg.ctx;
       pa.vocab = c->cfg.vocab; pa.rglru = c->cfg.rglru; pa.qk = c->cfg.qk; pa.sinks = c->cfg.sinks;

@@ -402,12 +402,17 @@ hipError_t launch_zero_u64(unsigned long long* p, uint32_t n, hipStream_t st);
 // state, and its exchange slots (entries into one parity's set).
 struct PLayer {
   uint64_t ra, wq, wa, lam, gq, gk, sink, wo, rf, wg, wd;
+  // the bf16 matrices' device addresses, each on 16 bytes (q|k|v, z, Wo,
+  // gate|up, down), or 0 where the layer reads fp32
+  uint64_t hq, ha, ho, hg, hd;
   uint64_t soff;
   uint64_t e_qkv, e_part, e_o, e_xa, e_hh, e_x;
   uint32_t gla, pad;
 };
 struct PersistArgs {
   const float* W;
+  const uint16_t* Wh;       // bf16 weights (past the first layer: PLayer's h* addresses; the head: the
+                            // tied embedding here, on 16 bytes), or null for fp32
   const PLayer* lay;        // [L], device
   uint32_t L, d, f, heads, ctx, vocab, rglru, qk, sinks, np;  // np: attention pieces a head
   uint64_t fin;             // the final norm's gains

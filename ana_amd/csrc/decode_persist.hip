@@ -140,6 +140,11 @@ __device__ __forceinline__ float dot4(float4 a, float4 b, float acc) {
   acc = fmaf(a.z, b.z, acc);
   return fmaf(a.w, b.w, acc);
 }
+// four bf16 (two a word, the lower half first) as floats
+__device__ __forceinline__ float4 bf4(uint32_t a, uint32_t b) {
+  return make_float4(__uint_as_float(a << 16), __uint_as_float(a & 0xFFFF0000u), __uint_as_float(b << 16),
+                     __uint_as_float(b & 0xFFFF0000u));
+}
 __device__ __forceinline__ float4 mul4(float4 a, float4 b) {
   return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
 }
@@ -172,21 +177,31 @@ typedef __attribute__((address_space(3))) void lds_void;
 // (four waves) a CU.
 //
 // A weight piece is 1 KB: a wave's global_load_lds_dwordx4 moves lane l's
-// 16 bytes to byte 16 l of the piece. A row of K = d is NFD pieces, lane
-// l's float4 of piece j at k = 4 (l + 64 j). Each phase's pieces are
-// numbered 0 .. P - 1 and wave u issues pieces u, u + 4, ....
+// 16 bytes to byte 16 l of the piece. In fp32 a row of K = d is NFD pieces,
+// lane l's float4 of piece j at k = 4 (l + 64 j); in bf16 (the first layer
+// aside) it is (NFD + 1) / 2 pieces, lane l's eight values of piece j at
+// k = 8 (l + 64 j). Each phase's pieces are numbered 0 .. P - 1 and wave u
+// issues pieces u, u + 4, ....
+//
+// WT: the weights' type past the first layer and in the head (0 fp32 from
+// a.W; 1 bf16, the layers' matrices at the PLayer h* addresses and the tied
+// embedding at a.Wh); gains, lambdas and the first layer are fp32 from a.W
+// in either build.
 //
 // TR: the trace build. Four clock readings a phase (the clock's low 32
 // bits) go into LDS by thread 0: the phase's start; its inputs all seen;
 // all waves met after their waits; its outputs published. The workgroup copies a step's stamps to a.trace
 // after the pick, for the first a.trace_steps steps.
-template <int HD, int NFD, int NFF, bool TR>
+template <int HD, int NFD, int NFF, bool TR, int WT>
 __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   constexpr int QD = HD / 4;            // attention: dims a score lane holds (4 lanes a slot)
   constexpr int C4 = HD / 4;            // float4 columns of a head
   constexpr int GS = kPT / C4;          // attention V lanes: slot groups
   constexpr int KPASS = 2;              // 64 slots a pass: pieces of up to 128 slots
-  constexpr int HBR = 5;                // head rows a wave a batch
+  constexpr int HBR = WT ? 8 : 5;       // head rows a wave a batch (its pieces fill a buffer)
+  // a bf16 row's pieces: 512 values each (lane l's eight at k = 8 (l + 64 j))
+  constexpr int PDH = (NFD + 1) / 2, PFH = (NFF + 1) / 2;
+  constexpr int XN = NFD > 2 * PDH ? NFD : 2 * PDH;   // float4s a lane holds of a d vector
   constexpr uint32_t WB = 4096;         // float4s a weight buffer (64 KB)
   constexpr uint32_t KVQ = KPASS * C4;  // pieces of an attention unit's K (and of its V)
   constexpr uint32_t KV_V = KVQ * 64;   // V's float4 offset in an attention buffer
@@ -242,18 +257,36 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   };
   // one 1 KB piece: lane l's 16 bytes from src (this lane's address) to
   // float4 at * 64 + l of the buffer
-  auto piece = [&](const float* src, float4* buf, uint32_t at) {
+  auto piece = [&](const void* src, float4* buf, uint32_t at) {
     __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)&buf[at * 64], 16, 0, 0);
+  };
+  // ---- weights in either layout: WL 0 fp32 (a row of K is K / 256
+  // pieces, lane l's float4 of piece j at k = 4 (l + 64 j)), WL 1 bf16 (a
+  // row of K is K / 512 pieces, rounded up, lane l's eight values of piece j
+  // at k = 8 (l + 64 j)). Every row takes the build's count of pieces (d <=
+  // 256 NFD, f <= 256 NFF): lanes past K read the row's start, L2-resident
+  // already, and meet zeros on the activation side
+  auto npd = [&](auto WLc) -> uint32_t { return decltype(WLc)::value ? PDH : NFD; };   // a K = d row
+  auto npf = [&](auto WLc) -> uint32_t { return decltype(WLc)::value ? PFH : NFF; };   // a K = f row
+  auto kof = [&](auto WLc, uint32_t j) -> uint32_t {
+    return decltype(WLc)::value ? 8 * (lane + 64 * j) : 4 * (lane + 64 * j);
+  };
+  // this lane's part of row r (rows of K), piece j, of the matrix at
+  // parameter offset off (fp32) or at device address hp (bf16)
+  auto wsrc = [&](auto WLc, uint64_t off, uint64_t hp, size_t r, uint32_t K, uint32_t j) -> const void* {
+    const uint32_t k = kof(WLc, j);
+    const size_t e = r * K + (k < K ? k : 0);
+    if constexpr (decltype(WLc)::value) return reinterpret_cast<const uint16_t*>(hp) + e;
+    else return W + off + e;
   };
   // ---- the pieces of each phase (issued by the loading waves)
   auto qkv_rows = [&](const PLayer& P) { return P.gla ? 4 * d : 3 * d; };
-  auto dma_qkv = [&](const PLayer& P, float4* buf) {
-    const uint32_t R = qkv_rows(P), RQ = (R + G - 1) / G, NP = RQ * NFD;
+  auto dma_qkv = [&](auto WLc, const PLayer& P, float4* buf) {
+    const uint32_t PD = npd(WLc);
+    const uint32_t R = qkv_rows(P), RQ = (R + G - 1) / G, NP = RQ * PD;
     for (uint32_t q = wv; q < NP; q += 4) {
-      const uint32_t i = q / NFD, j = q % NFD, r = min(w * RQ + i, R - 1);
-      const float* row = W + (r < 3 * d ? P.wq + (size_t)r * d : P.wa + (size_t)(r - 3 * d) * d);
-      const uint32_t k = 4 * (lane + 64 * j);
-      piece(row + (k < d ? k : 0), buf, q);
+      const uint32_t i = q / PD, j = q % PD, r = min(w * RQ + i, R - 1);
+      piece(r < 3 * d ? wsrc(WLc, P.wq, P.hq, r, d, j) : wsrc(WLc, P.wa, P.ha, r - 3 * d, d, j), buf, q);
     }
   };
   // an attention unit's K rows then V rows of its piece of the ring: slot i
@@ -272,40 +305,39 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       piece((q < KVQ ? Kr : Vr) + off, buf, q);
     }
   };
-  auto dma_wo = [&](const PLayer& P, float4* buf) {
-    const uint32_t NP = RO * NFD;
+  auto dma_wo = [&](auto WLc, const PLayer& P, float4* buf) {
+    const uint32_t PD = npd(WLc), NP = RO * PD;
     for (uint32_t q = wv; q < NP; q += 4) {
-      const uint32_t i = q / NFD, j = q % NFD, r = min(w * RO + i, d - 1);
-      const uint32_t k = 4 * (lane + 64 * j);
-      piece(W + P.wo + (size_t)r * d + (k < d ? k : 0), buf, q);
+      const uint32_t i = q / PD, j = q % PD, r = min(w * RO + i, d - 1);
+      piece(wsrc(WLc, P.wo, P.ho, r, d, j), buf, q);
     }
   };
-  auto dma_gu = [&](const PLayer& P, float4* buf) {
-    const uint32_t NP = RGp * 2 * NFD;
+  auto dma_gu = [&](auto WLc, const PLayer& P, float4* buf) {
+    const uint32_t PD = npd(WLc), NP = RGp * 2 * PD;
     for (uint32_t q = wv; q < NP; q += 4) {
-      const uint32_t pi = q / (2 * NFD), gu = (q / NFD) & 1, j = q % NFD, jp = min(w * RGp + pi, f - 1);
-      const uint32_t k = 4 * (lane + 64 * j);
-      piece(W + P.wg + (gu ? (size_t)f * d : 0) + (size_t)jp * d + (k < d ? k : 0), buf, q);
+      const uint32_t pi = q / (2 * PD), gu = (q / PD) & 1, j = q % PD, jp = min(w * RGp + pi, f - 1);
+      const uint64_t up = gu ? (uint64_t)f * d : 0;   // up's rows follow gate's: up values on
+      piece(wsrc(WLc, P.wg + up, P.hg + sizeof(uint16_t) * up, jp, d, j), buf, q);   // (hg: a byte address)
     }
   };
-  auto dma_wd = [&](const PLayer& P, float4* buf) {
-    const uint32_t NP = RO * NFF;
+  auto dma_wd = [&](auto WLc, const PLayer& P, float4* buf) {
+    const uint32_t PF = npf(WLc), NP = RO * PF;
     for (uint32_t q = wv; q < NP; q += 4) {
-      const uint32_t i = q / NFF, j = q % NFF, r = min(w * RO + i, d - 1);
-      const uint32_t k = 4 * (lane + 64 * j);
-      piece(W + P.wd + (size_t)r * f + (k < f ? k : 0), buf, q);
+      const uint32_t i = q / PF, j = q % PF, r = min(w * RO + i, d - 1);
+      piece(wsrc(WLc, P.wd, P.hd, r, f, j), buf, q);
     }
   };
   // the head's rows of batch b for wave u: h0 + u + 4 (b HBR + i), at
-  // pieces (u HBR + i) NFD + j (row 0 stands in past h1; its result is not
+  // pieces (u HBR + i) HPD + j (row 0 stands in past h1; its result is not
   // used). Batch 0 of every wave, by the loading waves:
+  constexpr IC<WT> HW{};                 // the head's layout (the mode's)
+  constexpr int HPD = WT ? PDH : NFD;     // its pieces a row
   auto dma_head0 = [&](float4* buf) {
-    const uint32_t NP = 4 * HBR * NFD;
+    const uint32_t NP = 4 * HBR * HPD;
     for (uint32_t q = wv; q < NP; q += 4) {
-      const uint32_t rl = q / NFD, j = q % NFD, u = rl / HBR, i = rl % HBR;
+      const uint32_t rl = q / HPD, j = q % HPD, u = rl / HBR, i = rl % HBR;
       const uint32_t r = h0 + u + 4 * i, rr = r < h1 ? r : 0u;
-      const uint32_t k = 4 * (lane + 64 * j);
-      piece(W + (size_t)rr * d + (k < d ? k : 0), buf, q);
+      piece(wsrc(HW, 0, (uint64_t)a.Wh, rr, d, j), buf, q);
     }
   };
   // ... and batch b of this wave's own rows, by the wave itself
@@ -314,38 +346,55 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     for (int i = 0; i < HBR; i++) {
       const uint32_t r = h0 + wv + 4 * (b * HBR + i), rr = r < h1 ? r : 0u;
 #pragma unroll
-      for (int j = 0; j < NFD; j++) {
-        const uint32_t k = 4 * (lane + 64 * j);
-        piece(W + (size_t)rr * d + (k < d ? k : 0), buf, (wv * HBR + i) * NFD + j);
-      }
+      for (int j = 0; j < HPD; j++) piece(wsrc(HW, 0, (uint64_t)a.Wh, rr, d, j), buf, (wv * HBR + i) * HPD + j);
     }
   };
-  // this lane's float4 j of xs[0..n) (zero past n)
-  auto xs4 = [&](uint32_t j, uint32_t n) {
-    const uint32_t k = 4 * (lane + 64 * j);
+  // this lane's float4 i of a vector in layout WL: fp32 at k = 4 (l + 64 i)
+  // (piece i), bf16 at k = 8 (l + 64 (i / 2)) + 4 (i % 2) (half i % 2 of
+  // piece i / 2); XW of them cover a d vector
+  auto kx = [&](auto WLc, uint32_t i) -> uint32_t {
+    return decltype(WLc)::value ? 8 * (lane + 64 * (i >> 1)) + 4 * (i & 1) : 4 * (lane + 64 * i);
+  };
+  // this lane's float4 i of xs[0..n) in layout WL (zero past n)
+  auto xsw = [&](auto WLc, uint32_t i, uint32_t n) {
+    const uint32_t k = kx(WLc, i);
     return k < n ? *reinterpret_cast<const float4*>(&xs[k]) : zero4();
   };
-  // this lane's float4s of a gain vector at W + off (d entries)
-  auto load_g4 = [&](float4 (&g)[NFD], uint64_t off) {
+  // this lane's float4s of a gain vector at W + off (d entries; gains are
+  // fp32 in every mode)
+  auto load_g = [&](auto WLc, float4 (&g)[XN], uint64_t off) {
+    constexpr int XW = decltype(WLc)::value ? 2 * PDH : NFD;
 #pragma unroll
-    for (int j = 0; j < NFD; j++) {
-      const uint32_t k = 4 * (lane + 64 * j);
-      g[j] = k < d ? *reinterpret_cast<const float4*>(W + off + k) : zero4();
+    for (int i = 0; i < XN; i++) {
+      const uint32_t k = kx(WLc, i);
+      g[i] = i < XW && k < d ? *reinterpret_cast<const float4*>(W + off + k) : zero4();
     }
   };
   // the RMSNorm of xs[0..d) folded into the products: xg = x g (this
   // lane's float4s), and the scale 1 / sqrt(mean(x^2) + 1e-5), which every
   // wave forms from the whole row itself
-  auto norm_fold = [&](const float4 (&g)[NFD], float4 (&xg)[NFD]) -> float {
+  auto norm_fold = [&](auto WLc, const float4 (&g)[XN], float4 (&xg)[XN]) -> float {
+    constexpr int XW = decltype(WLc)::value ? 2 * PDH : NFD;
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < NFD; j++) {
-      const float4 x = xs4(j, d);
+    for (int i = 0; i < XW; i++) {
+      const float4 x = xsw(WLc, i, d);
       ss = dot4(x, x, ss);
-      xg[j] = mul4(x, g[j]);
+      xg[i] = mul4(x, g[i]);
     }
     ss = wsum(ss);
     return rsq(ss * invd + 1.0e-5f);
+  };
+  // acc + this lane's part of piece pc of buf times x (its float4s of that
+  // piece: one in fp32, two in bf16)
+  auto dotw = [&](auto WLc, const float4* buf, uint32_t pc, const float4* x, float acc) -> float {
+    if constexpr (decltype(WLc)::value) {
+      const uint4 u = reinterpret_cast<const uint4*>(buf)[pc * 64 + lane];
+      acc = dot4(bf4(u.x, u.y), x[0], acc);
+      return dot4(bf4(u.z, u.w), x[1], acc);
+    } else {
+      return dot4(buf[pc * 64 + lane], x[0], acc);
+    }
   };
   auto fail_wg = [&]() {
     if (tid == 0) {
@@ -378,10 +427,16 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     ph++;
   };
 
-  // one layer, compiled for the buffer parity its first phase reads (B);
-  // false when a wait failed
-  auto layer = [&](auto B, uint32_t l, uint32_t ep, unsigned long long* LL) -> bool {
+  // one layer, compiled for the buffer parity its first phase reads (B)
+  // and the layout of its weights (WLc); false when a wait failed
+  auto layer = [&](auto B, auto WLc, uint32_t l, uint32_t ep, unsigned long long* LL) -> bool {
     constexpr int PB = decltype(B)::value;
+    constexpr bool WL = decltype(WLc)::value;
+    constexpr int PDc = WL ? PDH : NFD;           // pieces of a K = d row
+    constexpr int PFc = WL ? PFH : NFF;           // of a K = f row
+    constexpr int XW = WL ? 2 * PDH : NFD;        // float4s a lane holds of a d vector
+    constexpr int XF = WL ? 2 * PFH : NFF;        // of an f vector
+    constexpr int XS = WL ? 2 : 1;                // float4s a lane holds of a piece
     float4* bufB = bufp(IC<PB>{});
     float4* bufN = bufp(IC<1 - PB>{});
     const PLayer P = Ls[l];
@@ -389,8 +444,8 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     // wave wv the rows wv + 4 i
     lds_barrier();
     TS(0);
-    float4 g4[NFD];
-    load_g4(g4, P.ra);
+    float4 g4[XN];
+    load_g(WLc, g4, P.ra);
     float svr = 0.0f, lamr = 0.0f, gqr = 0.0f, gkr = 0.0f, sinkr = 0.0f;
     // the mix's own inputs that do not depend on this token: GLA column
     // 4 cb + wv of head h (lane a: row a of S) and the RG-LRU lambdas; the
@@ -422,8 +477,8 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     }
     if (!meet()) return false;
     {
-      float4 xg[NFD];
-      const float rs = norm_fold(g4, xg);
+      float4 xg[XN];
+      const float rs = norm_fold(WLc, g4, xg);
       const uint32_t R = qkv_rows(P), RQ = (R + G - 1) / G;
       float res[4];
 #pragma unroll
@@ -431,7 +486,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         const uint32_t i = min(wv + 4 * kk, RQ - 1);
         float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < NFD; j++) acc = dot4(bufB[(i * NFD + j) * 64 + lane], xg[j], acc);
+        for (int j = 0; j < PDc; j++) acc = dotw(WLc, bufB, i * PDc + j, &xg[XS * j], acc);
         res[kk] = wsum(acc) * rs;
       }
       if (lane < 4) {
@@ -444,7 +499,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     // ---- the mix (an attention unit's K and V pieces in bufN)
     lds_barrier();
     TS(0);
-    dma_wo(P, bufB);
+    dma_wo(WLc, P, bufB);
     if (P.gla) {
       {
         bool ok = true;
@@ -647,15 +702,18 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     // ---- xa = x + Wo o (Wo in bufB)
     lds_barrier();
     TS(0);
-    float4 gf[NFD];
-    load_g4(gf, P.rf);
-    dma_gu(P, bufN);
+    float4 gf[XN];
+    load_g(WLc, gf, P.rf);
+    dma_gu(WLc, P, bufN);
     gathered(poll_gather<PEX>(LL, d, ep, Ident{P.e_o}, xs, a.ctl, a.tmo));
     if (!meet()) return false;
     if (orow_ok) {
+      float4 xv[XW];
+#pragma unroll
+      for (int i = 0; i < XW; i++) xv[i] = xsw(WLc, i, d);
       float acc = 0.0f;
 #pragma unroll
-      for (int j = 0; j < NFD; j++) acc = dot4(bufB[(wv * NFD + j) * 64 + lane], xs4(j, d), acc);
+      for (int j = 0; j < PDc; j++) acc = dotw(WLc, bufB, wv * PDc + j, &xv[XS * j], acc);
       xa_own = x_own + wsum(acc);
       if (lane == 0) ll_put(LL + P.e_xa + orow, xa_own, ep);
     }
@@ -664,21 +722,21 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     // wv + 4 i
     lds_barrier();
     TS(0);
-    dma_wd(P, bufB);
+    dma_wd(WLc, P, bufB);
     gathered(poll_gather<PEX>(LL, d, ep, Ident{P.e_xa}, xs, a.ctl, a.tmo));
     if (!meet()) return false;
     {
-      float4 xg[NFD];
-      const float rs = norm_fold(gf, xg);
+      float4 xg[XN];
+      const float rs = norm_fold(WLc, gf, xg);
       float hv[2];
 #pragma unroll
       for (int i = 0; i < 2; i++) {
         const uint32_t pi = min(wv + 4 * i, RGp - 1);
         float g = 0.0f, u = 0.0f;
 #pragma unroll
-        for (int j = 0; j < NFD; j++) {
-          g = dot4(bufN[((pi * 2 + 0) * NFD + j) * 64 + lane], xg[j], g);
-          u = dot4(bufN[((pi * 2 + 1) * NFD + j) * 64 + lane], xg[j], u);
+        for (int j = 0; j < PDc; j++) {
+          g = dotw(WLc, bufN, (pi * 2 + 0) * PDc + j, &xg[XS * j], g);
+          u = dotw(WLc, bufN, (pi * 2 + 1) * PDc + j, &xg[XS * j], u);
         }
         g = wsum(g) * rs;
         u = wsum(u) * rs;
@@ -693,14 +751,17 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     // ---- x = xa + Wd hh (Wd in bufB)
     lds_barrier();
     TS(0);
-    if (l + 1 < L) dma_qkv(Ls[l + 1], bufN);
+    if (l + 1 < L) dma_qkv(IC<WT>{}, Ls[l + 1], bufN);   // (layers past the first: the mode's layout)
     else dma_head0(bufN);
     gathered(poll_gather<PEF>(LL, f, ep, Ident{P.e_hh}, xs, a.ctl, a.tmo));
     if (!meet()) return false;
     if (orow_ok) {
+      float4 xv[XF];
+#pragma unroll
+      for (int i = 0; i < XF; i++) xv[i] = xsw(WLc, i, f);
       float acc = 0.0f;
 #pragma unroll
-      for (int j = 0; j < NFF; j++) acc = dot4(bufB[(wv * NFF + j) * 64 + lane], xs4(j, f), acc);
+      for (int j = 0; j < PFc; j++) acc = dotw(WLc, bufB, wv * PFc + j, &xv[XS * j], acc);
       x_own = xa_own + wsum(acc);
       if (lane == 0) ll_put(LL + P.e_x + orow, x_own, ep);
     }
@@ -717,19 +778,19 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     float4* b1 = bufp(IC<1 - PB>{});
     lds_barrier();
     TS(0);
-    float4 gf[NFD];
-    load_g4(gf, a.fin);
+    float4 gf[XN];
+    load_g(HW, gf, a.fin);
     gathered(poll_gather<PEX>(LL, d, ep, Ident{Ls[L - 1].e_x}, xs, a.ctl, a.tmo));
     if (!meet()) return false;
-    float4 xg[NFD];
-    const float rs = norm_fold(gf, xg);
+    float4 xg[XN];
+    const float rs = norm_fold(HW, gf, xg);
     unsigned long long best = 0ull;
     auto rows = [&](float4* cur, uint32_t b) {
 #pragma unroll
       for (int i = 0; i < HBR; i++) {
         float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < NFD; j++) acc = dot4(cur[((wv * HBR + i) * NFD + j) * 64 + lane], xg[j], acc);
+        for (int j = 0; j < HPD; j++) acc = dotw(HW, cur, (wv * HBR + i) * HPD + j, &xg[(WT ? 2 : 1) * j], acc);
         acc = wsum(acc) * rs;
         const uint32_t r = h0 + wv + 4 * (b * HBR + i);
         if (lane == 0 && r < h1) {
@@ -745,7 +806,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     for (uint32_t b = 0; b < nhb; b += 2) {
       if (b + 1 < nhb) {
         dma_head_own(b + 1, b1);
-        if (b > 0) __builtin_amdgcn_s_waitcnt(ANA_VM(HBR * NFD));
+        if (b > 0) __builtin_amdgcn_s_waitcnt(ANA_VM(HBR * HPD));
       } else if (b > 0) {
         __builtin_amdgcn_s_waitcnt(0);
       }
@@ -753,7 +814,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       if (b + 1 < nhb) {
         if (b + 2 < nhb) {
           dma_head_own(b + 2, b0);
-          __builtin_amdgcn_s_waitcnt(ANA_VM(HBR * NFD));
+          __builtin_amdgcn_s_waitcnt(ANA_VM(HBR * HPD));
         } else {
           __builtin_amdgcn_s_waitcnt(0);
         }
@@ -789,7 +850,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     constexpr int PB = decltype(B)::value;
     lds_barrier();
     TS(0);
-    dma_qkv(Ls[0], bufp(IC<PB>{}));
+    dma_qkv(IC<0>{}, Ls[0], bufp(IC<PB>{}));   // (the first layer: fp32 in every mode)
     {
       const uint32_t pt = tid;
       unsigned long long kv[PES];
@@ -838,7 +899,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     return r;
   };
 
-  dma_qkv(Ls[0], wbA);
+  dma_qkv(IC<0>{}, Ls[0], wbA);
   __builtin_amdgcn_s_waitcnt(0);
   uint32_t pb = 0;          // the buffer parity the next phase reads
   uint32_t k = 0;
@@ -848,7 +909,10 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     unsigned long long* LL = a.ll + (size_t)(ep & 1) * a.ll_par;
     ph = 0;
     for (uint32_t l = 0; l < L; l++) {
-      const bool ok = pb ? layer(IC<1>{}, l, ep, LL) : layer(IC<0>{}, l, ep, LL);
+      // the first layer's weights are fp32 in every mode, the rest the mode's
+      bool ok;
+      if (l == 0) ok = pb ? layer(IC<1>{}, IC<0>{}, l, ep, LL) : layer(IC<0>{}, IC<0>{}, l, ep, LL);
+      else ok = pb ? layer(IC<1>{}, IC<WT>{}, l, ep, LL) : layer(IC<0>{}, IC<WT>{}, l, ep, LL);
       if (!ok) return;
       pb ^= 1;   // five buffer phases a layer
     }
@@ -925,13 +989,18 @@ hipError_t launch_decode1(const PersistArgs& a, uint32_t G, hipStream_t st) {
   if (a.f > 2048) return hipErrorInvalidValue;
   const bool tr = a.trace && a.trace_steps;
   if (tr && a.trace_phases > kMaxTracePhases) return hipErrorInvalidValue;
-#define L_(H)                                                                                                     \
-  return hipLaunchCooperativeKernel(tr ? (const void*)k_decode1<H, 3, 8, true> : (const void*)k_decode1<H, 3, 8, false>, \
-                                    dim3(G), dim3(kPT), args, 0, st)
+  // bf16 weights: 16-byte pieces of eight values, so rows of K = d and
+  // K = f start on 16 bytes when d and f are multiples of 8 (the host places
+  // every matrix on 16 bytes)
+  const bool bf = a.Wh != nullptr;
+  if (bf && (a.d % 8 || a.f % 8)) return hipErrorInvalidValue;
+#define K_(H, T) (bf ? (const void*)k_decode1<H, 3, 8, T, 1> : (const void*)k_decode1<H, 3, 8, T, 0>)
+#define L_(H) return hipLaunchCooperativeKernel(tr ? K_(H, true) : K_(H, false), dim3(G), dim3(kPT), args, 0, st)
   if (hd == 64) L_(64);
   if (hd == 32) L_(32);
   if (hd == 16) L_(16);
 #undef L_
+#undef K_
   return hipErrorInvalidValue;
 }
 

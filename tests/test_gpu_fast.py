@@ -498,31 +498,38 @@ def test_fast_decode_split_after_wrap(oracle, tmp_path, mode):
     assert worst <= TOL[mode], worst
 
 
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("model", ["small", "mid", "115m"])
-def test_fast_persistent_decode(oracle, small_ckpt, mid_ckpt, big_ckpt, model):
-    """The one-sequence greedy loop of ANA_FAST_FP32 as one persistent
-    launch per call (every phase of every step in one cooperative kernel,
-    phases exchanging epoch-tagged entries): each pick, teacher-forced into
-    the oracle, is within tolerance of the oracle's maximum logit, and the
-    logits after the call (the residual row it leaves) within 1e-4 of the
-    oracle's; the same with the captured graphs (ANA_PERSIST=0) for
-    comparison. The 115M case runs past the first 128 positions, so the
+def test_fast_persistent_decode(oracle, small_ckpt, mid_ckpt, big_ckpt, model, mode):
+    """The one-sequence greedy loop of a fast mode as one persistent launch
+    per call (every phase of every step in one cooperative kernel, phases
+    exchanging epoch-tagged entries; in bf16 the weights past the first
+    layer and the head read as bf16 pieces): each pick, teacher-forced into
+    the oracle, is within the mode's tolerance of the oracle's maximum
+    logit, and the logits after the call (the residual row it leaves)
+    within it of the oracle's; the same with the captured graphs
+    (ANA_PERSIST=0) for comparison. Then the persistent launch against the
+    step kernels on its own picks: the same tokens fed one step at a time
+    give logits within 1e-4 of the launch's (the same weights, the sums in
+    another order). The 115M case runs past the first 128 positions, so the
     attention pieces of 128 slots each get live slots one after another."""
-    print(f"case fast persistent decode {model}", flush=True)
+    print(f"case fast persistent decode {model} mode {mode}", flush=True)
     path = {"small": small_ckpt, "mid": mid_ckpt, "115m": big_ckpt}[model]
     oracle.set_threads(8)
     m = oracle.Model(path)
     steps = {"small": 70, "mid": 70, "115m": 150}[model]
     pr = [int(t) for t in ckpt.prompt(3, 9, m.vocab)]
+    runs = {}
     for persist in ("1", "0"):
         os.environ["ANA_PERSIST"] = persist
         try:
-            with ana_amd.Decoder(path, max_seqs=1, prefill_chunk=16, numerics=ana_amd.FAST_FP32) as dec:
+            with ana_amd.Decoder(path, max_seqs=1, prefill_chunk=16, numerics=mode) as dec:
                 dec.feeds(0, 0, pr[:-1])
                 out = dec.generate([0], [len(pr) - 1], [pr[-1]], steps)[0]
                 lg = dec.logits([0])[0]
         finally:
             os.environ.pop("ANA_PERSIST", None)
+        runs[persist] = (out, lg)
         st = oracle.State(m)
         for p, t in enumerate(pr):
             st.feed(p, t)
@@ -530,13 +537,21 @@ def test_fast_persistent_decode(oracle, small_ckpt, mid_ckpt, big_ckpt, model):
         for k, t in enumerate(out):
             want = st.logits()
             scale = np.abs(want).max()
-            assert want[t] >= want.max() - 2 * TOL[ana_amd.FAST_FP32] * scale, (persist, k, int(t), int(want.argmax()))
+            assert want[t] >= want.max() - 2 * TOL[mode] * scale, (persist, k, int(t), int(want.argmax()))
             if k + 1 < len(out):
                 st.feed(pos, int(t))
                 pos += 1
         e = rel_err(lg, want)
         print(f"persist {persist}: final relative error {e:.3e}", flush=True)
-        assert e <= TOL[ana_amd.FAST_FP32], (persist, e)
+        assert e <= TOL[mode], (persist, e)
+    out, lg = runs["1"]
+    with ana_amd.Decoder(path, max_seqs=1, prefill_chunk=16, numerics=mode) as dec:
+        dec.feeds(0, 0, pr[:-1])
+        for k, t in enumerate([pr[-1]] + [int(x) for x in out[:-1]]):
+            dec.feed([0], [len(pr) - 1 + k], [t])
+        e = rel_err(lg, dec.logits([0])[0])
+    print(f"persistent launch against the step kernels: relative difference {e:.3e}", flush=True)
+    assert e <= 1e-4, e
 
 
 @pytest.mark.parametrize("mode", MODES)
