@@ -87,7 +87,8 @@ __device__ __forceinline__ void lds_barrier() {
 template <int PE, class Map>
 __device__ __forceinline__ bool poll_gather(const unsigned long long* base, uint32_t n, uint32_t ep, Map map, float* dst,
                                             uint32_t* ctl, uint64_t tmo) {
-  const uint32_t pt = threadIdx.x;
+  uint32_t pt = threadIdx.x;
+  asm volatile("" : "+v"(pt));   // (its addresses are built here, not hoisted out of the caller's loop)
   unsigned long long v[PE];
 #pragma unroll
   for (int e = 0; e < PE; e++) {
@@ -223,7 +224,24 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       if (tid == 0) tr_s[ph][i] = (uint32_t)rtc();  \
     }                                               \
   } while (0)
-  const uint32_t w = blockIdx.x, G = gridDim.x, tid = threadIdx.x, lane = tid & 63;
+  // a phase's start: the barrier, its stamp, the thread index made opaque
+#define BEGIN() \
+  do {                  \
+    lds_barrier();      \
+    TS(0);              \
+    fresh();            \
+  } while (0)
+  const uint32_t w = blockIdx.x, G = gridDim.x;
+  // the thread's index and lane, made opaque again at every phase's start
+  // (fresh()): what the compiler derives from them (addresses, masks) is
+  // then rebuilt in each phase (a few instructions) instead of hoisted out
+  // of the step loop, where ~140 such values held registers across every
+  // phase (the build used all 256 VGPRs and spilled to AGPRs; 178 now)
+  uint32_t tid = threadIdx.x, lane = tid & 63;
+  auto fresh = [&]() {
+    asm volatile("" : "+v"(tid));
+    lane = tid & 63;
+  };
   const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // (a scalar: the wave's branches are uniform)
 
   const uint32_t d = a.d, f = a.f, H = a.heads, ctx = a.ctx, L = a.L;
@@ -370,32 +388,47 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       g[i] = i < XW && k < d ? *reinterpret_cast<const float4*>(W + off + k) : zero4();
     }
   };
-  // the RMSNorm of xs[0..d) folded into the products: xg = x g (this
-  // lane's float4s), and the scale 1 / sqrt(mean(x^2) + 1e-5), which every
-  // wave forms from the whole row itself
-  auto norm_fold = [&](auto WLc, const float4 (&g)[XN], float4 (&xg)[XN]) -> float {
+  // this lane's float4s of xs[0..n) in layout WL (XV of them)
+  auto xload = [&](auto WLc, auto& xv, uint32_t n) {
+    constexpr int XV = sizeof(xv) / sizeof(float4);
+#pragma unroll
+    for (int i = 0; i < XV; i++) xv[i] = xsw(WLc, i, n);
+  };
+  // the RMSNorm of a d vector (this lane's float4s xv) folded into the
+  // products: xg = x g, and the scale 1 / sqrt(mean(x^2) + 1e-5), which
+  // every wave forms from the whole row itself
+  auto norm_fold = [&](auto WLc, const float4 (&g)[XN], const float4 (&xv)[XN], float4 (&xg)[XN]) -> float {
     constexpr int XW = decltype(WLc)::value ? 2 * PDH : NFD;
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < XW; i++) {
-      const float4 x = xsw(WLc, i, d);
-      ss = dot4(x, x, ss);
-      xg[i] = mul4(x, g[i]);
+      ss = dot4(xv[i], xv[i], ss);
+      xg[i] = mul4(xv[i], g[i]);
     }
     ss = wsum(ss);
     return rsq(ss * invd + 1.0e-5f);
   };
-  // acc + this lane's part of piece pc of buf times x (its float4s of that
-  // piece: one in fp32, two in bf16)
-  auto dotw = [&](auto WLc, const float4* buf, uint32_t pc, const float4* x, float acc) -> float {
+  // this lane's 16 bytes of piece pc of buf
+  auto ldp = [&](const float4* buf, uint32_t pc) -> uint4 {
+    return reinterpret_cast<const uint4*>(buf)[pc * 64 + lane];
+  };
+  // acc + those 16 bytes (four fp32 or eight bf16 weights) times x (this
+  // lane's float4s of the piece: one in fp32, two in bf16)
+  auto dotp = [&](auto WLc, uint4 u, const float4* x, float acc) -> float {
     if constexpr (decltype(WLc)::value) {
-      const uint4 u = reinterpret_cast<const uint4*>(buf)[pc * 64 + lane];
       acc = dot4(bf4(u.x, u.y), x[0], acc);
       return dot4(bf4(u.z, u.w), x[1], acc);
     } else {
-      return dot4(buf[pc * 64 + lane], x[0], acc);
+      return dot4(make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                              __uint_as_float(u.w)),
+                  x[0], acc);
     }
   };
+  // Each phase's compute reads its x and its pieces out of LDS first, all
+  // of them, then computes: the scheduler (which takes an LDS read to be a
+  // few cycles) would otherwise put each read next to its use, and with one
+  // wave a SIMD nothing would hide the reads' real latency
+#define ISSUED() __builtin_amdgcn_sched_barrier(0)
   auto fail_wg = [&]() {
     if (tid == 0) {
       if (!aborted(a.ctl)) atomicOr(&a.ctl[0], 1u);
@@ -442,8 +475,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     const PLayer P = Ls[l];
     // ---- norm, then q|k|v (|z) (in bufB): rows w RQ .. w RQ + RQ - 1,
     // wave wv the rows wv + 4 i
-    lds_barrier();
-    TS(0);
+    BEGIN();
     float4 g4[XN];
     load_g(WLc, g4, P.ra);
     float svr = 0.0f, lamr = 0.0f, gqr = 0.0f, gkr = 0.0f, sinkr = 0.0f;
@@ -477,16 +509,24 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     }
     if (!meet()) return false;
     {
-      float4 xg[XN];
-      const float rs = norm_fold(WLc, g4, xg);
       const uint32_t R = qkv_rows(P), RQ = (R + G - 1) / G;
-      float res[4];
+      float4 xv[XN], xg[XN];
+      xload(WLc, xv, d);
+      uint4 pw[4][PDc];
 #pragma unroll
       for (int kk = 0; kk < 4; kk++) {
         const uint32_t i = min(wv + 4 * kk, RQ - 1);
+#pragma unroll
+        for (int j = 0; j < PDc; j++) pw[kk][j] = ldp(bufB, i * PDc + j);
+      }
+      ISSUED();
+      const float rs = norm_fold(WLc, g4, xv, xg);
+      float res[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; kk++) {
         float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < PDc; j++) acc = dotw(WLc, bufB, i * PDc + j, &xg[XS * j], acc);
+        for (int j = 0; j < PDc; j++) acc = dotp(WLc, pw[kk][j], &xg[XS * j], acc);
         res[kk] = wsum(acc) * rs;
       }
       if (lane < 4) {
@@ -497,8 +537,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     }
     pub();
     // ---- the mix (an attention unit's K and V pieces in bufN)
-    lds_barrier();
-    TS(0);
+    BEGIN();
     dma_wo(WLc, P, bufB);
     if (P.gla) {
       {
@@ -660,8 +699,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       pub();
       // ---- the pieces and the sink combined: o of head h, columns 4 cb ..
       // (no loads of its own: the Wo pieces stay in flight)
-      lds_barrier();
-      TS(0);
+      BEGIN();
       {
         bool ok = true;
         if (gla_unit) {
@@ -700,8 +738,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       pub();
     }
     // ---- xa = x + Wo o (Wo in bufB)
-    lds_barrier();
-    TS(0);
+    BEGIN();
     float4 gf[XN];
     load_g(WLc, gf, P.rf);
     dma_gu(WLc, P, bufN);
@@ -709,34 +746,47 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     if (!meet()) return false;
     if (orow_ok) {
       float4 xv[XW];
+      xload(WLc, xv, d);
+      uint4 pw[PDc];
 #pragma unroll
-      for (int i = 0; i < XW; i++) xv[i] = xsw(WLc, i, d);
+      for (int j = 0; j < PDc; j++) pw[j] = ldp(bufB, wv * PDc + j);
+      ISSUED();
       float acc = 0.0f;
 #pragma unroll
-      for (int j = 0; j < PDc; j++) acc = dotw(WLc, bufB, wv * PDc + j, &xv[XS * j], acc);
+      for (int j = 0; j < PDc; j++) acc = dotp(WLc, pw[j], &xv[XS * j], acc);
       xa_own = x_own + wsum(acc);
       if (lane == 0) ll_put(LL + P.e_xa + orow, xa_own, ep);
     }
     pub();
     // ---- hh = silu(g) u on norm(xa) (gate|up in bufN): wave wv the pairs
     // wv + 4 i
-    lds_barrier();
-    TS(0);
+    BEGIN();
     dma_wd(WLc, P, bufB);
     gathered(poll_gather<PEX>(LL, d, ep, Ident{P.e_xa}, xs, a.ctl, a.tmo));
     if (!meet()) return false;
     {
-      float4 xg[XN];
-      const float rs = norm_fold(WLc, gf, xg);
-      float hv[2];
+      float4 xv[XN], xg[XN];
+      xload(WLc, xv, d);
+      uint4 pw[2][2][PDc];
 #pragma unroll
       for (int i = 0; i < 2; i++) {
         const uint32_t pi = min(wv + 4 * i, RGp - 1);
+#pragma unroll
+        for (int j = 0; j < PDc; j++) {
+          pw[i][0][j] = ldp(bufN, (pi * 2 + 0) * PDc + j);
+          pw[i][1][j] = ldp(bufN, (pi * 2 + 1) * PDc + j);
+        }
+      }
+      ISSUED();
+      const float rs = norm_fold(WLc, gf, xv, xg);
+      float hv[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
         float g = 0.0f, u = 0.0f;
 #pragma unroll
         for (int j = 0; j < PDc; j++) {
-          g = dotw(WLc, bufN, (pi * 2 + 0) * PDc + j, &xg[XS * j], g);
-          u = dotw(WLc, bufN, (pi * 2 + 1) * PDc + j, &xg[XS * j], u);
+          g = dotp(WLc, pw[i][0][j], &xg[XS * j], g);
+          u = dotp(WLc, pw[i][1][j], &xg[XS * j], u);
         }
         g = wsum(g) * rs;
         u = wsum(u) * rs;
@@ -749,19 +799,21 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     }
     pub();
     // ---- x = xa + Wd hh (Wd in bufB)
-    lds_barrier();
-    TS(0);
+    BEGIN();
     if (l + 1 < L) dma_qkv(IC<WT>{}, Ls[l + 1], bufN);   // (layers past the first: the mode's layout)
     else dma_head0(bufN);
     gathered(poll_gather<PEF>(LL, f, ep, Ident{P.e_hh}, xs, a.ctl, a.tmo));
     if (!meet()) return false;
     if (orow_ok) {
       float4 xv[XF];
+      xload(WLc, xv, f);
+      uint4 pw[PFc];
 #pragma unroll
-      for (int i = 0; i < XF; i++) xv[i] = xsw(WLc, i, f);
+      for (int j = 0; j < PFc; j++) pw[j] = ldp(bufB, wv * PFc + j);
+      ISSUED();
       float acc = 0.0f;
 #pragma unroll
-      for (int j = 0; j < PFc; j++) acc = dotw(WLc, bufB, wv * PFc + j, &xv[XS * j], acc);
+      for (int j = 0; j < PFc; j++) acc = dotp(WLc, pw[j], &xv[XS * j], acc);
       x_own = xa_own + wsum(acc);
       if (lane == 0) ll_put(LL + P.e_x + orow, x_own, ep);
     }
@@ -776,21 +828,28 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     constexpr int PB = decltype(B)::value;
     float4* b0 = bufp(IC<PB>{});
     float4* b1 = bufp(IC<1 - PB>{});
-    lds_barrier();
-    TS(0);
+    BEGIN();
     float4 gf[XN];
     load_g(HW, gf, a.fin);
     gathered(poll_gather<PEX>(LL, d, ep, Ident{Ls[L - 1].e_x}, xs, a.ctl, a.tmo));
     if (!meet()) return false;
-    float4 xg[XN];
-    const float rs = norm_fold(HW, gf, xg);
+    float4 xv[XN], xg[XN];
+    xload(HW, xv, d);
+    const float rs = norm_fold(HW, gf, xv, xg);
     unsigned long long best = 0ull;
     auto rows = [&](float4* cur, uint32_t b) {
+      uint4 pw[HBR][HPD];
+#pragma unroll
+      for (int i = 0; i < HBR; i++) {
+#pragma unroll
+        for (int j = 0; j < HPD; j++) pw[i][j] = ldp(cur, (wv * HBR + i) * HPD + j);
+      }
+      ISSUED();
 #pragma unroll
       for (int i = 0; i < HBR; i++) {
         float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < HPD; j++) acc = dotw(HW, cur, (wv * HBR + i) * HPD + j, &xg[(WT ? 2 : 1) * j], acc);
+        for (int j = 0; j < HPD; j++) acc = dotp(HW, pw[i][j], &xg[(WT ? 2 : 1) * j], acc);
         acc = wsum(acc) * rs;
         const uint32_t r = h0 + wv + 4 * (b * HBR + i);
         if (lane == 0 && r < h1) {
@@ -848,8 +907,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   // buffer of parity B; the best key (0: no logit reached the maximum)
   auto pick = [&](auto B, uint32_t ep, unsigned long long* LL, bool& ok) -> unsigned long long {
     constexpr int PB = decltype(B)::value;
-    lds_barrier();
-    TS(0);
+    BEGIN();
     dma_qkv(IC<0>{}, Ls[0], bufp(IC<PB>{}));   // (the first layer: fp32 in every mode)
     {
       const uint32_t pt = tid;
@@ -952,6 +1010,8 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     a.ctl[3] = nan_stop ? 1u : 0u;
   }
 #undef TS
+#undef BEGIN
+#undef ISSUED
 }
 
 
