@@ -207,8 +207,12 @@ def cpu_baseline(path: str, c: cf.Config, seconds: float) -> dict:
     }
 
 
-KERNEL_PERSIST = ("k_decode1 (fast fp32, one greedy sequence: every phase of every step in one "
-                  "cooperative launch of one workgroup per CU; weights streamed into LDS a phase ahead)")
+KERNEL_PERSIST = {
+    "fast_fp32": ("k_decode1 (fast fp32, one greedy sequence: every phase of every step in one "
+                  "cooperative launch of one workgroup per CU; weights streamed into LDS a phase ahead)"),
+    "bf16": ("k_decode1 (bf16 weights past the first layer and in the head, one greedy sequence: every "
+             "phase of every step in one cooperative launch of one workgroup per CU; weights streamed "
+             "into LDS a phase ahead)")}
 KERNEL = {"exact": "k_gemv_small<1> (exact products, norm/residual/SiLU/argmax fused) + LM head",
           "fast_fp32": "k_gemv_fast<fp32> (split-K products, norm/residual/SiLU/argmax fused) + LM head",
           "bf16": "k_gemv_fast<bf16> (split-K products over bf16 weights) + LM head"}
@@ -230,10 +234,11 @@ def phase_names(c) -> list:
     return names + [(-1, "head"), (-1, "pick")]
 
 
-def run_phase_trace(path: str, c, steps: int) -> str:
-    """The bench's B=1 fast_fp32 workload (1920-token prompt, decode from
-    1919) with k_decode1's phase stamps armed for `steps` steps of one
-    call; returns a markdown summary. Per (phase, workgroup) the stamps
+def run_phase_trace(path: str, c, steps: int, mode: int = ana_amd.FAST_FP32) -> str:
+    """The bench's B=1 workload in a fast mode (fast_fp32, or bf16 with
+    --numerics bf16; 1920-token prompt, decode from 1919) with k_decode1's
+    phase stamps armed for `steps` steps of one call; returns a markdown
+    summary. Per (phase, workgroup) the stamps
     split a phase into: wait (start to every input seen: the exchange, and
     the weight loads issued before it, which retire first), land (to the
     phase's weights in LDS), compute (to the outputs published), and the gap
@@ -241,7 +246,7 @@ def run_phase_trace(path: str, c, steps: int) -> str:
     the traced steps after the first two."""
     TICK_US = 0.01   # the constant-rate clock runs at 100 MHz
     pr = ckpt.prompt(0, 1920, c.vocab)
-    with ana_amd.Decoder(path, max_seqs=1, numerics=ana_amd.FAST_FP32) as dec:
+    with ana_amd.Decoder(path, max_seqs=1, numerics=mode) as dec:
         dec.feeds(0, 0, pr[:-1])
         pos, tok = 1919, int(pr[-1])
         o = dec.generate([0], [pos], [tok], PRIME)[0]
@@ -427,7 +432,7 @@ def main() -> int:
             print(f"| {mib} MiB | {ana_amd.probe_reread(mib << 20, 20) / 1e3:.2f} TB/s |", flush=True)
         return 0
     if a.phase_trace:
-        print(run_phase_trace(path, c, a.phase_trace), flush=True)
+        print(run_phase_trace(path, c, a.phase_trace, MODES[a.numerics]), flush=True)
         release_device()
         return 0
     if a.prefill_only:
@@ -459,7 +464,7 @@ def main() -> int:
     persistent = r1["stats"]["step"][0] > 0
     if persistent:
         launches, ms, by = r1["stats"]["step"]
-        kernel = KERNEL_PERSIST
+        kernel = KERNEL_PERSIST[mode]
     else:
         g, h = r1["stats"]["gemv"], r1["stats"]["head"]
         launches, ms, by = g[0] + h[0], g[1] + h[1], g[2] + h[2]
@@ -471,7 +476,7 @@ def main() -> int:
         try:
             tj = json.load(open(tpath))
             if persistent:
-                per_step = tj.get("decode1_bytes_per_step")
+                per_step = tj.get(f"decode1_{mode}_bytes_per_step")
                 traffic = round(per_step * prof_steps / max(launches, 1)) if per_step else None
             else:
                 traffic = tj.get(f"gemv_{mode}_bytes_per_launch")

@@ -197,8 +197,8 @@ int ana_state(struct ana_ctx* ctx, uint32_t seq, uint32_t layer, float* out, siz
 #define ANA_K_ATTN 2     /* softmax attention over the ring */
 #define ANA_K_GLA 3      /* the GLA state update and readout */
 #define ANA_K_PICK 4     /* greedy pick / sampler */
-#define ANA_K_STEP 5     /* whole decode steps in one persistent launch (fast fp32, one
-                            greedy sequence): every kind above at once */
+#define ANA_K_STEP 5     /* whole decode steps in one persistent launch (fast fp32 or bf16,
+                            one greedy sequence): every kind above at once */
 #define ANA_K_KINDS 6
 int ana_prof(struct ana_ctx* ctx, int on);
 int ana_prof_read(struct ana_ctx* ctx, uint32_t kind, uint64_t* launches, double* ms,
