@@ -274,12 +274,16 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     else return wbA;
   };
   // one 1 KB piece: lane l's 16 bytes from src (this lane's address) to
-  // float4 at * 64 + l of the buffer. The non-temporal hint (cache policy
-  // 2, nt): every piece is read once a step and the step's stream is larger
-  // than the caches (fast_fp32: 4707 -> 4815 tok/s on one box; bf16, whose
-  // weights would fit the MALL, unchanged)
+  // float4 at * 64 + l of the buffer. Weights take the non-temporal hint
+  // (cache policy 2, nt): each is read once a step, and the step's stream
+  // is larger than the caches (fast_fp32: 4707 -> 4815 tok/s on one box;
+  // bf16, whose weights would fit the MALL, unchanged). K and V do not: the
+  // rings are read again every step (+0.8% in either mode)
   auto piece = [&](const void* src, float4* buf, uint32_t at) {
     __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)&buf[at * 64], 16, 0, 2);
+  };
+  auto piece_kv = [&](const void* src, float4* buf, uint32_t at) {
+    __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)&buf[at * 64], 16, 0, 0);
   };
   // ---- weights in either layout: WL 0 fp32 (a row of K is K / 256
   // pieces, lane l's float4 of piece j at k = 4 (l + 64 j)), WL 1 bf16 (a
@@ -323,7 +327,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       const uint32_t i = qq * (64 / C4) + lane / C4, t = t0 + i;
       const uint32_t tt = (i < PL && t < ctx) ? t : t0;
       const size_t off = (size_t)tt * d + h * HD + 4 * (lane % C4);
-      piece((q < KVQ ? Kr : Vr) + off, buf, q);
+      piece_kv((q < KVQ ? Kr : Vr) + off, buf, q);
     }
   };
   auto dma_wo = [&](auto WLc, const PLayer& P, float4* buf) {
