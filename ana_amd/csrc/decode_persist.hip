@@ -534,8 +534,11 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < PDc; j++) acc = dotp(WLc, pw[kk][j], &xg[XS * j], acc);
-        res[kk] = wsum(acc) * rs;
+        res[kk] = acc;
       }
+      wsum_n(res);
+#pragma unroll
+      for (int kk = 0; kk < 4; kk++) res[kk] *= rs;
       if (lane < 4) {
         const uint32_t i = wv + 4 * lane, r = w * RQ + i;
         const float val = lane == 0 ? res[0] : lane == 1 ? res[1] : lane == 2 ? res[2] : res[3];
@@ -786,7 +789,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       }
       ISSUED();
       const float rs = norm_fold(WLc, gf, xv, xg);
-      float hv[2];
+      float hv[2], gu4[4];
 #pragma unroll
       for (int i = 0; i < 2; i++) {
         float g = 0.0f, u = 0.0f;
@@ -795,8 +798,13 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
           g = dotp(WLc, pw[i][0][j], &xg[XS * j], g);
           u = dotp(WLc, pw[i][1][j], &xg[XS * j], u);
         }
-        g = wsum(g) * rs;
-        u = wsum(u) * rs;
+        gu4[2 * i] = g;
+        gu4[2 * i + 1] = u;
+      }
+      wsum_n(gu4);
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const float g = gu4[2 * i] * rs, u = gu4[2 * i + 1] * rs;
         hv[i] = g * rcp(1.0f + __expf(-g)) * u;
       }
       if (lane < 2) {
@@ -852,12 +860,18 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         for (int j = 0; j < HPD; j++) pw[i][j] = ldp(cur, (wv * HBR + i) * HPD + j);
       }
       ISSUED();
+      float hs[HBR];
 #pragma unroll
       for (int i = 0; i < HBR; i++) {
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < HPD; j++) acc = dotp(HW, pw[i][j], &xg[(WT ? 2 : 1) * j], acc);
-        acc = wsum(acc) * rs;
+        hs[i] = acc;
+      }
+      wsum_n(hs);
+#pragma unroll
+      for (int i = 0; i < HBR; i++) {
+        const float acc = hs[i] * rs;
         const uint32_t r = h0 + wv + 4 * (b * HBR + i);
         if (lane == 0 && r < h1) {
           lgs[wv][b * HBR + i] = acc;

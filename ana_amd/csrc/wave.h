@@ -37,6 +37,22 @@ __device__ __forceinline__ float wsum(float v) {
   v = row16_sum(v);
   return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
+// wsum of N values at once, each summed in wsum's order (so each result is
+// wsum's): every DPP step of all N before the next, so the steps of one
+// fill the others' DPP wait states instead of s_nop
+template <int N>
+__device__ __forceinline__ void wsum_n(float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; i++) v[i] += dpp<0xB1>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; i++) v[i] += dpp<0x4E>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; i++) v[i] += dpp<0x141>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; i++) v[i] += dpp<0x140>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; i++) v[i] = (lane_f(v[i], 0) + lane_f(v[i], 16)) + (lane_f(v[i], 32) + lane_f(v[i], 48));
+}
 // the maximum over the wave, the same way
 __device__ __forceinline__ float wmax(float v) {
   v = fmaxf(v, dpp<0xB1>(v));
