@@ -337,9 +337,18 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       piece(wsrc(WLc, P.wo, P.ho, r, d, j), buf, q);
     }
   };
-  auto dma_gu = [&](auto WLc, const PLayer& P, float4* buf) {
-    const uint32_t PD = npd(WLc), NP = RGp * 2 * PD;
-    for (uint32_t q = wv; q < NP; q += 4) {
+  // gate|up's pieces in three parts (part k: pieces [gu_cut(k), gu_cut(k +
+  // 1))), issued over the phases before Wo's where its buffer is free: a
+  // GLA layer's q|k|v|z and mix phases, a softmax layer's combine, then
+  // Wo's phase itself, so no phase's stream is much longer than the
+  // exchange it overlaps
+  auto gu_cut = [&](auto WLc, uint32_t k) -> uint32_t {
+    const uint32_t NP = RGp * 2 * npd(WLc), n1 = ((NP + 11) / 12) * 4;
+    return min(NP, k * n1);
+  };
+  auto dma_gu = [&](auto WLc, const PLayer& P, float4* buf, uint32_t k0, uint32_t k1) {
+    const uint32_t PD = npd(WLc), NP = k1 >= 3 ? RGp * 2 * PD : gu_cut(WLc, k1);
+    for (uint32_t q = gu_cut(WLc, k0) + wv; q < NP; q += 4) {
       const uint32_t pi = q / (2 * PD), gu = (q / PD) & 1, j = q % PD, jp = min(w * RGp + pi, f - 1);
       const uint64_t up = gu ? (uint64_t)f * d : 0;   // up's rows follow gate's: up values on
       piece(wsrc(WLc, P.wg + up, P.hg + sizeof(uint16_t) * up, jp, d, j), buf, q);   // (hg: a byte address)
@@ -504,6 +513,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     }
     if (l == 0 && orow_ok) x_own = W[(size_t)tok * d + orow];
     dma_kv(P, bufN);
+    if (P.gla) dma_gu(WLc, P, bufN, 0, 1);
     {
       bool ok = true;
       if (l == 0) {
@@ -550,6 +560,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     BEGIN();
     dma_wo(WLc, P, bufB);
     if (P.gla) {
+      dma_gu(WLc, P, bufN, 1, 2);
       {
         bool ok = true;
         if (gla_unit) {
@@ -708,8 +719,10 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       }
       pub();
       // ---- the pieces and the sink combined: o of head h, columns 4 cb ..
-      // (no loads of its own: the Wo pieces stay in flight)
+      // (the K and V pieces are read: gate|up's first two parts go to their
+      // buffer)
       BEGIN();
+      dma_gu(WLc, P, bufN, 0, 2);
       {
         bool ok = true;
         if (gla_unit) {
@@ -751,7 +764,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     BEGIN();
     float4 gf[XN];
     load_g(WLc, gf, P.rf);
-    dma_gu(WLc, P, bufN);
+    dma_gu(WLc, P, bufN, 2, 3);
     gathered(poll_gather<PEX>(LL, d, ep, Ident{P.e_o}, xs, a.ctl, a.tmo));
     if (!meet()) return false;
     if (orow_ok) {
