@@ -87,7 +87,7 @@ struct ana_ctx {
     int bf;                          // packed as bf16 (else fp32)
   };
   std::unordered_map<const float*, PkEnt> pk;
-  // the persistent one-sequence decode (ANA_FAST_FP32, ANA_BF16): its layer table,
+  // the persistent one-sequence decode (every mode; the exact build in ANA_EXACT_FP32): its layer table,
   // exchange entries (two sets of ll_par), control words, grid and the
   // epoch its next launch starts from
   bool persist = false, persist_off = false;
@@ -410,7 +410,7 @@ extern "C" int ana_open(const char* path, const ana_opts* opts, ana_ctx** out) {
         (e = hipMemsetAsync(c->d_hpctl, 0, 4, c->st)) != hipSuccess)
       return bad(e);
   }
-  if ((c->mode == ANA_FAST_FP32 || c->mode == ANA_BF16) && (e = persist_setup(c)) != hipSuccess) return bad(e);
+  if ((e = persist_setup(c)) != hipSuccess) return bad(e);
   // ANA_PERSIST=0 keeps one-sequence decode on the captured graphs
   if (const char* pv = getenv("ANA_PERSIST")) c->persist_off = strcmp(pv, "0") == 0;
   if ((e = launch_zero(c->state, c->seq_stride * c->max_seqs, c->st)) != hipSuccess) return bad(e);
@@ -641,7 +641,8 @@ static hipError_t persist_setup(ana_ctx* c) {
   int coop = 0;
   if ((e = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->device)) != hipSuccess) return e;
   const uint32_t G = (uint32_t)std::min(pr.multiProcessorCount, 256);
-  if (!coop || !decode1_fits(cf, G)) return hipSuccess;
+  const bool exact = c->mode == ANA_EXACT_FP32;
+  if (!coop || !decode1_fits(cf, G, exact)) return hipSuccess;
   int rate_khz = 0;   // the constant-rate clock the kernel's waits are timed by
   if ((e = hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, c->device)) != hipSuccess) return e;
   if (rate_khz <= 0) return hipSuccess;
@@ -660,7 +661,9 @@ static hipError_t persist_setup(ana_ctx* c) {
     P.soff = c->layer_off[l];
     P.gla = b.gla ? 1u : 0u;
     P.e_qkv = en; en += (b.gla ? 4ull : 3ull) * d;
-    if (!b.gla) { P.e_part = en; en += (uint64_t)cf.heads * np * (hd + 2); }
+    // the attention's partials (a piece's max, sum and hd columns; exact:
+    // the piece's raw scores)
+    if (!b.gla) { P.e_part = en; en += (uint64_t)cf.heads * np * std::max(hd + 2, (cf.ctx + np - 1) / np); }
     P.e_o = en; en += d;
     P.e_xa = en; en += d;
     P.e_hh = en; en += f;
@@ -1346,6 +1349,7 @@ static int generate_persist(ana_ctx* c, const uint32_t* pos, uint32_t steps, uin
       pa.L = c->cfg.layers; pa.d = c->cfg.d; pa.f = c->cfg.f; pa.heads = c->cfg.heads; pa.ctx = c->cfg.ctx;
       pa.vocab = c->cfg.vocab; pa.rglru = c->cfg.rglru; pa.qk = c->cfg.qk; pa.sinks = c->cfg.sinks;
       pa.np = c->pnp;
+      pa.exact = c->mode == ANA_EXACT_FP32 ? 1u : 0u;
       pa.fin = c->fin;
       pa.state = c->state; pa.seq_stride = c->seq_stride;
       pa.X = c->X; pa.LG = c->LG;

@@ -415,6 +415,7 @@ struct PersistArgs {
                             // tied embedding here, on 16 bytes), or null for fp32
   const PLayer* lay;        // [L], device
   uint32_t L, d, f, heads, ctx, vocab, rglru, qk, sinks, np;  // np: attention pieces a head
+  uint32_t exact;           // the exact build (ANA_EXACT_FP32; fp32 weights)
   uint64_t fin;             // the final norm's gains
   float* state;
   uint64_t seq_stride;
@@ -434,7 +435,7 @@ struct PersistArgs {
 // pieces of the ring a head's attention takes (one workgroup each)
 uint32_t decode1_pieces(const ana_config& c, uint32_t G);
 // whether the persistent kernel takes this configuration on G workgroups
-bool decode1_fits(const ana_config& c, uint32_t G);
+bool decode1_fits(const ana_config& c, uint32_t G, bool exact);
 hipError_t launch_decode1(const PersistArgs& a, uint32_t G, hipStream_t st);
 // phases a step of the persistent kernel takes (the trace's second extent)
 uint32_t decode1_phases(const ana_config& c);

@@ -167,6 +167,73 @@ using IC = std::integral_constant<int, B>;
 __device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 __device__ __forceinline__ float rsq(float x) { return __builtin_amdgcn_rsqf(x); }
 
+// ---- the exact build's reductions: one lane's chain in the reference's
+// order, a product and the sum it joins two roundings (bulk.c's product
+// loop)
+
+// s + v(0).x + v(0).y + ... + v(n4 - 1).w in order, the float4s read from
+// LDS by the accessor: every term a product formed beforehand by the whole
+// workgroup (a product next to its add puts its latency in the chain too,
+// about twice the add's cycles a term). Two sets of eight float4 in turn,
+// each read again as soon as its adds are issued (numerics.h's chain_lds
+// over an index map).
+template <class F>
+__device__ __forceinline__ float chain4(float s, uint32_t n4, F at) {
+  auto id = [](float x) { return x; };
+  uint32_t i = 0;
+  if (n4 >= 16) {
+    float4 a[8], b[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) a[u] = at(u);
+#pragma unroll
+    for (int u = 0; u < 8; u++) b[u] = at(8 + u);
+    for (i = 16; i + 16 <= n4; i += 16) {
+      s = chain_add8(s, a, id);
+#pragma unroll
+      for (int u = 0; u < 8; u++) a[u] = at(i + u);
+      s = chain_add8(s, b, id);
+#pragma unroll
+      for (int u = 0; u < 8; u++) b[u] = at(i + 8 + u);
+    }
+    s = chain_add8(s, a, id);
+    if (i + 8 <= n4) {
+#pragma unroll
+      for (int u = 0; u < 8; u++) a[u] = at(i + u);
+      s = chain_add8(s, b, id);
+      s = chain_add8(s, a, id);
+      i += 8;
+    } else {
+      s = chain_add8(s, b, id);
+    }
+  }
+  if (i + 8 <= n4) {
+    float4 a[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) a[u] = at(i + u);
+    s = chain_add8(s, a, id);
+    i += 8;
+  }
+  for (; i < n4; i++) {
+    const float4 v = at(i);
+    s = s + v.x;
+    s = s + v.y;
+    s = s + v.z;
+    s = s + v.w;
+  }
+  return s;
+}
+
+// a wave's maximum by r = t > r ? t : r (a NaN never wins), as the exact
+// attention takes its maxima
+__device__ __forceinline__ float wmax_gt(float r) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float t = __shfl_xor(r, m, 64);
+    r = t > r ? t : r;
+  }
+  return r;
+}
+
 }  // namespace
 
 
@@ -193,7 +260,15 @@ typedef __attribute__((address_space(3))) void lds_void;
 // bits) go into LDS by thread 0: the phase's start; its inputs all seen;
 // all waves met after their waits; its outputs published. The workgroup copies a step's stamps to a.trace
 // after the pick, for the first a.trace_steps steps.
-template <int HD, int NFD, int NFF, bool TR, int WT>
+//
+// EX: the exact build (ANA_EXACT_FP32, fp32 weights): every output takes
+// the F32 steps of the exact kernels, in their order: the norms' sums of
+// squares, the products, the GLA and attention sums as in-order chains in
+// one lane each, exp/log/sqrt through double, IEEE division. The phases,
+// the exchange and the weight stream are the fast build's; the attention
+// publishes its raw scores and a second phase runs the softmax's chains
+// over the whole window (its V columns streamed as slices of 4 columns).
+template <int HD, int NFD, int NFF, bool TR, int WT, bool EX>
 __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   constexpr int QD = HD / 4;            // attention: dims a score lane holds (4 lanes a slot)
   constexpr int C4 = HD / 4;            // float4 columns of a head
@@ -211,8 +286,11 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   constexpr int PES = 1;                // of up to 256 entries
   __shared__ __align__(16) float4 wbA[WB];
   __shared__ __align__(16) float4 wbB[WB];
-  __shared__ __align__(16) float xs[256 * NFF];
-  __shared__ float red[8], qv[HD], kvv[HD], vvv[HD], es[KPASS * 64], lgs[4][40];
+  __shared__ __align__(16) float xs[256 * NFF + (EX ? 256 : 0)];   // (exact: a window's scores and 4 values)
+  __shared__ __align__(16) float qv[HD];
+  __shared__ __align__(16) float kvv[HD];
+  __shared__ __align__(16) float vvv[HD];
+  __shared__ float red[8], es[KPASS * 64], lgs[4][40];
   __shared__ float4 part4[4][C4];
   __shared__ uint32_t bad_s;
   __shared__ unsigned long long key_s[4], pick_s[4];
@@ -258,7 +336,8 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   const float sc = 1.0f / sqrtf((float)HD), invd = 1.0f / (float)d;
   const uint32_t np = a.np, PL = (ctx + np - 1) / np;
   const uint32_t v = a.vocab, RH = (v + G - 1) / G, h0 = w * RH, h1 = min(v, h0 + RH);
-  const uint32_t nhb = (RH + 4 * HBR - 1) / (4 * HBR);   // head batches (each wave HBR rows a batch)
+  // head batches (each wave HBR rows a batch; exact: 16 rows' chunks of 256)
+  const uint32_t nhb = EX ? ((RH + 63) / 64) * ((d + 255) / 256) : (RH + 4 * HBR - 1) / (4 * HBR);
   const bool gla_unit = w < H * C4, att_unit = w < H * np;
   // the layer table in LDS: its fields are read there (a global copy would
   // be re-read after every store the compiler cannot tell apart from it)
@@ -317,12 +396,26 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   // an attention unit's K rows then V rows of its piece of the ring: slot i
   // of the piece at float4 i C4 .. (V from KV_V); slots past the ring or the
   // piece read slot t0 (never used)
+  // (exact: K only, then the combine unit's V slices: piece KVQ + j, lane
+  // l holds slot 64 j + l's 4 columns 4 cb .. of head h, read past the L2
+  // (sc1): the unit holding a slot writes it, another XCD may read it)
   auto dma_kv = [&](const PLayer& P, float4* buf) {
-    if (P.gla || !att_unit) return;
-    const uint32_t h = w / np, t0 = (w % np) * PL;
+    if (P.gla) return;
     const float* Kr = Sseq + P.soff;
     const float* Vr = Kr + (size_t)ctx * d;
-    for (uint32_t q = wv; q < 2 * KVQ; q += 4) {
+    if constexpr (EX) {
+      if (gla_unit) {
+        const uint32_t h = w / C4, cb = w % C4, NS = (ctx + 63) / 64;
+        for (uint32_t q = wv; q < NS; q += 4) {
+          const uint32_t t = 64 * q + lane, tt = t < ctx ? t : 0u;
+          __builtin_amdgcn_global_load_lds((const void*)(Vr + (size_t)tt * d + h * HD + 4 * cb),
+                                           (lds_void*)&buf[(KVQ + q) * 64], 16, 0, 16);
+        }
+      }
+    }
+    if (!att_unit) return;
+    const uint32_t h = w / np, t0 = (w % np) * PL;
+    for (uint32_t q = wv; q < (EX ? 1u : 2u) * KVQ; q += 4) {
       const uint32_t qq = q < KVQ ? q : q - KVQ;
       const uint32_t i = qq * (64 / C4) + lane / C4, t = t0 + i;
       const uint32_t tt = (i < PL && t < ctx) ? t : t0;
@@ -366,7 +459,21 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   // used). Batch 0 of every wave, by the loading waves:
   constexpr IC<WT> HW{};                 // the head's layout (the mode's)
   constexpr int HPD = WT ? PDH : NFD;     // its pieces a row
+  // (exact: batch b of wave u holds chunk c = b % NC (k = 256 c ..; NC
+  // chunks a row) of its rows h0 + u + 4 (16 (b / NC) + i), i < 16, at
+  // pieces 16 u + i)
+  auto dma_headx = [&](uint32_t u, uint32_t b, float4* buf) {
+    const uint32_t NC = (d + 255) / 256, g = b / NC, c = b % NC;
+    for (uint32_t i = 0; i < 16; i++) {
+      const uint32_t r = h0 + u + 4 * (16 * g + i), rr = r < h1 ? r : 0u;
+      piece(wsrc(IC<0>{}, 0, 0, rr, d, c), buf, 16 * u + i);
+    }
+  };
   auto dma_head0 = [&](float4* buf) {
+    if constexpr (EX) {
+      dma_headx(wv, 0, buf);
+      return;
+    }
     const uint32_t NP = 4 * HBR * HPD;
     for (uint32_t q = wv; q < NP; q += 4) {
       const uint32_t rl = q / HPD, j = q % HPD, u = rl / HBR, i = rl % HBR;
@@ -476,6 +583,51 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     ph++;
   };
 
+  // ---- exact build: M.norm (bend/Dense/Model.bend:27-30) of the d vector
+  // in xs, in place: ss = x0 x0 + x1 x1 + ... in order (the squares formed
+  // by every thread, then one lane's chain), then x = (x * (1 / sqrt(ss / d
+  // + 1e-5))) * g, thread t the float4 at k = 4 t (g its gains)
+  auto xnorm = [&](float4 g) {
+    float4* x4 = reinterpret_cast<float4*>(xs) + tid;
+    float4* q4 = reinterpret_cast<float4*>(xs + 1024) + tid;
+    if (4 * tid < d) {
+      const float4 v = *x4;
+      *q4 = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+    }
+    lds_barrier();
+    if (wv == 0) {
+      const float ss = chain_sum_lds(0.0f, xs + 1024, d);   // (every lane the same chain)
+      if (lane == 0) red[0] = ex_rms_scale(ss, (float)d);
+    }
+    lds_barrier();
+    if (4 * tid < d) {
+      const float rs = red[0];
+      const float4 v = *x4;
+      *x4 = make_float4((v.x * rs) * g.x, (v.y * rs) * g.y, (v.z * rs) * g.z, (v.w * rs) * g.w);
+    }
+    lds_barrier();
+  };
+  // ... the products x_k w_k of nrow rows of NP pieces each (row i from
+  // piece i NP; K of each row's values used), in place of the weights, by
+  // every thread
+  auto xprod = [&](float4* buf, uint32_t nrow, auto NPc, uint32_t K) {
+    constexpr uint32_t RP = decltype(NPc)::value * 64;
+    const float4* x4 = reinterpret_cast<const float4*>(xs);
+    for (uint32_t e = tid; e < nrow * RP; e += kPT) {
+      const uint32_t k4 = e % RP;
+      if (4 * k4 < K) {
+        const float4 w4 = buf[e], x = x4[k4];
+        buf[e] = make_float4(x.x * w4.x, x.y * w4.y, x.z * w4.z, x.w * w4.w);
+      }
+    }
+    lds_barrier();
+  };
+  // ... and a row's sum of its products, (((0 + p0) + p1) + ...), k
+  // ascending
+  auto xrow = [&](const float4* row, uint32_t K) -> float {
+    return chain4(0.0f, K >> 2, [&](uint32_t q) { return row[q]; });
+  };
+
   // one layer, compiled for the buffer parity its first phase reads (B)
   // and the layout of its weights (WLc); false when a wait failed
   auto layer = [&](auto B, auto WLc, uint32_t l, uint32_t ep, unsigned long long* LL) -> bool {
@@ -493,7 +645,8 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     // wave wv the rows wv + 4 i
     BEGIN();
     float4 g4[XN];
-    load_g(WLc, g4, P.ra);
+    if constexpr (EX) g4[0] = 4 * tid < d ? *reinterpret_cast<const float4*>(W + P.ra + 4 * tid) : zero4();
+    else load_g(WLc, g4, P.ra);
     float svr = 0.0f, lamr = 0.0f, gqr = 0.0f, gkr = 0.0f, sinkr = 0.0f;
     // the mix's own inputs that do not depend on this token: GLA column
     // 4 cb + wv of head h (lane a: row a of S) and the RG-LRU lambdas; the
@@ -525,7 +678,18 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       gathered(ok);
     }
     if (!meet()) return false;
-    {
+    if constexpr (EX) {
+      const uint32_t R = qkv_rows(P), RQ = (R + G - 1) / G;
+      xnorm(g4[0]);
+      xprod(bufB, RQ, IC<NFD>{}, d);
+      // row i on wave i % 4, lane i / 4: one chain over k (every lane
+      // runs one, those past the rows the last row's: a dependent add
+      // takes about half again the cycles with most lanes masked off)
+      const uint32_t i = wv + 4 * lane, ic = i < RQ ? i : RQ - 1;
+      const float s = xrow(bufB + ic * NFD * 64, d);
+      const uint32_t r = w * RQ + i;
+      if (lane < 4 && i < RQ && r < R) ll_put(LL + P.e_qkv + r, s, ep);
+    } else {
       const uint32_t R = qkv_rows(P), RQ = (R + G - 1) / G;
       float4 xv[XN], xg[XN];
       xload(WLc, xv, d);
@@ -578,7 +742,44 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         gathered(ok);
       }
       if (!meet()) return false;
-      if (gla_unit) {
+      if (EX && gla_unit) {
+        // dd.gla.tok as the exact kernels take it (k_gla_w): every lane
+        // runs the norms' chains over q and k; S'_ac = (al_a S_ac) + (kh_a
+        // v_c); o_c = ((0 + qh_0 S'_0c) + qh_1 S'_1c) + ..., a ascending
+        // (wave wv: column c = 4 cb + wv, lane a: row a)
+        const uint32_t h = w / C4, cb = w % C4, c = 4 * cb + wv;
+        const bool on = (int)lane < HD;
+        // q's and k's sums of squares: the squares by waves 0 and 1, one
+        // lane's chain each
+        if (wv < 2 && on) xs[1024 + 64 * wv + lane] = xs[HD * wv + lane] * xs[HD * wv + lane];
+        lds_barrier();
+        if (wv < 2) {
+          const float ss = chain_sum_lds(0.0f, xs + 1024 + 64 * wv, HD);
+          if (lane == 0) red[wv] = ss;
+        }
+        lds_barrier();
+        const float s0 = red[0], s1 = red[1];
+        const float qa = on ? xs[lane] : 0.0f, ka = on ? xs[HD + lane] : 0.0f;
+        const float z = on ? xs[2 * HD + lane] : 0.0f, vc = xs[3 * HD + wv];
+        const float kn = ka / csqrt(1.0e-6f + s1);
+        float al, kh;
+        if (a.rglru) {
+          const float la = ex_rglru_log_gate(z, lamr);
+          kh = kn * ex_rglru_write_scale(la);
+          al = dexp(la);
+        } else {
+          al = ex_sigmoid(z);
+          kh = kn;
+        }
+        const float qh = qa / csqrt(1.0e-6f + s0);
+        const float sn = (al * svr) + (kh * vc);
+        if (on) Sseq[P.soff + (size_t)h * HD * HD + (size_t)lane * HD + c] = sn;
+        float* pr = xs + 256 + 64 * wv;   // this wave's qh_a S'_ac (past the gathered values)
+        if (on) pr[lane] = qh * sn;
+        __builtin_amdgcn_wave_barrier();
+        const float o = chain_sum_lds(0.0f, pr, HD);
+        if (lane == 0) ll_put(LL + P.e_o + h * HD + c, o, ep);
+      } else if (gla_unit) {
         // wave wv: column c = 4 cb + wv of head h's state, lane a its row a
         const uint32_t h = w / C4, cb = w % C4, c = 4 * cb + wv;
         const bool on = (int)lane < HD;
@@ -619,7 +820,76 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         gathered(ok);
       }
       if (!meet()) return false;
-      if (att_unit) {
+      if (EX && att_unit) {
+        // k_attn_scores' steps: M.qkn (bend/Dense/Model.bend:39-42) by the
+        // norms' chains, dd.sm.write of the row's k and v by the unit
+        // holding the slot, then each live slot's score sc (q . k) (one
+        // chain a slot, c ascending), published raw (dead slots -inf)
+        const uint32_t h = w / np, p = w % np, t0 = p * PL;
+        if ((int)tid < HD) {
+          qv[tid] = xs[tid];
+          kvv[tid] = xs[HD + tid];
+          vvv[tid] = xs[2 * HD + tid];
+        }
+        lds_barrier();
+        if (a.qk) {
+          if ((int)tid < HD) {
+            xs[1024 + tid] = qv[tid] * qv[tid];
+            xs[1088 + tid] = kvv[tid] * kvv[tid];
+          }
+          lds_barrier();
+          if (wv < 2) {
+            const float ss = chain_sum_lds(0.0f, xs + 1024 + 64 * wv, HD);
+            if (lane == 0) red[wv] = ex_rms_scale(ss, (float)HD);
+          }
+          lds_barrier();
+          if ((int)tid < HD) {
+            qv[tid] = (qv[tid] * red[0]) * (1.0f + gqr);
+            kvv[tid] = (kvv[tid] * red[1]) * (1.0f + gkr);
+          }
+          lds_barrier();
+        }
+        if (slot >= t0 && slot < t0 + PL && (int)tid < HD) {
+          float* Kr = Sseq + P.soff;
+          __hip_atomic_store(Kr + (size_t)slot * d + h * HD + tid, kvv[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(Kr + (size_t)ctx * d + (size_t)slot * d + h * HD + tid, vvv[tid], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // the products q_c K_tc in place of K, slot i's float4 u at i C4 +
+        // (u + i) mod C4 (so the slots' chains read different banks), and
+        // the own slot's q_c k_c
+        {
+          const float4* q4 = reinterpret_cast<const float4*>(qv);
+          constexpr uint32_t NQ = (KPASS * 64 * C4 + kPT - 1) / kPT;
+          float4 pk[NQ];
+#pragma unroll
+          for (uint32_t j = 0; j < NQ; j++) {
+            const uint32_t e = tid + kPT * j, u = e % C4;
+            const float4 k4 = e < KPASS * 64 * C4 ? bufN[e] : zero4(), q = q4[u];
+            pk[j] = make_float4(q.x * k4.x, q.y * k4.y, q.z * k4.z, q.w * k4.w);
+          }
+          if ((int)tid < HD) xs[1152 + tid] = qv[tid] * kvv[tid];
+          lds_barrier();
+#pragma unroll
+          for (uint32_t j = 0; j < NQ; j++) {
+            const uint32_t e = tid + kPT * j, i = e / C4, u = e % C4;
+            if (e < KPASS * 64 * C4) bufN[i * C4 + (u + i) % C4] = pk[j];
+          }
+          lds_barrier();
+        }
+        if (tid < PL) {
+          const uint32_t t = t0 + tid;
+          float acc;
+          if (t == slot) {
+            acc = chain_sum_lds(0.0f, xs + 1152, HD);
+          } else {
+            const float4* k4 = bufN + tid * C4;
+            acc = chain4(0.0f, C4, [&](uint32_t u) { return k4[(u + tid) % C4]; });
+          }
+          const float sc = 1.0f / csqrt((float)HD);
+          ll_put(LL + P.e_part + (size_t)(h * np + p) * PL + tid, t <= npos ? sc * acc : -INFINITY, ep);
+        }
+      } else if (att_unit) {
         const uint32_t h = w / np, p = w % np, t0 = p * PL;
         float q = (int)tid < HD ? xs[tid] : 0.0f, kx = (int)tid < HD ? xs[HD + tid] : 0.0f;
         if (a.qk) {
@@ -722,8 +992,22 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       // (the K and V pieces are read: gate|up's first two parts go to their
       // buffer)
       BEGIN();
-      dma_gu(WLc, P, bufN, 0, 2);
-      {
+      if constexpr (!EX) dma_gu(WLc, P, bufN, 0, 2);   // (exact: the V slices in that buffer are read here)
+      if constexpr (EX) {
+        // exact: v's 4 columns into xs[0 .. 4), the head's scores of slots
+        // 0 .. npos into xs[4 ..)
+        bool ok = true;
+        if (gla_unit) {
+          const uint32_t h = w / C4, cb = w % C4;
+          auto map = [&](uint32_t i) -> uint64_t {
+            if (i < 4) return P.e_qkv + 2 * d + h * HD + 4 * cb + i;
+            const uint32_t t = i - 4;
+            return P.e_part + (uint64_t)(h * np + t / PL) * PL + t % PL;
+          };
+          ok = poll_gather<NFF + 1>(LL, npos + 5, ep, map, xs, a.ctl, a.tmo);
+        }
+        gathered(ok);
+      } else {
         bool ok = true;
         if (gla_unit) {
           const uint32_t h = w / C4, cb = w % C4;
@@ -740,7 +1024,52 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         gathered(ok);
       }
       if (!meet()) return false;
-      if (gla_unit && wv == 0) {
+      if (EX && gla_unit) {
+        // k_attn_out's steps over the whole window: m (a maximum: any
+        // order), dd.sm.max with the sink, e_t = exp(y_t - m), then one chain
+        // a column oi_c = ((0 + e_0 V_0c) + e_1 V_1c) + ... and se = ((0 +
+        // e_0) + e_1) + ..., t ascending; o_c = (1 / (se (+ exp(sink - m))))
+        // oi_c. The own slot's V comes from the gathered v.
+        const uint32_t h = w / C4, cb = w % C4, nl = npos + 1;
+        float* e = xs + 4;
+        float mloc = -INFINITY;
+        for (uint32_t t = tid; t < nl; t += kPT) {
+          const float y = e[t];
+          mloc = y > mloc ? y : mloc;
+        }
+        mloc = wmax_gt(mloc);
+        if (lane == 0) red[4 + wv] = mloc;
+        lds_barrier();
+        float m = red[4];
+        for (int u = 1; u < 4; u++) m = red[4 + u] > m ? red[4 + u] : m;
+        if (a.sinks) m = ex_max(m, sinkr);
+        for (uint32_t t = tid; t < nl; t += kPT) e[t] = dexp(e[t] - m);
+        const float4* vs = bufN + KVQ * 64;   // slot t's 4 columns
+        if (tid < 4) reinterpret_cast<float*>(bufN + KVQ * 64)[4 * slot + tid] = xs[tid];
+        lds_barrier();
+        // the products e_t V_tc, column c at pc + c PC (past Wo's pieces in
+        // the other buffer, which this phase neither reads nor loads)
+        constexpr uint32_t PC = 2048 + 4;
+        float* pc = reinterpret_cast<float*>(bufB) + 4096;
+        for (uint32_t t = tid; t < nl; t += kPT) {
+          const float4 v = vs[t];
+          const float et = e[t];
+          pc[t] = et * v.x;
+          pc[PC + t] = et * v.y;
+          pc[2 * PC + t] = et * v.z;
+          pc[3 * PC + t] = et * v.w;
+        }
+        lds_barrier();
+        if (wv == 0) {
+          const float oi = chain_sum_lds(0.0f, pc + (lane & 3) * PC, nl);
+          if (lane < 4) part4[0][lane].x = oi;
+        } else if (wv == 1) {
+          const float se = chain_sum_lds(0.0f, e, nl);
+          if (lane == 0) red[0] = a.sinks ? se + dexp(sinkr - m) : se;
+        }
+        lds_barrier();
+        if (wv == 0 && lane < 4) ll_put(LL + P.e_o + h * HD + 4 * cb + lane, (1.0f / red[0]) * part4[0][lane].x, ep);
+      } else if (gla_unit && wv == 0) {
         // lane i: piece i (np <= 64)
         const uint32_t h = w / C4, cb = w % C4;
         const bool on = lane < np;
@@ -763,11 +1092,20 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     // ---- xa = x + Wo o (Wo in bufB)
     BEGIN();
     float4 gf[XN];
-    load_g(WLc, gf, P.rf);
-    dma_gu(WLc, P, bufN, 2, 3);
+    if constexpr (EX) gf[0] = 4 * tid < d ? *reinterpret_cast<const float4*>(W + P.rf + 4 * tid) : zero4();
+    else load_g(WLc, gf, P.rf);
+    dma_gu(WLc, P, bufN, EX && !P.gla ? 0 : 2, 3);
     gathered(poll_gather<PEX>(LL, d, ep, Ident{P.e_o}, xs, a.ctl, a.tmo));
     if (!meet()) return false;
-    if (orow_ok) {
+    if constexpr (EX) {
+      // add2 (bend/Dense/Model.bend:44-45): x + (the row's chain), lane 0
+      xprod(bufB, RO, IC<NFD>{}, d);
+      const float s = xrow(bufB + (wv < RO ? wv : 0u) * NFD * 64, d);
+      if (orow_ok) {
+        xa_own = x_own + s;
+        if (lane == 0) ll_put(LL + P.e_xa + orow, xa_own, ep);
+      }
+    } else if (orow_ok) {
       float4 xv[XW];
       xload(WLc, xv, d);
       uint4 pw[PDc];
@@ -787,7 +1125,19 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     dma_wd(WLc, P, bufB);
     gathered(poll_gather<PEX>(LL, d, ep, Ident{P.e_xa}, xs, a.ctl, a.tmo));
     if (!meet()) return false;
-    {
+    if constexpr (EX) {
+      // M.norm, then lane 2 i + u: gate (u 0) or up (u 1) of pair wv + 4 i;
+      // hh = silu(g) u (bend/Dense/Model.bend:58-59)
+      xnorm(gf[0]);
+      xprod(bufN, 2 * RGp, IC<NFD>{}, d);
+      const uint32_t pi = wv + 4 * ((lane & 3) >> 1), u = lane & 1, pc = pi < RGp ? pi : RGp - 1;
+      const float s = xrow(bufN + (pc * 2 + u) * NFD * 64, d);
+      const float up = __shfl_down(s, 1, 64);
+      if (lane < 4 && u == 0) {
+        const uint32_t jp = w * RGp + pi;
+        if (pi < RGp && jp < f) ll_put(LL + P.e_hh + jp, ex_silu(s) * up, ep);
+      }
+    } else {
       float4 xv[XN], xg[XN];
       xload(WLc, xv, d);
       uint4 pw[2][2][PDc];
@@ -832,7 +1182,14 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     else dma_head0(bufN);
     gathered(poll_gather<PEF>(LL, f, ep, Ident{P.e_hh}, xs, a.ctl, a.tmo));
     if (!meet()) return false;
-    if (orow_ok) {
+    if constexpr (EX) {
+      xprod(bufB, RO, IC<NFF>{}, f);
+      const float s = xrow(bufB + (wv < RO ? wv : 0u) * NFF * 64, f);
+      if (orow_ok) {
+        x_own = xa_own + s;
+        if (lane == 0) ll_put(LL + P.e_x + orow, x_own, ep);
+      }
+    } else if (orow_ok) {
       float4 xv[XF];
       xload(WLc, xv, f);
       uint4 pw[PFc];
@@ -858,13 +1215,80 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     float4* b1 = bufp(IC<1 - PB>{});
     BEGIN();
     float4 gf[XN];
-    load_g(HW, gf, a.fin);
+    if constexpr (EX) gf[0] = 4 * tid < d ? *reinterpret_cast<const float4*>(W + a.fin + 4 * tid) : zero4();
+    else load_g(HW, gf, a.fin);
     gathered(poll_gather<PEX>(LL, d, ep, Ident{Ls[L - 1].e_x}, xs, a.ctl, a.tmo));
     if (!meet()) return false;
+    unsigned long long best = 0ull;
+    if constexpr (EX) {
+      // the final M.norm, then each row's chain over k (lane i < 16 of wave
+      // wv: row h0 + wv + 4 (16 g + i), its chunks c = 0 .. NC - 1 in
+      // batches g NC + c, the chain carried across them)
+      xnorm(gf[0]);
+      const uint32_t NC = (d + 255) / 256;
+      float hacc = 0.0f;
+      auto rowsx = [&](float4* cur, uint32_t b) {
+        const uint32_t g = b / NC, c = b % NC;
+        const uint32_t n4 = min(64u, (d - 256 * c) >> 2);
+        // the wave's products x_k w_k in place of its 16 pieces, piece i's
+        // float4 q at (q + i) mod 64 (so the 16 rows' chains read
+        // different banks): every lane's reads first, then its writes
+        {
+          float4* base = cur + 16 * wv * 64;
+          const float4 xv = lane < n4 ? reinterpret_cast<const float4*>(xs)[64 * c + lane] : zero4();
+          float4 pv[16];
+#pragma unroll
+          for (int i = 0; i < 16; i++) {
+            const float4 w4 = base[i * 64 + lane];
+            pv[i] = make_float4(xv.x * w4.x, xv.y * w4.y, xv.z * w4.z, xv.w * w4.w);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          __builtin_amdgcn_wave_barrier();
+#pragma unroll
+          for (int i = 0; i < 16; i++) base[i * 64 + ((lane + i) & 63)] = pv[i];
+          __builtin_amdgcn_wave_barrier();
+        }
+        {
+          const uint32_t li = lane & 15;   // (lanes 16 .. 63 repeat lanes 0 .. 15's chains)
+          const float4* wr = cur + (16 * wv + li) * 64;
+          hacc = chain4(hacc, n4, [&](uint32_t q) { return wr[(q + li) & 63]; });
+        }
+        if (c == NC - 1) {
+          const uint32_t i = 16 * g + lane, r = h0 + wv + 4 * i;
+          if (lane < 16 && r < h1) {
+            lgs[wv][i] = hacc;
+            const unsigned long long kk = argmax_key(hacc, r);
+            best = kk > best ? kk : best;
+          }
+          hacc = 0.0f;
+        }
+      };
+      for (uint32_t b = 0; b < nhb; b += 2) {
+        if (b + 1 < nhb) {
+          dma_headx(wv, b + 1, b1);
+          if (b > 0) __builtin_amdgcn_s_waitcnt(ANA_VM(16));
+        } else if (b > 0) {
+          __builtin_amdgcn_s_waitcnt(0);
+        }
+        rowsx(b0, b);
+        if (b + 1 < nhb) {
+          if (b + 2 < nhb) {
+            dma_headx(wv, b + 2, b0);
+            __builtin_amdgcn_s_waitcnt(ANA_VM(16));
+          } else {
+            __builtin_amdgcn_s_waitcnt(0);
+          }
+          rowsx(b1, b + 1);
+        }
+      }
+      for (int m = 32; m >= 1; m >>= 1) {
+        const unsigned long long o = __shfl_xor(best, m, 64);
+        best = o > best ? o : best;
+      }
+    } else {
     float4 xv[XN], xg[XN];
     xload(HW, xv, d);
     const float rs = norm_fold(HW, gf, xv, xg);
-    unsigned long long best = 0ull;
     auto rows = [&](float4* cur, uint32_t b) {
       uint4 pw[HBR][HPD];
 #pragma unroll
@@ -913,6 +1337,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         }
         rows(b1, b + 1);
       }
+    }
     }
     if (lane == 0) key_s[wv] = best;
     __syncthreads();
@@ -1057,7 +1482,7 @@ uint32_t decode1_pieces(const ana_config& c, uint32_t G) {
   return np;
 }
 
-bool decode1_fits(const ana_config& c, uint32_t G) {
+bool decode1_fits(const ana_config& c, uint32_t G, bool exact) {
   const uint32_t hd = c.heads ? c.d / c.heads : 0;
   if (G == 0 || G > 256 || c.layers == 0) return false;
   if (hd != 16 && hd != 32 && hd != 64) return false;
@@ -1069,6 +1494,9 @@ bool decode1_fits(const ana_config& c, uint32_t G) {
   const uint32_t np = decode1_pieces(c, G);
   if (np == 0 || c.heads * np > G || (c.ctx + np - 1) / np > 128 || 6 * np > 256) return false;
   if (c.vocab > 65536 || c.layers > kMaxPLayers) return false;
+  // exact: a head's scores of the whole window in LDS, and its K pieces
+  // with the combine's V slices in one buffer
+  if (exact && (c.ctx > 2048 || 2 * (hd / 4) + (c.ctx + 63) / 64 > 64)) return false;
   return true;
 }
 
@@ -1088,7 +1516,11 @@ hipError_t launch_decode1(const PersistArgs& a, uint32_t G, hipStream_t st) {
   // every matrix on 16 bytes)
   const bool bf = a.Wh != nullptr;
   if (bf && (a.d % 8 || a.f % 8)) return hipErrorInvalidValue;
-#define K_(H, T) (bf ? (const void*)k_decode1<H, 3, 8, T, 1> : (const void*)k_decode1<H, 3, 8, T, 0>)
+  if (a.exact && (bf || a.ctx > 2048)) return hipErrorInvalidValue;
+#define K_(H, T)                                                        \
+  (a.exact ? (const void*)k_decode1<H, 3, 8, T, 0, true>               \
+   : bf    ? (const void*)k_decode1<H, 3, 8, T, 1, false>              \
+           : (const void*)k_decode1<H, 3, 8, T, 0, false>)
 #define L_(H) return hipLaunchCooperativeKernel(tr ? K_(H, true) : K_(H, false), dim3(G), dim3(kPT), args, 0, st)
   if (hd == 64) L_(64);
   if (hd == 32) L_(32);

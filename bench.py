@@ -16,9 +16,10 @@ every mode, B = 64 x 512 prefill and window scoring, 64 agent episodes, and
 BASELINE's other decode configs (next: B = 32 at 1920+; v3: B = 64 sampled;
 bf16: B = 256), the last in a child process of their own.
 
-The roofline entry is the dominant kernel of the B = 1 step: in fast_fp32
-the persistent step kernel k_decode1 (one launch runs every step of a
-call), elsewhere the layer products with the LM head. `achieved` is their
+The roofline entry is the dominant kernel of the B = 1 step: the
+persistent step kernel k_decode1 (one launch runs every step of a call;
+every mode has a build of it), or, where it does not run, the layer
+products with the LM head. `achieved` is their
 algorithmic bytes (every weight once a step, the GLA states read and
 written, the live K/V rows read and the new ones written) over their
 launches' HIP-event time on the library's stream, against 8 TB/s;
@@ -208,6 +209,9 @@ def cpu_baseline(path: str, c: cf.Config, seconds: float) -> dict:
 
 
 KERNEL_PERSIST = {
+    "exact": ("k_decode1 (exact build, one greedy sequence: every phase of every step in one cooperative "
+              "launch of one workgroup per CU, each output an in-order chain in one lane; weights streamed "
+              "into LDS a phase ahead)"),
     "fast_fp32": ("k_decode1 (fast fp32, one greedy sequence: every phase of every step in one "
                   "cooperative launch of one workgroup per CU; weights streamed into LDS a phase ahead)"),
     "bf16": ("k_decode1 (bf16 weights past the first layer and in the head, one greedy sequence: every "

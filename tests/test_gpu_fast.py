@@ -554,6 +554,47 @@ def test_fast_persistent_decode(oracle, small_ckpt, mid_ckpt, big_ckpt, model, m
     assert e <= 1e-4, e
 
 
+@pytest.mark.parametrize("model", ["small", "mid", "115m"])
+def test_exact_persistent_decode(oracle, small_ckpt, mid_ckpt, big_ckpt, model):
+    """The exact mode's one-sequence greedy loop as one persistent launch a
+    call (the exact build of the persistent kernel: the norms, products, GLA
+    and attention sums as in-order chains, the attention's softmax over the
+    whole window in a phase of its own): every id and the logits after the
+    call bit for bit equal to the oracle's greedy loop, and to the captured
+    graphs' (ANA_PERSIST=0). The small and mid cases (ctx 64) run past the
+    ring's wrap; the 115M case past the first 128 positions, so each
+    attention piece gets live slots in turn."""
+    print(f"case exact persistent decode {model}", flush=True)
+    path = {"small": small_ckpt, "mid": mid_ckpt, "115m": big_ckpt}[model]
+    oracle.set_threads(8)
+    m = oracle.Model(path)
+    steps = {"small": 70, "mid": 70, "115m": 150}[model]
+    pr = [int(t) for t in ckpt.prompt(3, 9, m.vocab)]
+    st = oracle.State(m)
+    for p, t in enumerate(pr):
+        st.feed(p, t)
+    want, lg = [], None
+    for k in range(steps):
+        lg = st.logits()
+        t = int(oracle.top(lg))
+        want.append(t)
+        if k + 1 < steps:
+            st.feed(len(pr) + k, t)
+    for persist in ("1", "0"):
+        os.environ["ANA_PERSIST"] = persist
+        try:
+            with ana_amd.Decoder(path, max_seqs=1, prefill_chunk=16, numerics=ana_amd.EXACT_FP32) as dec:
+                dec.feeds(0, 0, pr[:-1])
+                out = [int(t) for t in dec.generate([0], [len(pr) - 1], [pr[-1]], steps)[0]]
+                got = dec.logits([0])[0]
+        finally:
+            os.environ.pop("ANA_PERSIST", None)
+        first = next((k for k, (a, b) in enumerate(zip(out, want)) if a != b), None)
+        assert first is None, (persist, first, out[first], want[first])
+        assert np.array_equal(got.view(np.uint32), lg.view(np.uint32)), (persist, float(np.abs(got - lg).max()))
+        print(f"persist {persist}: {steps} ids and the final logits bit-exact", flush=True)
+
+
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("model,n", [("v1", 40), ("v1", 5), ("v1", 3)])
 def test_fast_fused_head_sampler(oracle, mid_ckpt, tmp_path, mode, model, n):
