@@ -82,11 +82,12 @@ __device__ __forceinline__ void lds_barrier() {
 
 // The workgroup's threads poll n entries (entry i at base[map(i)]; thread t
 // takes i = t + 256 e, e < PE) until each carries epoch ep in its upper
-// half, then dst[i] = the value. False (for this wave) when the wait passed
-// tmo ticks or another workgroup gave up.
+// half, then dst[i] = the value (and sq[i] its square, when sq is given).
+// False (for this wave) when the wait passed tmo ticks or another
+// workgroup gave up.
 template <int PE, class Map>
 __device__ __forceinline__ bool poll_gather(const unsigned long long* base, uint32_t n, uint32_t ep, Map map, float* dst,
-                                            uint32_t* ctl, uint64_t tmo) {
+                                            uint32_t* ctl, uint64_t tmo, float* sq = nullptr) {
   uint32_t pt = threadIdx.x;
   asm volatile("" : "+v"(pt));   // (its addresses are built here, not hoisted out of the caller's loop)
   unsigned long long v[PE];
@@ -116,7 +117,11 @@ __device__ __forceinline__ bool poll_gather(const unsigned long long* base, uint
 #pragma unroll
   for (int e = 0; e < PE; e++) {
     const uint32_t i = pt + kPT * e;
-    if (i < n) dst[i] = __uint_as_float((uint32_t)v[e]);
+    if (i < n) {
+      const float f = __uint_as_float((uint32_t)v[e]);
+      dst[i] = f;
+      if (sq) sq[i] = f * f;
+    }
   }
   return ok;
 }
@@ -171,56 +176,12 @@ __device__ __forceinline__ float rsq(float x) { return __builtin_amdgcn_rsqf(x);
 // order, a product and the sum it joins two roundings (bulk.c's product
 // loop)
 
-// s + v(0).x + v(0).y + ... + v(n4 - 1).w in order, the float4s read from
-// LDS by the accessor: every term a product formed beforehand by the whole
-// workgroup (a product next to its add puts its latency in the chain too,
-// about twice the add's cycles a term). Two sets of eight float4 in turn,
-// each read again as soon as its adds are issued (numerics.h's chain_lds
-// over an index map).
+// s + v(0).x + v(0).y + ... + v(n4 - 1).w in order (numerics.h's block
+// chain), every term a product the workgroup formed beforehand: a product
+// formed next to its add puts its latency in the chain too
 template <class F>
 __device__ __forceinline__ float chain4(float s, uint32_t n4, F at) {
-  auto id = [](float x) { return x; };
-  uint32_t i = 0;
-  if (n4 >= 16) {
-    float4 a[8], b[8];
-#pragma unroll
-    for (int u = 0; u < 8; u++) a[u] = at(u);
-#pragma unroll
-    for (int u = 0; u < 8; u++) b[u] = at(8 + u);
-    for (i = 16; i + 16 <= n4; i += 16) {
-      s = chain_add8(s, a, id);
-#pragma unroll
-      for (int u = 0; u < 8; u++) a[u] = at(i + u);
-      s = chain_add8(s, b, id);
-#pragma unroll
-      for (int u = 0; u < 8; u++) b[u] = at(i + 8 + u);
-    }
-    s = chain_add8(s, a, id);
-    if (i + 8 <= n4) {
-#pragma unroll
-      for (int u = 0; u < 8; u++) a[u] = at(i + u);
-      s = chain_add8(s, b, id);
-      s = chain_add8(s, a, id);
-      i += 8;
-    } else {
-      s = chain_add8(s, b, id);
-    }
-  }
-  if (i + 8 <= n4) {
-    float4 a[8];
-#pragma unroll
-    for (int u = 0; u < 8; u++) a[u] = at(i + u);
-    s = chain_add8(s, a, id);
-    i += 8;
-  }
-  for (; i < n4; i++) {
-    const float4 v = at(i);
-    s = s + v.x;
-    s = s + v.y;
-    s = s + v.z;
-    s = s + v.w;
-  }
-  return s;
+  return chain4_lds(s, n4, at, [](float x) { return x; });
 }
 
 // a wave's maximum by r = t > r ? t : r (a NaN never wins), as the exact
@@ -584,26 +545,30 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   };
 
   // ---- exact build: M.norm (bend/Dense/Model.bend:27-30) of the d vector
-  // in xs, in place: ss = x0 x0 + x1 x1 + ... in order (the squares formed
-  // by every thread, then one lane's chain), then x = (x * (1 / sqrt(ss / d
-  // + 1e-5))) * g, thread t the float4 at k = 4 t (g its gains)
-  auto xnorm = [&](float4 g) {
-    float4* x4 = reinterpret_cast<float4*>(xs) + tid;
-    float4* q4 = reinterpret_cast<float4*>(xs + 1024) + tid;
-    if (4 * tid < d) {
-      const float4 v = *x4;
-      *q4 = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
-    }
-    lds_barrier();
+  // in xs: ss = x0 x0 + x1 x1 + ... in order (one wave's chain over the
+  // squares the gather left at xs + 1024), then rs = 1 / sqrt(ss / d +
+  // 1e-5); the normed values (x rs) g are formed where they are used
+  float* const sqx = EX ? xs + 1024 : nullptr;
+  auto xrs = [&]() -> float {
     if (wv == 0) {
       const float ss = chain_sum_lds(0.0f, xs + 1024, d);   // (every lane the same chain)
       if (lane == 0) red[0] = ex_rms_scale(ss, (float)d);
     }
     lds_barrier();
-    if (4 * tid < d) {
-      const float rs = red[0];
-      const float4 v = *x4;
-      *x4 = make_float4((v.x * rs) * g.x, (v.y * rs) * g.y, (v.z * rs) * g.z, (v.w * rs) * g.w);
+    return red[0];
+  };
+  // ... the products ((x_k rs) g_k) w_k of nrow rows (row i from piece i
+  // NP) in place of the weights: thread t the float4 at k = 4 t of every row
+  // (g its gains)
+  auto xprod_n = [&](float4* buf, uint32_t nrow, auto NPc, float rs, float4 g) {
+    constexpr uint32_t RP = decltype(NPc)::value * 64;
+    if (tid < RP && 4 * tid < d) {
+      const float4 v = reinterpret_cast<const float4*>(xs)[tid];
+      const float4 x = make_float4((v.x * rs) * g.x, (v.y * rs) * g.y, (v.z * rs) * g.z, (v.w * rs) * g.w);
+      for (uint32_t i = 0; i < nrow; i++) {
+        const float4 w4 = buf[i * RP + tid];
+        buf[i * RP + tid] = make_float4(x.x * w4.x, x.y * w4.y, x.z * w4.z, x.w * w4.w);
+      }
     }
     lds_barrier();
   };
@@ -671,17 +636,20 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
       bool ok = true;
       if (l == 0) {
         // layer 0's input is the token's embedding row
-        for (uint32_t i = tid; i < d; i += kPT) xs[i] = W[(size_t)tok * d + i];
+        for (uint32_t i = tid; i < d; i += kPT) {
+          const float v = W[(size_t)tok * d + i];
+          xs[i] = v;
+          if (EX) xs[1024 + i] = v * v;
+        }
       } else {
-        ok = poll_gather<PEX>(LL, d, ep, Ident{Ls[l - 1].e_x}, xs, a.ctl, a.tmo);
+        ok = poll_gather<PEX>(LL, d, ep, Ident{Ls[l - 1].e_x}, xs, a.ctl, a.tmo, sqx);
       }
       gathered(ok);
     }
     if (!meet()) return false;
     if constexpr (EX) {
       const uint32_t R = qkv_rows(P), RQ = (R + G - 1) / G;
-      xnorm(g4[0]);
-      xprod(bufB, RQ, IC<NFD>{}, d);
+      xprod_n(bufB, RQ, IC<NFD>{}, xrs(), g4[0]);
       // row i on wave i % 4, lane i / 4: one chain over k (every lane
       // runs one, those past the rows the last row's: a dependent add
       // takes about half again the cycles with most lanes masked off)
@@ -1123,13 +1091,12 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     // wv + 4 i
     BEGIN();
     dma_wd(WLc, P, bufB);
-    gathered(poll_gather<PEX>(LL, d, ep, Ident{P.e_xa}, xs, a.ctl, a.tmo));
+    gathered(poll_gather<PEX>(LL, d, ep, Ident{P.e_xa}, xs, a.ctl, a.tmo, sqx));
     if (!meet()) return false;
     if constexpr (EX) {
       // M.norm, then lane 2 i + u: gate (u 0) or up (u 1) of pair wv + 4 i;
       // hh = silu(g) u (bend/Dense/Model.bend:58-59)
-      xnorm(gf[0]);
-      xprod(bufN, 2 * RGp, IC<NFD>{}, d);
+      xprod_n(bufN, 2 * RGp, IC<NFD>{}, xrs(), gf[0]);
       const uint32_t pi = wv + 4 * ((lane & 3) >> 1), u = lane & 1, pc = pi < RGp ? pi : RGp - 1;
       const float s = xrow(bufN + (pc * 2 + u) * NFD * 64, d);
       const float up = __shfl_down(s, 1, 64);
@@ -1217,14 +1184,22 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     float4 gf[XN];
     if constexpr (EX) gf[0] = 4 * tid < d ? *reinterpret_cast<const float4*>(W + a.fin + 4 * tid) : zero4();
     else load_g(HW, gf, a.fin);
-    gathered(poll_gather<PEX>(LL, d, ep, Ident{Ls[L - 1].e_x}, xs, a.ctl, a.tmo));
+    gathered(poll_gather<PEX>(LL, d, ep, Ident{Ls[L - 1].e_x}, xs, a.ctl, a.tmo, sqx));
     if (!meet()) return false;
     unsigned long long best = 0ull;
     if constexpr (EX) {
       // the final M.norm, then each row's chain over k (lane i < 16 of wave
       // wv: row h0 + wv + 4 (16 g + i), its chunks c = 0 .. NC - 1 in
       // batches g NC + c, the chain carried across them)
-      xnorm(gf[0]);
+      {
+        const float rs = xrs();
+        if (4 * tid < d) {
+          float4* x4 = reinterpret_cast<float4*>(xs) + tid;
+          const float4 v = *x4, g = gf[0];
+          *x4 = make_float4((v.x * rs) * g.x, (v.y * rs) * g.y, (v.z * rs) * g.z, (v.w * rs) * g.w);
+        }
+        lds_barrier();
+      }
       const uint32_t NC = (d + 255) / 256;
       float hacc = 0.0f;
       auto rowsx = [&](float4* cur, uint32_t b) {
