@@ -557,40 +557,71 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     lds_barrier();
     return red[0];
   };
-  // ... the products ((x_k rs) g_k) w_k of nrow rows (row i from piece i
-  // NP) in place of the weights: thread t the float4 at k = 4 t of every row
-  // (g its gains)
-  auto xprod_n = [&](float4* buf, uint32_t nrow, auto NPc, float rs, float4 g) {
-    constexpr uint32_t RP = decltype(NPc)::value * 64;
-    if (tid < RP && 4 * tid < d) {
-      const float4 v = reinterpret_cast<const float4*>(xs)[tid];
-      const float4 x = make_float4((v.x * rs) * g.x, (v.y * rs) * g.y, (v.z * rs) * g.z, (v.w * rs) * g.w);
-      for (uint32_t i = 0; i < nrow; i++) {
-        const float4 w4 = buf[i * RP + tid];
-        buf[i * RP + tid] = make_float4(x.x * w4.x, x.y * w4.y, x.z * w4.z, x.w * w4.w);
-      }
-    }
-    lds_barrier();
-  };
-  // ... the products x_k w_k of nrow rows of NP pieces each (row i from
-  // piece i NP; K of each row's values used), in place of the weights, by
-  // every thread
-  auto xprod = [&](float4* buf, uint32_t nrow, auto NPc, uint32_t K) {
-    constexpr uint32_t RP = decltype(NPc)::value * 64;
+  // ... the products of nrow rows (row i from piece i NP, K values each) in
+  // place of the weights: x_k w_k, or with the norm (NORM) ((x_k rs) g_k)
+  // w_k, g the gains at k = 4 tid (the only float4 of x its thread takes
+  // then). With ROT row i's float4 k4 goes to (k4 + i mod 16) mod RP of
+  // the row, so the rows one wave chains at once start on different LDS
+  // banks (every row starts on bank 0: four such rows a wave on four waves
+  // took 16 cycles a dependent add against 7); gate|up takes it (four rows
+  // a wave), the others keep their places (one to three rows a wave, where
+  // the rotation's barriers cost more than it saved). Thread t takes k4 = t
+  // (and t + 256) of GR rows at a time: their reads, (ROT: a barrier,) their
+  // writes
+  auto xprod_rows = [&](float4* buf, uint32_t nrow, auto NPc, uint32_t K, auto NORMc, float rs, float4 g,
+                        auto ROTc) {
+    constexpr bool ROT = decltype(ROTc)::value;
+    constexpr uint32_t RP = decltype(NPc)::value * 64, KT = (RP + kPT - 1) / kPT, GR = ROT ? 8 : 4;
     const float4* x4 = reinterpret_cast<const float4*>(xs);
-    for (uint32_t e = tid; e < nrow * RP; e += kPT) {
-      const uint32_t k4 = e % RP;
-      if (4 * k4 < K) {
-        const float4 w4 = buf[e], x = x4[k4];
-        buf[e] = make_float4(x.x * w4.x, x.y * w4.y, x.z * w4.z, x.w * w4.w);
+    float4 x[KT];
+#pragma unroll
+    for (uint32_t kt = 0; kt < KT; kt++) {
+      const uint32_t k4 = tid + kPT * kt;
+      x[kt] = k4 < RP && 4 * k4 < K ? x4[k4] : zero4();
+      if constexpr (decltype(NORMc)::value)
+        x[kt] = make_float4((x[kt].x * rs) * g.x, (x[kt].y * rs) * g.y, (x[kt].z * rs) * g.z, (x[kt].w * rs) * g.w);
+    }
+    for (uint32_t i0 = 0; i0 < nrow; i0 += GR) {
+      float4 pr[GR][KT];
+#pragma unroll
+      for (uint32_t j = 0; j < GR; j++) {
+#pragma unroll
+        for (uint32_t kt = 0; kt < KT; kt++) {
+          const uint32_t k4 = tid + kPT * kt;
+          const float4 w4 = i0 + j < nrow && k4 < RP ? buf[(i0 + j) * RP + k4] : zero4();
+          pr[j][kt] = make_float4(x[kt].x * w4.x, x[kt].y * w4.y, x[kt].z * w4.z, x[kt].w * w4.w);
+        }
+      }
+      if constexpr (ROT) lds_barrier();
+#pragma unroll
+      for (uint32_t j = 0; j < GR; j++) {
+#pragma unroll
+        for (uint32_t kt = 0; kt < KT; kt++) {
+          const uint32_t k4 = tid + kPT * kt, i = i0 + j, q = k4 + (ROT ? i & 15 : 0);
+          if (i < nrow && k4 < RP && 4 * k4 < K) buf[i * RP + (q < RP ? q : q - RP)] = pr[j][kt];
+        }
       }
     }
     lds_barrier();
   };
-  // ... and a row's sum of its products, (((0 + p0) + p1) + ...), k
-  // ascending
-  auto xrow = [&](const float4* row, uint32_t K) -> float {
-    return chain4(0.0f, K >> 2, [&](uint32_t q) { return row[q]; });
+  auto xprod_n = [&](float4* buf, uint32_t nrow, auto NPc, float rs, float4 g, auto ROTc) {
+    xprod_rows(buf, nrow, NPc, d, std::true_type{}, rs, g, ROTc);
+  };
+  auto xprod = [&](float4* buf, uint32_t nrow, auto NPc, uint32_t K) {
+    xprod_rows(buf, nrow, NPc, K, std::false_type{}, 1.0f, zero4(), std::false_type{});
+  };
+  // ... and row i's sum of its products (so placed), (((0 + p0) + p1) +
+  // ...), k ascending
+  auto xrow = [&](const float4* buf, uint32_t i, auto NPc, uint32_t K, auto ROTc) -> float {
+    constexpr uint32_t RP = decltype(NPc)::value * 64;
+    // (two contiguous runs: float4s 0 .. RP - r - 1 at r .., the rest from
+    // the row's start; an index wrapped at each read put its VALU work in
+    // the chain)
+    const float4* row = buf + i * RP;
+    const uint32_t r = decltype(ROTc)::value ? i & 15 : 0u, K4 = K >> 2, n1 = K4 < RP - r ? K4 : RP - r;
+    const float4* a = row + r;
+    const float s1 = chain4(0.0f, n1, [&](uint32_t q) { return a[q]; });
+    return chain4(s1, K4 - n1, [&](uint32_t q) { return row[q]; });
   };
 
   // one layer, compiled for the buffer parity its first phase reads (B)
@@ -649,12 +680,12 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     if (!meet()) return false;
     if constexpr (EX) {
       const uint32_t R = qkv_rows(P), RQ = (R + G - 1) / G;
-      xprod_n(bufB, RQ, IC<NFD>{}, xrs(), g4[0]);
+      xprod_n(bufB, RQ, IC<NFD>{}, xrs(), g4[0], std::false_type{});
       // row i on wave i % 4, lane i / 4: one chain over k (every lane
       // runs one, those past the rows the last row's: a dependent add
       // takes about half again the cycles with most lanes masked off)
       const uint32_t i = wv + 4 * lane, ic = i < RQ ? i : RQ - 1;
-      const float s = xrow(bufB + ic * NFD * 64, d);
+      const float s = xrow(bufB, ic, IC<NFD>{}, d, std::false_type{});
       const uint32_t r = w * RQ + i;
       if (lane < 4 && i < RQ && r < R) ll_put(LL + P.e_qkv + r, s, ep);
     } else {
@@ -1019,13 +1050,25 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         // the other buffer, which this phase neither reads nor loads)
         constexpr uint32_t PC = 2048 + 4;
         float* pc = reinterpret_cast<float*>(bufB) + 4096;
-        for (uint32_t t = tid; t < nl; t += kPT) {
-          const float4 v = vs[t];
-          const float et = e[t];
-          pc[t] = et * v.x;
-          pc[PC + t] = et * v.y;
-          pc[2 * PC + t] = et * v.z;
-          pc[3 * PC + t] = et * v.w;
+        for (uint32_t t0 = tid; t0 < nl; t0 += 4 * kPT) {
+          float4 v[4];
+          float et[4];
+#pragma unroll
+          for (uint32_t j = 0; j < 4; j++) {
+            const uint32_t t = t0 + kPT * j < nl ? t0 + kPT * j : t0;
+            v[j] = vs[t];
+            et[j] = e[t];
+          }
+#pragma unroll
+          for (uint32_t j = 0; j < 4; j++) {
+            const uint32_t t = t0 + kPT * j;
+            if (t < nl) {
+              pc[t] = et[j] * v[j].x;
+              pc[PC + t] = et[j] * v[j].y;
+              pc[2 * PC + t] = et[j] * v[j].z;
+              pc[3 * PC + t] = et[j] * v[j].w;
+            }
+          }
         }
         lds_barrier();
         if (wv == 0) {
@@ -1068,7 +1111,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     if constexpr (EX) {
       // add2 (bend/Dense/Model.bend:44-45): x + (the row's chain), lane 0
       xprod(bufB, RO, IC<NFD>{}, d);
-      const float s = xrow(bufB + (wv < RO ? wv : 0u) * NFD * 64, d);
+      const float s = xrow(bufB, wv < RO ? wv : 0u, IC<NFD>{}, d, std::false_type{});
       if (orow_ok) {
         xa_own = x_own + s;
         if (lane == 0) ll_put(LL + P.e_xa + orow, xa_own, ep);
@@ -1096,9 +1139,9 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     if constexpr (EX) {
       // M.norm, then lane 2 i + u: gate (u 0) or up (u 1) of pair wv + 4 i;
       // hh = silu(g) u (bend/Dense/Model.bend:58-59)
-      xprod_n(bufN, 2 * RGp, IC<NFD>{}, xrs(), gf[0]);
+      xprod_n(bufN, 2 * RGp, IC<NFD>{}, xrs(), gf[0], std::true_type{});
       const uint32_t pi = wv + 4 * ((lane & 3) >> 1), u = lane & 1, pc = pi < RGp ? pi : RGp - 1;
-      const float s = xrow(bufN + (pc * 2 + u) * NFD * 64, d);
+      const float s = xrow(bufN, pc * 2 + u, IC<NFD>{}, d, std::true_type{});
       const float up = __shfl_down(s, 1, 64);
       if (lane < 4 && u == 0) {
         const uint32_t jp = w * RGp + pi;
@@ -1151,7 +1194,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     if (!meet()) return false;
     if constexpr (EX) {
       xprod(bufB, RO, IC<NFF>{}, f);
-      const float s = xrow(bufB + (wv < RO ? wv : 0u) * NFF * 64, f);
+      const float s = xrow(bufB, wv < RO ? wv : 0u, IC<NFF>{}, f, std::false_type{});
       if (orow_ok) {
         x_own = xa_own + s;
         if (lane == 0) ll_put(LL + P.e_x + orow, x_own, ep);
