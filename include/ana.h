@@ -162,7 +162,11 @@ void ana_rng_seeded(uint64_t seed, uint64_t rng[4]);
  * feed the pick back. tok[i] is sequence i's first token at pos[i]; out
  * receives n x steps picks (row i = sequence i). EOS does not stop the loop;
  * a caller wanting Generate's stop truncates each row after its first 1.
- * rng as ana_pick (NULL when greedy). */
+ * rng as ana_pick (NULL when greedy). One greedy sequence (n = 1) runs as
+ * one persistent launch a call in every mode where the device and the model
+ * allow it (the environment's ANA_PERSIST=0 keeps it on the step graphs);
+ * its results are those of the graphs (bit for bit in ANA_EXACT_FP32), and
+ * it can fail with ANA_ETIME. */
 int ana_generate(struct ana_ctx* ctx, uint32_t n, const uint32_t* seq, const uint32_t* pos,
                  const uint32_t* tok, uint32_t steps, const ana_sampling* s, uint64_t* rng,
                  uint32_t* out);
@@ -197,8 +201,8 @@ int ana_state(struct ana_ctx* ctx, uint32_t seq, uint32_t layer, float* out, siz
 #define ANA_K_ATTN 2     /* softmax attention over the ring */
 #define ANA_K_GLA 3      /* the GLA state update and readout */
 #define ANA_K_PICK 4     /* greedy pick / sampler */
-#define ANA_K_STEP 5     /* whole decode steps in one persistent launch (fast fp32 or bf16,
-                            one greedy sequence): every kind above at once */
+#define ANA_K_STEP 5     /* whole decode steps in one persistent launch (one greedy
+                            sequence, any mode): every kind above at once */
 #define ANA_K_KINDS 6
 int ana_prof(struct ana_ctx* ctx, int on);
 int ana_prof_read(struct ana_ctx* ctx, uint32_t kind, uint64_t* launches, double* ms,
