@@ -857,6 +857,9 @@ static int run_layers(ana_ctx* c, uint32_t B, const uint32_t* seq, const uint32_
       if (fast_path(c, B))
         HIPCHK(c, launch_gla_fast(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), seq,
                                   c->O, d, cf.heads, cf.rglru, B, c->st));
+      else if (fast_mode(c) && d == 64 * cf.heads)
+        HIPCHK(c, launch_gla_wfast(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), seq,
+                                   c->O, d, cf.heads, cf.rglru, B, c->st));
       else
         HIPCHK(c, launch_gla_step(c->QKV, c->Z, cf.rglru ? W + b.lam : nullptr, sref(c, l), seq,
                                   c->O, d, cf.heads, cf.rglru, B, c->st));

@@ -270,6 +270,10 @@ hipError_t launch_gla_fast(const float* QKV, const float* Z, const float* lam, S
                            const uint32_t* seq, float* O, uint32_t d, uint32_t heads,
                            uint32_t rglru, uint32_t B, hipStream_t st);
 hipError_t launch_attn_fast(const AttnArgs& a, hipStream_t st);
+// the fast modes' GLA step above kSmallB decode rows: one wave a (head,
+// row), hd 64 (k_gla_w's layout, the fast mode's arithmetic)
+hipError_t launch_gla_wfast(const float* QKV, const float* Z, const float* lam, StateRef S, const uint32_t* seq,
+                            float* O, uint32_t d, uint32_t heads, uint32_t rglru, uint32_t B, hipStream_t st);
 // a fast-mode prefill step's K/V ring writes (dd.sm.write over every row,
 // the qk-norm's sums reassociated): hd 16, 32 or 64
 hipError_t launch_kv_write_fast(const AttnArgs& a, hipStream_t st);

@@ -414,6 +414,70 @@ hipError_t launch_gla_fast(const float* QKV, const float* Z, const float* lam, S
   return hipGetLastError();
 }
 
+// The GLA step of a fast-mode decode batch above kSmallB rows (dd.gla.tok,
+// bend/Dense/Decode.bend): one wave per (head, row) as the exact k_gla_w
+// lays it out (lane b holds column b of S, the 64 rows in registers, loaded
+// and stored as coalesced rows, the rows issued before this token's q|k|v|z
+// since they do not depend on it), with the fast mode's arithmetic: the
+// norms' sums by DPP over the wave, the hardware's reciprocal square root,
+// the gates in float, S' = al_a S_ab + kh_a v_b as one fused multiply-add
+// and o_b = sum_a qh_a S'_ab in four interleaved partial sums. (The exact
+// kernel's in-order chains, double-precision gates and IEEE divisions held
+// it at 8 us a layer at B = 64.)
+__global__ __launch_bounds__(64) void k_gla_wf(const float* __restrict__ QKV, const float* __restrict__ Z,
+                                               const float* __restrict__ lam, StateRef S,
+                                               const uint32_t* __restrict__ seq, float* __restrict__ O,
+                                               uint32_t d, uint32_t rglru) {
+  constexpr int HD = 64;
+  __shared__ __align__(16) float al[HD], kh[HD], qh[HD];
+  const uint32_t h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  float* Sg = S.base + (size_t)seq[b] * S.seq_stride + S.layer_off + (size_t)h * HD * HD;
+  float s[HD];
+#pragma unroll
+  for (int a = 0; a < HD; a++) s[a] = Sg[a * HD + lane];
+  const float* x = QKV + (size_t)b * 3 * d;
+  const float qv = x[h * HD + lane], kv = x[d + h * HD + lane], vv = x[2 * d + h * HD + lane];
+  const float zv = Z[(size_t)b * d + h * HD + lane];
+  const float lv = rglru ? lam[h * HD + lane] : 0.0f;
+  const float s0 = wsum(qv * qv), s1 = wsum(kv * kv);
+  const float kn = kv * __builtin_amdgcn_rsqf(1.0e-6f + s1);
+  qh[lane] = qv * __builtin_amdgcn_rsqf(1.0e-6f + s0);
+  if (rglru) {
+    // dd.gate's RG-LRU arm (bend/Dense/Ex.bend:158-162)
+    const float la = fminf(ANA_CAP, (8.0f * f_sigmoid(zv)) * f_log_sigmoid(lv));
+    kh[lane] = kn * sqrtf(1.0f - expf(2.0f * la));
+    al[lane] = expf(la);
+  } else {
+    al[lane] = f_sigmoid(zv);
+    kh[lane] = kn;
+  }
+  __syncthreads();
+  const float4* al4 = reinterpret_cast<const float4*>(al);
+  const float4* kh4 = reinterpret_cast<const float4*>(kh);
+  const float4* qh4 = reinterpret_cast<const float4*>(qh);
+  float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int a4 = 0; a4 < HD / 4; a4++) {
+    const float4 A = al4[a4], K = kh4[a4], Q = qh4[a4];
+    const float an[4] = {A.x, A.y, A.z, A.w}, kn4[4] = {K.x, K.y, K.z, K.w}, qn[4] = {Q.x, Q.y, Q.z, Q.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int a = 4 * a4 + e;
+      const float sa = fmaf(an[e], s[a], kn4[e] * vv);
+      Sg[a * HD + lane] = sa;
+      o[e] = fmaf(qn[e], sa, o[e]);
+    }
+  }
+  O[(size_t)b * d + h * HD + lane] = (o[0] + o[1]) + (o[2] + o[3]);
+}
+
+hipError_t launch_gla_wfast(const float* QKV, const float* Z, const float* lam, StateRef S, const uint32_t* seq,
+                            float* O, uint32_t d, uint32_t heads, uint32_t rglru, uint32_t B, hipStream_t st) {
+  if (heads == 0 || d / heads != 64 || d % heads) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gla_wf, dim3(heads, B), dim3(64), 0, st, QKV, Z, lam, S, seq, O, d, rglru);
+  return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ attention
 
 // Split softmax attention (flash decoding). Pass 1, per (head, split of
