@@ -469,7 +469,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
 #pragma unroll
     for (int i = 0; i < XN; i++) {
       const uint32_t k = kx(WLc, i);
-      g[i] = i < XW && k < d ? *reinterpret_cast<const float4*>(W + off + k) : zero4();
+      g[i] = i < XW ? *reinterpret_cast<const float4*>(W + off + (k < d ? k : 0u)) : zero4();
     }
   };
   // this lane's float4s of xs[0..n) in layout WL (XV of them)
@@ -524,6 +524,7 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
   // (every wave) when a wait failed.
   auto meet = [&]() -> bool {
     lds_barrier();
+    __builtin_amdgcn_s_waitcnt(ANA_VM(0));
     TS(2);
     if (bad_s) {
       fail_wg();
@@ -643,22 +644,23 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
     float4 g4[XN];
     if constexpr (EX) g4[0] = 4 * tid < d ? *reinterpret_cast<const float4*>(W + P.ra + 4 * tid) : zero4();
     else load_g(WLc, g4, P.ra);
-    float svr = 0.0f, lamr = 0.0f, gqr = 0.0f, gkr = 0.0f, sinkr = 0.0f;
+    float svr, lamr, gqr, gkr, sinkr;
     // the mix's own inputs that do not depend on this token: GLA column
     // 4 cb + wv of head h (lane a: row a of S) and the RG-LRU lambdas; the
     // attention's qk gains and sink
-    if (P.gla) {
-      if (gla_unit && (int)lane < HD) {
-        const uint32_t h = w / C4, cb = w % C4;
-        svr = Sseq[P.soff + (size_t)h * HD * HD + (size_t)lane * HD + 4 * cb + wv];
-        if (a.rglru) lamr = W[P.lam + h * HD + lane];
-      }
-    } else {
-      if (a.qk && att_unit && (int)tid < HD) {
-        gqr = W[P.gq + tid];
-        gkr = W[P.gk + tid];
-      }
-      if (a.sinks && gla_unit) sinkr = W[P.sink + w / C4];
+    // (loaded by every thread, from a valid place where the thread has none:
+    // a load that only some paths make leaves the compiler unsure which
+    // registers still await one, and it then waits for every load in
+    // flight, this phase's weight pieces included, at the next write to
+    // such a register)
+    {
+      const uint32_t h = gla_unit ? w / C4 : 0u, cb = w % C4, la = (int)lane < HD ? lane : 0u;
+      const uint32_t tq = (int)tid < HD ? tid : 0u;
+      svr = Sseq[(P.gla ? P.soff : 0u) + (size_t)h * HD * HD + (size_t)la * HD + 4 * cb + wv];
+      lamr = W[(P.gla && a.rglru ? P.lam : 0u) + h * HD + la];
+      gqr = W[(!P.gla && a.qk ? P.gq : 0u) + tq];
+      gkr = W[(!P.gla && a.qk ? P.gk : 0u) + tq];
+      sinkr = W[(!P.gla && a.sinks ? P.sink : 0u) + h];
     }
     if (l == 0 && orow_ok) x_own = W[(size_t)tok * d + orow];
     dma_kv(P, bufN);
@@ -741,6 +743,9 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         gathered(ok);
       }
       if (!meet()) return false;
+      // (the layer's constants, opaque from here: nothing computed from them
+      // is moved up to where they were loaded, which would wait for them there)
+      asm volatile("" : "+v"(svr), "+v"(lamr), "+v"(gqr), "+v"(gkr), "+v"(sinkr));
       if (EX && gla_unit) {
         // dd.gla.tok as the exact kernels take it (k_gla_w): every lane
         // runs the norms' chains over q and k; S'_ac = (al_a S_ac) + (kh_a
@@ -819,6 +824,9 @@ __global__ __launch_bounds__(kPT, 1) void k_decode1(PersistArgs a) {
         gathered(ok);
       }
       if (!meet()) return false;
+      // (the layer's constants, opaque from here: nothing computed from them
+      // is moved up to where they were loaded, which would wait for them there)
+      asm volatile("" : "+v"(svr), "+v"(lamr), "+v"(gqr), "+v"(gkr), "+v"(sinkr));
       if (EX && att_unit) {
         // k_attn_scores' steps: M.qkn (bend/Dense/Model.bend:39-42) by the
         // norms' chains, dd.sm.write of the row's k and v by the unit
